@@ -1,0 +1,300 @@
+"""3dmaker_amd: MI355X-native (gfx950) per-sample training hot path of 3DMaker.
+
+The product is the C-ABI shared library ``lib3dmaker_amd.so`` built from
+``csrc/`` (declarations in ``include/*.h``).  This module binds it with ctypes
+for Python callers, tests and the benchmark; it adds no compute of its own and
+has no fallback: if the library is missing or a call fails, it raises.
+
+Device buffers are passed as raw device pointers (ints) or as any object with
+a ``data_ptr()`` method (e.g. torch tensors); streams as raw hipStream_t ints
+(0 = null stream).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib3dmaker_amd.so")
+
+__all__ = [
+    "LIB_PATH", "lib", "launch", "MLPOption", "MLPGridOptions", "HashGrid", "Net",
+    "OUT_ACT_NONE", "OUT_ACT_SIGMOID", "ptr", "check",
+]
+
+OUT_ACT_NONE = 0
+OUT_ACT_SIGMOID = 1
+
+
+class MLPOption(C.Structure):
+    """modules/TinyMLP/TinyMLP.h:26-33"""
+    _fields_ = [("inputDim", C.c_int), ("hiddenDim", C.c_int), ("outputDim", C.c_int),
+                ("numLayers", C.c_int), ("activationType", C.c_int), ("outputActivation", C.c_int)]
+
+
+class MLPGridOptions(C.Structure):
+    """modules/TinyMLP/TinyMLPHashGrid.h:11-23"""
+    _fields_ = [("vectorDim", C.c_int), ("hiddenDim", C.c_int), ("outputDim", C.c_int),
+                ("numLayers", C.c_int), ("activationType", C.c_int), ("tableSize", C.c_int),
+                ("numLevels", C.c_int), ("b", C.c_float), ("lowestSize", C.c_int),
+                ("featuresLevel", C.c_int)]
+
+
+class GridBuffers(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in (
+        "master_hashtable", "fwd_hashtable", "hashtable_grads", "hash_m", "hash_v",
+        "master_weights", "master_biases", "fwd_weights", "w_grad", "b_grad", "activations",
+        "dx_out", "dloss", "padded_inputs", "padded_outputs")] + [("hw", MLPGridOptions), ("step", C.c_int)]
+
+
+class NetBuffers(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in (
+        "master_weights", "master_biases", "fwd_weights", "w_grad", "b_grad", "activations",
+        "dloss", "padded_outputs")] + [("hw", MLPOption), ("step", C.c_int)]
+
+
+_vp, _i, _f, _u = C.c_void_p, C.c_int, C.c_float, C.c_uint
+
+# name -> (restype, argtypes); every symbol here is declared in include/*.h
+SIGNATURES = {
+    # include/tinymlp_abi.h (reference launchers)
+    "launchNetworkFusionKernel": (None, [_vp, _vp, _vp, _vp, _vp, _i, _vp]),
+    "launchNetworkFusionBackwardKernel": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp]),
+    "launchNetworkFusionGradKernel": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _vp]),
+    "launchAdamWeightsOptim": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _f, _f, _f, _f, _f, _f, _f, _vp]),
+    "launchAdamBiasOptim": (None, [_vp, _vp, _vp, _vp, _vp, _f, _f, _f, _f, _f, _f, _f, _vp]),
+    "launchMSELossGrad": (None, [_vp, _vp, _vp, _vp, _i, _i, _i, _f, _vp, _i]),
+    "launchZeroGradients": (None, [_vp, _vp, _vp, _vp]),
+    "launchNetworkFusionHashTableKernel": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _vp]),
+    "launchNetworkFusionHashTableGradKernel": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp]),
+    "launchNetworkFusionHashTableBackwardKernel": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp]),
+    "launchNetworkFusionScatterBackwardKernel": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp]),
+    "launchHashTableBackwardKernel": (None, [_vp, _vp, _vp, _i, _i, _i, _f, _i, _i, _vp]),
+    "launchAdamHashGridOptim": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _f, _f, _f, _f, _f, _f, _f, _vp]),
+    "launchHashEncodeKernel": (None, [_vp, _vp, _vp, _i, _vp, _i, _vp]),
+    "tinymlp_last_error": (_i, []),
+    "tinymlp_last_error_message": (C.c_char_p, []),
+    # include/tinymlp_capi.h (flat handle API)
+    "tmlp_grid_create": (_vp, [C.POINTER(MLPGridOptions), _i, _i, _u, _i]),
+    "tmlp_grid_destroy": (None, [_vp]),
+    "tmlp_grid_switch_mode": (_i, [_vp, _i]),
+    "tmlp_grid_zero_grad": (_i, [_vp, _vp]),
+    "tmlp_grid_forward": (_i, [_vp, _vp, _vp, _i, _vp]),
+    "tmlp_grid_inference": (_i, [_vp, _vp, _vp, _i, _vp]),
+    "tmlp_grid_loss": (_i, [_vp, _vp, _i, _f, _i, C.POINTER(_f), _vp]),
+    "tmlp_grid_backward": (_i, [_vp, _vp, _i, _vp]),
+    "tmlp_grid_set_split_scatter": (_i, [_vp, _i]),
+    "tmlp_grid_step": (_i, [_vp, _f, _f, _f, _f, _f, _vp]),
+    "tmlp_grid_reset_step": (_i, [_vp]),
+    "tmlp_grid_load_weights": (_i, [_vp, _vp, _vp]),
+    "tmlp_grid_save_weights": (_i, [_vp, _vp, _vp]),
+    "tmlp_grid_load_hashgrid": (_i, [_vp, _vp]),
+    "tmlp_grid_save_hashgrid": (_i, [_vp, _vp]),
+    "tmlp_grid_load_file": (_i, [_vp, C.c_char_p]),
+    "tmlp_grid_save_file": (_i, [_vp, C.c_char_p]),
+    "tmlp_grid_buffers": (_i, [_vp, C.POINTER(GridBuffers)]),
+    "tmlp_net_create": (_vp, [C.POINTER(MLPOption), _i, _i, _u, _i]),
+    "tmlp_net_destroy": (None, [_vp]),
+    "tmlp_net_switch_mode": (_i, [_vp, _i]),
+    "tmlp_net_zero_grad": (_i, [_vp, _vp]),
+    "tmlp_net_forward": (_i, [_vp, _vp, _vp, _i, _vp]),
+    "tmlp_net_inference": (_i, [_vp, _vp, _vp, _i, _vp]),
+    "tmlp_net_loss": (_i, [_vp, _vp, _i, _f, _i, C.POINTER(_f), _vp]),
+    "tmlp_net_backward": (_i, [_vp, _vp, _vp, _i, _vp]),
+    "tmlp_net_step": (_i, [_vp, _f, _f, _f, _f, _f, _vp]),
+    "tmlp_net_reset_step": (_i, [_vp]),
+    "tmlp_net_load_weights": (_i, [_vp, _vp, _vp]),
+    "tmlp_net_save_weights": (_i, [_vp, _vp, _vp]),
+    "tmlp_net_load_file": (_i, [_vp, C.c_char_p]),
+    "tmlp_net_save_file": (_i, [_vp, C.c_char_p]),
+    "tmlp_net_buffers": (_i, [_vp, C.POINTER(NetBuffers)]),
+    "tmlp_device_synchronize": (_i, []),
+    "tmlp_version": (C.c_char_p, []),
+}
+
+_LIB = None
+
+
+def lib():
+    """Load lib3dmaker_amd.so (raises if it has not been built)."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: run __graft_entry__.build() first")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _LIB = L
+    return _LIB
+
+
+def ptr(x) -> int | None:
+    """Device pointer of x (int, None, or an object with data_ptr())."""
+    if x is None:
+        return None
+    if isinstance(x, int):
+        return x
+    return int(x.data_ptr())
+
+
+def check(rc: int = None):
+    """Raise RuntimeError if the last library call failed."""
+    L = lib()
+    if (rc is not None and rc != 0) or L.tinymlp_last_error() != 0:
+        raise RuntimeError(L.tinymlp_last_error_message().decode())
+
+
+def launch(name: str, *args):
+    """Call a reference launcher from include/tinymlp_abi.h and raise on failure.
+
+    Objects with data_ptr() are passed as their device pointer; ctypes
+    structures should be passed by reference (ctypes.byref)."""
+    L = lib()
+    conv = [ptr(a) if hasattr(a, "data_ptr") else a for a in args]
+    getattr(L, name)(*conv)
+    check()
+
+
+class HashGrid:
+    """TinyMLPHashGrid (modules/TinyMLP/TinyMLPHashGrid.h:33-85) over the flat C API."""
+
+    def __init__(self, opt: MLPGridOptions, max_batch: int, infer_batch: int = 0, seed: int = 42,
+                 training: bool = True):
+        self._L = lib()
+        self.opt = opt
+        self.h = self._L.tmlp_grid_create(C.byref(opt), max_batch, infer_batch, seed, int(training))
+        if not self.h:
+            check(1)
+
+    def close(self):
+        if getattr(self, "h", None):
+            self._L.tmlp_grid_destroy(self.h)
+            self.h = None
+
+    __del__ = close
+
+    def _c(self, rc):
+        if rc != 0:
+            check(rc)
+
+    def switch_mode(self, training: bool):
+        self._c(self._L.tmlp_grid_switch_mode(self.h, int(training)))
+
+    def zero_grad(self, stream=0):
+        self._c(self._L.tmlp_grid_zero_grad(self.h, stream))
+
+    def forward(self, inputs, outputs, batch, stream=0):
+        self._c(self._L.tmlp_grid_forward(self.h, ptr(inputs), ptr(outputs), batch, stream))
+
+    def inference(self, inputs, outputs, batch, stream=0):
+        self._c(self._L.tmlp_grid_inference(self.h, ptr(inputs), ptr(outputs), batch, stream))
+
+    def calculate_loss_and_grad(self, targets, batch, loss_scale=65536.0, fetch_loss=False, stream=0):
+        out = C.c_float(0.0)
+        self._c(self._L.tmlp_grid_loss(self.h, ptr(targets), batch, loss_scale, int(fetch_loss),
+                                       C.byref(out), stream))
+        return out.value
+
+    def backward(self, batch, custom_grad=None, stream=0):
+        self._c(self._L.tmlp_grid_backward(self.h, ptr(custom_grad), batch, stream))
+
+    def set_split_scatter(self, enabled: bool):
+        self._c(self._L.tmlp_grid_set_split_scatter(self.h, int(enabled)))
+
+    def step(self, lr=3e-4, beta1=0.9, beta2=0.999, eps=1e-8, loss_scale=65536.0, stream=0):
+        self._c(self._L.tmlp_grid_step(self.h, lr, beta1, beta2, eps, loss_scale, stream))
+
+    def reset_step(self):
+        self._c(self._L.tmlp_grid_reset_step(self.h))
+
+    def load_weights(self, w, b):
+        self._c(self._L.tmlp_grid_load_weights(self.h, w.ctypes.data, b.ctypes.data))
+
+    def save_weights(self, w, b):
+        self._c(self._L.tmlp_grid_save_weights(self.h, w.ctypes.data, b.ctypes.data))
+
+    def load_hashgrid(self, t):
+        self._c(self._L.tmlp_grid_load_hashgrid(self.h, t.ctypes.data))
+
+    def save_hashgrid(self, t):
+        self._c(self._L.tmlp_grid_save_hashgrid(self.h, t.ctypes.data))
+
+    def load_file(self, path: str):
+        self._c(self._L.tmlp_grid_load_file(self.h, path.encode()))
+
+    def save_file(self, path: str):
+        self._c(self._L.tmlp_grid_save_file(self.h, path.encode()))
+
+    def buffers(self) -> GridBuffers:
+        b = GridBuffers()
+        self._c(self._L.tmlp_grid_buffers(self.h, C.byref(b)))
+        return b
+
+
+class Net:
+    """TinyMLP (modules/TinyMLP/TinyMLP.h:35-84) over the flat C API."""
+
+    def __init__(self, opt: MLPOption, max_batch: int, infer_batch: int = 0, seed: int = 42,
+                 training: bool = True):
+        self._L = lib()
+        self.opt = opt
+        self.h = self._L.tmlp_net_create(C.byref(opt), max_batch, infer_batch, seed, int(training))
+        if not self.h:
+            check(1)
+
+    def close(self):
+        if getattr(self, "h", None):
+            self._L.tmlp_net_destroy(self.h)
+            self.h = None
+
+    __del__ = close
+
+    def _c(self, rc):
+        if rc != 0:
+            check(rc)
+
+    def switch_mode(self, training: bool):
+        self._c(self._L.tmlp_net_switch_mode(self.h, int(training)))
+
+    def zero_grad(self, stream=0):
+        self._c(self._L.tmlp_net_zero_grad(self.h, stream))
+
+    def forward(self, inputs, outputs, batch, stream=0):
+        self._c(self._L.tmlp_net_forward(self.h, ptr(inputs), ptr(outputs), batch, stream))
+
+    def inference(self, inputs, outputs, batch, stream=0):
+        self._c(self._L.tmlp_net_inference(self.h, ptr(inputs), ptr(outputs), batch, stream))
+
+    def calculate_loss_and_grad(self, targets, batch, loss_scale=65536.0, fetch_loss=False, stream=0):
+        out = C.c_float(0.0)
+        self._c(self._L.tmlp_net_loss(self.h, ptr(targets), batch, loss_scale, int(fetch_loss),
+                                      C.byref(out), stream))
+        return out.value
+
+    def backward(self, batch, custom_grad=None, dx_out=None, stream=0):
+        self._c(self._L.tmlp_net_backward(self.h, ptr(custom_grad), ptr(dx_out), batch, stream))
+
+    def step(self, lr=3e-4, beta1=0.9, beta2=0.999, eps=1e-8, loss_scale=65536.0, stream=0):
+        self._c(self._L.tmlp_net_step(self.h, lr, beta1, beta2, eps, loss_scale, stream))
+
+    def reset_step(self):
+        self._c(self._L.tmlp_net_reset_step(self.h))
+
+    def load_weights(self, w, b):
+        self._c(self._L.tmlp_net_load_weights(self.h, w.ctypes.data, b.ctypes.data))
+
+    def save_weights(self, w, b):
+        self._c(self._L.tmlp_net_save_weights(self.h, w.ctypes.data, b.ctypes.data))
+
+    def load_file(self, path: str):
+        self._c(self._L.tmlp_net_load_file(self.h, path.encode()))
+
+    def save_file(self, path: str):
+        self._c(self._L.tmlp_net_save_file(self.h, path.encode()))
+
+    def buffers(self) -> NetBuffers:
+        b = NetBuffers()
+        self._c(self._L.tmlp_net_buffers(self.h, C.byref(b)))
+        return b

@@ -1,0 +1,16 @@
+// Internal interface of the hash-grid kernels (hashgrid.hip).
+#pragma once
+
+#include "common.h"
+
+namespace graft {
+
+// enc [N x 2L] fp16 from positions [N x pos_stride] (x, y, z, ...).
+void hash_encode(const GridMeta& m, const __half* table, const float* pos, int pos_stride,
+                 __half* enc, int N, hipStream_t stream);
+
+// grads [L][T][2] += scatter of denc [N x 2L] (backward clamp).
+void hash_scatter(const GridMeta& m, const __half* denc, const float* pos, int pos_stride,
+                  float* grads, int N, hipStream_t stream);
+
+}  // namespace graft

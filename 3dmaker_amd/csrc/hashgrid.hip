@@ -1,0 +1,235 @@
+// Multiresolution hash grid on gfx950: standalone encode and the gradient
+// scatter, plus the host-side level table shared with the fused forward.
+//
+//   encode   networkFusionHashtable.cu:441-551 (encode block of the fused kernel)
+//   scatter  networkFusionBackwardHashtable.cu:783-910 (hashTableScatter_Backward)
+//
+// Thread mapping: one thread per (sample, group of 4 levels), group fastest,
+// so the per-sample row of the encoding / its gradient (4 levels x 2 features
+// = 16 B per thread) is read and written with contiguous 16-byte accesses,
+// and the level metadata comes from LDS.
+#include "hashgrid.h"
+
+#include "hash_encode.h"
+
+#include <algorithm>
+#include <cmath>
+#include <mutex>
+
+namespace graft {
+
+int dense_level_start(int tableSize, int lowestSize, float b, int numLevels)
+{
+    // networkFusionHashtable.cu:367-377, host float arithmetic (libm).
+    float inner = (std::cbrt(static_cast<float>(tableSize)) - 1.0f) / (float)lowestSize;
+    float cont = std::log2(inner) / std::log2(b);
+    int d = static_cast<int>(std::floor(cont)) + 1;
+    return std::max(0, std::min(d, numLevels));
+}
+
+GridMeta make_grid_meta(int tableSize, int numLevels, float b, int lowestSize)
+{
+    if (numLevels < 1 || numLevels > kMaxLevels)
+        throw std::runtime_error("TinyMLPHashGrid: numLevels must be in [1, 64]");
+    if (tableSize < 2 || (tableSize & (tableSize - 1)))
+        throw std::runtime_error("TinyMLPHashGrid: tableSize must be a power of two");
+    GridMeta m{};
+    m.numLevels = numLevels;
+    m.tableSize = tableSize;
+    m.denseLevelStart = dense_level_start(tableSize, lowestSize, b, numLevels);
+    for (int l = 0; l < numLevels; l++) {
+        m.scale[l] = (float)((double)lowestSize * std::pow((double)b, (double)l));
+        m.res[l] = (int)std::floor(m.scale[l]);
+        if (l < m.denseLevelStart) {
+            const double cells = std::pow((double)m.res[l] + 1.0, 3.0);
+            if (cells > (double)tableSize)
+                throw std::runtime_error("TinyMLPHashGrid: dense level exceeds the table size");
+        }
+    }
+    return m;
+}
+
+namespace {
+
+struct GridKernelArgs {
+    int L, T, dense_start, pos_stride, N;
+    float scale[kMaxLevels];
+    int res[kMaxLevels];
+};
+
+__device__ __forceinline__ void stage_meta(const GridKernelArgs& a, float* ss, int* sr)
+{
+    for (int e = threadIdx.x; e < a.L; e += blockDim.x) {
+        ss[e] = a.scale[e];
+        sr[e] = a.res[e];
+    }
+    __syncthreads();
+}
+
+__global__ __launch_bounds__(256) void hash_encode_kernel(const GridKernelArgs a,
+                                                          const float* __restrict__ pos,
+                                                          const _Float16* __restrict__ table,
+                                                          _Float16* __restrict__ enc)
+{
+    __shared__ float ss[kMaxLevels];
+    __shared__ int sr[kMaxLevels];
+    stage_meta(a, ss, sr);
+    const int G = (a.L + 3) >> 2;
+    const uint32_t mask = (uint32_t)a.T - 1u;
+    const int D = 2 * a.L;
+    for (long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x; t < (long long)a.N * G;
+         t += (long long)gridDim.x * blockDim.x) {
+        const int n = (int)(t / G), g = (int)(t - (long long)n * G);
+        const float* pp = pos + (size_t)n * a.pos_stride;
+        const float px = pp[0], py = pp[1], pz = pp[2];
+        _Float16 v[8];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int l = 4 * g + k;
+            float2 e = make_float2(0.f, 0.f);
+            if (l < a.L)
+                e = encode_level(px, py, pz, ss[l], sr[l], l < a.dense_start, mask,
+                                 table + (size_t)l * a.T * 2);
+            v[2 * k] = to_h(e.x);
+            v[2 * k + 1] = to_h(e.y);
+        }
+        _Float16* dst = enc + (size_t)n * D + 8 * g;
+        const int cnt = min(8, D - 8 * g);
+        if (cnt == 8) {
+            *reinterpret_cast<h4*>(dst) = h4{v[0], v[1], v[2], v[3]};
+            *reinterpret_cast<h4*>(dst + 4) = h4{v[4], v[5], v[6], v[7]};
+        } else {
+            for (int k = 0; k < cnt; k++) dst[k] = v[k];
+        }
+    }
+}
+
+// grads[l][idx][f] += dL/denc[n][2l+f] * w_c for the 8 corners (scatter clamp).
+__global__ __launch_bounds__(256) void hash_scatter_kernel(const GridKernelArgs a,
+                                                           const float* __restrict__ pos,
+                                                           const _Float16* __restrict__ denc,
+                                                           float* __restrict__ grads)
+{
+    __shared__ float ss[kMaxLevels];
+    __shared__ int sr[kMaxLevels];
+    stage_meta(a, ss, sr);
+    const int G = (a.L + 3) >> 2;
+    const uint32_t mask = (uint32_t)a.T - 1u;
+    const int D = 2 * a.L;
+    for (long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x; t < (long long)a.N * G;
+         t += (long long)gridDim.x * blockDim.x) {
+        const int n = (int)(t / G), g = (int)(t - (long long)n * G);
+        const float* pp = pos + (size_t)n * a.pos_stride;
+        const float px = pp[0], py = pp[1], pz = pp[2];
+        const _Float16* src = denc + (size_t)n * D + 8 * g;
+        _Float16 gv[8];
+        if (8 * g + 8 <= D) {
+            const h4 a0 = *reinterpret_cast<const h4*>(src);
+            const h4 a1 = *reinterpret_cast<const h4*>(src + 4);
+            gv[0] = a0[0]; gv[1] = a0[1]; gv[2] = a0[2]; gv[3] = a0[3];
+            gv[4] = a1[0]; gv[5] = a1[1]; gv[6] = a1[2]; gv[7] = a1[3];
+        } else {
+            for (int k = 0; k < 8; k++) gv[k] = (8 * g + k < D) ? src[k] : (_Float16)0.f;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int l = 4 * g + k;
+            if (l >= a.L) break;
+            const float gx = (float)gv[2 * k], gy = (float)gv[2 * k + 1];
+            Corners c;
+            level_corners<true>(px, py, pz, ss[l], sr[l], l < a.dense_start, mask, c);
+            float* lvl = grads + (size_t)l * a.T * 2;
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                atomic_add_f32(lvl + c.idx[q], gx * c.w[q]);
+                atomic_add_f32(lvl + c.idx[q] + 1, gy * c.w[q]);
+            }
+        }
+    }
+}
+
+GridKernelArgs grid_args(const GridMeta& m, int N, int pos_stride)
+{
+    GridKernelArgs a{};
+    a.L = m.numLevels;
+    a.T = m.tableSize;
+    a.dense_start = m.denseLevelStart;
+    a.pos_stride = pos_stride;
+    a.N = N;
+    for (int l = 0; l < m.numLevels; l++) {
+        a.scale[l] = m.scale[l];
+        a.res[l] = m.res[l];
+    }
+    return a;
+}
+
+int grid_blocks(long long threads)
+{
+    long long b = (threads + 255) / 256;
+    return (int)std::max(1LL, std::min(b, (long long)num_cus() * 16));
+}
+
+}  // namespace
+
+void hash_encode(const GridMeta& m, const __half* table, const float* pos, int pos_stride,
+                 __half* enc, int N, hipStream_t stream)
+{
+    if (N <= 0) return;
+    if (pos_stride < 3) throw std::runtime_error("hash encode: position stride must be >= 3");
+    const GridKernelArgs a = grid_args(m, N, pos_stride);
+    const long long threads = (long long)N * ((m.numLevels + 3) / 4);
+    hipLaunchKernelGGL(hash_encode_kernel, dim3(grid_blocks(threads)), dim3(256), 0, stream, a, pos,
+                       reinterpret_cast<const _Float16*>(table), reinterpret_cast<_Float16*>(enc));
+    GRAFT_LAUNCH_CHECK();
+}
+
+void hash_scatter(const GridMeta& m, const __half* denc, const float* pos, int pos_stride,
+                  float* grads, int N, hipStream_t stream)
+{
+    if (N <= 0) return;
+    if (pos_stride < 3) throw std::runtime_error("hash scatter: position stride must be >= 3");
+    const GridKernelArgs a = grid_args(m, N, pos_stride);
+    const long long threads = (long long)N * ((m.numLevels + 3) / 4);
+    hipLaunchKernelGGL(hash_scatter_kernel, dim3(grid_blocks(threads)), dim3(256), 0, stream, a,
+                       pos, reinterpret_cast<const _Float16*>(denc), grads);
+    GRAFT_LAUNCH_CHECK();
+}
+
+// ---------------------------------------------------------------------------
+// process-wide helpers
+// ---------------------------------------------------------------------------
+
+namespace {
+std::mutex g_ws_mu;
+void* g_ws = nullptr;
+size_t g_ws_bytes = 0;
+int g_cus = 0;
+}  // namespace
+
+void* workspace(size_t bytes)
+{
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    if (bytes > g_ws_bytes) {
+        if (g_ws) GRAFT_HIP_CHECK(hipFree(g_ws));
+        g_ws = nullptr;
+        size_t nb = std::max(bytes, (size_t)1 << 20);
+        GRAFT_HIP_CHECK(hipMalloc(&g_ws, nb));
+        g_ws_bytes = nb;
+    }
+    return g_ws;
+}
+
+int num_cus()
+{
+    if (g_cus == 0) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+            g_cus = n;
+        else
+            g_cus = 256;
+    }
+    return g_cus;
+}
+
+}  // namespace graft

@@ -1,0 +1,42 @@
+// Internal interface of the fused MLP kernels (mlp.hip).
+#pragma once
+
+#include "common.h"
+
+namespace graft {
+
+constexpr int kMaxLayers = 16;
+
+// Hardware shape of a TinyMLP: layer l maps in_l -> out_l.
+struct MlpShape {
+    int in, hid, out, layers;
+    int in_l(int l) const { return l == 0 ? in : hid; }
+    int out_l(int l) const { return l == layers - 1 ? out : hid; }
+    int maxd() const { return std::max(in, std::max(hid, out)); }
+    void validate() const;
+};
+
+// Layer-0 input: either fp16 features x [N x in], or positions + hash table
+// (then the encoding is computed on the fly and saved to acts[0]).
+struct FwdInput {
+    const __half* x = nullptr;
+    bool save_x0 = false;   // plain input: also write x into acts[0]
+    const float* pos = nullptr;
+    int pos_stride = 4;
+    const __half* table = nullptr;
+    const GridMeta* meta = nullptr;
+};
+
+// W, B, acts are DEVICE arrays of per-layer device pointers.  acts == nullptr
+// selects the inference kernel (no activation saves).
+void mlp_forward(const MlpShape& s, const FwdInput& in, const __half* const* W,
+                 const float* const* B, __half* const* acts, float* out, int N, int out_act,
+                 hipStream_t stream);
+
+// dW/dB (device arrays of per-layer pointers) are accumulated (+=); dx may be
+// nullptr (then layer 0's dX is skipped).
+void mlp_backward(const MlpShape& s, const __half* dy, const __half* const* acts,
+                  const __half* const* W, float* const* dW, float* const* dB, __half* dx, int N,
+                  hipStream_t stream);
+
+}  // namespace graft

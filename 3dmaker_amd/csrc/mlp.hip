@@ -1,0 +1,573 @@
+// Fully-fused TinyMLP forward/backward for gfx950 (CDNA4), fp16 MFMA with fp32
+// accumulation.
+//
+// Layout idea: activations travel as the B operand of v_mfma_f32_16x16x16f16
+// with samples along N and features along K.  The D layout of one 16x16 MFMA
+// (lane l holds rows 4*(l/16)..+3 of column l%16) is exactly the B layout of
+// the next layer's K-block, so a 16-sample tile walks through every layer in
+// registers: bias, ReLU and the fp16 rounding happen in place, and weights are
+// the A operand, pre-swizzled into LDS once per block.
+//
+// Semantics follow the reference kernels:
+//   forward  networkFusion.cu:197-355, networkFusionHashtable.cu:408-682
+//   backward networkFusionBackward.cu:49-646,
+//            networkFusionBackwardHashtable.cu:71-781 (COMPUTE_HASHGRAD = 0)
+// Rounding points: hidden activations -> fp16 after bias+ReLU, the last layer
+// stays fp32 (optional sigmoid); each dX -> fp16, then masked where the saved
+// activation <= 0.  dW/db are fp32 sums.  Unlike the reference, dW/db are not
+// fp32 atomics: every block writes a partial into a workspace and a second
+// kernel reduces the partials in a fixed order (bitwise-repeatable grads).
+#include "mlp.h"
+
+#include "hash_encode.h"
+
+#include <algorithm>
+#include <vector>
+
+namespace graft {
+
+namespace {
+
+__host__ __device__ inline int tiles16(int d) { return (d + 15) / 16; }
+
+// ---------------------------------------------------------------------------
+// forward
+// ---------------------------------------------------------------------------
+
+struct FwdParams {
+    const float* pos;             // HASH: [N x pos_stride] positions
+    const _Float16* table;        // HASH: [L][T][2]
+    const _Float16* x;            // plain: [N x in]
+    _Float16* const* acts;        // SAVE: device array of per-layer activations
+    const _Float16* const* W;     // device array, W_l row-major [out_l][in_l]
+    const float* const* B;        // device array, b_l [out_l]
+    float* out;                   // [N x out]
+    int N, in, hid, out_dim, layers, pos_stride, save_x0;
+    int frag_off[kMaxLayers];     // in halves
+    int bias_off[kMaxLayers];     // in floats from bias_base
+    int bias_base, meta_base;     // byte offsets into dynamic LDS
+    int L, T, dense_start;
+    float scale[kMaxLevels];
+    int res[kMaxLevels];
+};
+
+template <int MAXD, bool HASH, bool SAVE, int OUT_ACT>
+__global__ __launch_bounds__(256) void mlp_fwd_kernel(const FwdParams p)
+{
+    extern __shared__ __align__(16) unsigned char smem[];
+    _Float16* sfrag = reinterpret_cast<_Float16*>(smem);
+    float* sbias = reinterpret_cast<float*>(smem + p.bias_base);
+    float* sscale = reinterpret_cast<float*>(smem + p.meta_base);
+    int* sres = reinterpret_cast<int*>(smem + p.meta_base + 4 * kMaxLevels);
+    const int tid = threadIdx.x;
+
+    // Stage A-operand fragments: frag(l, mt, ks)[lane][j] = W_l[16mt + lane%16][16ks + 4(lane/16) + j]
+    for (int l = 0; l < p.layers; l++) {
+        const int in_l = l == 0 ? p.in : p.hid;
+        const int out_l = l == p.layers - 1 ? p.out_dim : p.hid;
+        const int KS = tiles16(in_l), MT = tiles16(out_l);
+        const _Float16* w = p.W[l];
+        for (int e = tid; e < MT * KS * 256; e += blockDim.x) {
+            const int j = e & 3, ln = (e >> 2) & 63, f = e >> 8;
+            const int mt = f / KS, ks = f - mt * KS;
+            const int row = 16 * mt + (ln & 15), col = 16 * ks + 4 * (ln >> 4) + j;
+            sfrag[p.frag_off[l] + e] = (row < out_l && col < in_l) ? w[row * in_l + col] : (_Float16)0.f;
+        }
+        for (int e = tid; e < MT * 16; e += blockDim.x)
+            sbias[p.bias_off[l] + e] = e < out_l ? p.B[l][e] : 0.f;
+    }
+    if constexpr (HASH) {
+        for (int e = tid; e < p.L; e += blockDim.x) {
+            sscale[e] = p.scale[e];
+            sres[e] = p.res[e];
+        }
+    }
+    __syncthreads();
+
+    constexpr int NT = MAXD / 16;
+    const int lane = tid & 63, wave = tid >> 6, r = lane & 15, g = lane >> 4;
+    const int ntiles = (p.N + 15) >> 4;
+    const int KS0 = tiles16(p.in);
+    const uint32_t mask = (uint32_t)p.T - 1u;
+    _Float16* act0 = nullptr;
+    if constexpr (SAVE) act0 = p.acts[0];
+
+    for (int tile = blockIdx.x * 4 + wave; tile < ntiles; tile += gridDim.x * 4) {
+        const int n = tile * 16 + r;
+        const bool valid = n < p.N;
+        h4 X[NT];
+        if constexpr (HASH) {
+            float px = 0.f, py = 0.f, pz = 0.f;
+            if (valid) {
+                const float* pp = p.pos + (size_t)n * p.pos_stride;
+                px = pp[0];
+                py = pp[1];
+                pz = pp[2];
+            }
+#pragma unroll
+            for (int ks = 0; ks < NT; ks++) {
+                X[ks] = h4zero();
+                if (ks < KS0) {
+                    const int la = 8 * ks + 2 * g, lb = la + 1;
+                    float2 ea = make_float2(0.f, 0.f), eb = make_float2(0.f, 0.f);
+                    if (valid && la < p.L)
+                        ea = encode_level(px, py, pz, sscale[la], sres[la], la < p.dense_start, mask,
+                                          p.table + (size_t)la * p.T * 2);
+                    if (valid && lb < p.L)
+                        eb = encode_level(px, py, pz, sscale[lb], sres[lb], lb < p.dense_start, mask,
+                                          p.table + (size_t)lb * p.T * 2);
+                    X[ks] = h4{to_h(ea.x), to_h(ea.y), to_h(eb.x), to_h(eb.y)};
+                    if (SAVE && valid) {
+                        const int col = 16 * ks + 4 * g;
+                        _Float16* dst = act0 + (size_t)n * p.in + col;
+                        if (col + 4 <= p.in) st_h4(dst, X[ks]);
+                        else if (col + 2 <= p.in) *reinterpret_cast<h2*>(dst) = h2{X[ks].x, X[ks].y};
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int ks = 0; ks < NT; ks++) {
+                const int col = 16 * ks + 4 * g;
+                const bool in_range = valid && ks < KS0 && col < p.in;
+                X[ks] = in_range ? ld_h4(p.x + (size_t)n * p.in + col) : h4zero();
+                if (SAVE && in_range && p.save_x0) st_h4(act0 + (size_t)n * p.in + col, X[ks]);
+            }
+        }
+
+        for (int l = 0; l < p.layers; l++) {
+            const int in_l = l == 0 ? p.in : p.hid;
+            const int out_l = l == p.layers - 1 ? p.out_dim : p.hid;
+            const int KS = tiles16(in_l), MT = tiles16(out_l);
+            const _Float16* fr = sfrag + p.frag_off[l] + lane * 4;
+            const float* bl = sbias + p.bias_off[l];
+            f4 acc[NT];
+#pragma unroll
+            for (int mt = 0; mt < NT; mt++) {
+                acc[mt] = f4zero();
+                if (mt < MT) {
+#pragma unroll
+                    for (int ks = 0; ks < NT; ks++)
+                        if (ks < KS)
+                            acc[mt] = mfma16(*reinterpret_cast<const h4*>(fr + (mt * KS + ks) * 256), X[ks], acc[mt]);
+                }
+            }
+            if (l < p.layers - 1) {
+                _Float16* act = nullptr;
+                if constexpr (SAVE) act = p.acts[l + 1];
+#pragma unroll
+                for (int mt = 0; mt < NT; mt++) {
+                    h4 h = h4zero();
+                    if (mt < MT) {
+                        const f4 bv = *reinterpret_cast<const f4*>(bl + 16 * mt + 4 * g);
+#pragma unroll
+                        for (int j = 0; j < 4; j++) {
+                            const float v = acc[mt][j] + bv[j];
+                            h[j] = to_h(v > 0.f ? v : 0.f);
+                        }
+                        const int col = 16 * mt + 4 * g;
+                        if (SAVE && valid && col < out_l) st_h4(act + (size_t)n * out_l + col, h);
+                    }
+                    X[mt] = h;
+                }
+            } else {
+#pragma unroll
+                for (int mt = 0; mt < NT; mt++) {
+                    if (mt < MT && valid) {
+                        const f4 bv = *reinterpret_cast<const f4*>(bl + 16 * mt + 4 * g);
+#pragma unroll
+                        for (int j = 0; j < 4; j++) {
+                            const int col = 16 * mt + 4 * g + j;
+                            float v = acc[mt][j] + bv[j];
+                            if (OUT_ACT == 1) v = 1.0f / (1.0f + expf(-v));
+                            if (col < out_l) p.out[(size_t)n * out_l + col] = v;
+                        }
+                    }
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// backward
+// ---------------------------------------------------------------------------
+
+constexpr int kBwdTilesPerWave = 2;                   // 16-sample tiles per wave per chunk
+constexpr int kBwdChunk = 4 * 16 * kBwdTilesPerWave;  // samples per block-chunk
+constexpr int kBwdPitch = kBwdChunk + 8;              // LDS row pitch (halves), +16 B against bank conflicts
+
+struct BwdParams {
+    const _Float16* dy;             // [N x out]
+    const _Float16* const* acts;    // device array: acts[0] = layer-0 input, acts[l] = H_l
+    const _Float16* const* W;       // device array
+    float* ws;                      // [gridDim.x][P] partial dW (all layers) then db
+    _Float16* dx;                   // nullable [N x in]
+    int N, in, hid, out_dim, layers;
+    int fragT_off[kMaxLayers];      // halves
+    int wofs[kMaxLayers], bofs[kMaxLayers];
+    int P;
+    int gt_base, xt_base, acc_base; // byte offsets into dynamic LDS
+    int nchunks;
+};
+
+template <int MAXD>
+__global__ __launch_bounds__(256) void mlp_bwd_kernel(const BwdParams p)
+{
+    extern __shared__ __align__(16) unsigned char smem[];
+    _Float16* sfrag = reinterpret_cast<_Float16*>(smem);
+    _Float16* Gt = reinterpret_cast<_Float16*>(smem + p.gt_base);
+    _Float16* Xt = reinterpret_cast<_Float16*>(smem + p.xt_base);
+    float* sacc = reinterpret_cast<float*>(smem + p.acc_base);
+    const int tid = threadIdx.x;
+
+    // Transposed fragments for dX = W^T G: fragT(l, mt, ks)[lane][j] = W_l[16ks + 4(lane/16) + j][16mt + lane%16]
+    for (int l = 0; l < p.layers; l++) {
+        const int in_l = l == 0 ? p.in : p.hid;
+        const int out_l = l == p.layers - 1 ? p.out_dim : p.hid;
+        const int KS = tiles16(out_l), MT = tiles16(in_l);
+        const _Float16* w = p.W[l];
+        for (int e = tid; e < MT * KS * 256; e += blockDim.x) {
+            const int j = e & 3, ln = (e >> 2) & 63, f = e >> 8;
+            const int mt = f / KS, ks = f - mt * KS;
+            const int o = 16 * ks + 4 * (ln >> 4) + j, i = 16 * mt + (ln & 15);
+            sfrag[p.fragT_off[l] + e] = (o < out_l && i < in_l) ? w[o * in_l + i] : (_Float16)0.f;
+        }
+    }
+    for (int e = tid; e < p.P; e += blockDim.x) sacc[e] = 0.f;
+    __syncthreads();
+
+    constexpr int NT = MAXD / 16;
+    constexpr int TPW = kBwdTilesPerWave;
+    const int lane = tid & 63, wave = tid >> 6, r = lane & 15, g = lane >> 4;
+
+    for (int chunk = blockIdx.x; chunk < p.nchunks; chunk += gridDim.x) {
+        const int s0 = chunk * kBwdChunk;
+        h4 G[TPW][NT];
+        {
+            const int KSo = tiles16(p.out_dim);
+#pragma unroll
+            for (int t = 0; t < TPW; t++) {
+                const int n = s0 + (wave * TPW + t) * 16 + r;
+#pragma unroll
+                for (int ks = 0; ks < NT; ks++) {
+                    const int col = 16 * ks + 4 * g;
+                    G[t][ks] = (n < p.N && ks < KSo && col < p.out_dim)
+                                   ? ld_h4(p.dy + (size_t)n * p.out_dim + col)
+                                   : h4zero();
+                }
+            }
+        }
+
+        for (int l = p.layers - 1; l >= 0; l--) {
+            const int in_l = l == 0 ? p.in : p.hid;
+            const int out_l = l == p.layers - 1 ? p.out_dim : p.hid;
+            const int KSo = tiles16(out_l), MTi = tiles16(in_l);
+            const _Float16* xl = p.acts[l];
+
+            // Layer input activations in B layout, and both operands of dW into LDS (feature-major).
+            h4 X[TPW][NT];
+#pragma unroll
+            for (int t = 0; t < TPW; t++) {
+                const int sl = (wave * TPW + t) * 16 + r;
+                const int n = s0 + sl;
+#pragma unroll
+                for (int mt = 0; mt < NT; mt++) {
+                    const int col = 16 * mt + 4 * g;
+                    X[t][mt] = (n < p.N && mt < MTi && col < in_l) ? ld_h4(xl + (size_t)n * in_l + col) : h4zero();
+                    if (mt < MTi) {
+#pragma unroll
+                        for (int j = 0; j < 4; j++) Xt[(col + j) * kBwdPitch + sl] = X[t][mt][j];
+                    }
+                }
+#pragma unroll
+                for (int ks = 0; ks < NT; ks++) {
+                    if (ks < KSo) {
+                        const int row = 16 * ks + 4 * g;
+#pragma unroll
+                        for (int j = 0; j < 4; j++) Gt[(row + j) * kBwdPitch + sl] = G[t][ks][j];
+                    }
+                }
+            }
+
+            // dX = W^T G, rounded to fp16, ReLU-masked by the saved activation.
+            if (l > 0 || p.dx != nullptr) {
+                const _Float16* fr = sfrag + p.fragT_off[l] + lane * 4;
+#pragma unroll
+                for (int t = 0; t < TPW; t++) {
+                    const int n = s0 + (wave * TPW + t) * 16 + r;
+                    h4 Gn[NT];
+#pragma unroll
+                    for (int mt = 0; mt < NT; mt++) {
+                        Gn[mt] = h4zero();
+                        if (mt < MTi) {
+                            f4 acc = f4zero();
+#pragma unroll
+                            for (int ks = 0; ks < NT; ks++)
+                                if (ks < KSo)
+                                    acc = mfma16(*reinterpret_cast<const h4*>(fr + (mt * KSo + ks) * 256), G[t][ks], acc);
+                            h4 h;
+#pragma unroll
+                            for (int j = 0; j < 4; j++) h[j] = to_h(acc[j]);
+                            if (l > 0) {
+#pragma unroll
+                                for (int j = 0; j < 4; j++)
+                                    if (!((float)X[t][mt][j] > 0.f)) h[j] = (_Float16)0.f;
+                            } else {
+                                const int col = 16 * mt + 4 * g;
+                                if (n < p.N && col < in_l) st_h4(p.dx + (size_t)n * in_l + col, h);
+                            }
+                            Gn[mt] = h;
+                        }
+                    }
+#pragma unroll
+                    for (int mt = 0; mt < NT; mt++) G[t][mt] = Gn[mt];
+                }
+            }
+            __syncthreads();
+
+            // dW_l[o][i] += sum_s Gt[o][s] * Xt[i][s]; tiles (mo, mi) round-robin over the 4 waves.
+            const int ntile = KSo * MTi;
+            for (int q = wave; q < ntile; q += 4) {
+                const int mo = q / MTi, mi = q - mo * MTi;
+                const _Float16* ga = Gt + (16 * mo + r) * kBwdPitch + 4 * g;
+                const _Float16* xb = Xt + (16 * mi + r) * kBwdPitch + 4 * g;
+                f4 acc = f4zero();
+#pragma unroll
+                for (int kk = 0; kk < kBwdChunk / 16; kk++)
+                    acc = mfma16(*reinterpret_cast<const h4*>(ga + 16 * kk),
+                                 *reinterpret_cast<const h4*>(xb + 16 * kk), acc);
+                const int i = 16 * mi + r;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int o = 16 * mo + 4 * g + j;
+                    if (o < out_l && i < in_l) sacc[p.wofs[l] + o * in_l + i] += acc[j];
+                }
+            }
+            // db_l[o] += sum_s Gt[o][s] (fp32 sum of fp16 values)
+            for (int o = tid; o < out_l; o += blockDim.x) {
+                const _Float16* row = Gt + o * kBwdPitch;
+                float s = 0.f;
+                for (int k = 0; k < kBwdChunk; k += 4) {
+                    const h4 v = *reinterpret_cast<const h4*>(row + k);
+                    s += ((float)v[0] + (float)v[1]) + ((float)v[2] + (float)v[3]);
+                }
+                sacc[p.bofs[l] + o] += s;
+            }
+            __syncthreads();
+        }
+    }
+    float* dst = p.ws + (size_t)blockIdx.x * p.P;
+    for (int e = tid; e < p.P; e += blockDim.x) dst[e] = sacc[e];
+}
+
+// grad[p] += sum over blocks of ws[b][p], summed in block order.
+struct ReduceParams {
+    const float* ws;
+    float* const* dW;
+    float* const* dB;
+    int nparts, P, layers, wtot;
+    int wofs[kMaxLayers], bofs[kMaxLayers];
+};
+
+__global__ __launch_bounds__(256) void mlp_grad_reduce_kernel(const ReduceParams p)
+{
+    __shared__ float part[4][64];
+    const int pl = threadIdx.x & 63, grp = threadIdx.x >> 6;
+    const int idx = blockIdx.x * 64 + pl;
+    float s = 0.f;
+    if (idx < p.P)
+        for (int b = grp; b < p.nparts; b += 4) s += p.ws[(size_t)b * p.P + idx];
+    part[grp][pl] = s;
+    __syncthreads();
+    if (grp == 0 && idx < p.P) {
+        const float tot = (part[0][pl] + part[1][pl]) + (part[2][pl] + part[3][pl]);
+        if (idx < p.wtot) {
+            int l = 0;
+            while (l + 1 < p.layers && idx >= p.wofs[l + 1]) l++;
+            p.dW[l][idx - p.wofs[l]] += tot;
+        } else {
+            const int k = idx - p.wtot;
+            int l = 0;
+            while (l + 1 < p.layers && k >= p.bofs[l + 1] - p.wtot) l++;
+            p.dB[l][k - (p.bofs[l] - p.wtot)] += tot;
+        }
+    }
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+
+void MlpShape::validate() const
+{
+    if (layers < 1 || layers > kMaxLayers)
+        throw std::runtime_error("TinyMLP: numLayers must be in [1, " + std::to_string(kMaxLayers) + "]");
+    if (in < 1 || hid < 1 || out < 1)
+        throw std::runtime_error("TinyMLP: dimensions must be positive");
+    if (in % 4 || hid % 4 || out % 4)
+        throw std::runtime_error("TinyMLP: in/hidden/out dims must be multiples of 4");
+    if (maxd() > 128) throw std::runtime_error("TinyMLP: max(in, hidden, out) must be <= 128");
+}
+
+static int pick_maxd(int d)
+{
+    if (d <= 16) return 16;
+    if (d <= 32) return 32;
+    if (d <= 64) return 64;
+    return 128;
+}
+
+static void fill_layer_offsets(const MlpShape& s, bool transposed, int* frag_off, int* bias_off,
+                               int& frag_halves, int& bias_floats)
+{
+    frag_halves = 0;
+    bias_floats = 0;
+    for (int l = 0; l < s.layers; l++) {
+        const int a = tiles16(s.out_l(l)), b = tiles16(s.in_l(l));
+        frag_off[l] = frag_halves;
+        frag_halves += a * b * 256;
+        (void)transposed;
+        if (bias_off) {
+            bias_off[l] = bias_floats;
+            bias_floats += a * 16;
+        }
+    }
+}
+
+static constexpr int kMaxLdsBytes = 64 * 1024;
+
+void mlp_forward(const MlpShape& s, const FwdInput& in, const __half* const* W,
+                 const float* const* B, __half* const* acts, float* out, int N, int out_act,
+                 hipStream_t stream)
+{
+    s.validate();
+    if (N <= 0) return;
+    FwdParams p{};
+    p.pos = in.pos;
+    p.pos_stride = in.pos_stride;
+    p.table = reinterpret_cast<const _Float16*>(in.table);
+    p.x = reinterpret_cast<const _Float16*>(in.x);
+    p.acts = reinterpret_cast<_Float16* const*>(acts);
+    p.W = reinterpret_cast<const _Float16* const*>(W);
+    p.B = B;
+    p.out = out;
+    p.N = N;
+    p.in = s.in;
+    p.hid = s.hid;
+    p.out_dim = s.out;
+    p.layers = s.layers;
+    p.save_x0 = in.save_x0 ? 1 : 0;
+    int frag_halves = 0, bias_floats = 0;
+    fill_layer_offsets(s, false, p.frag_off, p.bias_off, frag_halves, bias_floats);
+    p.bias_base = (frag_halves * 2 + 15) & ~15;
+    p.meta_base = (p.bias_base + bias_floats * 4 + 15) & ~15;
+    const bool hash = in.table != nullptr;
+    int lds = p.meta_base + (hash ? 8 * kMaxLevels : 0);
+    if (lds > kMaxLdsBytes) throw std::runtime_error("TinyMLP: network too large for the fused kernel LDS budget");
+    if (hash) {
+        const GridMeta& m = *in.meta;
+        p.L = m.numLevels;
+        p.T = m.tableSize;
+        p.dense_start = m.denseLevelStart;
+        for (int l = 0; l < m.numLevels; l++) {
+            p.scale[l] = m.scale[l];
+            p.res[l] = m.res[l];
+        }
+        if (2 * p.L != s.in) throw std::runtime_error("TinyMLPHashGrid: inputDim must equal 2 * numLevels");
+    }
+    const bool save = acts != nullptr;
+    const int ntiles = (N + 15) / 16;
+    const int blocks = std::max(1, std::min((ntiles + 3) / 4, num_cus() * 8));
+    const int maxd = pick_maxd(s.maxd());
+
+#define GRAFT_FWD_LAUNCH(MD)                                                                       \
+    do {                                                                                           \
+        if (hash) {                                                                                \
+            if (save) hipLaunchKernelGGL((mlp_fwd_kernel<MD, true, true, 0>), dim3(blocks), dim3(256), lds, stream, p); \
+            else hipLaunchKernelGGL((mlp_fwd_kernel<MD, true, false, 0>), dim3(blocks), dim3(256), lds, stream, p);     \
+        } else if (out_act == 1) {                                                                 \
+            if (save) hipLaunchKernelGGL((mlp_fwd_kernel<MD, false, true, 1>), dim3(blocks), dim3(256), lds, stream, p); \
+            else hipLaunchKernelGGL((mlp_fwd_kernel<MD, false, false, 1>), dim3(blocks), dim3(256), lds, stream, p);     \
+        } else {                                                                                   \
+            if (save) hipLaunchKernelGGL((mlp_fwd_kernel<MD, false, true, 0>), dim3(blocks), dim3(256), lds, stream, p); \
+            else hipLaunchKernelGGL((mlp_fwd_kernel<MD, false, false, 0>), dim3(blocks), dim3(256), lds, stream, p);     \
+        }                                                                                          \
+    } while (0)
+
+    switch (maxd) {
+        case 16: GRAFT_FWD_LAUNCH(16); break;
+        case 32: GRAFT_FWD_LAUNCH(32); break;
+        case 64: GRAFT_FWD_LAUNCH(64); break;
+        default: GRAFT_FWD_LAUNCH(128); break;
+    }
+#undef GRAFT_FWD_LAUNCH
+    GRAFT_LAUNCH_CHECK();
+}
+
+void mlp_backward(const MlpShape& s, const __half* dy, const __half* const* acts,
+                  const __half* const* W, float* const* dW, float* const* dB, __half* dx, int N,
+                  hipStream_t stream)
+{
+    s.validate();
+    if (N <= 0) return;
+    BwdParams p{};
+    p.dy = reinterpret_cast<const _Float16*>(dy);
+    p.acts = reinterpret_cast<const _Float16* const*>(acts);
+    p.W = reinterpret_cast<const _Float16* const*>(W);
+    p.dx = reinterpret_cast<_Float16*>(dx);
+    p.N = N;
+    p.in = s.in;
+    p.hid = s.hid;
+    p.out_dim = s.out;
+    p.layers = s.layers;
+    int frag_halves = 0, unused = 0;
+    fill_layer_offsets(s, true, p.fragT_off, nullptr, frag_halves, unused);
+    int wtot = 0;
+    for (int l = 0; l < s.layers; l++) {
+        p.wofs[l] = wtot;
+        wtot += s.in_l(l) * s.out_l(l);
+    }
+    int btot = wtot;
+    for (int l = 0; l < s.layers; l++) {
+        p.bofs[l] = btot;
+        btot += s.out_l(l);
+    }
+    p.P = btot;
+    const int maxd = pick_maxd(s.maxd());
+    p.gt_base = (frag_halves * 2 + 15) & ~15;
+    p.xt_base = p.gt_base + maxd * kBwdPitch * 2;
+    p.acc_base = p.xt_base + maxd * kBwdPitch * 2;
+    const int lds = p.acc_base + p.P * 4;
+    if (lds > kMaxLdsBytes) throw std::runtime_error("TinyMLP: network too large for the fused backward LDS budget");
+    p.nchunks = (N + kBwdChunk - 1) / kBwdChunk;
+    const int blocks = std::max(1, std::min(p.nchunks, num_cus() * 2));
+    p.ws = static_cast<float*>(workspace((size_t)blocks * p.P * sizeof(float)));
+
+    switch (maxd) {
+        case 16: hipLaunchKernelGGL(mlp_bwd_kernel<16>, dim3(blocks), dim3(256), lds, stream, p); break;
+        case 32: hipLaunchKernelGGL(mlp_bwd_kernel<32>, dim3(blocks), dim3(256), lds, stream, p); break;
+        case 64: hipLaunchKernelGGL(mlp_bwd_kernel<64>, dim3(blocks), dim3(256), lds, stream, p); break;
+        default: hipLaunchKernelGGL(mlp_bwd_kernel<128>, dim3(blocks), dim3(256), lds, stream, p); break;
+    }
+    GRAFT_LAUNCH_CHECK();
+
+    ReduceParams rp{};
+    rp.ws = p.ws;
+    rp.dW = dW;
+    rp.dB = dB;
+    rp.nparts = blocks;
+    rp.P = p.P;
+    rp.layers = s.layers;
+    rp.wtot = wtot;
+    for (int l = 0; l < s.layers; l++) {
+        rp.wofs[l] = p.wofs[l];
+        rp.bofs[l] = p.bofs[l];
+    }
+    hipLaunchKernelGGL(mlp_grad_reduce_kernel, dim3((p.P + 63) / 64), dim3(256), 0, stream, rp);
+    GRAFT_LAUNCH_CHECK();
+}
+
+}  // namespace graft

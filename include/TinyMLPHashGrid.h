@@ -1,0 +1,130 @@
+// TinyMLPHashGrid: multiresolution hash-grid encoding fused with a TinyMLP
+// (the NeRF density head) for MI355X / gfx950.  Drop-in for
+// modules/TinyMLP/TinyMLPHashGrid.h:33-165 of the reference: same class name,
+// constructor, methods and default arguments, with cudaStream_t replaced by
+// hipStream_t.
+//
+// Behavioural differences (all strictly safer than the reference):
+//  - backward() before any forward() throws std::runtime_error (the reference
+//    dereferences an unset input pointer, TinyMLPHashGrid.cu:258,343);
+//  - unsupported shapes throw at construction instead of silent no-ops;
+//  - per-level scales come from one fp64-evaluated host table
+//    (float)(lowestSize * b^l) instead of device fast-math __powf/exp2f;
+//  - MLP weight gradients are reduced deterministically.
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime_api.h>
+
+#include <string>
+
+#include "TinyMLP.h"
+#include "tinymlp_abi.h"
+
+// TinyMLPHashGrid.h:25-27
+inline int inputDim(MLPGridOptions& opt) { return opt.featuresLevel * opt.numLevels; }
+
+class TinyMLPHashGrid {
+public:
+    // TinyMLPHashGrid.h:35
+    explicit TinyMLPHashGrid(const MLPGridOptions& options, int maxBatchSize, int inferBatchSize = 0,
+                             unsigned int seed = 42, bool isTraining = true);
+    ~TinyMLPHashGrid();
+
+    TinyMLPHashGrid(const TinyMLPHashGrid&) = delete;
+    TinyMLPHashGrid& operator=(const TinyMLPHashGrid&) = delete;
+
+    void switchToInferenceMode();
+    void switchToTrainingMode();
+
+    void zero_grad(hipStream_t stream = 0);
+
+    // d_unpadded_inputs: [batchSize x vectorDim] float positions in [0,1].
+    void forward(const float* d_unpadded_inputs, float* d_outputs, int batchSize, hipStream_t stream = 0);
+
+    float calculate_loss_and_grad(const half* d_unpadded_targets, int batchSize, float loss_scale = 65536.0f,
+                                  bool fetch_loss = false, hipStream_t stream = 0);
+
+    void backward(int batchSize, hipStream_t stream = 0);
+    void backward(const half* custom_loss_grad, int batchSize, hipStream_t stream = 0);
+
+    void setSplitScatter(bool enabled) { m_useSplitScatter = enabled; }
+    bool getSplitScatter() const { return m_useSplitScatter; }
+
+    void step(float lr = 3e-4f, float beta1 = 0.9f, float beta2 = 0.999f, float epsilon = 1e-8f,
+              float loss_scale = 65536.0f, hipStream_t stream = 0);
+    void reset_step();
+
+    void inference(const float* d_unpadded_inputs, float* d_outputs, int batchSize, hipStream_t stream = 0);
+
+    void loadWeights(const std::string& filename);
+    void saveWeights(const std::string& filename);
+    void loadWeights(const float* host_weights, const float* host_biases);
+    void saveWeights(float* host_weights, float* host_biases);
+    void loadHashgrid(const float* host_hashgrid);
+    void saveHashgrid(float* host_hashgrid);
+
+    // ---- additions (no reference counterpart): introspection for tests ----
+    struct Buffers {
+        float* master_hashtable;
+        half* fwd_hashtable;
+        float* hashtable_grads;
+        float* hash_m;
+        float* hash_v;
+        float** master_weights;   // device arrays of per-layer pointers
+        float** master_biases;
+        half** fwd_weights;
+        float** w_grad;
+        float** b_grad;
+        half** activations;       // [0] = encoding [maxBatch x 2L]
+        half* dx_out;             // dL/d(encoding) [maxBatch x 2L]
+        half* dloss;
+        float* padded_inputs;     // [maxBatch x 4]
+        float* padded_outputs;
+        MLPGridOptions hw;
+        int step;
+    };
+    Buffers buffers() const;
+
+private:
+    MLPGridOptions user_opt;
+    MLPGridOptions hw_opt;
+    MLPOption mlp_opt;
+    int m_maxBatchSize;
+    int m_inferBatchSize;
+    int current_step;
+    bool m_isTraining;
+    bool m_useSplitScatter = true;
+
+    float* d_padded_inputs = nullptr;
+    const float* d_current_inputs_backward = nullptr;
+    half* d_padded_targets = nullptr;
+    float* d_padded_outputs_float = nullptr;
+    half* d_dLoss_internal = nullptr;
+    float* d_total_loss = nullptr;
+
+    float* d_master_hashtable = nullptr;
+    half* d_fwd_hashtable = nullptr;
+    float* d_hashtable_grads = nullptr;
+    float* d_hash_m = nullptr;
+    float* d_hash_v = nullptr;
+    int m_totalHashElements;
+
+    float** d_master_weights = nullptr;
+    float** d_master_biases = nullptr;
+    half** d_fwd_weights = nullptr;
+    half** d_activations = nullptr;
+    half* d_dx_out = nullptr;
+    float** d_w_grad = nullptr;
+    float** d_b_grad = nullptr;
+    float** d_w_m = nullptr;
+    float** d_w_v = nullptr;
+    float** d_b_m = nullptr;
+    float** d_b_v = nullptr;
+    void* h_ptrs = nullptr;
+    void* m_meta = nullptr;   // hash-grid level table (opaque)
+
+    void allocate_memory();
+    void free_training_state();
+    void run_backward(int batchSize, hipStream_t stream);
+};

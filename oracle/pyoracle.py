@@ -1,0 +1,194 @@
+"""numpy bindings of the C oracle (oracle/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, never by the product package.  fp16 arrays are
+numpy float16 (their bit patterns are what the C code reads and writes).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB = None
+
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
+_u32p = np.ctypeslib.ndpointer(np.uint32, flags="C_CONTIGUOUS")
+
+
+def build(force: bool = False) -> str:
+    path = os.path.join(_HERE, "liboracle.so")
+    if force or not os.path.exists(path):
+        subprocess.run(["make", "-C", _HERE, "-B" if force else "liboracle.so"],
+                       check=True, stdout=subprocess.DEVNULL)
+    return path
+
+
+def lib():
+    global _LIB
+    if _LIB is None:
+        path = os.path.join(_HERE, "liboracle.so")
+        if not os.path.exists(path):
+            build()
+        L = C.CDLL(path)
+        i, f, d, sz = C.c_int, C.c_float, C.c_double, C.c_size_t
+        sig = {
+            "orc_f32_to_f16": (C.c_uint16, [f]),
+            "orc_f16_to_f32": (f, [C.c_uint16]),
+            "orc_hash_coords": (C.c_uint32, [i, i, i, i]),
+            "orc_dense_index": (C.c_uint32, [i, i, i, i]),
+            "orc_dense_level_start": (i, [i, i, f, i]),
+            "orc_level_scales": (None, [i, f, i, _f32p, np.ctypeslib.ndpointer(np.int32)]),
+            "orc_hash_corners": (None, [_f32p, i, i, i, i, i, f, i, _u32p, _f32p]),
+            "orc_hash_encode_fwd": (None, [_f32p, i, i, _u16p, i, i, i, f, _u16p]),
+            "orc_hash_scatter_bwd": (None, [_f32p, i, i, _u16p, i, i, i, f, _f32p]),
+            "orc_mlp_forward": (None, [_u16p, i, i, i, i, i, _u16p, _f32p, i, C.c_void_p, _f32p]),
+            "orc_mlp_backward": (None, [_u16p, _u16p, C.c_void_p, i, i, i, i, i, _u16p,
+                                        _f32p, _f32p, C.c_void_p]),
+            "orc_mse_loss_grad": (d, [_f32p, _u16p, _u16p, i, i, i, f, i]),
+            "orc_adam_dense": (None, [_f32p, C.c_void_p, _f32p, _f32p, _f32p, sz,
+                                      f, f, f, f, f, f, f]),
+            "orc_adam_hash": (None, [_f32p, C.c_void_p, _f32p, _f32p, _f32p, sz,
+                                     f, f, f, f, f, f, f]),
+            "orc_adam_bias_corrections": (None, [f, f, i, C.POINTER(f), C.POINTER(f)]),
+            "orc_num_threads": (i, []),
+            "orc_set_num_threads": (None, [i]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _LIB = L
+    return _LIB
+
+
+def _h(a):
+    """float16 array -> uint16 view (C-contiguous)."""
+    return np.ascontiguousarray(a, dtype=np.float16).view(np.uint16)
+
+
+def _vp(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+def f32_to_f16_bits(x: float) -> int:
+    return lib().orc_f32_to_f16(float(x))
+
+
+def hash_coords(cx, cy, cz, T):
+    return lib().orc_hash_coords(int(cx), int(cy), int(cz), int(T))
+
+
+def dense_index(cx, cy, cz, N):
+    return lib().orc_dense_index(int(cx), int(cy), int(cz), int(N))
+
+
+def dense_level_start(T, base, b, L):
+    return lib().orc_dense_level_start(int(T), int(base), float(b), int(L))
+
+
+def level_scales(base, b, L):
+    s = np.zeros(L, np.float32)
+    r = np.zeros(L, np.int32)
+    lib().orc_level_scales(int(base), float(b), int(L), s, r)
+    return s, r
+
+
+def _pos(pos):
+    pos = np.ascontiguousarray(pos, dtype=np.float32)
+    assert pos.ndim == 2 and pos.shape[1] in (3, 4)
+    return pos, pos.shape[1]
+
+
+def hash_corners(pos, T, L, base, b, bwd_clamp=False):
+    pos, st = _pos(pos)
+    N = pos.shape[0]
+    idx = np.zeros((N, L, 8), np.uint32)
+    w = np.zeros((N, L, 8), np.float32)
+    lib().orc_hash_corners(pos, st, N, T, L, base, float(b), int(bwd_clamp), idx, w)
+    return idx, w
+
+
+def hash_encode(pos, table, T, L, base, b):
+    """table: float16 [L*T*2]; returns float16 [N, 2L]."""
+    pos, st = _pos(pos)
+    N = pos.shape[0]
+    out = np.zeros((N, 2 * L), np.uint16)
+    lib().orc_hash_encode_fwd(pos, st, N, _h(table).ravel(), T, L, base, float(b), out)
+    return out.view(np.float16)
+
+
+def hash_scatter(pos, denc, T, L, base, b, grads=None):
+    pos, st = _pos(pos)
+    N = pos.shape[0]
+    g = np.zeros(L * T * 2, np.float32) if grads is None else grads
+    lib().orc_hash_scatter_bwd(pos, st, N, _h(denc).ravel(), T, L, base, float(b), g)
+    return g
+
+
+def _layer_shapes(inD, hid, outD, nl):
+    shapes = []
+    for l in range(nl):
+        shapes.append((outD if l == nl - 1 else hid, inD if l == 0 else hid))
+    return shapes
+
+
+def mlp_forward(x, W, B, inD, hid, outD, nl, out_act=0, save_acts=True):
+    """x float16 [N,in]; W flat float16; B flat float32 -> (y f32 [N,out], acts f16 [nl-1,N,hid])."""
+    N = x.shape[0]
+    y = np.zeros((N, outD), np.float32)
+    acts = np.zeros((max(nl - 1, 1), N, hid), np.uint16) if save_acts else None
+    lib().orc_mlp_forward(_h(x).ravel(), N, inD, hid, outD, nl, _h(W).ravel(),
+                          np.ascontiguousarray(B, np.float32), int(out_act), _vp(acts), y)
+    return y, (acts.view(np.float16) if acts is not None else None)
+
+
+def mlp_backward(dy, x0, acts, W, inD, hid, outD, nl, dW=None, dB=None, want_dx=True):
+    N = dy.shape[0]
+    wtot = sum(o * i for o, i in _layer_shapes(inD, hid, outD, nl))
+    btot = sum(o for o, _ in _layer_shapes(inD, hid, outD, nl))
+    dW = np.zeros(wtot, np.float32) if dW is None else dW
+    dB = np.zeros(btot, np.float32) if dB is None else dB
+    dx = np.zeros((N, inD), np.uint16) if want_dx else None
+    a = _h(acts) if acts is not None else None
+    lib().orc_mlp_backward(_h(dy).ravel(), _h(x0).ravel(), _vp(a), N, inD, hid, outD, nl,
+                           _h(W).ravel(), dW, dB, _vp(dx))
+    return dW, dB, (dx.view(np.float16) if dx is not None else None)
+
+
+def mse_loss_grad(pred, tgt, valid, loss_scale, out_act=0):
+    pred = np.ascontiguousarray(pred, np.float32)
+    N, P = pred.shape
+    d = np.zeros((N, P), np.uint16)
+    tot = lib().orc_mse_loss_grad(pred, _h(tgt).ravel(), d, N, P, valid, float(loss_scale), int(out_act))
+    return tot, d.view(np.float16)
+
+
+def adam_dense(w, g, m, v, lr, b1, b2, eps, bc1, bc2, inv_scale, want_f16=True):
+    w16 = np.zeros(w.size, np.uint16) if want_f16 else None
+    lib().orc_adam_dense(w, _vp(w16), g, m, v, w.size, lr, b1, b2, eps, bc1, bc2, inv_scale)
+    return None if w16 is None else w16.view(np.float16)
+
+
+def adam_hash(w, g, m, v, lr, b1, b2, eps, bc1, bc2, inv_scale, want_f16=True):
+    w16 = np.zeros(w.size, np.uint16) if want_f16 else None
+    lib().orc_adam_hash(w, _vp(w16), g, m, v, w.size, lr, b1, b2, eps, bc1, bc2, inv_scale)
+    return None if w16 is None else w16.view(np.float16)
+
+
+def adam_bias_corrections(b1, b2, step):
+    c1, c2 = C.c_float(), C.c_float()
+    lib().orc_adam_bias_corrections(float(b1), float(b2), int(step), C.byref(c1), C.byref(c2))
+    return c1.value, c2.value
+
+
+def num_threads():
+    return lib().orc_num_threads()
+
+
+def set_num_threads(n):
+    lib().orc_set_num_threads(int(n))
