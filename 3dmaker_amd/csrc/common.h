@@ -85,4 +85,8 @@ void* workspace(size_t bytes);
 
 int num_cus();
 
+// Largest dynamic LDS allocation one workgroup may request on the current
+// device (160 KiB on gfx950).
+int max_lds_per_block();
+
 }  // namespace graft

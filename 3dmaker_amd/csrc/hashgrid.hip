@@ -204,7 +204,21 @@ std::mutex g_ws_mu;
 void* g_ws = nullptr;
 size_t g_ws_bytes = 0;
 int g_cus = 0;
+int g_lds = 0;
 }  // namespace
+
+int max_lds_per_block()
+{
+    if (g_lds == 0) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess && n > 0)
+            g_lds = n;
+        else
+            g_lds = 64 * 1024;
+    }
+    return g_lds;
+}
 
 void* workspace(size_t bytes)
 {

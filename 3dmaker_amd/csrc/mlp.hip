@@ -437,7 +437,6 @@ static void fill_layer_offsets(const MlpShape& s, bool transposed, int* frag_off
     }
 }
 
-static constexpr int kMaxLdsBytes = 64 * 1024;
 
 void mlp_forward(const MlpShape& s, const FwdInput& in, const __half* const* W,
                  const float* const* B, __half* const* acts, float* out, int N, int out_act,
@@ -466,7 +465,7 @@ void mlp_forward(const MlpShape& s, const FwdInput& in, const __half* const* W,
     p.meta_base = (p.bias_base + bias_floats * 4 + 15) & ~15;
     const bool hash = in.table != nullptr;
     int lds = p.meta_base + (hash ? 8 * kMaxLevels : 0);
-    if (lds > kMaxLdsBytes) throw std::runtime_error("TinyMLP: network too large for the fused kernel LDS budget");
+    if (lds > max_lds_per_block()) throw std::runtime_error("TinyMLP: network too large for the fused kernel LDS budget");
     if (hash) {
         const GridMeta& m = *in.meta;
         p.L = m.numLevels;
@@ -541,7 +540,7 @@ void mlp_backward(const MlpShape& s, const __half* dy, const __half* const* acts
     p.xt_base = p.gt_base + maxd * kBwdPitch * 2;
     p.acc_base = p.xt_base + maxd * kBwdPitch * 2;
     const int lds = p.acc_base + p.P * 4;
-    if (lds > kMaxLdsBytes) throw std::runtime_error("TinyMLP: network too large for the fused backward LDS budget");
+    if (lds > max_lds_per_block()) throw std::runtime_error("TinyMLP: network too large for the fused backward LDS budget");
     p.nchunks = (N + kBwdChunk - 1) / kBwdChunk;
     const int blocks = std::max(1, std::min(p.nchunks, num_cus() * 2));
     p.ws = static_cast<float*>(workspace((size_t)blocks * p.P * sizeof(float)));

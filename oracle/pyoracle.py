@@ -174,8 +174,13 @@ def adam_dense(w, g, m, v, lr, b1, b2, eps, bc1, bc2, inv_scale, want_f16=True):
     return None if w16 is None else w16.view(np.float16)
 
 
-def adam_hash(w, g, m, v, lr, b1, b2, eps, bc1, bc2, inv_scale, want_f16=True):
-    w16 = np.zeros(w.size, np.uint16) if want_f16 else None
+def adam_hash(w, g, m, v, lr, b1, b2, eps, bc1, bc2, inv_scale, want_f16=True, w16_init=None):
+    """Entries with g == 0 keep their fp16 copy: pass the current fp16 table as
+    w16_init to get the full post-step fp16 table (zeros otherwise)."""
+    if w16_init is not None:
+        w16 = _h(w16_init).copy().ravel()
+    else:
+        w16 = np.zeros(w.size, np.uint16) if want_f16 else None
     lib().orc_adam_hash(w, _vp(w16), g, m, v, w.size, lr, b1, b2, eps, bc1, bc2, inv_scale)
     return None if w16 is None else w16.view(np.float16)
 

@@ -149,7 +149,8 @@ def test_grid_forward_backward_step(dev, N):
     tg = grads.copy()
     tm = np.zeros_like(tw)
     tv = np.zeros_like(tw)
-    t16 = orc.adam_hash(tw, tg, tm, tv, 1e-2, 0.9, 0.99, 1e-15, bc1, bc2, 1 / scale)
+    t16 = orc.adam_hash(tw, tg, tm, tv, 1e-2, 0.9, 0.99, 1e-15, bc1, bc2, 1 / scale,
+                        w16_init=table.astype(np.float16))
     np.testing.assert_array_equal(d2h(bufs.master_hashtable, tw.shape, np.float32).view(np.uint32), tw.view(np.uint32))
     np.testing.assert_array_equal(d2h(bufs.fwd_hashtable, tw.shape, np.float16).view(np.uint16), t16.view(np.uint16))
     np.testing.assert_array_equal(d2h(bufs.hash_m, tw.shape, np.float32), tm)
@@ -221,7 +222,8 @@ def test_adam_hash_100_steps_bit_exact(dev):
     opt = grid_opt(T_, L, 1.5)
     rng = np.random.default_rng(99)
     w = rng.standard_normal(n).astype(np.float32)
-    d_w, d_w16 = T(w, dev), torch.empty(n, dtype=torch.float16, device=dev)
+    w16 = w.astype(np.float16)
+    d_w, d_w16 = T(w, dev), T(w16, dev)
     d_m, d_v = torch.zeros(n, device=dev), torch.zeros(n, device=dev)
     d_g = torch.empty(n, device=dev)
     m = np.zeros(n, np.float32)
@@ -235,8 +237,9 @@ def test_adam_hash_100_steps_bit_exact(dev):
         bc1, bc2 = orc.adam_bias_corrections(0.9, 0.99, t)
         P.launch("launchAdamHashGridOptim", C.byref(opt), d_w, d_w16, d_g, d_m, d_v, 1e-2, 0.9, 0.99, 1e-15,
                  bc1, bc2, 1 / 128.0, None)
-        w16 = orc.adam_hash(w, g, m, v, 1e-2, 0.9, 0.99, 1e-15, bc1, bc2, 1 / 128.0)
+        w16 = orc.adam_hash(w, g, m, v, 1e-2, 0.9, 0.99, 1e-15, bc1, bc2, 1 / 128.0, w16_init=w16)
     torch.cuda.synchronize()
+    np.testing.assert_array_equal(d_w16.cpu().numpy().view(np.uint16), w16.view(np.uint16))
     np.testing.assert_array_equal(d_w.cpu().numpy().view(np.uint32), w.view(np.uint32))
     np.testing.assert_array_equal(d_m.cpu().numpy().view(np.uint32), m.view(np.uint32))
     np.testing.assert_array_equal(d_v.cpu().numpy().view(np.uint32), v.view(np.uint32))
