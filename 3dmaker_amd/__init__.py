@@ -19,7 +19,7 @@ LIB_PATH = os.path.join(_HERE, "lib3dmaker_amd.so")
 
 __all__ = [
     "LIB_PATH", "lib", "launch", "MLPOption", "MLPGridOptions", "HashGrid", "Net",
-    "OUT_ACT_NONE", "OUT_ACT_SIGMOID", "ptr", "check",
+    "OUT_ACT_NONE", "OUT_ACT_SIGMOID", "ptr", "check", "Float3", "Uint3", "NerfOptions", "Nerf",
 ]
 
 OUT_ACT_NONE = 0
@@ -53,7 +53,41 @@ class NetBuffers(C.Structure):
         "dloss", "padded_outputs")] + [("hw", MLPOption), ("step", C.c_int)]
 
 
+class Float3(C.Structure):
+    """HIP float3 passed by value (12 bytes)."""
+    _fields_ = [("x", C.c_float), ("y", C.c_float), ("z", C.c_float)]
+
+
+class Uint3(C.Structure):
+    """HIP uint3 passed by value (12 bytes)."""
+    _fields_ = [("x", C.c_uint), ("y", C.c_uint), ("z", C.c_uint)]
+
+
+class NerfOptions(C.Structure):
+    """modules/NeRF/InstantNerf.h:35-76 (byte layout of include/nerf_capi.h InerfOptions);
+    start from Nerf.default_options()."""
+    _fields_ = [("gridResolution", C.c_uint * 3), ("aabbMin", C.c_float * 3), ("aabbMax", C.c_float * 3),
+                ("levelsMipmap", C.c_int), ("numCascades", C.c_int), ("samplesPerVoxel", C.c_int),
+                ("densityHiddenDim", C.c_int), ("densityNumLayers", C.c_int),
+                ("colorHiddenDim", C.c_int), ("colorNumLayers", C.c_int),
+                ("hashTableSize", C.c_int), ("numLevels", C.c_int), ("growthFactor", C.c_float),
+                ("baseResolution", C.c_int), ("featuresPerLevel", C.c_int),
+                ("renderBatchSize", C.c_int), ("batchSize", C.c_int), ("rayChunkSize", C.c_int),
+                ("lambdaDepth", C.c_float), ("lambdaDist", C.c_float), ("learningRate", C.c_float),
+                ("beta1", C.c_float), ("beta2", C.c_float), ("epsilon", C.c_float), ("lossScale", C.c_float),
+                ("bgColor", C.c_float * 3), ("minDensityThreshold", C.c_float), ("decayValue", C.c_float),
+                ("densityBias", C.c_float), ("legacyRenderFlag", C.c_uint8), ("isProfiling", C.c_uint8)]
+
+
+class StepBuffers(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in (
+        "num_steps", "ray_offsets", "positions", "ray_indices", "t_sorted", "density_out", "color_input",
+        "color_output", "sigma", "render_rgb", "phi", "dw", "weight_sum", "dsigma", "color_dx", "density_grad",
+        "result")] + [("trainSteps", C.c_int)]
+
+
 _vp, _i, _f, _u = C.c_void_p, C.c_int, C.c_float, C.c_uint
+_u32 = C.c_uint32
 
 # name -> (restype, argtypes); every symbol here is declared in include/*.h
 SIGNATURES = {
@@ -109,6 +143,40 @@ SIGNATURES = {
     "tmlp_net_save_file": (_i, [_vp, C.c_char_p]),
     "tmlp_net_buffers": (_i, [_vp, C.POINTER(NetBuffers)]),
     "tmlp_device_synchronize": (_i, []),
+    # include/nerf_abi.h (NeRF launchers)
+    "processRaysHitLinear": (_i, [_u32, _vp, _vp, _vp, _vp, _vp, _vp, Uint3, Float3, Float3, _i, _i, _i, _i,
+                                  C.POINTER(_u32), _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "launchVolumeRendering": (None, [_u32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f, _f,
+                                     Float3, _u32, _u32, _vp]),
+    "launchComputeRayAabbInv": (None, [_u32, _vp, _vp, Float3, Float3, _i, _vp, _vp, _vp, _vp]),
+    "launchComputeSHGather": (None, [_vp, _vp, _i, _i, _f, _vp, _vp, _vp, _vp]),
+    "launchComputeColorGrad": (None, [_u32, _u32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f, _f,
+                                      _u32, _vp]),
+    "launchComputeDensityGrad": (None, [_u32, _vp, _vp, _vp, _vp]),
+    "launchUpdateMasterGrid": (None, [_vp, _vp, _f, _i, _vp]),
+    "launchReduceSum": (None, [_vp, _i, _vp, _vp]),
+    "launchUpdateOccupancyGrid": (None, [_vp, _vp, _vp, _i, _i, _i, _f, _f, _vp]),
+    "launchBuildMipmaps": (None, [_vp, Uint3, _i, _i, _vp]),
+    "nerf_abi_echo_vec": (None, [Float3, Uint3, C.POINTER(_f)]),
+    # include/nerf_capi.h (InstantNerf handle API)
+    "inerf_default_options": (None, [C.POINTER(NerfOptions)]),
+    "inerf_options_size": (C.c_size_t, []),
+    "inerf_create": (_vp, [C.POINTER(NerfOptions)]),
+    "inerf_destroy": (None, [_vp]),
+    "inerf_train": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, C.POINTER(_i), _vp, _vp, _vp]),
+    "inerf_set_learning_rate": (_i, [_vp, _f]),
+    "inerf_set_bg_color": (_i, [_vp, _f, _f, _f]),
+    "inerf_set_profiling": (_i, [_vp, _i]),
+    "inerf_print_stats": (_i, [_vp]),
+    "inerf_update_occupancy": (_i, [_vp, _vp]),
+    "inerf_occupancy_bytes": (C.c_size_t, [_vp]),
+    "inerf_get_occupancy": (_i, [_vp, _vp]),
+    "inerf_set_occupancy": (_i, [_vp, _vp]),
+    "inerf_get_master_grid": (_i, [_vp, _vp]),
+    "inerf_step_buffers": (_i, [_vp, C.POINTER(StepBuffers)]),
+    "inerf_density": (_vp, [_vp]),
+    "inerf_color": (_vp, [_vp]),
+    "inerf_philox4x32_10": (None, [C.POINTER(_u32), _u32, _u32]),
     "tmlp_version": (C.c_char_p, []),
 }
 
@@ -297,4 +365,103 @@ class Net:
     def buffers(self) -> NetBuffers:
         b = NetBuffers()
         self._c(self._L.tmlp_net_buffers(self.h, C.byref(b)))
+        return b
+
+
+def _grid_view(h, opt):
+    v = HashGrid.__new__(HashGrid)
+    v._L, v.opt, v.h = lib(), opt, h
+    v.close = lambda: None
+    return v
+
+
+def _net_view(h, opt):
+    v = Net.__new__(Net)
+    v._L, v.opt, v.h = lib(), opt, h
+    v.close = lambda: None
+    return v
+
+
+class Nerf:
+    """InstantNerf (modules/NeRF/InstantNerf.h:279-335) over the flat C API (include/nerf_capi.h)."""
+
+    @staticmethod
+    def default_options() -> NerfOptions:
+        o = NerfOptions()
+        lib().inerf_default_options(C.byref(o))
+        return o
+
+    def __init__(self, opts: NerfOptions):
+        self._L = lib()
+        self.opts = opts
+        self.h = self._L.inerf_create(C.byref(opts))
+        if not self.h:
+            check(1)
+        G = opts.gridResolution[0] * opts.gridResolution[1] * opts.gridResolution[2]
+        self.cells = opts.numCascades * G
+        dopt = MLPGridOptions(vectorDim=4, hiddenDim=opts.densityHiddenDim, outputDim=16,
+                              numLayers=opts.densityNumLayers, activationType=0, tableSize=opts.hashTableSize,
+                              numLevels=opts.numLevels, b=opts.growthFactor, lowestSize=opts.baseResolution,
+                              featuresLevel=opts.featuresPerLevel)
+        copt = MLPOption(inputDim=32, hiddenDim=opts.colorHiddenDim, outputDim=3, numLayers=opts.colorNumLayers,
+                         activationType=0, outputActivation=OUT_ACT_SIGMOID)
+        self.density = _grid_view(self._L.inerf_density(self.h), dopt)
+        self.color = _net_view(self._L.inerf_color(self.h), copt)
+
+    def close(self):
+        if getattr(self, "h", None):
+            self._L.inerf_destroy(self.h)
+            self.h = None
+
+    __del__ = close
+
+    def _c(self, rc):
+        if rc != 0:
+            check(rc)
+
+    def train(self, rays_o, rays_d, rgb_true, num_rays, rays_depth=None, rays_sigma=None, rgb_out=None, stream=0,
+              max_steps=4096):
+        """trainWithRaysHit; returns (steps taken, [compacted samples per step])."""
+        cnt = C.c_int(0)
+        hits = (_u32 * max_steps)()
+        self._c(self._L.inerf_train(self.h, ptr(rays_o), ptr(rays_d), ptr(rays_depth), ptr(rays_sigma),
+                                    ptr(rgb_true), int(num_rays), C.byref(cnt), hits, ptr(rgb_out), stream))
+        return cnt.value, list(hits[:cnt.value])
+
+    def set_learning_rate(self, lr):
+        self._c(self._L.inerf_set_learning_rate(self.h, float(lr)))
+
+    def set_bg_color(self, r, g, b):
+        self._c(self._L.inerf_set_bg_color(self.h, float(r), float(g), float(b)))
+
+    def set_profiling(self, on):
+        self._c(self._L.inerf_set_profiling(self.h, int(on)))
+
+    def print_stats(self):
+        self._c(self._L.inerf_print_stats(self.h))
+
+    def update_occupancy(self, stream=0):
+        self._c(self._L.inerf_update_occupancy(self.h, stream))
+
+    def occupancy(self):
+        import numpy as np
+        out = np.zeros(self._L.inerf_occupancy_bytes(self.h), np.uint8)
+        self._c(self._L.inerf_get_occupancy(self.h, out.ctypes.data))
+        return out
+
+    def set_occupancy(self, bits):
+        import numpy as np
+        bits = np.ascontiguousarray(bits, np.uint8)
+        assert bits.size == self._L.inerf_occupancy_bytes(self.h)
+        self._c(self._L.inerf_set_occupancy(self.h, bits.ctypes.data))
+
+    def master_grid(self):
+        import numpy as np
+        out = np.zeros(self.cells, np.float32)
+        self._c(self._L.inerf_get_master_grid(self.h, out.ctypes.data))
+        return out
+
+    def step_buffers(self) -> StepBuffers:
+        b = StepBuffers()
+        self._c(self._L.inerf_step_buffers(self.h, C.byref(b)))
         return b

@@ -7,6 +7,8 @@
 #include "tinymlp_abi.h"
 #include "tinymlp_capi.h"
 
+#include "abi_error.h"
+#include "capi_handles.h"
 #include "common.h"
 #include "hashgrid.h"
 #include "mlp.h"
@@ -17,27 +19,7 @@
 
 namespace {
 
-thread_local int t_err = 0;
-thread_local std::string t_msg;
-
-template <class F>
-int guarded(const char* what, F&& f)
-{
-    try {
-        f();
-        t_err = 0;
-        t_msg.clear();
-        return 0;
-    } catch (const std::exception& e) {
-        t_err = 1;
-        t_msg = std::string(what) + ": " + e.what();
-    } catch (...) {
-        t_err = 1;
-        t_msg = std::string(what) + ": unknown exception";
-    }
-    std::fprintf(stderr, "[tinymlp] %s\n", t_msg.c_str());
-    return t_err;
-}
+using graft::guarded;
 
 graft::MlpShape shape(const MLPOption* o)
 {
@@ -75,7 +57,17 @@ graft::AdamArgs adam(float lr, float b1, float b2, float eps, float bc1, float b
     return graft::AdamArgs{lr, b1, b2, eps, bc1, bc2, ils};
 }
 
+thread_local int t_err = 0;
+thread_local std::string t_msg;
+
 }  // namespace
+
+void graft::set_last_error(int code, const std::string& msg)
+{
+    t_err = code;
+    t_msg = msg;
+    if (code) std::fprintf(stderr, "[tinymlp] %s\n", msg.c_str());
+}
 
 extern "C" {
 
@@ -248,26 +240,20 @@ void launchHashEncodeKernel(MLPGridOptions* opt, half* d_hashtable, const float*
 // flat handle API
 // ---------------------------------------------------------------------------
 
-struct TmlpGrid {
-    TinyMLPHashGrid* g;
-};
-struct TmlpNet {
-    TinyMLP* n;
-};
 
 TmlpGrid* tmlp_grid_create(const MLPGridOptions* opt, int maxBatchSize, int inferBatchSize, unsigned seed,
                            int isTraining)
 {
     TmlpGrid* h = nullptr;
     guarded("tmlp_grid_create", [&] {
-        h = new TmlpGrid{new TinyMLPHashGrid(*opt, maxBatchSize, inferBatchSize, seed, isTraining != 0)};
+        h = new TmlpGrid{new TinyMLPHashGrid(*opt, maxBatchSize, inferBatchSize, seed, isTraining != 0), true};
     });
     return h;
 }
 
 void tmlp_grid_destroy(TmlpGrid* h)
 {
-    if (!h) return;
+    if (!h || !h->owned) return;
     delete h->g;
     delete h;
 }
@@ -344,7 +330,7 @@ TmlpNet* tmlp_net_create(const MLPOption* opt, int maxBatchSize, int inferBatchS
 
 void tmlp_net_destroy(TmlpNet* h)
 {
-    if (!h) return;
+    if (!h || !h->owned) return;
     delete h->n;
     delete h;
 }

@@ -10,7 +10,8 @@ void hash_encode(const GridMeta& m, const __half* table, const float* pos, int p
                  __half* enc, int N, hipStream_t stream);
 
 // grads [L][T][2] += scatter of denc [N x 2L] (backward clamp).
+// d_n (nullable): device-side sample count (<= N), as for the MLP kernels.
 void hash_scatter(const GridMeta& m, const __half* denc, const float* pos, int pos_stride,
-                  float* grads, int N, hipStream_t stream);
+                  float* grads, int N, hipStream_t stream, const uint32_t* d_n = nullptr);
 
 }  // namespace graft

@@ -52,6 +52,7 @@ GridMeta make_grid_meta(int tableSize, int numLevels, float b, int lowestSize)
 namespace {
 
 struct GridKernelArgs {
+    const uint32_t* d_n;   // nullable device-side sample count (<= N)
     int L, T, dense_start, pos_stride, N;
     float scale[kMaxLevels];
     int res[kMaxLevels];
@@ -105,6 +106,15 @@ __global__ __launch_bounds__(256) void hash_encode_kernel(const GridKernelArgs a
 }
 
 // grads[l][idx][f] += dL/denc[n][2l+f] * w_c for the 8 corners (scatter clamp).
+//
+// fp32 atomics on gfx950 are priced per cache-line request, not per lane, so
+// the lane mapping puts four atomics into one 128-byte line: thread t handles
+// (sample n, level l, x-corner xs, feature f) with f and xs fastest.  The two
+// x-neighbour corners of a level differ only in the low bits of their index
+// (dense: adjacent entries; hashed: x0 ^ (x0 + 1) touches the low bits only,
+// which stays inside one 16-entry = 128-byte block 15 times in 16), so the
+// quad's 4 atomics per y/z corner usually share a line, and each thread issues
+// 4 atomics (its x-corner's four y/z neighbours) instead of 16.
 __global__ __launch_bounds__(256) void hash_scatter_kernel(const GridKernelArgs a,
                                                            const float* __restrict__ pos,
                                                            const _Float16* __restrict__ denc,
@@ -113,38 +123,23 @@ __global__ __launch_bounds__(256) void hash_scatter_kernel(const GridKernelArgs 
     __shared__ float ss[kMaxLevels];
     __shared__ int sr[kMaxLevels];
     stage_meta(a, ss, sr);
-    const int G = (a.L + 3) >> 2;
     const uint32_t mask = (uint32_t)a.T - 1u;
     const int D = 2 * a.L;
-    for (long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x; t < (long long)a.N * G;
+    const int N = a.d_n ? min((int)*a.d_n, a.N) : a.N;
+    const long long total = (long long)N * a.L * 4;
+    for (long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x; t < total;
          t += (long long)gridDim.x * blockDim.x) {
-        const int n = (int)(t / G), g = (int)(t - (long long)n * G);
+        const int f = (int)(t & 1), xs = (int)((t >> 1) & 1);
+        const long long nl = t >> 2;
+        const int n = (int)(nl / a.L), l = (int)(nl - (long long)n * a.L);
         const float* pp = pos + (size_t)n * a.pos_stride;
         const float px = pp[0], py = pp[1], pz = pp[2];
-        const _Float16* src = denc + (size_t)n * D + 8 * g;
-        _Float16 gv[8];
-        if (8 * g + 8 <= D) {
-            const h4 a0 = *reinterpret_cast<const h4*>(src);
-            const h4 a1 = *reinterpret_cast<const h4*>(src + 4);
-            gv[0] = a0[0]; gv[1] = a0[1]; gv[2] = a0[2]; gv[3] = a0[3];
-            gv[4] = a1[0]; gv[5] = a1[1]; gv[6] = a1[2]; gv[7] = a1[3];
-        } else {
-            for (int k = 0; k < 8; k++) gv[k] = (8 * g + k < D) ? src[k] : (_Float16)0.f;
-        }
+        const float gv = (float)denc[(size_t)n * D + 2 * l + f];
+        Corners c;
+        level_corners<true>(px, py, pz, ss[l], sr[l], l < a.dense_start, mask, c);
+        float* lvl = grads + (size_t)l * a.T * 2 + f;
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const int l = 4 * g + k;
-            if (l >= a.L) break;
-            const float gx = (float)gv[2 * k], gy = (float)gv[2 * k + 1];
-            Corners c;
-            level_corners<true>(px, py, pz, ss[l], sr[l], l < a.dense_start, mask, c);
-            float* lvl = grads + (size_t)l * a.T * 2;
-#pragma unroll
-            for (int q = 0; q < 8; q++) {
-                atomic_add_f32(lvl + c.idx[q], gx * c.w[q]);
-                atomic_add_f32(lvl + c.idx[q] + 1, gy * c.w[q]);
-            }
-        }
+        for (int q = 0; q < 4; q++) atomic_add_f32(lvl + c.idx[xs + 2 * q], gv * c.w[xs + 2 * q]);
     }
 }
 
@@ -184,12 +179,13 @@ void hash_encode(const GridMeta& m, const __half* table, const float* pos, int p
 }
 
 void hash_scatter(const GridMeta& m, const __half* denc, const float* pos, int pos_stride,
-                  float* grads, int N, hipStream_t stream)
+                  float* grads, int N, hipStream_t stream, const uint32_t* d_n)
 {
     if (N <= 0) return;
     if (pos_stride < 3) throw std::runtime_error("hash scatter: position stride must be >= 3");
-    const GridKernelArgs a = grid_args(m, N, pos_stride);
-    const long long threads = (long long)N * ((m.numLevels + 3) / 4);
+    GridKernelArgs a = grid_args(m, N, pos_stride);
+    a.d_n = d_n;
+    const long long threads = (long long)N * m.numLevels * 4;
     hipLaunchKernelGGL(hash_scatter_kernel, dim3(grid_blocks(threads)), dim3(256), 0, stream, a,
                        pos, reinterpret_cast<const _Float16*>(denc), grads);
     GRAFT_LAUNCH_CHECK();

@@ -1,0 +1,589 @@
+// InstantNerf training engine on gfx950 (declared in include/InstantNerf.h).
+//
+// The step loop follows InstantNerf::trainWithRaysHit (InstantNerf.cu:359-583)
+// stage by stage; the occupancy refresh follows earlyOccupancyGridUpdate /
+// lateOccupancyGridUpdate (InstantNerf.cu:1009-1171).  Every launch of a step
+// is sized for the step's upper bounds (rayChunkSize rays, batchSize samples)
+// and reads the actual counts the compaction left in device memory.
+#include "InstantNerf.h"
+
+#include "hashgrid.h"
+#include "mlp.h"
+#include "nerf.h"
+#include "nerf_math.h"
+#include "occupancy.h"
+
+#include <algorithm>
+#include <cstdio>
+#include <map>
+#include <stdexcept>
+#include <vector>
+
+namespace {
+
+struct StageTimer {
+    const char* name;
+    hipEvent_t a, b;
+};
+
+struct NerfBuffers {
+    // per step, rays
+    float3* d_inv = nullptr;
+    float* nears = nullptr;
+    float* fars = nullptr;
+    uint32_t* counts = nullptr;
+    uint32_t* offsets = nullptr;
+    uint32_t* block_sums = nullptr;
+    uint32_t* result = nullptr;
+    uint32_t* h_result = nullptr;  // pinned
+    float* render_rgb = nullptr;
+    float* render_depth = nullptr;
+    float* phi = nullptr;
+    float* weight_sum = nullptr;
+    // per step, samples
+    float4* positions = nullptr;
+    uint32_t* ray_idx = nullptr;
+    float* t_sorted = nullptr;
+    float* density_out = nullptr;
+    float* sigma = nullptr;
+    float* dw = nullptr;
+    float* dsigma = nullptr;
+    __half* color_dx = nullptr;
+    // occupancy
+    float* tmp_grid = nullptr;
+    float4* occ_samples = nullptr;
+    float* occ_density = nullptr;
+    float* partials = nullptr;
+    float* sum = nullptr;
+    int* active_list = nullptr;
+    int* active_count = nullptr;
+    uint32_t* list_scratch = nullptr;
+    int occ_capacity = 0;
+    // model views
+    __half* color_in = nullptr;      // TinyMLP activation 0
+    graft::GridMeta meta{};
+    hipEvent_t ev_result = nullptr;
+    std::vector<StageTimer> pending;
+    std::map<std::string, std::pair<double, long>> stats;
+};
+
+template <class T>
+T* dalloc(size_t n)
+{
+    void* p = nullptr;
+    if (n) GRAFT_HIP_CHECK(hipMalloc(&p, n * sizeof(T)));
+    return static_cast<T*>(p);
+}
+
+template <class T>
+void dfree(T*& p)
+{
+    if (p) (void)hipFree(p);
+    p = nullptr;
+}
+
+int grid_cells(const NerfOptions& o) { return (int)(o.gridResolution.x * o.gridResolution.y * o.gridResolution.z); }
+
+NerfBuffers& B(void* p) { return *static_cast<NerfBuffers*>(p); }
+
+graft::OccGrid occ_grid(const NerfOptions& o, const uint8_t* bits)
+{
+    graft::OccGrid g{};
+    g.bits = bits;
+    g.res = o.gridResolution;
+    g.aabb_min = o.aabbMin;
+    g.aabb_max = o.aabbMax;
+    g.cascades = o.numCascades;
+    g.mip_levels = o.levelsMipmap;
+    return g;
+}
+
+graft::MlpShape shape_of(const MLPOption& o) { return graft::MlpShape{o.inputDim, o.hiddenDim, o.outputDim, o.numLayers}; }
+
+}  // namespace
+
+InstantNerf::~InstantNerf() { freeBuffers(); }
+
+void InstantNerf::freeBuffers()
+{
+    if (m_buf) {
+        NerfBuffers& b = B(m_buf);
+        dfree(b.d_inv);
+        dfree(b.nears);
+        dfree(b.fars);
+        dfree(b.counts);
+        dfree(b.offsets);
+        dfree(b.block_sums);
+        dfree(b.result);
+        if (b.h_result) (void)hipHostFree(b.h_result);
+        dfree(b.render_rgb);
+        dfree(b.render_depth);
+        dfree(b.phi);
+        dfree(b.weight_sum);
+        dfree(b.positions);
+        dfree(b.ray_idx);
+        dfree(b.t_sorted);
+        dfree(b.density_out);
+        dfree(b.sigma);
+        dfree(b.dw);
+        dfree(b.dsigma);
+        dfree(b.color_dx);
+        dfree(b.tmp_grid);
+        dfree(b.occ_samples);
+        dfree(b.occ_density);
+        dfree(b.partials);
+        dfree(b.sum);
+        dfree(b.active_list);
+        dfree(b.active_count);
+        dfree(b.list_scratch);
+        if (b.ev_result) (void)hipEventDestroy(b.ev_result);
+        for (auto& t : b.pending) {
+            (void)hipEventDestroy(t.a);
+            (void)hipEventDestroy(t.b);
+        }
+        delete &b;
+        m_buf = nullptr;
+    }
+    dfree(d_occupancyGrid);
+    dfree(d_masterOccupancyGrid);
+    delete m_colorMLP;
+    delete m_densityMLP;
+    m_colorMLP = nullptr;
+    m_densityMLP = nullptr;
+    m_init = false;
+}
+
+// InstantNerf.cu:282-339
+void InstantNerf::init(const NerfOptions& opts, MemoryMode memMode)
+{
+    freeBuffers();
+    if (memMode != TRAINING) throw std::logic_error("InstantNerf: only TRAINING mode is part of this build");
+    if (opts.batchSize < MAX_HITS)
+        throw std::runtime_error("InstantNerf: batchSize must be >= 1024 (one ray's maximum sample count)");
+    if (opts.rayChunkSize <= 0 || opts.rayChunkSize % 16)
+        throw std::runtime_error("InstantNerf: rayChunkSize must be a positive multiple of 16");
+    if (opts.featuresPerLevel != 2) throw std::runtime_error("InstantNerf: featuresPerLevel must be 2");
+    m_opts = opts;
+    m_memMode = memMode;
+    m_trainSteps = 0;
+
+    const int G = grid_cells(opts);
+    const int N = opts.numCascades * G;
+    const uint32_t S = graft::mip_offset(opts.gridResolution, opts.levelsMipmap);
+    if (G % 32 || S % 32) throw std::runtime_error("InstantNerf: grid cells per cascade must be multiples of 32");
+    m_occupancyBytes = ((size_t)S * opts.numCascades + 7) / 8;
+    d_occupancyGrid = dalloc<uint8_t>(m_occupancyBytes);
+    GRAFT_HIP_CHECK(hipMemset(d_occupancyGrid, 0, m_occupancyBytes));
+    d_masterOccupancyGrid = dalloc<float>((size_t)N);
+    GRAFT_HIP_CHECK(hipMemset(d_masterOccupancyGrid, 0, (size_t)N * sizeof(float)));
+
+    MLPGridOptions dopt{};
+    dopt.vectorDim = 4;
+    dopt.hiddenDim = opts.densityHiddenDim;
+    dopt.outputDim = 16;
+    dopt.numLayers = opts.densityNumLayers;
+    dopt.activationType = ACT_RELU;
+    dopt.tableSize = opts.hashTableSize;
+    dopt.numLevels = opts.numLevels;
+    dopt.b = opts.growthFactor;
+    dopt.lowestSize = opts.baseResolution;
+    dopt.featuresLevel = opts.featuresPerLevel;
+    const int densityInfer = std::max(G, opts.renderBatchSize);
+    m_densityMLP = new TinyMLPHashGrid(dopt, opts.batchSize, densityInfer);
+
+    MLPOption copt{};
+    copt.inputDim = 32;
+    copt.hiddenDim = opts.colorHiddenDim;
+    copt.outputDim = 3;
+    copt.numLayers = opts.colorNumLayers;
+    copt.activationType = ACT_RELU;
+    copt.outputActivation = OUT_ACT_SIGMOID;
+    m_colorMLP = new TinyMLP(copt, opts.batchSize, opts.renderBatchSize);
+
+    m_buf = new NerfBuffers();
+    allocate();
+    m_init = true;
+    earlyOccupancyGridUpdate(0);
+    GRAFT_HIP_CHECK(hipDeviceSynchronize());
+}
+
+void InstantNerf::allocate()
+{
+    NerfBuffers& b = B(m_buf);
+    const size_t R = (size_t)m_opts.rayChunkSize, Bn = (size_t)m_opts.batchSize;
+    const int G = grid_cells(m_opts);
+    const int N = m_opts.numCascades * G;
+    b.d_inv = dalloc<float3>(R);
+    b.nears = dalloc<float>(R);
+    b.fars = dalloc<float>(R);
+    b.counts = dalloc<uint32_t>(R);
+    b.offsets = dalloc<uint32_t>(R);
+    b.block_sums = dalloc<uint32_t>(graft::march_scratch_words((uint32_t)R));
+    b.result = dalloc<uint32_t>(2);
+    GRAFT_HIP_CHECK(hipMemset(b.result, 0, 2 * sizeof(uint32_t)));
+    GRAFT_HIP_CHECK(hipHostMalloc((void**)&b.h_result, 2 * sizeof(uint32_t), hipHostMallocDefault));
+    b.render_rgb = dalloc<float>(3 * R);
+    b.render_depth = dalloc<float>(R);
+    b.phi = dalloc<float>(3 * R);
+    b.weight_sum = dalloc<float>(R);
+    b.positions = dalloc<float4>(Bn);
+    b.ray_idx = dalloc<uint32_t>(Bn);
+    b.t_sorted = dalloc<float>(Bn);
+    b.density_out = dalloc<float>(16 * Bn);
+    b.sigma = dalloc<float>(Bn);
+    b.dw = dalloc<float>(Bn);
+    b.dsigma = dalloc<float>(Bn);
+    b.color_dx = dalloc<__half>(32 * Bn);
+    b.tmp_grid = dalloc<float>((size_t)N);
+    const int halfN = N / 2;
+    b.occ_capacity = std::max(G, halfN / std::max(1, m_opts.numCascades));
+    b.occ_samples = dalloc<float4>((size_t)b.occ_capacity);
+    b.occ_density = dalloc<float>((size_t)b.occ_capacity * 16);
+    b.partials = dalloc<float>(1024);
+    b.sum = dalloc<float>(1);
+    b.active_list = dalloc<int>((size_t)N);
+    b.active_count = dalloc<int>(1);
+    b.list_scratch = dalloc<uint32_t>(graft::occ_list_scratch_words(N));
+    GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_result, hipEventDisableTiming));
+
+    // The color head's activation-0 buffer receives the SH gather output directly.
+    const TinyMLP::Buffers cb = m_colorMLP->buffers();
+    __half* acts0 = nullptr;
+    GRAFT_HIP_CHECK(hipMemcpy(&acts0, cb.activations, sizeof(acts0), hipMemcpyDeviceToHost));
+    b.color_in = acts0;
+    b.meta = graft::make_grid_meta(m_opts.hashTableSize, m_opts.numLevels, m_opts.growthFactor, m_opts.baseResolution);
+}
+
+void InstantNerf::setMemoryMode(MemoryMode mode)
+{
+    if (mode != TRAINING) throw std::logic_error("InstantNerf: only TRAINING mode is part of this build");
+}
+
+// InstantNerf.cu:359-583
+void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_d, const float* d_rays_depth,
+                                   const float* d_rays_sigma, const float* d_rgb_true, uint32_t numRays,
+                                   int& trainStepCount, uint32_t* hitCounts, float* d_rgb_out, hipStream_t stream)
+{
+    if (!m_init) throw std::runtime_error("InstantNerf: init() must be called before trainWithRaysHit()");
+    if (!d_rgb_true) throw std::runtime_error("InstantNerf: trainWithRaysHit needs ground-truth colours");
+    NerfBuffers& b = B(m_buf);
+    const NerfOptions& o = m_opts;
+    const uint32_t Bn = (uint32_t)o.batchSize;
+    const graft::OccGrid g = occ_grid(o, d_occupancyGrid);
+    const uint32_t* d_rays = b.result;       // active rays of this step
+    const uint32_t* d_hits = b.result + 1;   // compacted samples of this step
+
+    const TinyMLPHashGrid::Buffers db = m_densityMLP->buffers();
+    const TinyMLP::Buffers cb = m_colorMLP->buffers();
+    const graft::MlpShape dshape{2 * o.numLevels, db.hw.hiddenDim, db.hw.outputDim, db.hw.numLayers};
+    const graft::MlpShape cshape = shape_of(cb.hw);
+    const int cstride = cb.hw.outputDim;
+
+    auto stage = [&](const char* name, auto&& fn) {
+        if (!o.isProfiling) {
+            fn();
+            return;
+        }
+        StageTimer t{name, nullptr, nullptr};
+        GRAFT_HIP_CHECK(hipEventCreate(&t.a));
+        GRAFT_HIP_CHECK(hipEventCreate(&t.b));
+        GRAFT_HIP_CHECK(hipEventRecord(t.a, stream));
+        fn();
+        GRAFT_HIP_CHECK(hipEventRecord(t.b, stream));
+        b.pending.push_back(t);
+    };
+
+    uint32_t raysDone = 0;
+    int i = 0;
+    while (raysDone < numRays) {
+        const uint32_t R = std::min<uint32_t>((uint32_t)o.rayChunkSize, numRays - raysDone);
+        const float3* co = d_rays_o + raysDone;
+        const float3* cd = d_rays_d + raysDone;
+        const float* cdep = d_rays_depth ? d_rays_depth + raysDone : nullptr;
+        const float* csig = d_rays_sigma ? d_rays_sigma + raysDone : nullptr;
+
+        stage("processRays", [&] {
+            graft::ray_aabb_inv(R, co, cd, o.aabbMin, o.aabbMax, o.numCascades, b.d_inv, b.nears, b.fars, stream);
+            graft::march_hits(R, co, cd, b.d_inv, b.nears, b.fars, g, o.samplesPerVoxel, Bn, b.counts, b.offsets,
+                              b.t_sorted, b.ray_idx, b.positions, graft::MarchScratch{b.block_sums, b.result}, stream);
+        });
+        GRAFT_HIP_CHECK(hipMemcpyAsync(b.h_result, b.result, 2 * sizeof(uint32_t), hipMemcpyDeviceToHost, stream));
+        GRAFT_HIP_CHECK(hipEventRecord(b.ev_result, stream));
+
+        // InstantNerf.cu:488-494: the refresh changes only the grid the next step marches.
+        if (m_trainSteps % 16 == 0) {
+            stage("occupancy", [&] {
+                if (m_trainSteps < 256) earlyOccupancyGridUpdate(stream);
+                else lateOccupancyGridUpdate(stream);
+            });
+        }
+
+        stage("zeroGrad", [&] {
+            m_densityMLP->zero_grad(stream);
+            m_colorMLP->zero_grad(stream);
+        });
+
+        stage("densityFwd", [&] {
+            graft::FwdInput in;
+            in.pos = reinterpret_cast<const float*>(b.positions);
+            in.pos_stride = 4;
+            in.table = db.fwd_hashtable;
+            in.meta = &b.meta;
+            graft::mlp_forward(dshape, in, db.fwd_weights, db.master_biases, db.activations, b.density_out, (int)Bn,
+                               OUT_ACT_NONE, stream, d_hits);
+        });
+        stage("computeSH", [&] {
+            graft::sh_gather(cd, b.ray_idx, d_hits, Bn, o.densityBias, b.density_out, b.color_in, b.sigma, stream);
+        });
+        stage("colorFwd", [&] {
+            graft::FwdInput in;
+            in.x = b.color_in;
+            graft::mlp_forward(cshape, in, cb.fwd_weights, cb.master_biases, cb.activations, cb.padded_outputs,
+                               (int)Bn, cb.hw.outputActivation, stream, d_hits);
+        });
+
+        float* final_rgb = d_rgb_out ? d_rgb_out + (size_t)raysDone * 3 : b.render_rgb;
+        stage("volumeRendering", [&] {
+            graft::CompositeArgs ca{};
+            ca.offsets = b.offsets;
+            ca.counts = b.counts;
+            ca.t = b.t_sorted;
+            ca.sigma = b.sigma;
+            ca.depth_prior = cdep;
+            ca.sigma_prior = csig;
+            ca.rgb = cb.padded_outputs;
+            ca.rgb_stride = cstride;
+            ca.rgb_true = d_rgb_true + (size_t)raysDone * 3;
+            ca.final_rgb = final_rgb;
+            ca.final_depth = b.render_depth;
+            ca.phi = b.phi;
+            ca.dw = b.dw;
+            ca.weight_sum = b.weight_sum;
+            ca.lambda_dist = o.lambdaDist;
+            ca.lambda_depth = o.lambdaDepth;
+            ca.bg = o.bgColor;
+            graft::composite(ca, d_rays, R, stream);
+        });
+        stage("colorGrad", [&] {
+            graft::ColorGradArgs ga{};
+            ga.initial_offset = 0;
+            ga.counts = b.counts;
+            ga.offsets = b.offsets;
+            ga.t = b.t_sorted;
+            ga.density_out = b.density_out;
+            ga.color_out = cb.padded_outputs;
+            ga.color_stride = cstride;
+            ga.phi = b.phi;
+            ga.final_rgb = final_rgb;
+            ga.dw = b.dw;
+            ga.weight_sum = b.weight_sum;
+            ga.color_grad = cb.dloss;
+            ga.grad_stride = cstride;
+            ga.dsigma = b.dsigma;
+            ga.loss_scale = o.lossScale;
+            ga.bias = o.densityBias;
+            ga.total_rays = numRays;
+            graft::color_grad(ga, d_rays, R, stream);
+        });
+        stage("colorBwd", [&] {
+            graft::mlp_backward(cshape, cb.dloss, cb.activations, cb.fwd_weights, cb.w_grad, cb.b_grad, b.color_dx,
+                                (int)Bn, stream, d_hits);
+        });
+        stage("densityGrad", [&] { graft::density_grad(d_hits, Bn, b.dsigma, b.color_dx, db.dloss, stream); });
+        stage("densityBwd", [&] {
+            graft::mlp_backward(dshape, db.dloss, db.activations, db.fwd_weights, db.w_grad, db.b_grad, db.dx_out,
+                                (int)Bn, stream, d_hits);
+            graft::hash_scatter(b.meta, db.dx_out, reinterpret_cast<const float*>(b.positions), 4, db.hashtable_grads,
+                                (int)Bn, stream, d_hits);
+        });
+        stage("colorOpt", [&] {
+            m_colorMLP->step(o.learningRate, o.beta1, o.beta2, o.epsilon, o.lossScale, stream);
+        });
+        stage("densityOpt", [&] {
+            m_densityMLP->step(o.learningRate, o.beta1, o.beta2, o.epsilon, o.lossScale, stream);
+        });
+
+        trainStepCount++;
+        m_trainSteps++;
+
+        // The only host read of the step: its active-ray count, to advance the cursor.
+        GRAFT_HIP_CHECK(hipEventSynchronize(b.ev_result));
+        const uint32_t active = b.h_result[0], hits = b.h_result[1];
+        if (active == 0) throw std::runtime_error("InstantNerf: no ray fits the batch");
+        if (hitCounts) hitCounts[i] = hits;
+        raysDone += active;
+        i++;
+    }
+
+    if (o.isProfiling && !b.pending.empty()) {
+        GRAFT_HIP_CHECK(hipEventSynchronize(b.pending.back().b));
+        for (auto& t : b.pending) {
+            float ms = 0.f;
+            GRAFT_HIP_CHECK(hipEventElapsedTime(&ms, t.a, t.b));
+            auto& s = b.stats[t.name];
+            s.first += ms;
+            s.second += 1;
+            (void)hipEventDestroy(t.a);
+            (void)hipEventDestroy(t.b);
+        }
+        b.pending.clear();
+    }
+}
+
+// InstantNerf.cu:82-148 (flat table instead of the reference's tree).
+void InstantNerf::printStats()
+{
+    if (!m_buf) return;
+    NerfBuffers& b = B(m_buf);
+    std::printf("%-18s %10s %8s\n", "stage", "mean ms", "calls");
+    for (const auto& kv : b.stats)
+        std::printf("%-18s %10.4f %8ld\n", kv.first.c_str(), kv.second.first / std::max(1L, kv.second.second),
+                    kv.second.second);
+}
+
+void InstantNerf::resetStats()
+{
+    if (m_buf) B(m_buf).stats.clear();
+}
+
+void InstantNerf::updateOccupancy(hipStream_t stream)
+{
+    if (!m_init) throw std::runtime_error("InstantNerf: init() first");
+    if (m_trainSteps < 256) earlyOccupancyGridUpdate(stream);
+    else lateOccupancyGridUpdate(stream);
+}
+
+// InstantNerf.cu:1108-1171: one jittered sample per cell of every cascade.
+void InstantNerf::earlyOccupancyGridUpdate(hipStream_t stream)
+{
+    NerfBuffers& b = B(m_buf);
+    const int G = grid_cells(m_opts);
+    const int N = m_opts.numCascades * G;
+    const TinyMLPHashGrid::Buffers db = m_densityMLP->buffers();
+    const graft::MlpShape dshape{2 * m_opts.numLevels, db.hw.hiddenDim, db.hw.outputDim, db.hw.numLayers};
+    GRAFT_HIP_CHECK(hipMemsetAsync(b.tmp_grid, 0, (size_t)N * sizeof(float), stream));
+    for (int c = 0; c < m_opts.numCascades; ++c) {
+        graft::occ_sample(b.occ_samples, G, graft::kSampleEveryCell, G, c * G, nullptr, nullptr,
+                          (uint64_t)m_trainSteps + (uint64_t)c, m_opts.gridResolution, m_opts.aabbMin, m_opts.aabbMax,
+                          stream);
+        graft::FwdInput in;
+        in.pos = reinterpret_cast<const float*>(b.occ_samples);
+        in.pos_stride = 4;
+        in.table = db.fwd_hashtable;
+        in.meta = &b.meta;
+        graft::mlp_forward(dshape, in, db.fwd_weights, db.master_biases, nullptr, b.occ_density, G, OUT_ACT_NONE,
+                           stream);
+        graft::occ_tmp_max(b.occ_samples, b.occ_density, b.tmp_grid, m_opts.densityBias, G, stream);
+    }
+    finishOccupancyUpdate(stream);
+}
+
+// InstantNerf.cu:1009-1106: half the cells' worth of samples, per cascade
+// chunk half from occupied cells and half uniform over all cells.
+void InstantNerf::lateOccupancyGridUpdate(hipStream_t stream)
+{
+    NerfBuffers& b = B(m_buf);
+    const int G = grid_cells(m_opts);
+    const int N = m_opts.numCascades * G;
+    const int S = (int)graft::mip_offset(m_opts.gridResolution, m_opts.levelsMipmap);
+    const TinyMLPHashGrid::Buffers db = m_densityMLP->buffers();
+    const graft::MlpShape dshape{2 * m_opts.numLevels, db.hw.hiddenDim, db.hw.outputDim, db.hw.numLayers};
+    GRAFT_HIP_CHECK(hipMemsetAsync(b.tmp_grid, 0, (size_t)N * sizeof(float), stream));
+    graft::occ_active_list(d_occupancyGrid, N, G, S, b.active_list, b.active_count, b.list_scratch, stream);
+    const int chunks = m_opts.numCascades;
+    const int perChunk = (N / 2) / chunks;
+    const int occPer = perChunk / 2;
+    const int uniPer = perChunk - occPer;
+    for (int ch = 0; ch < chunks; ++ch) {
+        const uint64_t seed = (uint64_t)m_trainSteps * (2ULL * chunks) + 2ULL * ch;
+        graft::occ_sample(b.occ_samples, occPer, graft::kSampleFromList, 0, 0, b.active_list, b.active_count, seed,
+                          m_opts.gridResolution, m_opts.aabbMin, m_opts.aabbMax, stream);
+        graft::occ_sample(b.occ_samples + occPer, uniPer, graft::kSampleRandomCell, N, 0, nullptr, nullptr, seed + 1,
+                          m_opts.gridResolution, m_opts.aabbMin, m_opts.aabbMax, stream);
+        const int cnt = occPer + uniPer;
+        graft::FwdInput in;
+        in.pos = reinterpret_cast<const float*>(b.occ_samples);
+        in.pos_stride = 4;
+        in.table = db.fwd_hashtable;
+        in.meta = &b.meta;
+        graft::mlp_forward(dshape, in, db.fwd_weights, db.master_biases, nullptr, b.occ_density, cnt, OUT_ACT_NONE,
+                           stream);
+        graft::occ_tmp_max(b.occ_samples, b.occ_density, b.tmp_grid, m_opts.densityBias, cnt, stream);
+    }
+    finishOccupancyUpdate(stream);
+}
+
+// EMA-max into the master grid, mean, level-0 bits, mip pyramid (InstantNerf.cu:1150-1171).
+void InstantNerf::finishOccupancyUpdate(hipStream_t stream)
+{
+    NerfBuffers& b = B(m_buf);
+    const int G = grid_cells(m_opts);
+    const int N = m_opts.numCascades * G;
+    const int S = (int)graft::mip_offset(m_opts.gridResolution, m_opts.levelsMipmap);
+    graft::update_master_grid(b.tmp_grid, d_masterOccupancyGrid, m_opts.decayValue, (uint32_t)N, stream);
+    graft::reduce_sum(d_masterOccupancyGrid, (uint32_t)N, b.partials, b.sum, stream);
+    const float base_voxel = (m_opts.aabbMax.x - m_opts.aabbMin.x) / (float)m_opts.gridResolution.x;
+    graft::update_occupancy_bits(reinterpret_cast<uint32_t*>(d_occupancyGrid), d_masterOccupancyGrid, b.sum, N, G, S,
+                                 m_opts.minDensityThreshold, base_voxel, stream);
+    graft::build_mipmaps(d_occupancyGrid, m_opts.gridResolution, m_opts.levelsMipmap, m_opts.numCascades, stream);
+}
+
+void InstantNerf::setOccupancyBits(const uint8_t* host_bits)
+{
+    if (!m_init) throw std::runtime_error("InstantNerf: init() first");
+    GRAFT_HIP_CHECK(hipMemcpy(d_occupancyGrid, host_bits, m_occupancyBytes, hipMemcpyHostToDevice));
+}
+
+InstantNerf::StepBuffers InstantNerf::stepBuffers() const
+{
+    if (!m_buf) throw std::runtime_error("InstantNerf: init() first");
+    const NerfBuffers& b = *static_cast<const NerfBuffers*>(m_buf);
+    StepBuffers s{};
+    s.num_steps = b.counts;
+    s.ray_offsets = b.offsets;
+    s.positions = b.positions;
+    s.ray_indices = b.ray_idx;
+    s.t_sorted = b.t_sorted;
+    s.density_out = b.density_out;
+    s.color_input = b.color_in;
+    s.color_output = m_colorMLP->buffers().padded_outputs;
+    s.sigma = b.sigma;
+    s.render_rgb = b.render_rgb;
+    s.phi = b.phi;
+    s.dw = b.dw;
+    s.weight_sum = b.weight_sum;
+    s.dsigma = b.dsigma;
+    s.color_dx = b.color_dx;
+    s.density_grad = m_densityMLP->buffers().dloss;
+    s.result = b.result;
+    s.trainSteps = m_trainSteps;
+    return s;
+}
+
+// ---- not part of this build (render and file paths) ----
+void InstantNerf::renderImage(const float3*, const float3*, uint32_t, float*, hipStream_t)
+{
+    throw std::logic_error("InstantNerf::renderImage is not part of this build");
+}
+void InstantNerf::renderImageHit(const float3*, const float3*, uint32_t, float*, hipStream_t)
+{
+    throw std::logic_error("InstantNerf::renderImageHit is not part of this build");
+}
+void InstantNerf::queryOccupancyGrid(const float*, int, uint32_t*, float, hipStream_t)
+{
+    throw std::logic_error("InstantNerf::queryOccupancyGrid is not part of this build");
+}
+void InstantNerf::queryDensityLogit(const float*, int, float*, hipStream_t)
+{
+    throw std::logic_error("InstantNerf::queryDensityLogit is not part of this build");
+}
+void InstantNerf::queryRadiance(const float*, int, float3, float*, hipStream_t)
+{
+    throw std::logic_error("InstantNerf::queryRadiance is not part of this build");
+}
+void InstantNerf::buildOccupancyBitgrid(uint8_t*, float, hipStream_t)
+{
+    throw std::logic_error("InstantNerf::buildOccupancyBitgrid is not part of this build");
+}
+void InstantNerf::save(const std::string&) { throw std::logic_error("InstantNerf::save is not part of this build"); }
+void InstantNerf::load(const std::string&) { throw std::logic_error("InstantNerf::load is not part of this build"); }

@@ -29,14 +29,16 @@ struct FwdInput {
 
 // W, B, acts are DEVICE arrays of per-layer device pointers.  acts == nullptr
 // selects the inference kernel (no activation saves).
+// d_n (nullable): device-side sample count; the kernels then process
+// min(*d_n, N) samples, N being the host upper bound the launch is sized for.
 void mlp_forward(const MlpShape& s, const FwdInput& in, const __half* const* W,
                  const float* const* B, __half* const* acts, float* out, int N, int out_act,
-                 hipStream_t stream);
+                 hipStream_t stream, const uint32_t* d_n = nullptr);
 
 // dW/dB (device arrays of per-layer pointers) are accumulated (+=); dx may be
 // nullptr (then layer 0's dX is skipped).
 void mlp_backward(const MlpShape& s, const __half* dy, const __half* const* acts,
                   const __half* const* W, float* const* dW, float* const* dB, __half* dx, int N,
-                  hipStream_t stream);
+                  hipStream_t stream, const uint32_t* d_n = nullptr);
 
 }  // namespace graft

@@ -42,6 +42,7 @@ struct FwdParams {
     const _Float16* const* W;     // device array, W_l row-major [out_l][in_l]
     const float* const* B;        // device array, b_l [out_l]
     float* out;                   // [N x out]
+    const uint32_t* d_n;          // nullable device-side sample count (<= N)
     int N, in, hid, out_dim, layers, pos_stride, save_x0;
     int frag_off[kMaxLayers];     // in halves
     int bias_off[kMaxLayers];     // in floats from bias_base
@@ -86,7 +87,8 @@ __global__ __launch_bounds__(256) void mlp_fwd_kernel(const FwdParams p)
 
     constexpr int NT = MAXD / 16;
     const int lane = tid & 63, wave = tid >> 6, r = lane & 15, g = lane >> 4;
-    const int ntiles = (p.N + 15) >> 4;
+    const int N = p.d_n ? min((int)*p.d_n, p.N) : p.N;
+    const int ntiles = (N + 15) >> 4;
     const int KS0 = tiles16(p.in);
     const uint32_t mask = (uint32_t)p.T - 1u;
     _Float16* act0 = nullptr;
@@ -94,7 +96,7 @@ __global__ __launch_bounds__(256) void mlp_fwd_kernel(const FwdParams p)
 
     for (int tile = blockIdx.x * 4 + wave; tile < ntiles; tile += gridDim.x * 4) {
         const int n = tile * 16 + r;
-        const bool valid = n < p.N;
+        const bool valid = n < N;
         h4 X[NT];
         if constexpr (HASH) {
             float px = 0.f, py = 0.f, pz = 0.f;
@@ -203,6 +205,7 @@ struct BwdParams {
     const _Float16* const* W;       // device array
     float* ws;                      // [gridDim.x][P] partial dW (all layers) then db
     _Float16* dx;                   // nullable [N x in]
+    const uint32_t* d_n;            // nullable device-side sample count (<= N)
     int N, in, hid, out_dim, layers;
     int fragT_off[kMaxLayers];      // halves
     int wofs[kMaxLayers], bofs[kMaxLayers];
@@ -240,8 +243,10 @@ __global__ __launch_bounds__(256) void mlp_bwd_kernel(const BwdParams p)
     constexpr int NT = MAXD / 16;
     constexpr int TPW = kBwdTilesPerWave;
     const int lane = tid & 63, wave = tid >> 6, r = lane & 15, g = lane >> 4;
+    const int N = p.d_n ? min((int)*p.d_n, p.N) : p.N;
+    const int nchunks = (N + kBwdChunk - 1) / kBwdChunk;
 
-    for (int chunk = blockIdx.x; chunk < p.nchunks; chunk += gridDim.x) {
+    for (int chunk = blockIdx.x; chunk < nchunks; chunk += gridDim.x) {
         const int s0 = chunk * kBwdChunk;
         h4 G[TPW][NT];
         {
@@ -252,7 +257,7 @@ __global__ __launch_bounds__(256) void mlp_bwd_kernel(const BwdParams p)
 #pragma unroll
                 for (int ks = 0; ks < NT; ks++) {
                     const int col = 16 * ks + 4 * g;
-                    G[t][ks] = (n < p.N && ks < KSo && col < p.out_dim)
+                    G[t][ks] = (n < N && ks < KSo && col < p.out_dim)
                                    ? ld_h4(p.dy + (size_t)n * p.out_dim + col)
                                    : h4zero();
                 }
@@ -274,7 +279,7 @@ __global__ __launch_bounds__(256) void mlp_bwd_kernel(const BwdParams p)
 #pragma unroll
                 for (int mt = 0; mt < NT; mt++) {
                     const int col = 16 * mt + 4 * g;
-                    X[t][mt] = (n < p.N && mt < MTi && col < in_l) ? ld_h4(xl + (size_t)n * in_l + col) : h4zero();
+                    X[t][mt] = (n < N && mt < MTi && col < in_l) ? ld_h4(xl + (size_t)n * in_l + col) : h4zero();
                     if (mt < MTi) {
 #pragma unroll
                         for (int j = 0; j < 4; j++) Xt[(col + j) * kBwdPitch + sl] = X[t][mt][j];
@@ -315,7 +320,7 @@ __global__ __launch_bounds__(256) void mlp_bwd_kernel(const BwdParams p)
                                     if (!((float)X[t][mt][j] > 0.f)) h[j] = (_Float16)0.f;
                             } else {
                                 const int col = 16 * mt + 4 * g;
-                                if (n < p.N && col < in_l) st_h4(p.dx + (size_t)n * in_l + col, h);
+                                if (n < N && col < in_l) st_h4(p.dx + (size_t)n * in_l + col, h);
                             }
                             Gn[mt] = h;
                         }
@@ -440,7 +445,7 @@ static void fill_layer_offsets(const MlpShape& s, bool transposed, int* frag_off
 
 void mlp_forward(const MlpShape& s, const FwdInput& in, const __half* const* W,
                  const float* const* B, __half* const* acts, float* out, int N, int out_act,
-                 hipStream_t stream)
+                 hipStream_t stream, const uint32_t* d_n)
 {
     s.validate();
     if (N <= 0) return;
@@ -453,6 +458,7 @@ void mlp_forward(const MlpShape& s, const FwdInput& in, const __half* const* W,
     p.W = reinterpret_cast<const _Float16* const*>(W);
     p.B = B;
     p.out = out;
+    p.d_n = d_n;
     p.N = N;
     p.in = s.in;
     p.hid = s.hid;
@@ -508,7 +514,7 @@ void mlp_forward(const MlpShape& s, const FwdInput& in, const __half* const* W,
 
 void mlp_backward(const MlpShape& s, const __half* dy, const __half* const* acts,
                   const __half* const* W, float* const* dW, float* const* dB, __half* dx, int N,
-                  hipStream_t stream)
+                  hipStream_t stream, const uint32_t* d_n)
 {
     s.validate();
     if (N <= 0) return;
@@ -517,6 +523,7 @@ void mlp_backward(const MlpShape& s, const __half* dy, const __half* const* acts
     p.acts = reinterpret_cast<const _Float16* const*>(acts);
     p.W = reinterpret_cast<const _Float16* const*>(W);
     p.dx = reinterpret_cast<_Float16*>(dx);
+    p.d_n = d_n;
     p.N = N;
     p.in = s.in;
     p.hid = s.hid;

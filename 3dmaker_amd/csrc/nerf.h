@@ -1,0 +1,103 @@
+// Internal interface of the NeRF-side kernels (raymarch.hip, render.hip).
+//
+// Counts that the previous kernel produced on the device (active rays,
+// compacted samples) are passed as `const uint32_t* d_n` next to a host upper
+// bound `n_max`: a kernel processes min(*d_n, n_max) items when d_n is set and
+// n_max otherwise, so a training step never has to read a count back to the
+// host to size its launches.
+#pragma once
+
+#include "common.h"
+
+namespace graft {
+
+struct OccGrid {
+    const uint8_t* bits;   // [C * S] bits, LSB-first, per cascade a mip pyramid
+    uint3 res;             // level-0 resolution
+    float3 aabb_min, aabb_max;
+    int cascades, mip_levels;
+};
+
+// compute_ray_aabb_inv_kernel (otherKernels.cu:91-154).
+void ray_aabb_inv(uint32_t R, const float3* o, const float3* d, float3 aabb_min, float3 aabb_max, int cascades,
+                  float3* d_inv, float* nears, float* fars, hipStream_t s);
+
+// Device scratch of one compaction: per-256-ray block sums and result[2] =
+// {active rays, compacted samples}.
+struct MarchScratch {
+    uint32_t* block_sums;  // >= ceil(R / 256)
+    uint32_t* result;      // [2]
+};
+size_t march_scratch_words(uint32_t R);
+
+// processRaysHitLinear (processRays.cu:931-1040) without host round trips:
+// count pass, block-sum scan + cutoff (one workgroup), fill pass.  counts and
+// offsets [R]; t_out, ray_idx, pos_out [batch].  Results stay on the device in
+// scratch.result.
+void march_hits(uint32_t R, const float3* o, const float3* d, const float3* d_inv, const float* nears,
+                const float* fars, const OccGrid& g, int K, uint32_t batch, uint32_t* counts, uint32_t* offsets,
+                float* t_out, uint32_t* ray_idx, float4* pos_out, const MarchScratch& scratch, hipStream_t s);
+
+// Count pass only (march_rays_dda_calc_hits, processRays.cu:626-737).
+void march_count(uint32_t R, const float3* o, const float3* d, const float3* d_inv, const float* nears,
+                 const float* fars, const OccGrid& g, int K, uint32_t* counts, hipStream_t s);
+
+// compute_SH_gather (otherKernels.cu:156-273).
+void sh_gather(const float3* dirs, const uint32_t* ray_idx, const uint32_t* d_n, uint32_t n_max, float bias,
+               const float* density_out, __half* color_in, float* sigma, hipStream_t s);
+
+// render_rays_distortion_kernel (compositing.cu:84-213).
+struct CompositeArgs {
+    const uint32_t* offsets;
+    const uint32_t* counts;
+    const float* t;
+    const float* sigma;
+    const float* depth_prior;   // nullable
+    const float* sigma_prior;   // nullable
+    const float* rgb;           // [N x rgb_stride], rgb in the first 3 columns
+    int rgb_stride;             // 3 in the reference layout
+    const float* rgb_true;      // nullable
+    float* final_rgb;
+    float* final_depth;
+    float* phi;                 // nullable
+    float* dw;
+    float* weight_sum;
+    float lambda_dist, lambda_depth;
+    float3 bg;
+};
+void composite(const CompositeArgs& a, const uint32_t* d_rays, uint32_t rays_max, hipStream_t s);
+
+// compute_color_grad (otherKernels.cu:303-409).
+struct ColorGradArgs {
+    uint32_t initial_offset;
+    const uint32_t* counts;
+    const uint32_t* offsets;
+    const float* t;
+    const float* density_out;
+    const float* color_out;     // [N x color_stride]
+    int color_stride;           // 3 in the reference layout
+    const float* phi;
+    const float* final_rgb;
+    const float* dw;
+    const float* weight_sum;
+    __half* color_grad;         // [N x grad_stride]: 3 gradients, then zeros
+    int grad_stride;            // 3 in the reference layout
+    float* dsigma;
+    float loss_scale, bias;
+    uint32_t total_rays;
+};
+void color_grad(const ColorGradArgs& a, const uint32_t* d_rays, uint32_t rays_max, hipStream_t s);
+
+// compute_density_grad (otherKernels.cu:506-562).
+void density_grad(const uint32_t* d_n, uint32_t n_max, const float* dsigma, const __half* color_dx,
+                  __half* density_grad, hipStream_t s);
+
+// Occupancy (otherKernels.cu:677-807; InstantNerf.cu:1177-1204).
+void update_master_grid(const float* tmp, float* master, float decay, uint32_t n, hipStream_t s);
+// out[0] = sum of in[0..n) in a fixed order (two passes, partials in scratch [>= 1024 floats]).
+void reduce_sum(const float* in, uint32_t n, float* partials, float* out, hipStream_t s);
+void update_occupancy_bits(uint32_t* bits32, const float* master, const float* d_sum, int total, int G, int S,
+                           float min_optical, float base_voxel, hipStream_t s);
+void build_mipmaps(uint8_t* bits, uint3 res, int mip_levels, int cascades, hipStream_t s);
+
+}  // namespace graft

@@ -1,0 +1,347 @@
+// extern "C" surface of the NeRF side: the reference's launchers
+// (modules/NeRF/InstantNerf.h:385-568), launchers for the kernels the
+// reference launches inline, and the flat handle API over InstantNerf.
+// Exceptions never cross this boundary (abi_error.h).
+#include "InstantNerf.h"
+#include "nerf_abi.h"
+#include "nerf_capi.h"
+
+#include "abi_error.h"
+#include "capi_handles.h"
+#include "nerf.h"
+#include "nerf_math.h"
+#include "occupancy.h"
+
+#include <cstddef>
+#include <cstring>
+#include <mutex>
+
+using graft::guarded;
+
+static_assert(sizeof(InerfOptions) == sizeof(NerfOptions), "InerfOptions must mirror NerfOptions");
+static_assert(offsetof(InerfOptions, levelsMipmap) == offsetof(NerfOptions, levelsMipmap), "layout");
+static_assert(offsetof(InerfOptions, growthFactor) == offsetof(NerfOptions, growthFactor), "layout");
+static_assert(offsetof(InerfOptions, lossScale) == offsetof(NerfOptions, lossScale), "layout");
+static_assert(offsetof(InerfOptions, bgColor) == offsetof(NerfOptions, bgColor), "layout");
+static_assert(offsetof(InerfOptions, densityBias) == offsetof(NerfOptions, densityBias), "layout");
+static_assert(offsetof(InerfOptions, isProfiling) == offsetof(NerfOptions, isProfiling), "layout");
+
+namespace {
+
+// Library-owned compaction scratch for processRaysHitLinear callers that pass
+// no block-sum buffer (grown on demand, one per process, single stream).
+std::mutex g_mu;
+uint32_t* g_scratch = nullptr;
+size_t g_scratch_words = 0;
+
+uint32_t* march_scratch(size_t words)
+{
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (words > g_scratch_words) {
+        if (g_scratch) GRAFT_HIP_CHECK(hipFree(g_scratch));
+        g_scratch = nullptr;
+        GRAFT_HIP_CHECK(hipMalloc(&g_scratch, words * sizeof(uint32_t)));
+        g_scratch_words = words;
+    }
+    return g_scratch;
+}
+
+float* reduce_partials()
+{
+    static float* p = nullptr;
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!p) GRAFT_HIP_CHECK(hipMalloc(&p, 1024 * sizeof(float)));
+    return p;
+}
+
+}  // namespace
+
+struct Inerf {
+    InstantNerf nerf;
+    TmlpGrid density{nullptr, false};
+    TmlpNet color{nullptr, false};
+};
+
+extern "C" {
+
+int processRaysHitLinear(const uint32_t num_rays, const float3* rays_o, const float3* rays_d,
+                         const float3* rays_d_inv, const float* nears, const float* fars,
+                         const uint8_t* occupancy_grid, const uint3 grid_resolution, const float3 aabb_min,
+                         const float3 aabb_max, const int numCascades, const int mipmapLevels,
+                         const int samplesPerVoxel, const int batchSize, uint32_t* totalHits,
+                         uint32_t* d_active_rays_count, uint32_t* d_num_steps, uint32_t* d_ray_offsets,
+                         float* d_mlp_positions_batch, uint32_t* d_ray_indices, float* d_t_sorted,
+                         uint32_t* d_block_sums, hipStream_t stream)
+{
+    int active = 0;
+    guarded("processRaysHitLinear", [&] {
+        if (batchSize < 0) throw std::runtime_error("batchSize must be >= 0");
+        graft::OccGrid g{};
+        g.bits = occupancy_grid;
+        g.res = grid_resolution;
+        g.aabb_min = aabb_min;
+        g.aabb_max = aabb_max;
+        g.cascades = numCascades;
+        g.mip_levels = mipmapLevels;
+        const size_t words = graft::march_scratch_words(num_rays);
+        (void)d_block_sums;  // sized (R + 1023) / 1024 by reference callers: too small, not used
+        uint32_t* sc = march_scratch(words);
+        graft::MarchScratch ms{sc, sc + (words - 2)};
+        graft::march_hits(num_rays, rays_o, rays_d, rays_d_inv, nears, fars, g, samplesPerVoxel, (uint32_t)batchSize,
+                          d_num_steps, d_ray_offsets, d_t_sorted, d_ray_indices,
+                          reinterpret_cast<float4*>(d_mlp_positions_batch), ms, stream);
+        uint32_t h[2] = {0, 0};
+        GRAFT_HIP_CHECK(hipMemcpyAsync(h, ms.result, sizeof(h), hipMemcpyDeviceToHost, stream));
+        GRAFT_HIP_CHECK(hipStreamSynchronize(stream));
+        if (d_active_rays_count)
+            GRAFT_HIP_CHECK(hipMemcpy(d_active_rays_count, &h[0], sizeof(uint32_t), hipMemcpyHostToDevice));
+        if (totalHits) *totalHits = h[1];
+        active = (int)h[0];
+    });
+    return active;
+}
+
+void launchVolumeRendering(const uint32_t num_rays, const uint32_t* d_ray_offsets, const uint32_t* d_num_steps,
+                           const float* d_t_sorted, const float* d_density_sigma, const float* d_depth_chunk,
+                           const float* d_sigma_chunk, const float* d_rgb_output, const float* d_rgb_true,
+                           float* d_render_rgb, float* d_render_depth, float* d_phi_out, float* d_dw_out,
+                           float* d_weight_sum, float lambda_dist, float lambda_depth, float3 bg_color,
+                           uint32_t base, uint32_t raysDone, hipStream_t stream)
+{
+    guarded("launchVolumeRendering", [&] {
+        (void)base;
+        (void)raysDone;
+        if (!d_dw_out)
+            throw std::logic_error("inference compositing (d_dw_out == NULL) is not part of this build");
+        graft::CompositeArgs a{};
+        a.offsets = d_ray_offsets;
+        a.counts = d_num_steps;
+        a.t = d_t_sorted;
+        a.sigma = d_density_sigma;
+        a.depth_prior = d_depth_chunk;
+        a.sigma_prior = d_sigma_chunk;
+        a.rgb = d_rgb_output;
+        a.rgb_stride = 3;
+        a.rgb_true = d_rgb_true;
+        a.final_rgb = d_render_rgb;
+        a.final_depth = d_render_depth;
+        a.phi = d_phi_out;
+        a.dw = d_dw_out;
+        a.weight_sum = d_weight_sum;
+        a.lambda_dist = lambda_dist;
+        a.lambda_depth = lambda_depth;
+        a.bg = bg_color;
+        graft::composite(a, nullptr, num_rays, stream);
+    });
+}
+
+void launchComputeRayAabbInv(uint32_t num_rays, const float3* rays_o, const float3* rays_d, float3 aabb_min,
+                             float3 aabb_max, int num_cascades, float3* rays_d_inv, float* nears, float* fars,
+                             hipStream_t stream)
+{
+    guarded("launchComputeRayAabbInv", [&] {
+        graft::ray_aabb_inv(num_rays, rays_o, rays_d, aabb_min, aabb_max, num_cascades, rays_d_inv, nears, fars,
+                            stream);
+    });
+}
+
+void launchComputeSHGather(const float3* d_chunk_d, const uint32_t* d_ray_indices, int offset, int batchSize,
+                           float densityBias, float* d_density_out, GRAFT_HALF* d_color_in, float* d_density_sigma,
+                           hipStream_t stream)
+{
+    guarded("launchComputeSHGather", [&] {
+        if (batchSize < 0 || offset < 0) throw std::runtime_error("negative size");
+        graft::sh_gather(d_chunk_d, d_ray_indices + offset, nullptr, (uint32_t)batchSize, densityBias, d_density_out,
+                         d_color_in, d_density_sigma, stream);
+    });
+}
+
+void launchComputeColorGrad(uint32_t numRays, uint32_t initialOffset, const uint32_t* num_steps,
+                            const uint32_t* ray_offsets, const float* t_sorted, const float* density_mlp_out,
+                            const float* color_mlp_out, const float* phi_chunk, const float* final_rgb,
+                            const float* dw_out, const float* weight_sum, GRAFT_HALF* custom_color_grad,
+                            float* tmp_dsigma, float loss_scale, float densityBias, uint32_t totalRaysBatch,
+                            hipStream_t stream)
+{
+    guarded("launchComputeColorGrad", [&] {
+        graft::ColorGradArgs a{};
+        a.initial_offset = initialOffset;
+        a.counts = num_steps;
+        a.offsets = ray_offsets;
+        a.t = t_sorted;
+        a.density_out = density_mlp_out;
+        a.color_out = color_mlp_out;
+        a.color_stride = 3;
+        a.phi = phi_chunk;
+        a.final_rgb = final_rgb;
+        a.dw = dw_out;
+        a.weight_sum = weight_sum;
+        a.color_grad = custom_color_grad;
+        a.grad_stride = 3;
+        a.dsigma = tmp_dsigma;
+        a.loss_scale = loss_scale;
+        a.bias = densityBias;
+        a.total_rays = totalRaysBatch;
+        graft::color_grad(a, nullptr, numRays, stream);
+    });
+}
+
+void launchComputeDensityGrad(uint32_t batch_size, const float* tmp_dsigma, const GRAFT_HALF* custom_dx_out,
+                              GRAFT_HALF* custom_density_grad, hipStream_t stream)
+{
+    guarded("launchComputeDensityGrad", [&] {
+        graft::density_grad(nullptr, batch_size, tmp_dsigma, custom_dx_out, custom_density_grad, stream);
+    });
+}
+
+void launchUpdateMasterGrid(const float* tmpGrid, float* masterGrid, float decayValue, int N, hipStream_t stream)
+{
+    guarded("launchUpdateMasterGrid", [&] {
+        if (N < 0) throw std::runtime_error("negative size");
+        graft::update_master_grid(tmpGrid, masterGrid, decayValue, (uint32_t)N, stream);
+    });
+}
+
+void launchReduceSum(const float* d_in, int n, float* d_out, hipStream_t stream)
+{
+    guarded("launchReduceSum", [&] {
+        if (n < 0) throw std::runtime_error("negative size");
+        graft::reduce_sum(d_in, (uint32_t)n, reduce_partials(), d_out, stream);
+    });
+}
+
+void launchUpdateOccupancyGrid(uint32_t* d_occupancy_grid, const float* d_master_grid, const float* d_sum,
+                               int total_cells, int cells_per_cascade, int pyramid_cells_per_cascade,
+                               float min_optical_thickness, float base_voxel, hipStream_t stream)
+{
+    guarded("launchUpdateOccupancyGrid", [&] {
+        graft::update_occupancy_bits(d_occupancy_grid, d_master_grid, d_sum, total_cells, cells_per_cascade,
+                                     pyramid_cells_per_cascade, min_optical_thickness, base_voxel, stream);
+    });
+}
+
+void launchBuildMipmaps(uint8_t* d_grid, uint3 grid_resolution, int mipmapLevels, int numCascades,
+                        hipStream_t stream)
+{
+    guarded("launchBuildMipmaps",
+            [&] { graft::build_mipmaps(d_grid, grid_resolution, mipmapLevels, numCascades, stream); });
+}
+
+void nerf_abi_echo_vec(float3 a, uint3 b, float* out)
+{
+    out[0] = a.x;
+    out[1] = a.y;
+    out[2] = a.z;
+    out[3] = (float)b.x;
+    out[4] = (float)b.y;
+    out[5] = (float)b.z;
+}
+
+// ---- flat handle API ----
+
+void inerf_default_options(InerfOptions* out)
+{
+    const NerfOptions d{};
+    std::memcpy(out, &d, sizeof(d));
+}
+
+size_t inerf_options_size(void) { return sizeof(NerfOptions); }
+
+Inerf* inerf_create(const InerfOptions* opts)
+{
+    Inerf* h = nullptr;
+    guarded("inerf_create", [&] {
+        NerfOptions o;
+        std::memcpy(&o, opts, sizeof(o));
+        h = new Inerf();
+        try {
+            h->nerf.init(o, TRAINING);
+        } catch (...) {
+            delete h;
+            h = nullptr;
+            throw;
+        }
+        h->density.g = h->nerf.densityMLP();
+        h->color.n = h->nerf.colorMLP();
+    });
+    return h;
+}
+
+void inerf_destroy(Inerf* h) { delete h; }
+
+#define NERF_CALL(name, body) guarded(name, [&] { if (!h) throw std::runtime_error("null handle"); body; })
+
+int inerf_train(Inerf* h, const float* rays_o, const float* rays_d, const float* rays_depth, const float* rays_sigma,
+                const float* rgb_true, uint32_t num_rays, int* train_step_count, uint32_t* hit_counts,
+                float* rgb_out, hipStream_t stream)
+{
+    return NERF_CALL("inerf_train", {
+        int dummy = 0;
+        h->nerf.trainWithRaysHit(reinterpret_cast<const float3*>(rays_o), reinterpret_cast<const float3*>(rays_d),
+                                 rays_depth, rays_sigma, rgb_true, num_rays,
+                                 train_step_count ? *train_step_count : dummy, hit_counts, rgb_out, stream);
+    });
+}
+
+int inerf_set_learning_rate(Inerf* h, float lr) { return NERF_CALL("inerf_set_learning_rate", h->nerf.setLearningRate(lr)); }
+int inerf_set_bg_color(Inerf* h, float r, float g, float b)
+{
+    return NERF_CALL("inerf_set_bg_color", h->nerf.setBgColor(make_float3(r, g, b)));
+}
+int inerf_set_profiling(Inerf* h, int on) { return NERF_CALL("inerf_set_profiling", h->nerf.setProfiling(on != 0)); }
+int inerf_print_stats(Inerf* h) { return NERF_CALL("inerf_print_stats", h->nerf.printStats()); }
+int inerf_update_occupancy(Inerf* h, hipStream_t stream)
+{
+    return NERF_CALL("inerf_update_occupancy", h->nerf.updateOccupancy(stream));
+}
+size_t inerf_occupancy_bytes(Inerf* h) { return h ? h->nerf.occupancyBytes() : 0; }
+int inerf_get_occupancy(Inerf* h, uint8_t* host_bits)
+{
+    return NERF_CALL("inerf_get_occupancy", {
+        GRAFT_HIP_CHECK(hipDeviceSynchronize());
+        GRAFT_HIP_CHECK(hipMemcpy(host_bits, h->nerf.occupancyGrid(), h->nerf.occupancyBytes(), hipMemcpyDeviceToHost));
+    });
+}
+int inerf_set_occupancy(Inerf* h, const uint8_t* host_bits)
+{
+    return NERF_CALL("inerf_set_occupancy", h->nerf.setOccupancyBits(host_bits));
+}
+int inerf_get_master_grid(Inerf* h, float* host_cells)
+{
+    return NERF_CALL("inerf_get_master_grid", {
+        const NerfOptions& o = h->nerf.options();
+        const size_t n = (size_t)o.numCascades * o.gridResolution.x * o.gridResolution.y * o.gridResolution.z;
+        GRAFT_HIP_CHECK(hipDeviceSynchronize());
+        GRAFT_HIP_CHECK(hipMemcpy(host_cells, h->nerf.masterOccupancyGrid(), n * sizeof(float), hipMemcpyDeviceToHost));
+    });
+}
+int inerf_step_buffers(Inerf* h, InerfStepBuffers* out)
+{
+    return NERF_CALL("inerf_step_buffers", {
+        const InstantNerf::StepBuffers b = h->nerf.stepBuffers();
+        out->num_steps = b.num_steps;
+        out->ray_offsets = b.ray_offsets;
+        out->positions = reinterpret_cast<float*>(b.positions);
+        out->ray_indices = b.ray_indices;
+        out->t_sorted = b.t_sorted;
+        out->density_out = b.density_out;
+        out->color_input = b.color_input;
+        out->color_output = b.color_output;
+        out->sigma = b.sigma;
+        out->render_rgb = b.render_rgb;
+        out->phi = b.phi;
+        out->dw = b.dw;
+        out->weight_sum = b.weight_sum;
+        out->dsigma = b.dsigma;
+        out->color_dx = b.color_dx;
+        out->density_grad = b.density_grad;
+        out->result = b.result;
+        out->trainSteps = b.trainSteps;
+    });
+}
+TmlpGrid* inerf_density(Inerf* h) { return h ? &h->density : nullptr; }
+TmlpNet* inerf_color(Inerf* h) { return h ? &h->color : nullptr; }
+
+void inerf_philox4x32_10(uint32_t* ctr, uint32_t k0, uint32_t k1) { graft::philox4x32_10_host(ctr, k0, k1); }
+
+}  // extern "C"

@@ -1,0 +1,331 @@
+// Cascaded-occupancy DDA raymarch with hit-centric compaction for gfx950.
+//
+//   ray setup   compute_ray_aabb_inv_kernel   otherKernels.cu:91-154
+//   count pass  march_rays_dda_calc_hits      processRays.cu:626-737
+//   scan+cutoff custom_exclusive_sum, find_cutoff_ray_kernel  processRays.cu:486-549, 739-769
+//   fill pass   march_rays_dda_offset         processRays.cu:801-929
+//
+// The reference orchestrates these with three blocking device->host reads per
+// step (processRays.cu:979-1013).  Here the whole compaction is three launches
+// with no host round trip:
+//   1. count: one thread per ray marches and counts its samples; each
+//      256-ray workgroup reduces its counts (wave shuffles, 4 LDS words) to one
+//      block sum.
+//   2. scan: one workgroup of 1024 threads scans the block sums and, since the
+//      inclusive prefix of counts is monotone, finds the one block holding the
+//      cutoff and resolves it ray by ray: active rays = the longest ray prefix
+//      whose samples fit in the batch, exactly the reference rule.
+//   3. fill: each workgroup rescans its 256 counts in LDS, writes the global
+//      exclusive offsets of all rays, and the active rays march again, writing
+//      their samples ray-major at their offsets (the reference order).
+// Both marches run the same code (template on FILL) with the reference's fp32
+// operations in the reference's order, so the two passes agree on every count.
+#include "nerf.h"
+#include "nerf_math.h"
+
+#include <algorithm>
+
+namespace graft {
+
+namespace {
+
+constexpr int kMaxMip = 16;
+
+struct MarchArgs {
+    const float3* o;
+    const float3* d;
+    const float3* di;
+    const float* nears;
+    const float* fars;
+    const uint8_t* bits;
+    uint3 res;
+    float3 mn, mx;
+    int C, L, K;
+    uint32_t R;
+    uint32_t total_cells;        // cells of one cascade pyramid
+    uint32_t cap;                // capacity of the sample outputs
+    uint32_t mip_off[kMaxMip];   // cells below level l
+};
+
+template <bool FILL>
+__device__ uint32_t march_ray(const MarchArgs& a, uint32_t i, uint32_t out_base, float* __restrict__ t_out,
+                              uint32_t* __restrict__ ridx, float4* __restrict__ pos_out)
+{
+    const float3 o = a.o[i], d = a.d[i], di = a.di[i];
+    float t = a.nears[i];
+    const float t_max = a.fars[i];
+    const float ex = a.mx.x - a.mn.x, ey = a.mx.y - a.mn.y, ez = a.mx.z - a.mn.z;
+    const float sx = d.x >= 0.0f ? 1.0f : 0.0f, sy = d.y >= 0.0f ? 1.0f : 0.0f, sz = d.z >= 0.0f ? 1.0f : 0.0f;
+    uint32_t hit = 0;
+    int level = a.L - 1;
+    for (int it = 0; t < t_max && hit < (uint32_t)kMaxHits && it < kMaxMarchIters; it++) {
+        const float px = o.x + t * d.x, py = o.y + t * d.y, pz = o.z + t * d.z;
+        const int c = get_cascade(px, py, pz, a.mn, a.mx, a.C);
+        const float cs = ldexpf(1.0f, c);
+        const float cminx = a.mn.x * cs, cminy = a.mn.y * cs, cminz = a.mn.z * cs;
+        const float cextx = ex * cs, cexty = ey * cs, cextz = ez * cs;
+        const uint32_t rlx = a.res.x >> level, rly = a.res.y >> level, rlz = a.res.z >> level;
+        const float vsx = cextx / (float)rlx, vsy = cexty / (float)rly, vsz = cextz / (float)rlz;
+        const int vix = clamp_floor_idx(floorf(((px - cminx) / cextx) * (float)rlx), (int)rlx - 1);
+        const int viy = clamp_floor_idx(floorf(((py - cminy) / cexty) * (float)rly), (int)rly - 1);
+        const int viz = clamp_floor_idx(floorf(((pz - cminz) / cextz) * (float)rlz), (int)rlz - 1);
+        const uint32_t flat = (uint32_t)c * a.total_cells + a.mip_off[level] + (uint32_t)viz * (rlx * rly) +
+                              (uint32_t)viy * rlx + (uint32_t)vix;
+        const bool occ = (a.bits[flat >> 3] >> (flat & 7)) & 1;
+        const float nbx = cminx + ((float)vix + sx) * vsx;
+        const float nby = cminy + ((float)viy + sy) * vsy;
+        const float nbz = cminz + ((float)viz + sz) * vsz;
+        if (occ) {
+            if (level > 0) {
+                level--;
+                continue;
+            }
+            if constexpr (!FILL) {
+                hit += (uint32_t)min(a.K, kMaxHits - (int)hit);
+            } else {
+                const float exit_t = fminf(fminf((nbx - o.x) * di.x, (nby - o.y) * di.y), (nbz - o.z) * di.z);
+                const float span = exit_t - t;
+                for (int k = 0; k < a.K; ++k) {
+                    if (hit >= (uint32_t)kMaxHits) break;
+                    const float tk = t + ((float)k + 0.5f) / (float)a.K * span;
+                    const uint32_t w = out_base + hit;
+                    if (w < a.cap) {
+                        t_out[w] = tk;
+                        ridx[w] = i;
+                        pos_out[w] = make_float4(contract_axis(o.x + tk * d.x, a.mn.x, a.mx.x),
+                                                 contract_axis(o.y + tk * d.y, a.mn.y, a.mx.y),
+                                                 contract_axis(o.z + tk * d.z, a.mn.z, a.mx.z), 0.0f);
+                    }
+                    hit++;
+                }
+            }
+        }
+        const float next_t = fminf(fminf((nbx - o.x) * di.x, (nby - o.y) * di.y), (nbz - o.z) * di.z);
+        t = fmaxf(t + 1e-5f, next_t + 1e-6f);
+        level = a.L - 1;
+    }
+    return hit;
+}
+
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v)
+{
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t u = __shfl_up(v, o, 64);
+        if (lane >= o) v += u;
+    }
+    return v;
+}
+
+// Inclusive scan over the workgroup (NW waves of 64); every thread must call.
+template <int NW>
+__device__ __forceinline__ uint32_t block_incl_scan(uint32_t v, uint32_t* s_wave /* [NW] */)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint32_t incl = wave_incl_scan(v);
+    if (lane == 63) s_wave[wave] = incl;
+    __syncthreads();
+    if (wave == 0) {
+        uint32_t w = lane < NW ? s_wave[lane] : 0u;
+        w = wave_incl_scan(w);
+        if (lane < NW) s_wave[lane] = w;
+    }
+    __syncthreads();
+    const uint32_t before = wave > 0 ? s_wave[wave - 1] : 0u;
+    __syncthreads();
+    return incl + before;
+}
+
+__global__ __launch_bounds__(256) void ray_aabb_kernel(uint32_t R, const float3* __restrict__ O,
+                                                       const float3* __restrict__ D, float3 lo, float3 hi,
+                                                       float3* __restrict__ DI, float* __restrict__ nears,
+                                                       float* __restrict__ fars)
+{
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= R) return;
+    const float3 o = O[i];
+    float3 d = D[i];
+    if (fabsf(d.x) < 1e-8f) d.x = 1e-8f;
+    if (fabsf(d.y) < 1e-8f) d.y = 1e-8f;
+    if (fabsf(d.z) < 1e-8f) d.z = 1e-8f;
+    const float3 inv = make_float3(1.0f / d.x, 1.0f / d.y, 1.0f / d.z);
+    DI[i] = inv;
+    float t1x = (lo.x - o.x) * inv.x, t2x = (hi.x - o.x) * inv.x;
+    if (t1x > t2x) { const float q = t1x; t1x = t2x; t2x = q; }
+    float t1y = (lo.y - o.y) * inv.y, t2y = (hi.y - o.y) * inv.y;
+    if (t1y > t2y) { const float q = t1y; t1y = t2y; t2y = q; }
+    float t1z = (lo.z - o.z) * inv.z, t2z = (hi.z - o.z) * inv.z;
+    if (t1z > t2z) { const float q = t1z; t1z = t2z; t2z = q; }
+    const float te = fmaxf(fmaxf(t1x, t1y), t1z);
+    const float tx = fminf(fminf(t2x, t2y), t2z);
+    if (te > tx || tx < 0.0f) {
+        nears[i] = 0.0f;
+        fars[i] = 0.0f;
+    } else {
+        nears[i] = fmaxf(te, 0.0f);
+        fars[i] = tx;
+    }
+}
+
+__global__ __launch_bounds__(256) void march_count_kernel(const MarchArgs a, uint32_t* __restrict__ counts,
+                                                          uint32_t* __restrict__ block_sums)
+{
+    __shared__ uint32_t s_wave[4];
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    uint32_t n = 0;
+    if (i < a.R) {
+        n = march_ray<false>(a, i, 0, nullptr, nullptr, nullptr);
+        counts[i] = n;
+    }
+    if (block_sums) {
+        uint32_t v = n;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+        if ((threadIdx.x & 63) == 0) s_wave[threadIdx.x >> 6] = v;
+        __syncthreads();
+        if (threadIdx.x == 0) block_sums[blockIdx.x] = (s_wave[0] + s_wave[1]) + (s_wave[2] + s_wave[3]);
+    }
+}
+
+// One workgroup: block_sums (in) -> exclusive block offsets (out, in place);
+// result = {active rays, compacted samples}.
+__global__ __launch_bounds__(1024) void march_scan_kernel(const uint32_t* __restrict__ counts,
+                                                          uint32_t* __restrict__ block_sums, uint32_t nb,
+                                                          uint32_t R, uint32_t batch, uint32_t* __restrict__ result)
+{
+    __shared__ uint32_t s_wave[16];
+    __shared__ uint32_t s_carry, s_bstar;
+    const uint32_t tid = threadIdx.x;
+    if (tid == 0) {
+        s_carry = 0;
+        s_bstar = 0xffffffffu;
+    }
+    __syncthreads();
+    for (uint32_t base = 0; base < nb; base += 1024) {
+        const uint32_t b = base + tid;
+        const uint32_t v = b < nb ? block_sums[b] : 0u;
+        const uint32_t carry = s_carry;
+        const uint32_t incl = carry + block_incl_scan<16>(v, s_wave);
+        const uint32_t excl = incl - v;
+        if (b < nb) {
+            block_sums[b] = excl;
+            if (excl <= batch && incl > batch) s_bstar = b;  // unique: prefixes are monotone
+        }
+        __syncthreads();
+        if (tid == 1023) s_carry = incl;
+        __syncthreads();
+    }
+    const uint32_t bstar = s_bstar;
+    if (bstar == 0xffffffffu) {
+        if (tid == 0) {
+            result[0] = R;
+            result[1] = s_carry;
+        }
+        return;
+    }
+    const uint32_t excl_b = block_sums[bstar];
+    const uint32_t i = bstar * 256 + tid;
+    const uint32_t c = (tid < 256 && i < R) ? counts[i] : 0u;
+    const uint32_t incl = block_incl_scan<16>(c, s_wave);
+    const bool ok = tid < 256 && i < R && excl_b + incl <= batch;
+    const int n_ok = __syncthreads_count(ok);
+    if (n_ok == 0) {
+        if (tid == 0) {
+            result[0] = bstar * 256;
+            result[1] = excl_b;
+        }
+    } else if ((int)tid == n_ok - 1) {
+        result[0] = bstar * 256 + (uint32_t)n_ok;
+        result[1] = excl_b + incl;
+    }
+}
+
+__global__ __launch_bounds__(256) void march_fill_kernel(const MarchArgs a, const uint32_t* __restrict__ counts,
+                                                         const uint32_t* __restrict__ block_excl,
+                                                         const uint32_t* __restrict__ result,
+                                                         uint32_t* __restrict__ offsets, float* __restrict__ t_out,
+                                                         uint32_t* __restrict__ ridx, float4* __restrict__ pos_out)
+{
+    __shared__ uint32_t s_wave[4];
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t c = i < a.R ? counts[i] : 0u;
+    const uint32_t incl = block_incl_scan<4>(c, s_wave);
+    const uint32_t off = block_excl[blockIdx.x] + (incl - c);
+    if (i < a.R) offsets[i] = off;
+    if (i < result[0]) march_ray<true>(a, i, off, t_out, ridx, pos_out);
+}
+
+MarchArgs march_args(uint32_t R, const float3* o, const float3* d, const float3* di, const float* nears,
+                     const float* fars, const OccGrid& g, int K, uint32_t cap)
+{
+    if (g.mip_levels < 1 || g.mip_levels > kMaxMip) throw std::runtime_error("raymarch: mip levels must be in [1, 16]");
+    if (g.cascades < 1) throw std::runtime_error("raymarch: need at least one cascade");
+    if (K < 1) throw std::runtime_error("raymarch: samplesPerVoxel must be >= 1");
+    if ((g.res.x >> (g.mip_levels - 1)) == 0 || (g.res.y >> (g.mip_levels - 1)) == 0 ||
+        (g.res.z >> (g.mip_levels - 1)) == 0)
+        throw std::runtime_error("raymarch: grid resolution too small for the mip levels");
+    MarchArgs a{};
+    a.o = o;
+    a.d = d;
+    a.di = di;
+    a.nears = nears;
+    a.fars = fars;
+    a.bits = g.bits;
+    a.res = g.res;
+    a.mn = g.aabb_min;
+    a.mx = g.aabb_max;
+    a.C = g.cascades;
+    a.L = g.mip_levels;
+    a.K = K;
+    a.R = R;
+    a.cap = cap;
+    for (int l = 0; l < g.mip_levels; l++) a.mip_off[l] = mip_offset(g.res, l);
+    a.total_cells = mip_offset(g.res, g.mip_levels);
+    return a;
+}
+
+}  // namespace
+
+void ray_aabb_inv(uint32_t R, const float3* o, const float3* d, float3 mn, float3 mx, int cascades,
+                  float3* d_inv, float* nears, float* fars, hipStream_t s)
+{
+    if (R == 0) return;
+    const float scale = ldexpf(1.0f, cascades - 1);
+    const float3 lo = make_float3(mn.x * scale, mn.y * scale, mn.z * scale);
+    const float3 hi = make_float3(mx.x * scale, mx.y * scale, mx.z * scale);
+    hipLaunchKernelGGL(ray_aabb_kernel, dim3((R + 255) / 256), dim3(256), 0, s, R, o, d, lo, hi, d_inv, nears, fars);
+    GRAFT_LAUNCH_CHECK();
+}
+
+size_t march_scratch_words(uint32_t R) { return (size_t)(R + 255) / 256 + 2; }
+
+void march_count(uint32_t R, const float3* o, const float3* d, const float3* d_inv, const float* nears,
+                 const float* fars, const OccGrid& g, int K, uint32_t* counts, hipStream_t s)
+{
+    if (R == 0) return;
+    const MarchArgs a = march_args(R, o, d, d_inv, nears, fars, g, K, 0);
+    hipLaunchKernelGGL(march_count_kernel, dim3((R + 255) / 256), dim3(256), 0, s, a, counts, nullptr);
+    GRAFT_LAUNCH_CHECK();
+}
+
+void march_hits(uint32_t R, const float3* o, const float3* d, const float3* d_inv, const float* nears,
+                const float* fars, const OccGrid& g, int K, uint32_t batch, uint32_t* counts, uint32_t* offsets,
+                float* t_out, uint32_t* ray_idx, float4* pos_out, const MarchScratch& sc, hipStream_t s)
+{
+    if (R == 0) {
+        GRAFT_HIP_CHECK(hipMemsetAsync(sc.result, 0, 2 * sizeof(uint32_t), s));
+        return;
+    }
+    const MarchArgs a = march_args(R, o, d, d_inv, nears, fars, g, K, batch);
+    const uint32_t nb = (R + 255) / 256;
+    hipLaunchKernelGGL(march_count_kernel, dim3(nb), dim3(256), 0, s, a, counts, sc.block_sums);
+    GRAFT_LAUNCH_CHECK();
+    hipLaunchKernelGGL(march_scan_kernel, dim3(1), dim3(1024), 0, s, counts, sc.block_sums, nb, R, batch, sc.result);
+    GRAFT_LAUNCH_CHECK();
+    hipLaunchKernelGGL(march_fill_kernel, dim3(nb), dim3(256), 0, s, a, counts, sc.block_sums, sc.result, offsets,
+                       t_out, ray_idx, pos_out);
+    GRAFT_LAUNCH_CHECK();
+}
+
+}  // namespace graft

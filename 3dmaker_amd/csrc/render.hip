@@ -1,0 +1,418 @@
+// Per-sample and per-ray kernels around the two MLPs, plus the occupancy
+// bitfield, for gfx950.
+//
+//   sh_gather       compute_SH_gather              otherKernels.cu:156-273
+//   composite       render_rays_distortion_kernel  compositing.cu:80-213
+//   color_grad      compute_color_grad             otherKernels.cu:303-409
+//   density_grad    compute_density_grad           otherKernels.cu:497-562
+//   master grid     updateMasterGrid               otherKernels.cu:677-690
+//   occupancy bits  updateOccupancyGrid            otherKernels.cu:700-750
+//   mip pyramid     bitfield_max_pool / buildMipmaps  otherKernels.cu:752-807, InstantNerf.cu:1177-1204
+//
+// Arithmetic follows the reference kernels operation by operation (fp32,
+// no contraction, correctly rounded division); e^x is nerf_expf.  Sample and
+// ray counts may come from device memory (see nerf.h).
+#include "nerf.h"
+#include "nerf_math.h"
+
+#include <algorithm>
+
+namespace graft {
+
+namespace {
+
+__device__ __forceinline__ uint32_t dev_count(const uint32_t* d_n, uint32_t n_max)
+{
+    return d_n ? min(*d_n, n_max) : n_max;
+}
+
+__device__ __forceinline__ float sanitize_logit(float v)
+{
+    v = fmaxf(-64.0f, fminf(64.0f, v));
+    return (v != v) ? 0.0f : v;
+}
+
+// One sample per thread: 64 B of density logits in, 64 B of fp16 color input
+// and the sigma out, all as 16-byte vectors.
+__global__ __launch_bounds__(256) void sh_gather_kernel(const float3* __restrict__ dirs,
+                                                        const uint32_t* __restrict__ ray_idx,
+                                                        const uint32_t* __restrict__ d_n, uint32_t n_max, float bias,
+                                                        const float* __restrict__ dout, _Float16* __restrict__ cin,
+                                                        float* __restrict__ sigma)
+{
+    const uint32_t N = dev_count(d_n, n_max);
+    const uint32_t n = blockIdx.x * blockDim.x + threadIdx.x;
+    if (n >= N) return;
+    const float3 d = dirs[ray_idx[n]];
+    const float x = d.x, y = d.y, z = d.z;
+    const float x2 = x * x, y2 = y * y, z2 = z * z;
+    float sh[16];
+    sh[0] = 0.28209479f;
+    sh[1] = -0.48860251f * y;
+    sh[2] = 0.48860251f * z;
+    sh[3] = -0.48860251f * x;
+    sh[4] = 1.09254843f * x * y;
+    sh[5] = -1.09254843f * y * z;
+    sh[6] = 0.31539156f * (3.0f * z2 - 1.0f);
+    sh[7] = -1.09254843f * x * z;
+    sh[8] = 0.54627421f * (x2 - y2);
+    sh[9] = -0.59004359f * y * (3.0f * x2 - y2);
+    sh[10] = 2.89061144f * x * y * z;
+    sh[11] = -0.45704580f * y * (5.0f * z2 - 1.0f);
+    sh[12] = 0.37317633f * z * (5.0f * z2 - 3.0f);
+    sh[13] = -0.45704580f * x * (5.0f * z2 - 1.0f);
+    sh[14] = 1.44530572f * z * (x2 - y2);
+    sh[15] = -0.59004359f * x * (x2 - 3.0f * y2);
+    const f4* src = reinterpret_cast<const f4*>(dout + 16 * (size_t)n);
+    float lg[16];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const f4 v = src[q];
+#pragma unroll
+        for (int j = 0; j < 4; j++) lg[4 * q + j] = sanitize_logit(v[j]);
+    }
+    sigma[n] = nerf_expf(fminf(lg[0] - bias, 8.0f));
+    h4* dst = reinterpret_cast<h4*>(cin + 32 * (size_t)n);
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        dst[q] = h4{to_h(lg[4 * q]), to_h(lg[4 * q + 1]), to_h(lg[4 * q + 2]), to_h(lg[4 * q + 3])};
+        dst[4 + q] = h4{to_h(sh[4 * q]), to_h(sh[4 * q + 1]), to_h(sh[4 * q + 2]), to_h(sh[4 * q + 3])};
+    }
+}
+
+__device__ __forceinline__ float disparity_warp(float t, float t_near, float inv_g_range)
+{
+    return (1.0f - t_near / fmaxf(t, 1e-4f)) * inv_g_range;
+}
+
+__global__ __launch_bounds__(256) void composite_kernel(const CompositeArgs a, const uint32_t* __restrict__ d_rays,
+                                                        uint32_t rays_max)
+{
+    const uint32_t R = dev_count(d_rays, rays_max);
+    const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= R) return;
+    const uint32_t off = a.offsets[r], cnt = a.counts[r];
+    const float d_prior = a.depth_prior ? a.depth_prior[r] : -1.0f;
+    const float s_prior = a.sigma_prior ? a.sigma_prior[r] : -1.0f;
+    const float dwl = (d_prior >= 0) ? a.lambda_depth : 0.0f;
+    const float t_near = (cnt > 0) ? fmaxf(a.t[off], 1e-4f) : 1.0f;
+    const float t_far = (cnt > 0) ? a.t[off + cnt - 1] : 1.0f;
+    const float g_far = 1.0f - t_near / fmaxf(t_far, t_near + 1e-4f);
+    const float inv_g = (g_far > 1e-6f) ? (1.0f / g_far) : 0.0f;
+    float T = 1.0f, rc = 0.0f, gc = 0.0f, bc = 0.0f, depth = 0.0f;
+    const float c = 2.0f / 3;
+    float dw_g = 0.0f, dwm_g = 0.0f, dw_s = 0.0f, dwm_s = 0.0f, dls = 0.0f;
+    for (uint32_t i = 0; i < cnt; i++) {
+        const uint32_t idx = off + i;
+        const float t = a.t[idx];
+        float t_next = (i < cnt - 1) ? a.t[idx + 1] : (t + 1e-3f);
+        float delta = t_next - t;
+        if (delta < 0.0f) {
+            delta = 0.0f;
+            t_next = t;
+        }
+        const float s = disparity_warp(t, t_near, inv_g);
+        const float s_next = disparity_warp(t_next, t_near, inv_g);
+        const float m = 0.5f * (s + s_next);
+        const float alpha = 1.0f - nerf_expf(-a.sigma[idx] * delta);
+        const float w = alpha * T;
+        const float* cc = a.rgb + (size_t)a.rgb_stride * idx;
+        rc += w * cc[0];
+        gc += w * cc[1];
+        bc += w * cc[2];
+        depth += w * t;
+        T *= (1.0f - alpha);
+        dw_g += w;
+        dwm_g += w * m;
+        const float tx = (t - d_prior) / s_prior;
+        dls += nerf_expf(-0.5f * tx * tx) * delta;
+        a.dw[idx] = w;
+    }
+    dls = 1.0f / fmaxf(dls, 1e-8f);
+    float wgs = 0.0f;
+    for (uint32_t i = 0; i < cnt; i++) {
+        const uint32_t idx = off + i;
+        const float t = a.t[idx];
+        float t_next = (i < cnt - 1) ? a.t[idx + 1] : (t + 1e-3f);
+        float delta = t_next - t;
+        if (delta < 0.0f) {
+            delta = 0.0f;
+            t_next = t;
+        }
+        const float s = disparity_warp(t, t_near, inv_g);
+        const float s_next = disparity_warp(t_next, t_near, inv_g);
+        const float m = 0.5f * (s + s_next);
+        float ds = s_next - s;
+        if (ds < 0.0f) ds = 0.0f;
+        const float w = a.dw[idx];
+        const float tx = (t - d_prior) / s_prior;
+        const float dwt = nerf_expf(-0.5f * tx * tx) * delta * dls;
+        const float dloss = -dwt * (1.0f / fmaxf(w, 1e-6f));
+        const float bil = m * (2 * dw_s - dw_g) + (dwm_g - 2 * dwm_s);
+        const float g = a.lambda_dist * (2 * (bil) + c * w * ds) + dwl * dloss;
+        a.dw[idx] = g;
+        wgs += w * g;
+        dw_s += w;
+        dwm_s += w * m;
+    }
+    a.weight_sum[r] = wgs;
+    rc += T * a.bg.x;
+    gc += T * a.bg.y;
+    bc += T * a.bg.z;
+    a.final_rgb[3 * r] = rc;
+    a.final_rgb[3 * r + 1] = gc;
+    a.final_rgb[3 * r + 2] = bc;
+    a.final_depth[r] = depth;
+    if (a.rgb_true && a.phi) {
+        a.phi[3 * r] = 2.0f * (rc - a.rgb_true[3 * r]);
+        a.phi[3 * r + 1] = 2.0f * (gc - a.rgb_true[3 * r + 1]);
+        a.phi[3 * r + 2] = 2.0f * (bc - a.rgb_true[3 * r + 2]);
+    }
+}
+
+__global__ __launch_bounds__(256) void color_grad_kernel(const ColorGradArgs a, const uint32_t* __restrict__ d_rays,
+                                                         uint32_t rays_max)
+{
+    const uint32_t R = dev_count(d_rays, rays_max);
+    const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= R) return;
+    const uint32_t r = idx + a.initial_offset;
+    float T = 1.0f, cr = 0.0f, cg = 0.0f, cb = 0.0f, wg = 0.0f;
+    const uint32_t base = a.offsets[r];
+    const float wgs = a.weight_sum[r];
+    const uint32_t cnt = a.counts[r];
+    const float pr = a.phi[3 * r], pg = a.phi[3 * r + 1], pb = a.phi[3 * r + 2];
+    const float fr = a.final_rgb[3 * r], fg = a.final_rgb[3 * r + 1], fb = a.final_rgb[3 * r + 2];
+    const uint32_t start = a.offsets[a.initial_offset];
+    const float bs = 1.0f / (float)a.total_rays;
+    for (uint32_t j = 0; j < cnt; j++) {
+        const uint32_t gi = base + j;
+        const size_t i = gi - start;
+        const float tc = a.t[gi];
+        const float delta = (j == cnt - 1) ? 1e-3f : fmaxf(a.t[gi + 1] - tc, 0.0f);
+        const float sigma = nerf_expf(fminf(a.density_out[16 * i] - a.bias, 8.0f));
+        const float alpha = 1.0f - nerf_expf(-sigma * delta);
+        const float w = T * alpha;
+        const float* co = a.color_out + (size_t)a.color_stride * i;
+        const float c_r = co[0], c_g = co[1], c_b = co[2];
+        cr += w * c_r;
+        cg += w * c_g;
+        cb += w * c_b;
+        float g_r = pr * w * c_r * (1.0f - c_r) * a.loss_scale * bs;
+        float g_g = pg * w * c_g * (1.0f - c_g) * a.loss_scale * bs;
+        float g_b = pb * w * c_b * (1.0f - c_b) * a.loss_scale * bs;
+        g_r = clamp_half_range(g_r);
+        g_g = clamp_half_range(g_g);
+        g_b = clamp_half_range(g_b);
+        if (g_r != g_r || g_g != g_g || g_b != g_b) g_r = g_g = g_b = 0.0f;
+        _Float16* cgo = reinterpret_cast<_Float16*>(a.color_grad) + (size_t)a.grad_stride * i;
+        cgo[0] = to_h(g_r);
+        cgo[1] = to_h(g_g);
+        cgo[2] = to_h(g_b);
+        for (int k = 3; k < a.grad_stride; k++) cgo[k] = (_Float16)0.0f;
+        const float sr = fr - cr, sg = fg - cg, sb = fb - cb;
+        const float dr = T * c_r * (1.0f - alpha) - sr;
+        const float dg = T * c_g * (1.0f - alpha) - sg;
+        const float db = T * c_b * (1.0f - alpha) - sb;
+        const float gw = a.dw[i];
+        wg += w * gw;
+        const float suffix = wgs - wg;
+        float dsi = delta * (dr * pr + dg * pg + db * pb);
+        dsi += delta * (gw * T * (1.0f - alpha) - suffix);
+        float ds = dsi * sigma * a.loss_scale * bs;
+        ds = clamp_half_range(ds);
+        if (ds != ds) ds = 0.0f;
+        a.dsigma[i] = ds;
+        T = T * (1.0f - alpha);
+    }
+}
+
+__global__ __launch_bounds__(256) void density_grad_kernel(const uint32_t* __restrict__ d_n, uint32_t n_max,
+                                                           const float* __restrict__ dsigma,
+                                                           const _Float16* __restrict__ cdx,
+                                                           _Float16* __restrict__ dgrad)
+{
+    const uint32_t N = dev_count(d_n, n_max);
+    const uint32_t n = blockIdx.x * blockDim.x + threadIdx.x;
+    if (n >= N) return;
+    const h4* src = reinterpret_cast<const h4*>(cdx + 32 * (size_t)n);
+    h4* dst = reinterpret_cast<h4*>(dgrad + 16 * (size_t)n);
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const h4 v = src[q];
+        h4 o;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            float f = (float)v[j];
+            if (q == 0 && j == 0) f += dsigma[n];
+            f = clamp_half_range(f);
+            if (f != f) f = 0.0f;
+            o[j] = to_h(f);
+        }
+        dst[q] = o;
+    }
+}
+
+__global__ __launch_bounds__(256) void master_grid_kernel(const float* __restrict__ tmp, float* __restrict__ master,
+                                                          float decay, uint32_t n)
+{
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float prev = master[i];
+    master[i] = (prev < 0.f) ? prev : fmaxf(prev * decay, tmp[i]);
+}
+
+// Fixed-order sum: block b sums elements b, b + gridDim, ... per thread, then
+// a fixed tree over the workgroup; the second pass sums the partials likewise.
+__global__ __launch_bounds__(256) void reduce_sum_kernel(const float* __restrict__ in, uint32_t n,
+                                                         float* __restrict__ out)
+{
+    __shared__ float s[256];
+    float acc = 0.0f;
+    for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) acc += in[i];
+    s[threadIdx.x] = acc;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) s[threadIdx.x] += s[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[blockIdx.x] = s[0];
+}
+
+// 64 cells per wave -> one ballot -> two 32-bit words (cells 32k..32k+31 in
+// word k, LSB = lowest cell), at the cascade's pyramid offset.
+__global__ __launch_bounds__(256) void occupancy_bits_kernel(uint32_t* __restrict__ bits32,
+                                                             const float* __restrict__ master,
+                                                             const float* __restrict__ d_sum, int total, int G, int S,
+                                                             float min_optical, float base_voxel)
+{
+    const int cell = blockIdx.x * blockDim.x + threadIdx.x;
+    bool active = false;
+    if (cell < total) {
+        const float mean = d_sum[0] / (float)total;
+        const int c = cell / G;
+        const float thr = fminf((min_optical / base_voxel) / ldexpf(1.0f, c), mean);
+        active = master[cell] > thr;
+    }
+    const uint64_t m = __ballot(active);
+    const int lane = threadIdx.x & 63;
+    if ((lane & 31) == 0 && cell < total) {
+        const int c = cell / G;
+        const int bitpos = c * S + (cell - c * G);
+        bits32[bitpos >> 5] = (uint32_t)(m >> lane);
+    }
+}
+
+__global__ __launch_bounds__(256) void mip_pool_kernel(const uint8_t* __restrict__ in, uint8_t* __restrict__ out,
+                                                       uint3 ro)
+{
+    const int o = blockIdx.x * blockDim.x + threadIdx.x;
+    const int total = (int)(ro.x * ro.y * ro.z);
+    bool occ = false;
+    if (o < total) {
+        const int x = o % (int)ro.x, y = (o / (int)ro.x) % (int)ro.y, z = o / (int)(ro.x * ro.y);
+        const int rix = 2 * (int)ro.x, riy = 2 * (int)ro.y;
+#pragma unroll
+        for (int dz = 0; dz < 2; ++dz)
+#pragma unroll
+            for (int dy = 0; dy < 2; ++dy)
+#pragma unroll
+                for (int dx = 0; dx < 2; ++dx) {
+                    const int idx = (2 * z + dz) * (rix * riy) + (2 * y + dy) * rix + (2 * x + dx);
+                    occ = occ || ((in[idx >> 3] >> (idx & 7)) & 1);
+                }
+    }
+    const uint64_t m = __ballot(occ);
+    const int lane = threadIdx.x & 63;
+    if (total >= 32) {
+        if ((lane & 31) == 0 && o < total) reinterpret_cast<uint32_t*>(out)[o >> 5] = (uint32_t)(m >> lane);
+    } else if (threadIdx.x == 0) {
+        for (int b = 0; b < (total + 7) / 8; ++b) out[b] = (uint8_t)((m >> (8 * b)) & 0xFF);
+    }
+}
+
+inline int blocks_for(uint32_t n) { return (int)std::max<uint32_t>(1, (n + 255) / 256); }
+
+}  // namespace
+
+void sh_gather(const float3* dirs, const uint32_t* ray_idx, const uint32_t* d_n, uint32_t n_max, float bias,
+               const float* density_out, __half* color_in, float* sigma, hipStream_t s)
+{
+    if (n_max == 0) return;
+    hipLaunchKernelGGL(sh_gather_kernel, dim3(blocks_for(n_max)), dim3(256), 0, s, dirs, ray_idx, d_n, n_max, bias,
+                       density_out, reinterpret_cast<_Float16*>(color_in), sigma);
+    GRAFT_LAUNCH_CHECK();
+}
+
+void composite(const CompositeArgs& a, const uint32_t* d_rays, uint32_t rays_max, hipStream_t s)
+{
+    if (rays_max == 0) return;
+    hipLaunchKernelGGL(composite_kernel, dim3(blocks_for(rays_max)), dim3(256), 0, s, a, d_rays, rays_max);
+    GRAFT_LAUNCH_CHECK();
+}
+
+void color_grad(const ColorGradArgs& a, const uint32_t* d_rays, uint32_t rays_max, hipStream_t s)
+{
+    if (rays_max == 0) return;
+    if (a.total_rays == 0) throw std::runtime_error("color grad: totalRaysBatch must be > 0");
+    hipLaunchKernelGGL(color_grad_kernel, dim3(blocks_for(rays_max)), dim3(256), 0, s, a, d_rays, rays_max);
+    GRAFT_LAUNCH_CHECK();
+}
+
+void density_grad(const uint32_t* d_n, uint32_t n_max, const float* dsigma, const __half* color_dx,
+                  __half* dgrad, hipStream_t s)
+{
+    if (n_max == 0) return;
+    hipLaunchKernelGGL(density_grad_kernel, dim3(blocks_for(n_max)), dim3(256), 0, s, d_n, n_max, dsigma,
+                       reinterpret_cast<const _Float16*>(color_dx), reinterpret_cast<_Float16*>(dgrad));
+    GRAFT_LAUNCH_CHECK();
+}
+
+void update_master_grid(const float* tmp, float* master, float decay, uint32_t n, hipStream_t s)
+{
+    if (n == 0) return;
+    hipLaunchKernelGGL(master_grid_kernel, dim3(blocks_for(n)), dim3(256), 0, s, tmp, master, decay, n);
+    GRAFT_LAUNCH_CHECK();
+}
+
+void reduce_sum(const float* in, uint32_t n, float* partials, float* out, hipStream_t s)
+{
+    const int nb = std::min(1024, blocks_for(n));
+    hipLaunchKernelGGL(reduce_sum_kernel, dim3(nb), dim3(256), 0, s, in, n, partials);
+    GRAFT_LAUNCH_CHECK();
+    hipLaunchKernelGGL(reduce_sum_kernel, dim3(1), dim3(256), 0, s, partials, (uint32_t)nb, out);
+    GRAFT_LAUNCH_CHECK();
+}
+
+void update_occupancy_bits(uint32_t* bits32, const float* master, const float* d_sum, int total, int G, int S,
+                           float min_optical, float base_voxel, hipStream_t s)
+{
+    if (total <= 0) return;
+    if (G % 32 || S % 32) throw std::runtime_error("occupancy: cells per cascade must be multiples of 32");
+    hipLaunchKernelGGL(occupancy_bits_kernel, dim3(blocks_for((uint32_t)total)), dim3(256), 0, s, bits32, master,
+                       d_sum, total, G, S, min_optical, base_voxel);
+    GRAFT_LAUNCH_CHECK();
+}
+
+void build_mipmaps(uint8_t* bits, uint3 res, int L, int C, hipStream_t s)
+{
+    const uint32_t S = mip_offset(res, L);
+    if (S % 8) throw std::runtime_error("occupancy: pyramid cells per cascade must be a multiple of 8");
+    for (int c = 0; c < C; ++c) {
+        uint8_t* cur = bits + (size_t)c * (S / 8);
+        uint3 r = res;
+        for (int l = 0; l < L - 1; ++l) {
+            const uint3 ro = make_uint3(r.x / 2, r.y / 2, r.z / 2);
+            const uint32_t cells = ro.x * ro.y * ro.z;
+            if (cells == 0) break;
+            if (cells >= 32 && cells % 32) throw std::runtime_error("occupancy: mip level cells must be a multiple of 32");
+            uint8_t* nxt = cur + (r.x * r.y * r.z) / 8;
+            hipLaunchKernelGGL(mip_pool_kernel, dim3(blocks_for(cells)), dim3(256), 0, s, cur, nxt, ro);
+            GRAFT_LAUNCH_CHECK();
+            cur = nxt;
+            r = ro;
+        }
+    }
+}
+
+}  // namespace graft

@@ -1,0 +1,102 @@
+/*
+ * C-ABI of the MI355X (gfx950) NeRF-side hot path: the reference's extern "C"
+ * launchers of modules/NeRF (InstantNerf.h:385-568) for the training path, and
+ * launchers for the kernels the reference launches inline from
+ * InstantNerf.cu.  cudaStream_t is replaced by hipStream_t; float3 / uint3 are
+ * HIP's (12 bytes, 4-byte aligned, like CUDA's).  Pointers are device
+ * pointers unless stated.  Failures set tinymlp_last_error() (tinymlp_abi.h)
+ * instead of printing and returning silently.
+ *
+ * Arithmetic deviations from the reference's fast-math device code, shared
+ * with the CPU oracle the tests compare against: e^x is one fixed
+ * Cody-Waite/Taylor routine (max 1.2 ulp), the cascade index uses an exact
+ * ceil(log2), division and square root are correctly rounded.
+ */
+#ifndef GRAFT_NERF_ABI_H
+#define GRAFT_NERF_ABI_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#include "tinymlp_abi.h"
+
+#ifdef __cplusplus
+#include <hip/hip_vector_types.h>
+extern "C" {
+#endif
+
+/* processRays.cu:931-1040 (declared InstantNerf.h:509-533).  Count pass,
+ * exclusive scan and cutoff at batchSize, fill pass; returns the number of
+ * active rays and writes the compacted sample count to *totalHits (host).
+ * The three blocking round trips of the reference become one read at the end.
+ * d_block_sums is accepted for signature compatibility and not used (the
+ * library keeps its own scratch); it may be NULL. */
+int processRaysHitLinear(const uint32_t num_rays, const float3* rays_o, const float3* rays_d,
+                         const float3* rays_d_inv, const float* nears, const float* fars,
+                         const uint8_t* occupancy_grid, const uint3 grid_resolution, const float3 aabb_min,
+                         const float3 aabb_max, const int numCascades, const int mipmapLevels,
+                         const int samplesPerVoxel, const int batchSize, uint32_t* totalHits,
+                         uint32_t* d_active_rays_count, uint32_t* d_num_steps, uint32_t* d_ray_offsets,
+                         float* d_mlp_positions_batch, uint32_t* d_ray_indices, float* d_t_sorted,
+                         uint32_t* d_block_sums, hipStream_t stream);
+
+/* compositing.cu:215-279 (declared InstantNerf.h:444-465): with d_dw_out set,
+ * the training compositor with the distortion loss (render_rays_distortion_kernel).
+ * base and raysDone are accepted for signature compatibility (the training
+ * path passes 0). */
+void launchVolumeRendering(const uint32_t num_rays, const uint32_t* d_ray_offsets, const uint32_t* d_num_steps,
+                           const float* d_t_sorted, const float* d_density_sigma, const float* d_depth_chunk,
+                           const float* d_sigma_chunk, const float* d_rgb_output, const float* d_rgb_true,
+                           float* d_render_rgb, float* d_render_depth, float* d_phi_out, float* d_dw_out,
+                           float* d_weight_sum, float lambda_dist, float lambda_depth, float3 bg_color,
+                           uint32_t base, uint32_t raysDone, hipStream_t stream);
+
+/* ---- kernels the reference launches inline (no extern "C" counterpart) ---- */
+
+/* compute_ray_aabb_inv_kernel (otherKernels.cu:91-154), launched at InstantNerf.cu:391-398. */
+void launchComputeRayAabbInv(uint32_t num_rays, const float3* rays_o, const float3* rays_d, float3 aabb_min,
+                             float3 aabb_max, int num_cascades, float3* rays_d_inv, float* nears, float* fars,
+                             hipStream_t stream);
+
+/* compute_SH_gather (otherKernels.cu:156-273), launched at InstantNerf.cu:444-450, 512-517. */
+void launchComputeSHGather(const float3* d_chunk_d, const uint32_t* d_ray_indices, int offset, int batchSize,
+                           float densityBias, float* d_density_out, GRAFT_HALF* d_color_in, float* d_density_sigma,
+                           hipStream_t stream);
+
+/* compute_color_grad (otherKernels.cu:303-409), launched at InstantNerf.cu:526-543. */
+void launchComputeColorGrad(uint32_t numRays, uint32_t initialOffset, const uint32_t* num_steps,
+                            const uint32_t* ray_offsets, const float* t_sorted, const float* density_mlp_out,
+                            const float* color_mlp_out, const float* phi_chunk, const float* final_rgb,
+                            const float* dw_out, const float* weight_sum, GRAFT_HALF* custom_color_grad,
+                            float* tmp_dsigma, float loss_scale, float densityBias, uint32_t totalRaysBatch,
+                            hipStream_t stream);
+
+/* compute_density_grad (otherKernels.cu:506-562), launched at InstantNerf.cu:552-557. */
+void launchComputeDensityGrad(uint32_t batch_size, const float* tmp_dsigma, const GRAFT_HALF* custom_dx_out,
+                              GRAFT_HALF* custom_density_grad, hipStream_t stream);
+
+/* updateMasterGrid (otherKernels.cu:677-690). */
+void launchUpdateMasterGrid(const float* tmpGrid, float* masterGrid, float decayValue, int N, hipStream_t stream);
+
+/* Sum of d_in[0..n) into d_out[0], fixed summation order (replaces the CUB
+ * DeviceReduce::Sum of otherKernels.cu:696-698). */
+void launchReduceSum(const float* d_in, int n, float* d_out, hipStream_t stream);
+
+/* updateOccupancyGrid (otherKernels.cu:700-750): level-0 bits from the master
+ * grid; G = cells per cascade, S = cells of one cascade's mip pyramid. */
+void launchUpdateOccupancyGrid(uint32_t* d_occupancy_grid, const float* d_master_grid, const float* d_sum,
+                               int total_cells, int cells_per_cascade, int pyramid_cells_per_cascade,
+                               float min_optical_thickness, float base_voxel, hipStream_t stream);
+
+/* InstantNerf::buildMipmaps + bitfield_max_pool (InstantNerf.cu:1177-1204,
+ * otherKernels.cu:752-807). */
+void launchBuildMipmaps(uint8_t* d_grid, uint3 grid_resolution, int mipmapLevels, int numCascades,
+                        hipStream_t stream);
+
+/* ABI self-check (no reference counterpart): writes a.xyz, b.xyz to out[0..6). */
+void nerf_abi_echo_vec(float3 a, uint3 b, float* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,88 @@
+/*
+ * Flat C handle API over InstantNerf (include/InstantNerf.h), for callers
+ * that cannot use C++ (ctypes, cgo, JNI).  Each function mirrors one method of
+ * the reference class modules/NeRF/InstantNerf.h:279-335; C++ exceptions are
+ * caught and reported as a non-zero return plus tinymlp_last_error_message().
+ * No counterpart exists in the reference, which is C++-only.
+ */
+#ifndef GRAFT_NERF_CAPI_H
+#define GRAFT_NERF_CAPI_H
+
+#include "nerf_abi.h"
+#include "tinymlp_capi.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Byte-for-byte the layout of NerfOptions (InstantNerf.h:35-76); C has no
+ * default member values, so start from inerf_default_options(). */
+typedef struct InerfOptions {
+    uint32_t gridResolution[3];
+    float aabbMin[3];
+    float aabbMax[3];
+    int levelsMipmap, numCascades, samplesPerVoxel;
+    int densityHiddenDim, densityNumLayers;
+    int colorHiddenDim, colorNumLayers;
+    int hashTableSize, numLevels;
+    float growthFactor;
+    int baseResolution, featuresPerLevel;
+    int renderBatchSize, batchSize, rayChunkSize;
+    float lambdaDepth, lambdaDist, learningRate, beta1, beta2, epsilon, lossScale;
+    float bgColor[3];
+    float minDensityThreshold, decayValue, densityBias;
+    uint8_t legacyRenderFlag, isProfiling;
+} InerfOptions;
+
+typedef struct Inerf Inerf;
+
+/* Device pointers of the last training step (see InstantNerf::StepBuffers). */
+typedef struct InerfStepBuffers {
+    uint32_t* num_steps;
+    uint32_t* ray_offsets;
+    float* positions;       /* float4 [batch] */
+    uint32_t* ray_indices;
+    float* t_sorted;
+    float* density_out;     /* [batch x 16] */
+    GRAFT_HALF* color_input;
+    float* color_output;    /* [batch x 8] */
+    float* sigma;
+    float* render_rgb;
+    float* phi;
+    float* dw;
+    float* weight_sum;
+    float* dsigma;
+    GRAFT_HALF* color_dx;
+    GRAFT_HALF* density_grad;
+    uint32_t* result;       /* [2] active rays, compacted samples */
+    int trainSteps;
+} InerfStepBuffers;
+
+void inerf_default_options(InerfOptions* out);
+size_t inerf_options_size(void);
+Inerf* inerf_create(const InerfOptions* opts);
+void inerf_destroy(Inerf* h);
+int inerf_train(Inerf* h, const float* rays_o, const float* rays_d, const float* rays_depth, const float* rays_sigma,
+                const float* rgb_true, uint32_t num_rays, int* train_step_count, uint32_t* hit_counts,
+                float* rgb_out, hipStream_t stream);
+int inerf_set_learning_rate(Inerf* h, float lr);
+int inerf_set_bg_color(Inerf* h, float r, float g, float b);
+int inerf_set_profiling(Inerf* h, int on);
+int inerf_print_stats(Inerf* h);
+int inerf_update_occupancy(Inerf* h, hipStream_t stream);
+size_t inerf_occupancy_bytes(Inerf* h);
+int inerf_get_occupancy(Inerf* h, uint8_t* host_bits);
+int inerf_set_occupancy(Inerf* h, const uint8_t* host_bits);
+int inerf_get_master_grid(Inerf* h, float* host_cells);
+int inerf_step_buffers(Inerf* h, InerfStepBuffers* out);
+/* Non-owning views of the two heads (tmlp_*_destroy on them is a no-op). */
+TmlpGrid* inerf_density(Inerf* h);
+TmlpNet* inerf_color(Inerf* h);
+
+/* Philox4x32-10 of the occupancy sampler on the host: ctr[4] in, out. */
+void inerf_philox4x32_10(uint32_t* ctr, uint32_t k0, uint32_t k1);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

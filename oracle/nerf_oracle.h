@@ -1,0 +1,111 @@
+/*
+ * CPU oracle for the NeRF side of the 3DMaker training hot path: ray/AABB
+ * setup, cascaded-occupancy DDA with hit-centric compaction, spherical-harmonic
+ * gather, volume compositing with the distortion loss, the color/density
+ * gradient glue and the occupancy bitfield.
+ *
+ * TEST INFRASTRUCTURE ONLY: the checker the HIP path is compared against
+ * (tests/, __graft_entry__.smoke(), bench.py's cpu_baseline leg).  Never linked
+ * into or used as a fallback of the product library.
+ *
+ * Every function restates one reference kernel (file:line relative to the
+ * reference checkout) in IEEE-754 fp32, round-to-nearest-even, no FP
+ * contraction, operation by operation in the reference's order.  Two
+ * deliberate, documented deviations from the reference's device fast-math:
+ *  - e^x is orc_expf() below (Cody-Waite reduction + degree-7 Taylor
+ *    polynomial), the same method the HIP kernels use, instead of CUDA __expf;
+ *  - the cascade index ceil(log2(s)) is taken exactly from frexpf() instead of
+ *    fast-math log2f (processRays.cu:17).
+ * Float3 arrays are tightly packed x,y,z (12-byte stride, like CUDA float3).
+ */
+#ifndef GRAFT_NERF_ORACLE_H
+#define GRAFT_NERF_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ORC_MAX_HITS 1024 /* InstantNerf.h:24 */
+
+/* e^x: x < -87.33654 -> 0 (no subnormal results), NaN -> NaN, overflow -> inf. */
+float orc_expf(float x);
+void orc_expf_array(const float* x, float* y, size_t n);
+
+/* get_cascade (processRays.cu:11-19) with exact ceil(log2). */
+int orc_get_cascade(const float* pos3, const float* aabb_min, const float* aabb_max, int num_cascades);
+
+/* contract_pos (processRays.cu:21-46). */
+void orc_contract_pos(const float* pos3, const float* aabb_min, const float* aabb_max, float* out3);
+
+/* Cells of one cascade's mip pyramid (InstantNerf.cu:286-299): sum over l<levels of (res>>l)^3. */
+uint32_t orc_pyramid_cells(const uint32_t* res3, int levels);
+
+/* compute_ray_aabb_inv_kernel (otherKernels.cu:91-154). */
+void orc_ray_aabb_inv(uint32_t R, const float* rays_o, const float* rays_d,
+                      const float* aabb_min, const float* aabb_max, int num_cascades,
+                      float* d_inv, float* nears, float* fars);
+
+/* march_rays_dda_calc_hits (processRays.cu:626-737): per-ray sample counts. */
+void orc_march_count(uint32_t R, const float* rays_o, const float* rays_d, const float* d_inv,
+                     const float* nears, const float* fars, const uint8_t* bits,
+                     const uint32_t* res3, const float* aabb_min, const float* aabb_max,
+                     int num_cascades, int mip_levels, int K, uint32_t* counts);
+
+/* processRaysHitLinear (processRays.cu:931-1040): count, exclusive scan, cutoff
+ * at batch_size (find_cutoff_ray_kernel :739-769), fill (march_rays_dda_offset
+ * :801-929).  Returns the active ray count; *total_hits receives the number of
+ * compacted samples.  offsets [R] is the exclusive scan of counts over ALL rays.
+ * t_out/ray_idx_out/pos_out (float4 x,y,z,0) are written for the active rays. */
+uint32_t orc_march_hits(uint32_t R, const float* rays_o, const float* rays_d, const float* d_inv,
+                        const float* nears, const float* fars, const uint8_t* bits,
+                        const uint32_t* res3, const float* aabb_min, const float* aabb_max,
+                        int num_cascades, int mip_levels, int K, uint32_t batch_size,
+                        uint32_t* counts, uint32_t* offsets, uint32_t* total_hits,
+                        float* t_out, uint32_t* ray_idx_out, float* pos_out);
+
+/* compute_SH_gather (otherKernels.cu:156-273): color input fp16 [N][32] =
+ * [16 sanitised density logits | 16 real SH (degree <= 3) of the ray direction],
+ * sigma [N] = exp(min(logit0 - bias, 8)). */
+void orc_sh_gather(uint32_t N, const float* dirs, const uint32_t* ray_idx, float density_bias,
+                   const float* density_out, uint16_t* color_in, float* sigma);
+
+/* render_rays_distortion_kernel (compositing.cu:84-213).  depth_prior and
+ * sigma_prior are nullable (depth supervision off); rgb_true and phi nullable. */
+void orc_composite_distortion(uint32_t R, const uint32_t* offsets, const uint32_t* counts,
+                              const float* t, const float* sigma, const float* depth_prior,
+                              const float* sigma_prior, const float* rgb, const float* rgb_true,
+                              float* final_rgb, float* final_depth, float* phi, float* dw,
+                              float* weight_sum, float lambda_dist, float lambda_depth,
+                              const float* bg3);
+
+/* compute_color_grad (otherKernels.cu:303-409) with initialOffset = 0:
+ * fp16 dL/dc [N][3] and fp32 dsigma [N]. */
+void orc_color_grad(uint32_t R, const uint32_t* counts, const uint32_t* offsets, const float* t,
+                    const float* density_out, const float* color_out, const float* phi,
+                    const float* final_rgb, const float* dw, const float* weight_sum,
+                    uint16_t* color_grad, float* dsigma, float loss_scale, float density_bias,
+                    uint32_t total_rays);
+
+/* compute_density_grad (otherKernels.cu:506-562): fp16 [N][16] from the color
+ * head's dL/dinput fp16 [N][32] (first 16) plus dsigma into slot 0. */
+void orc_density_grad(uint32_t N, const float* dsigma, const uint16_t* color_dx, uint16_t* density_grad);
+
+/* updateMasterGrid (otherKernels.cu:677-690): EMA-max with decay. */
+void orc_update_master_grid(const float* tmp, float* master, float decay, uint32_t n);
+
+/* updateOccupancyGrid (otherKernels.cu:700-750): level-0 bits of every cascade
+ * from the master grid; sum is the reduction of master over all cells. */
+void orc_update_occupancy_bits(uint8_t* bits, const float* master, float sum, int total_cells,
+                               int cells_per_cascade, int pyramid_cells, float min_optical_thickness,
+                               float base_voxel);
+
+/* buildMipmaps + bitfield_max_pool (InstantNerf.cu:1177-1204, otherKernels.cu:752-807). */
+void orc_build_mipmaps(uint8_t* bits, const uint32_t* res3, int mip_levels, int num_cascades);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

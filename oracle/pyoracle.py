@@ -18,6 +18,7 @@ _LIB = None
 _f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
 _u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
 _u32p = np.ctypeslib.ndpointer(np.uint32, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
 
 
 def build(force: bool = False) -> str:
@@ -55,6 +56,27 @@ def lib():
             "orc_adam_hash": (None, [_f32p, C.c_void_p, _f32p, _f32p, _f32p, sz,
                                      f, f, f, f, f, f, f]),
             "orc_adam_bias_corrections": (None, [f, f, i, C.POINTER(f), C.POINTER(f)]),
+            "orc_expf": (f, [f]),
+            "orc_expf_array": (None, [_f32p, _f32p, sz]),
+            "orc_get_cascade": (i, [_f32p, _f32p, _f32p, i]),
+            "orc_contract_pos": (None, [_f32p, _f32p, _f32p, _f32p]),
+            "orc_pyramid_cells": (C.c_uint32, [_u32p, i]),
+            "orc_ray_aabb_inv": (None, [C.c_uint32, _f32p, _f32p, _f32p, _f32p, i, _f32p, _f32p, _f32p]),
+            "orc_march_count": (None, [C.c_uint32, _f32p, _f32p, _f32p, _f32p, _f32p, _u8p, _u32p, _f32p,
+                                       _f32p, i, i, i, _u32p]),
+            "orc_march_hits": (C.c_uint32, [C.c_uint32, _f32p, _f32p, _f32p, _f32p, _f32p, _u8p, _u32p, _f32p,
+                                            _f32p, i, i, i, C.c_uint32, _u32p, _u32p, C.POINTER(C.c_uint32),
+                                            _f32p, _u32p, _f32p]),
+            "orc_sh_gather": (None, [C.c_uint32, _f32p, _u32p, f, _f32p, _u16p, _f32p]),
+            "orc_composite_distortion": (None, [C.c_uint32, _u32p, _u32p, _f32p, _f32p, C.c_void_p, C.c_void_p,
+                                                _f32p, C.c_void_p, _f32p, _f32p, C.c_void_p, _f32p, _f32p, f, f,
+                                                _f32p]),
+            "orc_color_grad": (None, [C.c_uint32, _u32p, _u32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p,
+                                      _u16p, _f32p, f, f, C.c_uint32]),
+            "orc_density_grad": (None, [C.c_uint32, _f32p, _u16p, _u16p]),
+            "orc_update_master_grid": (None, [_f32p, _f32p, f, C.c_uint32]),
+            "orc_update_occupancy_bits": (None, [_u8p, _f32p, f, i, i, i, f, f]),
+            "orc_build_mipmaps": (None, [_u8p, _u32p, i, i]),
             "orc_num_threads": (i, []),
             "orc_set_num_threads": (None, [i]),
         }
@@ -197,3 +219,141 @@ def num_threads():
 
 def set_num_threads(n):
     lib().orc_set_num_threads(int(n))
+
+
+# ---------------------------------------------------------------------------
+# NeRF side (oracle/nerf_oracle.h)
+# ---------------------------------------------------------------------------
+MAX_HITS = 1024
+
+
+def _f3(a):
+    return np.ascontiguousarray(a, np.float32).reshape(-1)
+
+
+def expf(x):
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    lib().orc_expf_array(x.ravel(), y.ravel(), x.size)
+    return y
+
+
+def get_cascade(pos, aabb_min, aabb_max, cascades):
+    return lib().orc_get_cascade(_f3(pos), _f3(aabb_min), _f3(aabb_max), int(cascades))
+
+
+def contract_pos(pos, aabb_min, aabb_max):
+    out = np.zeros(3, np.float32)
+    lib().orc_contract_pos(_f3(pos), _f3(aabb_min), _f3(aabb_max), out)
+    return out
+
+
+def pyramid_cells(res, levels):
+    return lib().orc_pyramid_cells(np.ascontiguousarray(res, np.uint32), int(levels))
+
+
+def grid_bytes(res, levels, cascades):
+    return (pyramid_cells(res, levels) * cascades + 7) // 8
+
+
+def ray_aabb_inv(o, d, aabb_min, aabb_max, cascades):
+    o, d = _f3(o), _f3(d)
+    R = o.size // 3
+    di = np.zeros(3 * R, np.float32)
+    nr = np.zeros(R, np.float32)
+    fr = np.zeros(R, np.float32)
+    lib().orc_ray_aabb_inv(R, o, d, _f3(aabb_min), _f3(aabb_max), int(cascades), di, nr, fr)
+    return di.reshape(R, 3), nr, fr
+
+
+def march_count(o, d, di, nears, fars, bits, res, aabb_min, aabb_max, cascades, L, K):
+    R = _f3(o).size // 3
+    cnt = np.zeros(R, np.uint32)
+    lib().orc_march_count(R, _f3(o), _f3(d), _f3(di), _f3(nears), _f3(fars), np.ascontiguousarray(bits, np.uint8),
+                          np.ascontiguousarray(res, np.uint32), _f3(aabb_min), _f3(aabb_max), int(cascades),
+                          int(L), int(K), cnt)
+    return cnt
+
+
+def march_hits(o, d, di, nears, fars, bits, res, aabb_min, aabb_max, cascades, L, K, batch):
+    """processRaysHitLinear -> dict(active, total, counts, offsets, t, ray_idx, pos[N,4])."""
+    R = _f3(o).size // 3
+    cnt = np.zeros(R, np.uint32)
+    off = np.zeros(R, np.uint32)
+    tot = C.c_uint32(0)
+    need = int(march_count(o, d, di, nears, fars, bits, res, aabb_min, aabb_max, cascades, L, K).sum(dtype=np.int64))
+    cap = max(min(int(batch), need), 1)
+    t = np.zeros(cap, np.float32)
+    ri = np.zeros(cap, np.uint32)
+    pos = np.zeros(4 * cap, np.float32)
+    act = lib().orc_march_hits(R, _f3(o), _f3(d), _f3(di), _f3(nears), _f3(fars),
+                               np.ascontiguousarray(bits, np.uint8), np.ascontiguousarray(res, np.uint32),
+                               _f3(aabb_min), _f3(aabb_max), int(cascades), int(L), int(K), int(batch), cnt, off,
+                               C.byref(tot), t, ri, pos)
+    n = tot.value
+    return dict(active=int(act), total=int(n), counts=cnt, offsets=off, t=t[:n], ray_idx=ri[:n],
+                pos=pos.reshape(-1, 4)[:n])
+
+
+def sh_gather(dirs, ray_idx, density_out, bias=0.0):
+    ray_idx = np.ascontiguousarray(ray_idx, np.uint32)
+    N = ray_idx.size
+    cin = np.zeros((N, 32), np.uint16)
+    sig = np.zeros(N, np.float32)
+    lib().orc_sh_gather(N, _f3(dirs), ray_idx, float(bias), _f3(density_out), cin, sig)
+    return cin.view(np.float16), sig
+
+
+def composite(offsets, counts, t, sigma, rgb, rgb_true, lambda_dist, bg, depth_prior=None, sigma_prior=None,
+              lambda_depth=0.0):
+    R = len(counts)
+    frgb = np.zeros(3 * R, np.float32)
+    fdep = np.zeros(R, np.float32)
+    phi = np.zeros(3 * R, np.float32)
+    dw = np.zeros(max(len(t), 1), np.float32)
+    ws = np.zeros(R, np.float32)
+    dp = None if depth_prior is None else _f3(depth_prior)
+    sp = None if sigma_prior is None else _f3(sigma_prior)
+    rt = None if rgb_true is None else _f3(rgb_true)
+    lib().orc_composite_distortion(R, np.ascontiguousarray(offsets, np.uint32), np.ascontiguousarray(counts, np.uint32),
+                                   _f3(t) if len(t) else np.zeros(1, np.float32),
+                                   _f3(sigma) if len(t) else np.zeros(1, np.float32), _vp(dp), _vp(sp),
+                                   _f3(rgb) if len(t) else np.zeros(3, np.float32), _vp(rt), frgb, fdep,
+                                   _vp(phi if rt is not None else None), dw, ws, float(lambda_dist),
+                                   float(lambda_depth), _f3(bg))
+    return dict(rgb=frgb.reshape(R, 3), depth=fdep, phi=phi.reshape(R, 3), dw=dw[:len(t)], weight_sum=ws)
+
+
+def color_grad(counts, offsets, t, density_out, color_out, phi, final_rgb, dw, weight_sum, loss_scale,
+               bias, total_rays):
+    R = len(counts)
+    N = len(t)
+    cg = np.zeros((max(N, 1), 3), np.uint16)
+    ds = np.zeros(max(N, 1), np.float32)
+    lib().orc_color_grad(R, np.ascontiguousarray(counts, np.uint32), np.ascontiguousarray(offsets, np.uint32),
+                         _f3(t), _f3(density_out), _f3(color_out), _f3(phi), _f3(final_rgb), _f3(dw),
+                         _f3(weight_sum), cg.reshape(-1), ds, float(loss_scale), float(bias), int(total_rays))
+    return cg[:N].view(np.float16), ds[:N]
+
+
+def density_grad(dsigma, color_dx):
+    N = len(dsigma)
+    out = np.zeros((N, 16), np.uint16)
+    lib().orc_density_grad(N, _f3(dsigma), _h(color_dx).reshape(-1), out.reshape(-1))
+    return out.view(np.float16)
+
+
+def update_master_grid(tmp, master, decay):
+    lib().orc_update_master_grid(_f3(tmp), master, float(decay), master.size)
+    return master
+
+
+def update_occupancy_bits(bits, master, total_sum, G, S, min_optical, base_voxel):
+    lib().orc_update_occupancy_bits(bits, _f3(master), float(total_sum), int(master.size), int(G), int(S),
+                                    float(min_optical), float(base_voxel))
+    return bits
+
+
+def build_mipmaps(bits, res, L, cascades):
+    lib().orc_build_mipmaps(bits, np.ascontiguousarray(res, np.uint32), int(L), int(cascades))
+    return bits

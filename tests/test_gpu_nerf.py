@@ -1,0 +1,413 @@
+"""GPU parity of the NeRF-side HIP kernels (through the C-ABI) against the oracle.
+
+Bars: ray setup, compaction (counts, offsets, cutoff, sample t / ray index /
+contracted position), SH gather, compositing, colour/density gradient glue,
+occupancy bits and mips are bit-exact (same fp32 operations in the same order,
+one e^x routine on both sides); the fixed-order occupancy sum is within 1e-6
+relative of the fp64 sum; the MLP stages of a full training step are within
+2e-3 abs / 1e-2 rel (fp16 operands, fp32 accumulation).
+"""
+import ctypes as C
+import importlib
+
+import numpy as np
+import pytest
+
+import pyoracle as orc
+from helpers import assert_close, d2h, h2d, make_mlp, pkg, ptr_array
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+scenes = importlib.import_module("3dmaker_amd.scenes")
+
+MN = np.float32([-1.5, -1.5, -1.5])
+MX = np.float32([1.5, 1.5, 1.5])
+
+
+@pytest.fixture(scope="module")
+def dev():
+    assert torch.cuda.is_available(), "GPU tests need cuda:0"
+    return torch.device("cuda:0")
+
+
+def T(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def f3(v):
+    return pkg().Float3(float(v[0]), float(v[1]), float(v[2]))
+
+
+def u3(v):
+    return pkg().Uint3(int(v[0]), int(v[1]), int(v[2]))
+
+
+def bits_eq(a, b):
+    np.testing.assert_array_equal(np.asarray(a).view(np.uint32 if np.asarray(a).dtype == np.float32 else
+                                                     np.asarray(a).dtype),
+                                  np.asarray(b).view(np.uint32 if np.asarray(b).dtype == np.float32 else
+                                                     np.asarray(b).dtype))
+
+
+def random_rays(R, seed, spread=2.5):
+    rng = np.random.default_rng(seed)
+    o = rng.uniform(-spread, spread, (R, 3)).astype(np.float32)
+    d = rng.normal(size=(R, 3)).astype(np.float32)
+    d /= np.linalg.norm(d, axis=1, keepdims=True)
+    k = min(3, R)  # axis-aligned and near-degenerate directions
+    d[:k] = np.float32([[1, 0, 0], [0, -1e-9, 1], [0, 0, -1]])[:k]
+    return o, d
+
+
+# --------------------------------------------------------------------------- ray setup
+
+
+def test_ray_aabb_bit_exact(dev):
+    P = pkg()
+    R, Cc = 10007, 5
+    o, d = random_rays(R, 1, spread=40.0)
+    di = torch.empty((R, 3), device=dev)
+    nr = torch.empty(R, device=dev)
+    fr = torch.empty(R, device=dev)
+    P.launch("launchComputeRayAabbInv", R, T(o, dev), T(d, dev), f3(MN), f3(MX), Cc, di, nr, fr, None)
+    torch.cuda.synchronize()
+    w_di, w_nr, w_fr = orc.ray_aabb_inv(o, d, MN, MX, Cc)
+    bits_eq(di.cpu().numpy(), w_di)
+    bits_eq(nr.cpu().numpy(), w_nr)
+    bits_eq(fr.cpu().numpy(), w_fr)
+
+
+# --------------------------------------------------------------------------- compaction
+
+
+def run_march(dev, o, d, bits, res, Cc, L, K, batch):
+    P = pkg()
+    R = len(o)
+    di, nr, fr = orc.ray_aabb_inv(o, d, MN, MX, Cc)
+    cnt = torch.zeros(R, dtype=torch.int32, device=dev)
+    off = torch.zeros(R, dtype=torch.int32, device=dev)
+    cap = max(batch, 1)
+    pos = torch.zeros((cap, 4), device=dev)
+    ridx = torch.zeros(cap, dtype=torch.int32, device=dev)
+    ts = torch.zeros(cap, device=dev)
+    act_d = torch.zeros(1, dtype=torch.int32, device=dev)
+    total = C.c_uint32(0)
+    keep = [T(a, dev) for a in (o, d, di, nr, fr, bits)]  # alive until the call returns
+    active = P.lib().processRaysHitLinear(R, *[k.data_ptr() for k in keep],
+                                          u3([res] * 3), f3(MN), f3(MX), Cc, L, K, batch, C.byref(total),
+                                          act_d.data_ptr(), cnt.data_ptr(), off.data_ptr(), pos.data_ptr(),
+                                          ridx.data_ptr(), ts.data_ptr(), None, None)
+    P.check()
+    torch.cuda.synchronize()
+    n = total.value
+    got = dict(active=active, total=n, counts=cnt.cpu().numpy().view(np.uint32),
+               offsets=off.cpu().numpy().view(np.uint32), t=ts.cpu().numpy()[:n],
+               ray_idx=ridx.cpu().numpy().view(np.uint32)[:n], pos=pos.cpu().numpy()[:n])
+    assert int(act_d.item()) == active
+    want = orc.march_hits(o, d, di, nr, fr, bits, [res] * 3, MN, MX, Cc, L, K, batch)
+    return got, want
+
+
+def check_march(got, want):
+    assert got["active"] == want["active"] and got["total"] == want["total"]
+    np.testing.assert_array_equal(got["counts"], want["counts"])
+    np.testing.assert_array_equal(got["offsets"], want["offsets"])
+    bits_eq(got["t"], want["t"])
+    np.testing.assert_array_equal(got["ray_idx"], want["ray_idx"])
+    bits_eq(got["pos"], want["pos"])
+
+
+@pytest.mark.parametrize("R,batch_frac,K", [(3001, None, 2), (3001, 0.3, 2), (257, None, 1), (1, None, 3),
+                                            (4096, 0.05, 1)])
+def test_march_small_grid_bit_exact(dev, R, batch_frac, K):
+    print(f"[march] R={R} batch_frac={batch_frac} K={K}", flush=True)
+    res, Cc, L = 32, 3, 4
+    rng = np.random.default_rng(5)
+    per = [rng.random((res, res, res)) < 0.15 for _ in range(Cc)]
+    bits = scenes.pack_grid(per, L)
+    o, d = random_rays(R, 6)
+    full = orc.march_hits(o, d, *orc.ray_aabb_inv(o, d, MN, MX, Cc), bits, [res] * 3, MN, MX, Cc, L, K, 1 << 30)
+    batch = (1 << 30) if batch_frac is None else max(1, int(full["total"] * batch_frac))
+    batch = min(batch, max(full["total"], 1) + 7)
+    got, want = run_march(dev, o, d, bits, res, Cc, L, K, batch)
+    check_march(got, want)
+
+
+def test_march_edge_cases(dev):
+    res, Cc, L = 16, 2, 3
+    rng = np.random.default_rng(7)
+    bits = scenes.pack_grid([rng.random((res,) * 3) < 0.5 for _ in range(Cc)], L)
+    o, d = random_rays(600, 8, spread=1.0)
+    # nothing occupied: every ray is active, no samples
+    got, want = run_march(dev, o, d, np.zeros_like(bits), res, Cc, L, 1, 64)
+    check_march(got, want)
+    assert got["active"] == 600 and got["total"] == 0
+    # the first ray alone exceeds the batch: no active ray
+    first = orc.march_hits(o, d, *orc.ray_aabb_inv(o, d, MN, MX, Cc), bits, [res] * 3, MN, MX, Cc, L, 4, 1 << 20)
+    i0 = int(np.argmax(first["counts"] > 1))
+    got, want = run_march(dev, o[i0:], d[i0:], bits, res, Cc, L, 4, int(first["counts"][i0]) - 1)
+    check_march(got, want)
+    assert got["active"] == 0
+
+
+def test_march_c4_full_scale_bit_exact(dev):
+    """BASELINE C4: 128^3 x 5 cascades, 2^18 camera rays, K = 1, batch 2^18."""
+    print("[march] C4 full scale", flush=True)
+    bits = scenes.occupancy_c4(seed=1)
+    o, d = scenes.rays_c4(1 << 18, seed=2)
+    got, want = run_march(dev, o, d, bits, 128, 5, 4, 1, 1 << 18)
+    check_march(got, want)
+    assert got["total"] > 10000
+
+
+# --------------------------------------------------------------------------- per-sample / per-ray kernels
+
+
+def test_sh_gather_bit_exact(dev):
+    P = pkg()
+    R, N, off = 999, 5000, 7
+    rng = np.random.default_rng(9)
+    dirs = rng.normal(size=(R, 3)).astype(np.float32)
+    dirs /= np.linalg.norm(dirs, axis=1, keepdims=True)
+    idx = rng.integers(0, R, N + off).astype(np.uint32)
+    dout = rng.normal(0, 4, (N, 16)).astype(np.float32)
+    dout[0, :6] = [np.nan, np.inf, -np.inf, 100, -100, 63.99]
+    dout[1, 0] = 30.0
+    cin = torch.zeros((N, 32), dtype=torch.float16, device=dev)
+    sig = torch.zeros(N, device=dev)
+    P.launch("launchComputeSHGather", T(dirs, dev), T(idx, dev), off, N, 0.25, T(dout, dev), cin, sig, None)
+    torch.cuda.synchronize()
+    w_cin, w_sig = orc.sh_gather(dirs, idx[off:], dout, 0.25)
+    np.testing.assert_array_equal(cin.cpu().numpy().view(np.uint16), w_cin.view(np.uint16))
+    bits_eq(sig.cpu().numpy(), w_sig)
+
+
+def ray_batch(R, max_n, seed):
+    rng = np.random.default_rng(seed)
+    cnt = rng.integers(0, max_n + 1, R).astype(np.uint32)
+    off = np.concatenate([[0], np.cumsum(cnt)[:-1]]).astype(np.uint32)
+    N = int(cnt.sum())
+    t = np.zeros(N, np.float32)
+    for r in range(R):
+        if cnt[r]:
+            t[off[r]:off[r] + cnt[r]] = np.sort(rng.uniform(0.05, 4.0, cnt[r])).astype(np.float32)
+    return cnt, off, t, rng
+
+
+@pytest.mark.parametrize("with_depth", [False, True])
+def test_composite_and_color_grad_bit_exact(dev, with_depth):
+    P = pkg()
+    R = 3000
+    cnt, off, t, rng = ray_batch(R, 24, 10)
+    N = len(t)
+    dout = np.zeros((N, 16), np.float32)
+    dout[:, 0] = rng.normal(0.5, 2.0, N)
+    sig = orc.expf(np.minimum(dout[:, 0], 8).astype(np.float32))
+    rgb = rng.random((N, 3)).astype(np.float32)
+    gt = rng.random((R, 3)).astype(np.float32)
+    bg = np.float32([0.9, 0.1, 0.5])
+    dp = rng.uniform(0.5, 3.0, R).astype(np.float32) if with_depth else None
+    sp = rng.uniform(0.05, 0.3, R).astype(np.float32) if with_depth else None
+    if with_depth:
+        dp[::3] = -1.0
+    out = {k: torch.zeros(s, device=dev) for k, s in
+           [("rgb", (R, 3)), ("depth", R), ("phi", (R, 3)), ("dw", max(N, 1)), ("ws", R)]}
+    P.launch("launchVolumeRendering", R, T(off, dev), T(cnt, dev), T(t, dev), T(sig, dev),
+             T(dp, dev) if with_depth else None, T(sp, dev) if with_depth else None, T(rgb, dev), T(gt, dev),
+             out["rgb"], out["depth"], out["phi"], out["dw"], out["ws"], 0.1, 0.05, f3(bg), 0, 0, None)
+    torch.cuda.synchronize()
+    want = orc.composite(off, cnt, t, sig, rgb, gt, 0.1, bg, depth_prior=dp, sigma_prior=sp, lambda_depth=0.05)
+    bits_eq(out["rgb"].cpu().numpy(), want["rgb"])
+    bits_eq(out["depth"].cpu().numpy(), want["depth"])
+    bits_eq(out["phi"].cpu().numpy(), want["phi"])
+    bits_eq(out["dw"].cpu().numpy()[:N], want["dw"])
+    bits_eq(out["ws"].cpu().numpy(), want["weight_sum"])
+
+    cg = torch.zeros((max(N, 1), 3), dtype=torch.float16, device=dev)
+    ds = torch.zeros(max(N, 1), device=dev)
+    P.launch("launchComputeColorGrad", R, 0, T(cnt, dev), T(off, dev), T(t, dev), T(dout, dev), T(rgb, dev),
+             out["phi"], out["rgb"], out["dw"], out["ws"], cg, ds, 128.0, 0.0, 65536, None)
+    torch.cuda.synchronize()
+    w_cg, w_ds = orc.color_grad(cnt, off, t, dout, rgb, want["phi"], want["rgb"], want["dw"], want["weight_sum"],
+                                128.0, 0.0, 65536)
+    np.testing.assert_array_equal(cg.cpu().numpy()[:N].view(np.uint16), w_cg.view(np.uint16))
+    bits_eq(ds.cpu().numpy()[:N], w_ds)
+
+
+def test_density_grad_bit_exact(dev):
+    P = pkg()
+    N = 7777
+    rng = np.random.default_rng(11)
+    cdx = rng.normal(0, 200, (N, 32)).astype(np.float16)
+    cdx[0, :3] = [np.inf, -np.inf, np.nan]
+    ds = rng.normal(0, 100, N).astype(np.float32)
+    ds[1:4] = [1e9, -1e9, np.nan]
+    out = torch.zeros((N, 16), dtype=torch.float16, device=dev)
+    P.launch("launchComputeDensityGrad", N, T(ds, dev), T(cdx, dev), out, None)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy().view(np.uint16), orc.density_grad(ds, cdx).view(np.uint16))
+
+
+# --------------------------------------------------------------------------- occupancy
+
+
+def test_occupancy_update_bit_exact(dev):
+    P = pkg()
+    res, Cc, L = 64, 3, 4
+    G = res ** 3
+    S = orc.pyramid_cells([res] * 3, L)
+    rng = np.random.default_rng(12)
+    master = rng.exponential(0.3, Cc * G).astype(np.float32)
+    master[::101] = -1.0
+    tmp = rng.exponential(0.4, Cc * G).astype(np.float32)
+    d_master = T(master, dev)
+    P.launch("launchUpdateMasterGrid", T(tmp, dev), d_master, 0.95, Cc * G, None)
+    d_sum = torch.zeros(1, device=dev)
+    P.launch("launchReduceSum", d_master, Cc * G, d_sum, None)
+    torch.cuda.synchronize()
+    w_master = orc.update_master_grid(tmp, master.copy(), 0.95)
+    bits_eq(d_master.cpu().numpy(), w_master)
+    s = float(d_sum.item())
+    ref = float(w_master.astype(np.float64).sum())
+    assert abs(s - ref) <= 1e-6 * abs(ref)
+    nbytes = (Cc * S + 7) // 8
+    bits0 = rng.integers(0, 256, nbytes).astype(np.uint8)
+    d_bits = T(bits0, dev)
+    P.launch("launchUpdateOccupancyGrid", d_bits, d_master, d_sum, Cc * G, G, S, 0.01, 3.0 / res, None)
+    P.launch("launchBuildMipmaps", d_bits, u3([res] * 3), L, Cc, None)
+    torch.cuda.synchronize()
+    want = bits0.copy()
+    orc.update_occupancy_bits(want, w_master, np.float32(s), G, S, 0.01, 3.0 / res)
+    orc.build_mipmaps(want, [res] * 3, L, Cc)
+    np.testing.assert_array_equal(d_bits.cpu().numpy(), want)
+
+
+# --------------------------------------------------------------------------- one full InstantNerf step
+
+
+def small_options(P, batch=1 << 14, chunk=4096):
+    o = P.Nerf.default_options()
+    o.gridResolution[:] = [32, 32, 32]
+    o.aabbMin[:] = [-1.5] * 3
+    o.aabbMax[:] = [1.5] * 3
+    o.numCascades = 2
+    o.levelsMipmap = 4
+    o.samplesPerVoxel = 1
+    o.hashTableSize = 1 << 14
+    o.growthFactor = 1.447
+    o.colorHiddenDim = 64
+    o.colorNumLayers = 3
+    o.batchSize = batch
+    o.rayChunkSize = chunk
+    o.renderBatchSize = batch
+    o.learningRate = 1e-2
+    o.beta2 = 0.99
+    o.epsilon = 1e-15
+    o.lossScale = 128.0
+    o.lambdaDist = 0.1
+    o.densityBias = 0.0
+    return o
+
+
+def test_instant_nerf_step_matches_oracle_chain(dev):
+    """One trainWithRaysHit step; every stage checked on the GPU's own inputs."""
+    P = pkg()
+    opts = small_options(P, batch=1 << 16)
+    nerf = P.Nerf(opts)
+    res, Cc, L = 32, 2, 4
+    rng = np.random.default_rng(13)
+    c = (np.arange(res) + 0.5) / res * 3 - 1.5
+    z, y, x = np.meshgrid(c, c, c, indexing="ij")
+    l0 = (x * x + y * y + z * z < 0.8) & (rng.random((res,) * 3) < 0.6)
+    bits = scenes.pack_grid([l0, np.zeros_like(l0)], L)
+    nerf.set_occupancy(bits)
+    # parameters before the step
+    dW = np.zeros(64 * 32 + 16 * 64, np.float32)
+    dB = np.zeros(64 + 16, np.float32)
+    nerf.density.save_weights(dW, dB)
+    table = np.zeros(16 * (1 << 14) * 2, np.float32)
+    nerf.density.save_hashgrid(table)
+    cw_n = 64 * 32 + 64 * 64 + 8 * 64
+    cW = np.zeros(cw_n, np.float32)
+    cB = np.zeros(64 + 64 + 8, np.float32)
+    nerf.color.save_weights(cW, cB)
+
+    R = 1000
+    o, d = scenes.rays_c4(R, n_cams=20, seed=14)
+    gt = rng.random((R, 3)).astype(np.float32)
+    d_o, d_d, d_gt = T(o, dev), T(d, dev), T(gt, dev)
+    rgb_out = torch.zeros((R, 3), device=dev)
+    steps, hits = nerf.train(d_o, d_d, d_gt, R, rgb_out=rgb_out)
+    torch.cuda.synchronize()
+    assert steps == 1 and hits[0] > 1000
+
+    b = nerf.step_buffers()
+    # compaction
+    want = orc.march_hits(o, d, *orc.ray_aabb_inv(o, d, MN, MX, Cc), bits, [res] * 3, MN, MX, Cc, L, 1, 1 << 16)
+    assert want["active"] == R and want["total"] == hits[0]
+    N = hits[0]
+    np.testing.assert_array_equal(d2h(b.num_steps, (R,), np.uint32), want["counts"])
+    np.testing.assert_array_equal(d2h(b.ray_offsets, (R,), np.uint32), want["offsets"])
+    bits_eq(d2h(b.t_sorted, (N,), np.float32), want["t"])
+    np.testing.assert_array_equal(d2h(b.ray_indices, (N,), np.uint32), want["ray_idx"])
+    pos = d2h(b.positions, (N, 4), np.float32)
+    bits_eq(pos, want["pos"])
+    # density head: fused encode + MLP
+    enc = orc.hash_encode(pos, table.astype(np.float16), 1 << 14, 16, 16, 1.447)
+    y_ref, _ = orc.mlp_forward(enc, dW.astype(np.float16), dB, 32, 64, 16, 2)
+    dout = d2h(b.density_out, (N, 16), np.float32)
+    assert_close(dout, y_ref, what="density output")
+    # SH gather on the GPU's density output: bit-exact
+    cin = d2h(b.color_input, (N, 32), np.float16)
+    w_cin, w_sig = orc.sh_gather(d, want["ray_idx"], dout, 0.0)
+    np.testing.assert_array_equal(cin.view(np.uint16), w_cin.view(np.uint16))
+    bits_eq(d2h(b.sigma, (N,), np.float32), w_sig)
+    # color head
+    cout = d2h(b.color_output, (N, 8), np.float32)
+    c_ref, c_acts = orc.mlp_forward(cin, cW.astype(np.float16), cB, 32, 64, 8, 3, out_act=1)
+    assert_close(cout, c_ref, what="color output")
+    # compositing + colour gradient on the GPU's own inputs: bit-exact
+    comp = orc.composite(want["offsets"], want["counts"], want["t"], w_sig, np.ascontiguousarray(cout[:, :3]), gt,
+                         0.1, np.float32([1, 1, 1]))
+    bits_eq(rgb_out.cpu().numpy(), comp["rgb"])
+    bits_eq(d2h(b.phi, (R, 3), np.float32), comp["phi"])
+    bits_eq(d2h(b.dw, (N,), np.float32), comp["dw"])
+    cg, ds = orc.color_grad(want["counts"], want["offsets"], want["t"], dout, np.ascontiguousarray(cout[:, :3]),
+                            comp["phi"], comp["rgb"], comp["dw"], comp["weight_sum"], 128.0, 0.0, R)
+    bits_eq(d2h(b.dsigma, (N,), np.float32), ds)
+    # colour backward (dX) and density gradient
+    cgp = np.zeros((N, 8), np.float16)
+    cgp[:, :3] = cg
+    h = [d2h(p, (N, 64), np.float16) for p in ptr_array(nerf.color.buffers().activations, 3)[1:]]
+    _, _, cdx_ref = orc.mlp_backward(cgp, cin, np.stack(h), cW.astype(np.float16), 32, 64, 8, 3)
+    cdx = d2h(b.color_dx, (N, 32), np.float16)
+    scale = max(1.0, float(np.abs(cdx_ref.astype(np.float32)).max()))
+    assert_close(cdx, cdx_ref, atol=2e-3 * scale, what="color dL/dinput")
+    np.testing.assert_array_equal(d2h(b.density_grad, (N, 16), np.float16).view(np.uint16),
+                                  orc.density_grad(ds, cdx).view(np.uint16))
+    # the step moved the parameters and kept them finite
+    t2 = np.zeros_like(table)
+    nerf.density.save_hashgrid(t2)
+    assert np.isfinite(t2).all() and not np.array_equal(t2, table)
+    nerf.close()
+
+
+def test_instant_nerf_trains_over_many_batches(dev):
+    """Rays spanning several hit batches; occupancy refresh on step 0 and 16; finite, non-empty steps."""
+    P = pkg()
+    opts = small_options(P, batch=1 << 13, chunk=2048)
+    nerf = P.Nerf(opts)
+    R = 40000
+    o, d = scenes.rays_c4(R, n_cams=30, seed=15)
+    scene = scenes.SphereScene(seed=3)
+    gt = scene.render(o, d, steps=128)
+    d_o, d_d, d_gt = T(o, dev), T(d, dev), T(gt, dev)
+    rgb_out = torch.zeros((R, 3), device=dev)
+    steps, hits = nerf.train(d_o, d_d, d_gt, R, rgb_out=rgb_out)
+    torch.cuda.synchronize()
+    assert steps >= 20 and all(h <= (1 << 13) for h in hits)
+    assert np.isfinite(rgb_out.cpu().numpy()).all()
+    occ = nerf.occupancy()
+    assert occ.any()
+    nerf.close()
