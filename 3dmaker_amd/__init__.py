@@ -83,7 +83,7 @@ class StepBuffers(C.Structure):
     _fields_ = [(n, C.c_void_p) for n in (
         "num_steps", "ray_offsets", "positions", "ray_indices", "t_sorted", "density_out", "color_input",
         "color_output", "sigma", "render_rgb", "phi", "dw", "weight_sum", "dsigma", "color_dx", "density_grad",
-        "result")] + [("trainSteps", C.c_int)]
+        "result")] + [("trainSteps", C.c_int), ("windowStart", C.c_uint32)]
 
 
 _vp, _i, _f, _u = C.c_void_p, C.c_int, C.c_float, C.c_uint
@@ -168,6 +168,8 @@ SIGNATURES = {
     "inerf_set_bg_color": (_i, [_vp, _f, _f, _f]),
     "inerf_set_profiling": (_i, [_vp, _i]),
     "inerf_print_stats": (_i, [_vp]),
+    "inerf_stats": (_i, [_vp, C.c_char_p, _i]),
+    "inerf_reset_stats": (_i, [_vp]),
     "inerf_update_occupancy": (_i, [_vp, _vp]),
     "inerf_occupancy_bytes": (C.c_size_t, [_vp]),
     "inerf_get_occupancy": (_i, [_vp, _vp]),
@@ -439,6 +441,20 @@ class Nerf:
 
     def print_stats(self):
         self._c(self._L.inerf_print_stats(self.h))
+
+    def stats(self) -> dict:
+        """{stage: (mean ms, calls)} of the profiled steps (set_profiling(True))."""
+        buf = C.create_string_buffer(8192)
+        self._L.inerf_stats(self.h, buf, 8192)
+        out = {}
+        for ent in buf.value.decode().split(";"):
+            if ent:
+                name, ms, n = ent.split(":")
+                out[name] = (float(ms), int(n))
+        return out
+
+    def reset_stats(self):
+        self._c(self._L.inerf_reset_stats(self.h))
 
     def update_occupancy(self, stream=0):
         self._c(self._L.inerf_update_occupancy(self.h, stream))

@@ -31,8 +31,12 @@ struct NerfBuffers {
     float3* d_inv = nullptr;
     float* nears = nullptr;
     float* fars = nullptr;
-    uint32_t* counts = nullptr;
+    uint32_t* counts = nullptr;      // counts of the cached window [c0, c1)
+    float* t_scratch = nullptr;      // [rayChunkSize x MAX_HITS] sample t of the cached window
     uint32_t* offsets = nullptr;
+    uint32_t cache_c0 = 0, cache_c1 = 0;
+    long cache_version = -1;         // grid version the cached counts were marched on
+    uint32_t* step_counts = nullptr; // window counts of the last step
     uint32_t* block_sums = nullptr;
     uint32_t* result = nullptr;
     uint32_t* h_result = nullptr;  // pinned
@@ -112,6 +116,7 @@ void InstantNerf::freeBuffers()
         dfree(b.nears);
         dfree(b.fars);
         dfree(b.counts);
+        dfree(b.t_scratch);
         dfree(b.offsets);
         dfree(b.block_sums);
         dfree(b.result);
@@ -217,6 +222,7 @@ void InstantNerf::allocate()
     b.nears = dalloc<float>(R);
     b.fars = dalloc<float>(R);
     b.counts = dalloc<uint32_t>(R);
+    b.t_scratch = dalloc<float>(R * (size_t)MAX_HITS);
     b.offsets = dalloc<uint32_t>(R);
     b.block_sums = dalloc<uint32_t>(graft::march_scratch_words((uint32_t)R));
     b.result = dalloc<uint32_t>(2);
@@ -295,6 +301,7 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
 
     uint32_t raysDone = 0;
     int i = 0;
+    b.cache_version = -1;  // new rays: nothing cached
     while (raysDone < numRays) {
         const uint32_t R = std::min<uint32_t>((uint32_t)o.rayChunkSize, numRays - raysDone);
         const float3* co = d_rays_o + raysDone;
@@ -302,10 +309,27 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         const float* cdep = d_rays_depth ? d_rays_depth + raysDone : nullptr;
         const float* csig = d_rays_sigma ? d_rays_sigma + raysDone : nullptr;
 
-        stage("processRays", [&] {
-            graft::ray_aabb_inv(R, co, cd, o.aabbMin, o.aabbMax, o.numCascades, b.d_inv, b.nears, b.fars, stream);
-            graft::march_hits(R, co, cd, b.d_inv, b.nears, b.fars, g, o.samplesPerVoxel, Bn, b.counts, b.offsets,
-                              b.t_sorted, b.ray_idx, b.positions, graft::MarchScratch{b.block_sums, b.result}, stream);
+        // March the window only when it is not covered by the cached march on the current grid.
+        if (b.cache_version != m_gridVersion || raysDone < b.cache_c0 || raysDone + R > b.cache_c1) {
+            stage("rayAabb", [&] {
+                graft::ray_aabb_inv(R, co, cd, o.aabbMin, o.aabbMax, o.numCascades, b.d_inv, b.nears, b.fars,
+                                    stream);
+            });
+            stage("march", [&] {
+                graft::march_store(R, co, cd, b.d_inv, b.nears, b.fars, g, o.samplesPerVoxel, b.counts, b.t_scratch,
+                                   stream);
+            });
+            b.cache_c0 = raysDone;
+            b.cache_c1 = raysDone + R;
+            b.cache_version = m_gridVersion;
+        }
+        const uint32_t woff = raysDone - b.cache_c0;
+        m_windowStart = raysDone;
+        b.step_counts = b.counts + woff;
+        stage("compaction", [&] {
+            graft::march_compact_stored(R, co, cd, g, Bn, b.step_counts, b.t_scratch + (size_t)woff * MAX_HITS,
+                                        b.offsets, b.t_sorted, b.ray_idx, b.positions,
+                                        graft::MarchScratch{b.block_sums, b.result}, stream);
         });
         GRAFT_HIP_CHECK(hipMemcpyAsync(b.h_result, b.result, 2 * sizeof(uint32_t), hipMemcpyDeviceToHost, stream));
         GRAFT_HIP_CHECK(hipEventRecord(b.ev_result, stream));
@@ -346,7 +370,7 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         stage("volumeRendering", [&] {
             graft::CompositeArgs ca{};
             ca.offsets = b.offsets;
-            ca.counts = b.counts;
+            ca.counts = b.step_counts;
             ca.t = b.t_sorted;
             ca.sigma = b.sigma;
             ca.depth_prior = cdep;
@@ -367,7 +391,7 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         stage("colorGrad", [&] {
             graft::ColorGradArgs ga{};
             ga.initial_offset = 0;
-            ga.counts = b.counts;
+            ga.counts = b.step_counts;
             ga.offsets = b.offsets;
             ga.t = b.t_sorted;
             ga.density_out = b.density_out;
@@ -393,6 +417,8 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         stage("densityBwd", [&] {
             graft::mlp_backward(dshape, db.dloss, db.activations, db.fwd_weights, db.w_grad, db.b_grad, db.dx_out,
                                 (int)Bn, stream, d_hits);
+        });
+        stage("hashScatter", [&] {
             graft::hash_scatter(b.meta, db.dx_out, reinterpret_cast<const float*>(b.positions), 4, db.hashtable_grads,
                                 (int)Bn, stream, d_hits);
         });
@@ -444,6 +470,20 @@ void InstantNerf::printStats()
 void InstantNerf::resetStats()
 {
     if (m_buf) B(m_buf).stats.clear();
+}
+
+std::string InstantNerf::statsString() const
+{
+    std::string out;
+    if (!m_buf) return out;
+    const NerfBuffers& b = *static_cast<const NerfBuffers*>(m_buf);
+    char line[160];
+    for (const auto& kv : b.stats) {
+        std::snprintf(line, sizeof(line), "%s:%.6f:%ld;", kv.first.c_str(),
+                      kv.second.first / std::max(1L, kv.second.second), kv.second.second);
+        out += line;
+    }
+    return out;
 }
 
 void InstantNerf::updateOccupancy(hipStream_t stream)
@@ -516,6 +556,7 @@ void InstantNerf::lateOccupancyGridUpdate(hipStream_t stream)
 // EMA-max into the master grid, mean, level-0 bits, mip pyramid (InstantNerf.cu:1150-1171).
 void InstantNerf::finishOccupancyUpdate(hipStream_t stream)
 {
+    m_gridVersion++;
     NerfBuffers& b = B(m_buf);
     const int G = grid_cells(m_opts);
     const int N = m_opts.numCascades * G;
@@ -532,6 +573,7 @@ void InstantNerf::setOccupancyBits(const uint8_t* host_bits)
 {
     if (!m_init) throw std::runtime_error("InstantNerf: init() first");
     GRAFT_HIP_CHECK(hipMemcpy(d_occupancyGrid, host_bits, m_occupancyBytes, hipMemcpyHostToDevice));
+    m_gridVersion++;
 }
 
 InstantNerf::StepBuffers InstantNerf::stepBuffers() const
@@ -539,7 +581,7 @@ InstantNerf::StepBuffers InstantNerf::stepBuffers() const
     if (!m_buf) throw std::runtime_error("InstantNerf: init() first");
     const NerfBuffers& b = *static_cast<const NerfBuffers*>(m_buf);
     StepBuffers s{};
-    s.num_steps = b.counts;
+    s.num_steps = b.step_counts ? b.step_counts : b.counts;
     s.ray_offsets = b.offsets;
     s.positions = b.positions;
     s.ray_indices = b.ray_idx;
@@ -557,6 +599,7 @@ InstantNerf::StepBuffers InstantNerf::stepBuffers() const
     s.density_grad = m_densityMLP->buffers().dloss;
     s.result = b.result;
     s.trainSteps = m_trainSteps;
+    s.windowStart = m_windowStart;
     return s;
 }
 

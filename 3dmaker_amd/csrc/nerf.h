@@ -30,17 +30,20 @@ struct MarchScratch {
 };
 size_t march_scratch_words(uint32_t R);
 
-// processRaysHitLinear (processRays.cu:931-1040) without host round trips:
-// count pass, block-sum scan + cutoff (one workgroup), fill pass.  counts and
-// offsets [R]; t_out, ray_idx, pos_out [batch].  Results stay on the device in
-// scratch.result.
-void march_hits(uint32_t R, const float3* o, const float3* d, const float3* d_inv, const float* nears,
-                const float* fars, const OccGrid& g, int K, uint32_t batch, uint32_t* counts, uint32_t* offsets,
-                float* t_out, uint32_t* ray_idx, float4* pos_out, const MarchScratch& scratch, hipStream_t s);
-
-// Count pass only (march_rays_dda_calc_hits, processRays.cu:626-737).
-void march_count(uint32_t R, const float3* o, const float3* d, const float3* d_inv, const float* nears,
-                 const float* fars, const OccGrid& g, int K, uint32_t* counts, hipStream_t s);
+// processRaysHitLinear (processRays.cu:931-1040) without host round trips, in
+// two halves so that a caller can re-compact one window of rays several times
+// (one hit batch after the other) on an unchanged grid: march_store marches
+// every ray once (march_rays_dda_calc_hits, :626-737) and keeps its sample t
+// values at t_scratch[i * kMaxHits + k] (the values march_rays_dda_offset
+// writes, :896-909); march_compact_stored scans the counts, applies the cutoff
+// (find_cutoff_ray_kernel, :739-769) and gathers the samples, one thread per
+// sample.  counts, offsets [R]; t_out, ray_idx, pos_out [batch]; the active ray
+// and sample counts stay on the device in scratch.result.
+void march_store(uint32_t R, const float3* o, const float3* d, const float3* d_inv, const float* nears,
+                 const float* fars, const OccGrid& g, int K, uint32_t* counts, float* t_scratch, hipStream_t s);
+void march_compact_stored(uint32_t R, const float3* o, const float3* d, const OccGrid& g, uint32_t batch,
+                          const uint32_t* counts, const float* t_scratch, uint32_t* offsets, float* t_out,
+                          uint32_t* ray_idx, float4* pos_out, const MarchScratch& scratch, hipStream_t s);
 
 // compute_SH_gather (otherKernels.cu:156-273).
 void sh_gather(const float3* dirs, const uint32_t* ray_idx, const uint32_t* d_n, uint32_t n_max, float bias,

@@ -13,6 +13,7 @@
 #include "occupancy.h"
 
 #include <cstddef>
+#include <algorithm>
 #include <cstring>
 #include <mutex>
 
@@ -34,6 +35,9 @@ std::mutex g_mu;
 uint32_t* g_scratch = nullptr;
 size_t g_scratch_words = 0;
 
+float* g_tstore = nullptr;
+size_t g_tstore_floats = 0;
+
 uint32_t* march_scratch(size_t words)
 {
     std::lock_guard<std::mutex> lk(g_mu);
@@ -44,6 +48,19 @@ uint32_t* march_scratch(size_t words)
         g_scratch_words = words;
     }
     return g_scratch;
+}
+
+// Per-ray sample store of the one-pass march (MAX_HITS floats per ray).
+float* march_tstore(size_t floats)
+{
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (floats > g_tstore_floats) {
+        if (g_tstore) GRAFT_HIP_CHECK(hipFree(g_tstore));
+        g_tstore = nullptr;
+        GRAFT_HIP_CHECK(hipMalloc(&g_tstore, floats * sizeof(float)));
+        g_tstore_floats = floats;
+    }
+    return g_tstore;
 }
 
 float* reduce_partials()
@@ -87,9 +104,12 @@ int processRaysHitLinear(const uint32_t num_rays, const float3* rays_o, const fl
         (void)d_block_sums;  // sized (R + 1023) / 1024 by reference callers: too small, not used
         uint32_t* sc = march_scratch(words);
         graft::MarchScratch ms{sc, sc + (words - 2)};
-        graft::march_hits(num_rays, rays_o, rays_d, rays_d_inv, nears, fars, g, samplesPerVoxel, (uint32_t)batchSize,
-                          d_num_steps, d_ray_offsets, d_t_sorted, d_ray_indices,
-                          reinterpret_cast<float4*>(d_mlp_positions_batch), ms, stream);
+        float* ts = march_tstore((size_t)std::max<uint32_t>(num_rays, 1) * graft::kMaxHits);
+        graft::march_store(num_rays, rays_o, rays_d, rays_d_inv, nears, fars, g, samplesPerVoxel, d_num_steps, ts,
+                           stream);
+        graft::march_compact_stored(num_rays, rays_o, rays_d, g, (uint32_t)batchSize, d_num_steps, ts, d_ray_offsets,
+                                    d_t_sorted, d_ray_indices, reinterpret_cast<float4*>(d_mlp_positions_batch), ms,
+                                    stream);
         uint32_t h[2] = {0, 0};
         GRAFT_HIP_CHECK(hipMemcpyAsync(h, ms.result, sizeof(h), hipMemcpyDeviceToHost, stream));
         GRAFT_HIP_CHECK(hipStreamSynchronize(stream));
@@ -290,6 +310,18 @@ int inerf_set_bg_color(Inerf* h, float r, float g, float b)
 }
 int inerf_set_profiling(Inerf* h, int on) { return NERF_CALL("inerf_set_profiling", h->nerf.setProfiling(on != 0)); }
 int inerf_print_stats(Inerf* h) { return NERF_CALL("inerf_print_stats", h->nerf.printStats()); }
+int inerf_stats(Inerf* h, char* buf, int len)
+{
+    if (!h) return 0;
+    const std::string s = h->nerf.statsString();
+    if (buf && len > 0) {
+        const size_t n = std::min(s.size(), (size_t)len - 1);
+        std::memcpy(buf, s.data(), n);
+        buf[n] = 0;
+    }
+    return (int)s.size();
+}
+int inerf_reset_stats(Inerf* h) { return NERF_CALL("inerf_reset_stats", h->nerf.resetStats()); }
 int inerf_update_occupancy(Inerf* h, hipStream_t stream)
 {
     return NERF_CALL("inerf_update_occupancy", h->nerf.updateOccupancy(stream));
@@ -337,6 +369,7 @@ int inerf_step_buffers(Inerf* h, InerfStepBuffers* out)
         out->density_grad = b.density_grad;
         out->result = b.result;
         out->trainSteps = b.trainSteps;
+        out->windowStart = b.windowStart;
     });
 }
 TmlpGrid* inerf_density(Inerf* h) { return h ? &h->density : nullptr; }

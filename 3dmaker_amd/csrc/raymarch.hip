@@ -6,20 +6,27 @@
 //   fill pass   march_rays_dda_offset         processRays.cu:801-929
 //
 // The reference orchestrates these with three blocking device->host reads per
-// step (processRays.cu:979-1013).  Here the whole compaction is three launches
-// with no host round trip:
-//   1. count: one thread per ray marches and counts its samples; each
-//      256-ray workgroup reduces its counts (wave shuffles, 4 LDS words) to one
-//      block sum.
-//   2. scan: one workgroup of 1024 threads scans the block sums and, since the
+// step (processRays.cu:979-1013) and marches every ray twice (count, fill).
+// Here the compaction runs without any host round trip and marches once:
+//   1. store: one thread per ray marches and keeps its sample t values in a
+//      rays x 1024 scratch (4 KiB per ray: HBM capacity traded for the second
+//      march) and its sample count;
+//   2. block sums: each 256-ray workgroup reduces its counts;
+//   3. scan: one workgroup of 1024 threads scans the block sums and, since the
 //      inclusive prefix of counts is monotone, finds the one block holding the
 //      cutoff and resolves it ray by ray: active rays = the longest ray prefix
-//      whose samples fit in the batch, exactly the reference rule.
-//   3. fill: each workgroup rescans its 256 counts in LDS, writes the global
-//      exclusive offsets of all rays, and the active rays march again, writing
-//      their samples ray-major at their offsets (the reference order).
-// Both marches run the same code (template on FILL) with the reference's fp32
-// operations in the reference's order, so the two passes agree on every count.
+//      whose samples fit in the batch, exactly the reference rule;
+//   4. offsets: each workgroup rescans its 256 counts in LDS and writes the
+//      exclusive offsets of its rays;
+//   5. gather: one thread per compacted sample finds its ray by binary search
+//      over the offsets, copies its t and contracts o + t d, writing the
+//      samples ray-major (the reference order).
+// The march performs the reference's fp32 operations in the reference's
+// order, so counts, t values and positions are bit-identical to its count and
+// fill passes.  A training step re-compacts the rest of its ray window after
+// every hit batch (processRays.cu:931-1040 runs once per optimizer step); the
+// counts depend only on the occupancy grid, so a caller re-runs steps 2-5 on
+// the stored march until the grid changes.
 #include "nerf.h"
 #include "nerf_math.h"
 
@@ -43,13 +50,12 @@ struct MarchArgs {
     int C, L, K;
     uint32_t R;
     uint32_t total_cells;        // cells of one cascade pyramid
-    uint32_t cap;                // capacity of the sample outputs
     uint32_t mip_off[kMaxMip];   // cells below level l
 };
 
-template <bool FILL>
-__device__ uint32_t march_ray(const MarchArgs& a, uint32_t i, uint32_t out_base, float* __restrict__ t_out,
-                              uint32_t* __restrict__ ridx, float4* __restrict__ pos_out)
+// Marches ray i and stores its sample t values at t_out[i * kMaxHits + k];
+// returns the sample count.
+__device__ uint32_t march_ray(const MarchArgs& a, uint32_t i, float* __restrict__ t_out)
 {
     const float3 o = a.o[i], d = a.d[i], di = a.di[i];
     float t = a.nears[i];
@@ -80,24 +86,12 @@ __device__ uint32_t march_ray(const MarchArgs& a, uint32_t i, uint32_t out_base,
                 level--;
                 continue;
             }
-            if constexpr (!FILL) {
-                hit += (uint32_t)min(a.K, kMaxHits - (int)hit);
-            } else {
-                const float exit_t = fminf(fminf((nbx - o.x) * di.x, (nby - o.y) * di.y), (nbz - o.z) * di.z);
-                const float span = exit_t - t;
-                for (int k = 0; k < a.K; ++k) {
-                    if (hit >= (uint32_t)kMaxHits) break;
-                    const float tk = t + ((float)k + 0.5f) / (float)a.K * span;
-                    const uint32_t w = out_base + hit;
-                    if (w < a.cap) {
-                        t_out[w] = tk;
-                        ridx[w] = i;
-                        pos_out[w] = make_float4(contract_axis(o.x + tk * d.x, a.mn.x, a.mx.x),
-                                                 contract_axis(o.y + tk * d.y, a.mn.y, a.mx.y),
-                                                 contract_axis(o.z + tk * d.z, a.mn.z, a.mx.z), 0.0f);
-                    }
-                    hit++;
-                }
+            const float exit_t = fminf(fminf((nbx - o.x) * di.x, (nby - o.y) * di.y), (nbz - o.z) * di.z);
+            const float span = exit_t - t;
+            for (int k = 0; k < a.K; ++k) {
+                if (hit >= (uint32_t)kMaxHits) break;
+                t_out[(size_t)i * kMaxHits + hit] = t + ((float)k + 0.5f) / (float)a.K * span;
+                hit++;
             }
         }
         const float next_t = fminf(fminf((nbx - o.x) * di.x, (nby - o.y) * di.y), (nbz - o.z) * di.z);
@@ -168,26 +162,6 @@ __global__ __launch_bounds__(256) void ray_aabb_kernel(uint32_t R, const float3*
     }
 }
 
-__global__ __launch_bounds__(256) void march_count_kernel(const MarchArgs a, uint32_t* __restrict__ counts,
-                                                          uint32_t* __restrict__ block_sums)
-{
-    __shared__ uint32_t s_wave[4];
-    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
-    uint32_t n = 0;
-    if (i < a.R) {
-        n = march_ray<false>(a, i, 0, nullptr, nullptr, nullptr);
-        counts[i] = n;
-    }
-    if (block_sums) {
-        uint32_t v = n;
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-        if ((threadIdx.x & 63) == 0) s_wave[threadIdx.x >> 6] = v;
-        __syncthreads();
-        if (threadIdx.x == 0) block_sums[blockIdx.x] = (s_wave[0] + s_wave[1]) + (s_wave[2] + s_wave[3]);
-    }
-}
-
 // One workgroup: block_sums (in) -> exclusive block offsets (out, in place);
 // result = {active rays, compacted samples}.
 __global__ __launch_bounds__(1024) void march_scan_kernel(const uint32_t* __restrict__ counts,
@@ -241,23 +215,75 @@ __global__ __launch_bounds__(1024) void march_scan_kernel(const uint32_t* __rest
     }
 }
 
-__global__ __launch_bounds__(256) void march_fill_kernel(const MarchArgs a, const uint32_t* __restrict__ counts,
-                                                         const uint32_t* __restrict__ block_excl,
-                                                         const uint32_t* __restrict__ result,
-                                                         uint32_t* __restrict__ offsets, float* __restrict__ t_out,
-                                                         uint32_t* __restrict__ ridx, float4* __restrict__ pos_out)
+__global__ __launch_bounds__(256) void march_store_kernel(const MarchArgs a, uint32_t* __restrict__ counts,
+                                                          float* __restrict__ t_scratch)
+{
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i < a.R) counts[i] = march_ray(a, i, t_scratch);
+}
+
+__global__ __launch_bounds__(256) void block_sums_kernel(const uint32_t* __restrict__ counts, uint32_t n,
+                                                         uint32_t* __restrict__ block_sums)
 {
     __shared__ uint32_t s_wave[4];
     const uint32_t i = blockIdx.x * 256 + threadIdx.x;
-    const uint32_t c = i < a.R ? counts[i] : 0u;
+    uint32_t v = i < n ? counts[i] : 0u;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    if ((threadIdx.x & 63) == 0) s_wave[threadIdx.x >> 6] = v;
+    __syncthreads();
+    if (threadIdx.x == 0) block_sums[blockIdx.x] = (s_wave[0] + s_wave[1]) + (s_wave[2] + s_wave[3]);
+}
+
+__global__ __launch_bounds__(256) void offsets_kernel(const uint32_t* __restrict__ counts, uint32_t n,
+                                                      const uint32_t* __restrict__ block_excl,
+                                                      uint32_t* __restrict__ offsets)
+{
+    __shared__ uint32_t s_wave[4];
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t c = i < n ? counts[i] : 0u;
     const uint32_t incl = block_incl_scan<4>(c, s_wave);
-    const uint32_t off = block_excl[blockIdx.x] + (incl - c);
-    if (i < a.R) offsets[i] = off;
-    if (i < result[0]) march_ray<true>(a, i, off, t_out, ridx, pos_out);
+    if (i < n) offsets[i] = block_excl[blockIdx.x] + (incl - c);
+}
+
+// One thread per compacted sample j < result[1]: its ray is the last active
+// ray whose offset is <= j (rays without samples share the next ray's offset);
+// t comes from the stored march, the position is contracted as in the fill.
+struct GatherArgs {
+    const float3* o;
+    const float3* d;
+    float3 mn, mx;
+    const uint32_t* offsets;
+    const float* t_scratch;
+    const uint32_t* result;
+    float* t_out;
+    uint32_t* ridx;
+    float4* pos_out;
+};
+
+__global__ __launch_bounds__(256) void gather_samples_kernel(const GatherArgs g)
+{
+    const uint32_t active = g.result[0], total = g.result[1];
+    for (uint32_t j = blockIdx.x * 256 + threadIdx.x; j < total; j += gridDim.x * 256) {
+        uint32_t lo = 0, hi = active - 1;
+        while (lo < hi) {
+            const uint32_t mid = (lo + hi + 1) >> 1;
+            if (g.offsets[mid] <= j) lo = mid;
+            else hi = mid - 1;
+        }
+        const uint32_t k = j - g.offsets[lo];
+        const float tk = g.t_scratch[(size_t)lo * kMaxHits + k];
+        const float3 o = g.o[lo], d = g.d[lo];
+        g.t_out[j] = tk;
+        g.ridx[j] = lo;
+        g.pos_out[j] = make_float4(contract_axis(o.x + tk * d.x, g.mn.x, g.mx.x),
+                                   contract_axis(o.y + tk * d.y, g.mn.y, g.mx.y),
+                                   contract_axis(o.z + tk * d.z, g.mn.z, g.mx.z), 0.0f);
+    }
 }
 
 MarchArgs march_args(uint32_t R, const float3* o, const float3* d, const float3* di, const float* nears,
-                     const float* fars, const OccGrid& g, int K, uint32_t cap)
+                     const float* fars, const OccGrid& g, int K)
 {
     if (g.mip_levels < 1 || g.mip_levels > kMaxMip) throw std::runtime_error("raymarch: mip levels must be in [1, 16]");
     if (g.cascades < 1) throw std::runtime_error("raymarch: need at least one cascade");
@@ -279,7 +305,6 @@ MarchArgs march_args(uint32_t R, const float3* o, const float3* d, const float3*
     a.L = g.mip_levels;
     a.K = K;
     a.R = R;
-    a.cap = cap;
     for (int l = 0; l < g.mip_levels; l++) a.mip_off[l] = mip_offset(g.res, l);
     a.total_cells = mip_offset(g.res, g.mip_levels);
     return a;
@@ -300,31 +325,33 @@ void ray_aabb_inv(uint32_t R, const float3* o, const float3* d, float3 mn, float
 
 size_t march_scratch_words(uint32_t R) { return (size_t)(R + 255) / 256 + 2; }
 
-void march_count(uint32_t R, const float3* o, const float3* d, const float3* d_inv, const float* nears,
-                 const float* fars, const OccGrid& g, int K, uint32_t* counts, hipStream_t s)
+void march_store(uint32_t R, const float3* o, const float3* d, const float3* d_inv, const float* nears,
+                 const float* fars, const OccGrid& g, int K, uint32_t* counts, float* t_scratch, hipStream_t s)
 {
     if (R == 0) return;
-    const MarchArgs a = march_args(R, o, d, d_inv, nears, fars, g, K, 0);
-    hipLaunchKernelGGL(march_count_kernel, dim3((R + 255) / 256), dim3(256), 0, s, a, counts, nullptr);
+    const MarchArgs a = march_args(R, o, d, d_inv, nears, fars, g, K);
+    hipLaunchKernelGGL(march_store_kernel, dim3((R + 255) / 256), dim3(256), 0, s, a, counts, t_scratch);
     GRAFT_LAUNCH_CHECK();
 }
 
-void march_hits(uint32_t R, const float3* o, const float3* d, const float3* d_inv, const float* nears,
-                const float* fars, const OccGrid& g, int K, uint32_t batch, uint32_t* counts, uint32_t* offsets,
-                float* t_out, uint32_t* ray_idx, float4* pos_out, const MarchScratch& sc, hipStream_t s)
+void march_compact_stored(uint32_t R, const float3* o, const float3* d, const OccGrid& g, uint32_t batch,
+                          const uint32_t* counts, const float* t_scratch, uint32_t* offsets, float* t_out,
+                          uint32_t* ray_idx, float4* pos_out, const MarchScratch& sc, hipStream_t s)
 {
     if (R == 0) {
         GRAFT_HIP_CHECK(hipMemsetAsync(sc.result, 0, 2 * sizeof(uint32_t), s));
         return;
     }
-    const MarchArgs a = march_args(R, o, d, d_inv, nears, fars, g, K, batch);
     const uint32_t nb = (R + 255) / 256;
-    hipLaunchKernelGGL(march_count_kernel, dim3(nb), dim3(256), 0, s, a, counts, sc.block_sums);
+    hipLaunchKernelGGL(block_sums_kernel, dim3(nb), dim3(256), 0, s, counts, R, sc.block_sums);
     GRAFT_LAUNCH_CHECK();
     hipLaunchKernelGGL(march_scan_kernel, dim3(1), dim3(1024), 0, s, counts, sc.block_sums, nb, R, batch, sc.result);
     GRAFT_LAUNCH_CHECK();
-    hipLaunchKernelGGL(march_fill_kernel, dim3(nb), dim3(256), 0, s, a, counts, sc.block_sums, sc.result, offsets,
-                       t_out, ray_idx, pos_out);
+    hipLaunchKernelGGL(offsets_kernel, dim3(nb), dim3(256), 0, s, counts, R, sc.block_sums, offsets);
+    GRAFT_LAUNCH_CHECK();
+    GatherArgs ga{o, d, g.aabb_min, g.aabb_max, offsets, t_scratch, sc.result, t_out, ray_idx, pos_out};
+    const int gblocks = (int)std::max<uint32_t>(1, std::min<uint32_t>((batch + 255) / 256, 4096));
+    hipLaunchKernelGGL(gather_samples_kernel, dim3(gblocks), dim3(256), 0, s, ga);
     GRAFT_LAUNCH_CHECK();
 }
 

@@ -159,3 +159,28 @@ class SphereScene:
             c = self.colour(p)
             out[s:s + chunk] = (w[..., None] * c).sum(1) + (T[:, -1] * (1.0 - alpha[:, -1]))[:, None] * bgv
         return out.astype(np.float32)
+
+    def render_device(self, o, d, near=0.0, far=3.5, steps=1024, bg=(1.0, 1.0, 1.0), chunk=1 << 16):
+        """render() evaluated with torch on the tensors' device (fp32): the same
+        quadrature for ray pools too large for the host."""
+        import torch
+        dev = o.device
+        cen = torch.tensor(self.centres, dtype=torch.float32, device=dev)
+        rad = torch.tensor(self.radii, dtype=torch.float32, device=dev)
+        fr = torch.tensor(self.freq, dtype=torch.float32, device=dev)
+        ph = torch.tensor(self.phase, dtype=torch.float32, device=dev)
+        bgv = torch.tensor(bg, dtype=torch.float32, device=dev)
+        dt = (far - near) / steps
+        ts = near + (torch.arange(steps, device=dev, dtype=torch.float32) + 0.5) * dt
+        out = torch.empty((o.shape[0], 3), dtype=torch.float32, device=dev)
+        for s in range(0, o.shape[0], chunk):
+            oo, dd = o[s:s + chunk], d[s:s + chunk]
+            p = oo[:, None, :] + ts[None, :, None] * dd[:, None, :]
+            sdf = (torch.linalg.norm(p[..., None, :] - cen, dim=-1) - rad).min(dim=-1).values
+            sig = self.sigma_max * torch.sigmoid(-sdf / self.width)
+            alpha = 1.0 - torch.exp(-sig * dt)
+            T = torch.cumprod(torch.cat([torch.ones_like(alpha[:, :1]), 1.0 - alpha[:, :-1]], dim=1), dim=1)
+            w = T * alpha
+            c = 0.5 + 0.5 * torch.sin(p @ fr.T + ph)
+            out[s:s + chunk] = (w[..., None] * c).sum(1) + (T[:, -1] * (1.0 - alpha[:, -1]))[:, None] * bgv
+        return out

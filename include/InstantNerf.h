@@ -8,6 +8,10 @@
 //  - ray/AABB setup, DDA count + scan + cutoff + fill without host round
 //    trips; the compacted sample and active-ray counts stay on the device and
 //    every later kernel of the step reads them there;
+//  - the ray window is marched once per call (and again after each occupancy
+//    refresh), keeping every sample's t in a rayChunkSize x 1024 scratch
+//    (4 KiB per ray); later hit batches of the window re-scan the stored
+//    counts and gather their samples instead of re-marching the window;
 //  - ONE forward of each MLP with activation saves (the reference runs an
 //    inference pre-pass and then the training forward on identical inputs);
 //  - the only device->host read per step is the active-ray count, which the
@@ -128,6 +132,8 @@ public:
     float* masterOccupancyGrid() { return d_masterOccupancyGrid; }
     // Overwrite the occupancy bitfield (host bytes, occupancyBytes() long).
     void setOccupancyBits(const uint8_t* host_bits);
+    // Profiling results as "stage:mean_ms:calls;" entries (setProfiling(true)).
+    std::string statsString() const;
     // Refresh the occupancy grid now (the step loop does it every 16 steps).
     void updateOccupancy(hipStream_t stream = 0);
     // Device buffers of the last step (introspection for tests).
@@ -150,6 +156,7 @@ public:
         half* density_grad;       // [batchSize x 16]
         uint32_t* result;         // [2]: active rays, compacted samples of the last step
         int trainSteps;
+        uint32_t windowStart;     // index of the last step's first ray in the last call's rays
     };
     StepBuffers stepBuffers() const;
 
@@ -166,6 +173,8 @@ private:
     TinyMLPHashGrid* m_densityMLP = nullptr;
     bool m_init = false;
     int m_trainSteps = 0;
+    long m_gridVersion = 0;  // bumped whenever the occupancy bitfield changes
+    uint32_t m_windowStart = 0;
 
     uint8_t* d_occupancyGrid = nullptr;
     size_t m_occupancyBytes = 0;

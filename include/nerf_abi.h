@@ -28,9 +28,11 @@ extern "C" {
 /* processRays.cu:931-1040 (declared InstantNerf.h:509-533).  Count pass,
  * exclusive scan and cutoff at batchSize, fill pass; returns the number of
  * active rays and writes the compacted sample count to *totalHits (host).
- * The three blocking round trips of the reference become one read at the end.
- * d_block_sums is accepted for signature compatibility and not used (the
- * library keeps its own scratch); it may be NULL. */
+ * The three blocking round trips of the reference become one read at the end,
+ * and the second march of the fill pass becomes a gather: the rays are marched
+ * once into a library-owned store of 4 KiB per ray (grown on demand, kept
+ * until the process ends).  d_block_sums is accepted for signature
+ * compatibility and not used; it may be NULL. */
 int processRaysHitLinear(const uint32_t num_rays, const float3* rays_o, const float3* rays_d,
                          const float3* rays_d_inv, const float* nears, const float* fars,
                          const uint8_t* occupancy_grid, const uint3 grid_resolution, const float3 aabb_min,

@@ -56,6 +56,7 @@ typedef struct InerfStepBuffers {
     GRAFT_HALF* density_grad;
     uint32_t* result;       /* [2] active rays, compacted samples */
     int trainSteps;
+    uint32_t windowStart;   /* first ray of the last step within the last call's rays */
 } InerfStepBuffers;
 
 void inerf_default_options(InerfOptions* out);
@@ -69,6 +70,10 @@ int inerf_set_learning_rate(Inerf* h, float lr);
 int inerf_set_bg_color(Inerf* h, float r, float g, float b);
 int inerf_set_profiling(Inerf* h, int on);
 int inerf_print_stats(Inerf* h);
+/* Per-stage profiling means as "stage:mean_ms:calls;..." into buf (NUL-terminated,
+ * truncated to len); returns the full length.  inerf_reset_stats clears them. */
+int inerf_stats(Inerf* h, char* buf, int len);
+int inerf_reset_stats(Inerf* h);
 int inerf_update_occupancy(Inerf* h, hipStream_t stream);
 size_t inerf_occupancy_bytes(Inerf* h);
 int inerf_get_occupancy(Inerf* h, uint8_t* host_bits);

@@ -151,6 +151,24 @@ def test_march_edge_cases(dev):
     assert got["active"] == 0
 
 
+def test_march_successive_windows_like_the_step_loop(dev):
+    """processRaysHitLinear on the rays left after each cutoff (InstantNerf.cu:379-578)."""
+    res, Cc, L = 32, 3, 4
+    rng = np.random.default_rng(21)
+    bits = scenes.pack_grid([rng.random((res,) * 3) < 0.2 for _ in range(Cc)], L)
+    o, d = random_rays(5000, 22)
+    full = orc.march_hits(o, d, *orc.ray_aabb_inv(o, d, MN, MX, Cc), bits, [res] * 3, MN, MX, Cc, L, 1, 1 << 30)
+    batch = max(1024, full["total"] // 5)
+    done, calls = 0, 0
+    while done < len(o):
+        got, want = run_march(dev, o[done:], d[done:], bits, res, Cc, L, 1, batch)
+        check_march(got, want)
+        assert got["active"] > 0
+        done += got["active"]
+        calls += 1
+    assert calls >= 4
+
+
 def test_march_c4_full_scale_bit_exact(dev):
     """BASELINE C4: 128^3 x 5 cascades, 2^18 camera rays, K = 1, batch 2^18."""
     print("[march] C4 full scale", flush=True)
@@ -410,4 +428,32 @@ def test_instant_nerf_trains_over_many_batches(dev):
     assert np.isfinite(rgb_out.cpu().numpy()).all()
     occ = nerf.occupancy()
     assert occ.any()
+    nerf.close()
+
+
+def test_instant_nerf_cached_window_steps_match_oracle(dev):
+    """Later hit batches of one call re-compact the stored march; the last one
+    must equal a fresh oracle march of its window on the grid it used."""
+    P = pkg()
+    opts = small_options(P, batch=8192, chunk=4096)
+    nerf = P.Nerf(opts)
+    R = 1000
+    o, d = scenes.rays_c4(R, n_cams=20, seed=31)
+    gt = np.random.default_rng(32).random((R, 3)).astype(np.float32)
+    steps, hits = nerf.train(T(o, dev), T(d, dev), T(gt, dev), R)
+    torch.cuda.synchronize()
+    assert 3 <= steps < 16, steps  # one occupancy refresh (after step 0): steps 1.. share one grid
+    grid = nerf.occupancy()
+    b = nerf.step_buffers()
+    w0 = b.windowStart
+    assert w0 > 0
+    ow, dw = o[w0:], d[w0:]
+    want = orc.march_hits(ow, dw, *orc.ray_aabb_inv(ow, dw, MN, MX, 2), grid, [32] * 3, MN, MX, 2, 4, 1, 8192)
+    n, Rw = want["total"], len(ow)
+    assert n == hits[-1]
+    np.testing.assert_array_equal(d2h(b.num_steps, (Rw,), np.uint32), want["counts"])
+    np.testing.assert_array_equal(d2h(b.ray_offsets, (Rw,), np.uint32), want["offsets"])
+    bits_eq(d2h(b.t_sorted, (n,), np.float32), want["t"])
+    np.testing.assert_array_equal(d2h(b.ray_indices, (n,), np.uint32), want["ray_idx"])
+    bits_eq(d2h(b.positions, (n, 4), np.float32), want["pos"])
     nerf.close()
