@@ -152,6 +152,8 @@ SIGNATURES = {
     "launchComputeSHGather": (None, [_vp, _vp, _i, _i, _f, _vp, _vp, _vp, _vp]),
     "launchComputeColorGrad": (None, [_u32, _u32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f, _f,
                                       _u32, _vp]),
+    "launchVolumeRenderingColorGrad": (None, [_u32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp,
+                                              _vp, _f, _f, Float3, _vp, _vp, _i, _vp, _f, _f, _u32, _vp]),
     "launchComputeDensityGrad": (None, [_u32, _vp, _vp, _vp, _vp]),
     "launchUpdateMasterGrid": (None, [_vp, _vp, _f, _i, _vp]),
     "launchReduceSum": (None, [_vp, _i, _vp, _vp]),

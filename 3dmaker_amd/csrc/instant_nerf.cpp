@@ -367,7 +367,7 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         });
 
         float* final_rgb = d_rgb_out ? d_rgb_out + (size_t)raysDone * 3 : b.render_rgb;
-        stage("volumeRendering", [&] {
+        stage("renderGrad", [&] {
             graft::CompositeArgs ca{};
             ca.offsets = b.offsets;
             ca.counts = b.step_counts;
@@ -386,9 +386,6 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
             ca.lambda_dist = o.lambdaDist;
             ca.lambda_depth = o.lambdaDepth;
             ca.bg = o.bgColor;
-            graft::composite(ca, d_rays, R, stream);
-        });
-        stage("colorGrad", [&] {
             graft::ColorGradArgs ga{};
             ga.initial_offset = 0;
             ga.counts = b.step_counts;
@@ -407,7 +404,7 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
             ga.loss_scale = o.lossScale;
             ga.bias = o.densityBias;
             ga.total_rays = numRays;
-            graft::color_grad(ga, d_rays, R, stream);
+            graft::render_grad(ca, ga, d_rays, R, stream);
         });
         stage("colorBwd", [&] {
             graft::mlp_backward(cshape, cb.dloss, cb.activations, cb.fwd_weights, cb.w_grad, cb.b_grad, b.color_dx,

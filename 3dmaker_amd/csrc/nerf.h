@@ -91,6 +91,13 @@ struct ColorGradArgs {
 };
 void color_grad(const ColorGradArgs& a, const uint32_t* d_rays, uint32_t rays_max, hipStream_t s);
 
+// composite() followed by color_grad() with initial_offset 0, fused: one wave
+// per ray, bit-identical outputs (compositing.cu:84-213, otherKernels.cu:303-409).
+// The colour-gradient arguments read the weights' gradients from a.dw and
+// final colours, phi and weight sums from the compositing results.
+void render_grad(const CompositeArgs& a, const ColorGradArgs& g, const uint32_t* d_rays, uint32_t rays_max,
+                 hipStream_t s);
+
 // compute_density_grad (otherKernels.cu:506-562).
 void density_grad(const uint32_t* d_n, uint32_t n_max, const float* dsigma, const __half* color_dx,
                   __half* density_grad, hipStream_t s);

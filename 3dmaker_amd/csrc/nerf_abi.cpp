@@ -206,6 +206,57 @@ void launchComputeColorGrad(uint32_t numRays, uint32_t initialOffset, const uint
     });
 }
 
+void launchVolumeRenderingColorGrad(uint32_t num_rays, const uint32_t* d_ray_offsets, const uint32_t* d_num_steps,
+                                    const float* d_t_sorted, const float* d_density_sigma, const float* d_depth_chunk,
+                                    const float* d_sigma_chunk, const float* d_rgb_output, int rgb_stride,
+                                    const float* d_rgb_true, float* d_render_rgb, float* d_render_depth,
+                                    float* d_phi_out, float* d_dw_out, float* d_weight_sum, float lambda_dist,
+                                    float lambda_depth, float3 bg_color, const float* density_mlp_out,
+                                    GRAFT_HALF* custom_color_grad, int grad_stride, float* tmp_dsigma,
+                                    float loss_scale, float densityBias, uint32_t totalRaysBatch, hipStream_t stream)
+{
+    guarded("launchVolumeRenderingColorGrad", [&] {
+        if (rgb_stride < 3 || grad_stride < 3) throw std::runtime_error("row pitches must be >= 3");
+        graft::CompositeArgs a{};
+        a.offsets = d_ray_offsets;
+        a.counts = d_num_steps;
+        a.t = d_t_sorted;
+        a.sigma = d_density_sigma;
+        a.depth_prior = d_depth_chunk;
+        a.sigma_prior = d_sigma_chunk;
+        a.rgb = d_rgb_output;
+        a.rgb_stride = rgb_stride;
+        a.rgb_true = d_rgb_true;
+        a.final_rgb = d_render_rgb;
+        a.final_depth = d_render_depth;
+        a.phi = d_phi_out;
+        a.dw = d_dw_out;
+        a.weight_sum = d_weight_sum;
+        a.lambda_dist = lambda_dist;
+        a.lambda_depth = lambda_depth;
+        a.bg = bg_color;
+        graft::ColorGradArgs g{};
+        g.initial_offset = 0;
+        g.counts = d_num_steps;
+        g.offsets = d_ray_offsets;
+        g.t = d_t_sorted;
+        g.density_out = density_mlp_out;
+        g.color_out = d_rgb_output;
+        g.color_stride = rgb_stride;
+        g.phi = d_phi_out;
+        g.final_rgb = d_render_rgb;
+        g.dw = d_dw_out;
+        g.weight_sum = d_weight_sum;
+        g.color_grad = custom_color_grad;
+        g.grad_stride = grad_stride;
+        g.dsigma = tmp_dsigma;
+        g.loss_scale = loss_scale;
+        g.bias = densityBias;
+        g.total_rays = totalRaysBatch;
+        graft::render_grad(a, g, nullptr, num_rays, stream);
+    });
+}
+
 void launchComputeDensityGrad(uint32_t batch_size, const float* tmp_dsigma, const GRAFT_HALF* custom_dx_out,
                               GRAFT_HALF* custom_density_grad, hipStream_t stream)
 {

@@ -227,6 +227,214 @@ __global__ __launch_bounds__(256) void color_grad_kernel(const ColorGradArgs a, 
     }
 }
 
+// ---------------------------------------------------------------------------
+// Fused compositing + distortion gradient + colour gradient, one wave per ray.
+//
+// The reference runs two thread-per-ray kernels whose loops walk the ray's
+// samples in order (compositing.cu:131-196, otherKernels.cu:346-407).  When a
+// few hundred rays carry ~1000 samples each, such loops are bound by one load
+// latency per sample.  Here the 64 lanes of a wave load and precompute 64
+// samples at a time (exp, disparity warps, clamps), and only the running
+// products and sums walk the samples in order: lane values are broadcast with
+// v_readlane and every lane applies the same fp32 operation sequence as the
+// reference loop, so every output is bit-identical to the two kernels above.
+// Each lane keeps the results that belong to its own sample.
+__device__ __forceinline__ float bcast(float v, int k)
+{
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), k));
+}
+
+__global__ __launch_bounds__(256) void render_grad_kernel(const CompositeArgs a, const ColorGradArgs gr,
+                                                          const uint32_t* __restrict__ d_rays, uint32_t rays_max)
+{
+    const uint32_t R = dev_count(d_rays, rays_max);
+    const int lane = threadIdx.x & 63;
+    const uint32_t r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= R) return;  // whole waves leave together
+    const uint32_t off = a.offsets[r], cnt = a.counts[r];
+    const float d_prior = a.depth_prior ? a.depth_prior[r] : -1.0f;
+    const float s_prior = a.sigma_prior ? a.sigma_prior[r] : -1.0f;
+    const float dwl = (d_prior >= 0) ? a.lambda_depth : 0.0f;
+    const float t_near = (cnt > 0) ? fmaxf(a.t[off], 1e-4f) : 1.0f;
+    const float t_far = (cnt > 0) ? a.t[off + cnt - 1] : 1.0f;
+    const float g_far = 1.0f - t_near / fmaxf(t_far, t_near + 1e-4f);
+    const float inv_g = (g_far > 1e-6f) ? (1.0f / g_far) : 0.0f;
+    const float c23 = 2.0f / 3;
+
+    // ---- compositing: weights, colour, depth, distortion sums ----
+    float T = 1.0f, rc = 0.0f, gc = 0.0f, bc = 0.0f, depth = 0.0f;
+    float dw_g = 0.0f, dwm_g = 0.0f, dls = 0.0f;
+    for (uint32_t base = 0; base < cnt; base += 64) {
+        const uint32_t i = base + lane;
+        const bool valid = i < cnt;
+        const uint32_t idx = off + i;
+        float tt = 0.f, alpha = 0.f, m = 0.f, e = 0.f, cr = 0.f, cg = 0.f, cb = 0.f;
+        if (valid) {
+            tt = a.t[idx];
+            float t_next = (i < cnt - 1) ? a.t[idx + 1] : (tt + 1e-3f);
+            float delta = t_next - tt;
+            if (delta < 0.0f) {
+                delta = 0.0f;
+                t_next = tt;
+            }
+            const float s = disparity_warp(tt, t_near, inv_g);
+            const float s_next = disparity_warp(t_next, t_near, inv_g);
+            m = 0.5f * (s + s_next);
+            alpha = 1.0f - nerf_expf(-a.sigma[idx] * delta);
+            const float* cc = a.rgb + (size_t)a.rgb_stride * idx;
+            cr = cc[0];
+            cg = cc[1];
+            cb = cc[2];
+            const float tx = (tt - d_prior) / s_prior;
+            e = nerf_expf(-0.5f * tx * tx) * delta;
+        }
+        const int nk = (int)min(64u, cnt - base);
+        float w_mine = 0.0f;
+        for (int k = 0; k < nk; k++) {
+            const float al = bcast(alpha, k);
+            const float w = al * T;
+            rc += w * bcast(cr, k);
+            gc += w * bcast(cg, k);
+            bc += w * bcast(cb, k);
+            depth += w * bcast(tt, k);
+            T *= (1.0f - al);
+            dw_g += w;
+            dwm_g += w * bcast(m, k);
+            dls += bcast(e, k);
+            if (lane == k) w_mine = w;
+        }
+        if (valid) a.dw[idx] = w_mine;
+    }
+    dls = 1.0f / fmaxf(dls, 1e-8f);
+
+    // ---- distortion (+ depth prior) gradient per weight ----
+    float wgs = 0.0f, dw_s = 0.0f, dwm_s = 0.0f;
+    for (uint32_t base = 0; base < cnt; base += 64) {
+        const uint32_t i = base + lane;
+        const bool valid = i < cnt;
+        const uint32_t idx = off + i;
+        float w = 0.f, m = 0.f, ds = 0.f, dloss = 0.f;
+        if (valid) {
+            const float tt = a.t[idx];
+            float t_next = (i < cnt - 1) ? a.t[idx + 1] : (tt + 1e-3f);
+            float delta = t_next - tt;
+            if (delta < 0.0f) {
+                delta = 0.0f;
+                t_next = tt;
+            }
+            const float s = disparity_warp(tt, t_near, inv_g);
+            const float s_next = disparity_warp(t_next, t_near, inv_g);
+            m = 0.5f * (s + s_next);
+            ds = s_next - s;
+            if (ds < 0.0f) ds = 0.0f;
+            w = a.dw[idx];
+            const float tx = (tt - d_prior) / s_prior;
+            const float dwt = nerf_expf(-0.5f * tx * tx) * delta * dls;
+            dloss = -dwt * (1.0f / fmaxf(w, 1e-6f));
+        }
+        const int nk = (int)min(64u, cnt - base);
+        float g_mine = 0.0f;
+        for (int k = 0; k < nk; k++) {
+            const float wk = bcast(w, k), mk = bcast(m, k);
+            const float bil = mk * (2 * dw_s - dw_g) + (dwm_g - 2 * dwm_s);
+            const float g = a.lambda_dist * (2 * (bil) + c23 * wk * bcast(ds, k)) + dwl * bcast(dloss, k);
+            wgs += wk * g;
+            dw_s += wk;
+            dwm_s += wk * mk;
+            if (lane == k) g_mine = g;
+        }
+        if (valid) a.dw[idx] = g_mine;
+    }
+    rc += T * a.bg.x;
+    gc += T * a.bg.y;
+    bc += T * a.bg.z;
+    float pr = 0.f, pg = 0.f, pb = 0.f;
+    if (a.rgb_true && a.phi) {
+        pr = 2.0f * (rc - a.rgb_true[3 * r]);
+        pg = 2.0f * (gc - a.rgb_true[3 * r + 1]);
+        pb = 2.0f * (bc - a.rgb_true[3 * r + 2]);
+    }
+    if (lane == 0) {
+        a.weight_sum[r] = wgs;
+        a.final_rgb[3 * r] = rc;
+        a.final_rgb[3 * r + 1] = gc;
+        a.final_rgb[3 * r + 2] = bc;
+        a.final_depth[r] = depth;
+        if (a.rgb_true && a.phi) {
+            a.phi[3 * r] = pr;
+            a.phi[3 * r + 1] = pg;
+            a.phi[3 * r + 2] = pb;
+        }
+    }
+
+    // ---- colour gradient (compute_color_grad with initialOffset 0) ----
+    const uint32_t start = gr.offsets[0];
+    const float bs = 1.0f / (float)gr.total_rays;
+    float T2 = 1.0f, cr2 = 0.0f, cg2 = 0.0f, cb2 = 0.0f, wg = 0.0f;
+    for (uint32_t base = 0; base < cnt; base += 64) {
+        const uint32_t j = base + lane;
+        const bool valid = j < cnt;
+        const uint32_t gi = off + j;
+        const size_t i = (size_t)gi - start;
+        float delta = 0.f, sigma = 0.f, alpha = 0.f, c_r = 0.f, c_g = 0.f, c_b = 0.f, gw = 0.f;
+        if (valid) {
+            const float tc = gr.t[gi];
+            delta = (j == cnt - 1) ? 1e-3f : fmaxf(gr.t[gi + 1] - tc, 0.0f);
+            sigma = nerf_expf(fminf(gr.density_out[16 * i] - gr.bias, 8.0f));
+            alpha = 1.0f - nerf_expf(-sigma * delta);
+            const float* co = gr.color_out + (size_t)gr.color_stride * i;
+            c_r = co[0];
+            c_g = co[1];
+            c_b = co[2];
+            gw = gr.dw[i];
+        }
+        const int nk = (int)min(64u, cnt - base);
+        float Tm = 0.f, wm = 0.f, crm = 0.f, cgm = 0.f, cbm = 0.f, wgm = 0.f;
+        for (int k = 0; k < nk; k++) {
+            const float al = bcast(alpha, k);
+            const float w = T2 * al;
+            cr2 += w * bcast(c_r, k);
+            cg2 += w * bcast(c_g, k);
+            cb2 += w * bcast(c_b, k);
+            wg += w * bcast(gw, k);
+            if (lane == k) {
+                Tm = T2;
+                wm = w;
+                crm = cr2;
+                cgm = cg2;
+                cbm = cb2;
+                wgm = wg;
+            }
+            T2 = T2 * (1.0f - al);
+        }
+        if (valid) {
+            float g_r = pr * wm * c_r * (1.0f - c_r) * gr.loss_scale * bs;
+            float g_g = pg * wm * c_g * (1.0f - c_g) * gr.loss_scale * bs;
+            float g_b = pb * wm * c_b * (1.0f - c_b) * gr.loss_scale * bs;
+            g_r = clamp_half_range(g_r);
+            g_g = clamp_half_range(g_g);
+            g_b = clamp_half_range(g_b);
+            if (g_r != g_r || g_g != g_g || g_b != g_b) g_r = g_g = g_b = 0.0f;
+            _Float16* cgo = reinterpret_cast<_Float16*>(gr.color_grad) + (size_t)gr.grad_stride * i;
+            cgo[0] = to_h(g_r);
+            cgo[1] = to_h(g_g);
+            cgo[2] = to_h(g_b);
+            for (int q = 3; q < gr.grad_stride; q++) cgo[q] = (_Float16)0.0f;
+            const float sr = rc - crm, sg = gc - cgm, sb = bc - cbm;
+            const float dr = Tm * c_r * (1.0f - alpha) - sr;
+            const float dg = Tm * c_g * (1.0f - alpha) - sg;
+            const float db = Tm * c_b * (1.0f - alpha) - sb;
+            const float suffix = wgs - wgm;
+            float dsi = delta * (dr * pr + dg * pg + db * pb);
+            dsi += delta * (gw * Tm * (1.0f - alpha) - suffix);
+            float dsv = dsi * sigma * gr.loss_scale * bs;
+            dsv = clamp_half_range(dsv);
+            if (dsv != dsv) dsv = 0.0f;
+            gr.dsigma[i] = dsv;
+        }
+    }
+}
+
 __global__ __launch_bounds__(256) void density_grad_kernel(const uint32_t* __restrict__ d_n, uint32_t n_max,
                                                            const float* __restrict__ dsigma,
                                                            const _Float16* __restrict__ cdx,
@@ -356,6 +564,16 @@ void color_grad(const ColorGradArgs& a, const uint32_t* d_rays, uint32_t rays_ma
     if (rays_max == 0) return;
     if (a.total_rays == 0) throw std::runtime_error("color grad: totalRaysBatch must be > 0");
     hipLaunchKernelGGL(color_grad_kernel, dim3(blocks_for(rays_max)), dim3(256), 0, s, a, d_rays, rays_max);
+    GRAFT_LAUNCH_CHECK();
+}
+
+void render_grad(const CompositeArgs& a, const ColorGradArgs& g, const uint32_t* d_rays, uint32_t rays_max,
+                 hipStream_t s)
+{
+    if (rays_max == 0) return;
+    if (g.total_rays == 0) throw std::runtime_error("color grad: totalRaysBatch must be > 0");
+    if (!a.rgb_true || !a.phi) throw std::runtime_error("render_grad: needs ground truth and phi");
+    hipLaunchKernelGGL(render_grad_kernel, dim3((rays_max + 3) / 4), dim3(256), 0, s, a, g, d_rays, rays_max);
     GRAFT_LAUNCH_CHECK();
 }
 

@@ -73,6 +73,21 @@ void launchComputeColorGrad(uint32_t numRays, uint32_t initialOffset, const uint
                             float* tmp_dsigma, float loss_scale, float densityBias, uint32_t totalRaysBatch,
                             hipStream_t stream);
 
+/* launchVolumeRendering (training compositor, d_dw_out set) followed by
+ * launchComputeColorGrad with initialOffset 0, as one kernel with one wave per
+ * ray (InstantNerf.cu:463-481 then 526-543; no single reference counterpart).
+ * Outputs are bit-identical to the two launches; colour gradients are written
+ * with row pitch grad_stride (3 in the reference layout, extra columns zeroed)
+ * and colours read with row pitch rgb_stride. */
+void launchVolumeRenderingColorGrad(uint32_t num_rays, const uint32_t* d_ray_offsets, const uint32_t* d_num_steps,
+                                    const float* d_t_sorted, const float* d_density_sigma, const float* d_depth_chunk,
+                                    const float* d_sigma_chunk, const float* d_rgb_output, int rgb_stride,
+                                    const float* d_rgb_true, float* d_render_rgb, float* d_render_depth,
+                                    float* d_phi_out, float* d_dw_out, float* d_weight_sum, float lambda_dist,
+                                    float lambda_depth, float3 bg_color, const float* density_mlp_out,
+                                    GRAFT_HALF* custom_color_grad, int grad_stride, float* tmp_dsigma,
+                                    float loss_scale, float densityBias, uint32_t totalRaysBatch, hipStream_t stream);
+
 /* compute_density_grad (otherKernels.cu:506-562), launched at InstantNerf.cu:552-557. */
 void launchComputeDensityGrad(uint32_t batch_size, const float* tmp_dsigma, const GRAFT_HALF* custom_dx_out,
                               GRAFT_HALF* custom_density_grad, hipStream_t stream);

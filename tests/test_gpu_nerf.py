@@ -253,6 +253,44 @@ def test_composite_and_color_grad_bit_exact(dev, with_depth):
     bits_eq(ds.cpu().numpy()[:N], w_ds)
 
 
+@pytest.mark.parametrize("max_n,R,stride", [(300, 700, 8), (3, 5000, 3), (1024, 40, 3)])
+def test_fused_render_color_grad_bit_exact(dev, max_n, R, stride):
+    """One wave per ray over rays of up to max_n samples (several 64-sample chunks)."""
+    P = pkg()
+    print(f"[render_grad] max_n={max_n} R={R} stride={stride}", flush=True)
+    cnt, off, t, rng = ray_batch(R, max_n, 20 + max_n)
+    N = len(t)
+    dout = np.zeros((N, 16), np.float32)
+    dout[:, 0] = rng.normal(0.5, 2.0, N)
+    sig = orc.expf(np.minimum(dout[:, 0], 8).astype(np.float32))
+    rgb = rng.random((N, stride)).astype(np.float32)
+    gt = rng.random((R, 3)).astype(np.float32)
+    bg = np.float32([0.3, 0.6, 0.9])
+    dp = rng.uniform(0.5, 3.0, R).astype(np.float32)
+    sp = rng.uniform(0.05, 0.3, R).astype(np.float32)
+    dp[::2] = -1.0
+    out = {k: torch.zeros(s, device=dev) for k, s in
+           [("rgb", (R, 3)), ("depth", R), ("phi", (R, 3)), ("dw", max(N, 1)), ("ws", R), ("ds", max(N, 1))]}
+    cg = torch.full((max(N, 1), stride), 7.0, dtype=torch.float16, device=dev)
+    P.launch("launchVolumeRenderingColorGrad", R, T(off, dev), T(cnt, dev), T(t, dev), T(sig, dev), T(dp, dev),
+             T(sp, dev), T(rgb, dev), stride, T(gt, dev), out["rgb"], out["depth"], out["phi"], out["dw"], out["ws"],
+             0.1, 0.05, f3(bg), T(dout, dev), cg, stride, out["ds"], 128.0, 0.0, 4096, None)
+    torch.cuda.synchronize()
+    rgb3 = np.ascontiguousarray(rgb[:, :3])
+    want = orc.composite(off, cnt, t, sig, rgb3, gt, 0.1, bg, depth_prior=dp, sigma_prior=sp, lambda_depth=0.05)
+    bits_eq(out["rgb"].cpu().numpy(), want["rgb"])
+    bits_eq(out["depth"].cpu().numpy(), want["depth"])
+    bits_eq(out["phi"].cpu().numpy(), want["phi"])
+    bits_eq(out["dw"].cpu().numpy()[:N], want["dw"])
+    bits_eq(out["ws"].cpu().numpy(), want["weight_sum"])
+    w_cg, w_ds = orc.color_grad(cnt, off, t, dout, rgb3, want["phi"], want["rgb"], want["dw"], want["weight_sum"],
+                                128.0, 0.0, 4096)
+    got_cg = cg.cpu().numpy()[:N]
+    np.testing.assert_array_equal(got_cg[:, :3].view(np.uint16), w_cg.view(np.uint16))
+    assert (got_cg[:, 3:] == 0).all()
+    bits_eq(out["ds"].cpu().numpy()[:N], w_ds)
+
+
 def test_density_grad_bit_exact(dev):
     P = pkg()
     N = 7777
