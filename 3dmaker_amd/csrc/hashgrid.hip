@@ -107,14 +107,19 @@ __global__ __launch_bounds__(256) void hash_encode_kernel(const GridKernelArgs a
 
 // grads[l][idx][f] += dL/denc[n][2l+f] * w_c for the 8 corners (scatter clamp).
 //
-// fp32 atomics on gfx950 are priced per cache-line request, not per lane, so
-// the lane mapping puts four atomics into one 128-byte line: thread t handles
-// (sample n, level l, x-corner xs, feature f) with f and xs fastest.  The two
-// x-neighbour corners of a level differ only in the low bits of their index
-// (dense: adjacent entries; hashed: x0 ^ (x0 + 1) touches the low bits only,
-// which stays inside one 16-entry = 128-byte block 15 times in 16), so the
-// quad's 4 atomics per y/z corner usually share a line, and each thread issues
-// 4 atomics (its x-corner's four y/z neighbours) instead of 16.
+// fp32 atomics on gfx950 are priced per cache-line request rather than per
+// lane (measured: 4 atomics into one line cost about as much as one), so:
+//  - a wave covers 16 consecutive samples at one level, four lanes per sample
+//    for (x-corner xs, feature f).  The two x-neighbour corners of a level
+//    differ only in the low bits of their index (dense: adjacent entries;
+//    hashed: x0 ^ (x0 + 1) touches the low bits only, inside one 16-entry =
+//    128-byte block 15 times in 16), so the quad's 4 atomics per y/z corner
+//    usually share a line and each lane issues 4 atomics instead of 16;
+//  - samples arrive ray by ray, closely spaced, so at coarse levels
+//    consecutive samples share corners: a segmented sum over the 16 samples
+//    merges equal addresses and only the last lane of each run issues the
+//    atomic.  The products g_f * w_c are unchanged; only the order of the
+//    fp32 additions differs (the reference's red.add order is unspecified).
 __global__ __launch_bounds__(256) void hash_scatter_kernel(const GridKernelArgs a,
                                                            const float* __restrict__ pos,
                                                            const _Float16* __restrict__ denc,
@@ -126,20 +131,42 @@ __global__ __launch_bounds__(256) void hash_scatter_kernel(const GridKernelArgs 
     const uint32_t mask = (uint32_t)a.T - 1u;
     const int D = 2 * a.L;
     const int N = a.d_n ? min((int)*a.d_n, a.N) : a.N;
-    const long long total = (long long)N * a.L * 4;
-    for (long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x; t < total;
-         t += (long long)gridDim.x * blockDim.x) {
-        const int f = (int)(t & 1), xs = (int)((t >> 1) & 1);
-        const long long nl = t >> 2;
-        const int n = (int)(nl / a.L), l = (int)(nl - (long long)n * a.L);
-        const float* pp = pos + (size_t)n * a.pos_stride;
-        const float px = pp[0], py = pp[1], pz = pp[2];
-        const float gv = (float)denc[(size_t)n * D + 2 * l + f];
+    const int lane = threadIdx.x & 63;
+    const int s = lane >> 2, xs = (lane >> 1) & 1, f = lane & 1;
+    const long long nwaves = (long long)((N + 15) / 16) * a.L;
+    const long long wstride = ((long long)gridDim.x * blockDim.x) >> 6;
+    for (long long w = ((long long)blockIdx.x * blockDim.x + threadIdx.x) >> 6; w < nwaves; w += wstride) {
+        const int l = (int)(w % a.L);
+        const int n = (int)((w / a.L) * 16 + s);
+        const bool valid = n < N;
         Corners c;
-        level_corners<true>(px, py, pz, ss[l], sr[l], l < a.dense_start, mask, c);
-        float* lvl = grads + (size_t)l * a.T * 2 + f;
+        float gv = 0.0f;
+        if (valid) {
+            const float* pp = pos + (size_t)n * a.pos_stride;
+            gv = (float)denc[(size_t)n * D + 2 * l + f];
+            level_corners<true>(pp[0], pp[1], pp[2], ss[l], sr[l], l < a.dense_start, mask, c);
+        }
+        float* lvl = grads + (size_t)l * a.T * 2;
 #pragma unroll
-        for (int q = 0; q < 4; q++) atomic_add_f32(lvl + c.idx[xs + 2 * q], gv * c.w[xs + 2 * q]);
+        for (int q = 0; q < 4; q++) {
+            const uint32_t A = valid ? c.idx[xs + 2 * q] + (uint32_t)f : 0xffffffffu;
+            float v = valid ? gv * c.w[xs + 2 * q] : 0.0f;
+            const uint32_t A_prev = __shfl_up(A, 4, 64);
+            bool seen = (s == 0) || (A != A_prev);  // run head
+            const bool head = seen;
+#pragma unroll
+            for (int d = 1; d < 16; d <<= 1) {
+                const float vp = __shfl_up(v, 4 * d, 64);
+                const int sp = __shfl_up((int)seen, 4 * d, 64);
+                if (s >= d && !seen) {
+                    v += vp;
+                    seen = sp != 0;
+                }
+            }
+            const int next_head = __shfl_down((int)head, 4, 64);
+            const bool tail = (s == 15) || next_head;
+            if (valid && tail) atomic_add_f32(lvl + A, v);
+        }
     }
 }
 
@@ -185,7 +212,7 @@ void hash_scatter(const GridMeta& m, const __half* denc, const float* pos, int p
     if (pos_stride < 3) throw std::runtime_error("hash scatter: position stride must be >= 3");
     GridKernelArgs a = grid_args(m, N, pos_stride);
     a.d_n = d_n;
-    const long long threads = (long long)N * m.numLevels * 4;
+    const long long threads = (long long)((N + 15) / 16) * m.numLevels * 64;
     hipLaunchKernelGGL(hash_scatter_kernel, dim3(grid_blocks(threads)), dim3(256), 0, stream, a,
                        pos, reinterpret_cast<const _Float16*>(denc), grads);
     GRAFT_LAUNCH_CHECK();

@@ -65,6 +65,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline leg")
     ap.add_argument("--profile-steps", type=int, default=0,
                     help="run --warmup steps, then this many, and exit (for rocprofv3)")
+    ap.add_argument("--components", action="store_true",
+                    help="only time the stand-alone encode / scatter launches at 2^18 and exit")
     return ap.parse_args()
 
 
@@ -209,6 +211,9 @@ def main():
     dev = torch.device("cuda:0")
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
+    if args.components:
+        print(json.dumps({"components": components(P, torch, stream, sp)}))
+        return
 
     o_np, d_np = scenes.rays_c4(POOL, n_cams=100, seed=2024)
     scene = scenes.SphereScene(seed=5)

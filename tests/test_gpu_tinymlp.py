@@ -60,6 +60,37 @@ def test_encode_bit_exact(dev, N, T_, b, L):
     np.testing.assert_array_equal(got.view(np.uint16), want.view(np.uint16))
 
 
+@pytest.mark.parametrize("N,T_,L,b,dist", [
+    (1 << 18, 1 << 19, 16, (2048 / 16) ** (1 / 15), "uniform"),   # BASELINE C2 backward
+    (1 << 16, 1 << 14, 16, 1.447, "clustered"),                   # collision-heavy dense levels
+    (3000, 1 << 19, 16, 1.3819, "uniform"),                        # small, ragged batch
+    (1 << 16, 1 << 19, 16, 1.3819, "rays"),                        # ray-ordered: merged runs
+])
+def test_scatter_matches_oracle(dev, N, T_, L, b, dist):
+    P = pkg()
+    print(f"[scatter] N={N} T={T_} {dist}", flush=True)
+    rng = np.random.default_rng(17)
+    pos = positions(N, 18)
+    if dist == "clustered":
+        pos[:, :3] = (0.5 + 0.02 * rng.normal(size=(N, 3))).clip(0, 1).astype(np.float32)
+    elif dist == "rays":  # 256 samples per ray, 0.002 apart, as the compaction emits them
+        R = N // 256
+        o = rng.uniform(0.3, 0.7, (R, 1, 3))
+        dirs = rng.normal(size=(R, 1, 3))
+        dirs /= np.linalg.norm(dirs, axis=2, keepdims=True)
+        tt = 0.002 * np.arange(256)[None, :, None]
+        pos[:, :3] = (o + tt * dirs).reshape(N, 3).clip(0, 1).astype(np.float32)
+    denc = rng.normal(0, 1, (N, 2 * L)).astype(np.float16)
+    grads = torch.zeros(L * T_ * 2, dtype=torch.float32, device=dev)
+    grads += 0.5  # the scatter accumulates
+    P.launch("launchHashTableBackwardKernel", T(denc, dev), T(pos, dev), grads, N, T_, L, b, 16, 2, None)
+    torch.cuda.synchronize()
+    want = orc.hash_scatter(pos, denc, T_, L, 16, b) + 0.5
+    got = grads.cpu().numpy()
+    scale = np.abs(want - 0.5).max()
+    assert_close(got, want, atol=2e-6 * scale + 1e-6, rtol=1e-5, what="hash grads")
+
+
 def test_encode_stride3(dev):
     P = pkg()
     N, T_, L, b = 777, 1 << 14, 16, 1.447
