@@ -55,6 +55,18 @@ ENC_BYTES_PER_SAMPLE = 16 + L * 8 * 4 + 2 * L * 2                    # 592
 SCATTER_BYTES_PER_SAMPLE = 16 + 2 * L * 2 + L * 8 * 2 * 8               # 2,128 (pos 16 + denc 64 + RMW 2,048)
 ADAM_BYTES_PER_PARAM = 34
 MLP_FLOP_PER_SAMPLE = 3 * (2 * (32 * 64 + 64 * 16) + 2 * (32 * 64 + 64 * 64 + 64 * 3))  # 56,448 fwd + bwd
+COPY_BYTES = 256 << 20         # copy-calibration kernel of the PMC runs (read and write each)
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary, or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+        return t["kernels"][kernel]["hbm_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def parse():
@@ -79,7 +91,8 @@ def options(P):
     o.densityHiddenDim, o.densityNumLayers = 64, 2
     o.colorHiddenDim, o.colorNumLayers = 64, 3
     o.hashTableSize, o.numLevels, o.growthFactor, o.baseResolution, o.featuresPerLevel = TBL, L, GROWTH, BASE, F
-    o.batchSize, o.rayChunkSize, o.renderBatchSize = BATCH, BATCH, BATCH
+    # NerfTrainer.cu:72-73: rayChunkSize = batchSize / 4, the rays of one trainWithRaysHit call
+    o.batchSize, o.rayChunkSize, o.renderBatchSize = BATCH, RAYS_PER_CALL, BATCH
     o.lambdaDist, o.lambdaDepth = 0.1, 0.0
     o.learningRate, o.beta1, o.beta2, o.epsilon, o.lossScale = LR_MAX, 0.9, 0.999, 1e-8, 128.0
     o.bgColor[:] = [1.0, 1.0, 1.0]
@@ -229,7 +242,15 @@ def main():
     if args.profile_steps:
         hits = tr.run(args.profile_steps)
         torch.cuda.synchronize()
-        print(json.dumps({"profile_steps": len(hits), "mean_samples": float(np.mean(hits))}))
+        # Copy calibration for HBM counters: an elementwise kernel reading and
+        # writing exactly COPY_BYTES each (torch's neg), three launches.
+        src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        print(json.dumps({"profile_steps": len(hits), "mean_samples": float(np.mean(hits)),
+                          "copy_calibration_bytes": COPY_BYTES}))
         return
 
     torch.cuda.synchronize()
@@ -250,6 +271,8 @@ def main():
     st = nerf.stats()
     n_prof = float(np.mean(prof_hits))
     stage_ms = {k: round(v[0], 4) for k, v in st.items()}
+    # per training step: mean per call x calls / steps (march and occupancy run less than once a step)
+    stage_ms_per_step = {k: round(v[0] * v[1] / len(prof_hits), 4) for k, v in st.items()}
 
     # roofline of the dominant kernel of the step (per-call averages of the profiled window)
     candidates = {
@@ -262,8 +285,8 @@ def main():
     dom_ms = st[dom][0]
     ach = algo / (dom_ms * 1e-3) / 1e9
     roofline = {"bound": bound, "kernel": dom, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None, "algorithmic_bytes_per_launch": int(algo),
-                "avg_launch_ms": round(dom_ms, 4)}
+                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom),
+                "algorithmic_bytes_per_launch": int(algo), "avg_launch_ms": round(dom_ms, 4)}
     mlp_ms = sum(st[k][0] for k in ("densityFwd", "colorFwd", "colorBwd", "densityBwd") if k in st)
     mfma_util = MLP_FLOP_PER_SAMPLE * n_prof / (mlp_ms * 1e-3) / 1e12 / FP16_PEAK_TFLOPS if mlp_ms else None
 
@@ -285,6 +308,7 @@ def main():
                    "grid": "128^3 x 5 cascades x 4 mips", "table_size": TBL, "levels": L, "density": "32-64-16",
                    "color": "32-64-64-3", "lambda_dist": 0.1, "loss_scale": 128.0, "occupancy_refresh": 16},
         "stage_ms": stage_ms,
+        "stage_ms_per_step": stage_ms_per_step,
         "hash_encodes_per_s": round(n_prof / (st["densityFwd"][0] * 1e-3), 1) if "densityFwd" in st else None,
         "mfma_util": round(mfma_util, 5) if mfma_util else None,
         "roofline": roofline,
