@@ -32,7 +32,7 @@ struct NerfBuffers {
     float* nears = nullptr;
     float* fars = nullptr;
     uint32_t* counts = nullptr;      // counts of the cached window [c0, c1)
-    float* t_scratch = nullptr;      // [rayChunkSize x MAX_HITS] sample t of the cached window
+    float* t_scratch = nullptr;      // march store of the cached window (march_store_floats(rayChunkSize))
     uint32_t* offsets = nullptr;
     uint32_t cache_c0 = 0, cache_c1 = 0;
     long cache_version = -1;         // grid version the cached counts were marched on
@@ -222,7 +222,7 @@ void InstantNerf::allocate()
     b.nears = dalloc<float>(R);
     b.fars = dalloc<float>(R);
     b.counts = dalloc<uint32_t>(R);
-    b.t_scratch = dalloc<float>(R * (size_t)MAX_HITS);
+    b.t_scratch = dalloc<float>(graft::march_store_floats((uint32_t)R));
     b.offsets = dalloc<uint32_t>(R);
     b.block_sums = dalloc<uint32_t>(graft::march_scratch_words((uint32_t)R));
     b.result = dalloc<uint32_t>(2);
@@ -327,9 +327,8 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         m_windowStart = raysDone;
         b.step_counts = b.counts + woff;
         stage("compaction", [&] {
-            graft::march_compact_stored(R, co, cd, g, Bn, b.step_counts, b.t_scratch + (size_t)woff * MAX_HITS,
-                                        b.offsets, b.t_sorted, b.ray_idx, b.positions,
-                                        graft::MarchScratch{b.block_sums, b.result}, stream);
+            graft::march_compact_stored(R, co, cd, g, Bn, b.step_counts, b.t_scratch, woff, b.offsets, b.t_sorted,
+                                        b.ray_idx, b.positions, graft::MarchScratch{b.block_sums, b.result}, stream);
         });
         GRAFT_HIP_CHECK(hipMemcpyAsync(b.h_result, b.result, 2 * sizeof(uint32_t), hipMemcpyDeviceToHost, stream));
         GRAFT_HIP_CHECK(hipEventRecord(b.ev_result, stream));
@@ -341,11 +340,6 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
                 else lateOccupancyGridUpdate(stream);
             });
         }
-
-        stage("zeroGrad", [&] {
-            m_densityMLP->zero_grad(stream);
-            m_colorMLP->zero_grad(stream);
-        });
 
         stage("densityFwd", [&] {
             graft::FwdInput in;
@@ -407,13 +401,15 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
             graft::render_grad(ca, ga, d_rays, R, stream);
         });
         stage("colorBwd", [&] {
+            // this step's gradient overwrites the last one: no zero_grad pass
             graft::mlp_backward(cshape, cb.dloss, cb.activations, cb.fwd_weights, cb.w_grad, cb.b_grad, b.color_dx,
-                                (int)Bn, stream, d_hits);
+                                (int)Bn, stream, d_hits, /*accumulate=*/false);
         });
         stage("densityGrad", [&] { graft::density_grad(d_hits, Bn, b.dsigma, b.color_dx, db.dloss, stream); });
         stage("densityBwd", [&] {
             graft::mlp_backward(dshape, db.dloss, db.activations, db.fwd_weights, db.w_grad, db.b_grad, db.dx_out,
-                                (int)Bn, stream, d_hits);
+                                (int)Bn, stream, d_hits,
+                                /*accumulate=*/false);
         });
         stage("hashScatter", [&] {
             graft::hash_scatter(b.meta, db.dx_out, reinterpret_cast<const float*>(b.positions), 4, db.hashtable_grads,

@@ -35,10 +35,11 @@ void mlp_forward(const MlpShape& s, const FwdInput& in, const __half* const* W,
                  const float* const* B, __half* const* acts, float* out, int N, int out_act,
                  hipStream_t stream, const uint32_t* d_n = nullptr);
 
-// dW/dB (device arrays of per-layer pointers) are accumulated (+=); dx may be
+// dW/dB (device arrays of per-layer pointers) are accumulated (+=), or
+// overwritten with this batch's gradient when accumulate is false; dx may be
 // nullptr (then layer 0's dX is skipped).
 void mlp_backward(const MlpShape& s, const __half* dy, const __half* const* acts,
                   const __half* const* W, float* const* dW, float* const* dB, __half* dx, int N,
-                  hipStream_t stream, const uint32_t* d_n = nullptr);
+                  hipStream_t stream, const uint32_t* d_n = nullptr, bool accumulate = true);
 
 }  // namespace graft

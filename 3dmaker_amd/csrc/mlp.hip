@@ -371,32 +371,54 @@ struct ReduceParams {
     const float* ws;
     float* const* dW;
     float* const* dB;
-    int nparts, P, layers, wtot;
+    int nparts, P, layers, wtot, accumulate;
     int wofs[kMaxLayers], bofs[kMaxLayers];
 };
 
-__global__ __launch_bounds__(256) void mlp_grad_reduce_kernel(const ReduceParams p)
+// 64 parameters x 16 row groups per 1024-thread block: group q sums partial
+// rows q, q + 16, ... (eight independent loads in flight per thread), then the
+// 16 group sums are added in a fixed tree, so the result is bitwise
+// repeatable.  accumulate = 0 stores the sum (the gradients need no zeroing).
+__global__ __launch_bounds__(1024) void mlp_grad_reduce_kernel(const ReduceParams p)
 {
-    __shared__ float part[4][64];
+    constexpr int kGroups = 16;
+    __shared__ float part[kGroups][64];
     const int pl = threadIdx.x & 63, grp = threadIdx.x >> 6;
     const int idx = blockIdx.x * 64 + pl;
     float s = 0.f;
-    if (idx < p.P)
-        for (int b = grp; b < p.nparts; b += 4) s += p.ws[(size_t)b * p.P + idx];
+    if (idx < p.P) {
+        const float* src = p.ws + idx;
+        int b = grp;
+        for (; b + 7 * kGroups < p.nparts; b += 8 * kGroups) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v[u] = src[(size_t)(b + u * kGroups) * p.P];
+#pragma unroll
+            for (int u = 0; u < 8; u++) s += v[u];
+        }
+        for (; b < p.nparts; b += kGroups) s += src[(size_t)b * p.P];
+    }
     part[grp][pl] = s;
     __syncthreads();
+#pragma unroll
+    for (int h = kGroups / 2; h > 0; h >>= 1) {
+        if (grp < h) part[grp][pl] += part[grp + h][pl];
+        __syncthreads();
+    }
     if (grp == 0 && idx < p.P) {
-        const float tot = (part[0][pl] + part[1][pl]) + (part[2][pl] + part[3][pl]);
+        const float tot = part[0][pl];
+        float* dst;
         if (idx < p.wtot) {
             int l = 0;
             while (l + 1 < p.layers && idx >= p.wofs[l + 1]) l++;
-            p.dW[l][idx - p.wofs[l]] += tot;
+            dst = p.dW[l] + (idx - p.wofs[l]);
         } else {
             const int k = idx - p.wtot;
             int l = 0;
             while (l + 1 < p.layers && k >= p.bofs[l + 1] - p.wtot) l++;
-            p.dB[l][k - (p.bofs[l] - p.wtot)] += tot;
+            dst = p.dB[l] + (k - (p.bofs[l] - p.wtot));
         }
+        *dst = p.accumulate ? *dst + tot : tot;
     }
 }
 
@@ -514,7 +536,7 @@ void mlp_forward(const MlpShape& s, const FwdInput& in, const __half* const* W,
 
 void mlp_backward(const MlpShape& s, const __half* dy, const __half* const* acts,
                   const __half* const* W, float* const* dW, float* const* dB, __half* dx, int N,
-                  hipStream_t stream, const uint32_t* d_n)
+                  hipStream_t stream, const uint32_t* d_n, bool accumulate)
 {
     s.validate();
     if (N <= 0) return;
@@ -568,11 +590,12 @@ void mlp_backward(const MlpShape& s, const __half* dy, const __half* const* acts
     rp.P = p.P;
     rp.layers = s.layers;
     rp.wtot = wtot;
+    rp.accumulate = accumulate ? 1 : 0;
     for (int l = 0; l < s.layers; l++) {
         rp.wofs[l] = p.wofs[l];
         rp.bofs[l] = p.bofs[l];
     }
-    hipLaunchKernelGGL(mlp_grad_reduce_kernel, dim3((p.P + 63) / 64), dim3(256), 0, stream, rp);
+    hipLaunchKernelGGL(mlp_grad_reduce_kernel, dim3((p.P + 63) / 64), dim3(1024), 0, stream, rp);
     GRAFT_LAUNCH_CHECK();
 }
 

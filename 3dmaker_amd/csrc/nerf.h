@@ -8,6 +8,7 @@
 #pragma once
 
 #include "common.h"
+#include "nerf_math.h"
 
 namespace graft {
 
@@ -33,17 +34,29 @@ size_t march_scratch_words(uint32_t R);
 // processRaysHitLinear (processRays.cu:931-1040) without host round trips, in
 // two halves so that a caller can re-compact one window of rays several times
 // (one hit batch after the other) on an unchanged grid: march_store marches
-// every ray once (march_rays_dda_calc_hits, :626-737) and keeps its sample t
-// values at t_scratch[i * kMaxHits + k] (the values march_rays_dda_offset
-// writes, :896-909); march_compact_stored scans the counts, applies the cutoff
-// (find_cutoff_ray_kernel, :739-769) and gathers the samples, one thread per
-// sample.  counts, offsets [R]; t_out, ray_idx, pos_out [batch]; the active ray
-// and sample counts stay on the device in scratch.result.
+// every ray once (march_rays_dda_calc_hits, :626-737) and keeps sample k of ray
+// i (the t value march_rays_dda_offset writes, :896-909) in the march store at
+// march_store_index(i, k); march_compact_stored scans the counts, applies the
+// cutoff (find_cutoff_ray_kernel, :739-769) and gathers the samples, one thread
+// per sample.  counts, offsets [R]; t_out, ray_idx, pos_out [batch]; the active
+// ray and sample counts stay on the device in scratch.result.
+//
+// Store layout: tiles of 64 rays (one wave of the march) x kMaxHits, hit-major
+// inside a tile, so lanes that emit their k-th sample together write one
+// contiguous 256-byte row and a tile's rows fill up in L2 before they leave it.
+__host__ __device__ inline size_t march_store_index(uint32_t ray, uint32_t k)
+{
+    return (size_t)(ray >> 6) * (64 * kMaxHits) + (size_t)k * 64 + (ray & 63);
+}
+inline size_t march_store_floats(uint32_t R) { return (size_t)((R + 63) / 64) * 64 * kMaxHits; }
 void march_store(uint32_t R, const float3* o, const float3* d, const float3* d_inv, const float* nears,
                  const float* fars, const OccGrid& g, int K, uint32_t* counts, float* t_scratch, hipStream_t s);
+// Compacts rays [ray_base, ray_base + R) of the stored march (counts already
+// offset to the window's first ray; o, d too).
 void march_compact_stored(uint32_t R, const float3* o, const float3* d, const OccGrid& g, uint32_t batch,
-                          const uint32_t* counts, const float* t_scratch, uint32_t* offsets, float* t_out,
-                          uint32_t* ray_idx, float4* pos_out, const MarchScratch& scratch, hipStream_t s);
+                          const uint32_t* counts, const float* t_scratch, uint32_t ray_base, uint32_t* offsets,
+                          float* t_out, uint32_t* ray_idx, float4* pos_out, const MarchScratch& scratch,
+                          hipStream_t s);
 
 // compute_SH_gather (otherKernels.cu:156-273).
 void sh_gather(const float3* dirs, const uint32_t* ray_idx, const uint32_t* d_n, uint32_t n_max, float bias,

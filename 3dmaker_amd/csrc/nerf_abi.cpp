@@ -104,10 +104,10 @@ int processRaysHitLinear(const uint32_t num_rays, const float3* rays_o, const fl
         (void)d_block_sums;  // sized (R + 1023) / 1024 by reference callers: too small, not used
         uint32_t* sc = march_scratch(words);
         graft::MarchScratch ms{sc, sc + (words - 2)};
-        float* ts = march_tstore((size_t)std::max<uint32_t>(num_rays, 1) * graft::kMaxHits);
+        float* ts = march_tstore(graft::march_store_floats(std::max<uint32_t>(num_rays, 1)));
         graft::march_store(num_rays, rays_o, rays_d, rays_d_inv, nears, fars, g, samplesPerVoxel, d_num_steps, ts,
                            stream);
-        graft::march_compact_stored(num_rays, rays_o, rays_d, g, (uint32_t)batchSize, d_num_steps, ts, d_ray_offsets,
+        graft::march_compact_stored(num_rays, rays_o, rays_d, g, (uint32_t)batchSize, d_num_steps, ts, 0, d_ray_offsets,
                                     d_t_sorted, d_ray_indices, reinterpret_cast<float4*>(d_mlp_positions_batch), ms,
                                     stream);
         uint32_t h[2] = {0, 0};

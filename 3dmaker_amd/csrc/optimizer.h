@@ -23,6 +23,11 @@ void adam_layers(float* const* w, __half* const* w16, float* const* g, float* co
                  float* const* v, const LayerSizes& sz, int layers, const AdamArgs& a,
                  hipStream_t stream);
 
+// adam_layers over the weights (with fp16 copy) and the biases in one launch.
+void adam_dense(float* const* wW, __half* const* w16, float* const* gW, float* const* mW, float* const* vW,
+                const LayerSizes& szW, float* const* wB, float* const* gB, float* const* mB, float* const* vB,
+                const LayerSizes& szB, int layers, const AdamArgs& a, hipStream_t stream);
+
 void zero_layers(float* const* a, float* const* b, const LayerSizes& sa, const LayerSizes& sb, int layers,
                  hipStream_t stream);
 

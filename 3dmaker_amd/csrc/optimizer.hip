@@ -94,6 +94,39 @@ __global__ __launch_bounds__(256) void adam_layers_kernel(float* const* w, _Floa
     }
 }
 
+// Weights (with fp16 copy) and biases of every layer in one launch:
+// blockIdx.y < layers -> weights of layer y, else biases of layer y - layers.
+struct DenseGroup {
+    float* const* w;
+    _Float16* const* w16;  // nullable
+    float* const* g;
+    float* const* m;
+    float* const* v;
+    LayerSizes sz;
+};
+
+__global__ __launch_bounds__(256) void adam_dense_kernel(const DenseGroup W, const DenseGroup B, int layers,
+                                                         AdamArgs a)
+{
+    const bool is_w = (int)blockIdx.y < layers;
+    const DenseGroup& G = is_w ? W : B;
+    const int l = is_w ? blockIdx.y : blockIdx.y - layers;
+    const int n = G.sz.n[l];
+    float* wl = G.w[l];
+    float* gl = G.g[l];
+    float* ml = G.m[l];
+    float* vl = G.v[l];
+    _Float16* hl = G.w16 ? G.w16[l] : nullptr;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        float mi = ml[i], vi = vl[i], wi = wl[i];
+        adam_update(gl[i], mi, vi, wi, a);
+        ml[i] = mi;
+        vl[i] = vi;
+        wl[i] = wi;
+        if (hl) hl[i] = to_h(wi);
+    }
+}
+
 __global__ __launch_bounds__(256) void zero_layers_kernel(float* const* a, float* const* b, LayerSizes sa,
                                                           LayerSizes sb)
 {
@@ -182,6 +215,19 @@ void adam_layers(float* const* w, __half* const* w16, float* const* g, float* co
     if (mx == 0) return;
     hipLaunchKernelGGL(adam_layers_kernel, dim3((mx + 255) / 256, layers), dim3(256), 0, stream, w,
                        reinterpret_cast<_Float16* const*>(w16), g, m, v, sz, a);
+    GRAFT_LAUNCH_CHECK();
+}
+
+void adam_dense(float* const* wW, __half* const* w16, float* const* gW, float* const* mW, float* const* vW,
+                const LayerSizes& szW, float* const* wB, float* const* gB, float* const* mB, float* const* vB,
+                const LayerSizes& szB, int layers, const AdamArgs& a, hipStream_t stream)
+{
+    int mx = 0;
+    for (int l = 0; l < layers; l++) mx = std::max(mx, std::max(szW.n[l], szB.n[l]));
+    if (mx == 0) return;
+    const DenseGroup W{wW, reinterpret_cast<_Float16* const*>(w16), gW, mW, vW, szW};
+    const DenseGroup B{wB, nullptr, gB, mB, vB, szB};
+    hipLaunchKernelGGL(adam_dense_kernel, dim3((mx + 255) / 256, 2 * layers), dim3(256), 0, stream, W, B, layers, a);
     GRAFT_LAUNCH_CHECK();
 }
 

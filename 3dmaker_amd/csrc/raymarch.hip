@@ -9,8 +9,9 @@
 // step (processRays.cu:979-1013) and marches every ray twice (count, fill).
 // Here the compaction runs without any host round trip and marches once:
 //   1. store: one thread per ray marches and keeps its sample t values in a
-//      rays x 1024 scratch (4 KiB per ray: HBM capacity traded for the second
-//      march) and its sample count;
+//      rays x 1024 store (4 KiB per ray: HBM capacity traded for the second
+//      march; tiles of 64 rays, hit-major, see march_store_index) and its
+//      sample count;
 //   2. block sums: each 256-ray workgroup reduces its counts;
 //   3. scan: one workgroup of 1024 threads scans the block sums and, since the
 //      inclusive prefix of counts is monotone, finds the one block holding the
@@ -53,7 +54,7 @@ struct MarchArgs {
     uint32_t mip_off[kMaxMip];   // cells below level l
 };
 
-// Marches ray i and stores its sample t values at t_out[i * kMaxHits + k];
+// Marches ray i and stores its sample t values at t_out[march_store_index(i, k)];
 // returns the sample count.
 __device__ uint32_t march_ray(const MarchArgs& a, uint32_t i, float* __restrict__ t_out)
 {
@@ -90,7 +91,7 @@ __device__ uint32_t march_ray(const MarchArgs& a, uint32_t i, float* __restrict_
             const float span = exit_t - t;
             for (int k = 0; k < a.K; ++k) {
                 if (hit >= (uint32_t)kMaxHits) break;
-                t_out[(size_t)i * kMaxHits + hit] = t + ((float)k + 0.5f) / (float)a.K * span;
+                t_out[march_store_index(i, hit)] = t + ((float)k + 0.5f) / (float)a.K * span;
                 hit++;
             }
         }
@@ -255,6 +256,7 @@ struct GatherArgs {
     float3 mn, mx;
     const uint32_t* offsets;
     const float* t_scratch;
+    uint32_t ray_base;
     const uint32_t* result;
     float* t_out;
     uint32_t* ridx;
@@ -272,7 +274,7 @@ __global__ __launch_bounds__(256) void gather_samples_kernel(const GatherArgs g)
             else hi = mid - 1;
         }
         const uint32_t k = j - g.offsets[lo];
-        const float tk = g.t_scratch[(size_t)lo * kMaxHits + k];
+        const float tk = g.t_scratch[march_store_index(g.ray_base + lo, k)];
         const float3 o = g.o[lo], d = g.d[lo];
         g.t_out[j] = tk;
         g.ridx[j] = lo;
@@ -335,8 +337,8 @@ void march_store(uint32_t R, const float3* o, const float3* d, const float3* d_i
 }
 
 void march_compact_stored(uint32_t R, const float3* o, const float3* d, const OccGrid& g, uint32_t batch,
-                          const uint32_t* counts, const float* t_scratch, uint32_t* offsets, float* t_out,
-                          uint32_t* ray_idx, float4* pos_out, const MarchScratch& sc, hipStream_t s)
+                          const uint32_t* counts, const float* t_scratch, uint32_t ray_base, uint32_t* offsets,
+                          float* t_out, uint32_t* ray_idx, float4* pos_out, const MarchScratch& sc, hipStream_t s)
 {
     if (R == 0) {
         GRAFT_HIP_CHECK(hipMemsetAsync(sc.result, 0, 2 * sizeof(uint32_t), s));
@@ -349,7 +351,7 @@ void march_compact_stored(uint32_t R, const float3* o, const float3* d, const Oc
     GRAFT_LAUNCH_CHECK();
     hipLaunchKernelGGL(offsets_kernel, dim3(nb), dim3(256), 0, s, counts, R, sc.block_sums, offsets);
     GRAFT_LAUNCH_CHECK();
-    GatherArgs ga{o, d, g.aabb_min, g.aabb_max, offsets, t_scratch, sc.result, t_out, ray_idx, pos_out};
+    GatherArgs ga{o, d, g.aabb_min, g.aabb_max, offsets, t_scratch, ray_base, sc.result, t_out, ray_idx, pos_out};
     const int gblocks = (int)std::max<uint32_t>(1, std::min<uint32_t>((batch + 255) / 256, 4096));
     hipLaunchKernelGGL(gather_samples_kernel, dim3(gblocks), dim3(256), 0, s, ga);
     GRAFT_LAUNCH_CHECK();

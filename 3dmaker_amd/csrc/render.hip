@@ -230,18 +230,98 @@ __global__ __launch_bounds__(256) void color_grad_kernel(const ColorGradArgs a, 
 // ---------------------------------------------------------------------------
 // Fused compositing + distortion gradient + colour gradient, one wave per ray.
 //
-// The reference runs two thread-per-ray kernels whose loops walk the ray's
-// samples in order (compositing.cu:131-196, otherKernels.cu:346-407).  When a
-// few hundred rays carry ~1000 samples each, such loops are bound by one load
-// latency per sample.  Here the 64 lanes of a wave load and precompute 64
-// samples at a time (exp, disparity warps, clamps), and only the running
-// products and sums walk the samples in order: lane values are broadcast with
-// v_readlane and every lane applies the same fp32 operation sequence as the
-// reference loop, so every output is bit-identical to the two kernels above.
-// Each lane keeps the results that belong to its own sample.
-__device__ __forceinline__ float bcast(float v, int k)
+// The reference runs two thread-per-ray kernels whose loops walk a ray's
+// samples in order (compositing.cu:131-196, otherKernels.cu:346-407).  A step
+// holds a few hundred to a few thousand rays of up to 1024 samples, so such
+// loops are bound by the longest ray: one load latency and a chain of
+// dependent fp32 operations per sample.
+//
+// Here one wave takes one ray and every lane owns a run of n = ceil(cnt / 64)
+// consecutive samples.  The running transmittance T and the running sums of
+// the reference loops become two-level scans: each lane folds its own run
+// (products of 1 - alpha, sums of weight x value relative to its run's start),
+// a 64-lane scan combines the runs, and a second pass over the run emits the
+// per-sample results from the lane's prefix.  Four passes over the run:
+//   A  T and the weighted sums of the compositing (colour, depth, sum w,
+//      sum w m, sum of depth-prior terms);
+//   B  the distortion (+ depth-prior) gradient per weight, from exclusive
+//      prefix sums of w and w m (compositing.cu:177-195);
+//   C  the colour gradient's own transmittance and the weighted sums of
+//      colour and of w g (otherKernels.cu:346-366);
+//   D  colour gradient and d sigma per sample (otherKernels.cu:367-407).
+// The arithmetic per sample is the reference's; only the association of the
+// products and sums differs (scans instead of left-to-right folds), so
+// results agree with the serial kernels above to fp32 rounding.
+__device__ __forceinline__ float wave_sum(float v)
 {
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), k));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;  // identical in every lane: each pairwise add is commutative
+}
+
+__device__ __forceinline__ float wave_excl_sum(float v, int lane)
+{
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const float u = __shfl_up(v, o, 64);
+        if (lane >= o) v += u;
+    }
+    const float e = __shfl_up(v, 1, 64);
+    return lane == 0 ? 0.0f : e;
+}
+
+__device__ __forceinline__ float wave_excl_prod(float v, int lane)
+{
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const float u = __shfl_up(v, o, 64);
+        if (lane >= o) v *= u;
+    }
+    const float e = __shfl_up(v, 1, 64);
+    return lane == 0 ? 1.0f : e;
+}
+
+// Per-sample terms of the compositing pass (compositing.cu:131-160).
+struct CompSample {
+    float t, delta, m, ds, alpha, e;
+};
+
+__device__ __forceinline__ CompSample comp_sample(const CompositeArgs& a, uint32_t idx, uint32_t i, uint32_t cnt,
+                                                  float t_near, float inv_g, float d_prior, float s_prior)
+{
+    CompSample c;
+    c.t = a.t[idx];
+    float t_next = (i < cnt - 1) ? a.t[idx + 1] : (c.t + 1e-3f);
+    c.delta = t_next - c.t;
+    if (c.delta < 0.0f) {
+        c.delta = 0.0f;
+        t_next = c.t;
+    }
+    const float s = disparity_warp(c.t, t_near, inv_g);
+    const float s_next = disparity_warp(t_next, t_near, inv_g);
+    c.m = 0.5f * (s + s_next);
+    c.ds = s_next - s;
+    if (c.ds < 0.0f) c.ds = 0.0f;
+    c.alpha = 1.0f - nerf_expf(-a.sigma[idx] * c.delta);
+    const float tx = (c.t - d_prior) / s_prior;
+    c.e = nerf_expf(-0.5f * tx * tx) * c.delta;
+    return c;
+}
+
+// Per-sample terms of the colour-gradient pass (otherKernels.cu:349-356).
+struct GradSample {
+    float delta, sigma, alpha;
+};
+
+__device__ __forceinline__ GradSample grad_sample(const ColorGradArgs& g, uint32_t gi, size_t i, uint32_t j,
+                                                  uint32_t cnt)
+{
+    GradSample s;
+    const float tc = g.t[gi];
+    s.delta = (j == cnt - 1) ? 1e-3f : fmaxf(g.t[gi + 1] - tc, 0.0f);
+    s.sigma = nerf_expf(fminf(g.density_out[16 * i] - g.bias, 8.0f));
+    s.alpha = 1.0f - nerf_expf(-s.sigma * s.delta);
+    return s;
 }
 
 __global__ __launch_bounds__(256) void render_grad_kernel(const CompositeArgs a, const ColorGradArgs gr,
@@ -249,168 +329,115 @@ __global__ __launch_bounds__(256) void render_grad_kernel(const CompositeArgs a,
 {
     const uint32_t R = dev_count(d_rays, rays_max);
     const int lane = threadIdx.x & 63;
-    const uint32_t r = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (r >= R) return;  // whole waves leave together
-    const uint32_t off = a.offsets[r], cnt = a.counts[r];
-    const float d_prior = a.depth_prior ? a.depth_prior[r] : -1.0f;
-    const float s_prior = a.sigma_prior ? a.sigma_prior[r] : -1.0f;
-    const float dwl = (d_prior >= 0) ? a.lambda_depth : 0.0f;
-    const float t_near = (cnt > 0) ? fmaxf(a.t[off], 1e-4f) : 1.0f;
-    const float t_far = (cnt > 0) ? a.t[off + cnt - 1] : 1.0f;
-    const float g_far = 1.0f - t_near / fmaxf(t_far, t_near + 1e-4f);
-    const float inv_g = (g_far > 1e-6f) ? (1.0f / g_far) : 0.0f;
+    const uint32_t nwaves = gridDim.x * 4;
+    const uint32_t start = gr.offsets[0];
+    const float bs = 1.0f / (float)gr.total_rays;
     const float c23 = 2.0f / 3;
+    for (uint32_t r = blockIdx.x * 4 + (threadIdx.x >> 6); r < R; r += nwaves) {  // wave-uniform
+        const uint32_t off = a.offsets[r], cnt = a.counts[r];
+        const float d_prior = a.depth_prior ? a.depth_prior[r] : -1.0f;
+        const float s_prior = a.sigma_prior ? a.sigma_prior[r] : -1.0f;
+        const float dwl = (d_prior >= 0) ? a.lambda_depth : 0.0f;
+        const float t_near = (cnt > 0) ? fmaxf(a.t[off], 1e-4f) : 1.0f;
+        const float t_far = (cnt > 0) ? a.t[off + cnt - 1] : 1.0f;
+        const float g_far = 1.0f - t_near / fmaxf(t_far, t_near + 1e-4f);
+        const float inv_g = (g_far > 1e-6f) ? (1.0f / g_far) : 0.0f;
+        const uint32_t run = (cnt + 63) / 64;
+        const uint32_t k0 = min((uint32_t)lane * run, cnt), k1 = min(k0 + run, cnt);
 
-    // ---- compositing: weights, colour, depth, distortion sums ----
-    float T = 1.0f, rc = 0.0f, gc = 0.0f, bc = 0.0f, depth = 0.0f;
-    float dw_g = 0.0f, dwm_g = 0.0f, dls = 0.0f;
-    for (uint32_t base = 0; base < cnt; base += 64) {
-        const uint32_t i = base + lane;
-        const bool valid = i < cnt;
-        const uint32_t idx = off + i;
-        float tt = 0.f, alpha = 0.f, m = 0.f, e = 0.f, cr = 0.f, cg = 0.f, cb = 0.f;
-        if (valid) {
-            tt = a.t[idx];
-            float t_next = (i < cnt - 1) ? a.t[idx + 1] : (tt + 1e-3f);
-            float delta = t_next - tt;
-            if (delta < 0.0f) {
-                delta = 0.0f;
-                t_next = tt;
-            }
-            const float s = disparity_warp(tt, t_near, inv_g);
-            const float s_next = disparity_warp(t_next, t_near, inv_g);
-            m = 0.5f * (s + s_next);
-            alpha = 1.0f - nerf_expf(-a.sigma[idx] * delta);
+        // ---- A: transmittance and weighted sums of the compositing ----
+        float tl = 1.0f, sr = 0.f, sg = 0.f, sb = 0.f, sd = 0.f, sw = 0.f, swm = 0.f, se = 0.f;
+        for (uint32_t i = k0; i < k1; i++) {
+            const uint32_t idx = off + i;
+            const CompSample c = comp_sample(a, idx, i, cnt, t_near, inv_g, d_prior, s_prior);
             const float* cc = a.rgb + (size_t)a.rgb_stride * idx;
-            cr = cc[0];
-            cg = cc[1];
-            cb = cc[2];
-            const float tx = (tt - d_prior) / s_prior;
-            e = nerf_expf(-0.5f * tx * tx) * delta;
+            const float w = c.alpha * tl;
+            sr += w * cc[0];
+            sg += w * cc[1];
+            sb += w * cc[2];
+            sd += w * c.t;
+            sw += w;
+            swm += w * c.m;
+            se += c.e;
+            tl *= (1.0f - c.alpha);
         }
-        const int nk = (int)min(64u, cnt - base);
-        float w_mine = 0.0f;
-        for (int k = 0; k < nk; k++) {
-            const float al = bcast(alpha, k);
-            const float w = al * T;
-            rc += w * bcast(cr, k);
-            gc += w * bcast(cg, k);
-            bc += w * bcast(cb, k);
-            depth += w * bcast(tt, k);
-            T *= (1.0f - al);
-            dw_g += w;
-            dwm_g += w * bcast(m, k);
-            dls += bcast(e, k);
-            if (lane == k) w_mine = w;
-        }
-        if (valid) a.dw[idx] = w_mine;
-    }
-    dls = 1.0f / fmaxf(dls, 1e-8f);
+        const float tj = wave_excl_prod(tl, lane);
+        const float t_end = __shfl(tj * tl, 63, 64);
+        const float lw = tj * sw, lwm = tj * swm;
+        float rc = wave_sum(tj * sr), gc = wave_sum(tj * sg), bc = wave_sum(tj * sb);
+        const float depth = wave_sum(tj * sd);
+        const float dw_g = wave_sum(lw), dwm_g = wave_sum(lwm);
+        const float dls = 1.0f / fmaxf(wave_sum(se), 1e-8f);
+        float dw_s = wave_excl_sum(lw, lane), dwm_s = wave_excl_sum(lwm, lane);
 
-    // ---- distortion (+ depth prior) gradient per weight ----
-    float wgs = 0.0f, dw_s = 0.0f, dwm_s = 0.0f;
-    for (uint32_t base = 0; base < cnt; base += 64) {
-        const uint32_t i = base + lane;
-        const bool valid = i < cnt;
-        const uint32_t idx = off + i;
-        float w = 0.f, m = 0.f, ds = 0.f, dloss = 0.f;
-        if (valid) {
-            const float tt = a.t[idx];
-            float t_next = (i < cnt - 1) ? a.t[idx + 1] : (tt + 1e-3f);
-            float delta = t_next - tt;
-            if (delta < 0.0f) {
-                delta = 0.0f;
-                t_next = tt;
-            }
-            const float s = disparity_warp(tt, t_near, inv_g);
-            const float s_next = disparity_warp(t_next, t_near, inv_g);
-            m = 0.5f * (s + s_next);
-            ds = s_next - s;
-            if (ds < 0.0f) ds = 0.0f;
-            w = a.dw[idx];
-            const float tx = (tt - d_prior) / s_prior;
-            const float dwt = nerf_expf(-0.5f * tx * tx) * delta * dls;
-            dloss = -dwt * (1.0f / fmaxf(w, 1e-6f));
+        // ---- B: distortion (+ depth prior) gradient per weight ----
+        float tr = tj, wgl = 0.0f;
+        for (uint32_t i = k0; i < k1; i++) {
+            const uint32_t idx = off + i;
+            const CompSample c = comp_sample(a, idx, i, cnt, t_near, inv_g, d_prior, s_prior);
+            const float w = c.alpha * tr;
+            tr *= (1.0f - c.alpha);
+            const float dloss = -(c.e * dls) * (1.0f / fmaxf(w, 1e-6f));
+            const float bil = c.m * (2 * dw_s - dw_g) + (dwm_g - 2 * dwm_s);
+            const float g = a.lambda_dist * (2 * (bil) + c23 * w * c.ds) + dwl * dloss;
+            a.dw[idx] = g;
+            wgl += w * g;
+            dw_s += w;
+            dwm_s += w * c.m;
         }
-        const int nk = (int)min(64u, cnt - base);
-        float g_mine = 0.0f;
-        for (int k = 0; k < nk; k++) {
-            const float wk = bcast(w, k), mk = bcast(m, k);
-            const float bil = mk * (2 * dw_s - dw_g) + (dwm_g - 2 * dwm_s);
-            const float g = a.lambda_dist * (2 * (bil) + c23 * wk * bcast(ds, k)) + dwl * bcast(dloss, k);
-            wgs += wk * g;
-            dw_s += wk;
-            dwm_s += wk * mk;
-            if (lane == k) g_mine = g;
-        }
-        if (valid) a.dw[idx] = g_mine;
-    }
-    rc += T * a.bg.x;
-    gc += T * a.bg.y;
-    bc += T * a.bg.z;
-    float pr = 0.f, pg = 0.f, pb = 0.f;
-    if (a.rgb_true && a.phi) {
-        pr = 2.0f * (rc - a.rgb_true[3 * r]);
-        pg = 2.0f * (gc - a.rgb_true[3 * r + 1]);
-        pb = 2.0f * (bc - a.rgb_true[3 * r + 2]);
-    }
-    if (lane == 0) {
-        a.weight_sum[r] = wgs;
-        a.final_rgb[3 * r] = rc;
-        a.final_rgb[3 * r + 1] = gc;
-        a.final_rgb[3 * r + 2] = bc;
-        a.final_depth[r] = depth;
-        if (a.rgb_true && a.phi) {
+        const float wgs = wave_sum(wgl);
+        rc += t_end * a.bg.x;
+        gc += t_end * a.bg.y;
+        bc += t_end * a.bg.z;
+        const float pr = 2.0f * (rc - a.rgb_true[3 * r]);
+        const float pg = 2.0f * (gc - a.rgb_true[3 * r + 1]);
+        const float pb = 2.0f * (bc - a.rgb_true[3 * r + 2]);
+        if (lane == 0) {
+            a.weight_sum[r] = wgs;
+            a.final_rgb[3 * r] = rc;
+            a.final_rgb[3 * r + 1] = gc;
+            a.final_rgb[3 * r + 2] = bc;
+            a.final_depth[r] = depth;
             a.phi[3 * r] = pr;
             a.phi[3 * r + 1] = pg;
             a.phi[3 * r + 2] = pb;
         }
-    }
 
-    // ---- colour gradient (compute_color_grad with initialOffset 0) ----
-    const uint32_t start = gr.offsets[0];
-    const float bs = 1.0f / (float)gr.total_rays;
-    float T2 = 1.0f, cr2 = 0.0f, cg2 = 0.0f, cb2 = 0.0f, wg = 0.0f;
-    for (uint32_t base = 0; base < cnt; base += 64) {
-        const uint32_t j = base + lane;
-        const bool valid = j < cnt;
-        const uint32_t gi = off + j;
-        const size_t i = (size_t)gi - start;
-        float delta = 0.f, sigma = 0.f, alpha = 0.f, c_r = 0.f, c_g = 0.f, c_b = 0.f, gw = 0.f;
-        if (valid) {
-            const float tc = gr.t[gi];
-            delta = (j == cnt - 1) ? 1e-3f : fmaxf(gr.t[gi + 1] - tc, 0.0f);
-            sigma = nerf_expf(fminf(gr.density_out[16 * i] - gr.bias, 8.0f));
-            alpha = 1.0f - nerf_expf(-sigma * delta);
+        // ---- C: the colour gradient's transmittance and weighted sums ----
+        float tl2 = 1.0f, qr = 0.f, qg = 0.f, qb = 0.f, qw = 0.f;
+        for (uint32_t j = k0; j < k1; j++) {
+            const uint32_t gi = off + j;
+            const size_t i = (size_t)gi - start;
+            const GradSample s = grad_sample(gr, gi, i, j, cnt);
             const float* co = gr.color_out + (size_t)gr.color_stride * i;
-            c_r = co[0];
-            c_g = co[1];
-            c_b = co[2];
-            gw = gr.dw[i];
+            const float w = tl2 * s.alpha;
+            qr += w * co[0];
+            qg += w * co[1];
+            qb += w * co[2];
+            qw += w * gr.dw[i];
+            tl2 *= (1.0f - s.alpha);
         }
-        const int nk = (int)min(64u, cnt - base);
-        float Tm = 0.f, wm = 0.f, crm = 0.f, cgm = 0.f, cbm = 0.f, wgm = 0.f;
-        for (int k = 0; k < nk; k++) {
-            const float al = bcast(alpha, k);
-            const float w = T2 * al;
-            cr2 += w * bcast(c_r, k);
-            cg2 += w * bcast(c_g, k);
-            cb2 += w * bcast(c_b, k);
-            wg += w * bcast(gw, k);
-            if (lane == k) {
-                Tm = T2;
-                wm = w;
-                crm = cr2;
-                cgm = cg2;
-                cbm = cb2;
-                wgm = wg;
-            }
-            T2 = T2 * (1.0f - al);
-        }
-        if (valid) {
-            float g_r = pr * wm * c_r * (1.0f - c_r) * gr.loss_scale * bs;
-            float g_g = pg * wm * c_g * (1.0f - c_g) * gr.loss_scale * bs;
-            float g_b = pb * wm * c_b * (1.0f - c_b) * gr.loss_scale * bs;
+        const float tj2 = wave_excl_prod(tl2, lane);
+        float cr2 = wave_excl_sum(tj2 * qr, lane), cg2 = wave_excl_sum(tj2 * qg, lane);
+        float cb2 = wave_excl_sum(tj2 * qb, lane), wg = wave_excl_sum(tj2 * qw, lane);
+
+        // ---- D: colour gradient and d sigma per sample ----
+        float T2 = tj2;
+        for (uint32_t j = k0; j < k1; j++) {
+            const uint32_t gi = off + j;
+            const size_t i = (size_t)gi - start;
+            const GradSample s = grad_sample(gr, gi, i, j, cnt);
+            const float* co = gr.color_out + (size_t)gr.color_stride * i;
+            const float c_r = co[0], c_g = co[1], c_b = co[2];
+            const float gw = gr.dw[i];
+            const float w = T2 * s.alpha;
+            cr2 += w * c_r;
+            cg2 += w * c_g;
+            cb2 += w * c_b;
+            wg += w * gw;
+            float g_r = pr * w * c_r * (1.0f - c_r) * gr.loss_scale * bs;
+            float g_g = pg * w * c_g * (1.0f - c_g) * gr.loss_scale * bs;
+            float g_b = pb * w * c_b * (1.0f - c_b) * gr.loss_scale * bs;
             g_r = clamp_half_range(g_r);
             g_g = clamp_half_range(g_g);
             g_b = clamp_half_range(g_b);
@@ -420,17 +447,17 @@ __global__ __launch_bounds__(256) void render_grad_kernel(const CompositeArgs a,
             cgo[1] = to_h(g_g);
             cgo[2] = to_h(g_b);
             for (int q = 3; q < gr.grad_stride; q++) cgo[q] = (_Float16)0.0f;
-            const float sr = rc - crm, sg = gc - cgm, sb = bc - cbm;
-            const float dr = Tm * c_r * (1.0f - alpha) - sr;
-            const float dg = Tm * c_g * (1.0f - alpha) - sg;
-            const float db = Tm * c_b * (1.0f - alpha) - sb;
-            const float suffix = wgs - wgm;
-            float dsi = delta * (dr * pr + dg * pg + db * pb);
-            dsi += delta * (gw * Tm * (1.0f - alpha) - suffix);
-            float dsv = dsi * sigma * gr.loss_scale * bs;
+            const float dr = T2 * c_r * (1.0f - s.alpha) - (rc - cr2);
+            const float dg = T2 * c_g * (1.0f - s.alpha) - (gc - cg2);
+            const float db = T2 * c_b * (1.0f - s.alpha) - (bc - cb2);
+            const float suffix = wgs - wg;
+            float dsi = s.delta * (dr * pr + dg * pg + db * pb);
+            dsi += s.delta * (gw * T2 * (1.0f - s.alpha) - suffix);
+            float dsv = dsi * s.sigma * gr.loss_scale * bs;
             dsv = clamp_half_range(dsv);
             if (dsv != dsv) dsv = 0.0f;
             gr.dsigma[i] = dsv;
+            T2 = T2 * (1.0f - s.alpha);
         }
     }
 }
@@ -573,7 +600,8 @@ void render_grad(const CompositeArgs& a, const ColorGradArgs& g, const uint32_t*
     if (rays_max == 0) return;
     if (g.total_rays == 0) throw std::runtime_error("color grad: totalRaysBatch must be > 0");
     if (!a.rgb_true || !a.phi) throw std::runtime_error("render_grad: needs ground truth and phi");
-    hipLaunchKernelGGL(render_grad_kernel, dim3((rays_max + 3) / 4), dim3(256), 0, s, a, g, d_rays, rays_max);
+    const int blocks = (int)std::min<uint32_t>((rays_max + 3) / 4, (uint32_t)num_cus() * 8);
+    hipLaunchKernelGGL(render_grad_kernel, dim3(blocks), dim3(256), 0, s, a, g, d_rays, rays_max);
     GRAFT_LAUNCH_CHECK();
 }
 

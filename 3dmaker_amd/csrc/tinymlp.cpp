@@ -429,8 +429,8 @@ void TinyMLP::step(float lr, float beta1, float beta2, float epsilon, float loss
     if (current_step < 50000) current_step++;
     const AdamArgs a = adam_args(current_step, lr, beta1, beta2, epsilon, loss_scale);
     const Dims d = dims_of(hw_opt);
-    graft::adam_layers(d_master_weights, d_fwd_weights, d_w_grad, d_w_m, d_w_v, d.wsizes(), d.layers, a, stream);
-    graft::adam_layers(d_master_biases, nullptr, d_b_grad, d_b_m, d_b_v, d.bsizes(), d.layers, a, stream);
+    graft::adam_dense(d_master_weights, d_fwd_weights, d_w_grad, d_w_m, d_w_v, d.wsizes(), d_master_biases,
+                      d_b_grad, d_b_m, d_b_v, d.bsizes(), d.layers, a, stream);
 }
 
 // TinyMLP.cu:406-481: raw MLPOption header, then per layer W then B (fp32).
@@ -767,8 +767,8 @@ void TinyMLPHashGrid::step(float lr, float beta1, float beta2, float epsilon, fl
     if (current_step < 50000) current_step++;
     const AdamArgs a = adam_args(current_step, lr, beta1, beta2, epsilon, loss_scale);
     const Dims d = dims_of(mlp_opt);
-    graft::adam_layers(d_master_weights, d_fwd_weights, d_w_grad, d_w_m, d_w_v, d.wsizes(), d.layers, a, stream);
-    graft::adam_layers(d_master_biases, nullptr, d_b_grad, d_b_m, d_b_v, d.bsizes(), d.layers, a, stream);
+    graft::adam_dense(d_master_weights, d_fwd_weights, d_w_grad, d_w_m, d_w_v, d.wsizes(), d_master_biases,
+                      d_b_grad, d_b_m, d_b_v, d.bsizes(), d.layers, a, stream);
     graft::adam_hash(d_master_hashtable, d_fwd_hashtable, d_hashtable_grads, d_hash_m, d_hash_v,
                      (size_t)m_totalHashElements, a, stream);
 }

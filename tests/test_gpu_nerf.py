@@ -1,11 +1,16 @@
 """GPU parity of the NeRF-side HIP kernels (through the C-ABI) against the oracle.
 
 Bars: ray setup, compaction (counts, offsets, cutoff, sample t / ray index /
-contracted position), SH gather, compositing, colour/density gradient glue,
-occupancy bits and mips are bit-exact (same fp32 operations in the same order,
-one e^x routine on both sides); the fixed-order occupancy sum is within 1e-6
-relative of the fp64 sum; the MLP stages of a full training step are within
-2e-3 abs / 1e-2 rel (fp16 operands, fp32 accumulation).
+contracted position), SH gather, the reference-shaped compositing and colour
+gradient kernels, the density gradient glue, occupancy bits and mips are
+bit-exact (same fp32 operations in the same order, one e^x routine on both
+sides); the fused compositing + colour-gradient kernel of the training step
+scans along each ray, so it agrees to fp32 rounding of the association
+(scan_close: 2e-5 of the largest value + 1e-4 relative; 1e-4 for d sigma, whose
+suffix differences cancel; fp16 colour gradients 2e-3 relative); the
+fixed-order occupancy sum is within 1e-6 relative of the fp64 sum; the MLP
+stages of a full training step are within 2e-3 abs / 1e-2 rel (fp16 operands,
+fp32 accumulation).
 """
 import ctypes as C
 import importlib
@@ -41,6 +46,15 @@ def f3(v):
 
 def u3(v):
     return pkg().Uint3(int(v[0]), int(v[1]), int(v[2]))
+
+
+def scan_close(got, want, what, atol_rel=2e-5, rtol=1e-4):
+    """Agreement up to fp32 rounding of a different summation/product order:
+    |got - want| <= atol_rel * max|want| + rtol * |want|."""
+    want = np.asarray(want, np.float64)
+    scale = float(np.abs(want).max()) if want.size else 0.0
+    assert np.isfinite(np.asarray(got, np.float64)).all(), what
+    assert_close(got, want, atol=atol_rel * max(scale, 1e-30), rtol=rtol, what=what)
 
 
 def bits_eq(a, b):
@@ -254,8 +268,11 @@ def test_composite_and_color_grad_bit_exact(dev, with_depth):
 
 
 @pytest.mark.parametrize("max_n,R,stride", [(300, 700, 8), (3, 5000, 3), (1024, 40, 3)])
-def test_fused_render_color_grad_bit_exact(dev, max_n, R, stride):
-    """One wave per ray over rays of up to max_n samples (several 64-sample chunks)."""
+def test_fused_render_color_grad_matches_oracle(dev, max_n, R, stride):
+    """One wave per ray over rays of up to max_n samples, each lane owning a run of
+    samples.  The fused kernel sums and multiplies along the ray by scans, so it
+    matches the oracle's left-to-right loops to fp32 rounding of the association
+    (tolerances below); the reference-shaped kernels are the bit-exact ones."""
     P = pkg()
     print(f"[render_grad] max_n={max_n} R={R} stride={stride}", flush=True)
     cnt, off, t, rng = ray_batch(R, max_n, 20 + max_n)
@@ -278,17 +295,17 @@ def test_fused_render_color_grad_bit_exact(dev, max_n, R, stride):
     torch.cuda.synchronize()
     rgb3 = np.ascontiguousarray(rgb[:, :3])
     want = orc.composite(off, cnt, t, sig, rgb3, gt, 0.1, bg, depth_prior=dp, sigma_prior=sp, lambda_depth=0.05)
-    bits_eq(out["rgb"].cpu().numpy(), want["rgb"])
-    bits_eq(out["depth"].cpu().numpy(), want["depth"])
-    bits_eq(out["phi"].cpu().numpy(), want["phi"])
-    bits_eq(out["dw"].cpu().numpy()[:N], want["dw"])
-    bits_eq(out["ws"].cpu().numpy(), want["weight_sum"])
+    scan_close(out["rgb"].cpu().numpy(), want["rgb"], "rgb")
+    scan_close(out["depth"].cpu().numpy(), want["depth"], "depth")
+    scan_close(out["phi"].cpu().numpy(), want["phi"], "phi")
+    scan_close(out["dw"].cpu().numpy()[:N], want["dw"], "dL/dw")
+    scan_close(out["ws"].cpu().numpy(), want["weight_sum"], "sum w dL/dw")
     w_cg, w_ds = orc.color_grad(cnt, off, t, dout, rgb3, want["phi"], want["rgb"], want["dw"], want["weight_sum"],
                                 128.0, 0.0, 4096)
     got_cg = cg.cpu().numpy()[:N]
-    np.testing.assert_array_equal(got_cg[:, :3].view(np.uint16), w_cg.view(np.uint16))
+    scan_close(got_cg[:, :3], w_cg, "colour grad (fp16)", rtol=2e-3)
     assert (got_cg[:, 3:] == 0).all()
-    bits_eq(out["ds"].cpu().numpy()[:N], w_ds)
+    scan_close(out["ds"].cpu().numpy()[:N], w_ds, "d sigma", atol_rel=1e-4)
 
 
 def test_density_grad_bit_exact(dev):
@@ -423,15 +440,16 @@ def test_instant_nerf_step_matches_oracle_chain(dev):
     cout = d2h(b.color_output, (N, 8), np.float32)
     c_ref, c_acts = orc.mlp_forward(cin, cW.astype(np.float16), cB, 32, 64, 8, 3, out_act=1)
     assert_close(cout, c_ref, what="color output")
-    # compositing + colour gradient on the GPU's own inputs: bit-exact
+    # compositing + colour gradient on the GPU's own inputs (scan order: fp32 rounding)
     comp = orc.composite(want["offsets"], want["counts"], want["t"], w_sig, np.ascontiguousarray(cout[:, :3]), gt,
                          0.1, np.float32([1, 1, 1]))
-    bits_eq(rgb_out.cpu().numpy(), comp["rgb"])
-    bits_eq(d2h(b.phi, (R, 3), np.float32), comp["phi"])
-    bits_eq(d2h(b.dw, (N,), np.float32), comp["dw"])
+    scan_close(rgb_out.cpu().numpy(), comp["rgb"], "rgb")
+    scan_close(d2h(b.phi, (R, 3), np.float32), comp["phi"], "phi")
+    scan_close(d2h(b.dw, (N,), np.float32), comp["dw"], "dL/dw")
     cg, ds = orc.color_grad(want["counts"], want["offsets"], want["t"], dout, np.ascontiguousarray(cout[:, :3]),
                             comp["phi"], comp["rgb"], comp["dw"], comp["weight_sum"], 128.0, 0.0, R)
-    bits_eq(d2h(b.dsigma, (N,), np.float32), ds)
+    got_ds = d2h(b.dsigma, (N,), np.float32)
+    scan_close(got_ds, ds, "d sigma", atol_rel=1e-4)
     # colour backward (dX) and density gradient
     cgp = np.zeros((N, 8), np.float16)
     cgp[:, :3] = cg
@@ -441,7 +459,7 @@ def test_instant_nerf_step_matches_oracle_chain(dev):
     scale = max(1.0, float(np.abs(cdx_ref.astype(np.float32)).max()))
     assert_close(cdx, cdx_ref, atol=2e-3 * scale, what="color dL/dinput")
     np.testing.assert_array_equal(d2h(b.density_grad, (N, 16), np.float16).view(np.uint16),
-                                  orc.density_grad(ds, cdx).view(np.uint16))
+                                  orc.density_grad(got_ds, cdx).view(np.uint16))
     # the step moved the parameters and kept them finite
     t2 = np.zeros_like(table)
     nerf.density.save_hashgrid(t2)
