@@ -52,10 +52,24 @@ struct MarchArgs {
     uint32_t R;
     uint32_t total_cells;        // cells of one cascade pyramid
     uint32_t mip_off[kMaxMip];   // cells below level l
+    float3 vs0[kMaxMip];         // cascade-0 voxel size of level l: extent / (res >> l)
 };
 
 // Marches ray i and stores its sample t values at t_out[march_store_index(i, k)];
 // returns the sample count.
+//
+// The reference loop (processRays.cu:660-733) spends one iteration per mip
+// level: at a t it starts at level L-1 and descends while the cell is
+// occupied, recomputing the position, cascade and cell coordinates each time
+// although t does not change.  Here everything that depends only on t is
+// computed once per t, the L cell bytes are loaded together, and the level the
+// reference would stop at (the first unoccupied level from the top, else 0) is
+// read off the loaded bits.  The operations that produce each value are the
+// reference's, so t, the cell indices and the sample t values are
+// bit-identical; `it` counts the reference's iterations, descents included.
+// The voxel size uses (e * 2^c) / r == 2^c * (e / r), exact for powers of two,
+// with e / r precomputed per level.
+template <int MAXL>
 __device__ uint32_t march_ray(const MarchArgs& a, uint32_t i, float* __restrict__ t_out)
 {
     const float3 o = a.o[i], d = a.d[i], di = a.di[i];
@@ -63,41 +77,61 @@ __device__ uint32_t march_ray(const MarchArgs& a, uint32_t i, float* __restrict_
     const float t_max = a.fars[i];
     const float ex = a.mx.x - a.mn.x, ey = a.mx.y - a.mn.y, ez = a.mx.z - a.mn.z;
     const float sx = d.x >= 0.0f ? 1.0f : 0.0f, sy = d.y >= 0.0f ? 1.0f : 0.0f, sz = d.z >= 0.0f ? 1.0f : 0.0f;
+    const int L = a.L;  // <= MAXL
     uint32_t hit = 0;
-    int level = a.L - 1;
-    for (int it = 0; t < t_max && hit < (uint32_t)kMaxHits && it < kMaxMarchIters; it++) {
+    for (int it = 0; t < t_max && hit < (uint32_t)kMaxHits && it < kMaxMarchIters;) {
         const float px = o.x + t * d.x, py = o.y + t * d.y, pz = o.z + t * d.z;
         const int c = get_cascade(px, py, pz, a.mn, a.mx, a.C);
         const float cs = ldexpf(1.0f, c);
         const float cminx = a.mn.x * cs, cminy = a.mn.y * cs, cminz = a.mn.z * cs;
         const float cextx = ex * cs, cexty = ey * cs, cextz = ez * cs;
-        const uint32_t rlx = a.res.x >> level, rly = a.res.y >> level, rlz = a.res.z >> level;
-        const float vsx = cextx / (float)rlx, vsy = cexty / (float)rly, vsz = cextz / (float)rlz;
-        const int vix = clamp_floor_idx(floorf(((px - cminx) / cextx) * (float)rlx), (int)rlx - 1);
-        const int viy = clamp_floor_idx(floorf(((py - cminy) / cexty) * (float)rly), (int)rly - 1);
-        const int viz = clamp_floor_idx(floorf(((pz - cminz) / cextz) * (float)rlz), (int)rlz - 1);
-        const uint32_t flat = (uint32_t)c * a.total_cells + a.mip_off[level] + (uint32_t)viz * (rlx * rly) +
-                              (uint32_t)viy * rlx + (uint32_t)vix;
-        const bool occ = (a.bits[flat >> 3] >> (flat & 7)) & 1;
+        const float rx = (px - cminx) / cextx, ry = (py - cminy) / cexty, rz = (pz - cminz) / cextz;
+        const uint32_t cbase = (uint32_t)c * a.total_cells;
+        uint32_t bit[MAXL];
+        int ix[MAXL], iy[MAXL], iz[MAXL];
+#pragma unroll
+        for (int l = 0; l < MAXL; l++) {
+            if (l < L) {
+                const uint32_t rlx = a.res.x >> l, rly = a.res.y >> l, rlz = a.res.z >> l;
+                ix[l] = clamp_floor_idx(floorf(rx * (float)rlx), (int)rlx - 1);
+                iy[l] = clamp_floor_idx(floorf(ry * (float)rly), (int)rly - 1);
+                iz[l] = clamp_floor_idx(floorf(rz * (float)rlz), (int)rlz - 1);
+                const uint32_t flat = cbase + a.mip_off[l] + (uint32_t)iz[l] * (rlx * rly) +
+                                      (uint32_t)iy[l] * rlx + (uint32_t)ix[l];
+                bit[l] = ((uint32_t)a.bits[flat >> 3] >> (flat & 7)) & 1u;
+            }
+        }
+        // the reference's level sequence L-1, L-2, ... stops at the first
+        // unoccupied level, or at level 0
+        int level = L - 1, vix = 0, viy = 0, viz = 0;
+        float3 v0 = a.vs0[0];
+        bool occ = false;
+#pragma unroll
+        for (int l = MAXL - 1; l >= 0; l--) {
+            if (l == level) {
+                vix = ix[l];
+                viy = iy[l];
+                viz = iz[l];
+                v0 = a.vs0[l];
+                occ = bit[l] != 0;
+                if (occ && l > 0) level = l - 1;
+            }
+        }
+        it += L - level;
+        const float vsx = v0.x * cs, vsy = v0.y * cs, vsz = v0.z * cs;
         const float nbx = cminx + ((float)vix + sx) * vsx;
         const float nby = cminy + ((float)viy + sy) * vsy;
         const float nbz = cminz + ((float)viz + sz) * vsz;
-        if (occ) {
-            if (level > 0) {
-                level--;
-                continue;
-            }
-            const float exit_t = fminf(fminf((nbx - o.x) * di.x, (nby - o.y) * di.y), (nbz - o.z) * di.z);
-            const float span = exit_t - t;
+        const float next_t = fminf(fminf((nbx - o.x) * di.x, (nby - o.y) * di.y), (nbz - o.z) * di.z);
+        if (occ) {  // occupied at level 0: K samples over the voxel, whose exit is next_t
+            const float span = next_t - t;
             for (int k = 0; k < a.K; ++k) {
                 if (hit >= (uint32_t)kMaxHits) break;
                 t_out[march_store_index(i, hit)] = t + ((float)k + 0.5f) / (float)a.K * span;
                 hit++;
             }
         }
-        const float next_t = fminf(fminf((nbx - o.x) * di.x, (nby - o.y) * di.y), (nbz - o.z) * di.z);
         t = fmaxf(t + 1e-5f, next_t + 1e-6f);
-        level = a.L - 1;
     }
     return hit;
 }
@@ -216,11 +250,12 @@ __global__ __launch_bounds__(1024) void march_scan_kernel(const uint32_t* __rest
     }
 }
 
+template <int MAXL>
 __global__ __launch_bounds__(256) void march_store_kernel(const MarchArgs a, uint32_t* __restrict__ counts,
                                                           float* __restrict__ t_scratch)
 {
     const uint32_t i = blockIdx.x * 256 + threadIdx.x;
-    if (i < a.R) counts[i] = march_ray(a, i, t_scratch);
+    if (i < a.R) counts[i] = march_ray<MAXL>(a, i, t_scratch);
 }
 
 __global__ __launch_bounds__(256) void block_sums_kernel(const uint32_t* __restrict__ counts, uint32_t n,
@@ -307,7 +342,11 @@ MarchArgs march_args(uint32_t R, const float3* o, const float3* d, const float3*
     a.L = g.mip_levels;
     a.K = K;
     a.R = R;
-    for (int l = 0; l < g.mip_levels; l++) a.mip_off[l] = mip_offset(g.res, l);
+    const float ex = g.aabb_max.x - g.aabb_min.x, ey = g.aabb_max.y - g.aabb_min.y, ez = g.aabb_max.z - g.aabb_min.z;
+    for (int l = 0; l < g.mip_levels; l++) {
+        a.mip_off[l] = mip_offset(g.res, l);
+        a.vs0[l] = make_float3(ex / (float)(g.res.x >> l), ey / (float)(g.res.y >> l), ez / (float)(g.res.z >> l));
+    }
     a.total_cells = mip_offset(g.res, g.mip_levels);
     return a;
 }
@@ -332,7 +371,10 @@ void march_store(uint32_t R, const float3* o, const float3* d, const float3* d_i
 {
     if (R == 0) return;
     const MarchArgs a = march_args(R, o, d, d_inv, nears, fars, g, K);
-    hipLaunchKernelGGL(march_store_kernel, dim3((R + 255) / 256), dim3(256), 0, s, a, counts, t_scratch);
+    const dim3 grid((R + 255) / 256);
+    if (a.L <= 4) hipLaunchKernelGGL(march_store_kernel<4>, grid, dim3(256), 0, s, a, counts, t_scratch);
+    else if (a.L <= 8) hipLaunchKernelGGL(march_store_kernel<8>, grid, dim3(256), 0, s, a, counts, t_scratch);
+    else hipLaunchKernelGGL(march_store_kernel<kMaxMip>, grid, dim3(256), 0, s, a, counts, t_scratch);
     GRAFT_LAUNCH_CHECK();
 }
 
