@@ -172,6 +172,12 @@ SIGNATURES = {
     "inerf_print_stats": (_i, [_vp]),
     "inerf_stats": (_i, [_vp, C.c_char_p, _i]),
     "inerf_reset_stats": (_i, [_vp]),
+    "inerf_set_memory_mode": (_i, [_vp, _i]),
+    "inerf_render": (_i, [_vp, _vp, _vp, _u32, _vp, _vp]),
+    "inerf_query_occupancy": (_i, [_vp, _vp, _i, _vp, _f, _vp]),
+    "inerf_query_density_logit": (_i, [_vp, _vp, _i, _vp, _vp]),
+    "inerf_query_radiance": (_i, [_vp, _vp, _i, _f, _f, _f, _vp, _vp]),
+    "inerf_build_occupancy_bitgrid": (_i, [_vp, _vp, _f, _vp]),
     "inerf_update_occupancy": (_i, [_vp, _vp]),
     "inerf_occupancy_bytes": (C.c_size_t, [_vp]),
     "inerf_get_occupancy": (_i, [_vp, _vp]),
@@ -427,7 +433,7 @@ class Nerf:
               max_steps=4096):
         """trainWithRaysHit; returns (steps taken, [compacted samples per step])."""
         cnt = C.c_int(0)
-        hits = (_u32 * max_steps)()
+        hits = (_u32 * max(int(max_steps), int(num_rays), 1))()  # one step consumes >= 1 ray
         self._c(self._L.inerf_train(self.h, ptr(rays_o), ptr(rays_d), ptr(rays_depth), ptr(rays_sigma),
                                     ptr(rgb_true), int(num_rays), C.byref(cnt), hits, ptr(rgb_out), stream))
         return cnt.value, list(hits[:cnt.value])
@@ -457,6 +463,27 @@ class Nerf:
 
     def reset_stats(self):
         self._c(self._L.inerf_reset_stats(self.h))
+
+    def set_memory_mode(self, inference: bool):
+        """INFERENCE selects renderBatchSize as the render hit batch; training needs TRAINING."""
+        self._c(self._L.inerf_set_memory_mode(self.h, int(bool(inference))))
+
+    def render(self, rays_o, rays_d, num_rays, rgb_out, stream=0):
+        """renderImageHit: rgb_out [num_rays x 3] (device)."""
+        self._c(self._L.inerf_render(self.h, ptr(rays_o), ptr(rays_d), num_rays, ptr(rgb_out), stream))
+
+    def query_occupancy(self, pos, n, words_out, min_optical, stream=0):
+        self._c(self._L.inerf_query_occupancy(self.h, ptr(pos), n, ptr(words_out), min_optical, stream))
+
+    def query_density_logit(self, pos, n, logit_out, stream=0):
+        self._c(self._L.inerf_query_density_logit(self.h, ptr(pos), n, ptr(logit_out), stream))
+
+    def query_radiance(self, pos, n, view_dir, rgb_out, stream=0):
+        self._c(self._L.inerf_query_radiance(self.h, ptr(pos), n, float(view_dir[0]), float(view_dir[1]),
+                                             float(view_dir[2]), ptr(rgb_out), stream))
+
+    def build_occupancy_bitgrid(self, bits_out, min_density, stream=0):
+        self._c(self._L.inerf_build_occupancy_bitgrid(self.h, ptr(bits_out), min_density, stream))
 
     def update_occupancy(self, stream=0):
         self._c(self._L.inerf_update_occupancy(self.h, stream))

@@ -12,6 +12,7 @@
 #include "nerf.h"
 #include "nerf_math.h"
 #include "occupancy.h"
+#include "optimizer.h"
 
 #include <algorithm>
 #include <cstdio>
@@ -63,6 +64,18 @@ struct NerfBuffers {
     int* active_count = nullptr;
     uint32_t* list_scratch = nullptr;
     int occ_capacity = 0;
+    // inference render / queries (allocated on first use, sized to the hit batch)
+    struct Render {
+        uint32_t cap = 0;
+        float4* positions = nullptr;
+        uint32_t* ray_idx = nullptr;
+        float* t = nullptr;
+        float* density_out = nullptr;  // [cap x 16]
+        __half* color_in = nullptr;    // [cap x 32]
+        float* sigma = nullptr;
+        float* rgb = nullptr;          // [cap x colour head width] (padded)
+        float3* dir = nullptr;         // one view direction (queryRadiance)
+    } render;
     // model views
     __half* color_in = nullptr;      // TinyMLP activation 0
     graft::GridMeta meta{};
@@ -141,6 +154,14 @@ void InstantNerf::freeBuffers()
         dfree(b.active_list);
         dfree(b.active_count);
         dfree(b.list_scratch);
+        dfree(b.render.positions);
+        dfree(b.render.ray_idx);
+        dfree(b.render.t);
+        dfree(b.render.density_out);
+        dfree(b.render.color_in);
+        dfree(b.render.sigma);
+        dfree(b.render.rgb);
+        dfree(b.render.dir);
         if (b.ev_result) (void)hipEventDestroy(b.ev_result);
         for (auto& t : b.pending) {
             (void)hipEventDestroy(t.a);
@@ -162,7 +183,6 @@ void InstantNerf::freeBuffers()
 void InstantNerf::init(const NerfOptions& opts, MemoryMode memMode)
 {
     freeBuffers();
-    if (memMode != TRAINING) throw std::logic_error("InstantNerf: only TRAINING mode is part of this build");
     if (opts.batchSize < MAX_HITS)
         throw std::runtime_error("InstantNerf: batchSize must be >= 1024 (one ray's maximum sample count)");
     if (opts.rayChunkSize <= 0 || opts.rayChunkSize % 16)
@@ -260,9 +280,13 @@ void InstantNerf::allocate()
     b.meta = graft::make_grid_meta(m_opts.hashTableSize, m_opts.numLevels, m_opts.growthFactor, m_opts.baseResolution);
 }
 
+// InstantNerf.cu:341-359.  The mode picks the hit batch of the render path
+// (renderBatchSize in INFERENCE, batchSize in TRAINING); training state stays
+// allocated (the reference frees it), and training requires TRAINING mode.
 void InstantNerf::setMemoryMode(MemoryMode mode)
 {
-    if (mode != TRAINING) throw std::logic_error("InstantNerf: only TRAINING mode is part of this build");
+    if (!m_init) return;
+    m_memMode = mode;
 }
 
 // InstantNerf.cu:359-583
@@ -272,6 +296,7 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
 {
     if (!m_init) throw std::runtime_error("InstantNerf: init() must be called before trainWithRaysHit()");
     if (!d_rgb_true) throw std::runtime_error("InstantNerf: trainWithRaysHit needs ground-truth colours");
+    if (m_memMode != TRAINING) throw std::runtime_error("InstantNerf: trainWithRaysHit needs setMemoryMode(TRAINING)");
     NerfBuffers& b = B(m_buf);
     const NerfOptions& o = m_opts;
     const uint32_t Bn = (uint32_t)o.batchSize;
@@ -596,30 +621,202 @@ InstantNerf::StepBuffers InstantNerf::stepBuffers() const
     return s;
 }
 
-// ---- not part of this build (render and file paths) ----
-void InstantNerf::renderImage(const float3*, const float3*, uint32_t, float*, hipStream_t)
+// ---- inference render and queries ----
+
+namespace {
+
+void ensure_render(NerfBuffers& b, uint32_t cap, int color_width)
 {
-    throw std::logic_error("InstantNerf::renderImage is not part of this build");
+    if (b.render.cap >= cap) return;
+    dfree(b.render.positions);
+    dfree(b.render.ray_idx);
+    dfree(b.render.t);
+    dfree(b.render.density_out);
+    dfree(b.render.color_in);
+    dfree(b.render.sigma);
+    dfree(b.render.rgb);
+    b.render.positions = dalloc<float4>(cap);
+    b.render.ray_idx = dalloc<uint32_t>(cap);
+    b.render.t = dalloc<float>(cap);
+    b.render.density_out = dalloc<float>((size_t)cap * 16);
+    b.render.color_in = dalloc<__half>((size_t)cap * 32);
+    b.render.sigma = dalloc<float>(cap);
+    b.render.rgb = dalloc<float>((size_t)cap * color_width);
+    b.render.cap = cap;
 }
-void InstantNerf::renderImageHit(const float3*, const float3*, uint32_t, float*, hipStream_t)
+
+}  // namespace
+
+uint32_t InstantNerf::renderHitBatch() const
 {
-    throw std::logic_error("InstantNerf::renderImageHit is not part of this build");
+    const int hb = (m_memMode == INFERENCE) ? m_opts.renderBatchSize : m_opts.batchSize;
+    return (uint32_t)std::max(hb, MAX_HITS) & ~15u;
 }
-void InstantNerf::queryOccupancyGrid(const float*, int, uint32_t*, float, hipStream_t)
+
+// renderImageHit (InstantNerf.cu:713-864): per chunk of rayChunkSize rays,
+// march once, then per hit batch: compaction from the first unrendered ray,
+// density inference, SH gather, colour inference, inference compositing
+// (compositing.cu:5-78) straight into d_rgb_out.  One host read per hit batch
+// (its active-ray count); the reference makes three blocking ones.
+void InstantNerf::renderImageHit(const float3* d_rays_o, const float3* d_rays_d, uint32_t numRays, float* d_rgb_out,
+                                 hipStream_t stream)
 {
-    throw std::logic_error("InstantNerf::queryOccupancyGrid is not part of this build");
+    if (!m_init) throw std::runtime_error("InstantNerf: init() must be called before renderImageHit()");
+    NerfBuffers& b = B(m_buf);
+    const NerfOptions& o = m_opts;
+    const uint32_t hitBatch = renderHitBatch();
+    const TinyMLPHashGrid::Buffers db = m_densityMLP->buffers();
+    const TinyMLP::Buffers cb = m_colorMLP->buffers();
+    const graft::MlpShape dshape{2 * o.numLevels, db.hw.hiddenDim, db.hw.outputDim, db.hw.numLayers};
+    const graft::MlpShape cshape = shape_of(cb.hw);
+    ensure_render(b, hitBatch, cshape.out);
+    const graft::OccGrid g = occ_grid(o, d_occupancyGrid);
+    const uint32_t* d_rays = b.result;
+    const uint32_t* d_hits = b.result + 1;
+    b.cache_version = -1;  // the march store is reused below
+
+    for (uint32_t c0 = 0; c0 < numRays; c0 += (uint32_t)o.rayChunkSize) {
+        const uint32_t R = std::min<uint32_t>((uint32_t)o.rayChunkSize, numRays - c0);
+        const float3* co = d_rays_o + c0;
+        const float3* cd = d_rays_d + c0;
+        graft::ray_aabb_inv(R, co, cd, o.aabbMin, o.aabbMax, o.numCascades, b.d_inv, b.nears, b.fars, stream);
+        graft::march_store(R, co, cd, b.d_inv, b.nears, b.fars, g, o.samplesPerVoxel, b.counts, b.t_scratch, stream);
+        uint32_t done = 0;
+        while (done < R) {
+            graft::march_compact_stored(R - done, co + done, cd + done, g, hitBatch, b.counts + done, b.t_scratch, done,
+                                        b.offsets, b.render.t, b.render.ray_idx, b.render.positions,
+                                        graft::MarchScratch{b.block_sums, b.result}, stream);
+            GRAFT_HIP_CHECK(hipMemcpyAsync(b.h_result, b.result, 2 * sizeof(uint32_t), hipMemcpyDeviceToHost, stream));
+            GRAFT_HIP_CHECK(hipEventRecord(b.ev_result, stream));
+            graft::FwdInput din;
+            din.pos = reinterpret_cast<const float*>(b.render.positions);
+            din.pos_stride = 4;
+            din.table = db.fwd_hashtable;
+            din.meta = &b.meta;
+            graft::mlp_forward(dshape, din, db.fwd_weights, db.master_biases, nullptr, b.render.density_out,
+                               (int)hitBatch, OUT_ACT_NONE, stream, d_hits);
+            graft::sh_gather(cd + done, b.render.ray_idx, d_hits, hitBatch, o.densityBias, b.render.density_out,
+                             b.render.color_in, b.render.sigma, stream);
+            graft::FwdInput cin;
+            cin.x = b.render.color_in;
+            graft::mlp_forward(cshape, cin, cb.fwd_weights, cb.master_biases, nullptr, b.render.rgb, (int)hitBatch,
+                               cb.hw.outputActivation, stream, d_hits);
+            graft::CompositeArgs ca{};
+            ca.offsets = b.offsets;
+            ca.counts = b.counts + done;
+            ca.t = b.render.t;
+            ca.sigma = b.render.sigma;
+            ca.rgb = b.render.rgb;
+            ca.rgb_stride = cshape.out;
+            ca.final_rgb = d_rgb_out ? d_rgb_out + (size_t)(c0 + done) * 3 : b.render_rgb;
+            ca.final_depth = b.render_depth;
+            ca.bg = o.bgColor;
+            graft::composite_infer(ca, 0, 0, d_rays, R - done, stream);
+            GRAFT_HIP_CHECK(hipEventSynchronize(b.ev_result));
+            const uint32_t active = b.h_result[0];
+            if (active == 0) throw std::runtime_error("InstantNerf: the render hit batch cannot hold one ray");
+            done += active;
+        }
+    }
 }
-void InstantNerf::queryDensityLogit(const float*, int, float*, hipStream_t)
+
+// renderImage (InstantNerf.cu:585-711), the legacy path behind legacyRenderFlag:
+// every ray's samples, MLP outputs and composite are those of renderImageHit.
+void InstantNerf::renderImage(const float3* d_rays_o, const float3* d_rays_d, uint32_t numRays, float* d_rgb_out,
+                              hipStream_t stream)
 {
-    throw std::logic_error("InstantNerf::queryDensityLogit is not part of this build");
+    if (!m_opts.legacyRenderFlag)
+        throw std::runtime_error("InstantNerf: renderImage() requires legacyRenderFlag=true; use renderImageHit()");
+    renderImageHit(d_rays_o, d_rays_d, numRays, d_rgb_out, stream);
 }
-void InstantNerf::queryRadiance(const float*, int, float3, float*, hipStream_t)
+
+// queryOccupancyGrid (InstantNerf.cu:941-946): d_pos [n x 3].
+void InstantNerf::queryOccupancyGrid(const float* d_pos, int n, uint32_t* d_data_out, float minOpticalThreshold,
+                                     hipStream_t stream)
 {
-    throw std::logic_error("InstantNerf::queryRadiance is not part of this build");
+    if (!m_init) throw std::runtime_error("InstantNerf: init() must be called before queryOccupancyGrid()");
+    graft::query_occupancy(d_masterOccupancyGrid, d_pos, d_data_out, m_opts.gridResolution, m_opts.aabbMin,
+                           m_opts.aabbMax, minOpticalThreshold, m_opts.numCascades, n, stream);
 }
-void InstantNerf::buildOccupancyBitgrid(uint8_t*, float, hipStream_t)
+
+// queryDensityLogit (InstantNerf.cu:948-961): raw density logit (output 0 of
+// the density head) of contracted positions d_pos [n x 3]; n % 16 == 0.
+void InstantNerf::queryDensityLogit(const float* d_pos, int n, float* d_logit_out, hipStream_t stream)
 {
-    throw std::logic_error("InstantNerf::buildOccupancyBitgrid is not part of this build");
+    if (n <= 0) return;
+    if (n % 16 != 0) throw std::runtime_error("queryDensityLogit: n must be a multiple of 16 (caller pads)");
+    if (!m_init) throw std::runtime_error("InstantNerf: query before init()");
+    NerfBuffers& b = B(m_buf);
+    const TinyMLPHashGrid::Buffers db = m_densityMLP->buffers();
+    const graft::MlpShape dshape{2 * m_opts.numLevels, db.hw.hiddenDim, db.hw.outputDim, db.hw.numLayers};
+    const uint32_t cap = renderHitBatch();
+    ensure_render(b, cap, m_colorMLP->buffers().hw.outputDim);
+    for (int off = 0; off < n; off += (int)cap) {
+        const int cn = std::min<int>((int)cap, n - off);
+        graft::FwdInput in;
+        in.pos = d_pos + (size_t)off * 3;
+        in.pos_stride = 3;
+        in.table = db.fwd_hashtable;
+        in.meta = &b.meta;
+        graft::mlp_forward(dshape, in, db.fwd_weights, db.master_biases, nullptr, b.render.density_out, cn,
+                           OUT_ACT_NONE, stream);
+        graft::extract_column(b.render.density_out, 16, d_logit_out + off, cn, stream);
+    }
 }
+
+// queryRadiance (InstantNerf.cu:963-984): colour of contracted positions
+// d_pos [n x 3] seen along viewDir; d_rgb_out [n x 3]; n % 16 == 0.
+void InstantNerf::queryRadiance(const float* d_pos, int n, float3 viewDir, float* d_rgb_out, hipStream_t stream)
+{
+    if (n <= 0) return;
+    if (n % 16 != 0) throw std::runtime_error("queryRadiance: n must be a multiple of 16 (caller pads)");
+    if (!m_init) throw std::runtime_error("InstantNerf: query before init()");
+    NerfBuffers& b = B(m_buf);
+    const TinyMLPHashGrid::Buffers db = m_densityMLP->buffers();
+    const TinyMLP::Buffers cb = m_colorMLP->buffers();
+    const graft::MlpShape dshape{2 * m_opts.numLevels, db.hw.hiddenDim, db.hw.outputDim, db.hw.numLayers};
+    const graft::MlpShape cshape = shape_of(cb.hw);
+    const uint32_t cap = renderHitBatch();
+    ensure_render(b, cap, cshape.out);
+    if (!b.render.dir) b.render.dir = dalloc<float3>(1);
+    GRAFT_HIP_CHECK(hipMemcpyAsync(b.render.dir, &viewDir, sizeof(float3), hipMemcpyHostToDevice, stream));
+    GRAFT_HIP_CHECK(hipMemsetAsync(b.render.ray_idx, 0, (size_t)std::min<int>((int)cap, n) * sizeof(uint32_t), stream));
+    for (int off = 0; off < n; off += (int)cap) {
+        const int cn = std::min<int>((int)cap, n - off);
+        graft::FwdInput in;
+        in.pos = d_pos + (size_t)off * 3;
+        in.pos_stride = 3;
+        in.table = db.fwd_hashtable;
+        in.meta = &b.meta;
+        graft::mlp_forward(dshape, in, db.fwd_weights, db.master_biases, nullptr, b.render.density_out, cn,
+                           OUT_ACT_NONE, stream);
+        graft::sh_gather(b.render.dir, b.render.ray_idx, nullptr, (uint32_t)cn, m_opts.densityBias,
+                         b.render.density_out, b.render.color_in, b.render.sigma, stream);
+        graft::FwdInput ci;
+        ci.x = b.render.color_in;
+        graft::mlp_forward(cshape, ci, cb.fwd_weights, cb.master_biases, nullptr, b.render.rgb, cn,
+                           cb.hw.outputActivation, stream);
+        graft::unpad_f32(b.render.rgb, d_rgb_out + (size_t)off * 3, cn, cshape.out, 3, stream);
+    }
+    GRAFT_HIP_CHECK(hipStreamSynchronize(stream));  // viewDir is a host value
+}
+
+// buildOccupancyBitgrid (InstantNerf.cu:986-1007): bits from the master grid
+// with the per-cascade threshold only (no mean floor), then the mip pyramid.
+void InstantNerf::buildOccupancyBitgrid(uint8_t* d_out, float minDensityThreshold, hipStream_t stream)
+{
+    if (!m_init) throw std::runtime_error("InstantNerf: buildOccupancyBitgrid before init()");
+    NerfBuffers& b = B(m_buf);
+    const int G = grid_cells(m_opts);
+    const int N = m_opts.numCascades * G;
+    const int S = (int)graft::mip_offset(m_opts.gridResolution, m_opts.levelsMipmap);
+    static const float kNoFloor = 1e30f;
+    GRAFT_HIP_CHECK(hipMemcpyAsync(b.sum, &kNoFloor, sizeof(float), hipMemcpyHostToDevice, stream));
+    const float base_voxel = (m_opts.aabbMax.x - m_opts.aabbMin.x) / (float)m_opts.gridResolution.x;
+    graft::update_occupancy_bits(reinterpret_cast<uint32_t*>(d_out), d_masterOccupancyGrid, b.sum, N, G, S,
+                                 minDensityThreshold, base_voxel, stream);
+    graft::build_mipmaps(d_out, m_opts.gridResolution, m_opts.levelsMipmap, m_opts.numCascades, stream);
+}
+
 void InstantNerf::save(const std::string&) { throw std::logic_error("InstantNerf::save is not part of this build"); }
 void InstantNerf::load(const std::string&) { throw std::logic_error("InstantNerf::load is not part of this build"); }

@@ -83,6 +83,13 @@ struct CompositeArgs {
 };
 void composite(const CompositeArgs& a, const uint32_t* d_rays, uint32_t rays_max, hipStream_t s);
 
+// render_rays_kernel (compositing.cu:5-78), the inference compositor: ray r's
+// samples start at offsets[r + rays_done] - base, counts[r] of them; early stop
+// once T < 1e-4.  Uses offsets, counts, t, sigma, rgb (rgb_stride), rgb_true
+// and phi (nullable), final_rgb, final_depth, bg of CompositeArgs.
+void composite_infer(const CompositeArgs& a, uint32_t base, uint32_t rays_done, const uint32_t* d_rays,
+                     uint32_t rays_max, hipStream_t s);
+
 // compute_color_grad (otherKernels.cu:303-409).
 struct ColorGradArgs {
     uint32_t initial_offset;
@@ -122,5 +129,12 @@ void reduce_sum(const float* in, uint32_t n, float* partials, float* out, hipStr
 void update_occupancy_bits(uint32_t* bits32, const float* master, const float* d_sum, int total, int G, int S,
                            float min_optical, float base_voxel, hipStream_t s);
 void build_mipmaps(uint8_t* bits, uint3 res, int mip_levels, int cascades, hipStream_t s);
+
+// extractOccupancyGrid (InstantNerf.cu:882-939): pos [n x 3]; out [ceil(n / 32)]
+// words, bit k of word i for point 32 i + k (exact cascade index).
+void query_occupancy(const float* master, const float* pos, uint32_t* out, uint3 res, float3 mn, float3 mx,
+                     float min_optical, int cascades, int n, hipStream_t s);
+// out[i] = src[i * stride], i < n.
+void extract_column(const float* src, int stride, float* out, int n, hipStream_t s);
 
 }  // namespace graft

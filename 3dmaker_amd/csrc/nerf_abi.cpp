@@ -129,10 +129,22 @@ void launchVolumeRendering(const uint32_t num_rays, const uint32_t* d_ray_offset
                            uint32_t base, uint32_t raysDone, hipStream_t stream)
 {
     guarded("launchVolumeRendering", [&] {
-        (void)base;
-        (void)raysDone;
-        if (!d_dw_out)
-            throw std::logic_error("inference compositing (d_dw_out == NULL) is not part of this build");
+        if (!d_dw_out) {  // render_rays_kernel (compositing.cu:5-78)
+            graft::CompositeArgs a{};
+            a.offsets = d_ray_offsets;
+            a.counts = d_num_steps;
+            a.t = d_t_sorted;
+            a.sigma = d_density_sigma;
+            a.rgb = d_rgb_output;
+            a.rgb_stride = 3;
+            a.rgb_true = d_rgb_true;
+            a.final_rgb = d_render_rgb;
+            a.final_depth = d_render_depth;
+            a.phi = d_phi_out;
+            a.bg = bg_color;
+            graft::composite_infer(a, base, raysDone, nullptr, num_rays, stream);
+            return;
+        }
         graft::CompositeArgs a{};
         a.offsets = d_ray_offsets;
         a.counts = d_num_steps;
@@ -373,6 +385,37 @@ int inerf_stats(Inerf* h, char* buf, int len)
     return (int)s.size();
 }
 int inerf_reset_stats(Inerf* h) { return NERF_CALL("inerf_reset_stats", h->nerf.resetStats()); }
+int inerf_set_memory_mode(Inerf* h, int inference)
+{
+    return NERF_CALL("inerf_set_memory_mode", h->nerf.setMemoryMode(inference ? INFERENCE : TRAINING));
+}
+int inerf_render(Inerf* h, const float* rays_o, const float* rays_d, uint32_t num_rays, float* rgb_out,
+                 hipStream_t stream)
+{
+    return NERF_CALL("inerf_render",
+                     h->nerf.renderImageHit(reinterpret_cast<const float3*>(rays_o),
+                                            reinterpret_cast<const float3*>(rays_d), num_rays, rgb_out, stream));
+}
+int inerf_query_occupancy(Inerf* h, const float* pos, int n, uint32_t* words_out, float min_optical,
+                          hipStream_t stream)
+{
+    return NERF_CALL("inerf_query_occupancy", h->nerf.queryOccupancyGrid(pos, n, words_out, min_optical, stream));
+}
+int inerf_query_density_logit(Inerf* h, const float* pos, int n, float* logit_out, hipStream_t stream)
+{
+    return NERF_CALL("inerf_query_density_logit", h->nerf.queryDensityLogit(pos, n, logit_out, stream));
+}
+int inerf_query_radiance(Inerf* h, const float* pos, int n, float dx, float dy, float dz, float* rgb_out,
+                         hipStream_t stream)
+{
+    return NERF_CALL("inerf_query_radiance",
+                     h->nerf.queryRadiance(pos, n, make_float3(dx, dy, dz), rgb_out, stream));
+}
+int inerf_build_occupancy_bitgrid(Inerf* h, uint8_t* bits_out, float min_density, hipStream_t stream)
+{
+    return NERF_CALL("inerf_build_occupancy_bitgrid", h->nerf.buildOccupancyBitgrid(bits_out, min_density, stream));
+}
+
 int inerf_update_occupancy(Inerf* h, hipStream_t stream)
 {
     return NERF_CALL("inerf_update_occupancy", h->nerf.updateOccupancy(stream));

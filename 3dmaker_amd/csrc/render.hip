@@ -3,6 +3,7 @@
 //
 //   sh_gather       compute_SH_gather              otherKernels.cu:156-273
 //   composite       render_rays_distortion_kernel  compositing.cu:80-213
+//   composite_infer render_rays_kernel             compositing.cu:5-78
 //   color_grad      compute_color_grad             otherKernels.cu:303-409
 //   density_grad    compute_density_grad           otherKernels.cu:497-562
 //   master grid     updateMasterGrid               otherKernels.cu:677-690
@@ -163,6 +164,44 @@ __global__ __launch_bounds__(256) void composite_kernel(const CompositeArgs a, c
     a.final_rgb[3 * r + 1] = gc;
     a.final_rgb[3 * r + 2] = bc;
     a.final_depth[r] = depth;
+    if (a.rgb_true && a.phi) {
+        a.phi[3 * r] = 2.0f * (rc - a.rgb_true[3 * r]);
+        a.phi[3 * r + 1] = 2.0f * (gc - a.rgb_true[3 * r + 1]);
+        a.phi[3 * r + 2] = 2.0f * (bc - a.rgb_true[3 * r + 2]);
+    }
+}
+
+__global__ __launch_bounds__(256) void composite_infer_kernel(const CompositeArgs a, uint32_t base,
+                                                              uint32_t rays_done, const uint32_t* __restrict__ d_rays,
+                                                              uint32_t rays_max)
+{
+    const uint32_t R = dev_count(d_rays, rays_max);
+    const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= R) return;
+    const uint32_t off = a.offsets[r + rays_done] - base, cnt = a.counts[r];
+    float T = 1.0f, rc = 0.0f, gc = 0.0f, bc = 0.0f, depth = 0.0f;
+    for (uint32_t i = 0; i < cnt; i++) {
+        const uint32_t idx = off + i;
+        const float t = a.t[idx];
+        float delta = (i < cnt - 1) ? a.t[idx + 1] - t : 1e-3f;
+        if (delta < 0.0f) delta = 0.0f;
+        const float alpha = 1.0f - nerf_expf(-a.sigma[idx] * delta);
+        const float w = alpha * T;
+        const float* c = a.rgb + (size_t)a.rgb_stride * idx;
+        rc += w * c[0];
+        gc += w * c[1];
+        bc += w * c[2];
+        depth += w * t;
+        T *= (1.0f - alpha);
+        if (T < 1e-4f) break;
+    }
+    rc += T * a.bg.x;
+    gc += T * a.bg.y;
+    bc += T * a.bg.z;
+    a.final_rgb[3 * r] = rc;
+    a.final_rgb[3 * r + 1] = gc;
+    a.final_rgb[3 * r + 2] = bc;
+    if (a.final_depth) a.final_depth[r] = depth;
     if (a.rgb_true && a.phi) {
         a.phi[3 * r] = 2.0f * (rc - a.rgb_true[3 * r]);
         a.phi[3 * r + 1] = 2.0f * (gc - a.rgb_true[3 * r + 1]);
@@ -538,6 +577,44 @@ __global__ __launch_bounds__(256) void occupancy_bits_kernel(uint32_t* __restric
     }
 }
 
+// extractOccupancyGrid (InstantNerf.cu:882-939): one bit per query point, set
+// when the master-grid cell holding it exceeds the cascade's threshold; 32
+// points per output word (bit k of word i = point 32 i + k).
+__global__ __launch_bounds__(256) void query_occupancy_kernel(const float* __restrict__ master,
+                                                              const float* __restrict__ pos,
+                                                              uint32_t* __restrict__ out, uint3 res, float3 mn,
+                                                              float3 mx, float min_optical, int C, int n)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    bool active = false;
+    if (i < n) {
+        const float px = pos[3 * i], py = pos[3 * i + 1], pz = pos[3 * i + 2];
+        const int c = get_cascade(px, py, pz, mn, mx, C);
+        const float cs = ldexpf(1.0f, c);
+        const float ex = mx.x - mn.x, ey = mx.y - mn.y, ez = mx.z - mn.z;
+        const float rx = (px - mn.x * cs) / (ex * cs), ry = (py - mn.y * cs) / (ey * cs);
+        const float rz = (pz - mn.z * cs) / (ez * cs);
+        const int vx = clamp_floor_idx(floorf(rx * (float)res.x), (int)res.x - 1);
+        const int vy = clamp_floor_idx(floorf(ry * (float)res.y), (int)res.y - 1);
+        const int vz = clamp_floor_idx(floorf(rz * (float)res.z), (int)res.z - 1);
+        const uint32_t flat = (uint32_t)c * (res.x * res.y * res.z) + (uint32_t)vz * (res.x * res.y) +
+                              (uint32_t)vy * res.x + (uint32_t)vx;
+        const float base_voxel = ex / (float)res.x;
+        active = master[flat] > (min_optical / base_voxel) / cs;
+    }
+    const uint64_t m = __ballot(active);
+    const int lane = threadIdx.x & 63;
+    if ((lane & 31) == 0 && i < n) out[i >> 5] = (uint32_t)(m >> lane);
+}
+
+// out[i] = src[i * stride] (k_extractDensityLogit, InstantNerf.cu:866-870).
+__global__ __launch_bounds__(256) void column_kernel(const float* __restrict__ src, int stride,
+                                                     float* __restrict__ out, int n)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = src[(size_t)i * stride];
+}
+
 __global__ __launch_bounds__(256) void mip_pool_kernel(const uint8_t* __restrict__ in, uint8_t* __restrict__ out,
                                                        uint3 ro)
 {
@@ -583,6 +660,15 @@ void composite(const CompositeArgs& a, const uint32_t* d_rays, uint32_t rays_max
 {
     if (rays_max == 0) return;
     hipLaunchKernelGGL(composite_kernel, dim3(blocks_for(rays_max)), dim3(256), 0, s, a, d_rays, rays_max);
+    GRAFT_LAUNCH_CHECK();
+}
+
+void composite_infer(const CompositeArgs& a, uint32_t base, uint32_t rays_done, const uint32_t* d_rays,
+                     uint32_t rays_max, hipStream_t s)
+{
+    if (rays_max == 0) return;
+    hipLaunchKernelGGL(composite_infer_kernel, dim3(blocks_for(rays_max)), dim3(256), 0, s, a, base, rays_done,
+                       d_rays, rays_max);
     GRAFT_LAUNCH_CHECK();
 }
 
@@ -637,6 +723,22 @@ void update_occupancy_bits(uint32_t* bits32, const float* master, const float* d
     if (G % 32 || S % 32) throw std::runtime_error("occupancy: cells per cascade must be multiples of 32");
     hipLaunchKernelGGL(occupancy_bits_kernel, dim3(blocks_for((uint32_t)total)), dim3(256), 0, s, bits32, master,
                        d_sum, total, G, S, min_optical, base_voxel);
+    GRAFT_LAUNCH_CHECK();
+}
+
+void query_occupancy(const float* master, const float* pos, uint32_t* out, uint3 res, float3 mn, float3 mx,
+                     float min_optical, int C, int n, hipStream_t s)
+{
+    if (n <= 0) return;
+    hipLaunchKernelGGL(query_occupancy_kernel, dim3(blocks_for((uint32_t)n)), dim3(256), 0, s, master, pos, out, res,
+                       mn, mx, min_optical, C, n);
+    GRAFT_LAUNCH_CHECK();
+}
+
+void extract_column(const float* src, int stride, float* out, int n, hipStream_t s)
+{
+    if (n <= 0) return;
+    hipLaunchKernelGGL(column_kernel, dim3(blocks_for((uint32_t)n)), dim3(256), 0, s, src, stride, out, n);
     GRAFT_LAUNCH_CHECK();
 }
 

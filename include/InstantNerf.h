@@ -21,8 +21,12 @@
 //    never end up with zero active rays (the reference prints and returns);
 //  - occupancy refresh uses this library's own Philox4x32-10 stream and a
 //    fixed-order sum, so its random samples are not the reference's.
-// Render paths (renderImage/renderImageHit/query*) and .inerf save/load are
-// not part of this build and throw std::logic_error.
+// Rendering (renderImageHit, InstantNerf.cu:713-864; renderImage behind
+// legacyRenderFlag) marches each ray chunk once and composites every hit
+// batch with the inference compositor (compositing.cu:5-78).  MemoryMode only
+// selects the render hit batch (renderBatchSize in INFERENCE, batchSize in
+// TRAINING); training state stays allocated, and trainWithRaysHit requires
+// TRAINING.  .inerf save/load throw std::logic_error (not part of this build).
 #pragma once
 
 #include <hip/hip_fp16.h>
@@ -113,6 +117,8 @@ public:
                      hipStream_t stream = 0);
     void renderImageHit(const float3* d_rays_o, const float3* d_rays_d, uint32_t numRays, float* d_rgb_out,
                         hipStream_t stream);
+    // InstantNerf.cu:941-984.  d_pos holds n contracted positions as x,y,z
+    // triples; density/radiance queries need n % 16 == 0.
     void queryOccupancyGrid(const float* d_pos, int n, uint32_t* d_data_out, float minOpticalThreshold,
                             hipStream_t stream = 0);
     void queryDensityLogit(const float* d_pos, int n, float* d_logit_out, hipStream_t stream = 0);
@@ -166,6 +172,7 @@ private:
     void earlyOccupancyGridUpdate(hipStream_t stream);
     void lateOccupancyGridUpdate(hipStream_t stream);
     void finishOccupancyUpdate(hipStream_t stream);
+    uint32_t renderHitBatch() const;
 
     NerfOptions m_opts{};
     MemoryMode m_memMode = TRAINING;

@@ -42,10 +42,12 @@ int processRaysHitLinear(const uint32_t num_rays, const float3* rays_o, const fl
                          float* d_mlp_positions_batch, uint32_t* d_ray_indices, float* d_t_sorted,
                          uint32_t* d_block_sums, hipStream_t stream);
 
-/* compositing.cu:215-279 (declared InstantNerf.h:444-465): with d_dw_out set,
- * the training compositor with the distortion loss (render_rays_distortion_kernel).
- * base and raysDone are accepted for signature compatibility (the training
- * path passes 0). */
+/* compositing.cu:215-279 (declared InstantNerf.h:444-465).  d_dw_out set: the
+ * training compositor with the distortion loss (render_rays_distortion_kernel;
+ * base and raysDone unused, the training path passes 0).  d_dw_out NULL: the
+ * inference compositor (render_rays_kernel, compositing.cu:5-78): ray r's
+ * samples start at d_ray_offsets[r + raysDone] - base, d_num_steps[r] of them,
+ * early stop once transmittance < 1e-4; d_rgb_true / d_phi_out nullable. */
 void launchVolumeRendering(const uint32_t num_rays, const uint32_t* d_ray_offsets, const uint32_t* d_num_steps,
                            const float* d_t_sorted, const float* d_density_sigma, const float* d_depth_chunk,
                            const float* d_sigma_chunk, const float* d_rgb_output, const float* d_rgb_true,

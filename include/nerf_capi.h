@@ -74,6 +74,20 @@ int inerf_print_stats(Inerf* h);
  * truncated to len); returns the full length.  inerf_reset_stats clears them. */
 int inerf_stats(Inerf* h, char* buf, int len);
 int inerf_reset_stats(Inerf* h);
+/* InstantNerf::setMemoryMode (InstantNerf.h:294): 0 TRAINING, 1 INFERENCE. */
+int inerf_set_memory_mode(Inerf* h, int inference);
+/* InstantNerf::renderImageHit (InstantNerf.h:317-323): rays as float3 [n],
+ * rgb_out [n x 3] device pointers. */
+int inerf_render(Inerf* h, const float* rays_o, const float* rays_d, uint32_t num_rays, float* rgb_out,
+                 hipStream_t stream);
+/* InstantNerf::queryOccupancyGrid / queryDensityLogit / queryRadiance /
+ * buildOccupancyBitgrid (InstantNerf.h:325-328); pos is [n x 3] on the device. */
+int inerf_query_occupancy(Inerf* h, const float* pos, int n, uint32_t* words_out, float min_optical,
+                          hipStream_t stream);
+int inerf_query_density_logit(Inerf* h, const float* pos, int n, float* logit_out, hipStream_t stream);
+int inerf_query_radiance(Inerf* h, const float* pos, int n, float dx, float dy, float dz, float* rgb_out,
+                         hipStream_t stream);
+int inerf_build_occupancy_bitgrid(Inerf* h, uint8_t* bits_out, float min_density, hipStream_t stream);
 int inerf_update_occupancy(Inerf* h, hipStream_t stream);
 size_t inerf_occupancy_bytes(Inerf* h);
 int inerf_get_occupancy(Inerf* h, uint8_t* host_bits);

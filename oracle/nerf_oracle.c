@@ -308,6 +308,45 @@ static float disparity_warp(float t, float t_near, float inv_g_range)
     return (1.0f - t_near / fmaxf(t, 1e-4f)) * inv_g_range;
 }
 
+void orc_composite_infer(uint32_t R, uint32_t base, uint32_t rays_done, const uint32_t* offsets,
+                         const uint32_t* counts, const float* ts, const float* sig, const float* rgb,
+                         int rgb_stride, const float* rgb_true, float* final_rgb, float* final_depth, float* phi,
+                         const float* bg)
+{
+#pragma omp parallel for schedule(dynamic, 256)
+    for (long long r = 0; r < (long long)R; r++) {
+        const uint32_t off = offsets[r + rays_done] - base, cnt = counts[r];
+        float T = 1.0f, rc = 0.0f, gc = 0.0f, bc = 0.0f, depth = 0.0f;
+        for (uint32_t i = 0; i < cnt; i++) {
+            const uint32_t idx = off + i;
+            const float t = ts[idx];
+            float delta = (i < cnt - 1) ? ts[idx + 1] - t : 1e-3f;
+            if (delta < 0.0f) delta = 0.0f;
+            const float alpha = 1.0f - orc_expf(-sig[idx] * delta);
+            const float w = alpha * T;
+            const float* c = rgb + (size_t)rgb_stride * idx;
+            rc += w * c[0];
+            gc += w * c[1];
+            bc += w * c[2];
+            depth += w * t;
+            T *= (1.0f - alpha);
+            if (T < 1e-4f) break;
+        }
+        rc += T * bg[0];
+        gc += T * bg[1];
+        bc += T * bg[2];
+        final_rgb[3 * r] = rc;
+        final_rgb[3 * r + 1] = gc;
+        final_rgb[3 * r + 2] = bc;
+        final_depth[r] = depth;
+        if (rgb_true && phi) {
+            phi[3 * r] = 2.0f * (rc - rgb_true[3 * r]);
+            phi[3 * r + 1] = 2.0f * (gc - rgb_true[3 * r + 1]);
+            phi[3 * r + 2] = 2.0f * (bc - rgb_true[3 * r + 2]);
+        }
+    }
+}
+
 void orc_composite_distortion(uint32_t R, const uint32_t* offsets, const uint32_t* counts, const float* ts,
                               const float* sig, const float* depth_prior, const float* sigma_prior,
                               const float* rgb, const float* rgb_true, float* final_rgb, float* final_depth,

@@ -81,6 +81,15 @@ void orc_composite_distortion(uint32_t R, const uint32_t* offsets, const uint32_
                               float* weight_sum, float lambda_dist, float lambda_depth,
                               const float* bg3);
 
+/* render_rays_kernel (compositing.cu:5-78), the inference compositor: sample
+ * i of ray r sits at offsets[r + rays_done] - base + i, the last sample's
+ * delta is 1e-3, rays stop early once T < 1e-4; rgb has rgb_stride floats per
+ * sample (3 in the reference).  rgb_true and phi are nullable. */
+void orc_composite_infer(uint32_t R, uint32_t base, uint32_t rays_done, const uint32_t* offsets,
+                         const uint32_t* counts, const float* t, const float* sigma, const float* rgb,
+                         int rgb_stride, const float* rgb_true, float* final_rgb, float* final_depth, float* phi,
+                         const float* bg3);
+
 /* compute_color_grad (otherKernels.cu:303-409) with initialOffset = 0:
  * fp16 dL/dc [N][3] and fp32 dsigma [N]. */
 void orc_color_grad(uint32_t R, const uint32_t* counts, const uint32_t* offsets, const float* t,

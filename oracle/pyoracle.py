@@ -71,6 +71,8 @@ def lib():
             "orc_composite_distortion": (None, [C.c_uint32, _u32p, _u32p, _f32p, _f32p, C.c_void_p, C.c_void_p,
                                                 _f32p, C.c_void_p, _f32p, _f32p, C.c_void_p, _f32p, _f32p, f, f,
                                                 _f32p]),
+            "orc_composite_infer": (None, [C.c_uint32, C.c_uint32, C.c_uint32, _u32p, _u32p, _f32p, _f32p, _f32p,
+                                           i, C.c_void_p, _f32p, _f32p, C.c_void_p, _f32p]),
             "orc_color_grad": (None, [C.c_uint32, _u32p, _u32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p,
                                       _u16p, _f32p, f, f, C.c_uint32]),
             "orc_density_grad": (None, [C.c_uint32, _f32p, _u16p, _u16p]),
@@ -322,6 +324,24 @@ def composite(offsets, counts, t, sigma, rgb, rgb_true, lambda_dist, bg, depth_p
                                    _vp(phi if rt is not None else None), dw, ws, float(lambda_dist),
                                    float(lambda_depth), _f3(bg))
     return dict(rgb=frgb.reshape(R, 3), depth=fdep, phi=phi.reshape(R, 3), dw=dw[:len(t)], weight_sum=ws)
+
+
+def composite_infer(offsets, counts, t, sigma, rgb, bg, rgb_true=None, base=0, rays_done=0):
+    """Inference compositor; offsets indexed from rays_done, counts per ray of this call."""
+    R = len(counts)
+    rgb = np.ascontiguousarray(rgb, np.float32)
+    stride = rgb.shape[1] if rgb.ndim == 2 else 3
+    frgb = np.zeros(3 * R, np.float32)
+    fdep = np.zeros(R, np.float32)
+    phi = np.zeros(3 * R, np.float32)
+    rt = None if rgb_true is None else _f3(rgb_true)
+    lib().orc_composite_infer(R, int(base), int(rays_done), np.ascontiguousarray(offsets, np.uint32),
+                              np.ascontiguousarray(counts, np.uint32),
+                              _f3(t) if len(t) else np.zeros(1, np.float32),
+                              _f3(sigma) if len(t) else np.zeros(1, np.float32),
+                              rgb.reshape(-1) if len(t) else np.zeros(3, np.float32), int(stride), _vp(rt), frgb,
+                              fdep, _vp(phi if rt is not None else None), _f3(bg))
+    return dict(rgb=frgb.reshape(R, 3), depth=fdep, phi=phi.reshape(R, 3))
 
 
 def color_grad(counts, offsets, t, density_out, color_out, phi, final_rgb, dw, weight_sum, loss_scale,

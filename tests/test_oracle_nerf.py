@@ -365,6 +365,48 @@ def test_composite_closed_forms_and_distortion_gradient():
         np.testing.assert_allclose(r["weight_sum"][i], (w * want).sum(), rtol=tol, atol=1e-7)
 
 
+def test_composite_infer_closed_forms_early_stop_and_offsets():
+    """Inference compositor (compositing.cu:5-78): NeRF quadrature in fp64 up to
+    the first sample after which T < 1e-4; last delta 1e-3; offsets read at
+    r + rays_done minus base."""
+    cnt, off, t, rng = make_rays(300, 40, 17)
+    N = len(t)
+    sig = rng.exponential(4.0, N).astype(np.float32)
+    sig[::7] *= 200.0  # opaque samples: early termination inside rays
+    rgb = rng.random((N, 8)).astype(np.float32)  # padded stride 8, colour in columns 0..2
+    bg = np.float32([0.3, 0.5, 0.7])
+    gt = rng.random((300, 3)).astype(np.float32)
+    r = orc.composite_infer(off, cnt, t, sig, rgb, bg, rgb_true=gt)
+    stopped = 0
+    for i in range(300):
+        a, n = int(off[i]), int(cnt[i])
+        T, C, D = 1.0, np.zeros(3), 0.0
+        for k in range(n):
+            delta = (float(t[a + k + 1]) - float(t[a + k])) if k < n - 1 else 1e-3
+            alpha = 1 - np.exp(-float(sig[a + k]) * max(delta, 0.0))
+            C += alpha * T * rgb[a + k, :3]
+            D += alpha * T * float(t[a + k])
+            T *= 1 - alpha
+            if T < 1e-4:
+                stopped += k < n - 1
+                break
+        C += T * bg
+        np.testing.assert_allclose(r["rgb"][i], C, rtol=2e-5, atol=2e-6)
+        np.testing.assert_allclose(r["depth"][i], D, rtol=2e-5, atol=2e-6)
+        np.testing.assert_allclose(r["phi"][i], 2 * (C - gt[i]), rtol=1e-4, atol=1e-5)
+    assert stopped > 20
+    # constant sigma and colour: C = c (1 - T_N) + T_N bg with T_N = exp(-sigma sum delta)
+    t1 = np.float32([0.5, 0.75, 1.0, 1.25])
+    one = orc.composite_infer(np.uint32([0]), np.uint32([4]), t1, np.full(4, 0.8, np.float32),
+                              np.full((4, 3), 0.25, np.float32), bg)
+    TN = np.exp(-0.8 * (0.75 + 1e-3))
+    np.testing.assert_allclose(one["rgb"][0], 0.25 * (1 - TN) + TN * bg, rtol=1e-6)
+    # offsets of a later batch: sample i of ray r at offsets[r + rays_done] - base
+    base, done = int(off[100]), 100
+    sub = orc.composite_infer(off, cnt[done:], t[base:], sig[base:], rgb[base:], bg, base=base, rays_done=done)
+    np.testing.assert_array_equal(sub["rgb"].view(np.uint32), r["rgb"][done:].view(np.uint32))
+
+
 def render_loss(logits, t, c_pre, gt, bg, lam):
     """fp64 loss of one ray as a function of density logits and pre-sigmoid colours."""
     n = len(t)
