@@ -149,6 +149,8 @@ SIGNATURES = {
     "launchVolumeRendering": (None, [_u32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f, _f,
                                      Float3, _u32, _u32, _vp]),
     "launchComputeRayAabbInv": (None, [_u32, _vp, _vp, Float3, Float3, _i, _vp, _vp, _vp, _vp]),
+    "launchFetchRayChunk": (None, [_i, _i, _i, _u32, _i, _i, _i, _f, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                   _vp, _vp, _vp, _vp, _vp, _u32, _f, _f, _f, Float3, _i, _vp]),
     "launchComputeSHGather": (None, [_vp, _vp, _i, _i, _f, _vp, _vp, _vp, _vp]),
     "launchComputeColorGrad": (None, [_u32, _u32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f, _f,
                                       _u32, _vp]),

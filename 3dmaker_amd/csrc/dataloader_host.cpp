@@ -1,0 +1,142 @@
+// DataLoader (include/DataLoader.h): device-resident dataset + ray feed, and
+// the launchFetchRayChunk C-ABI entry point.
+#include "DataLoader.h"
+
+#include "abi_error.h"
+#include "dataloader.h"
+#include "nerf_abi.h"
+
+#include <stdexcept>
+
+namespace {
+
+template <class T>
+T* dcopy(const T* host, size_t n)
+{
+    void* p = nullptr;
+    GRAFT_HIP_CHECK(hipMalloc(&p, n * sizeof(T)));
+    if (host) GRAFT_HIP_CHECK(hipMemcpy(p, host, n * sizeof(T), hipMemcpyHostToDevice));
+    return static_cast<T*>(p);
+}
+
+template <class T>
+void dfree(T*& p)
+{
+    if (p) (void)hipFree(p);
+    p = nullptr;
+}
+
+}  // namespace
+
+DataLoader::DataLoader(const uint8_t* host_rgba, const float* host_transforms, int numImages, int w, int h, float f,
+                       uint32_t ray_chunk_size, bool is_training, float dense_fraction)
+    : width(w), height(h), num_images(numImages), focal(f), m_chunk(ray_chunk_size), m_is_training(is_training),
+      m_dense_fraction(dense_fraction)
+{
+    if (!host_rgba || !host_transforms || numImages <= 0 || w <= 0 || h <= 0 || ray_chunk_size == 0)
+        throw std::runtime_error("DataLoader: empty dataset or chunk");
+    const size_t pixels = (size_t)w * (size_t)h * (size_t)numImages;
+    if (pixels > 0xffffffffull) throw std::runtime_error("DataLoader: more than 2^32 pixels");
+    total_rays = (uint32_t)pixels;
+    d_images_rgba = dcopy(host_rgba, pixels * 4);
+    d_transforms = dcopy(host_transforms, (size_t)numImages * 16);
+    d_chunk_rays_o = dcopy<float3>(nullptr, m_chunk);
+    d_chunk_rays_d = dcopy<float3>(nullptr, m_chunk);
+    d_chunk_rgb_true = dcopy<float>(nullptr, (size_t)m_chunk * 3);
+    d_chunk_rays_dense = dcopy<float>(nullptr, m_chunk);
+    d_chunk_rays_sigma = dcopy<float>(nullptr, m_chunk);
+}
+
+DataLoader::~DataLoader() { freeVRAM(); }
+
+void DataLoader::freeVRAM()
+{
+    dfree(d_images_rgba);
+    dfree(d_transforms);
+    dfree(d_chunk_rays_o);
+    dfree(d_chunk_rays_d);
+    dfree(d_chunk_rgb_true);
+    dfree(d_chunk_rays_dense);
+    dfree(d_chunk_rays_sigma);
+    dfree(d_rec_frame);
+    dfree(d_rec_u);
+    dfree(d_rec_v);
+    dfree(d_rec_D);
+    dfree(d_rec_sigma);
+    m_num_records = 0;
+}
+
+void DataLoader::setDepthPriors(const int* frame, const float* u, const float* v, const float* D, const float* sigma,
+                                uint32_t n, int depth_width, int depth_height)
+{
+    dfree(d_rec_frame);
+    dfree(d_rec_u);
+    dfree(d_rec_v);
+    dfree(d_rec_D);
+    dfree(d_rec_sigma);
+    m_num_records = 0;
+    if (n == 0) return;
+    for (uint32_t i = 0; i < n; i++)
+        if (frame[i] < 0 || frame[i] >= num_images) throw std::runtime_error("DataLoader: depth prior frame out of range");
+    d_rec_frame = dcopy(frame, n);
+    d_rec_u = dcopy(u, n);
+    d_rec_v = dcopy(v, n);
+    d_rec_D = dcopy(D, n);
+    d_rec_sigma = dcopy(sigma, n);
+    m_num_records = n;
+    m_depth_width = depth_width;
+    m_depth_height = depth_height;
+}
+
+void DataLoader::fetchRayChunk(int offset, int size, uint32_t seed, float3 bg_color, hipStream_t stream,
+                               bool forceSequential, int holdout_every)
+{
+    if (!d_images_rgba) throw std::runtime_error("DataLoader: data freed");
+    if (size < 0 || (uint32_t)size > m_chunk) throw std::runtime_error("DataLoader: chunk larger than ray_chunk_size");
+    graft::RayFeedArgs a{};
+    a.offset = offset;
+    a.size = size;
+    a.total_rays = (int)total_rays;
+    a.seed = seed;
+    a.randomize = (m_is_training && !forceSequential) ? 1 : 0;
+    a.width = width;
+    a.height = height;
+    a.focal = focal;
+    a.transforms = d_transforms;
+    a.images_rgba = d_images_rgba;
+    a.rays_o = d_chunk_rays_o;
+    a.rays_d = d_chunk_rays_d;
+    a.rgb = d_chunk_rgb_true;
+    a.dense = d_chunk_rays_dense;
+    a.sigma = d_chunk_rays_sigma;
+    a.rec_frame = d_rec_frame;
+    a.rec_u = d_rec_u;
+    a.rec_v = d_rec_v;
+    a.rec_D = d_rec_D;
+    a.rec_sigma = d_rec_sigma;
+    a.num_records = m_num_records;
+    a.dense_fraction = m_dense_fraction;
+    a.uv_scale_x = m_depth_width > 0 ? (float)width / (float)m_depth_width : 1.0f;
+    a.uv_scale_y = m_depth_height > 0 ? (float)height / (float)m_depth_height : 1.0f;
+    a.bg = bg_color;
+    a.holdout_every = holdout_every;
+    graft::fetch_ray_chunk(a, stream);
+}
+
+extern "C" void launchFetchRayChunk(int offset, int size, int total_rays, uint32_t seed, int randomize, int width,
+                                    int height, float focal_length, const float* d_transforms,
+                                    const uint8_t* d_images_rgba, float3* d_chunk_rays_o, float3* d_chunk_rays_d,
+                                    float* d_chunk_rgb, float* d_chunk_dense, float* d_chunk_sigma,
+                                    const int* rec_frame, const float* rec_u, const float* rec_v, const float* rec_D,
+                                    const float* rec_sigma, uint32_t num_records, float dense_fraction,
+                                    float uv_scale_x, float uv_scale_y, float3 bg_color, int holdout_every,
+                                    hipStream_t stream)
+{
+    graft::guarded("launchFetchRayChunk", [&] {
+        graft::RayFeedArgs a{offset, size, total_rays, seed, randomize, width, height, focal_length, d_transforms,
+                             d_images_rgba, d_chunk_rays_o, d_chunk_rays_d, d_chunk_rgb, d_chunk_dense,
+                             d_chunk_sigma, rec_frame, rec_u, rec_v, rec_D, rec_sigma, num_records, dense_fraction,
+                             uv_scale_x, uv_scale_y, bg_color, holdout_every};
+        graft::fetch_ray_chunk(a, stream);
+    });
+}

@@ -160,19 +160,19 @@ class SphereScene:
             out[s:s + chunk] = (w[..., None] * c).sum(1) + (T[:, -1] * (1.0 - alpha[:, -1]))[:, None] * bgv
         return out.astype(np.float32)
 
-    def render_device(self, o, d, near=0.0, far=3.5, steps=1024, bg=(1.0, 1.0, 1.0), chunk=1 << 16):
-        """render() evaluated with torch on the tensors' device (fp32): the same
-        quadrature for ray pools too large for the host."""
+    def render_device_rgba(self, o, d, near=0.0, far=3.5, steps=1024, chunk=1 << 16):
+        """(colour over a black background [N, 3], opacity 1 - T [N]) by the
+        quadrature of render(), evaluated with torch on the tensors' device (fp32)."""
         import torch
         dev = o.device
         cen = torch.tensor(self.centres, dtype=torch.float32, device=dev)
         rad = torch.tensor(self.radii, dtype=torch.float32, device=dev)
         fr = torch.tensor(self.freq, dtype=torch.float32, device=dev)
         ph = torch.tensor(self.phase, dtype=torch.float32, device=dev)
-        bgv = torch.tensor(bg, dtype=torch.float32, device=dev)
         dt = (far - near) / steps
         ts = near + (torch.arange(steps, device=dev, dtype=torch.float32) + 0.5) * dt
-        out = torch.empty((o.shape[0], 3), dtype=torch.float32, device=dev)
+        col = torch.empty((o.shape[0], 3), dtype=torch.float32, device=dev)
+        alpha_out = torch.empty(o.shape[0], dtype=torch.float32, device=dev)
         for s in range(0, o.shape[0], chunk):
             oo, dd = o[s:s + chunk], d[s:s + chunk]
             p = oo[:, None, :] + ts[None, :, None] * dd[:, None, :]
@@ -182,5 +182,48 @@ class SphereScene:
             T = torch.cumprod(torch.cat([torch.ones_like(alpha[:, :1]), 1.0 - alpha[:, :-1]], dim=1), dim=1)
             w = T * alpha
             c = 0.5 + 0.5 * torch.sin(p @ fr.T + ph)
-            out[s:s + chunk] = (w[..., None] * c).sum(1) + (T[:, -1] * (1.0 - alpha[:, -1]))[:, None] * bgv
-        return out
+            col[s:s + chunk] = (w[..., None] * c).sum(1)
+            alpha_out[s:s + chunk] = 1.0 - T[:, -1] * (1.0 - alpha[:, -1])
+        return col, alpha_out
+
+    def render_device(self, o, d, near=0.0, far=3.5, steps=1024, bg=(1.0, 1.0, 1.0), chunk=1 << 16):
+        """render() evaluated with torch on the tensors' device (fp32): the same
+        quadrature for ray pools too large for the host."""
+        import torch
+        col, a = self.render_device_rgba(o, d, near, far, steps, chunk)
+        bgv = torch.tensor(bg, dtype=torch.float32, device=o.device)
+        return col + (1.0 - a)[:, None] * bgv
+
+def feed_pixel_rays(c2w: np.ndarray, cam: int, width: int, height: int, focal: float):
+    """Rays of every pixel of camera cam as the training ray feed builds them
+    (DataLoader.cu:623-641): pixel (px, py) -> ((px - w/2)/f, -(py - h/2)/f, -1)."""
+    py, px = np.meshgrid(np.arange(height, dtype=np.float64), np.arange(width, dtype=np.float64), indexing="ij")
+    dx = (px.ravel() - width * 0.5) / focal
+    dy = -(py.ravel() - height * 0.5) / focal
+    v = np.stack([dx, dy, -np.ones_like(dx)], axis=1)
+    v /= np.linalg.norm(v, axis=1, keepdims=True)
+    d = v @ c2w[cam, :, :3].T
+    o = np.broadcast_to(c2w[cam, :, 3], d.shape)
+    return np.ascontiguousarray(o, np.float32), np.ascontiguousarray(d, np.float32)
+
+
+def render_views(scene: "SphereScene", c2w: np.ndarray, width: int, height: int, fov_x: float, device, steps=1024):
+    """A dataset for the ray feed: RGBA8 images [n, h, w, 4] (uint8 tensor on device,
+    straight colour + opacity) and camera-to-world matrices [n, 16] (float32,
+    row-major 4x4) of the analytic scene seen from cameras c2w [n, 3, 4]."""
+    import torch
+    focal = focal_from_fov(width, fov_x)
+    n = c2w.shape[0]
+    imgs = torch.empty((n, height, width, 4), dtype=torch.uint8, device=device)
+    for k in range(n):
+        o, d = feed_pixel_rays(c2w, k, width, height, focal)
+        c0, a = scene.render_device_rgba(torch.from_numpy(o).to(device), torch.from_numpy(d).to(device), steps=steps)
+        straight = torch.where(a[:, None] > 1e-6, c0 / a.clamp_min(1e-6)[:, None], torch.zeros_like(c0))
+        rgba = torch.cat([straight.clamp(0, 1), a[:, None]], dim=1)
+        imgs[k] = torch.round(rgba * 255.0).to(torch.uint8).view(height, width, 4)
+    T = np.zeros((n, 16), np.float32)
+    for k in range(n):
+        m = np.eye(4)
+        m[:3, :] = c2w[k]
+        T[k] = m.reshape(-1)
+    return imgs, T

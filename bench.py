@@ -2,25 +2,32 @@
 """Benchmark: the full NeRF training step of 3DMaker on one MI355X.
 
 Workload (the end-to-end configuration; the reference's
-step is InstantNerf::trainWithRaysHit, modules/NeRF/InstantNerf.cu:359-583):
+step is InstantNerf::trainWithRaysHit, modules/NeRF/InstantNerf.cu:359-583,
+driven by INerfTrainer::trainOneChunk, NerfTrainer.cu:137-179):
   procedural scene (3 seeded spheres, sigma_max * sigmoid(-sdf / 0.01), 3-band
-  sinusoidal colour), ground truth rendered by fixed-step quadrature for a pool
-  of rays from 100 cameras at 800x800, fov 50 deg, on a radius-1.5 sphere;
-  occupancy 128^3 x 5 cascades x 4 mips, AABB +-1.5, K = 1; hash grid L = 16,
-  F = 2, T = 2^19, base 16, b = 1.3819; density 32 -> 64 -> 16, colour
+  sinusoidal colour) rendered by fixed-step quadrature into 100 RGBA8 views of
+  800x800 (fov 50 deg, cameras on a radius-1.5 sphere), resident in HBM; the
+  ray feed (launchFetchRayChunk, DataLoader.cu:548-661) draws 2^16 rays per
+  trainWithRaysHit call with pcg_hash and composites them over a random
+  background colour per call, as the reference trainer does; occupancy
+  128^3 x 5 cascades x 4 mips, AABB +-1.5, K = 1; hash grid L = 16, F = 2,
+  T = 2^19, base 16, b = 1.3819; density 32 -> 64 -> 16, colour
   32 -> 64 -> 64 -> 3 (sigmoid); distortion loss lambda = 0.1; loss scale 128;
   Adam (0.9, 0.999, 1e-8); cosine LR 1e-2 -> 1e-4 over 2000 steps; occupancy
   refreshed every 16 steps (one jittered sample per cell for the first 256
   steps, then half the cells' worth of occupied/uniform samples).
 One step = one optimizer step on one hit batch of at most 2^18 compacted
-samples: ray setup, DDA count/scan/cutoff/fill, fused hash encode + density
-MLP forward, SH gather, colour MLP forward, compositing with distortion,
-colour/density gradients, both MLP backwards, hash scatter, Adam over all
-parameters (16.8 M table entries), plus the amortised occupancy refresh.
-Rays come 2^16 per trainWithRaysHit call (the reference trainer's chunk), the
-ray pool and ground truth are resident in HBM before timing starts.
+samples: ray setup, DDA march (once per ray window and grid version),
+compaction, fused hash encode + density MLP forward, SH gather, colour MLP
+forward, compositing with distortion, colour/density gradients, both MLP
+backwards, hash scatter, Adam over all parameters (16.8 M table entries),
+plus the amortised ray fetch and occupancy refresh.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--profile-steps N]
+After the timed steps the run continues (untimed) to the end of the 2000-step
+cosine schedule and reports PSNR on 12 held-out 800x800 views (their own
+camera lattice), rendered with renderImageHit over sequential feed chunks.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--profile-steps N] [--psnr-steps S]
 
 Prints ONE JSON line.
 """
@@ -46,7 +53,7 @@ REF_HASHGRID_TRAIN_MS = 12.200  # TinyMLPHashGrid 64x2 train step at 2^18, RTX 4
 
 BATCH = 1 << 18
 RAYS_PER_CALL = 1 << 16
-POOL = 1 << 21
+N_VIEWS, N_HELDOUT, IMG_W, IMG_H, FOV_X = 100, 12, 800, 800, 50.0
 L, F, TBL, BASE, GROWTH = 16, 2, 1 << 19, 16, 1.3819
 LR_MAX, LR_MIN, ANNEAL = 1e-2, 1e-4, 2000
 
@@ -77,6 +84,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline leg")
     ap.add_argument("--profile-steps", type=int, default=0,
                     help="run --warmup steps, then this many, and exit (for rocprofv3)")
+    ap.add_argument("--psnr-steps", type=int, default=ANNEAL,
+                    help="train (untimed) up to this many steps, then report PSNR on 12 held-out views (-1: skip)")
     ap.add_argument("--components", action="store_true",
                     help="only time the stand-alone encode / scatter launches at 2^18 and exit")
     return ap.parse_args()
@@ -105,23 +114,57 @@ def cosine_lr(step):
     return LR_MIN + 0.5 * (LR_MAX - LR_MIN) * (1.0 + math.cos(math.pi * p))
 
 
-class Trainer:
-    """Feeds the ray pool to InstantNerf 2^16 rays per call (NerfTrainer.cu:137-179)."""
+class RayFeed:
+    """Device-resident RGBA8 views + launchFetchRayChunk (DataLoader.cu:548-679)."""
 
-    def __init__(self, nerf, o, d, gt, stream):
-        self.nerf, self.o, self.d, self.gt, self.stream = nerf, o, d, gt, stream
+    def __init__(self, P, torch, imgs, transforms, width, height, focal, chunk):
+        dev = imgs.device
+        self.P, self.imgs, self.w, self.h, self.focal, self.chunk = P, imgs, width, height, focal, chunk
+        self.T = torch.from_numpy(transforms).to(dev)
+        self.total = int(imgs.shape[0]) * width * height
+        self.o = torch.empty((chunk, 3), device=dev)
+        self.d = torch.empty((chunk, 3), device=dev)
+        self.rgb = torch.empty((chunk, 3), device=dev)
+        self.dense = torch.empty(chunk, device=dev)
+        self.sigma = torch.empty(chunk, device=dev)
+
+    def fetch(self, offset, size, seed, bg, stream, sequential=False):
+        self.P.lib().launchFetchRayChunk(int(offset), int(size), self.total, int(seed) & 0xffffffff,
+                                         0 if sequential else 1, self.w, self.h, float(self.focal),
+                                         self.T.data_ptr(), self.imgs.data_ptr(), self.o.data_ptr(),
+                                         self.d.data_ptr(), self.rgb.data_ptr(), self.dense.data_ptr(),
+                                         self.sigma.data_ptr(), None, None, None, None, None, 0, 0.0, 1.0, 1.0,
+                                         self.P.Float3(*map(float, bg)), 0, stream)
+
+
+class Trainer:
+    """INerfTrainer::trainOneChunk (NerfTrainer.cu:137-179): per call a 2^16-ray
+    chunk drawn by the ray feed with the epoch's seed, a random background
+    colour (the reference's random-bg augmentation), cosine LR, trainWithRaysHit."""
+
+    def __init__(self, nerf, feed, stream):
+        self.nerf, self.feed, self.stream = nerf, feed, stream
+        self.rng = np.random.default_rng(42)
         self.cursor = 0
         self.step = 0
+        self.epoch_seed = 0
 
     def run(self, nsteps):
         hits = []
+        f = self.feed
         while len(hits) < nsteps:
-            if self.cursor + RAYS_PER_CALL > self.o.shape[0]:
+            if self.cursor >= f.total:
                 self.cursor = 0
-            s = slice(self.cursor, self.cursor + RAYS_PER_CALL)
+            if self.cursor == 0:
+                self.epoch_seed = int(self.rng.integers(0, 1 << 32))
+            size = min(RAYS_PER_CALL, f.total - self.cursor)
             self.nerf.set_learning_rate(cosine_lr(self.step))
-            n, h = self.nerf.train(self.o[s], self.d[s], self.gt[s], RAYS_PER_CALL, stream=self.stream)
-            self.cursor += RAYS_PER_CALL
+            bg = self.rng.random(3)
+            self.nerf.set_bg_color(*map(float, bg))
+            f.fetch(self.cursor, size, self.epoch_seed, bg, self.stream)
+            n, h = self.nerf.train(f.o, f.d, f.rgb, size, rays_depth=f.dense, rays_sigma=f.sigma,
+                                   stream=self.stream)
+            self.cursor += size
             self.step += n
             hits.extend(h)
         return hits
@@ -134,7 +177,7 @@ def cpu_baseline(P, nerf, o, d, gt):
     bits = nerf.occupancy()
     mn, mx = np.float32([-1.5] * 3), np.float32([1.5] * 3)
     R = 1 << 14
-    oo, dd, gg = o[:R].cpu().numpy(), d[:R].cpu().numpy(), gt[:R].cpu().numpy()
+    oo, dd, gg = o[:R], d[:R], gt[:R]
     dW = np.zeros(64 * 32 + 16 * 64, np.float32)
     dB = np.zeros(80, np.float32)
     nerf.density.save_weights(dW, dB)
@@ -174,6 +217,29 @@ def cpu_baseline(P, nerf, o, d, gt):
             "sample": f"one full training step (march, encode, both MLPs fwd/bwd, compositing, gradients, scatter, "
                       f"Adam over all 16.8 M table entries) on {R} rays = {N} compacted samples of the same scene "
                       f"and model state, {dt:.2f} s"}
+
+
+def heldout_psnr(P, torch, nerf, feed, sp):
+    """INerfTrainer::validate (NerfTrainer.cu:373-408): sequential ray chunks of
+    the held-out views, GT composited over white, renderImageHit in INFERENCE
+    mode, PSNR of the mean squared error over all pixels and channels."""
+    nerf.set_bg_color(1.0, 1.0, 1.0)
+    nerf.set_memory_mode(True)
+    se, n, t_render = 0.0, 0, 0.0
+    rgb = torch.empty((feed.chunk, 3), device=feed.o.device)
+    for off in range(0, feed.total, feed.chunk):
+        size = min(feed.chunk, feed.total - off)
+        feed.fetch(off, size, 0, (1.0, 1.0, 1.0), sp, sequential=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        nerf.render(feed.o, feed.d, size, rgb, stream=sp)
+        torch.cuda.synchronize()
+        t_render += time.perf_counter() - t0
+        se += float(((rgb[:size] - feed.rgb[:size]) ** 2).sum().item())
+        n += 3 * size
+    nerf.set_memory_mode(False)
+    return {"value": round(-10.0 * math.log10(max(se / n, 1e-12)), 3), "views": int(feed.imgs.shape[0]),
+            "resolution": f"{feed.w}x{feed.h}", "render_rays_per_s": round(feed.total / t_render, 1)}
 
 
 def components(P, torch, stream, sp):
@@ -228,15 +294,14 @@ def main():
         print(json.dumps({"components": components(P, torch, stream, sp)}))
         return
 
-    o_np, d_np = scenes.rays_c4(POOL, n_cams=100, seed=2024)
     scene = scenes.SphereScene(seed=5)
-    d_o = torch.from_numpy(o_np).to(dev)
-    d_d = torch.from_numpy(d_np).to(dev)
-    d_gt = scene.render_device(d_o, d_d, steps=1024).contiguous()
+    focal = scenes.focal_from_fov(IMG_W, FOV_X)
+    imgs, tf = scenes.render_views(scene, scenes.cameras(N_VIEWS, 1.5, seed=2024), IMG_W, IMG_H, FOV_X, dev)
+    feed = RayFeed(P, torch, imgs, tf, IMG_W, IMG_H, focal, RAYS_PER_CALL)
     torch.cuda.synchronize()
 
     nerf = P.Nerf(options(P))
-    tr = Trainer(nerf, d_o, d_d, d_gt, sp)
+    tr = Trainer(nerf, feed, sp)
     tr.run(args.warmup)
     torch.cuda.synchronize()
     if args.profile_steps:
@@ -306,16 +371,30 @@ def main():
         "config": {"workload": "InstantNerf.trainWithRaysHit on the procedural 3-sphere scene (BASELINE configs[4])",
                    "batch_samples": BATCH, "rays_per_call": RAYS_PER_CALL, "mean_samples_per_step": round(samples / steps, 1),
                    "grid": "128^3 x 5 cascades x 4 mips", "table_size": TBL, "levels": L, "density": "32-64-16",
-                   "color": "32-64-64-3", "lambda_dist": 0.1, "loss_scale": 128.0, "occupancy_refresh": 16},
+                   "color": "32-64-64-3", "lambda_dist": 0.1, "loss_scale": 128.0, "occupancy_refresh": 16,
+                   "feed": "100 RGBA8 800x800 views in HBM, pcg_hash draws, random background per call"},
         "stage_ms": stage_ms,
         "stage_ms_per_step": stage_ms_per_step,
         "hash_encodes_per_s": round(n_prof / (st["densityFwd"][0] * 1e-3), 1) if "densityFwd" in st else None,
         "mfma_util": round(mfma_util, 5) if mfma_util else None,
         "roofline": roofline,
     }
+    # finish the cosine schedule (untimed), then PSNR on 12 held-out views
+    if args.psnr_steps > tr.step:
+        tr.run(args.psnr_steps - tr.step)
+        torch.cuda.synchronize()
+    if args.psnr_steps >= 0:
+        himgs, htf = scenes.render_views(scene, scenes.cameras(N_HELDOUT, 1.5, seed=4242), IMG_W, IMG_H, FOV_X, dev)
+        hfeed = RayFeed(P, torch, himgs, htf, IMG_W, IMG_H, focal, RAYS_PER_CALL)
+        out["psnr_heldout"] = dict(heldout_psnr(P, torch, nerf, hfeed, sp), after_steps=tr.step)
+        del hfeed, himgs
     out["components"] = components(P, torch, stream, sp)
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(P, nerf, d_o, d_d, d_gt)
+        feed.fetch(0, RAYS_PER_CALL, 12345, (1.0, 1.0, 1.0), sp)
+        torch.cuda.synchronize()
+        nerf.set_bg_color(1.0, 1.0, 1.0)
+        out["cpu_baseline"] = cpu_baseline(P, nerf, feed.o.cpu().numpy(), feed.d.cpu().numpy(),
+                                           feed.rgb.cpu().numpy())
     print(json.dumps(out))
 
 

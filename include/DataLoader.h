@@ -1,0 +1,75 @@
+// DataLoader: the training ray feed of 3DMaker on MI355X (gfx950).
+// Drop-in for the ray-fetch part of modules/NeRF/DataLoader.h:8-103 of the
+// reference: same fetchRayChunk() signature and chunk getters, with
+// cudaStream_t replaced by hipStream_t.  Images live in device memory
+// (RGBA8, [image][row][column][4]) instead of mapped pinned host memory.
+//
+// Not part of this build: the path constructors (transforms.json parsing,
+// image decoding, scene recentring / bounds derivation, DataLoader.cu:1-530);
+// the dataset is handed over in memory instead.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+#include <hip/hip_vector_types.h>
+
+#include <cstdint>
+
+class DataLoader {
+public:
+    // host_rgba: numImages x height x width x 4 bytes; host_transforms:
+    // numImages x 16 floats, row-major camera-to-world (NeRF convention,
+    // camera looking down -z); focal in pixels.  dense_fraction as in the
+    // reference constructor (fraction of depth-prior rays per chunk).
+    DataLoader(const uint8_t* host_rgba, const float* host_transforms, int numImages, int width, int height,
+               float focal, uint32_t ray_chunk_size, bool is_training = true, float dense_fraction = 0.0f);
+    ~DataLoader();
+
+    DataLoader(const DataLoader&) = delete;
+    DataLoader& operator=(const DataLoader&) = delete;
+
+    const float3* getChunkRaysO() const { return d_chunk_rays_o; }
+    const float3* getChunkRaysD() const { return d_chunk_rays_d; }
+    const float* getChunkRgbTrue() const { return d_chunk_rgb_true; }
+    const float* getChunkRaysDense() const { return d_chunk_rays_dense; }
+    const float* getChunkRaysSigma() const { return d_chunk_rays_sigma; }
+
+    void setDenseRaysFraction(float f) { m_dense_fraction = f; }
+    float getDenseRaysFraction() const { return m_dense_fraction; }
+    uint32_t getNumDepthRecords() const { return m_num_records; }
+    // Depth priors (host arrays of n records): frame index, pixel (u, v) in a
+    // depth_width x depth_height image, along-ray depth D and its sigma.
+    void setDepthPriors(const int* frame, const float* u, const float* v, const float* D, const float* sigma,
+                        uint32_t n, int depth_width, int depth_height);
+
+    // DataLoader.cu:663-679: size rays from offset (sequential) or drawn with
+    // pcg_hash from seed (training), skipping every holdout_every-th image.
+    void fetchRayChunk(int offset, int size, uint32_t seed, float3 bg_color = make_float3(1.0f, 1.0f, 1.0f),
+                       hipStream_t stream = 0, bool forceSequential = false, int holdout_every = 0);
+    void freeVRAM();
+
+    uint32_t getTotalRays() const { return total_rays; }
+    int getWidth() const { return width; }
+    int getHeight() const { return height; }
+    float getFocal() const { return focal; }
+    int getNumImages() const { return num_images; }
+
+private:
+    int width = 0, height = 0, num_images = 0;
+    float focal = 0.0f;
+    uint32_t total_rays = 0, m_chunk = 0, m_num_records = 0;
+    bool m_is_training = true;
+    float m_dense_fraction = 0.0f;
+    int m_depth_width = 0, m_depth_height = 0;
+    uint8_t* d_images_rgba = nullptr;
+    float* d_transforms = nullptr;
+    float3* d_chunk_rays_o = nullptr;
+    float3* d_chunk_rays_d = nullptr;
+    float* d_chunk_rgb_true = nullptr;
+    float* d_chunk_rays_dense = nullptr;
+    float* d_chunk_rays_sigma = nullptr;
+    int* d_rec_frame = nullptr;
+    float* d_rec_u = nullptr;
+    float* d_rec_v = nullptr;
+    float* d_rec_D = nullptr;
+    float* d_rec_sigma = nullptr;
+};

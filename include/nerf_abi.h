@@ -55,6 +55,20 @@ void launchVolumeRendering(const uint32_t num_rays, const uint32_t* d_ray_offset
                            float* d_weight_sum, float lambda_dist, float lambda_depth, float3 bg_color,
                            uint32_t base, uint32_t raysDone, hipStream_t stream);
 
+/* fetchRayChunkStreamingKernel (DataLoader.cu:548-661) as launched by
+ * DataLoader::fetchRayChunk (:663-679): size rays from offset (randomize = 0)
+ * or drawn with pcg_hash from seed, skipping every holdout_every-th image,
+ * with depth-prior rays for dense_fraction of them when num_records > 0 (rec_*
+ * nullable otherwise); RGBA8 pixels composited over bg_color.  d_transforms:
+ * [images][16] row-major camera-to-world; d_images_rgba: [images][h][w][4];
+ * total_rays = images * w * h.  d_chunk_dense / d_chunk_sigma nullable. */
+void launchFetchRayChunk(int offset, int size, int total_rays, uint32_t seed, int randomize, int width, int height,
+                         float focal_length, const float* d_transforms, const uint8_t* d_images_rgba,
+                         float3* d_chunk_rays_o, float3* d_chunk_rays_d, float* d_chunk_rgb, float* d_chunk_dense,
+                         float* d_chunk_sigma, const int* rec_frame, const float* rec_u, const float* rec_v,
+                         const float* rec_D, const float* rec_sigma, uint32_t num_records, float dense_fraction,
+                         float uv_scale_x, float uv_scale_y, float3 bg_color, int holdout_every, hipStream_t stream);
+
 /* ---- kernels the reference launches inline (no extern "C" counterpart) ---- */
 
 /* compute_ray_aabb_inv_kernel (otherKernels.cu:91-154), launched at InstantNerf.cu:391-398. */

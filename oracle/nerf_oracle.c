@@ -565,3 +565,96 @@ void orc_build_mipmaps(uint8_t* bits, const uint32_t* res, int L, int C)
         }
     }
 }
+
+/* ---- training ray feed (DataLoader.cu:542-661) ---- */
+
+uint32_t orc_pcg_hash(uint32_t input)
+{
+    const uint32_t state = input * 747796405u + 2891336453u;
+    const uint32_t word = ((state >> ((state >> 28u) + 4u)) ^ state) * 277803737u;
+    return (word >> 22u) ^ word;
+}
+
+void orc_fetch_ray_chunk(int offset, int size, int total_rays, uint32_t seed, int randomize, int width, int height,
+                         float focal, const float* transforms, const uint8_t* images_rgba, float* rays_o,
+                         float* rays_d, float* rgb, float* dense, float* sigma, const int* rec_frame,
+                         const float* rec_u, const float* rec_v, const float* rec_D, const float* rec_sigma,
+                         uint32_t num_records, float dense_fraction, float uv_scale_x, float uv_scale_y,
+                         const float* bg, int holdout_every)
+{
+    const int pixels = width * height;
+    for (int idx = 0; idx < size; idx++) {
+        uint32_t global_idx;
+        if (randomize) {
+            const uint32_t rand_val = orc_pcg_hash((uint32_t)(offset + idx) + seed);
+            if (holdout_every >= 2) {
+                const int num_imgs = total_rays / pixels;
+                const int num_test = (num_imgs + holdout_every - 1) / holdout_every;
+                const int num_train = num_imgs - num_test;
+                if (num_train < 1) {
+                    global_idx = rand_val % (uint32_t)total_rays;
+                } else {
+                    const int train_slot = (int)(rand_val % (uint32_t)num_train);
+                    const int block = train_slot / (holdout_every - 1);
+                    const int within = train_slot % (holdout_every - 1);
+                    const int img_idx = block * holdout_every + within + 1;
+                    const uint32_t r2 = orc_pcg_hash(rand_val);
+                    const int pixel_idx = (int)(r2 % (uint32_t)pixels);
+                    global_idx = (uint32_t)img_idx * (uint32_t)pixels + (uint32_t)pixel_idx;
+                }
+            } else {
+                global_idx = rand_val % (uint32_t)total_rays;
+            }
+        } else {
+            global_idx = (uint32_t)((offset + idx) % total_rays);
+        }
+        int img_idx = (int)(global_idx / (uint32_t)pixels);
+        const int pixel_idx = (int)(global_idx % (uint32_t)pixels);
+        float px = (float)(pixel_idx % width);
+        float py = (float)(pixel_idx / width);
+        float out_D = -1.0f, out_sigma = -1.0f;
+        if (randomize && dense_fraction > 0.0f && num_records > 0) {
+            const uint32_t hsel = orc_pcg_hash(((uint32_t)idx + 0x9E3779B9u) ^ (seed * 2654435761u));
+            if ((float)hsel * (1.0f / 4294967296.0f) < dense_fraction) {
+                const uint32_t r = orc_pcg_hash(hsel) % num_records;
+                const int f = rec_frame[r];
+                if (!(holdout_every >= 2 && (f % holdout_every == 0))) {
+                    img_idx = f;
+                    px = rec_u[r] * uv_scale_x;
+                    py = rec_v[r] * uv_scale_y;
+                    out_D = rec_D[r];
+                    out_sigma = rec_sigma[r];
+                    int px_i = (int)(px + 0.5f), py_i = (int)(py + 0.5f);
+                    px_i = px_i < 0 ? 0 : (px_i > width - 1 ? width - 1 : px_i);
+                    py_i = py_i < 0 ? 0 : (py_i > height - 1 ? height - 1 : py_i);
+                    global_idx = (uint32_t)img_idx * (uint32_t)pixels + (uint32_t)(py_i * width + px_i);
+                }
+            }
+        }
+        float dx = (px - (float)width * 0.5f) / focal;
+        float dy = -(py - (float)height * 0.5f) / focal;
+        float dz = -1.0f;
+        const float inv = 1.0f / sqrtf(dx * dx + dy * dy + dz * dz);
+        dx *= inv;
+        dy *= inv;
+        dz *= inv;
+        const float* c2w = transforms + (size_t)img_idx * 16;
+        rays_d[3 * idx] = c2w[0] * dx + c2w[1] * dy + c2w[2] * dz;
+        rays_d[3 * idx + 1] = c2w[4] * dx + c2w[5] * dy + c2w[6] * dz;
+        rays_d[3 * idx + 2] = c2w[8] * dx + c2w[9] * dy + c2w[10] * dz;
+        rays_o[3 * idx] = c2w[3];
+        rays_o[3 * idx + 1] = c2w[7];
+        rays_o[3 * idx + 2] = c2w[11];
+        const uint8_t* p = images_rgba + (size_t)global_idx * 4;
+        float fr = p[0] / 255.0f, fg = p[1] / 255.0f, fb = p[2] / 255.0f;
+        const float fa = p[3] / 255.0f;
+        fr = fr * fa + bg[0] * (1.0f - fa);
+        fg = fg * fa + bg[1] * (1.0f - fa);
+        fb = fb * fa + bg[2] * (1.0f - fa);
+        rgb[3 * idx] = fr;
+        rgb[3 * idx + 1] = fg;
+        rgb[3 * idx + 2] = fb;
+        if (dense) dense[idx] = out_D;
+        if (sigma) sigma[idx] = out_sigma;
+    }
+}

@@ -114,6 +114,21 @@ void orc_update_occupancy_bits(uint8_t* bits, const float* master, float sum, in
 /* buildMipmaps + bitfield_max_pool (InstantNerf.cu:1177-1204, otherKernels.cu:752-807). */
 void orc_build_mipmaps(uint8_t* bits, const uint32_t* res3, int mip_levels, int num_cascades);
 
+/* pcg_hash (DataLoader.cu:542-546). */
+uint32_t orc_pcg_hash(uint32_t input);
+
+/* fetchRayChunkStreamingKernel (DataLoader.cu:548-661) for rays [0, size) of
+ * a chunk: transforms [images][16] row-major, images_rgba [images][h][w][4];
+ * outputs rays_o/rays_d [size][3], rgb [size][3], dense/sigma [size].  The
+ * direction is normalised with a correctly rounded 1/sqrt (the reference uses
+ * fast-math rsqrtf).  rec_* may be NULL when num_records == 0. */
+void orc_fetch_ray_chunk(int offset, int size, int total_rays, uint32_t seed, int randomize, int width, int height,
+                         float focal, const float* transforms, const uint8_t* images_rgba, float* rays_o,
+                         float* rays_d, float* rgb, float* dense, float* sigma, const int* rec_frame,
+                         const float* rec_u, const float* rec_v, const float* rec_D, const float* rec_sigma,
+                         uint32_t num_records, float dense_fraction, float uv_scale_x, float uv_scale_y,
+                         const float* bg3, int holdout_every);
+
 #ifdef __cplusplus
 }
 #endif

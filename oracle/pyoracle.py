@@ -79,6 +79,10 @@ def lib():
             "orc_update_master_grid": (None, [_f32p, _f32p, f, C.c_uint32]),
             "orc_update_occupancy_bits": (None, [_u8p, _f32p, f, i, i, i, f, f]),
             "orc_build_mipmaps": (None, [_u8p, _u32p, i, i]),
+            "orc_pcg_hash": (C.c_uint32, [C.c_uint32]),
+            "orc_fetch_ray_chunk": (None, [i, i, i, C.c_uint32, i, i, i, f, _f32p, _u8p, _f32p, _f32p, _f32p,
+                                           C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                           C.c_void_p, C.c_uint32, f, f, f, _f32p, i]),
             "orc_num_threads": (i, []),
             "orc_set_num_threads": (None, [i]),
         }
@@ -377,3 +381,31 @@ def update_occupancy_bits(bits, master, total_sum, G, S, min_optical, base_voxel
 def build_mipmaps(bits, res, L, cascades):
     lib().orc_build_mipmaps(bits, np.ascontiguousarray(res, np.uint32), int(L), int(cascades))
     return bits
+
+
+def pcg_hash(x):
+    return lib().orc_pcg_hash(int(x) & 0xffffffff)
+
+
+def fetch_ray_chunk(offset, size, seed, randomize, transforms, images_rgba, focal, bg, holdout_every=0,
+                    records=None, dense_fraction=0.0, uv_scale=(1.0, 1.0)):
+    """images_rgba uint8 [n, h, w, 4]; transforms float32 [n, 16]; records = dict(frame, u, v, D, sigma)."""
+    imgs = np.ascontiguousarray(images_rgba, np.uint8)
+    n, h, w = imgs.shape[:3]
+    o = np.zeros((size, 3), np.float32)
+    d = np.zeros((size, 3), np.float32)
+    rgb = np.zeros((size, 3), np.float32)
+    dense = np.zeros(size, np.float32)
+    sig = np.zeros(size, np.float32)
+    if records is None:
+        rec = [None] * 5
+        nrec = 0
+    else:
+        rec = [np.ascontiguousarray(records["frame"], np.int32)] + \
+              [np.ascontiguousarray(records[k], np.float32) for k in ("u", "v", "D", "sigma")]
+        nrec = len(rec[0])
+    lib().orc_fetch_ray_chunk(int(offset), int(size), n * h * w, int(seed) & 0xffffffff, int(bool(randomize)), w, h,
+                              float(focal), _f3(transforms), imgs.reshape(-1), o, d, rgb, dense.ctypes.data,
+                              sig.ctypes.data, *[_vp(r) for r in rec], nrec, float(dense_fraction),
+                              float(uv_scale[0]), float(uv_scale[1]), _f3(bg), int(holdout_every))
+    return dict(o=o, d=d, rgb=rgb, dense=dense, sigma=sig)
