@@ -186,6 +186,9 @@ SIGNATURES = {
     "inerf_set_occupancy": (_i, [_vp, _vp]),
     "inerf_get_master_grid": (_i, [_vp, _vp]),
     "inerf_step_buffers": (_i, [_vp, C.POINTER(StepBuffers)]),
+    "inerf_save": (_i, [_vp, C.c_char_p]),
+    "inerf_load": (_i, [_vp, C.c_char_p]),
+    "inerf_get_options": (_i, [_vp, C.POINTER(NerfOptions)]),
     "inerf_density": (_vp, [_vp]),
     "inerf_color": (_vp, [_vp]),
     "inerf_philox4x32_10": (None, [C.POINTER(_u32), _u32, _u32]),
@@ -405,10 +408,13 @@ class Nerf:
 
     def __init__(self, opts: NerfOptions):
         self._L = lib()
-        self.opts = opts
         self.h = self._L.inerf_create(C.byref(opts))
         if not self.h:
             check(1)
+        self._views(opts)
+
+    def _views(self, opts: NerfOptions):
+        self.opts = opts
         G = opts.gridResolution[0] * opts.gridResolution[1] * opts.gridResolution[2]
         self.cells = opts.numCascades * G
         dopt = MLPGridOptions(vectorDim=4, hiddenDim=opts.densityHiddenDim, outputDim=16,
@@ -465,6 +471,17 @@ class Nerf:
 
     def reset_stats(self):
         self._c(self._L.inerf_reset_stats(self.h))
+
+    def save(self, path: str):
+        """.inerf file of the reference (InstantNerf.cu:1206-1276)."""
+        self._c(self._L.inerf_save(self.h, os.fsencode(path)))
+
+    def load(self, path: str):
+        """Re-initialise from an .inerf file; the options become the file's."""
+        self._c(self._L.inerf_load(self.h, os.fsencode(path)))
+        o = NerfOptions()
+        self._c(self._L.inerf_get_options(self.h, C.byref(o)))
+        self._views(o)
 
     def set_memory_mode(self, inference: bool):
         """INFERENCE selects renderBatchSize as the render hit batch; training needs TRAINING."""

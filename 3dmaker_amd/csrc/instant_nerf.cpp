@@ -16,6 +16,7 @@
 
 #include <algorithm>
 #include <cstdio>
+#include <cstring>
 #include <map>
 #include <stdexcept>
 #include <vector>
@@ -818,5 +819,125 @@ void InstantNerf::buildOccupancyBitgrid(uint8_t* d_out, float minDensityThreshol
     graft::build_mipmaps(d_out, m_opts.gridResolution, m_opts.levelsMipmap, m_opts.numCascades, stream);
 }
 
-void InstantNerf::save(const std::string&) { throw std::logic_error("InstantNerf::save is not part of this build"); }
-void InstantNerf::load(const std::string&) { throw std::logic_error("InstantNerf::load is not part of this build"); }
+// ---- .inerf files (InstantNerf.cu:1206-1352) ----
+//
+// "INERF1", the raw NerfOptions (152 bytes, the CUDA layout), the fp32 master
+// hash table [L][T][F], density weights then biases (every layer, hardware
+// shapes, output 16), colour weights then biases sized as if the colour head
+// had 16 outputs (the hardware head has 8: the rest is zero), the fp32 master
+// occupancy grid [C][res^3] and the occupancy bitfield.
+static_assert(sizeof(NerfOptions) == 152, "NerfOptions must keep the reference's 152-byte layout (.inerf header)");
+
+namespace {
+
+struct InerfLayout {
+    size_t hash, dW, dB, cW, cB, master, bits;
+};
+
+InerfLayout inerf_layout(const NerfOptions& o)
+{
+    InerfLayout s{};
+    s.hash = (size_t)o.numLevels * (size_t)o.hashTableSize * (size_t)o.featuresPerLevel;
+    const int d_in = o.numLevels * o.featuresPerLevel;
+    for (int l = 0; l < o.densityNumLayers; l++) {
+        const int in = l == 0 ? d_in : o.densityHiddenDim, out = l == o.densityNumLayers - 1 ? 16 : o.densityHiddenDim;
+        s.dW += (size_t)in * out;
+        s.dB += (size_t)out;
+    }
+    for (int l = 0; l < o.colorNumLayers; l++) {
+        const int in = l == 0 ? 32 : o.colorHiddenDim, out = l == o.colorNumLayers - 1 ? 16 : o.colorHiddenDim;
+        s.cW += (size_t)in * out;
+        s.cB += (size_t)out;
+    }
+    const size_t G = (size_t)o.gridResolution.x * o.gridResolution.y * o.gridResolution.z;
+    s.master = (size_t)o.numCascades * G;
+    s.bits = ((size_t)graft::mip_offset(o.gridResolution, o.levelsMipmap) * o.numCascades + 7) / 8;
+    return s;
+}
+
+template <class T>
+void write_block(std::FILE* f, const std::vector<T>& v)
+{
+    if (!v.empty() && std::fwrite(v.data(), sizeof(T), v.size(), f) != v.size())
+        throw std::runtime_error("InstantNerf::save: write failed");
+}
+
+template <class T>
+void read_block(std::FILE* f, std::vector<T>& v)
+{
+    if (!v.empty() && std::fread(v.data(), sizeof(T), v.size(), f) != v.size())
+        throw std::runtime_error("InstantNerf::load: truncated .inerf file");
+}
+
+struct FileCloser {
+    std::FILE* f;
+    ~FileCloser()
+    {
+        if (f) std::fclose(f);
+    }
+};
+
+}  // namespace
+
+void InstantNerf::save(const std::string& filename)
+{
+    if (!m_init) throw std::runtime_error("InstantNerf not initialized, cannot save.");
+    GRAFT_HIP_CHECK(hipDeviceSynchronize());
+    const InerfLayout L = inerf_layout(m_opts);
+    std::vector<float> hash(L.hash), dW(L.dW, 0.f), dB(L.dB, 0.f), cW(L.cW, 0.f), cB(L.cB, 0.f), master(L.master);
+    std::vector<uint8_t> bits(L.bits);
+    m_densityMLP->saveHashgrid(hash.data());
+    m_densityMLP->saveWeights(dW.data(), dB.data());
+    m_colorMLP->saveWeights(cW.data(), cB.data());
+    GRAFT_HIP_CHECK(hipMemcpy(master.data(), d_masterOccupancyGrid, L.master * sizeof(float), hipMemcpyDeviceToHost));
+    GRAFT_HIP_CHECK(hipMemcpy(bits.data(), d_occupancyGrid, L.bits, hipMemcpyDeviceToHost));
+    FileCloser fc{std::fopen(filename.c_str(), "wb")};
+    if (!fc.f) throw std::runtime_error("Cannot open file for saving: " + filename);
+    static const char magic[6] = {'I', 'N', 'E', 'R', 'F', '1'};
+    NerfOptions header;
+    std::memset(static_cast<void*>(&header), 0, sizeof(header));  // deterministic padding bytes
+    header = m_opts;
+    if (std::fwrite(magic, 1, 6, fc.f) != 6 || std::fwrite(&header, sizeof(header), 1, fc.f) != 1)
+        throw std::runtime_error("InstantNerf::save: write failed");
+    write_block(fc.f, hash);
+    write_block(fc.f, dW);
+    write_block(fc.f, dB);
+    write_block(fc.f, cW);
+    write_block(fc.f, cB);
+    write_block(fc.f, master);
+    write_block(fc.f, bits);
+}
+
+void InstantNerf::load(const std::string& filename)
+{
+    FileCloser fc{std::fopen(filename.c_str(), "rb")};
+    if (!fc.f) throw std::runtime_error("Cannot open file for loading: " + filename);
+    char magic[6];
+    if (std::fread(magic, 1, 6, fc.f) != 6 || std::string(magic, 6) != "INERF1")
+        throw std::runtime_error("Invalid INERF file format");
+    NerfOptions o;
+    if (std::fread(&o, sizeof(o), 1, fc.f) != 1) throw std::runtime_error("InstantNerf::load: truncated .inerf file");
+    if (o.numLevels <= 0 || o.numLevels > 32 || o.hashTableSize <= 0 || o.featuresPerLevel != 2 ||
+        o.numCascades <= 0 || o.numCascades > 16 || o.levelsMipmap <= 0 || o.densityNumLayers <= 0 ||
+        o.colorNumLayers <= 0 || o.gridResolution.x == 0 || o.gridResolution.x > 1024 ||
+        o.gridResolution.y == 0 || o.gridResolution.y > 1024 || o.gridResolution.z == 0 || o.gridResolution.z > 1024)
+        throw std::runtime_error("InstantNerf::load: implausible options in .inerf header");
+    const InerfLayout L = inerf_layout(o);
+    std::vector<float> hash(L.hash), dW(L.dW), dB(L.dB), cW(L.cW), cB(L.cB), master(L.master);
+    std::vector<uint8_t> bits(L.bits);
+    read_block(fc.f, hash);
+    read_block(fc.f, dW);
+    read_block(fc.f, dB);
+    read_block(fc.f, cW);
+    read_block(fc.f, cB);
+    read_block(fc.f, master);
+    read_block(fc.f, bits);
+    o.isProfiling = false;
+    init(o, m_memMode);
+    m_densityMLP->loadHashgrid(hash.data());
+    m_densityMLP->loadWeights(dW.data(), dB.data());
+    m_colorMLP->loadWeights(cW.data(), cB.data());
+    GRAFT_HIP_CHECK(hipMemcpy(d_masterOccupancyGrid, master.data(), L.master * sizeof(float), hipMemcpyHostToDevice));
+    GRAFT_HIP_CHECK(hipMemcpy(d_occupancyGrid, bits.data(), L.bits, hipMemcpyHostToDevice));
+    m_gridVersion++;
+}

@@ -466,6 +466,30 @@ int inerf_step_buffers(Inerf* h, InerfStepBuffers* out)
         out->windowStart = b.windowStart;
     });
 }
+int inerf_save(Inerf* h, const char* path)
+{
+    return NERF_CALL("inerf_save", {
+        if (!path) throw std::runtime_error("null path");
+        h->nerf.save(path);
+    });
+}
+int inerf_load(Inerf* h, const char* path)
+{
+    return NERF_CALL("inerf_load", {
+        if (!path) throw std::runtime_error("null path");
+        h->nerf.load(path);
+        h->density.g = h->nerf.densityMLP();  // load() rebuilt both heads
+        h->color.n = h->nerf.colorMLP();
+    });
+}
+int inerf_get_options(Inerf* h, InerfOptions* out)
+{
+    return NERF_CALL("inerf_get_options", {
+        if (!out) throw std::runtime_error("null output");
+        std::memcpy(out, &h->nerf.options(), sizeof(NerfOptions));
+    });
+}
+
 TmlpGrid* inerf_density(Inerf* h) { return h ? &h->density : nullptr; }
 TmlpNet* inerf_color(Inerf* h) { return h ? &h->color : nullptr; }
 

@@ -26,7 +26,9 @@
 // batch with the inference compositor (compositing.cu:5-78).  MemoryMode only
 // selects the render hit batch (renderBatchSize in INFERENCE, batchSize in
 // TRAINING); training state stays allocated, and trainWithRaysHit requires
-// TRAINING.  .inerf save/load throw std::logic_error (not part of this build).
+// TRAINING.  save/load write and read the reference's .inerf format
+// (InstantNerf.cu:1206-1352) byte for byte; load re-initialises the model with
+// the file's options.
 #pragma once
 
 #include <hip/hip_fp16.h>

@@ -94,7 +94,15 @@ int inerf_get_occupancy(Inerf* h, uint8_t* host_bits);
 int inerf_set_occupancy(Inerf* h, const uint8_t* host_bits);
 int inerf_get_master_grid(Inerf* h, float* host_cells);
 int inerf_step_buffers(Inerf* h, InerfStepBuffers* out);
-/* Non-owning views of the two heads (tmlp_*_destroy on them is a no-op). */
+/* InstantNerf::save / load (InstantNerf.h:333-334): the reference's .inerf
+ * format ("INERF1", raw NerfOptions, hash table, density and colour weights,
+ * master occupancy grid, bitfield).  load re-initialises the model with the
+ * file's options; inerf_get_options reads them back. */
+int inerf_save(Inerf* h, const char* path);
+int inerf_load(Inerf* h, const char* path);
+int inerf_get_options(Inerf* h, InerfOptions* out);
+/* Non-owning views of the two heads (tmlp_*_destroy on them is a no-op); they
+ * stay valid across inerf_load. */
 TmlpGrid* inerf_density(Inerf* h);
 TmlpNet* inerf_color(Inerf* h);
 

@@ -214,3 +214,66 @@ def test_query_occupancy_and_bitgrid_bit_exact(dev):
     orc.build_mipmaps(w, [res] * 3, 4, Cc)
     np.testing.assert_array_equal(d_bits.cpu().numpy(), w)
     nerf.close()
+
+
+def test_inerf_save_load_round_trip_and_layout(dev, tmp_path):
+    """.inerf (InstantNerf.cu:1206-1352): a trained model saved and loaded into a
+    differently configured instance renders the same bits; the file parses with
+    the reference's block layout (colour blocks sized for 16 outputs, zero tail)."""
+    P = pkg()
+    o1 = options(P, batch=2048, chunk=1024)
+    nerf = P.Nerf(o1)
+    R = 4000
+    o, d = scenes.rays_c4(R, n_cams=20, seed=44)
+    gt = np.random.default_rng(45).random((R, 3)).astype(np.float32)
+    d_o, d_d = T(o, dev), T(d, dev)
+    nerf.train(d_o, d_d, T(gt, dev), R)
+    torch.cuda.synchronize()
+    rgb1 = torch.zeros((R, 3), device=dev)
+    nerf.render(d_o, d_d, R, rgb1)
+    torch.cuda.synchronize()
+    path = str(tmp_path / "model.inerf")
+    nerf.save(path)
+    m = model(nerf)
+    master, bits = nerf.master_grid(), nerf.occupancy()
+
+    raw = open(path, "rb").read()
+    assert raw[:6] == b"INERF1" and P.lib().inerf_options_size() == 152
+    hdr = P.NerfOptions.from_buffer_copy(raw[6:6 + 152])
+    assert (hdr.batchSize, hdr.rayChunkSize, hdr.numCascades) == (2048, 1024, 2)
+    pos = 6 + 152
+
+    def block(n, dtype=np.float32):
+        nonlocal pos
+        a = np.frombuffer(raw, dtype, n, pos)
+        pos += a.nbytes
+        return a
+    np.testing.assert_array_equal(block(16 * (1 << 14) * 2), m[2])
+    np.testing.assert_array_equal(block(64 * 32 + 16 * 64), m[0])
+    np.testing.assert_array_equal(block(64 + 16), m[1])
+    cw = block(64 * 32 + 64 * 64 + 16 * 64)
+    np.testing.assert_array_equal(cw[:m[3].size], m[3])
+    assert (cw[m[3].size:] == 0).all()
+    cb = block(64 + 64 + 16)
+    np.testing.assert_array_equal(cb[:m[4].size], m[4])
+    assert (cb[m[4].size:] == 0).all()
+    np.testing.assert_array_equal(block(master.size), master)
+    np.testing.assert_array_equal(block(bits.size, np.uint8), bits)
+    assert pos == len(raw)
+
+    other = P.Nerf(options(P, batch=4096, chunk=512))
+    other.load(path)
+    assert other.opts.batchSize == 2048 and other.opts.rayChunkSize == 1024
+    rgb2 = torch.zeros((R, 3), device=dev)
+    other.render(d_o, d_d, R, rgb2)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(rgb2.cpu().numpy().view(np.uint32), rgb1.cpu().numpy().view(np.uint32))
+    m2 = model(other)
+    for a, b in zip(m, m2):
+        np.testing.assert_array_equal(a, b)
+    # a truncated file is refused
+    open(str(tmp_path / "bad.inerf"), "wb").write(raw[:len(raw) // 2])
+    with pytest.raises(RuntimeError):
+        other.load(str(tmp_path / "bad.inerf"))
+    nerf.close()
+    other.close()
