@@ -81,6 +81,9 @@ struct NerfBuffers {
     __half* color_in = nullptr;      // TinyMLP activation 0
     graft::GridMeta meta{};
     hipEvent_t ev_result = nullptr;
+    // occupancy refresh on its own stream, overlapped with the rest of its step
+    hipStream_t side = nullptr;
+    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
     std::vector<StageTimer> pending;
     std::map<std::string, std::pair<double, long>> stats;
 };
@@ -164,6 +167,9 @@ void InstantNerf::freeBuffers()
         dfree(b.render.rgb);
         dfree(b.render.dir);
         if (b.ev_result) (void)hipEventDestroy(b.ev_result);
+        if (b.ev_fork) (void)hipEventDestroy(b.ev_fork);
+        if (b.ev_join) (void)hipEventDestroy(b.ev_join);
+        if (b.side) (void)hipStreamDestroy(b.side);
         for (auto& t : b.pending) {
             (void)hipEventDestroy(t.a);
             (void)hipEventDestroy(t.b);
@@ -272,6 +278,9 @@ void InstantNerf::allocate()
     b.active_count = dalloc<int>(1);
     b.list_scratch = dalloc<uint32_t>(graft::occ_list_scratch_words(N));
     GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_result, hipEventDisableTiming));
+    GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_fork, hipEventDisableTiming));
+    GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_join, hipEventDisableTiming));
+    GRAFT_HIP_CHECK(hipStreamCreateWithFlags(&b.side, hipStreamNonBlocking));
 
     // The color head's activation-0 buffer receives the SH gather output directly.
     const TinyMLP::Buffers cb = m_colorMLP->buffers();
@@ -311,7 +320,7 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
     const graft::MlpShape cshape = shape_of(cb.hw);
     const int cstride = cb.hw.outputDim;
 
-    auto stage = [&](const char* name, auto&& fn) {
+    auto stage_on = [&](hipStream_t s, const char* name, auto&& fn) {
         if (!o.isProfiling) {
             fn();
             return;
@@ -319,11 +328,12 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         StageTimer t{name, nullptr, nullptr};
         GRAFT_HIP_CHECK(hipEventCreate(&t.a));
         GRAFT_HIP_CHECK(hipEventCreate(&t.b));
-        GRAFT_HIP_CHECK(hipEventRecord(t.a, stream));
+        GRAFT_HIP_CHECK(hipEventRecord(t.a, s));
         fn();
-        GRAFT_HIP_CHECK(hipEventRecord(t.b, stream));
+        GRAFT_HIP_CHECK(hipEventRecord(t.b, s));
         b.pending.push_back(t);
     };
+    auto stage = [&](const char* name, auto&& fn) { stage_on(stream, name, fn); };
 
     uint32_t raysDone = 0;
     int i = 0;
@@ -359,12 +369,19 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         GRAFT_HIP_CHECK(hipMemcpyAsync(b.h_result, b.result, 2 * sizeof(uint32_t), hipMemcpyDeviceToHost, stream));
         GRAFT_HIP_CHECK(hipEventRecord(b.ev_result, stream));
 
-        // InstantNerf.cu:488-494: the refresh changes only the grid the next step marches.
-        if (m_trainSteps % 16 == 0) {
-            stage("occupancy", [&] {
-                if (m_trainSteps < 256) earlyOccupancyGridUpdate(stream);
-                else lateOccupancyGridUpdate(stream);
+        // InstantNerf.cu:488-494: the refresh changes only the grid the next step
+        // marches and reads only the density head, so it runs on the side stream
+        // beside this step's forward/backward; the density head's Adam update
+        // waits for it, so it sees the same parameters as in the serial order.
+        const bool refresh = (m_trainSteps % 16 == 0);
+        if (refresh) {
+            GRAFT_HIP_CHECK(hipEventRecord(b.ev_fork, stream));
+            GRAFT_HIP_CHECK(hipStreamWaitEvent(b.side, b.ev_fork, 0));
+            stage_on(b.side, "occupancy", [&] {
+                if (m_trainSteps < 256) earlyOccupancyGridUpdate(b.side);
+                else lateOccupancyGridUpdate(b.side);
             });
+            GRAFT_HIP_CHECK(hipEventRecord(b.ev_join, b.side));
         }
 
         stage("densityFwd", [&] {
@@ -444,6 +461,7 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         stage("colorOpt", [&] {
             m_colorMLP->step(o.learningRate, o.beta1, o.beta2, o.epsilon, o.lossScale, stream);
         });
+        if (refresh) GRAFT_HIP_CHECK(hipStreamWaitEvent(stream, b.ev_join, 0));
         stage("densityOpt", [&] {
             m_densityMLP->step(o.learningRate, o.beta1, o.beta2, o.epsilon, o.lossScale, stream);
         });

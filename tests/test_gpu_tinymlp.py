@@ -395,3 +395,53 @@ def test_launchers_plain_mlp(dev):
     assert_close(dW, dW_ref, atol=2e-3 * np.abs(dW_ref).max(), what="launcher dW")
     assert_close(d_dx.cpu().numpy(), dx_ref, atol=2e-3 * max(1, np.abs(dx_ref.astype(np.float32)).max()),
                  what="launcher dx")
+
+
+def test_weight_files_round_trip_and_layout(dev, tmp_path):
+    """TinyMLP / TinyMLPHashGrid weight files (TinyMLP.cu:406-481,
+    TinyMLPHashGrid.cu:394-455): raw options header of the hardware shape, then
+    (grid: the fp32 table, then) per layer W then b, fp32."""
+    P = pkg()
+    opt = P.MLPOption(inputDim=32, hiddenDim=64, outputDim=3, numLayers=3, activationType=0, outputActivation=1)
+    net = P.Net(opt, 256, seed=5)
+    hw = net.buffers().hw
+    W, B = make_mlp(hw.inputDim, hw.hiddenDim, hw.outputDim, 3, seed=3, bias_scale=0.1)
+    net.load_weights(W, B)
+    path = str(tmp_path / "color.bin")
+    net.save_file(path)
+    raw = open(path, "rb").read()
+    hdr = P.MLPOption.from_buffer_copy(raw[:C.sizeof(P.MLPOption)])
+    assert (hdr.inputDim, hdr.hiddenDim, hdr.outputDim, hdr.numLayers) == (32, 64, 8, 3)
+    body = np.frombuffer(raw, np.float32, offset=C.sizeof(P.MLPOption))
+    wo = bo = po = 0
+    for o, i in [(64, 32), (64, 64), (8, 64)]:
+        np.testing.assert_array_equal(body[po:po + o * i], W[wo:wo + o * i])
+        np.testing.assert_array_equal(body[po + o * i:po + o * i + o], B[bo:bo + o])
+        po += o * i + o
+        wo += o * i
+        bo += o
+    assert po == body.size
+    net2 = P.Net(opt, 256, seed=99)
+    net2.load_file(path)
+    W2, B2 = np.zeros_like(W), np.zeros_like(B)
+    net2.save_weights(W2, B2)
+    np.testing.assert_array_equal(W2, W)
+    np.testing.assert_array_equal(B2, B)
+
+    gopt = grid_opt(1 << 12, 4, 1.5)
+    g = P.HashGrid(gopt, 256, seed=1)
+    gpath = str(tmp_path / "grid.bin")
+    g.save_file(gpath)
+    g2 = P.HashGrid(gopt, 256, seed=2)
+    g2.load_file(gpath)
+    t1, t2 = np.zeros(4 * (1 << 12) * 2, np.float32), np.zeros(4 * (1 << 12) * 2, np.float32)
+    g.save_hashgrid(t1)
+    g2.save_hashgrid(t2)
+    np.testing.assert_array_equal(t1, t2)
+    graw = open(gpath, "rb").read()
+    off = C.sizeof(P.MLPGridOptions)
+    np.testing.assert_array_equal(np.frombuffer(graw, np.float32, t1.size, off), t1)
+    bad = P.HashGrid(grid_opt(1 << 12, 4, 1.5), 256, seed=1)
+    open(str(tmp_path / "short.bin"), "wb").write(graw[:len(graw) - 100])
+    with pytest.raises(RuntimeError):
+        bad.load_file(str(tmp_path / "short.bin"))
