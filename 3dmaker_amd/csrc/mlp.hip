@@ -214,7 +214,13 @@ struct BwdParams {
     int nchunks;
 };
 
-template <int MAXD>
+// LMAX > 0: at most LMAX layers and every wave keeps the dW tiles it owns
+// (tile q of a layer belongs to wave q % 4 in every chunk) and one db per
+// thread in registers; the LDS then holds only the weights and one chunk's
+// transposed activations, so several blocks share a CU.  LMAX == 0: any
+// depth, block partials accumulated in LDS.  Both add each chunk's sums in the
+// same order, so their partials are bitwise equal.
+template <int MAXD, int LMAX>
 __global__ __launch_bounds__(256) void mlp_bwd_kernel(const BwdParams p)
 {
     extern __shared__ __align__(16) unsigned char smem[];
@@ -237,14 +243,25 @@ __global__ __launch_bounds__(256) void mlp_bwd_kernel(const BwdParams p)
             sfrag[p.fragT_off[l] + e] = (o < out_l && i < in_l) ? w[o * in_l + i] : (_Float16)0.f;
         }
     }
-    for (int e = tid; e < p.P; e += blockDim.x) sacc[e] = 0.f;
+    if constexpr (LMAX == 0)
+        for (int e = tid; e < p.P; e += blockDim.x) sacc[e] = 0.f;
     __syncthreads();
 
     constexpr int NT = MAXD / 16;
     constexpr int TPW = kBwdTilesPerWave;
+    constexpr int QW = (NT * NT + 3) / 4;  // dW tiles a wave owns per layer
+    constexpr int LR = LMAX > 0 ? LMAX : 1;
     const int lane = tid & 63, wave = tid >> 6, r = lane & 15, g = lane >> 4;
     const int N = p.d_n ? min((int)*p.d_n, p.N) : p.N;
     const int nchunks = (N + kBwdChunk - 1) / kBwdChunk;
+    f4 dwacc[LR][QW];
+    float dbacc[LR];
+#pragma unroll
+    for (int a = 0; a < LR; a++) {
+        dbacc[a] = 0.f;
+#pragma unroll
+        for (int k = 0; k < QW; k++) dwacc[a][k] = f4zero();
+    }
 
     for (int chunk = blockIdx.x; chunk < nchunks; chunk += gridDim.x) {
         const int s0 = chunk * kBwdChunk;
@@ -264,7 +281,9 @@ __global__ __launch_bounds__(256) void mlp_bwd_kernel(const BwdParams p)
             }
         }
 
-        for (int l = p.layers - 1; l >= 0; l--) {
+        // One layer of the backward; dw/db: this wave's register accumulators
+        // of layer l (LMAX > 0) or nullptr (LDS partials).
+        auto layer = [&](int l, f4* dw, float* db) {
             const int in_l = l == 0 ? p.in : p.hid;
             const int out_l = l == p.layers - 1 ? p.out_dim : p.hid;
             const int KSo = tiles16(out_l), MTi = tiles16(in_l);
@@ -331,25 +350,34 @@ __global__ __launch_bounds__(256) void mlp_bwd_kernel(const BwdParams p)
             }
             __syncthreads();
 
-            // dW_l[o][i] += sum_s Gt[o][s] * Xt[i][s]; tiles (mo, mi) round-robin over the 4 waves.
+            // dW_l[o][i] += sum_s Gt[o][s] * Xt[i][s]; tile q = (mo, mi) belongs to wave q % 4.
             const int ntile = KSo * MTi;
-            for (int q = wave; q < ntile; q += 4) {
-                const int mo = q / MTi, mi = q - mo * MTi;
-                const _Float16* ga = Gt + (16 * mo + r) * kBwdPitch + 4 * g;
-                const _Float16* xb = Xt + (16 * mi + r) * kBwdPitch + 4 * g;
-                f4 acc = f4zero();
 #pragma unroll
-                for (int kk = 0; kk < kBwdChunk / 16; kk++)
-                    acc = mfma16(*reinterpret_cast<const h4*>(ga + 16 * kk),
-                                 *reinterpret_cast<const h4*>(xb + 16 * kk), acc);
-                const int i = 16 * mi + r;
+            for (int k = 0; k < QW; k++) {
+                const int q = wave + 4 * k;
+                if (q < ntile) {
+                    const int mo = q / MTi, mi = q - mo * MTi;
+                    const _Float16* ga = Gt + (16 * mo + r) * kBwdPitch + 4 * g;
+                    const _Float16* xb = Xt + (16 * mi + r) * kBwdPitch + 4 * g;
+                    f4 acc = f4zero();
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const int o = 16 * mo + 4 * g + j;
-                    if (o < out_l && i < in_l) sacc[p.wofs[l] + o * in_l + i] += acc[j];
+                    for (int kk = 0; kk < kBwdChunk / 16; kk++)
+                        acc = mfma16(*reinterpret_cast<const h4*>(ga + 16 * kk),
+                                     *reinterpret_cast<const h4*>(xb + 16 * kk), acc);
+                    if (dw) {
+#pragma unroll
+                        for (int j = 0; j < 4; j++) dw[k][j] += acc[j];
+                    } else {
+                        const int i = 16 * mi + r;
+#pragma unroll
+                        for (int j = 0; j < 4; j++) {
+                            const int o = 16 * mo + 4 * g + j;
+                            if (o < out_l && i < in_l) sacc[p.wofs[l] + o * in_l + i] += acc[j];
+                        }
+                    }
                 }
             }
-            // db_l[o] += sum_s Gt[o][s] (fp32 sum of fp16 values)
+            // db_l[o] += sum_s Gt[o][s] (fp32 sum of fp16 values), o = tid
             for (int o = tid; o < out_l; o += blockDim.x) {
                 const _Float16* row = Gt + o * kBwdPitch;
                 float s = 0.f;
@@ -357,13 +385,45 @@ __global__ __launch_bounds__(256) void mlp_bwd_kernel(const BwdParams p)
                     const h4 v = *reinterpret_cast<const h4*>(row + k);
                     s += ((float)v[0] + (float)v[1]) + ((float)v[2] + (float)v[3]);
                 }
-                sacc[p.bofs[l] + o] += s;
+                if (db) *db += s;
+                else sacc[p.bofs[l] + o] += s;
             }
             __syncthreads();
+        };
+
+        if constexpr (LMAX > 0) {
+#pragma unroll
+            for (int l = LMAX - 1; l >= 0; l--)
+                if (l < p.layers) layer(l, dwacc[l], &dbacc[l]);
+        } else {
+            for (int l = p.layers - 1; l >= 0; l--) layer(l, nullptr, nullptr);
         }
     }
+
     float* dst = p.ws + (size_t)blockIdx.x * p.P;
-    for (int e = tid; e < p.P; e += blockDim.x) dst[e] = sacc[e];
+    if constexpr (LMAX > 0) {
+#pragma unroll
+        for (int l = 0; l < LMAX; l++) {
+            if (l >= p.layers) continue;
+            const int in_l = l == 0 ? p.in : p.hid;
+            const int out_l = l == p.layers - 1 ? p.out_dim : p.hid;
+            const int MTi = tiles16(in_l), ntile = tiles16(out_l) * MTi;
+#pragma unroll
+            for (int k = 0; k < QW; k++) {
+                const int q = wave + 4 * k;
+                if (q >= ntile) continue;
+                const int mo = q / MTi, mi = q - mo * MTi, i = 16 * mi + r;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int o = 16 * mo + 4 * g + j;
+                    if (o < out_l && i < in_l) dst[p.wofs[l] + o * in_l + i] = dwacc[l][k][j];
+                }
+            }
+            if (tid < out_l) dst[p.bofs[l] + tid] = dbacc[l];
+        }
+    } else {
+        for (int e = tid; e < p.P; e += blockDim.x) dst[e] = sacc[e];
+    }
 }
 
 // grad[p] += sum over blocks of ws[b][p], summed in block order.
@@ -565,20 +625,31 @@ void mlp_backward(const MlpShape& s, const __half* dy, const __half* const* acts
     }
     p.P = btot;
     const int maxd = pick_maxd(s.maxd());
+    // register accumulators for nets of up to 4 layers of width <= 64 (the NeRF heads)
+    const bool reg = maxd <= 64 && s.layers <= 4;
     p.gt_base = (frag_halves * 2 + 15) & ~15;
     p.xt_base = p.gt_base + maxd * kBwdPitch * 2;
     p.acc_base = p.xt_base + maxd * kBwdPitch * 2;
-    const int lds = p.acc_base + p.P * 4;
+    const int lds = p.acc_base + (reg ? 0 : p.P * 4);
     if (lds > max_lds_per_block()) throw std::runtime_error("TinyMLP: network too large for the fused backward LDS budget");
     p.nchunks = (N + kBwdChunk - 1) / kBwdChunk;
-    const int blocks = std::max(1, std::min(p.nchunks, num_cus() * 2));
+    const int per_cu = reg ? std::max(1, std::min(4, max_lds_per_block() / std::max(lds, 1))) : 2;
+    const int blocks = std::max(1, std::min(p.nchunks, num_cus() * per_cu));
     p.ws = static_cast<float*>(workspace((size_t)blocks * p.P * sizeof(float)));
 
-    switch (maxd) {
-        case 16: hipLaunchKernelGGL(mlp_bwd_kernel<16>, dim3(blocks), dim3(256), lds, stream, p); break;
-        case 32: hipLaunchKernelGGL(mlp_bwd_kernel<32>, dim3(blocks), dim3(256), lds, stream, p); break;
-        case 64: hipLaunchKernelGGL(mlp_bwd_kernel<64>, dim3(blocks), dim3(256), lds, stream, p); break;
-        default: hipLaunchKernelGGL(mlp_bwd_kernel<128>, dim3(blocks), dim3(256), lds, stream, p); break;
+    if (reg) {
+        switch (maxd) {
+            case 16: hipLaunchKernelGGL((mlp_bwd_kernel<16, 4>), dim3(blocks), dim3(256), lds, stream, p); break;
+            case 32: hipLaunchKernelGGL((mlp_bwd_kernel<32, 4>), dim3(blocks), dim3(256), lds, stream, p); break;
+            default: hipLaunchKernelGGL((mlp_bwd_kernel<64, 4>), dim3(blocks), dim3(256), lds, stream, p); break;
+        }
+    } else {
+        switch (maxd) {
+            case 16: hipLaunchKernelGGL((mlp_bwd_kernel<16, 0>), dim3(blocks), dim3(256), lds, stream, p); break;
+            case 32: hipLaunchKernelGGL((mlp_bwd_kernel<32, 0>), dim3(blocks), dim3(256), lds, stream, p); break;
+            case 64: hipLaunchKernelGGL((mlp_bwd_kernel<64, 0>), dim3(blocks), dim3(256), lds, stream, p); break;
+            default: hipLaunchKernelGGL((mlp_bwd_kernel<128, 0>), dim3(blocks), dim3(256), lds, stream, p); break;
+        }
     }
     GRAFT_LAUNCH_CHECK();
 
