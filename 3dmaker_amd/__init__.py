@@ -19,7 +19,7 @@ LIB_PATH = os.path.join(_HERE, "lib3dmaker_amd.so")
 
 __all__ = [
     "LIB_PATH", "lib", "launch", "MLPOption", "MLPGridOptions", "HashGrid", "Net",
-    "OUT_ACT_NONE", "OUT_ACT_SIGMOID", "ptr", "check", "Float3", "Uint3", "NerfOptions", "Nerf",
+    "OUT_ACT_NONE", "OUT_ACT_SIGMOID", "ptr", "check", "Float3", "Uint3", "NerfOptions", "Nerf", "NerfTrainer", "NtrConfig", "NtrStats",
 ]
 
 OUT_ACT_NONE = 0
@@ -77,6 +77,20 @@ class NerfOptions(C.Structure):
                 ("beta1", C.c_float), ("beta2", C.c_float), ("epsilon", C.c_float), ("lossScale", C.c_float),
                 ("bgColor", C.c_float * 3), ("minDensityThreshold", C.c_float), ("decayValue", C.c_float),
                 ("densityBias", C.c_float), ("legacyRenderFlag", C.c_uint8), ("isProfiling", C.c_uint8)]
+
+
+class NtrConfig(C.Structure):
+    """modules/NeRF/NerfTrainer.h:27-41 (include/trainer_capi.h NtrConfig); start from NerfTrainer.default_config()."""
+    _fields_ = [("lambdaDepth", C.c_float), ("lambdaDist", C.c_float), ("numCascades", C.c_int),
+                ("minDensityThreshold", C.c_float), ("sampleK", C.c_int), ("batchSize", C.c_int),
+                ("renderBatchSize", C.c_int), ("depthFraction", C.c_float), ("shouldValidate", C.c_uint8),
+                ("maxLR", C.c_float), ("minLR", C.c_float), ("annealSteps", C.c_int)]
+
+
+class NtrStats(C.Structure):
+    """TrainStats (NerfTrainer.h:16-25)."""
+    _fields_ = [("step", C.c_int), ("targetSteps", C.c_int), ("loss", C.c_float), ("psnr", C.c_float),
+                ("lr", C.c_float), ("epochs", C.c_float), ("msPerStep", C.c_float), ("etaSeconds", C.c_float)]
 
 
 class StepBuffers(C.Structure):
@@ -192,6 +206,20 @@ SIGNATURES = {
     "inerf_density": (_vp, [_vp]),
     "inerf_color": (_vp, [_vp]),
     "inerf_philox4x32_10": (None, [C.POINTER(_u32), _u32, _u32]),
+    # include/trainer_capi.h
+    "ntr_default_config": (None, [C.POINTER(NtrConfig)]),
+    "ntr_create": (_vp, [C.POINTER(NtrConfig)]),
+    "ntr_destroy": (None, [_vp]),
+    "ntr_load_dataset": (_i, [_vp, _vp, _vp, _i, _i, _i, _f]),
+    "ntr_begin_training": (_i, [_vp, _i]),
+    "ntr_train_steps": (_i, [_vp, _i, C.POINTER(NtrStats)]),
+    "ntr_validate": (_i, [_vp, C.POINTER(_f)]),
+    "ntr_save": (_i, [_vp, C.c_char_p]),
+    "ntr_load": (_i, [_vp, C.c_char_p]),
+    "ntr_render_orbit": (_i, [_vp, _f, _f, _f, _f, _i, _i, _vp]),
+    "ntr_render_train_view": (_i, [_vp, _i, _i, _i, _vp]),
+    "ntr_num_train_views": (_i, [_vp]),
+    "ntr_step": (_i, [_vp]),
     "tmlp_version": (C.c_char_p, []),
 }
 
@@ -529,3 +557,80 @@ class Nerf:
         b = StepBuffers()
         self._c(self._L.inerf_step_buffers(self.h, C.byref(b)))
         return b
+
+
+class NerfTrainer:
+    """INerfTrainer (modules/NeRF/NerfTrainer.h:43-112) over include/trainer_capi.h."""
+
+    @staticmethod
+    def default_config() -> NtrConfig:
+        c = NtrConfig()
+        lib().ntr_default_config(C.byref(c))
+        return c
+
+    def __init__(self, config: NtrConfig):
+        self._L = lib()
+        self.h = self._L.ntr_create(C.byref(config))
+        if not self.h:
+            check(1)
+
+    def close(self):
+        if self.h:
+            self._L.ntr_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _c(self, rc):
+        if rc:
+            raise RuntimeError(self._L.tinymlp_last_error_message().decode())
+
+    def load_dataset(self, rgba, transforms, focal):
+        """rgba: uint8 [n, h, w, 4] (host); transforms: float32 [n, 16] row-major camera-to-world."""
+        import numpy as np
+        rgba = np.ascontiguousarray(rgba, np.uint8)
+        tf = np.ascontiguousarray(transforms, np.float32)
+        n, hh, ww = rgba.shape[:3]
+        self._c(self._L.ntr_load_dataset(self.h, rgba.ctypes.data, tf.ctypes.data, n, ww, hh, float(focal)))
+
+    def begin_training(self, total_steps):
+        self._c(self._L.ntr_begin_training(self.h, int(total_steps)))
+
+    def train_steps(self, n) -> NtrStats:
+        st = NtrStats()
+        self._c(self._L.ntr_train_steps(self.h, int(n), C.byref(st)))
+        return st
+
+    def validate(self) -> float:
+        p = C.c_float(0)
+        self._c(self._L.ntr_validate(self.h, C.byref(p)))
+        return p.value
+
+    def save(self, path):
+        self._c(self._L.ntr_save(self.h, os.fsencode(path)))
+
+    def load(self, path):
+        self._c(self._L.ntr_load(self.h, os.fsencode(path)))
+
+    def render_orbit(self, azimuth, elevation, radius, fov=50.0, width=800, height=800):
+        import numpy as np
+        out = np.zeros((height, width, 3), np.float32)
+        self._c(self._L.ntr_render_orbit(self.h, float(azimuth), float(elevation), float(radius), float(fov), width,
+                                         height, out.ctypes.data))
+        return out
+
+    def render_train_view(self, index, width, height):
+        import numpy as np
+        out = np.zeros((height, width, 3), np.float32)
+        self._c(self._L.ntr_render_train_view(self.h, int(index), width, height, out.ctypes.data))
+        return out
+
+    def num_train_views(self) -> int:
+        return self._L.ntr_num_train_views(self.h)
+
+    def step(self) -> int:
+        return self._L.ntr_step(self.h)

@@ -40,4 +40,13 @@ struct RayFeedArgs {
 
 void fetch_ray_chunk(const RayFeedArgs& a, hipStream_t s);
 
+struct PinholeCam {
+    float m[12];  // rows of the camera-to-world 3x4
+};
+// generate_custom_rays_kernel (NerfTrainer.cu:25-47): width x height pinhole
+// rays, pixel (px, py) -> ((px - w/2)/f, -(py - h/2)/f, -1) rotated by c2w12.
+void pinhole_rays(int width, int height, float focal, const float* c2w12, float3* o, float3* d, hipStream_t s);
+// out[i] = |pred_i - target_i|^2 / 3 over rgb triples.
+void ray_sq_err(const float* pred, const float* target, float* out, int n, hipStream_t s);
+
 }  // namespace graft

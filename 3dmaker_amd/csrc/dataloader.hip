@@ -85,7 +85,57 @@ __global__ __launch_bounds__(256) void fetch_ray_chunk_kernel(const RayFeedArgs 
     if (a.sigma) a.sigma[idx] = out_sigma;
 }
 
+// generate_custom_rays_kernel (NerfTrainer.cu:25-47): one pinhole ray per
+// pixel (px, py) of a width x height image, c2w row-major 3x4.
+__global__ __launch_bounds__(256) void pinhole_rays_kernel(int width, int height, float focal, PinholeCam cam,
+                                                           float3* __restrict__ o, float3* __restrict__ d)
+{
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= width * height) return;
+    const float px = (float)(idx % width), py = (float)(idx / width);
+    float dx = (px - (float)width * 0.5f) / focal;
+    float dy = -(py - (float)height * 0.5f) / focal;
+    float dz = -1.0f;
+    const float inv = 1.0f / sqrtf(dx * dx + dy * dy + dz * dz);
+    dx *= inv;
+    dy *= inv;
+    dz *= inv;
+    const float* m = cam.m;
+    o[idx] = make_float3(m[3], m[7], m[11]);
+    d[idx] = make_float3(m[0] * dx + m[1] * dy + m[2] * dz, m[4] * dx + m[5] * dy + m[6] * dz,
+                         m[8] * dx + m[9] * dy + m[10] * dz);
+}
+
+// Per-ray squared error (r^2 + g^2 + b^2) / 3 of mse_kernel (NerfTrainer.cu:15-23).
+__global__ __launch_bounds__(256) void ray_sq_err_kernel(const float* __restrict__ pred,
+                                                         const float* __restrict__ target, float* __restrict__ out,
+                                                         int n)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float r = pred[3 * i] - target[3 * i], g = pred[3 * i + 1] - target[3 * i + 1];
+    const float b = pred[3 * i + 2] - target[3 * i + 2];
+    out[i] = (r * r + g * g + b * b) / 3.0f;
+}
+
 }  // namespace
+
+void pinhole_rays(int width, int height, float focal, const float* c2w12, float3* o, float3* d, hipStream_t s)
+{
+    const int n = width * height;
+    if (n <= 0) return;
+    PinholeCam cam{};
+    for (int k = 0; k < 12; k++) cam.m[k] = c2w12[k];
+    hipLaunchKernelGGL(pinhole_rays_kernel, dim3((n + 255) / 256), dim3(256), 0, s, width, height, focal, cam, o, d);
+    GRAFT_LAUNCH_CHECK();
+}
+
+void ray_sq_err(const float* pred, const float* target, float* out, int n, hipStream_t s)
+{
+    if (n <= 0) return;
+    hipLaunchKernelGGL(ray_sq_err_kernel, dim3((n + 255) / 256), dim3(256), 0, s, pred, target, out, n);
+    GRAFT_LAUNCH_CHECK();
+}
 
 void fetch_ray_chunk(const RayFeedArgs& a, hipStream_t s)
 {

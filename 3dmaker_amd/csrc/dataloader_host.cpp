@@ -6,6 +6,7 @@
 #include "dataloader.h"
 #include "nerf_abi.h"
 
+#include <cmath>
 #include <stdexcept>
 
 namespace {
@@ -38,6 +39,7 @@ DataLoader::DataLoader(const uint8_t* host_rgba, const float* host_transforms, i
     const size_t pixels = (size_t)w * (size_t)h * (size_t)numImages;
     if (pixels > 0xffffffffull) throw std::runtime_error("DataLoader: more than 2^32 pixels");
     total_rays = (uint32_t)pixels;
+    h_transforms.assign(host_transforms, host_transforms + (size_t)numImages * 16);
     d_images_rgba = dcopy(host_rgba, pixels * 4);
     d_transforms = dcopy(host_transforms, (size_t)numImages * 16);
     d_chunk_rays_o = dcopy<float3>(nullptr, m_chunk);
@@ -48,6 +50,35 @@ DataLoader::DataLoader(const uint8_t* host_rgba, const float* host_transforms, i
 }
 
 DataLoader::~DataLoader() { freeVRAM(); }
+
+float DataLoader::getCameraAngleX() const { return 2.0f * std::atan(0.5f * (float)width / focal); }
+
+void DataLoader::getFramePose(int i, float out[16]) const
+{
+    for (int k = 0; k < 16; ++k) out[k] = (i >= 0 && i < num_images) ? h_transforms[(size_t)i * 16 + k] : 0.0f;
+}
+
+void DataLoader::getSceneOrientation(float3& center, float3& up) const
+{
+    if (num_images == 0) {
+        center = make_float3(0, 0, 0);
+        up = make_float3(0, 0, 1);
+        return;
+    }
+    float px = 0, py = 0, pz = 0, ux = 0, uy = 0, uz = 0;
+    for (int i = 0; i < num_images; i++) {
+        const float* m = &h_transforms[(size_t)i * 16];
+        px += m[3];
+        py += m[7];
+        pz += m[11];
+        ux += m[1];
+        uy += m[5];
+        uz += m[9];
+    }
+    center = make_float3(px / num_images, py / num_images, pz / num_images);
+    const float len = std::sqrt(ux * ux + uy * uy + uz * uz);
+    up = len > 0 ? make_float3(ux / len, uy / len, uz / len) : make_float3(0, 0, 1);
+}
 
 void DataLoader::freeVRAM()
 {

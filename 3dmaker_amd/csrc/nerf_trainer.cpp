@@ -1,0 +1,396 @@
+// INerfTrainer (include/NerfTrainer.h): the reference's training driver
+// (modules/NeRF/NerfTrainer.cu) over InstantNerf and the device-resident
+// DataLoader.  Host logic only; every device step is a library kernel.
+#include "NerfTrainer.h"
+
+#include "dataloader.h"
+#include "nerf.h"
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <stdexcept>
+
+namespace {
+
+constexpr float kPI = 3.14159265359f;
+constexpr char kSceneMagic[4] = {'S', 'C', 'N', '1'};
+constexpr std::streamoff kSceneFooterBytes = 4 + 8 * (std::streamoff)sizeof(float);
+
+template <class T>
+T* dalloc(size_t n)
+{
+    void* p = nullptr;
+    GRAFT_HIP_CHECK(hipMalloc(&p, std::max<size_t>(n, 1) * sizeof(T)));
+    return static_cast<T*>(p);
+}
+
+}  // namespace
+
+// NerfTrainer.cu:49-93: the trainer's fixed model (density 64 x 2, colour
+// 32 x 3, T = 2^19, 16 levels, b = 1.3819, 128^3 grid, AABB +-1.5).
+void INerfTrainer::init(const NerfConfig& config)
+{
+    m_config = config;
+    NerfOptions& o = m_masterConfig;
+    o = NerfOptions{};
+    o.gridResolution = make_uint3(128, 128, 128);
+    o.aabbMin = make_float3(-1.5f, -1.5f, -1.5f);
+    o.aabbMax = make_float3(1.5f, 1.5f, 1.5f);
+    o.levelsMipmap = 4;
+    o.numCascades = config.numCascades > 0 ? config.numCascades : 1;
+    o.samplesPerVoxel = config.sampleK;
+    o.densityHiddenDim = 64;
+    o.densityNumLayers = 2;
+    o.colorHiddenDim = 32;
+    o.colorNumLayers = 3;
+    o.hashTableSize = 1 << 19;
+    o.numLevels = 16;
+    o.growthFactor = 1.3819f;
+    o.baseResolution = 16;
+    o.featuresPerLevel = 2;
+    o.renderBatchSize = config.renderBatchSize;
+    o.batchSize = config.batchSize;
+    o.rayChunkSize = config.batchSize / 4;
+    o.lambdaDepth = config.lambdaDepth;
+    o.lambdaDist = config.lambdaDist;
+    o.learningRate = config.maxLR;
+    o.beta1 = 0.9f;
+    o.beta2 = 0.999f;
+    o.epsilon = 1e-8f;
+    o.lossScale = 128.0f;
+    o.bgColor = make_float3(1.0f, 1.0f, 1.0f);
+    o.minDensityThreshold = config.minDensityThreshold;
+    o.decayValue = 0.95f;
+    o.densityBias = 0.0f;
+    o.legacyRenderFlag = false;
+    o.isProfiling = false;
+    m_holdout_every = config.shouldValidate ? 8 : 0;
+
+    if (!m_d_loss) m_d_loss = dalloc<float>(1);
+    GRAFT_HIP_CHECK(hipFree(m_d_chunkRgb));
+    GRAFT_HIP_CHECK(hipFree(m_d_err));
+    GRAFT_HIP_CHECK(hipFree(m_d_partials));
+    m_d_chunkRgb = dalloc<float>((size_t)o.rayChunkSize * 3);
+    m_d_err = dalloc<float>((size_t)o.rayChunkSize);
+    m_d_partials = dalloc<float>(1024);
+}
+
+INerfTrainer::~INerfTrainer()
+{
+    delete m_nerf;
+    delete m_dataloader;
+    (void)hipFree(m_d_loss);
+    (void)hipFree(m_d_chunkRgb);
+    (void)hipFree(m_d_err);
+    (void)hipFree(m_d_partials);
+}
+
+void INerfTrainer::buildModel()
+{
+    if (m_nerf) return;
+    m_nerf = new InstantNerf();
+    m_nerf->init(m_masterConfig, TRAINING);
+}
+
+void INerfTrainer::loadDataset(const std::string& path)
+{
+    throw std::logic_error("INerfTrainer::loadDataset(" + path +
+                           "): dataset files are not read by this build; pass the images in memory");
+}
+
+void INerfTrainer::loadDataset(const uint8_t* host_rgba, const float* host_transforms, int numImages, int width,
+                               int height, float focal)
+{
+    if (m_masterConfig.rayChunkSize <= 0) throw std::runtime_error("INerfTrainer: init() first");
+    delete m_dataloader;
+    m_dataloader = nullptr;
+    m_dataloader = new DataLoader(host_rgba, host_transforms, numImages, width, height, focal,
+                                  (uint32_t)m_masterConfig.rayChunkSize, true, m_config.depthFraction);
+    m_total_rays = m_dataloader->getTotalRays();
+    buildModel();
+    float3 c, up;
+    m_dataloader->getSceneOrientation(c, up);
+    m_sceneCenter = {0.0f, 0.0f, 0.0f};
+    m_sceneUp = {up.x, up.y, up.z};
+    m_sceneScale = 1.0f;
+    m_cameraAngleX = m_dataloader->getCameraAngleX();
+    m_globalStep = 0;
+    m_rayCursor = 0;
+    m_lossHistory.clear();
+}
+
+// NerfTrainer.cu:131-135
+float INerfTrainer::currentLR() const
+{
+    const int anneal = (m_config.annealSteps > 0) ? m_config.annealSteps : std::max(1, m_targetSteps);
+    const float progress = fminf((float)m_globalStep / (float)anneal, 1.0f);
+    return m_config.minLR + 0.5f * (m_config.maxLR - m_config.minLR) * (1.0f + cosf(kPI * progress));
+}
+
+float INerfTrainer::chunkMse(const float* d_pred, const float* d_target, int n)
+{
+    graft::ray_sq_err(d_pred, d_target, m_d_err, n, 0);
+    graft::reduce_sum(m_d_err, (uint32_t)n, m_d_partials, m_d_loss, 0);
+    float h = 0.0f;
+    GRAFT_HIP_CHECK(hipMemcpy(&h, m_d_loss, sizeof(float), hipMemcpyDeviceToHost));
+    return h;
+}
+
+// NerfTrainer.cu:137-179: one ray chunk from the epoch's seed with a random
+// background, all of its hit batches, optionally the chunk's colour MSE.
+float INerfTrainer::trainOneChunk(bool computeLoss)
+{
+    const uint32_t rayChunk = (uint32_t)m_masterConfig.rayChunkSize;
+    if (m_rayCursor >= m_total_rays) m_rayCursor = 0;
+    if (m_rayCursor == 0) m_epochSeed = m_seed_dist(m_rng);
+    const int chunkSize = (int)std::min(rayChunk, m_total_rays - m_rayCursor);
+
+    m_nerf->setLearningRate(currentLR());
+    m_nerf->setMemoryMode(TRAINING);
+    const float3 bg = make_float3(m_dist(m_rng), m_dist(m_rng), m_dist(m_rng));
+    m_nerf->setBgColor(bg);
+    m_dataloader->fetchRayChunk((int)m_rayCursor, chunkSize, m_epochSeed, bg, 0, false, (int)m_holdout_every);
+
+    std::vector<uint32_t> hitCounts((size_t)chunkSize, 0);
+    m_nerf->trainWithRaysHit(m_dataloader->getChunkRaysO(), m_dataloader->getChunkRaysD(),
+                             m_dataloader->getChunkRaysDense(), m_dataloader->getChunkRaysSigma(),
+                             m_dataloader->getChunkRgbTrue(), (uint32_t)chunkSize, m_globalStep, hitCounts.data(),
+                             computeLoss ? m_d_chunkRgb : nullptr, 0);
+    m_rayCursor += (uint32_t)chunkSize;
+    m_raysSeen += chunkSize;
+    if (!computeLoss) return -1.0f;
+    return chunkMse(m_d_chunkRgb, m_dataloader->getChunkRgbTrue(), chunkSize) / (float)std::max(1, chunkSize);
+}
+
+void INerfTrainer::beginTraining(int totalSteps)
+{
+    m_targetSteps = std::max(1, totalSteps);
+    m_globalStep = 0;
+    m_rayCursor = 0;
+    m_raysSeen = 0.0;
+    m_emaMsPerStep = 0.0;
+    m_lossHistory.clear();
+}
+
+TrainStats INerfTrainer::trainSteps(int nSteps)
+{
+    TrainStats s;
+    if (!m_nerf || !m_dataloader || m_total_rays == 0) return s;
+    if (m_targetSteps == 0) beginTraining(20000);
+    const int target = std::min(m_globalStep + std::max(1, nSteps), m_targetSteps);
+    const int startStep = m_globalStep;
+    const auto t0 = std::chrono::high_resolution_clock::now();
+    float mse = -1.0f;
+    bool first = true;
+    while (m_globalStep < target) {
+        const float chunkMse_ = trainOneChunk(first);
+        if (chunkMse_ > 0.0f) mse = chunkMse_;
+        first = false;
+    }
+    GRAFT_HIP_CHECK(hipDeviceSynchronize());
+    const auto t1 = std::chrono::high_resolution_clock::now();
+    const int stepsDone = m_globalStep - startStep;
+    if (stepsDone > 0) {
+        const double ms = std::chrono::duration<double, std::milli>(t1 - t0).count() / stepsDone;
+        m_emaMsPerStep = (m_emaMsPerStep > 0.0) ? (0.70 * m_emaMsPerStep + 0.30 * ms) : ms;
+    }
+    if (mse > 0.0f) m_lossHistory.push_back(mse);
+    const int remaining = std::max(0, m_targetSteps - m_globalStep);
+    s.step = m_globalStep;
+    s.targetSteps = m_targetSteps;
+    s.loss = (mse > 0.0f) ? mse : (m_lossHistory.empty() ? 0.0f : m_lossHistory.back());
+    s.psnr = (s.loss > 0.0f) ? -10.0f * log10f(fmaxf(s.loss, 1e-8f)) : 0.0f;
+    s.lr = currentLR();
+    s.epochs = epochs();
+    s.msPerStep = (float)m_emaMsPerStep;
+    s.etaSeconds = (float)(m_emaMsPerStep * remaining / 1000.0);
+    return s;
+}
+
+// NerfTrainer.cu:228-252: progress bar on stdout.
+void INerfTrainer::train(int maxSteps, int maxEpochs)
+{
+    (void)maxEpochs;
+    if (!m_nerf || !m_dataloader || m_total_rays == 0)
+        throw std::runtime_error("INerfTrainer: train() called before loadDataset()");
+    beginTraining(maxSteps);
+    const int tick = std::max(1, maxSteps / 100);
+    while (!isTrainingDone()) {
+        const TrainStats s = trainSteps(tick);
+        const float frac = s.targetSteps > 0 ? std::min(1.0f, (float)s.step / (float)s.targetSteps) : 0.0f;
+        const int filled = (int)(frac * 28 + 0.5f);
+        std::printf("\r[%s%s] %d/%d steps | epoch %.2f | %.2f ms/step | PSNR %.1f   ",
+                    std::string((size_t)filled, '#').c_str(), std::string((size_t)(28 - filled), ' ').c_str(), s.step,
+                    s.targetSteps, s.epochs, s.msPerStep, s.psnr);
+        std::fflush(stdout);
+    }
+    std::printf("\n");
+}
+
+// NerfTrainer.cu:302-327
+Image INerfTrainer::renderC2W(const float c2w[16], float focal, int width, int height)
+{
+    Image img;
+    img.width = width;
+    img.height = height;
+    img.rgb.assign((size_t)width * height * 3, 0.0f);
+    if (!m_nerf || width <= 0 || height <= 0) return img;
+    const int numRays = width * height;
+    float3* d_o = dalloc<float3>((size_t)numRays);
+    float3* d_d = dalloc<float3>((size_t)numRays);
+    float* d_rgb = dalloc<float>((size_t)numRays * 3);
+    try {
+        graft::pinhole_rays(width, height, focal, c2w, d_o, d_d, 0);
+        m_nerf->setMemoryMode(INFERENCE);
+        m_nerf->renderImageHit(d_o, d_d, (uint32_t)numRays, d_rgb, 0);
+        GRAFT_HIP_CHECK(hipMemcpy(img.rgb.data(), d_rgb, (size_t)numRays * 3 * sizeof(float), hipMemcpyDeviceToHost));
+    } catch (...) {
+        (void)hipFree(d_o);
+        (void)hipFree(d_d);
+        (void)hipFree(d_rgb);
+        throw;
+    }
+    (void)hipFree(d_o);
+    (void)hipFree(d_d);
+    (void)hipFree(d_rgb);
+    return img;
+}
+
+// NerfTrainer.cu:329-360: camera on a sphere around the scene centre, looking at it.
+Image INerfTrainer::renderOrbit(float azimuthDeg, float elevationDeg, float radius, float fovDeg, int width,
+                                int height)
+{
+    if (!m_nerf) return Image{};
+    const float cx = m_sceneCenter.x, cy = m_sceneCenter.y, cz = m_sceneCenter.z;
+    float ux = m_sceneUp.x, uy = m_sceneUp.y, uz = m_sceneUp.z;
+    const float ul = std::sqrt(ux * ux + uy * uy + uz * uz);
+    if (ul > 0) {
+        ux /= ul;
+        uy /= ul;
+        uz /= ul;
+    }
+    // a, b: an orthonormal basis of the plane normal to up
+    const float rx = std::fabs(uy) < 0.9f ? 0.0f : 1.0f, ry = std::fabs(uy) < 0.9f ? 1.0f : 0.0f, rz = 0.0f;
+    float ax = uy * rz - uz * ry, ay = uz * rx - ux * rz, az_ = ux * ry - uy * rx;
+    const float al = std::sqrt(ax * ax + ay * ay + az_ * az_);
+    ax /= al;
+    ay /= al;
+    az_ /= al;
+    const float bx = uy * az_ - uz * ay, by = uz * ax - ux * az_, bz = ux * ay - uy * ax;
+    const float az = azimuthDeg * kPI / 180.0f, el = elevationDeg * kPI / 180.0f;
+    const float px = std::cos(az) * ax + std::sin(az) * bx, py = std::cos(az) * ay + std::sin(az) * by;
+    const float pz = std::cos(az) * az_ + std::sin(az) * bz;
+    const float dx = std::cos(el) * px + std::sin(el) * ux, dy = std::cos(el) * py + std::sin(el) * uy;
+    const float dz = std::cos(el) * pz + std::sin(el) * uz;
+    const float ex = cx + radius * dx, ey = cy + radius * dy, ez = cz + radius * dz;
+    float fx = cx - ex, fy = cy - ey, fz = cz - ez;
+    const float fl = std::sqrt(fx * fx + fy * fy + fz * fz);
+    fx /= fl;
+    fy /= fl;
+    fz /= fl;
+    float sx = fy * uz - fz * uy, sy = fz * ux - fx * uz, sz = fx * uy - fy * ux;
+    const float sl = std::sqrt(sx * sx + sy * sy + sz * sz);
+    sx /= sl;
+    sy /= sl;
+    sz /= sl;
+    const float vx = sy * fz - sz * fy, vy = sz * fx - sx * fz, vz = sx * fy - sy * fx;
+    const float c2w[16] = {sx, vx, -fx, ex, sy, vy, -fy, ey, sz, vz, -fz, ez, 0.0f, 0.0f, 0.0f, 1.0f};
+    const float focal = 0.5f * (float)width / std::tan(0.5f * fovDeg * kPI / 180.0f);
+    return renderC2W(c2w, focal, width, height);
+}
+
+// NerfTrainer.cu:362-371
+Image INerfTrainer::renderTrainView(int index, int width, int height)
+{
+    if (!m_nerf || !m_dataloader) return Image{};
+    if (width <= 0) width = m_dataloader->getWidth();
+    if (height <= 0) height = m_dataloader->getHeight();
+    float c2w[16];
+    m_dataloader->getFramePose(index, c2w);
+    const float focal = 0.5f * (float)width / std::tan(0.5f * m_dataloader->getCameraAngleX());
+    return renderC2W(c2w, focal, width, height);
+}
+
+// NerfTrainer.cu:373-408: held-out views (every 8th image) in sequential
+// tiles of rayChunkSize rays, ground truth composited over white, mean over
+// pixels of (r^2 + g^2 + b^2) / 3.  As in the reference, the model renders
+// with its current background colour (the last training chunk's).
+float INerfTrainer::validate()
+{
+    if (!m_nerf || !m_dataloader) return 0.0f;
+    const int HOLDOUT = 8;
+    const int pixels = m_dataloader->getWidth() * m_dataloader->getHeight();
+    if (pixels <= 0) return 0.0f;
+    const int numImgs = m_dataloader->getNumImages();
+    const int tile = m_masterConfig.rayChunkSize;
+    m_nerf->setMemoryMode(INFERENCE);
+    const float3 valBg = make_float3(1.0f, 1.0f, 1.0f);
+    double se = 0.0;
+    long long totalPixels = 0;
+    for (int i = 0; i < numImgs; ++i) {
+        if (i % HOLDOUT != 0) continue;
+        for (int off = 0; off < pixels; off += tile) {
+            const int count = std::min(tile, pixels - off);
+            m_dataloader->fetchRayChunk(i * pixels + off, count, 0, valBg, 0, true, 0);
+            m_nerf->renderImageHit(m_dataloader->getChunkRaysO(), m_dataloader->getChunkRaysD(), (uint32_t)count,
+                                   m_d_chunkRgb, 0);
+            se += chunkMse(m_d_chunkRgb, m_dataloader->getChunkRgbTrue(), count);
+            totalPixels += count;
+        }
+    }
+    m_nerf->setMemoryMode(TRAINING);
+    const float mse = (float)(se / (double)std::max(1LL, totalPixels));
+    return -10.0f * log10f(fmaxf(mse, 1e-8f));
+}
+
+int INerfTrainer::numTrainViews() const
+{
+    if (!m_dataloader) return 0;
+    const int px = m_dataloader->getWidth() * m_dataloader->getHeight();
+    return px > 0 ? (int)(m_total_rays / (uint32_t)px) : 0;
+}
+
+// NerfTrainer.cu:269-300
+void INerfTrainer::save(const std::string& path)
+{
+    if (!m_nerf) return;
+    m_nerf->save(path);
+    std::ofstream out(path, std::ios::binary | std::ios::app);
+    if (!out) throw std::runtime_error("INerfTrainer::save: cannot append the scene footer to " + path);
+    const float buf[8] = {m_sceneCenter.x, m_sceneCenter.y, m_sceneCenter.z, m_sceneUp.x,
+                          m_sceneUp.y,     m_sceneUp.z,     m_sceneScale,    m_cameraAngleX};
+    out.write(kSceneMagic, 4);
+    out.write(reinterpret_cast<const char*>(buf), sizeof(buf));
+}
+
+void INerfTrainer::load(const std::string& path)
+{
+    if (!m_nerf) m_nerf = new InstantNerf();
+    m_nerf->load(path);
+    m_masterConfig = m_nerf->options();
+    (void)hipFree(m_d_chunkRgb);
+    (void)hipFree(m_d_err);
+    m_d_chunkRgb = dalloc<float>((size_t)m_masterConfig.rayChunkSize * 3);
+    m_d_err = dalloc<float>((size_t)m_masterConfig.rayChunkSize);
+    if (!m_d_loss) m_d_loss = dalloc<float>(1);
+    if (!m_d_partials) m_d_partials = dalloc<float>(1024);
+    std::ifstream in(path, std::ios::binary | std::ios::ate);
+    if (!in) return;
+    const std::streamoff size = in.tellg();
+    if (size < kSceneFooterBytes) return;
+    in.seekg(size - kSceneFooterBytes, std::ios::beg);
+    char magic[4];
+    in.read(magic, 4);
+    if (std::memcmp(magic, kSceneMagic, 4) != 0) return;
+    float buf[8];
+    in.read(reinterpret_cast<char*>(buf), sizeof(buf));
+    if (!in) return;
+    m_sceneCenter = {buf[0], buf[1], buf[2]};
+    m_sceneUp = {buf[3], buf[4], buf[5]};
+    m_sceneScale = buf[6];
+    m_cameraAngleX = buf[7];
+}

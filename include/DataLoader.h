@@ -13,6 +13,7 @@
 #include <hip/hip_vector_types.h>
 
 #include <cstdint>
+#include <vector>
 
 class DataLoader {
 public:
@@ -52,6 +53,12 @@ public:
     int getHeight() const { return height; }
     float getFocal() const { return focal; }
     int getNumImages() const { return num_images; }
+    // DataLoader.h:69: horizontal field of view, 2 atan(w / (2 focal)).
+    float getCameraAngleX() const;
+    // DataLoader.h:89-92: camera-to-world of frame i (row-major 4x4), zeros when out of range.
+    void getFramePose(int i, float out[16]) const;
+    // DataLoader.h:49-68: mean camera position and normalised mean camera up axis.
+    void getSceneOrientation(float3& center, float3& up) const;
 
 private:
     int width = 0, height = 0, num_images = 0;
@@ -60,6 +67,7 @@ private:
     bool m_is_training = true;
     float m_dense_fraction = 0.0f;
     int m_depth_width = 0, m_depth_height = 0;
+    std::vector<float> h_transforms;  // [images][16]
     uint8_t* d_images_rgba = nullptr;
     float* d_transforms = nullptr;
     float3* d_chunk_rays_o = nullptr;
