@@ -426,6 +426,228 @@ __global__ __launch_bounds__(256) void mlp_bwd_kernel(const BwdParams p)
     }
 }
 
+// ---------------------------------------------------------------------------
+// backward for the NeRF head shapes, all in registers
+// ---------------------------------------------------------------------------
+//
+// dW = sum_s G[o][s] X[i][s] needs both operands with the sample index along
+// K, while the MFMA chain of the layers holds every 16-sample tile with the
+// sample along N ("S layout": lane l has features 4(l/16)..+3 of sample l%16).
+// One MFMA against the identity, D = T * I, moves a 16x16 tile from A layout
+// to D layout, which for these tiles is exactly S -> "F layout" (lane l has
+// feature l%16 of samples 4(l/16)..+3); it is exact for every finite fp16
+// (a -0 becomes +0, which no sum or mask here can see).  A tile holding inf or
+// NaN would spread it through the 0 * x products, so such a tile is moved with
+// lane shuffles instead.  Each wave then runs its tiles layer by layer with no
+// LDS traffic but the weights, keeps its dW/db in registers, and the four waves
+// of a block add their partials in a fixed order at the end.
+
+__device__ __forceinline__ h4 ident_h4(int lane)
+{
+    const int g = lane >> 4, r = lane & 15;
+    h4 v;
+#pragma unroll
+    for (int j = 0; j < 4; j++) v[j] = (4 * g + j == r) ? (_Float16)1.0f : (_Float16)0.0f;
+    return v;
+}
+
+__device__ __forceinline__ bool h4_nonfinite(h4 v)
+{
+    bool bad = false;
+#pragma unroll
+    for (int j = 0; j < 4; j++) bad |= (__builtin_bit_cast(uint16_t, v[j]) & 0x7c00u) == 0x7c00u;
+    return bad;
+}
+
+// S layout -> F layout of one 16x16 tile.
+__device__ __forceinline__ h4 tile_transpose(h4 v, h4 id, bool exact_slow, int lane)
+{
+    if (!exact_slow) {
+        const f4 d = mfma16(v, id, f4zero());
+        return h4{(_Float16)d[0], (_Float16)d[1], (_Float16)d[2], (_Float16)d[3]};
+    }
+    // element (row 4g + j, col r) lives in lane (4g + j) + 16 (r / 4), component r % 4
+    const int g = lane >> 4, r = lane & 15;
+    const uint32_t w0 = __builtin_bit_cast(uint32_t, h2{v[0], v[1]});
+    const uint32_t w1 = __builtin_bit_cast(uint32_t, h2{v[2], v[3]});
+    h4 out;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int src = 4 * g + j + 16 * (r >> 2);
+        const uint32_t a = (uint32_t)__shfl((int)w0, src, 64), b = (uint32_t)__shfl((int)w1, src, 64);
+        const uint32_t w = (r & 2) ? b : a;
+        out[j] = __builtin_bit_cast(_Float16, (uint16_t)((r & 1) ? (w >> 16) : (w & 0xffffu)));
+    }
+    return out;
+}
+
+template <int IN, int HID, int OUT, int LAYERS>
+struct HeadShape {
+    static constexpr int in_l(int l) { return l == 0 ? IN : HID; }
+    static constexpr int out_l(int l) { return l == LAYERS - 1 ? OUT : HID; }
+    static constexpr int ib(int l) { return (in_l(l) + 15) / 16; }
+    static constexpr int ob(int l) { return (out_l(l) + 15) / 16; }
+    static constexpr int acc_off(int l) { return l == 0 ? 0 : acc_off(l - 1) + ob(l - 1) * ib(l - 1); }
+    static constexpr int nacc() { return acc_off(LAYERS - 1) + ob(LAYERS - 1) * ib(LAYERS - 1); }
+    static constexpr int db_off(int l) { return l == 0 ? 0 : db_off(l - 1) + ob(l - 1); }
+    static constexpr int ndb() { return db_off(LAYERS - 1) + ob(LAYERS - 1); }
+};
+
+template <int IN, int HID, int OUT, int LAYERS>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void mlp_bwd_head_kernel(const BwdParams p)
+{
+    using S = HeadShape<IN, HID, OUT, LAYERS>;
+    constexpr int MB = 4;  // max 16-wide blocks per layer (width <= 64)
+    extern __shared__ __align__(16) unsigned char smem[];
+    _Float16* sfrag = reinterpret_cast<_Float16*>(smem);
+    float* sred = reinterpret_cast<float*>(smem + p.acc_base);  // [P] block partial
+    const int tid = threadIdx.x;
+
+    // Transposed fragments for dX = W^T G (as mlp_bwd_kernel).
+#pragma unroll
+    for (int l = 0; l < LAYERS; l++) {
+        const int in_l = S::in_l(l), out_l = S::out_l(l);
+        const int KS = S::ob(l), MT = S::ib(l);
+        const _Float16* w = p.W[l];
+        for (int e = tid; e < MT * KS * 256; e += blockDim.x) {
+            const int j = e & 3, ln = (e >> 2) & 63, f = e >> 8;
+            const int mt = f / KS, ks = f - mt * KS;
+            const int o = 16 * ks + 4 * (ln >> 4) + j, i = 16 * mt + (ln & 15);
+            sfrag[p.fragT_off[l] + e] = (o < out_l && i < in_l) ? w[o * in_l + i] : (_Float16)0.f;
+        }
+    }
+    __syncthreads();
+
+    const int lane = tid & 63, wave = tid >> 6, g = lane >> 4, r = lane & 15;
+    const int N = p.d_n ? min((int)*p.d_n, p.N) : p.N;
+    const int ntiles = (N + 15) >> 4;
+    const h4 id = ident_h4(lane);
+    f4 acc[S::nacc()];
+    float dbs[S::ndb()];
+#pragma unroll
+    for (int a = 0; a < S::nacc(); a++) acc[a] = f4zero();
+#pragma unroll
+    for (int a = 0; a < S::ndb(); a++) dbs[a] = 0.f;
+
+    for (int tile = blockIdx.x * 4 + wave; tile < ntiles; tile += gridDim.x * 4) {
+        const int n = tile * 16 + r;
+        const bool valid = n < N;
+        h4 G[MB];
+#pragma unroll
+        for (int ob = 0; ob < MB; ob++) {
+            const int col = 16 * ob + 4 * g;
+            G[ob] = (ob < S::ob(LAYERS - 1) && valid && col < OUT) ? ld_h4(p.dy + (size_t)n * OUT + col) : h4zero();
+        }
+#pragma unroll
+        for (int l = LAYERS - 1; l >= 0; l--) {
+            const int in_l = S::in_l(l);
+            h4 X[MB];
+#pragma unroll
+            for (int ib = 0; ib < MB; ib++) {
+                const int col = 16 * ib + 4 * g;
+                X[ib] = (ib < S::ib(l) && valid) ? ld_h4(p.acts[l] + (size_t)n * in_l + col) : h4zero();
+            }
+            // exact-slow transposes only for a tile holding inf / NaN
+            bool bad = false;
+#pragma unroll
+            for (int b = 0; b < MB; b++) bad |= h4_nonfinite(G[b]) | h4_nonfinite(X[b]);
+            const bool slow = __ballot(bad) != 0;
+            h4 GF[MB], XF[MB];
+#pragma unroll
+            for (int ob = 0; ob < MB; ob++)
+                if (ob < S::ob(l)) GF[ob] = tile_transpose(G[ob], id, slow, lane);
+#pragma unroll
+            for (int ib = 0; ib < MB; ib++)
+                if (ib < S::ib(l)) XF[ib] = tile_transpose(X[ib], id, slow, lane);
+            // dW[o][i] += G_F(o) X_F(i); db[o] += sum of this lane's 4 samples
+#pragma unroll
+            for (int ob = 0; ob < MB; ob++) {
+                if (ob >= S::ob(l)) continue;
+#pragma unroll
+                for (int ib = 0; ib < MB; ib++)
+                    if (ib < S::ib(l)) {
+                        f4& a = acc[S::acc_off(l) + ob * S::ib(l) + ib];
+                        a = mfma16(GF[ob], XF[ib], a);
+                    }
+                const h4 v = GF[ob];
+                dbs[S::db_off(l) + ob] += ((float)v[0] + (float)v[1]) + ((float)v[2] + (float)v[3]);
+            }
+            // dX = W^T G, rounded to fp16, ReLU-masked by this layer's input
+            if (l > 0 || p.dx != nullptr) {
+                const _Float16* fr = sfrag + p.fragT_off[l] + lane * 4;
+                h4 Gn[MB];
+#pragma unroll
+                for (int ib = 0; ib < MB; ib++) {
+                    Gn[ib] = h4zero();
+                    if (ib >= S::ib(l)) continue;
+                    f4 d = f4zero();
+#pragma unroll
+                    for (int ob = 0; ob < MB; ob++)
+                        if (ob < S::ob(l))
+                            d = mfma16(*reinterpret_cast<const h4*>(fr + (ib * S::ob(l) + ob) * 256), G[ob], d);
+                    h4 h;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) h[j] = to_h(d[j]);
+                    if (l > 0) {
+#pragma unroll
+                        for (int j = 0; j < 4; j++)
+                            if (!((float)X[ib][j] > 0.f)) h[j] = (_Float16)0.f;
+                    } else {
+                        const int col = 16 * ib + 4 * g;
+                        if (valid && col < IN) st_h4(p.dx + (size_t)n * IN + col, h);
+                    }
+                    Gn[ib] = h;
+                }
+#pragma unroll
+                for (int b = 0; b < MB; b++) G[b] = Gn[b];
+            }
+        }
+    }
+
+    // db: the 4 lanes of a feature (g = 0..3) in a fixed order
+#pragma unroll
+    for (int a = 0; a < S::ndb(); a++) {
+        const float v0 = __shfl(dbs[a], r, 64), v1 = __shfl(dbs[a], r + 16, 64);
+        const float v2 = __shfl(dbs[a], r + 32, 64), v3 = __shfl(dbs[a], r + 48, 64);
+        dbs[a] = (v0 + v1) + (v2 + v3);
+    }
+    // block partial: wave 0 writes, waves 1..3 add in order
+    for (int w = 0; w < 4; w++) {
+        if (wave == w) {
+#pragma unroll
+            for (int l = 0; l < LAYERS; l++) {
+                const int in_l = S::in_l(l), out_l = S::out_l(l);
+#pragma unroll
+                for (int ob = 0; ob < MB; ob++) {
+                    if (ob >= S::ob(l)) continue;
+#pragma unroll
+                    for (int ib = 0; ib < MB; ib++) {
+                        if (ib >= S::ib(l)) continue;
+                        const f4 a = acc[S::acc_off(l) + ob * S::ib(l) + ib];
+                        const int i = 16 * ib + r;
+#pragma unroll
+                        for (int j = 0; j < 4; j++) {
+                            const int o = 16 * ob + 4 * g + j;
+                            if (o < out_l && i < in_l) {
+                                float* dst = sred + p.wofs[l] + o * in_l + i;
+                                *dst = (w == 0) ? a[j] : *dst + a[j];
+                            }
+                        }
+                    }
+                    const int o = 16 * ob + r;
+                    if (g == 0 && o < out_l) {
+                        float* dst = sred + p.bofs[l] + o;
+                        *dst = (w == 0) ? dbs[S::db_off(l) + ob] : *dst + dbs[S::db_off(l) + ob];
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+    float* dstp = p.ws + (size_t)blockIdx.x * p.P;
+    for (int e = tid; e < p.P; e += blockDim.x) dstp[e] = sred[e];
+}
+
 // grad[p] += sum over blocks of ws[b][p], summed in block order.
 struct ReduceParams {
     const float* ws;
@@ -625,7 +847,41 @@ void mlp_backward(const MlpShape& s, const __half* dy, const __half* const* acts
     }
     p.P = btot;
     const int maxd = pick_maxd(s.maxd());
-    // register accumulators for nets of up to 4 layers of width <= 64 (the NeRF heads)
+    // the two NeRF heads: registers only, transposes on the MFMA unit
+    const bool density_head = s.in == 32 && s.hid == 64 && s.out == 16 && s.layers == 2;
+    const bool color_head = s.in == 32 && s.hid == 64 && s.out == 8 && s.layers == 3;
+    if (density_head || color_head) {
+        p.acc_base = (frag_halves * 2 + 15) & ~15;
+        const int lds = p.acc_base + p.P * 4;
+        if (lds > max_lds_per_block()) throw std::runtime_error("TinyMLP: backward LDS budget");
+        const int ntiles = (N + 15) / 16;
+        const auto kern = density_head ? mlp_bwd_head_kernel<32, 64, 16, 2> : mlp_bwd_head_kernel<32, 64, 8, 3>;
+        // one block per resident slot: the grid-stride split then ends in a
+        // single wave of blocks (a second, partial wave would run alone)
+        int per_cu = 0;
+        GRAFT_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, lds));
+        const int blocks = std::max(1, std::min((ntiles + 3) / 4, num_cus() * std::max(1, per_cu)));
+        p.ws = static_cast<float*>(workspace((size_t)blocks * p.P * sizeof(float)));
+        hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), lds, stream, p);
+        GRAFT_LAUNCH_CHECK();
+        ReduceParams rp{};
+        rp.ws = p.ws;
+        rp.dW = dW;
+        rp.dB = dB;
+        rp.nparts = blocks;
+        rp.P = p.P;
+        rp.layers = s.layers;
+        rp.wtot = wtot;
+        rp.accumulate = accumulate ? 1 : 0;
+        for (int l = 0; l < s.layers; l++) {
+            rp.wofs[l] = p.wofs[l];
+            rp.bofs[l] = p.bofs[l];
+        }
+        hipLaunchKernelGGL(mlp_grad_reduce_kernel, dim3((p.P + 63) / 64), dim3(1024), 0, stream, rp);
+        GRAFT_LAUNCH_CHECK();
+        return;
+    }
+    // register accumulators for nets of up to 4 layers of width <= 64
     const bool reg = maxd <= 64 && s.layers <= 4;
     p.gt_base = (frag_halves * 2 + 15) & ~15;
     p.xt_base = p.gt_base + maxd * kBwdPitch * 2;

@@ -138,7 +138,7 @@ __global__ __launch_bounds__(256) void zero_layers_kernel(float* const* a, float
 // Two elements per thread as half2 pairs; padded columns carry zero gradient.
 template <int OUT_ACT>
 __global__ __launch_bounds__(256) void mse_kernel(const float* __restrict__ pred, const _Float16* __restrict__ tgt,
-                                                  _Float16* __restrict__ dloss, float* __restrict__ total,
+                                                  _Float16* __restrict__ dloss, float* __restrict__ partials,
                                                   long long n2, int padded, int valid, float grad_scale)
 {
     __shared__ float red[4];
@@ -161,7 +161,25 @@ __global__ __launch_bounds__(256) void mse_kernel(const float* __restrict__ pred
     for (int o = 32; o > 0; o >>= 1) local += __shfl_down(local, o, 64);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = local;
     __syncthreads();
-    if (threadIdx.x == 0) atomicAdd(total, (red[0] + red[1]) + (red[2] + red[3]));
+    if (threadIdx.x == 0) partials[blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// *total += the block partials of mse_kernel, summed in a fixed order (one
+// block; a same-address atomic per block would serialise thousands of adds).
+__global__ __launch_bounds__(1024) void sum_into_kernel(const float* __restrict__ partials, int n,
+                                                        float* __restrict__ total)
+{
+    __shared__ float red[16];
+    float v = 0.0f;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) v += partials[i];
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_down(v, o, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float t = 0.0f;
+        for (int w = 0; w < (int)(blockDim.x >> 6); w++) t += red[w];
+        *total += t;
+    }
 }
 
 template <typename TI, typename TO>
@@ -251,10 +269,15 @@ void mse_loss_grad(const float* pred, const __half* tgt, __half* dloss, float* t
     const int blocks = blocks_for(n2);
     const _Float16* t = reinterpret_cast<const _Float16*>(tgt);
     _Float16* d = reinterpret_cast<_Float16*>(dloss);
+    float* partials = static_cast<float*>(workspace((size_t)blocks * sizeof(float)));
     if (out_act == 1)
-        hipLaunchKernelGGL(mse_kernel<1>, dim3(blocks), dim3(256), 0, stream, pred, t, d, total, n2, padded, valid, grad_scale);
+        hipLaunchKernelGGL(mse_kernel<1>, dim3(blocks), dim3(256), 0, stream, pred, t, d, partials, n2, padded, valid,
+                           grad_scale);
     else
-        hipLaunchKernelGGL(mse_kernel<0>, dim3(blocks), dim3(256), 0, stream, pred, t, d, total, n2, padded, valid, grad_scale);
+        hipLaunchKernelGGL(mse_kernel<0>, dim3(blocks), dim3(256), 0, stream, pred, t, d, partials, n2, padded, valid,
+                           grad_scale);
+    GRAFT_LAUNCH_CHECK();
+    hipLaunchKernelGGL(sum_into_kernel, dim3(1), dim3(1024), 0, stream, partials, blocks, total);
     GRAFT_LAUNCH_CHECK();
 }
 

@@ -10,7 +10,8 @@ driven by INerfTrainer::trainOneChunk, NerfTrainer.cu:137-179):
   ray feed (launchFetchRayChunk, DataLoader.cu:548-661) draws 2^16 rays per
   trainWithRaysHit call with pcg_hash and composites them over a random
   background colour per call, as the reference trainer does; occupancy
-  128^3 x 5 cascades x 4 mips, AABB +-1.5, K = 1; hash grid L = 16, F = 2,
+  128^3 x 1 cascade x 4 mips (the reference loader's choice for an orbit),
+  AABB +-1.5, K = 1; hash grid L = 16, F = 2,
   T = 2^19, base 16, b = 1.3819; density 32 -> 64 -> 16, colour
   32 -> 64 -> 64 -> 3 (sigmoid); distortion loss lambda = 0.1; loss scale 128;
   Adam (0.9, 0.999, 1e-8); cosine LR 1e-2 -> 1e-4 over 2000 steps; occupancy
@@ -56,6 +57,7 @@ RAYS_PER_CALL = 1 << 16
 N_VIEWS, N_HELDOUT, IMG_W, IMG_H, FOV_X = 100, 12, 800, 800, 50.0
 L, F, TBL, BASE, GROWTH = 16, 2, 1 << 19, 16, 1.3819
 LR_MAX, LR_MIN, ANNEAL = 1e-2, 1e-4, 2000
+CPU_FEED_CHUNKS = 8            # feed chunks of rays available to the CPU-oracle leg (stops after ~10 s)
 
 # Algorithmic counts per unit.
 ENC_BYTES_PER_SAMPLE = 16 + L * 8 * 4 + 2 * L * 2                    # 592
@@ -96,7 +98,10 @@ def options(P):
     o.gridResolution[:] = [128, 128, 128]
     o.aabbMin[:] = [-1.5] * 3
     o.aabbMax[:] = [1.5] * 3
-    o.levelsMipmap, o.numCascades, o.samplesPerVoxel = 4, 5, 1
+    # One cascade: INerfTrainer takes the loader's estimate (NerfTrainer.cu:113-114), and the loader's pose
+    # heuristic gives 1 for cameras orbiting the scene, as here (DataLoader.cu:368-376).  With 5 cascades
+    # the far field holds a fog shell whose colour follows the random background of the last ray chunk.
+    o.levelsMipmap, o.numCascades, o.samplesPerVoxel = 4, 1, 1
     o.densityHiddenDim, o.densityNumLayers = 64, 2
     o.colorHiddenDim, o.colorNumLayers = 64, 3
     o.hashTableSize, o.numLevels, o.growthFactor, o.baseResolution, o.featuresPerLevel = TBL, L, GROWTH, BASE, F
@@ -170,14 +175,16 @@ class Trainer:
         return hits
 
 
-def cpu_baseline(P, nerf, o, d, gt):
-    """The C oracle on the host: one full training step on a bounded ray sample."""
+def cpu_baseline(P, nerf, o, d, gt, min_seconds=10.0, max_steps=64):
+    """The C oracle on the host cores: full training steps of up to BATCH compacted
+    samples each, chained (each step marches the next rays and trains the
+    parameters the previous step updated), until min_seconds have passed."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import pyoracle as orc
     bits = nerf.occupancy()
+    casc = int(nerf.opts.numCascades)
     mn, mx = np.float32([-1.5] * 3), np.float32([1.5] * 3)
-    R = 1 << 14
-    oo, dd, gg = o[:R], d[:R], gt[:R]
+    window = 1 << 14  # rays marched per step; the batch fills from their front
     dW = np.zeros(64 * 32 + 16 * 64, np.float32)
     dB = np.zeros(80, np.float32)
     nerf.density.save_weights(dW, dB)
@@ -187,36 +194,43 @@ def cpu_baseline(P, nerf, o, d, gt):
     cB = np.zeros(136, np.float32)
     nerf.color.save_weights(cW, cB)
     t16 = table.astype(np.float16)
+    mt, vt = np.zeros_like(table), np.zeros_like(table)
+    state = [(w, np.zeros_like(w), np.zeros_like(w)) for w in (dW, dB, cW, cB)]
+    ray0, steps, samples = 0, 0, 0
     t0 = time.perf_counter()
-    di, nr, fr = orc.ray_aabb_inv(oo, dd, mn, mx, 5)
-    m = orc.march_hits(oo, dd, di, nr, fr, bits, [128] * 3, mn, mx, 5, 4, 1, 1 << 16)
-    N = m["total"]
-    enc = orc.hash_encode(m["pos"], t16, TBL, L, BASE, GROWTH)
-    dout, dacts = orc.mlp_forward(enc, dW.astype(np.float16), dB, 32, 64, 16, 2)
-    cin, sig = orc.sh_gather(dd, m["ray_idx"], dout, 0.0)
-    cout, cacts = orc.mlp_forward(cin, cW.astype(np.float16), cB, 32, 64, 8, 3, out_act=1)
-    rgb = np.ascontiguousarray(cout[:, :3])
-    act = m["active"]
-    comp = orc.composite(m["offsets"][:act], m["counts"][:act], m["t"], sig, rgb, gg[:act], 0.1,
-                         np.float32([1, 1, 1]))
-    cg, ds = orc.color_grad(m["counts"][:act], m["offsets"][:act], m["t"], dout, rgb, comp["phi"], comp["rgb"],
-                            comp["dw"], comp["weight_sum"], 128.0, 0.0, R)
-    cgp = np.zeros((N, 8), np.float16)
-    cgp[:, :3] = cg
-    gW, gB, cdx = orc.mlp_backward(cgp, cin, cacts, cW.astype(np.float16), 32, 64, 8, 3)
-    dg = orc.density_grad(ds, cdx)
-    hW, hB, denc = orc.mlp_backward(dg, enc, dacts, dW.astype(np.float16), 32, 64, 16, 2)
-    grads = orc.hash_scatter(m["pos"], denc, TBL, L, BASE, GROWTH)
-    bc1, bc2 = orc.adam_bias_corrections(0.9, 0.999, 1)
-    z = np.zeros_like(table)
-    orc.adam_hash(table, grads, z, z.copy(), 1e-2, 0.9, 0.999, 1e-8, bc1, bc2, 1 / 128.0)
-    for w, g in ((dW, hW), (dB, hB), (cW, gW), (cB, gB)):
-        orc.adam_dense(w, g, np.zeros_like(w), np.zeros_like(w), 1e-2, 0.9, 0.999, 1e-8, bc1, bc2, 1 / 128.0)
+    while steps < max_steps and ray0 < len(o) and (steps == 0 or time.perf_counter() - t0 < min_seconds):
+        oo, dd, gg = o[ray0:ray0 + window], d[ray0:ray0 + window], gt[ray0:ray0 + window]
+        di, nr, fr = orc.ray_aabb_inv(oo, dd, mn, mx, casc)
+        m = orc.march_hits(oo, dd, di, nr, fr, bits, [128] * 3, mn, mx, casc, 4, 1, BATCH)
+        N, act = m["total"], m["active"]
+        dW16, cW16 = dW.astype(np.float16), cW.astype(np.float16)
+        enc = orc.hash_encode(m["pos"], t16, TBL, L, BASE, GROWTH)
+        dout, dacts = orc.mlp_forward(enc, dW16, dB, 32, 64, 16, 2)
+        cin, sig = orc.sh_gather(dd, m["ray_idx"], dout, 0.0)
+        cout, cacts = orc.mlp_forward(cin, cW16, cB, 32, 64, 8, 3, out_act=1)
+        rgb = np.ascontiguousarray(cout[:, :3])
+        comp = orc.composite(m["offsets"][:act], m["counts"][:act], m["t"], sig, rgb, gg[:act], 0.1,
+                             np.float32([1, 1, 1]))
+        cg, ds = orc.color_grad(m["counts"][:act], m["offsets"][:act], m["t"], dout, rgb, comp["phi"], comp["rgb"],
+                                comp["dw"], comp["weight_sum"], 128.0, 0.0, RAYS_PER_CALL)
+        cgp = np.zeros((N, 8), np.float16)
+        cgp[:, :3] = cg
+        gW, gB, cdx = orc.mlp_backward(cgp, cin, cacts, cW16, 32, 64, 8, 3)
+        dg = orc.density_grad(ds, cdx)
+        hW, hB, denc = orc.mlp_backward(dg, enc, dacts, dW16, 32, 64, 16, 2)
+        grads = orc.hash_scatter(m["pos"], denc, TBL, L, BASE, GROWTH)
+        bc1, bc2 = orc.adam_bias_corrections(0.9, 0.999, steps + 1)
+        t16 = orc.adam_hash(table, grads, mt, vt, 1e-2, 0.9, 0.999, 1e-8, bc1, bc2, 1 / 128.0, w16_init=t16)
+        for (w, mw, vw), g in zip(state, (hW, hB, gW, gB)):
+            orc.adam_dense(w, g, mw, vw, 1e-2, 0.9, 0.999, 1e-8, bc1, bc2, 1 / 128.0)
+        ray0 += act
+        steps += 1
+        samples += N
     dt = time.perf_counter() - t0
-    return {"value": round(N / dt, 1), "unit": "samples/s", "cores": orc.num_threads(), "kind": "port",
-            "sample": f"one full training step (march, encode, both MLPs fwd/bwd, compositing, gradients, scatter, "
-                      f"Adam over all 16.8 M table entries) on {R} rays = {N} compacted samples of the same scene "
-                      f"and model state, {dt:.2f} s"}
+    return {"value": round(samples / dt, 1), "unit": "samples/s", "cores": orc.num_threads(), "kind": "port",
+            "sample": f"{steps} chained full training steps (march, encode, both MLPs fwd/bwd, compositing, "
+                      f"gradients, scatter, Adam over all 16.8 M table entries) on {ray0} feed rays = "
+                      f"{samples} compacted samples, same scene and model state as the GPU run, {dt:.1f} s"}
 
 
 def heldout_psnr(P, torch, nerf, feed, sp):
@@ -271,10 +285,109 @@ def components(P, torch, stream, sp):
     t_enc = timed(lambda: P.launch("launchHashEncodeKernel", C.byref(opt), d_tab, d_pos, 4, d_enc, BATCH, sp))
     t_sc = timed(lambda: P.launch("launchHashTableBackwardKernel", d_denc, d_pos, d_grads, BATCH, TBL, L,
                                   opt.b, BASE, F, sp))
-    return {"hash_encode_ms_2p18": round(t_enc, 4), "hash_encodes_per_s": round(BATCH / (t_enc * 1e-3), 1),
-            "hash_encode_gbs": round(ENC_BYTES_PER_SAMPLE * BATCH / (t_enc * 1e-3) / 1e9, 1),
-            "hash_scatter_ms_2p18": round(t_sc, 4),
-            "hash_scatter_gbs": round(SCATTER_BYTES_PER_SAMPLE * BATCH / (t_sc * 1e-3) / 1e9, 1)}
+    out = {"hash_encode_ms_2p18": round(t_enc, 4), "hash_encodes_per_s": round(BATCH / (t_enc * 1e-3), 1),
+           "hash_encode_gbs": round(ENC_BYTES_PER_SAMPLE * BATCH / (t_enc * 1e-3) / 1e9, 1),
+           "hash_scatter_ms_2p18": round(t_sc, 4),
+           "hash_scatter_gbs": round(SCATTER_BYTES_PER_SAMPLE * BATCH / (t_sc * 1e-3) / 1e9, 1)}
+    big = 1 << 20  # BASELINE configs[1] at 2^20
+    pos20 = np.zeros((big, 4), np.float32)
+    pos20[:, :3] = rng.random((big, 3), dtype=np.float32)
+    d_pos20 = torch.from_numpy(pos20).to(dev)
+    d_enc20 = torch.empty((big, 2 * L), dtype=torch.float16, device=dev)
+    t_enc20 = timed(lambda: P.launch("launchHashEncodeKernel", C.byref(opt), d_tab, d_pos20, 4, d_enc20, big, sp))
+    out.update({"hash_encode_ms_2p20": round(t_enc20, 4), "hash_encodes_per_s_2p20": round(big / (t_enc20 * 1e-3), 1)})
+    del d_pos20, d_enc20
+
+    # both heads forward + backward at 2^18 (density 32-64-16 on N(0,1) inputs, SH of
+    # directions on the sphere, colour 32-64-64-3 sigmoid, L2 to U[0,1] targets), then Adam over both
+    # heads and the dense T = 2^19 table gradient of the scatter above.
+    dn = P.Net(P.MLPOption(inputDim=32, hiddenDim=64, outputDim=16, numLayers=2, activationType=0,
+                           outputActivation=0), BATCH)
+    cn = P.Net(P.MLPOption(inputDim=32, hiddenDim=64, outputDim=3, numLayers=3, activationType=0,
+                           outputActivation=1), BATCH)
+    x = torch.from_numpy(rng.normal(0, 1, (BATCH, 32)).astype(np.float16)).to(dev)
+    dirs = rng.normal(size=(BATCH, 3)).astype(np.float32)
+    dirs /= np.linalg.norm(dirs, axis=1, keepdims=True)
+    d_dirs = torch.from_numpy(dirs).to(dev)
+    ridx = torch.arange(BATCH, dtype=torch.int32, device=dev)
+    tgt = torch.from_numpy(rng.random((BATCH, 3)).astype(np.float16)).to(dev)
+    dout = torch.empty((BATCH, 16), device=dev)
+    cin = torch.empty((BATCH, 32), dtype=torch.float16, device=dev)
+    sig = torch.empty(BATCH, device=dev)
+    cout = torch.empty((BATCH, 3), device=dev)
+    cdx = torch.empty((BATCH, 32), dtype=torch.float16, device=dev)
+    zero_ds = torch.zeros(BATCH, device=dev)
+    dgrad = torch.empty((BATCH, 16), dtype=torch.float16, device=dev)
+
+    def mlp_step():
+        dn.zero_grad(sp)
+        cn.zero_grad(sp)
+        dn.forward(x, dout, BATCH, sp)
+        P.launch("launchComputeSHGather", d_dirs, ridx, 0, BATCH, 0.0, dout, cin, sig, sp)
+        cn.forward(cin, cout, BATCH, sp)
+        cn.calculate_loss_and_grad(tgt, BATCH, 128.0, False, sp)
+        cn.backward(BATCH, None, cdx, sp)
+        P.launch("launchComputeDensityGrad", BATCH, zero_ds, cdx, dgrad, sp)
+        dn.backward(BATCH, dgrad, None, sp)
+
+    t_mlp = timed(mlp_step)
+    flops = MLP_FLOP_PER_SAMPLE * BATCH
+    out.update({"mlp_fwd_bwd_ms_2p18": round(t_mlp, 4),
+                "mlp_tflops": round(flops / (t_mlp * 1e-3) / 1e12, 2),
+                "mlp_mfma_util": round(flops / (t_mlp * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 5)})
+    # Adam over both heads and the dense table gradient (a fresh copy per launch: consumed grads are cleared)
+    n_tab = L * TBL * F
+    master = torch.from_numpy(rng.uniform(-1e-4, 1e-4, n_tab).astype(np.float32)).to(dev)
+    mm, vv = torch.zeros(n_tab, device=dev), torch.zeros(n_tab, device=dev)
+    reps = 5
+    gcopies = [d_grads.clone() for _ in range(reps + 1)]
+    it = iter(range(reps + 1))
+
+    def adam_all():
+        k = next(it)
+        P.launch("launchAdamHashGridOptim", C.byref(opt), master, d_tab, gcopies[k], mm, vv, 1e-2, 0.9, 0.99,
+                 1e-15, 0.1, 0.01, 1.0 / 128.0, sp)
+        dn.step(1e-2, 0.9, 0.99, 1e-15, 128.0, sp)
+        cn.step(1e-2, 0.9, 0.99, 1e-15, 128.0, sp)
+
+    t_adam = timed(adam_all, reps=reps)
+    out.update({"adam_all_params_ms": round(t_adam, 4),
+                "adam_gbs": round(ADAM_BYTES_PER_PARAM * n_tab / (t_adam * 1e-3) / 1e9, 1)})
+    del gcopies, master, mm, vv
+    dn.close()
+    cn.close()
+
+    # DDA march + compaction of 2^18 camera rays over the C4 grid (processRaysHitLinear,
+    # one host read per call), batch 2^18 samples
+    scenes = importlib.import_module("3dmaker_amd.scenes")
+    bits = scenes.occupancy_c4(128, 5, 4, 0.1, 0.3, 1.5, seed=0)
+    o4, d4 = scenes.rays_c4(1 << 18, n_cams=100, seed=1)
+    R4 = o4.shape[0]
+    t_o, t_d = torch.from_numpy(o4).to(dev), torch.from_numpy(d4).to(dev)
+    t_bits = torch.from_numpy(bits).to(dev)
+    di = torch.empty((R4, 3), device=dev)
+    nr, fr = torch.empty(R4, device=dev), torch.empty(R4, device=dev)
+    cnt = torch.empty(R4, dtype=torch.int32, device=dev)
+    offs = torch.empty(R4, dtype=torch.int32, device=dev)
+    posb = torch.empty((BATCH, 4), device=dev)
+    rib = torch.empty(BATCH, dtype=torch.int32, device=dev)
+    tsb = torch.empty(BATCH, device=dev)
+    act = torch.empty(1, dtype=torch.int32, device=dev)
+    total = C.c_uint32(0)
+    mn3, mx3 = P.Float3(-1.5, -1.5, -1.5), P.Float3(1.5, 1.5, 1.5)
+
+    def march():
+        P.launch("launchComputeRayAabbInv", R4, t_o, t_d, mn3, mx3, 5, di, nr, fr, sp)
+        P.lib().processRaysHitLinear(R4, t_o.data_ptr(), t_d.data_ptr(), di.data_ptr(), nr.data_ptr(), fr.data_ptr(),
+                                     t_bits.data_ptr(), P.Uint3(128, 128, 128), mn3, mx3, 5, 4, 1, BATCH,
+                                     C.byref(total), act.data_ptr(), cnt.data_ptr(), offs.data_ptr(),
+                                     posb.data_ptr(), rib.data_ptr(), tsb.data_ptr(), None, sp)
+        P.check()
+
+    t_march = timed(march)
+    out.update({"march_compact_ms_2p18_rays": round(t_march, 4), "march_rays_per_s": round(R4 / (t_march * 1e-3), 1),
+                "march_samples": int(total.value)})
+    return out
 
 
 def main():
@@ -370,7 +483,7 @@ def main():
         "data": "synthetic",
         "config": {"workload": "InstantNerf.trainWithRaysHit on the procedural 3-sphere scene (BASELINE configs[4])",
                    "batch_samples": BATCH, "rays_per_call": RAYS_PER_CALL, "mean_samples_per_step": round(samples / steps, 1),
-                   "grid": "128^3 x 5 cascades x 4 mips", "table_size": TBL, "levels": L, "density": "32-64-16",
+                   "grid": "128^3 x 1 cascade x 4 mips", "table_size": TBL, "levels": L, "density": "32-64-16",
                    "color": "32-64-64-3", "lambda_dist": 0.1, "loss_scale": 128.0, "occupancy_refresh": 16,
                    "feed": "100 RGBA8 800x800 views in HBM, pcg_hash draws, random background per call"},
         "stage_ms": stage_ms,
@@ -390,11 +503,14 @@ def main():
         del hfeed, himgs
     out["components"] = components(P, torch, stream, sp)
     if not args.no_cpu:
-        feed.fetch(0, RAYS_PER_CALL, 12345, (1.0, 1.0, 1.0), sp)
-        torch.cuda.synchronize()
+        chunks = []
+        for k in range(CPU_FEED_CHUNKS):
+            feed.fetch(k * RAYS_PER_CALL, RAYS_PER_CALL, 12345, (1.0, 1.0, 1.0), sp)
+            torch.cuda.synchronize()
+            chunks.append((feed.o.cpu().numpy(), feed.d.cpu().numpy(), feed.rgb.cpu().numpy()))
         nerf.set_bg_color(1.0, 1.0, 1.0)
-        out["cpu_baseline"] = cpu_baseline(P, nerf, feed.o.cpu().numpy(), feed.d.cpu().numpy(),
-                                           feed.rgb.cpu().numpy())
+        o_h, d_h, g_h = (np.concatenate(c) for c in zip(*chunks))
+        out["cpu_baseline"] = cpu_baseline(P, nerf, o_h, d_h, g_h)
     print(json.dumps(out))
 
 

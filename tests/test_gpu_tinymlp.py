@@ -281,7 +281,8 @@ def test_adam_hash_100_steps_bit_exact(dev):
 
 @pytest.mark.parametrize("inD,hid,outD,nl,act,N", [(32, 64, 3, 3, 1, 4096), (32, 32, 3, 3, 1, 999),
                                                    (64, 64, 64, 2, 0, 2048), (16, 128, 16, 2, 0, 1024),
-                                                   (3, 16, 8, 4, 0, 333)])
+                                                   (3, 16, 8, 4, 0, 333), (32, 64, 3, 3, 1, 1 << 18),
+                                                   (32, 64, 16, 2, 0, 1 << 18)])
 def test_net_forward_backward(dev, inD, hid, outD, nl, act, N):
     """TinyMLP (color head and benchmark shapes): forward, MSE/sigmoid', backward with dX."""
     print(f"[net] in={inD} hid={hid} out={outD} layers={nl} act={act} N={N}", flush=True)
