@@ -88,12 +88,14 @@ def parse():
                     help="run --warmup steps, then this many, and exit (for rocprofv3)")
     ap.add_argument("--psnr-steps", type=int, default=ANNEAL,
                     help="train (untimed) up to this many steps, then report PSNR on 12 held-out views (-1: skip)")
+    ap.add_argument("--cascades", type=int, default=1,
+                    help="occupancy cascades of the end-to-end run (1: the reference loader's choice for an orbit)")
     ap.add_argument("--components", action="store_true",
                     help="only time the stand-alone encode / scatter launches at 2^18 and exit")
     return ap.parse_args()
 
 
-def options(P):
+def options(P, cascades=1):
     o = P.Nerf.default_options()
     o.gridResolution[:] = [128, 128, 128]
     o.aabbMin[:] = [-1.5] * 3
@@ -101,7 +103,7 @@ def options(P):
     # One cascade: INerfTrainer takes the loader's estimate (NerfTrainer.cu:113-114), and the loader's pose
     # heuristic gives 1 for cameras orbiting the scene, as here (DataLoader.cu:368-376).  With 5 cascades
     # the far field holds a fog shell whose colour follows the random background of the last ray chunk.
-    o.levelsMipmap, o.numCascades, o.samplesPerVoxel = 4, 1, 1
+    o.levelsMipmap, o.numCascades, o.samplesPerVoxel = 4, cascades, 1
     o.densityHiddenDim, o.densityNumLayers = 64, 2
     o.colorHiddenDim, o.colorNumLayers = 64, 3
     o.hashTableSize, o.numLevels, o.growthFactor, o.baseResolution, o.featuresPerLevel = TBL, L, GROWTH, BASE, F
@@ -413,7 +415,7 @@ def main():
     feed = RayFeed(P, torch, imgs, tf, IMG_W, IMG_H, focal, RAYS_PER_CALL)
     torch.cuda.synchronize()
 
-    nerf = P.Nerf(options(P))
+    nerf = P.Nerf(options(P, args.cascades))
     tr = Trainer(nerf, feed, sp)
     tr.run(args.warmup)
     torch.cuda.synchronize()
@@ -427,7 +429,7 @@ def main():
         for _ in range(3):
             torch.neg(src, out=dst)
         torch.cuda.synchronize()
-        print(json.dumps({"profile_steps": len(hits), "mean_samples": float(np.mean(hits)),
+        print(json.dumps({"profile_steps": len(hits), "total_steps": tr.step, "mean_samples": float(np.mean(hits)),
                           "copy_calibration_bytes": COPY_BYTES}))
         return
 
@@ -483,7 +485,7 @@ def main():
         "data": "synthetic",
         "config": {"workload": "InstantNerf.trainWithRaysHit on the procedural 3-sphere scene (BASELINE configs[4])",
                    "batch_samples": BATCH, "rays_per_call": RAYS_PER_CALL, "mean_samples_per_step": round(samples / steps, 1),
-                   "grid": "128^3 x 1 cascade x 4 mips", "table_size": TBL, "levels": L, "density": "32-64-16",
+                   "grid": f"128^3 x {args.cascades} cascade(s) x 4 mips", "table_size": TBL, "levels": L, "density": "32-64-16",
                    "color": "32-64-64-3", "lambda_dist": 0.1, "loss_scale": 128.0, "occupancy_refresh": 16,
                    "feed": "100 RGBA8 800x800 views in HBM, pcg_hash draws, random background per call"},
         "stage_ms": stage_ms,
