@@ -30,6 +30,67 @@ namespace {
 
 __host__ __device__ inline int tiles16(int d) { return (d + 15) / 16; }
 
+// Stages the fp16 weights of every layer into LDS as MFMA A-operand
+// fragments, one quad of 4 halves per (layer, 16x16 block, lane):
+//   forward     frag(l, mt, ks)[lane][j] = W_l[16 mt + lane%16][16 ks + 4 (lane/16) + j]
+//   transposed fragT(l, mt, ks)[lane][j] = W_l[16 ks + 4 (lane/16) + j][16 mt + lane%16]
+// Blocks are stored mt-major (ks fastest), layer after layer, with zeros
+// outside the matrix.  Every thread issues the global loads of kStageBatch
+// quads before it stores any, so a block waits about one memory latency per
+// batch instead of one per element.  Ends with a barrier.
+constexpr int kStageBatch = 8;
+
+template <bool TRANSPOSED>
+__device__ void stage_fragments(_Float16* __restrict__ sfrag, const _Float16* const* W, int in, int hid, int out,
+                                int layers)
+{
+    __shared__ const _Float16* sW[kMaxLayers];
+    const int tid = threadIdx.x;
+    if (tid < layers) sW[tid] = W[tid];
+    __syncthreads();
+    auto quads = [&](int l) {
+        const int in_l = l == 0 ? in : hid, out_l = l == layers - 1 ? out : hid;
+        return tiles16(out_l) * tiles16(in_l) * 64;
+    };
+    int total = 0;
+    for (int l = 0; l < layers; l++) total += quads(l);
+    for (int base = 0; base < total; base += kStageBatch * (int)blockDim.x) {
+        h4 v[kStageBatch];
+#pragma unroll
+        for (int k = 0; k < kStageBatch; k++) {
+            const int q = base + k * (int)blockDim.x + tid;
+            v[k] = h4zero();
+            if (q >= total) continue;
+            int l = 0, q0 = 0;
+            while (q >= q0 + quads(l)) q0 += quads(l++);
+            const int in_l = l == 0 ? in : hid, out_l = l == layers - 1 ? out : hid;
+            const int f = (q - q0) >> 6, ln = (q - q0) & 63;
+            const _Float16* w = sW[l];
+            // in_l and out_l are multiples of 4: a quad is wholly inside or outside
+            if constexpr (!TRANSPOSED) {
+                const int KS = tiles16(in_l), mt = f / KS, ks = f - mt * KS;
+                const int row = 16 * mt + (ln & 15), col = 16 * ks + 4 * (ln >> 4);
+                if (row < out_l && col < in_l) {
+                    const _Float16* src = w + row * in_l + col;
+                    if ((reinterpret_cast<uintptr_t>(src) & 7u) == 0) v[k] = ld_h4(src);
+                    else v[k] = h4{src[0], src[1], src[2], src[3]};
+                }
+            } else {
+                const int KS = tiles16(out_l), mt = f / KS, ks = f - mt * KS;
+                const int i = 16 * mt + (ln & 15), o = 16 * ks + 4 * (ln >> 4);
+                if (i < in_l && o < out_l)
+                    v[k] = h4{w[o * in_l + i], w[(o + 1) * in_l + i], w[(o + 2) * in_l + i], w[(o + 3) * in_l + i]};
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kStageBatch; k++) {
+            const int q = base + k * (int)blockDim.x + tid;
+            if (q < total) st_h4(sfrag + 4 * q, v[k]);
+        }
+    }
+    __syncthreads();
+}
+
 // ---------------------------------------------------------------------------
 // forward
 // ---------------------------------------------------------------------------
@@ -62,19 +123,9 @@ __global__ __launch_bounds__(256) void mlp_fwd_kernel(const FwdParams p)
     int* sres = reinterpret_cast<int*>(smem + p.meta_base + 4 * kMaxLevels);
     const int tid = threadIdx.x;
 
-    // Stage A-operand fragments: frag(l, mt, ks)[lane][j] = W_l[16mt + lane%16][16ks + 4(lane/16) + j]
     for (int l = 0; l < p.layers; l++) {
-        const int in_l = l == 0 ? p.in : p.hid;
         const int out_l = l == p.layers - 1 ? p.out_dim : p.hid;
-        const int KS = tiles16(in_l), MT = tiles16(out_l);
-        const _Float16* w = p.W[l];
-        for (int e = tid; e < MT * KS * 256; e += blockDim.x) {
-            const int j = e & 3, ln = (e >> 2) & 63, f = e >> 8;
-            const int mt = f / KS, ks = f - mt * KS;
-            const int row = 16 * mt + (ln & 15), col = 16 * ks + 4 * (ln >> 4) + j;
-            sfrag[p.frag_off[l] + e] = (row < out_l && col < in_l) ? w[row * in_l + col] : (_Float16)0.f;
-        }
-        for (int e = tid; e < MT * 16; e += blockDim.x)
+        for (int e = tid; e < tiles16(out_l) * 16; e += blockDim.x)
             sbias[p.bias_off[l] + e] = e < out_l ? p.B[l][e] : 0.f;
     }
     if constexpr (HASH) {
@@ -83,7 +134,7 @@ __global__ __launch_bounds__(256) void mlp_fwd_kernel(const FwdParams p)
             sres[e] = p.res[e];
         }
     }
-    __syncthreads();
+    stage_fragments<false>(sfrag, p.W, p.in, p.hid, p.out_dim, p.layers);
 
     constexpr int NT = MAXD / 16;
     const int lane = tid & 63, wave = tid >> 6, r = lane & 15, g = lane >> 4;
@@ -230,22 +281,10 @@ __global__ __launch_bounds__(256) void mlp_bwd_kernel(const BwdParams p)
     float* sacc = reinterpret_cast<float*>(smem + p.acc_base);
     const int tid = threadIdx.x;
 
-    // Transposed fragments for dX = W^T G: fragT(l, mt, ks)[lane][j] = W_l[16ks + 4(lane/16) + j][16mt + lane%16]
-    for (int l = 0; l < p.layers; l++) {
-        const int in_l = l == 0 ? p.in : p.hid;
-        const int out_l = l == p.layers - 1 ? p.out_dim : p.hid;
-        const int KS = tiles16(out_l), MT = tiles16(in_l);
-        const _Float16* w = p.W[l];
-        for (int e = tid; e < MT * KS * 256; e += blockDim.x) {
-            const int j = e & 3, ln = (e >> 2) & 63, f = e >> 8;
-            const int mt = f / KS, ks = f - mt * KS;
-            const int o = 16 * ks + 4 * (ln >> 4) + j, i = 16 * mt + (ln & 15);
-            sfrag[p.fragT_off[l] + e] = (o < out_l && i < in_l) ? w[o * in_l + i] : (_Float16)0.f;
-        }
-    }
+    // Transposed fragments for dX = W^T G
     if constexpr (LMAX == 0)
         for (int e = tid; e < p.P; e += blockDim.x) sacc[e] = 0.f;
-    __syncthreads();
+    stage_fragments<true>(sfrag, p.W, p.in, p.hid, p.out_dim, p.layers);
 
     constexpr int NT = MAXD / 16;
     constexpr int TPW = kBwdTilesPerWave;
@@ -504,19 +543,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
     const int tid = threadIdx.x;
 
     // Transposed fragments for dX = W^T G (as mlp_bwd_kernel).
-#pragma unroll
-    for (int l = 0; l < LAYERS; l++) {
-        const int in_l = S::in_l(l), out_l = S::out_l(l);
-        const int KS = S::ob(l), MT = S::ib(l);
-        const _Float16* w = p.W[l];
-        for (int e = tid; e < MT * KS * 256; e += blockDim.x) {
-            const int j = e & 3, ln = (e >> 2) & 63, f = e >> 8;
-            const int mt = f / KS, ks = f - mt * KS;
-            const int o = 16 * ks + 4 * (ln >> 4) + j, i = 16 * mt + (ln & 15);
-            sfrag[p.fragT_off[l] + e] = (o < out_l && i < in_l) ? w[o * in_l + i] : (_Float16)0.f;
-        }
-    }
-    __syncthreads();
+    stage_fragments<true>(sfrag, p.W, IN, HID, OUT, LAYERS);
 
     const int lane = tid & 63, wave = tid >> 6, g = lane >> 4, r = lane & 15;
     const int N = p.d_n ? min((int)*p.d_n, p.N) : p.N;
