@@ -384,23 +384,31 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
             GRAFT_HIP_CHECK(hipEventRecord(b.ev_join, b.side));
         }
 
-        stage("densityFwd", [&] {
-            graft::FwdInput in;
-            in.pos = reinterpret_cast<const float*>(b.positions);
-            in.pos_stride = 4;
-            in.table = db.fwd_hashtable;
-            in.meta = &b.meta;
-            graft::mlp_forward(dshape, in, db.fwd_weights, db.master_biases, db.activations, b.density_out, (int)Bn,
-                               OUT_ACT_NONE, stream, d_hits);
-        });
-        stage("computeSH", [&] {
-            graft::sh_gather(cd, b.ray_idx, d_hits, Bn, o.densityBias, b.density_out, b.color_in, b.sigma, stream);
-        });
-        stage("colorFwd", [&] {
-            graft::FwdInput in;
-            in.x = b.color_in;
-            graft::mlp_forward(cshape, in, cb.fwd_weights, cb.master_biases, cb.activations, cb.padded_outputs,
-                               (int)Bn, cb.hw.outputActivation, stream, d_hits);
+        // hash encode + density head, SH gather (into the colour head's
+        // activation 0), colour head: one launch, activations saved
+        stage("forward", [&] {
+            graft::NerfFwdArgs fa;
+            fa.dshape = dshape;
+            fa.pos = reinterpret_cast<const float*>(b.positions);
+            fa.pos_stride = 4;
+            fa.table = db.fwd_hashtable;
+            fa.meta = &b.meta;
+            fa.dW = db.fwd_weights;
+            fa.dB = db.master_biases;
+            fa.dacts = db.activations;
+            fa.density_out = b.density_out;
+            fa.dirs = cd;
+            fa.ray_idx = b.ray_idx;
+            fa.density_bias = o.densityBias;
+            fa.sigma = b.sigma;
+            fa.cshape = cshape;
+            fa.out_act = cb.hw.outputActivation;
+            fa.cW = cb.fwd_weights;
+            fa.cB = cb.master_biases;
+            fa.cacts = cb.activations;
+            fa.color_in = b.color_in;
+            fa.color_out = cb.padded_outputs;
+            graft::nerf_forward(fa, (int)Bn, stream, d_hits);
         });
 
         float* final_rgb = d_rgb_out ? d_rgb_out + (size_t)raysDone * 3 : b.render_rgb;
@@ -707,19 +715,24 @@ void InstantNerf::renderImageHit(const float3* d_rays_o, const float3* d_rays_d,
                                         graft::MarchScratch{b.block_sums, b.result}, stream);
             GRAFT_HIP_CHECK(hipMemcpyAsync(b.h_result, b.result, 2 * sizeof(uint32_t), hipMemcpyDeviceToHost, stream));
             GRAFT_HIP_CHECK(hipEventRecord(b.ev_result, stream));
-            graft::FwdInput din;
-            din.pos = reinterpret_cast<const float*>(b.render.positions);
-            din.pos_stride = 4;
-            din.table = db.fwd_hashtable;
-            din.meta = &b.meta;
-            graft::mlp_forward(dshape, din, db.fwd_weights, db.master_biases, nullptr, b.render.density_out,
-                               (int)hitBatch, OUT_ACT_NONE, stream, d_hits);
-            graft::sh_gather(cd + done, b.render.ray_idx, d_hits, hitBatch, o.densityBias, b.render.density_out,
-                             b.render.color_in, b.render.sigma, stream);
-            graft::FwdInput cin;
-            cin.x = b.render.color_in;
-            graft::mlp_forward(cshape, cin, cb.fwd_weights, cb.master_biases, nullptr, b.render.rgb, (int)hitBatch,
-                               cb.hw.outputActivation, stream, d_hits);
+            graft::NerfFwdArgs fa;
+            fa.dshape = dshape;
+            fa.pos = reinterpret_cast<const float*>(b.render.positions);
+            fa.pos_stride = 4;
+            fa.table = db.fwd_hashtable;
+            fa.meta = &b.meta;
+            fa.dW = db.fwd_weights;
+            fa.dB = db.master_biases;
+            fa.dirs = cd + done;
+            fa.ray_idx = b.render.ray_idx;
+            fa.density_bias = o.densityBias;
+            fa.sigma = b.render.sigma;
+            fa.cshape = cshape;
+            fa.out_act = cb.hw.outputActivation;
+            fa.cW = cb.fwd_weights;
+            fa.cB = cb.master_biases;
+            fa.color_out = b.render.rgb;
+            graft::nerf_forward(fa, (int)hitBatch, stream, d_hits);
             graft::CompositeArgs ca{};
             ca.offsets = b.offsets;
             ca.counts = b.counts + done;

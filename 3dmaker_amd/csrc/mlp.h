@@ -42,4 +42,32 @@ void mlp_backward(const MlpShape& s, const __half* dy, const __half* const* acts
                   const __half* const* W, float* const* dW, float* const* dB, __half* dx, int N,
                   hipStream_t stream, const uint32_t* d_n = nullptr, bool accumulate = true);
 
+// The forward of a NeRF step (hash encode + density head, SH gather, colour
+// head) in one launch; bitwise equal to mlp_forward(density), sh_gather,
+// mlp_forward(colour).  dacts / density_out / cacts / color_in may be null
+// (inference); sigma and color_out are always written.
+struct NerfFwdArgs {
+    MlpShape dshape;                 // density head, out == 16
+    const float* pos = nullptr;      // [N x pos_stride] contracted positions
+    int pos_stride = 4;
+    const __half* table = nullptr;   // fp16 hash table [L][T][2]
+    const GridMeta* meta = nullptr;
+    const __half* const* dW = nullptr;
+    const float* const* dB = nullptr;
+    __half* const* dacts = nullptr;  // device array: encodings, hidden activations
+    float* density_out = nullptr;    // [N x 16]
+    const float3* dirs = nullptr;    // per ray
+    const uint32_t* ray_idx = nullptr;
+    float density_bias = 0.0f;
+    float* sigma = nullptr;          // [N]
+    MlpShape cshape;                 // colour head, in == 32
+    int out_act = 1;                 // colour output activation (0 none, 1 sigmoid)
+    const __half* const* cW = nullptr;
+    const float* const* cB = nullptr;
+    __half* const* cacts = nullptr;  // device array; entries 1.. receive the hidden activations
+    __half* color_in = nullptr;      // [N x 32] logits | SH (the colour head's activation 0)
+    float* color_out = nullptr;      // [N x cshape.out]
+};
+void nerf_forward(const NerfFwdArgs& a, int N, hipStream_t stream, const uint32_t* d_n = nullptr);
+
 }  // namespace graft

@@ -20,6 +20,7 @@
 #include "mlp.h"
 
 #include "hash_encode.h"
+#include "mlp_device.h"
 
 #include <algorithm>
 #include <vector>
@@ -27,69 +28,6 @@
 namespace graft {
 
 namespace {
-
-__host__ __device__ inline int tiles16(int d) { return (d + 15) / 16; }
-
-// Stages the fp16 weights of every layer into LDS as MFMA A-operand
-// fragments, one quad of 4 halves per (layer, 16x16 block, lane):
-//   forward     frag(l, mt, ks)[lane][j] = W_l[16 mt + lane%16][16 ks + 4 (lane/16) + j]
-//   transposed fragT(l, mt, ks)[lane][j] = W_l[16 ks + 4 (lane/16) + j][16 mt + lane%16]
-// Blocks are stored mt-major (ks fastest), layer after layer, with zeros
-// outside the matrix.  Every thread issues the global loads of kStageBatch
-// quads before it stores any, so a block waits about one memory latency per
-// batch instead of one per element.  Ends with a barrier.
-constexpr int kStageBatch = 8;
-
-template <bool TRANSPOSED>
-__device__ void stage_fragments(_Float16* __restrict__ sfrag, const _Float16* const* W, int in, int hid, int out,
-                                int layers)
-{
-    __shared__ const _Float16* sW[kMaxLayers];
-    const int tid = threadIdx.x;
-    if (tid < layers) sW[tid] = W[tid];
-    __syncthreads();
-    auto quads = [&](int l) {
-        const int in_l = l == 0 ? in : hid, out_l = l == layers - 1 ? out : hid;
-        return tiles16(out_l) * tiles16(in_l) * 64;
-    };
-    int total = 0;
-    for (int l = 0; l < layers; l++) total += quads(l);
-    for (int base = 0; base < total; base += kStageBatch * (int)blockDim.x) {
-        h4 v[kStageBatch];
-#pragma unroll
-        for (int k = 0; k < kStageBatch; k++) {
-            const int q = base + k * (int)blockDim.x + tid;
-            v[k] = h4zero();
-            if (q >= total) continue;
-            int l = 0, q0 = 0;
-            while (q >= q0 + quads(l)) q0 += quads(l++);
-            const int in_l = l == 0 ? in : hid, out_l = l == layers - 1 ? out : hid;
-            const int f = (q - q0) >> 6, ln = (q - q0) & 63;
-            const _Float16* w = sW[l];
-            // in_l and out_l are multiples of 4: a quad is wholly inside or outside
-            if constexpr (!TRANSPOSED) {
-                const int KS = tiles16(in_l), mt = f / KS, ks = f - mt * KS;
-                const int row = 16 * mt + (ln & 15), col = 16 * ks + 4 * (ln >> 4);
-                if (row < out_l && col < in_l) {
-                    const _Float16* src = w + row * in_l + col;
-                    if ((reinterpret_cast<uintptr_t>(src) & 7u) == 0) v[k] = ld_h4(src);
-                    else v[k] = h4{src[0], src[1], src[2], src[3]};
-                }
-            } else {
-                const int KS = tiles16(out_l), mt = f / KS, ks = f - mt * KS;
-                const int i = 16 * mt + (ln & 15), o = 16 * ks + 4 * (ln >> 4);
-                if (i < in_l && o < out_l)
-                    v[k] = h4{w[o * in_l + i], w[(o + 1) * in_l + i], w[(o + 2) * in_l + i], w[(o + 3) * in_l + i]};
-            }
-        }
-#pragma unroll
-        for (int k = 0; k < kStageBatch; k++) {
-            const int q = base + k * (int)blockDim.x + tid;
-            if (q < total) st_h4(sfrag + 4 * q, v[k]);
-        }
-    }
-    __syncthreads();
-}
 
 // ---------------------------------------------------------------------------
 // forward
@@ -123,11 +61,7 @@ __global__ __launch_bounds__(256) void mlp_fwd_kernel(const FwdParams p)
     int* sres = reinterpret_cast<int*>(smem + p.meta_base + 4 * kMaxLevels);
     const int tid = threadIdx.x;
 
-    for (int l = 0; l < p.layers; l++) {
-        const int out_l = l == p.layers - 1 ? p.out_dim : p.hid;
-        for (int e = tid; e < tiles16(out_l) * 16; e += blockDim.x)
-            sbias[p.bias_off[l] + e] = e < out_l ? p.B[l][e] : 0.f;
-    }
+    stage_biases(sbias, p.B, p.bias_off, p.hid, p.out_dim, p.layers);
     if constexpr (HASH) {
         for (int e = tid; e < p.L; e += blockDim.x) {
             sscale[e] = p.scale[e];
@@ -135,13 +69,13 @@ __global__ __launch_bounds__(256) void mlp_fwd_kernel(const FwdParams p)
         }
     }
     stage_fragments<false>(sfrag, p.W, p.in, p.hid, p.out_dim, p.layers);
+    const NetView net{sfrag, sbias, p.frag_off, p.bias_off, p.in, p.hid, p.out_dim, p.layers};
 
     constexpr int NT = MAXD / 16;
     const int lane = tid & 63, wave = tid >> 6, r = lane & 15, g = lane >> 4;
     const int N = p.d_n ? min((int)*p.d_n, p.N) : p.N;
     const int ntiles = (N + 15) >> 4;
     const int KS0 = tiles16(p.in);
-    const uint32_t mask = (uint32_t)p.T - 1u;
     _Float16* act0 = nullptr;
     if constexpr (SAVE) act0 = p.acts[0];
 
@@ -157,27 +91,7 @@ __global__ __launch_bounds__(256) void mlp_fwd_kernel(const FwdParams p)
                 py = pp[1];
                 pz = pp[2];
             }
-#pragma unroll
-            for (int ks = 0; ks < NT; ks++) {
-                X[ks] = h4zero();
-                if (ks < KS0) {
-                    const int la = 8 * ks + 2 * g, lb = la + 1;
-                    float2 ea = make_float2(0.f, 0.f), eb = make_float2(0.f, 0.f);
-                    if (valid && la < p.L)
-                        ea = encode_level(px, py, pz, sscale[la], sres[la], la < p.dense_start, mask,
-                                          p.table + (size_t)la * p.T * 2);
-                    if (valid && lb < p.L)
-                        eb = encode_level(px, py, pz, sscale[lb], sres[lb], lb < p.dense_start, mask,
-                                          p.table + (size_t)lb * p.T * 2);
-                    X[ks] = h4{to_h(ea.x), to_h(ea.y), to_h(eb.x), to_h(eb.y)};
-                    if (SAVE && valid) {
-                        const int col = 16 * ks + 4 * g;
-                        _Float16* dst = act0 + (size_t)n * p.in + col;
-                        if (col + 4 <= p.in) st_h4(dst, X[ks]);
-                        else if (col + 2 <= p.in) *reinterpret_cast<h2*>(dst) = h2{X[ks].x, X[ks].y};
-                    }
-                }
-            }
+            encode_tile<NT>(X, px, py, pz, sscale, sres, p.L, p.T, p.dense_start, p.table, p.in, act0, n, valid, g);
         } else {
 #pragma unroll
             for (int ks = 0; ks < NT; ks++) {
@@ -187,58 +101,16 @@ __global__ __launch_bounds__(256) void mlp_fwd_kernel(const FwdParams p)
                 if (SAVE && in_range && p.save_x0) st_h4(act0 + (size_t)n * p.in + col, X[ks]);
             }
         }
-
-        for (int l = 0; l < p.layers; l++) {
-            const int in_l = l == 0 ? p.in : p.hid;
-            const int out_l = l == p.layers - 1 ? p.out_dim : p.hid;
-            const int KS = tiles16(in_l), MT = tiles16(out_l);
-            const _Float16* fr = sfrag + p.frag_off[l] + lane * 4;
-            const float* bl = sbias + p.bias_off[l];
-            f4 acc[NT];
+        net_tile<NT>(X, net, SAVE ? p.acts : nullptr, n, valid, lane, [&](int mt, f4 y) {
+            if (!valid) return;
 #pragma unroll
-            for (int mt = 0; mt < NT; mt++) {
-                acc[mt] = f4zero();
-                if (mt < MT) {
-#pragma unroll
-                    for (int ks = 0; ks < NT; ks++)
-                        if (ks < KS)
-                            acc[mt] = mfma16(*reinterpret_cast<const h4*>(fr + (mt * KS + ks) * 256), X[ks], acc[mt]);
-                }
+            for (int j = 0; j < 4; j++) {
+                const int col = 16 * mt + 4 * g + j;
+                float v = y[j];
+                if (OUT_ACT == 1) v = 1.0f / (1.0f + expf(-v));
+                if (col < p.out_dim) p.out[(size_t)n * p.out_dim + col] = v;
             }
-            if (l < p.layers - 1) {
-                _Float16* act = nullptr;
-                if constexpr (SAVE) act = p.acts[l + 1];
-#pragma unroll
-                for (int mt = 0; mt < NT; mt++) {
-                    h4 h = h4zero();
-                    if (mt < MT) {
-                        const f4 bv = *reinterpret_cast<const f4*>(bl + 16 * mt + 4 * g);
-#pragma unroll
-                        for (int j = 0; j < 4; j++) {
-                            const float v = acc[mt][j] + bv[j];
-                            h[j] = to_h(v > 0.f ? v : 0.f);
-                        }
-                        const int col = 16 * mt + 4 * g;
-                        if (SAVE && valid && col < out_l) st_h4(act + (size_t)n * out_l + col, h);
-                    }
-                    X[mt] = h;
-                }
-            } else {
-#pragma unroll
-                for (int mt = 0; mt < NT; mt++) {
-                    if (mt < MT && valid) {
-                        const f4 bv = *reinterpret_cast<const f4*>(bl + 16 * mt + 4 * g);
-#pragma unroll
-                        for (int j = 0; j < 4; j++) {
-                            const int col = 16 * mt + 4 * g + j;
-                            float v = acc[mt][j] + bv[j];
-                            if (OUT_ACT == 1) v = 1.0f / (1.0f + expf(-v));
-                            if (col < out_l) p.out[(size_t)n * out_l + col] = v;
-                        }
-                    }
-                }
-            }
-        }
+        });
     }
 }
 

@@ -1,0 +1,229 @@
+// The forward half of a NeRF step in one kernel: hash encode + density MLP,
+// SH gather, colour MLP, per 16-sample tile in registers.
+//
+// The reference runs it as three launches with two HBM round trips
+// (networkFusionHashtable.cu:441-682, compute_SH_gather otherKernels.cu:
+// 156-273, networkFusion.cu:197-355).  Here the density head's output block,
+// already in the MFMA D layout that is the colour head's B layout for input
+// features 0..15, is sanitised and rounded to fp16 in place; each lane adds
+// the 4 SH coefficients of its sample it holds as features 16..31.  Every
+// value is produced by the same fp32 operations in the same order as the
+// three-launch chain, so the outputs are bitwise those of that chain.  The
+// saved buffers (density output, sigma, both heads' activations) are the
+// ones the backward reads; an inference caller passes nulls and keeps only
+// sigma and the colour output.
+#include "mlp_device.h"
+#include "nerf.h"
+
+#include <algorithm>
+
+namespace graft {
+
+namespace {
+
+struct NerfFwdParams {
+    const float* pos;
+    const _Float16* table;
+    const _Float16* const* dW;
+    const float* const* dB;
+    _Float16* const* dacts;   // nullable
+    float* dout;              // nullable [N x 16]
+    const float3* dirs;
+    const uint32_t* ray_idx;
+    float* sigma;             // [N]
+    const _Float16* const* cW;
+    const float* const* cB;
+    _Float16* const* cacts;   // nullable (hidden activations of the colour head)
+    _Float16* cin;            // nullable [N x 32]
+    float* cout;              // [N x c_out]
+    const uint32_t* d_n;
+    float density_bias;
+    int N, pos_stride;
+    int L, T, dense_start;
+    int d_in, d_hid, d_layers;
+    int c_hid, c_out, c_layers;
+    int d_frag_off[kMaxLayers], d_bias_off[kMaxLayers];
+    int c_frag_off[kMaxLayers], c_bias_off[kMaxLayers];
+    int c_frag_base, d_bias_base, c_bias_base, meta_base;  // LDS byte offsets
+    float scale[kMaxLevels];
+    int res[kMaxLevels];
+};
+
+template <int NT, int OUT_ACT>
+__global__ __launch_bounds__(256) void nerf_fwd_kernel(const NerfFwdParams p)
+{
+    extern __shared__ __align__(16) unsigned char smem[];
+    _Float16* dfrag = reinterpret_cast<_Float16*>(smem);
+    _Float16* cfrag = reinterpret_cast<_Float16*>(smem + p.c_frag_base);
+    float* dbias = reinterpret_cast<float*>(smem + p.d_bias_base);
+    float* cbias = reinterpret_cast<float*>(smem + p.c_bias_base);
+    float* sscale = reinterpret_cast<float*>(smem + p.meta_base);
+    int* sres = reinterpret_cast<int*>(smem + p.meta_base + 4 * kMaxLevels);
+    const int tid = threadIdx.x;
+
+    stage_biases(dbias, p.dB, p.d_bias_off, p.d_hid, 16, p.d_layers);
+    stage_biases(cbias, p.cB, p.c_bias_off, p.c_hid, p.c_out, p.c_layers);
+    for (int e = tid; e < p.L; e += blockDim.x) {
+        sscale[e] = p.scale[e];
+        sres[e] = p.res[e];
+    }
+    stage_fragments<false>(dfrag, p.dW, p.d_in, p.d_hid, 16, p.d_layers);
+    stage_fragments<false>(cfrag, p.cW, 32, p.c_hid, p.c_out, p.c_layers);
+    const NetView dnet{dfrag, dbias, p.d_frag_off, p.d_bias_off, p.d_in, p.d_hid, 16, p.d_layers};
+    const NetView cnet{cfrag, cbias, p.c_frag_off, p.c_bias_off, 32, p.c_hid, p.c_out, p.c_layers};
+
+    const int lane = tid & 63, wave = tid >> 6, r = lane & 15, g = lane >> 4;
+    const int N = p.d_n ? min((int)*p.d_n, p.N) : p.N;
+    const int ntiles = (N + 15) >> 4;
+    _Float16* act0 = p.dacts != nullptr ? p.dacts[0] : nullptr;
+
+    for (int tile = blockIdx.x * 4 + wave; tile < ntiles; tile += gridDim.x * 4) {
+        const int n = tile * 16 + r;
+        const bool valid = n < N;
+        float px = 0.f, py = 0.f, pz = 0.f;
+        float3 dir = make_float3(0.f, 0.f, 0.f);
+        if (valid) {
+            const float* pp = p.pos + (size_t)n * p.pos_stride;
+            px = pp[0];
+            py = pp[1];
+            pz = pp[2];
+            dir = p.dirs[p.ray_idx[n]];
+        }
+        h4 X[NT];
+        encode_tile<NT>(X, px, py, pz, sscale, sres, p.L, p.T, p.dense_start, p.table, p.d_in, act0, n, valid, g);
+
+        // density head -> colour input features 0..15 (sanitised logits), sigma
+        h4 C[NT];
+#pragma unroll
+        for (int k = 0; k < NT; k++) C[k] = h4zero();
+        net_tile<NT>(X, dnet, p.dacts, n, valid, lane, [&](int mt, f4 y) {
+            if (mt != 0) return;
+            if (valid && p.dout != nullptr) *reinterpret_cast<f4*>(p.dout + (size_t)n * 16 + 4 * g) = y;
+            float lg[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) lg[j] = sanitize_logit(y[j]);
+            C[0] = h4{to_h(lg[0]), to_h(lg[1]), to_h(lg[2]), to_h(lg[3])};
+            if (valid && g == 0) p.sigma[n] = nerf_expf(fminf(lg[0] - p.density_bias, 8.0f));
+        });
+        // features 16..31: SH coefficients 4 g .. 4 g + 3 of this lane's sample
+        {
+            float sh[16];
+            sh_basis16(dir.x, dir.y, dir.z, sh);
+            h4 s;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float v = g == 0 ? sh[j] : g == 1 ? sh[4 + j] : g == 2 ? sh[8 + j] : sh[12 + j];
+                s[j] = to_h(v);
+            }
+            if constexpr (NT > 1) C[1] = s;
+        }
+        if (valid && p.cin != nullptr) {
+            st_h4(p.cin + (size_t)n * 32 + 4 * g, C[0]);
+            if constexpr (NT > 1) st_h4(p.cin + (size_t)n * 32 + 16 + 4 * g, C[1]);
+        }
+
+        // colour head
+        net_tile<NT>(C, cnet, p.cacts, n, valid, lane, [&](int mt, f4 y) {
+            const int col = 16 * mt + 4 * g;
+            if (!valid || col >= p.c_out) return;
+            f4 v = y;
+            if (OUT_ACT == 1) {
+#pragma unroll
+                for (int j = 0; j < 4; j++) v[j] = 1.0f / (1.0f + expf(-v[j]));
+            }
+            *reinterpret_cast<f4*>(p.cout + (size_t)n * p.c_out + col) = v;
+        });
+    }
+}
+
+int pick_nt(int d)
+{
+    if (d <= 32) return 2;  // the colour input alone is 32 wide
+    if (d <= 64) return 4;
+    return 8;
+}
+
+}  // namespace
+
+void nerf_forward(const NerfFwdArgs& a, int N, hipStream_t stream, const uint32_t* d_n)
+{
+    a.dshape.validate();
+    a.cshape.validate();
+    if (N <= 0) return;
+    if (a.dshape.out != 16) throw std::runtime_error("NeRF forward: the density head must have 16 outputs");
+    if (a.cshape.in != 32) throw std::runtime_error("NeRF forward: the colour head must take 32 inputs");
+    if (a.out_act != 0 && a.out_act != 1) throw std::runtime_error("NeRF forward: unsupported output activation");
+    if (a.pos_stride < 3) throw std::runtime_error("NeRF forward: position stride must be >= 3");
+    const GridMeta& m = *a.meta;
+    if (2 * m.numLevels != a.dshape.in) throw std::runtime_error("NeRF forward: density input must be 2 * numLevels");
+
+    NerfFwdParams p{};
+    p.pos = a.pos;
+    p.pos_stride = a.pos_stride;
+    p.table = reinterpret_cast<const _Float16*>(a.table);
+    p.dW = reinterpret_cast<const _Float16* const*>(a.dW);
+    p.dB = a.dB;
+    p.dacts = reinterpret_cast<_Float16* const*>(a.dacts);
+    p.dout = a.density_out;
+    p.dirs = a.dirs;
+    p.ray_idx = a.ray_idx;
+    p.sigma = a.sigma;
+    p.density_bias = a.density_bias;
+    p.cW = reinterpret_cast<const _Float16* const*>(a.cW);
+    p.cB = a.cB;
+    p.cacts = reinterpret_cast<_Float16* const*>(a.cacts);
+    p.cin = reinterpret_cast<_Float16*>(a.color_in);
+    p.cout = a.color_out;
+    p.d_n = d_n;
+    p.N = N;
+    p.L = m.numLevels;
+    p.T = m.tableSize;
+    p.dense_start = m.denseLevelStart;
+    for (int l = 0; l < m.numLevels; l++) {
+        p.scale[l] = m.scale[l];
+        p.res[l] = m.res[l];
+    }
+    p.d_in = a.dshape.in;
+    p.d_hid = a.dshape.hid;
+    p.d_layers = a.dshape.layers;
+    p.c_hid = a.cshape.hid;
+    p.c_out = a.cshape.out;
+    p.c_layers = a.cshape.layers;
+
+    auto offsets = [](const MlpShape& s, int* frag_off, int* bias_off, int& halves, int& floats) {
+        halves = floats = 0;
+        for (int l = 0; l < s.layers; l++) {
+            frag_off[l] = halves;
+            bias_off[l] = floats;
+            halves += tiles16(s.out_l(l)) * tiles16(s.in_l(l)) * 256;
+            floats += tiles16(s.out_l(l)) * 16;
+        }
+    };
+    int dh = 0, df = 0, ch = 0, cf = 0;
+    offsets(a.dshape, p.d_frag_off, p.d_bias_off, dh, df);
+    offsets(a.cshape, p.c_frag_off, p.c_bias_off, ch, cf);
+    p.c_frag_base = (dh * 2 + 15) & ~15;
+    p.d_bias_base = (p.c_frag_base + ch * 2 + 15) & ~15;
+    p.c_bias_base = (p.d_bias_base + df * 4 + 15) & ~15;
+    p.meta_base = (p.c_bias_base + cf * 4 + 15) & ~15;
+    const int lds = p.meta_base + 8 * kMaxLevels;
+    if (lds > max_lds_per_block()) throw std::runtime_error("NeRF forward: networks too large for the LDS budget");
+
+    const int ntiles = (N + 15) / 16;
+    const int blocks = std::max(1, std::min((ntiles + 3) / 4, num_cus() * 8));
+    const int nt = pick_nt(std::max(a.dshape.maxd(), a.cshape.maxd()));
+#define GRAFT_NERF_FWD(NTV)                                                                                   \
+    do {                                                                                                      \
+        if (a.out_act == 1) hipLaunchKernelGGL((nerf_fwd_kernel<NTV, 1>), dim3(blocks), dim3(256), lds, stream, p); \
+        else hipLaunchKernelGGL((nerf_fwd_kernel<NTV, 0>), dim3(blocks), dim3(256), lds, stream, p);         \
+    } while (0)
+    switch (nt) {
+        case 2: GRAFT_NERF_FWD(2); break;
+        case 4: GRAFT_NERF_FWD(4); break;
+        default: GRAFT_NERF_FWD(8); break;
+    }
+#undef GRAFT_NERF_FWD
+    GRAFT_LAUNCH_CHECK();
+}
+
+}  // namespace graft

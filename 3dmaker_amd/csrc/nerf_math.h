@@ -86,4 +86,36 @@ __host__ __device__ __forceinline__ uint32_t mip_offset(uint3 res, int level)
 
 __host__ __device__ __forceinline__ float clamp_half_range(float v) { return fmaxf(-65504.0f, fminf(65504.0f, v)); }
 
+// Density logit as the colour head sees it (otherKernels.cu:208-211): clamped
+// to [-64, 64], NaN -> 0.
+__host__ __device__ __forceinline__ float sanitize_logit(float v)
+{
+    v = fmaxf(-64.0f, fminf(64.0f, v));
+    return (v != v) ? 0.0f : v;
+}
+
+// Real spherical harmonics of degree <= 3 at a unit direction, with the
+// published constants (Sloan, "Stupid Spherical Harmonics Tricks") in the
+// reference's sign convention and order (otherKernels.cu:182-200).
+__host__ __device__ __forceinline__ void sh_basis16(float x, float y, float z, float (&sh)[16])
+{
+    const float x2 = x * x, y2 = y * y, z2 = z * z;
+    sh[0] = 0.28209479f;
+    sh[1] = -0.48860251f * y;
+    sh[2] = 0.48860251f * z;
+    sh[3] = -0.48860251f * x;
+    sh[4] = 1.09254843f * x * y;
+    sh[5] = -1.09254843f * y * z;
+    sh[6] = 0.31539156f * (3.0f * z2 - 1.0f);
+    sh[7] = -1.09254843f * x * z;
+    sh[8] = 0.54627421f * (x2 - y2);
+    sh[9] = -0.59004359f * y * (3.0f * x2 - y2);
+    sh[10] = 2.89061144f * x * y * z;
+    sh[11] = -0.45704580f * y * (5.0f * z2 - 1.0f);
+    sh[12] = 0.37317633f * z * (5.0f * z2 - 3.0f);
+    sh[13] = -0.45704580f * x * (5.0f * z2 - 1.0f);
+    sh[14] = 1.44530572f * z * (x2 - y2);
+    sh[15] = -0.59004359f * x * (x2 - 3.0f * y2);
+}
+
 }  // namespace graft

@@ -27,11 +27,6 @@ __device__ __forceinline__ uint32_t dev_count(const uint32_t* d_n, uint32_t n_ma
     return d_n ? min(*d_n, n_max) : n_max;
 }
 
-__device__ __forceinline__ float sanitize_logit(float v)
-{
-    v = fmaxf(-64.0f, fminf(64.0f, v));
-    return (v != v) ? 0.0f : v;
-}
 
 // One sample per thread: 64 B of density logits in, 64 B of fp16 color input
 // and the sigma out, all as 16-byte vectors.
@@ -45,25 +40,8 @@ __global__ __launch_bounds__(256) void sh_gather_kernel(const float3* __restrict
     const uint32_t n = blockIdx.x * blockDim.x + threadIdx.x;
     if (n >= N) return;
     const float3 d = dirs[ray_idx[n]];
-    const float x = d.x, y = d.y, z = d.z;
-    const float x2 = x * x, y2 = y * y, z2 = z * z;
     float sh[16];
-    sh[0] = 0.28209479f;
-    sh[1] = -0.48860251f * y;
-    sh[2] = 0.48860251f * z;
-    sh[3] = -0.48860251f * x;
-    sh[4] = 1.09254843f * x * y;
-    sh[5] = -1.09254843f * y * z;
-    sh[6] = 0.31539156f * (3.0f * z2 - 1.0f);
-    sh[7] = -1.09254843f * x * z;
-    sh[8] = 0.54627421f * (x2 - y2);
-    sh[9] = -0.59004359f * y * (3.0f * x2 - y2);
-    sh[10] = 2.89061144f * x * y * z;
-    sh[11] = -0.45704580f * y * (5.0f * z2 - 1.0f);
-    sh[12] = 0.37317633f * z * (5.0f * z2 - 3.0f);
-    sh[13] = -0.45704580f * x * (5.0f * z2 - 1.0f);
-    sh[14] = 1.44530572f * z * (x2 - y2);
-    sh[15] = -0.59004359f * x * (x2 - 3.0f * y2);
+    sh_basis16(d.x, d.y, d.z, sh);
     const f4* src = reinterpret_cast<const f4*>(dout + 16 * (size_t)n);
     float lg[16];
 #pragma unroll

@@ -457,7 +457,7 @@ def main():
     # roofline of the dominant kernel of the step (per-call averages of the profiled window)
     candidates = {
         "hashScatter": ("hbm", SCATTER_BYTES_PER_SAMPLE * n_prof),
-        "densityFwd": ("hbm", ENC_BYTES_PER_SAMPLE * n_prof),
+        "forward": ("hbm", ENC_BYTES_PER_SAMPLE * n_prof),  # encode + both heads' forward, one launch
         "densityOpt": ("hbm", ADAM_BYTES_PER_PARAM * (L * TBL * F)),
     }
     dom = max((k for k in candidates if k in st), key=lambda k: st[k][0])
@@ -467,7 +467,7 @@ def main():
     roofline = {"bound": bound, "kernel": dom, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom),
                 "algorithmic_bytes_per_launch": int(algo), "avg_launch_ms": round(dom_ms, 4)}
-    mlp_ms = sum(st[k][0] for k in ("densityFwd", "colorFwd", "colorBwd", "densityBwd") if k in st)
+    mlp_ms = sum(st[k][0] for k in ("forward", "colorBwd", "densityBwd") if k in st)
     mfma_util = MLP_FLOP_PER_SAMPLE * n_prof / (mlp_ms * 1e-3) / 1e12 / FP16_PEAK_TFLOPS if mlp_ms else None
 
     out = {
@@ -490,7 +490,7 @@ def main():
                    "feed": "100 RGBA8 800x800 views in HBM, pcg_hash draws, random background per call"},
         "stage_ms": stage_ms,
         "stage_ms_per_step": stage_ms_per_step,
-        "hash_encodes_per_s": round(n_prof / (st["densityFwd"][0] * 1e-3), 1) if "densityFwd" in st else None,
+        "forward_samples_per_s": round(n_prof / (st["forward"][0] * 1e-3), 1) if "forward" in st else None,
         "mfma_util": round(mfma_util, 5) if mfma_util else None,
         "roofline": roofline,
     }
