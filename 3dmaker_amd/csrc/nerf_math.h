@@ -39,9 +39,8 @@ __host__ __device__ __forceinline__ float nerf_expf(float x)
 // hardware spelled out (NaN and negatives -> 0, f >= hi -> hi).
 __host__ __device__ __forceinline__ int clamp_floor_idx(float f, int hi)
 {
-    if (!(f >= 0.0f)) return 0;
-    if (f >= (float)hi) return hi;
-    return (int)f;
+    // branch-free: fmaxf turns NaN and negatives into 0, fminf caps at hi (exact: hi < 2^24)
+    return (int)fminf(fmaxf(f, 0.0f), (float)hi);
 }
 
 // get_cascade (processRays.cu:11-19): the smallest cascade c whose box

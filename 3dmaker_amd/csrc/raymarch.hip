@@ -87,20 +87,26 @@ __device__ uint32_t march_ray(const MarchArgs& a, uint32_t i, float* __restrict_
         const float cextx = ex * cs, cexty = ey * cs, cextz = ez * cs;
         const float rx = (px - cminx) / cextx, ry = (py - cminy) / cexty, rz = (pz - cminz) / cextz;
         const uint32_t cbase = (uint32_t)c * a.total_cells;
-        uint32_t bit[MAXL];
+        // every level's byte is loaded without a branch (levels >= L read
+        // byte 0 and are ignored), so the loads issue together and the
+        // iteration waits for memory once
+        uint32_t bit[MAXL], flat[MAXL];
         int ix[MAXL], iy[MAXL], iz[MAXL];
 #pragma unroll
         for (int l = 0; l < MAXL; l++) {
-            if (l < L) {
-                const uint32_t rlx = a.res.x >> l, rly = a.res.y >> l, rlz = a.res.z >> l;
-                ix[l] = clamp_floor_idx(floorf(rx * (float)rlx), (int)rlx - 1);
-                iy[l] = clamp_floor_idx(floorf(ry * (float)rly), (int)rly - 1);
-                iz[l] = clamp_floor_idx(floorf(rz * (float)rlz), (int)rlz - 1);
-                const uint32_t flat = cbase + a.mip_off[l] + (uint32_t)iz[l] * (rlx * rly) +
-                                      (uint32_t)iy[l] * rlx + (uint32_t)ix[l];
-                bit[l] = ((uint32_t)a.bits[flat >> 3] >> (flat & 7)) & 1u;
-            }
+            const uint32_t rlx = a.res.x >> l, rly = a.res.y >> l, rlz = a.res.z >> l;
+            ix[l] = clamp_floor_idx(floorf(rx * (float)rlx), (int)rlx - 1);
+            iy[l] = clamp_floor_idx(floorf(ry * (float)rly), (int)rly - 1);
+            iz[l] = clamp_floor_idx(floorf(rz * (float)rlz), (int)rlz - 1);
+            flat[l] = l < L ? cbase + a.mip_off[l] + (uint32_t)iz[l] * (rlx * rly) + (uint32_t)iy[l] * rlx +
+                                  (uint32_t)ix[l]
+                            : 0u;
         }
+        uint8_t byte[MAXL];
+#pragma unroll
+        for (int l = 0; l < MAXL; l++) byte[l] = a.bits[flat[l] >> 3];
+#pragma unroll
+        for (int l = 0; l < MAXL; l++) bit[l] = ((uint32_t)byte[l] >> (flat[l] & 7)) & 1u;
         // the reference's level sequence L-1, L-2, ... stops at the first
         // unoccupied level, or at level 0
         int level = L - 1, vix = 0, viy = 0, viz = 0;
