@@ -53,6 +53,7 @@ struct MarchArgs {
     uint32_t total_cells;        // cells of one cascade pyramid
     uint32_t mip_off[kMaxMip];   // cells below level l
     float3 vs0[kMaxMip];         // cascade-0 voxel size of level l: extent / (res >> l)
+    int shift_levels;            // res divisible by 2^(L-1): level-l cells are level-0 cells >> l
 };
 
 // Marches ray i and stores its sample t values at t_out[march_store_index(i, k)];
@@ -81,7 +82,8 @@ __device__ uint32_t march_ray(const MarchArgs& a, uint32_t i, float* __restrict_
     uint32_t hit = 0;
     for (int it = 0; t < t_max && hit < (uint32_t)kMaxHits && it < kMaxMarchIters;) {
         const float px = o.x + t * d.x, py = o.y + t * d.y, pz = o.z + t * d.z;
-        const int c = get_cascade(px, py, pz, a.mn, a.mx, a.C);
+        int c = 0;
+        if (a.C > 1) c = get_cascade(px, py, pz, a.mn, a.mx, a.C);  // one cascade: always 0
         const float cs = ldexpf(1.0f, c);
         const float cminx = a.mn.x * cs, cminy = a.mn.y * cs, cminz = a.mn.z * cs;
         const float cextx = ex * cs, cexty = ey * cs, cextz = ez * cs;
@@ -92,14 +94,32 @@ __device__ uint32_t march_ray(const MarchArgs& a, uint32_t i, float* __restrict_
         // iteration waits for memory once
         uint32_t bit[MAXL], flat[MAXL];
         int ix[MAXL], iy[MAXL], iz[MAXL];
+        if (a.shift_levels) {
+            // floor(r * (res >> l)) = floor(r * res) >> l when 2^l divides res:
+            // the scaling by 2^-l is exact, and so is the clamp's upper end
+            const int x0 = clamp_floor_idx(floorf(rx * (float)a.res.x), (int)a.res.x - 1);
+            const int y0 = clamp_floor_idx(floorf(ry * (float)a.res.y), (int)a.res.y - 1);
+            const int z0 = clamp_floor_idx(floorf(rz * (float)a.res.z), (int)a.res.z - 1);
+#pragma unroll
+            for (int l = 0; l < MAXL; l++) {
+                ix[l] = x0 >> l;
+                iy[l] = y0 >> l;
+                iz[l] = z0 >> l;
+            }
+        } else {
+#pragma unroll
+            for (int l = 0; l < MAXL; l++) {
+                const uint32_t rlx = a.res.x >> l, rly = a.res.y >> l, rlz = a.res.z >> l;
+                ix[l] = clamp_floor_idx(floorf(rx * (float)rlx), (int)rlx - 1);
+                iy[l] = clamp_floor_idx(floorf(ry * (float)rly), (int)rly - 1);
+                iz[l] = clamp_floor_idx(floorf(rz * (float)rlz), (int)rlz - 1);
+            }
+        }
 #pragma unroll
         for (int l = 0; l < MAXL; l++) {
-            const uint32_t rlx = a.res.x >> l, rly = a.res.y >> l, rlz = a.res.z >> l;
-            ix[l] = clamp_floor_idx(floorf(rx * (float)rlx), (int)rlx - 1);
-            iy[l] = clamp_floor_idx(floorf(ry * (float)rly), (int)rly - 1);
-            iz[l] = clamp_floor_idx(floorf(rz * (float)rlz), (int)rlz - 1);
-            flat[l] = l < L ? cbase + a.mip_off[l] + (uint32_t)iz[l] * (rlx * rly) + (uint32_t)iy[l] * rlx +
-                                  (uint32_t)ix[l]
+            const uint32_t rlx = a.res.x >> l, rly = a.res.y >> l;
+            flat[l] = l < L ? cbase + a.mip_off[l] + __umul24((uint32_t)iz[l], rlx * rly) +
+                                  __umul24((uint32_t)iy[l], rlx) + (uint32_t)ix[l]
                             : 0u;
         }
         uint8_t byte[MAXL];
@@ -334,6 +354,8 @@ MarchArgs march_args(uint32_t R, const float3* o, const float3* d, const float3*
     if ((g.res.x >> (g.mip_levels - 1)) == 0 || (g.res.y >> (g.mip_levels - 1)) == 0 ||
         (g.res.z >> (g.mip_levels - 1)) == 0)
         throw std::runtime_error("raymarch: grid resolution too small for the mip levels");
+    if ((uint64_t)g.res.x * g.res.y >= (1ull << 24) || g.res.z >= (1u << 24))
+        throw std::runtime_error("raymarch: grid resolution too large (res.x * res.y must be < 2^24)");
     MarchArgs a{};
     a.o = o;
     a.d = d;
@@ -354,6 +376,8 @@ MarchArgs march_args(uint32_t R, const float3* o, const float3* d, const float3*
         a.vs0[l] = make_float3(ex / (float)(g.res.x >> l), ey / (float)(g.res.y >> l), ez / (float)(g.res.z >> l));
     }
     a.total_cells = mip_offset(g.res, g.mip_levels);
+    const uint32_t m = (1u << (g.mip_levels - 1)) - 1u;
+    a.shift_levels = ((g.res.x | g.res.y | g.res.z) & m) == 0 ? 1 : 0;
     return a;
 }
 
