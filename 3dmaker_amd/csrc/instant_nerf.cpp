@@ -28,6 +28,21 @@ struct StageTimer {
     hipEvent_t a, b;
 };
 
+// What one compaction produces.  Two sets alternate, so the compaction of the
+// next hit batch can run on the side stream while the current step still
+// reads its own set.
+struct StepSet {
+    uint32_t* offsets = nullptr;   // [rayChunkSize] per-ray sample offsets
+    uint32_t* counts = nullptr;    // [rayChunkSize] per-ray sample counts (copied from the march store)
+    float4* positions = nullptr;   // [batchSize]
+    uint32_t* ray_idx = nullptr;   // [batchSize]
+    float* t_sorted = nullptr;     // [batchSize]
+    uint32_t* result = nullptr;    // [2] active rays, compacted samples
+    uint32_t* h_result = nullptr;  // pinned copy of result
+    hipEvent_t ev_result = nullptr, ev_ready = nullptr, ev_free = nullptr;
+    uint32_t raysDone = 0;         // first ray of the batch in the call's rays
+};
+
 struct NerfBuffers {
     // per step, rays
     float3* d_inv = nullptr;
@@ -35,21 +50,16 @@ struct NerfBuffers {
     float* fars = nullptr;
     uint32_t* counts = nullptr;      // counts of the cached window [c0, c1)
     float* t_scratch = nullptr;      // march store of the cached window (march_store_floats(rayChunkSize))
-    uint32_t* offsets = nullptr;
     uint32_t cache_c0 = 0, cache_c1 = 0;
     long cache_version = -1;         // grid version the cached counts were marched on
-    uint32_t* step_counts = nullptr; // window counts of the last step
     uint32_t* block_sums = nullptr;
-    uint32_t* result = nullptr;
-    uint32_t* h_result = nullptr;  // pinned
+    StepSet set[2];
+    int last_set = 0;                // set of the last training step
     float* render_rgb = nullptr;
     float* render_depth = nullptr;
     float* phi = nullptr;
     float* weight_sum = nullptr;
     // per step, samples
-    float4* positions = nullptr;
-    uint32_t* ray_idx = nullptr;
-    float* t_sorted = nullptr;
     float* density_out = nullptr;
     float* sigma = nullptr;
     float* dw = nullptr;
@@ -80,10 +90,11 @@ struct NerfBuffers {
     // model views
     __half* color_in = nullptr;      // TinyMLP activation 0
     graft::GridMeta meta{};
-    hipEvent_t ev_result = nullptr;
-    // occupancy refresh on its own stream, overlapped with the rest of its step
+    // ray setup, march and compaction of the next hit batch, and the occupancy
+    // refresh run on their own stream, overlapped with the main stream's step
     hipStream_t side = nullptr;
-    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
+    hipEvent_t ev_fork = nullptr, ev_join = nullptr, ev_done = nullptr;
+    hipEvent_t ev_params = nullptr;  // main stream: the last step's Adam updates are done
     std::vector<StageTimer> pending;
     std::map<std::string, std::pair<double, long>> stats;
 };
@@ -134,17 +145,23 @@ void InstantNerf::freeBuffers()
         dfree(b.fars);
         dfree(b.counts);
         dfree(b.t_scratch);
-        dfree(b.offsets);
         dfree(b.block_sums);
-        dfree(b.result);
-        if (b.h_result) (void)hipHostFree(b.h_result);
+        for (StepSet& S : b.set) {
+            dfree(S.offsets);
+            dfree(S.counts);
+            dfree(S.positions);
+            dfree(S.ray_idx);
+            dfree(S.t_sorted);
+            dfree(S.result);
+            if (S.h_result) (void)hipHostFree(S.h_result);
+            if (S.ev_result) (void)hipEventDestroy(S.ev_result);
+            if (S.ev_ready) (void)hipEventDestroy(S.ev_ready);
+            if (S.ev_free) (void)hipEventDestroy(S.ev_free);
+        }
         dfree(b.render_rgb);
         dfree(b.render_depth);
         dfree(b.phi);
         dfree(b.weight_sum);
-        dfree(b.positions);
-        dfree(b.ray_idx);
-        dfree(b.t_sorted);
         dfree(b.density_out);
         dfree(b.sigma);
         dfree(b.dw);
@@ -166,9 +183,10 @@ void InstantNerf::freeBuffers()
         dfree(b.render.sigma);
         dfree(b.render.rgb);
         dfree(b.render.dir);
-        if (b.ev_result) (void)hipEventDestroy(b.ev_result);
         if (b.ev_fork) (void)hipEventDestroy(b.ev_fork);
         if (b.ev_join) (void)hipEventDestroy(b.ev_join);
+        if (b.ev_done) (void)hipEventDestroy(b.ev_done);
+        if (b.ev_params) (void)hipEventDestroy(b.ev_params);
         if (b.side) (void)hipStreamDestroy(b.side);
         for (auto& t : b.pending) {
             (void)hipEventDestroy(t.a);
@@ -250,18 +268,24 @@ void InstantNerf::allocate()
     b.fars = dalloc<float>(R);
     b.counts = dalloc<uint32_t>(R);
     b.t_scratch = dalloc<float>(graft::march_store_floats((uint32_t)R));
-    b.offsets = dalloc<uint32_t>(R);
     b.block_sums = dalloc<uint32_t>(graft::march_scratch_words((uint32_t)R));
-    b.result = dalloc<uint32_t>(2);
-    GRAFT_HIP_CHECK(hipMemset(b.result, 0, 2 * sizeof(uint32_t)));
-    GRAFT_HIP_CHECK(hipHostMalloc((void**)&b.h_result, 2 * sizeof(uint32_t), hipHostMallocDefault));
+    for (StepSet& S : b.set) {
+        S.offsets = dalloc<uint32_t>(R);
+        S.counts = dalloc<uint32_t>(R);
+        S.positions = dalloc<float4>(Bn);
+        S.ray_idx = dalloc<uint32_t>(Bn);
+        S.t_sorted = dalloc<float>(Bn);
+        S.result = dalloc<uint32_t>(2);
+        GRAFT_HIP_CHECK(hipMemset(S.result, 0, 2 * sizeof(uint32_t)));
+        GRAFT_HIP_CHECK(hipHostMalloc((void**)&S.h_result, 2 * sizeof(uint32_t), hipHostMallocDefault));
+        GRAFT_HIP_CHECK(hipEventCreateWithFlags(&S.ev_result, hipEventDisableTiming));
+        GRAFT_HIP_CHECK(hipEventCreateWithFlags(&S.ev_ready, hipEventDisableTiming));
+        GRAFT_HIP_CHECK(hipEventCreateWithFlags(&S.ev_free, hipEventDisableTiming));
+    }
     b.render_rgb = dalloc<float>(3 * R);
     b.render_depth = dalloc<float>(R);
     b.phi = dalloc<float>(3 * R);
     b.weight_sum = dalloc<float>(R);
-    b.positions = dalloc<float4>(Bn);
-    b.ray_idx = dalloc<uint32_t>(Bn);
-    b.t_sorted = dalloc<float>(Bn);
     b.density_out = dalloc<float>(16 * Bn);
     b.sigma = dalloc<float>(Bn);
     b.dw = dalloc<float>(Bn);
@@ -277,9 +301,10 @@ void InstantNerf::allocate()
     b.active_list = dalloc<int>((size_t)N);
     b.active_count = dalloc<int>(1);
     b.list_scratch = dalloc<uint32_t>(graft::occ_list_scratch_words(N));
-    GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_result, hipEventDisableTiming));
     GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_fork, hipEventDisableTiming));
     GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_join, hipEventDisableTiming));
+    GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_done, hipEventDisableTiming));
+    GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_params, hipEventDisableTiming));
     GRAFT_HIP_CHECK(hipStreamCreateWithFlags(&b.side, hipStreamNonBlocking));
 
     // The color head's activation-0 buffer receives the SH gather output directly.
@@ -307,13 +332,11 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
     if (!m_init) throw std::runtime_error("InstantNerf: init() must be called before trainWithRaysHit()");
     if (!d_rgb_true) throw std::runtime_error("InstantNerf: trainWithRaysHit needs ground-truth colours");
     if (m_memMode != TRAINING) throw std::runtime_error("InstantNerf: trainWithRaysHit needs setMemoryMode(TRAINING)");
+    if (numRays == 0) return;
     NerfBuffers& b = B(m_buf);
     const NerfOptions& o = m_opts;
     const uint32_t Bn = (uint32_t)o.batchSize;
     const graft::OccGrid g = occ_grid(o, d_occupancyGrid);
-    const uint32_t* d_rays = b.result;       // active rays of this step
-    const uint32_t* d_hits = b.result + 1;   // compacted samples of this step
-
     const TinyMLPHashGrid::Buffers db = m_densityMLP->buffers();
     const TinyMLP::Buffers cb = m_colorMLP->buffers();
     const graft::MlpShape dshape{2 * o.numLevels, db.hw.hiddenDim, db.hw.outputDim, db.hw.numLayers};
@@ -335,48 +358,69 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
     };
     auto stage = [&](const char* name, auto&& fn) { stage_on(stream, name, fn); };
 
-    uint32_t raysDone = 0;
-    int i = 0;
-    b.cache_version = -1;  // new rays: nothing cached
-    while (raysDone < numRays) {
+    // processRaysHitLinear (processRays.cu:931-1040) for the hit batch that
+    // starts at ray raysDone, into step set k, on the side stream: the window
+    // is marched only when it is not covered by the cached march on the
+    // current grid; the set is reused once the main stream has finished the
+    // step that last read it.
+    auto compact = [&](int k, uint32_t raysDone) {
+        StepSet& S = b.set[k];
         const uint32_t R = std::min<uint32_t>((uint32_t)o.rayChunkSize, numRays - raysDone);
         const float3* co = d_rays_o + raysDone;
         const float3* cd = d_rays_d + raysDone;
-        const float* cdep = d_rays_depth ? d_rays_depth + raysDone : nullptr;
-        const float* csig = d_rays_sigma ? d_rays_sigma + raysDone : nullptr;
-
-        // March the window only when it is not covered by the cached march on the current grid.
+        GRAFT_HIP_CHECK(hipStreamWaitEvent(b.side, S.ev_free, 0));
         if (b.cache_version != m_gridVersion || raysDone < b.cache_c0 || raysDone + R > b.cache_c1) {
-            stage("rayAabb", [&] {
+            stage_on(b.side, "rayAabb", [&] {
                 graft::ray_aabb_inv(R, co, cd, o.aabbMin, o.aabbMax, o.numCascades, b.d_inv, b.nears, b.fars,
-                                    stream);
+                                    b.side);
             });
-            stage("march", [&] {
+            stage_on(b.side, "march", [&] {
                 graft::march_store(R, co, cd, b.d_inv, b.nears, b.fars, g, o.samplesPerVoxel, b.counts, b.t_scratch,
-                                   stream);
+                                   b.side);
             });
             b.cache_c0 = raysDone;
             b.cache_c1 = raysDone + R;
             b.cache_version = m_gridVersion;
         }
         const uint32_t woff = raysDone - b.cache_c0;
-        m_windowStart = raysDone;
-        b.step_counts = b.counts + woff;
-        stage("compaction", [&] {
-            graft::march_compact_stored(R, co, cd, g, Bn, b.step_counts, b.t_scratch, woff, b.offsets, b.t_sorted,
-                                        b.ray_idx, b.positions, graft::MarchScratch{b.block_sums, b.result}, stream);
+        stage_on(b.side, "compaction", [&] {
+            graft::march_compact_stored(R, co, cd, g, Bn, b.counts + woff, b.t_scratch, woff, S.offsets, S.t_sorted,
+                                        S.ray_idx, S.positions, graft::MarchScratch{b.block_sums, S.result}, b.side,
+                                        S.counts);
         });
-        GRAFT_HIP_CHECK(hipMemcpyAsync(b.h_result, b.result, 2 * sizeof(uint32_t), hipMemcpyDeviceToHost, stream));
-        GRAFT_HIP_CHECK(hipEventRecord(b.ev_result, stream));
+        GRAFT_HIP_CHECK(hipMemcpyAsync(S.h_result, S.result, 2 * sizeof(uint32_t), hipMemcpyDeviceToHost, b.side));
+        GRAFT_HIP_CHECK(hipEventRecord(S.ev_result, b.side));
+        GRAFT_HIP_CHECK(hipEventRecord(S.ev_ready, b.side));
+        S.raysDone = raysDone;
+    };
 
-        // InstantNerf.cu:488-494: the refresh changes only the grid the next step
-        // marches and reads only the density head, so it runs on the side stream
+    // the side stream starts after everything the caller queued (rays, grid)
+    GRAFT_HIP_CHECK(hipEventRecord(b.ev_fork, stream));
+    GRAFT_HIP_CHECK(hipStreamWaitEvent(b.side, b.ev_fork, 0));
+    b.cache_version = -1;  // new rays: nothing cached
+    int k = 0, i = 0;
+    compact(k, 0);
+    while (true) {
+        StepSet& S = b.set[k];
+        const uint32_t raysDone = S.raysDone;
+        const float3* cd = d_rays_d + raysDone;
+        const float* cdep = d_rays_depth ? d_rays_depth + raysDone : nullptr;
+        const float* csig = d_rays_sigma ? d_rays_sigma + raysDone : nullptr;
+        const uint32_t R = std::min<uint32_t>((uint32_t)o.rayChunkSize, numRays - raysDone);
+        const uint32_t* d_rays = S.result;      // active rays of this step
+        const uint32_t* d_hits = S.result + 1;  // compacted samples of this step
+        m_windowStart = raysDone;
+        b.last_set = k;
+
+        // InstantNerf.cu:488-494: the refresh changes only the grid that later
+        // batches march and reads only the density head, so it runs on the
+        // side stream (after this batch's compaction, before the next one's)
         // beside this step's forward/backward; the density head's Adam update
         // waits for it, so it sees the same parameters as in the serial order.
         const bool refresh = (m_trainSteps % 16 == 0);
         if (refresh) {
-            GRAFT_HIP_CHECK(hipEventRecord(b.ev_fork, stream));
-            GRAFT_HIP_CHECK(hipStreamWaitEvent(b.side, b.ev_fork, 0));
+            // density inference on the parameters after the previous step's Adam
+            if (i > 0) GRAFT_HIP_CHECK(hipStreamWaitEvent(b.side, b.ev_params, 0));
             stage_on(b.side, "occupancy", [&] {
                 if (m_trainSteps < 256) earlyOccupancyGridUpdate(b.side);
                 else lateOccupancyGridUpdate(b.side);
@@ -384,12 +428,13 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
             GRAFT_HIP_CHECK(hipEventRecord(b.ev_join, b.side));
         }
 
+        GRAFT_HIP_CHECK(hipStreamWaitEvent(stream, S.ev_ready, 0));
         // hash encode + density head, SH gather (into the colour head's
         // activation 0), colour head: one launch, activations saved
         stage("forward", [&] {
             graft::NerfFwdArgs fa;
             fa.dshape = dshape;
-            fa.pos = reinterpret_cast<const float*>(b.positions);
+            fa.pos = reinterpret_cast<const float*>(S.positions);
             fa.pos_stride = 4;
             fa.table = db.fwd_hashtable;
             fa.meta = &b.meta;
@@ -398,7 +443,7 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
             fa.dacts = db.activations;
             fa.density_out = b.density_out;
             fa.dirs = cd;
-            fa.ray_idx = b.ray_idx;
+            fa.ray_idx = S.ray_idx;
             fa.density_bias = o.densityBias;
             fa.sigma = b.sigma;
             fa.cshape = cshape;
@@ -414,9 +459,9 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         float* final_rgb = d_rgb_out ? d_rgb_out + (size_t)raysDone * 3 : b.render_rgb;
         stage("renderGrad", [&] {
             graft::CompositeArgs ca{};
-            ca.offsets = b.offsets;
-            ca.counts = b.step_counts;
-            ca.t = b.t_sorted;
+            ca.offsets = S.offsets;
+            ca.counts = S.counts;
+            ca.t = S.t_sorted;
             ca.sigma = b.sigma;
             ca.depth_prior = cdep;
             ca.sigma_prior = csig;
@@ -433,9 +478,9 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
             ca.bg = o.bgColor;
             graft::ColorGradArgs ga{};
             ga.initial_offset = 0;
-            ga.counts = b.step_counts;
-            ga.offsets = b.offsets;
-            ga.t = b.t_sorted;
+            ga.counts = S.counts;
+            ga.offsets = S.offsets;
+            ga.t = S.t_sorted;
             ga.density_out = b.density_out;
             ga.color_out = cb.padded_outputs;
             ga.color_stride = cstride;
@@ -463,9 +508,10 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
                                 /*accumulate=*/false);
         });
         stage("hashScatter", [&] {
-            graft::hash_scatter(b.meta, db.dx_out, reinterpret_cast<const float*>(b.positions), 4, db.hashtable_grads,
+            graft::hash_scatter(b.meta, db.dx_out, reinterpret_cast<const float*>(S.positions), 4, db.hashtable_grads,
                                 (int)Bn, stream, d_hits);
         });
+        GRAFT_HIP_CHECK(hipEventRecord(S.ev_free, stream));  // the last read of this set
         stage("colorOpt", [&] {
             m_colorMLP->step(o.learningRate, o.beta1, o.beta2, o.epsilon, o.lossScale, stream);
         });
@@ -473,18 +519,25 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         stage("densityOpt", [&] {
             m_densityMLP->step(o.learningRate, o.beta1, o.beta2, o.epsilon, o.lossScale, stream);
         });
+        GRAFT_HIP_CHECK(hipEventRecord(b.ev_params, stream));
 
         trainStepCount++;
         m_trainSteps++;
 
-        // The only host read of the step: its active-ray count, to advance the cursor.
-        GRAFT_HIP_CHECK(hipEventSynchronize(b.ev_result));
-        const uint32_t active = b.h_result[0], hits = b.h_result[1];
+        // The only host read of the step: its active-ray count, to advance the
+        // cursor; the next batch's compaction then runs beside this step.
+        GRAFT_HIP_CHECK(hipEventSynchronize(S.ev_result));
+        const uint32_t active = S.h_result[0], hits = S.h_result[1];
         if (active == 0) throw std::runtime_error("InstantNerf: no ray fits the batch");
         if (hitCounts) hitCounts[i] = hits;
-        raysDone += active;
         i++;
+        if (raysDone + active >= numRays) break;
+        k ^= 1;
+        compact(k, raysDone + active);
     }
+    // nothing of this call stays on the side stream past the return
+    GRAFT_HIP_CHECK(hipEventRecord(b.ev_done, b.side));
+    GRAFT_HIP_CHECK(hipStreamWaitEvent(stream, b.ev_done, 0));
 
     if (o.isProfiling && !b.pending.empty()) {
         GRAFT_HIP_CHECK(hipEventSynchronize(b.pending.back().b));
@@ -626,11 +679,12 @@ InstantNerf::StepBuffers InstantNerf::stepBuffers() const
     if (!m_buf) throw std::runtime_error("InstantNerf: init() first");
     const NerfBuffers& b = *static_cast<const NerfBuffers*>(m_buf);
     StepBuffers s{};
-    s.num_steps = b.step_counts ? b.step_counts : b.counts;
-    s.ray_offsets = b.offsets;
-    s.positions = b.positions;
-    s.ray_indices = b.ray_idx;
-    s.t_sorted = b.t_sorted;
+    const StepSet& S = b.set[b.last_set];
+    s.num_steps = S.counts;
+    s.ray_offsets = S.offsets;
+    s.positions = S.positions;
+    s.ray_indices = S.ray_idx;
+    s.t_sorted = S.t_sorted;
     s.density_out = b.density_out;
     s.color_input = b.color_in;
     s.color_output = m_colorMLP->buffers().padded_outputs;
@@ -642,7 +696,7 @@ InstantNerf::StepBuffers InstantNerf::stepBuffers() const
     s.dsigma = b.dsigma;
     s.color_dx = b.color_dx;
     s.density_grad = m_densityMLP->buffers().dloss;
-    s.result = b.result;
+    s.result = S.result;
     s.trainSteps = m_trainSteps;
     s.windowStart = m_windowStart;
     return s;
@@ -698,8 +752,9 @@ void InstantNerf::renderImageHit(const float3* d_rays_o, const float3* d_rays_d,
     const graft::MlpShape cshape = shape_of(cb.hw);
     ensure_render(b, hitBatch, cshape.out);
     const graft::OccGrid g = occ_grid(o, d_occupancyGrid);
-    const uint32_t* d_rays = b.result;
-    const uint32_t* d_hits = b.result + 1;
+    StepSet& S = b.set[0];  // the render path runs on the caller's stream only
+    const uint32_t* d_rays = S.result;
+    const uint32_t* d_hits = S.result + 1;
     b.cache_version = -1;  // the march store is reused below
 
     for (uint32_t c0 = 0; c0 < numRays; c0 += (uint32_t)o.rayChunkSize) {
@@ -711,10 +766,10 @@ void InstantNerf::renderImageHit(const float3* d_rays_o, const float3* d_rays_d,
         uint32_t done = 0;
         while (done < R) {
             graft::march_compact_stored(R - done, co + done, cd + done, g, hitBatch, b.counts + done, b.t_scratch, done,
-                                        b.offsets, b.render.t, b.render.ray_idx, b.render.positions,
-                                        graft::MarchScratch{b.block_sums, b.result}, stream);
-            GRAFT_HIP_CHECK(hipMemcpyAsync(b.h_result, b.result, 2 * sizeof(uint32_t), hipMemcpyDeviceToHost, stream));
-            GRAFT_HIP_CHECK(hipEventRecord(b.ev_result, stream));
+                                        S.offsets, b.render.t, b.render.ray_idx, b.render.positions,
+                                        graft::MarchScratch{b.block_sums, S.result}, stream);
+            GRAFT_HIP_CHECK(hipMemcpyAsync(S.h_result, S.result, 2 * sizeof(uint32_t), hipMemcpyDeviceToHost, stream));
+            GRAFT_HIP_CHECK(hipEventRecord(S.ev_result, stream));
             graft::NerfFwdArgs fa;
             fa.dshape = dshape;
             fa.pos = reinterpret_cast<const float*>(b.render.positions);
@@ -734,7 +789,7 @@ void InstantNerf::renderImageHit(const float3* d_rays_o, const float3* d_rays_d,
             fa.color_out = b.render.rgb;
             graft::nerf_forward(fa, (int)hitBatch, stream, d_hits);
             graft::CompositeArgs ca{};
-            ca.offsets = b.offsets;
+            ca.offsets = S.offsets;
             ca.counts = b.counts + done;
             ca.t = b.render.t;
             ca.sigma = b.render.sigma;
@@ -744,8 +799,8 @@ void InstantNerf::renderImageHit(const float3* d_rays_o, const float3* d_rays_d,
             ca.final_depth = b.render_depth;
             ca.bg = o.bgColor;
             graft::composite_infer(ca, 0, 0, d_rays, R - done, stream);
-            GRAFT_HIP_CHECK(hipEventSynchronize(b.ev_result));
-            const uint32_t active = b.h_result[0];
+            GRAFT_HIP_CHECK(hipEventSynchronize(S.ev_result));
+            const uint32_t active = S.h_result[0];
             if (active == 0) throw std::runtime_error("InstantNerf: the render hit batch cannot hold one ray");
             done += active;
         }

@@ -52,11 +52,13 @@ inline size_t march_store_floats(uint32_t R) { return (size_t)((R + 63) / 64) * 
 void march_store(uint32_t R, const float3* o, const float3* d, const float3* d_inv, const float* nears,
                  const float* fars, const OccGrid& g, int K, uint32_t* counts, float* t_scratch, hipStream_t s);
 // Compacts rays [ray_base, ray_base + R) of the stored march (counts already
-// offset to the window's first ray; o, d too).
+// offset to the window's first ray; o, d too).  counts_out (nullable)
+// receives a copy of the R counts, so that the step can read them after the
+// march store has been overwritten.
 void march_compact_stored(uint32_t R, const float3* o, const float3* d, const OccGrid& g, uint32_t batch,
                           const uint32_t* counts, const float* t_scratch, uint32_t ray_base, uint32_t* offsets,
                           float* t_out, uint32_t* ray_idx, float4* pos_out, const MarchScratch& scratch,
-                          hipStream_t s);
+                          hipStream_t s, uint32_t* counts_out = nullptr);
 
 // compute_SH_gather (otherKernels.cu:156-273).
 void sh_gather(const float3* dirs, const uint32_t* ray_idx, const uint32_t* d_n, uint32_t n_max, float bias,

@@ -299,13 +299,16 @@ __global__ __launch_bounds__(256) void block_sums_kernel(const uint32_t* __restr
 
 __global__ __launch_bounds__(256) void offsets_kernel(const uint32_t* __restrict__ counts, uint32_t n,
                                                       const uint32_t* __restrict__ block_excl,
-                                                      uint32_t* __restrict__ offsets)
+                                                      uint32_t* __restrict__ offsets, uint32_t* __restrict__ counts_out)
 {
     __shared__ uint32_t s_wave[4];
     const uint32_t i = blockIdx.x * 256 + threadIdx.x;
     const uint32_t c = i < n ? counts[i] : 0u;
     const uint32_t incl = block_incl_scan<4>(c, s_wave);
-    if (i < n) offsets[i] = block_excl[blockIdx.x] + (incl - c);
+    if (i < n) {
+        offsets[i] = block_excl[blockIdx.x] + (incl - c);
+        if (counts_out != nullptr) counts_out[i] = c;
+    }
 }
 
 // One thread per compacted sample j < result[1]: its ray is the last active
@@ -410,7 +413,8 @@ void march_store(uint32_t R, const float3* o, const float3* d, const float3* d_i
 
 void march_compact_stored(uint32_t R, const float3* o, const float3* d, const OccGrid& g, uint32_t batch,
                           const uint32_t* counts, const float* t_scratch, uint32_t ray_base, uint32_t* offsets,
-                          float* t_out, uint32_t* ray_idx, float4* pos_out, const MarchScratch& sc, hipStream_t s)
+                          float* t_out, uint32_t* ray_idx, float4* pos_out, const MarchScratch& sc, hipStream_t s,
+                          uint32_t* counts_out)
 {
     if (R == 0) {
         GRAFT_HIP_CHECK(hipMemsetAsync(sc.result, 0, 2 * sizeof(uint32_t), s));
@@ -421,7 +425,7 @@ void march_compact_stored(uint32_t R, const float3* o, const float3* d, const Oc
     GRAFT_LAUNCH_CHECK();
     hipLaunchKernelGGL(march_scan_kernel, dim3(1), dim3(1024), 0, s, counts, sc.block_sums, nb, R, batch, sc.result);
     GRAFT_LAUNCH_CHECK();
-    hipLaunchKernelGGL(offsets_kernel, dim3(nb), dim3(256), 0, s, counts, R, sc.block_sums, offsets);
+    hipLaunchKernelGGL(offsets_kernel, dim3(nb), dim3(256), 0, s, counts, R, sc.block_sums, offsets, counts_out);
     GRAFT_LAUNCH_CHECK();
     GatherArgs ga{o, d, g.aabb_min, g.aabb_max, offsets, t_scratch, ray_base, sc.result, t_out, ray_idx, pos_out};
     const int gblocks = (int)std::max<uint32_t>(1, std::min<uint32_t>((batch + 255) / 256, 4096));
