@@ -212,8 +212,13 @@ void hash_scatter(const GridMeta& m, const __half* denc, const float* pos, int p
     if (pos_stride < 3) throw std::runtime_error("hash scatter: position stride must be >= 3");
     GridKernelArgs a = grid_args(m, N, pos_stride);
     a.d_n = d_n;
+    // One workgroup per CU: the memory-side atomic rate, not the number of
+    // waves issuing atomics, bounds this kernel (measured on a training step:
+    // 1 block per CU is as fast as 16), and the idle CU slots then run the
+    // side stream's work (next batch's compaction, occupancy refresh).
     const long long threads = (long long)((N + 15) / 16) * m.numLevels * 64;
-    hipLaunchKernelGGL(hash_scatter_kernel, dim3(grid_blocks(threads)), dim3(256), 0, stream, a,
+    const int blocks = (int)std::max(1LL, std::min((threads + 255) / 256, (long long)num_cus()));
+    hipLaunchKernelGGL(hash_scatter_kernel, dim3(blocks), dim3(256), 0, stream, a,
                        pos, reinterpret_cast<const _Float16*>(denc), grads);
     GRAFT_LAUNCH_CHECK();
 }
