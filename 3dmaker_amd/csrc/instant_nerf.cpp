@@ -90,11 +90,14 @@ struct NerfBuffers {
     // model views
     __half* color_in = nullptr;      // TinyMLP activation 0
     graft::GridMeta meta{};
-    // ray setup, march and compaction of the next hit batch, and the occupancy
-    // refresh run on their own stream, overlapped with the main stream's step
-    hipStream_t side = nullptr;
-    hipEvent_t ev_fork = nullptr, ev_join = nullptr, ev_done = nullptr;
-    hipEvent_t ev_params = nullptr;  // main stream: the last step's Adam updates are done
+    // Beside the main stream: `side` runs the ray setup, march and compaction
+    // of the next hit batch and the MLP weight gradients and Adam updates;
+    // `occ` runs the occupancy refresh.
+    hipStream_t side = nullptr, occ = nullptr;
+    hipEvent_t ev_fork = nullptr, ev_join = nullptr, ev_done = nullptr, ev_done_occ = nullptr;
+    hipEvent_t ev_params = nullptr;  // main: the last step's hash-table Adam is done
+    hipEvent_t ev_dl = nullptr;      // main: this step's MLP output gradients are written
+    hipEvent_t ev_mlp = nullptr;     // side: this step's MLP Adam is done
     std::vector<StageTimer> pending;
     std::map<std::string, std::pair<double, long>> stats;
 };
@@ -186,7 +189,11 @@ void InstantNerf::freeBuffers()
         if (b.ev_fork) (void)hipEventDestroy(b.ev_fork);
         if (b.ev_join) (void)hipEventDestroy(b.ev_join);
         if (b.ev_done) (void)hipEventDestroy(b.ev_done);
+        if (b.ev_done_occ) (void)hipEventDestroy(b.ev_done_occ);
         if (b.ev_params) (void)hipEventDestroy(b.ev_params);
+        if (b.ev_dl) (void)hipEventDestroy(b.ev_dl);
+        if (b.ev_mlp) (void)hipEventDestroy(b.ev_mlp);
+        if (b.occ) (void)hipStreamDestroy(b.occ);
         if (b.side) (void)hipStreamDestroy(b.side);
         for (auto& t : b.pending) {
             (void)hipEventDestroy(t.a);
@@ -304,7 +311,11 @@ void InstantNerf::allocate()
     GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_fork, hipEventDisableTiming));
     GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_join, hipEventDisableTiming));
     GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_done, hipEventDisableTiming));
+    GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_done_occ, hipEventDisableTiming));
     GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_params, hipEventDisableTiming));
+    GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_dl, hipEventDisableTiming));
+    GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_mlp, hipEventDisableTiming));
+    GRAFT_HIP_CHECK(hipStreamCreateWithFlags(&b.occ, hipStreamNonBlocking));
     GRAFT_HIP_CHECK(hipStreamCreateWithFlags(&b.side, hipStreamNonBlocking));
 
     // The color head's activation-0 buffer receives the SH gather output directly.
@@ -394,9 +405,10 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         S.raysDone = raysDone;
     };
 
-    // the side stream starts after everything the caller queued (rays, grid)
+    // the side streams start after everything the caller queued (rays, grid)
     GRAFT_HIP_CHECK(hipEventRecord(b.ev_fork, stream));
     GRAFT_HIP_CHECK(hipStreamWaitEvent(b.side, b.ev_fork, 0));
+    GRAFT_HIP_CHECK(hipStreamWaitEvent(b.occ, b.ev_fork, 0));
     b.cache_version = -1;  // new rays: nothing cached
     int k = 0, i = 0;
     compact(k, 0);
@@ -413,22 +425,28 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         b.last_set = k;
 
         // InstantNerf.cu:488-494: the refresh changes only the grid that later
-        // batches march and reads only the density head, so it runs on the
-        // side stream (after this batch's compaction, before the next one's)
-        // beside this step's forward/backward; the density head's Adam update
-        // waits for it, so it sees the same parameters as in the serial order.
+        // batches march and reads only the density head, so it runs on its
+        // own stream beside this step's forward/backward, on the parameters
+        // the previous step's Adam left; this step's Adam updates and the
+        // next batch's march wait for it, so every kernel sees the same
+        // parameters and grid as in the serial order.
         const bool refresh = (m_trainSteps % 16 == 0);
         if (refresh) {
-            // density inference on the parameters after the previous step's Adam
-            if (i > 0) GRAFT_HIP_CHECK(hipStreamWaitEvent(b.side, b.ev_params, 0));
-            stage_on(b.side, "occupancy", [&] {
-                if (m_trainSteps < 256) earlyOccupancyGridUpdate(b.side);
-                else lateOccupancyGridUpdate(b.side);
+            if (i > 0) {
+                GRAFT_HIP_CHECK(hipStreamWaitEvent(b.occ, b.ev_params, 0));
+                GRAFT_HIP_CHECK(hipStreamWaitEvent(b.occ, b.ev_mlp, 0));
+            }
+            stage_on(b.occ, "occupancy", [&] {
+                if (m_trainSteps < 256) earlyOccupancyGridUpdate(b.occ);
+                else lateOccupancyGridUpdate(b.occ);
             });
-            GRAFT_HIP_CHECK(hipEventRecord(b.ev_join, b.side));
+            GRAFT_HIP_CHECK(hipEventRecord(b.ev_join, b.occ));
         }
 
         GRAFT_HIP_CHECK(hipStreamWaitEvent(stream, S.ev_ready, 0));
+        // the previous step's MLP weight gradients have been read and its Adam
+        // has updated the weights this forward uses
+        if (i > 0) GRAFT_HIP_CHECK(hipStreamWaitEvent(stream, b.ev_mlp, 0));
         // hash encode + density head, SH gather (into the colour head's
         // activation 0), colour head: one launch, activations saved
         stage("forward", [&] {
@@ -496,30 +514,63 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
             ga.total_rays = numRays;
             graft::render_grad(ca, ga, d_rays, R, stream);
         });
-        stage("colorBwd", [&] {
+        // The hash scatter waits only for dL/d(encoding): the main stream runs
+        // the dX chain of both heads (dX-only kernels for the NeRF shapes) and
+        // the side stream the weight gradients and MLP Adam beside the scatter.
+        const bool dx_only = graft::mlp_has_dx_kernel(cshape) && graft::mlp_has_dx_kernel(dshape);
+        if (dx_only) {
+            stage("colorDx", [&] {
+                graft::mlp_backward_dx(cshape, cb.dloss, cb.activations, cb.fwd_weights, b.color_dx, (int)Bn, stream,
+                                       d_hits);
+            });
+            stage("densityGrad", [&] { graft::density_grad(d_hits, Bn, b.dsigma, b.color_dx, db.dloss, stream); });
+            stage("densityDx", [&] {
+                graft::mlp_backward_dx(dshape, db.dloss, db.activations, db.fwd_weights, db.dx_out, (int)Bn, stream,
+                                       d_hits);
+            });
+            GRAFT_HIP_CHECK(hipEventRecord(b.ev_dl, stream));
+            GRAFT_HIP_CHECK(hipStreamWaitEvent(b.side, b.ev_dl, 0));
             // this step's gradient overwrites the last one: no zero_grad pass
-            graft::mlp_backward(cshape, cb.dloss, cb.activations, cb.fwd_weights, cb.w_grad, cb.b_grad, b.color_dx,
-                                (int)Bn, stream, d_hits, /*accumulate=*/false);
-        });
-        stage("densityGrad", [&] { graft::density_grad(d_hits, Bn, b.dsigma, b.color_dx, db.dloss, stream); });
-        stage("densityBwd", [&] {
-            graft::mlp_backward(dshape, db.dloss, db.activations, db.fwd_weights, db.w_grad, db.b_grad, db.dx_out,
-                                (int)Bn, stream, d_hits,
-                                /*accumulate=*/false);
-        });
+            stage_on(b.side, "colorBwd", [&] {
+                graft::mlp_backward(cshape, cb.dloss, cb.activations, cb.fwd_weights, cb.w_grad, cb.b_grad, nullptr,
+                                    (int)Bn, b.side, d_hits, /*accumulate=*/false);
+            });
+            stage_on(b.side, "densityBwd", [&] {
+                graft::mlp_backward(dshape, db.dloss, db.activations, db.fwd_weights, db.w_grad, db.b_grad, nullptr,
+                                    (int)Bn, b.side, d_hits, /*accumulate=*/false);
+            });
+        } else {
+            stage("colorBwd", [&] {
+                graft::mlp_backward(cshape, cb.dloss, cb.activations, cb.fwd_weights, cb.w_grad, cb.b_grad,
+                                    b.color_dx, (int)Bn, stream, d_hits, /*accumulate=*/false);
+            });
+            stage("densityGrad", [&] { graft::density_grad(d_hits, Bn, b.dsigma, b.color_dx, db.dloss, stream); });
+            stage("densityBwd", [&] {
+                graft::mlp_backward(dshape, db.dloss, db.activations, db.fwd_weights, db.w_grad, db.b_grad,
+                                    db.dx_out, (int)Bn, stream, d_hits, /*accumulate=*/false);
+            });
+            GRAFT_HIP_CHECK(hipEventRecord(b.ev_dl, stream));
+            GRAFT_HIP_CHECK(hipStreamWaitEvent(b.side, b.ev_dl, 0));
+        }
         stage("hashScatter", [&] {
             graft::hash_scatter(b.meta, db.dx_out, reinterpret_cast<const float*>(S.positions), 4, db.hashtable_grads,
                                 (int)Bn, stream, d_hits);
         });
         GRAFT_HIP_CHECK(hipEventRecord(S.ev_free, stream));  // the last read of this set
-        stage("colorOpt", [&] {
-            m_colorMLP->step(o.learningRate, o.beta1, o.beta2, o.epsilon, o.lossScale, stream);
+        // Adam: MLP layers of both heads on the side stream, the hash table on
+        // the main stream; both after the refresh has read the parameters
+        if (refresh) {
+            GRAFT_HIP_CHECK(hipStreamWaitEvent(stream, b.ev_join, 0));
+            GRAFT_HIP_CHECK(hipStreamWaitEvent(b.side, b.ev_join, 0));
+        }
+        stage_on(b.side, "colorOpt", [&] {
+            m_colorMLP->step(o.learningRate, o.beta1, o.beta2, o.epsilon, o.lossScale, b.side);
         });
-        if (refresh) GRAFT_HIP_CHECK(hipStreamWaitEvent(stream, b.ev_join, 0));
         stage("densityOpt", [&] {
-            m_densityMLP->step(o.learningRate, o.beta1, o.beta2, o.epsilon, o.lossScale, stream);
+            m_densityMLP->stepSplit(o.learningRate, o.beta1, o.beta2, o.epsilon, o.lossScale, b.side, stream);
         });
         GRAFT_HIP_CHECK(hipEventRecord(b.ev_params, stream));
+        GRAFT_HIP_CHECK(hipEventRecord(b.ev_mlp, b.side));
 
         trainStepCount++;
         m_trainSteps++;
@@ -535,9 +586,11 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         k ^= 1;
         compact(k, raysDone + active);
     }
-    // nothing of this call stays on the side stream past the return
+    // nothing of this call stays on the side streams past the return
     GRAFT_HIP_CHECK(hipEventRecord(b.ev_done, b.side));
     GRAFT_HIP_CHECK(hipStreamWaitEvent(stream, b.ev_done, 0));
+    GRAFT_HIP_CHECK(hipEventRecord(b.ev_done_occ, b.occ));
+    GRAFT_HIP_CHECK(hipStreamWaitEvent(stream, b.ev_done_occ, 0));
 
     if (o.isProfiling && !b.pending.empty()) {
         GRAFT_HIP_CHECK(hipEventSynchronize(b.pending.back().b));

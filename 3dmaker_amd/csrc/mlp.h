@@ -42,6 +42,13 @@ void mlp_backward(const MlpShape& s, const __half* dy, const __half* const* acts
                   const __half* const* W, float* const* dW, float* const* dB, __half* dx, int N,
                   hipStream_t stream, const uint32_t* d_n = nullptr, bool accumulate = true);
 
+// dx = dL/dx alone, bitwise the dx of mlp_backward, for the NeRF head shapes
+// (32-64-16, 2 layers; 32-64-8, 3 layers); returns false for other shapes.
+// mlp_backward(..., dx = nullptr) then yields the weight gradients.
+bool mlp_backward_dx(const MlpShape& s, const __half* dy, const __half* const* acts, const __half* const* W,
+                     __half* dx, int N, hipStream_t stream, const uint32_t* d_n = nullptr);
+bool mlp_has_dx_kernel(const MlpShape& s);
+
 // The forward of a NeRF step (hash encode + density head, SH gather, colour
 // head) in one launch; bitwise equal to mlp_forward(density), sh_gather,
 // mlp_forward(colour).  dacts / density_out / cacts / color_in may be null

@@ -547,6 +547,66 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
     for (int e = tid; e < p.P; e += blockDim.x) dstp[e] = sred[e];
 }
 
+// dL/dx alone (no dW/db) for the NeRF head shapes: the same chain of MFMAs
+// as mlp_bwd_head_kernel's dX in the same order, so the result is bitwise its
+// dx.  A caller that needs dx first (the hash scatter waits for it) runs this,
+// and the weight gradients later with mlp_backward(dx = nullptr), which
+// recomputes the chain beside other work.
+template <int IN, int HID, int OUT, int LAYERS>
+__global__ __launch_bounds__(256) void mlp_bwd_dx_kernel(const BwdParams p)
+{
+    using S = HeadShape<IN, HID, OUT, LAYERS>;
+    constexpr int MB = 4;
+    extern __shared__ __align__(16) unsigned char smem[];
+    _Float16* sfrag = reinterpret_cast<_Float16*>(smem);
+    stage_fragments<true>(sfrag, p.W, IN, HID, OUT, LAYERS);
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, r = lane & 15;
+    const int N = p.d_n ? min((int)*p.d_n, p.N) : p.N;
+    const int ntiles = (N + 15) >> 4;
+    for (int tile = blockIdx.x * 4 + wave; tile < ntiles; tile += gridDim.x * 4) {
+        const int n = tile * 16 + r;
+        const bool valid = n < N;
+        h4 G[MB];
+#pragma unroll
+        for (int ob = 0; ob < MB; ob++) {
+            const int col = 16 * ob + 4 * g;
+            G[ob] = (ob < S::ob(LAYERS - 1) && valid && col < OUT) ? ld_h4(p.dy + (size_t)n * OUT + col) : h4zero();
+        }
+#pragma unroll
+        for (int l = LAYERS - 1; l >= 0; l--) {
+            const int in_l = S::in_l(l);
+            const _Float16* fr = sfrag + p.fragT_off[l] + lane * 4;
+            h4 Gn[MB];
+#pragma unroll
+            for (int ib = 0; ib < MB; ib++) {
+                Gn[ib] = h4zero();
+                if (ib >= S::ib(l)) continue;
+                f4 d = f4zero();
+#pragma unroll
+                for (int ob = 0; ob < MB; ob++)
+                    if (ob < S::ob(l)) d = mfma16(*reinterpret_cast<const h4*>(fr + (ib * S::ob(l) + ob) * 256), G[ob], d);
+                h4 h;
+#pragma unroll
+                for (int j = 0; j < 4; j++) h[j] = to_h(d[j]);
+                const int col = 16 * ib + 4 * g;
+                if (l > 0) {
+                    // ReLU mask of this layer's input activation
+                    const h4 X = valid ? ld_h4(p.acts[l] + (size_t)n * in_l + col) : h4zero();
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        if (!((float)X[j] > 0.f)) h[j] = (_Float16)0.f;
+                } else if (valid && col < IN) {
+                    st_h4(p.dx + (size_t)n * IN + col, h);
+                }
+                Gn[ib] = h;
+            }
+#pragma unroll
+            for (int b = 0; b < MB; b++) G[b] = Gn[b];
+        }
+    }
+}
+
 // grad[p] += sum over blocks of ws[b][p], summed in block order.
 struct ReduceParams {
     const float* ws;
@@ -713,6 +773,43 @@ void mlp_forward(const MlpShape& s, const FwdInput& in, const __half* const* W,
     }
 #undef GRAFT_FWD_LAUNCH
     GRAFT_LAUNCH_CHECK();
+}
+
+bool mlp_has_dx_kernel(const MlpShape& s)
+{
+    return s.in == 32 && s.hid == 64 && (s.out == 16 && s.layers == 2 || s.out == 8 && s.layers == 3);
+}
+
+bool mlp_backward_dx(const MlpShape& s, const __half* dy, const __half* const* acts, const __half* const* W,
+                     __half* dx, int N, hipStream_t stream, const uint32_t* d_n)
+{
+    s.validate();
+    if (!mlp_has_dx_kernel(s)) return false;
+    const bool density_head = s.out == 16;
+    if (dx == nullptr) throw std::runtime_error("TinyMLP: dX-only backward needs dx");
+    if (N <= 0) return true;
+    BwdParams p{};
+    p.dy = reinterpret_cast<const _Float16*>(dy);
+    p.acts = reinterpret_cast<const _Float16* const*>(acts);
+    p.W = reinterpret_cast<const _Float16* const*>(W);
+    p.dx = reinterpret_cast<_Float16*>(dx);
+    p.d_n = d_n;
+    p.N = N;
+    p.in = s.in;
+    p.hid = s.hid;
+    p.out_dim = s.out;
+    p.layers = s.layers;
+    int frag_halves = 0, unused = 0;
+    fill_layer_offsets(s, true, p.fragT_off, nullptr, frag_halves, unused);
+    const int lds = frag_halves * 2;
+    const auto kern = density_head ? mlp_bwd_dx_kernel<32, 64, 16, 2> : mlp_bwd_dx_kernel<32, 64, 8, 3>;
+    int per_cu = 0;
+    GRAFT_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, lds));
+    const int ntiles = (N + 15) / 16;
+    const int blocks = std::max(1, std::min((ntiles + 3) / 4, num_cus() * std::max(1, per_cu)));
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), lds, stream, p);
+    GRAFT_LAUNCH_CHECK();
+    return true;
 }
 
 void mlp_backward(const MlpShape& s, const __half* dy, const __half* const* acts,

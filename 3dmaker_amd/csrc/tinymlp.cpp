@@ -773,6 +773,19 @@ void TinyMLPHashGrid::step(float lr, float beta1, float beta2, float epsilon, fl
                      (size_t)m_totalHashElements, a, stream);
 }
 
+void TinyMLPHashGrid::stepSplit(float lr, float beta1, float beta2, float epsilon, float loss_scale,
+                                hipStream_t mlp_stream, hipStream_t hash_stream)
+{
+    if (!m_isTraining) throw std::runtime_error("step called while in inference mode!");
+    if (current_step < 50000) current_step++;
+    const AdamArgs a = adam_args(current_step, lr, beta1, beta2, epsilon, loss_scale);
+    const Dims d = dims_of(mlp_opt);
+    graft::adam_dense(d_master_weights, d_fwd_weights, d_w_grad, d_w_m, d_w_v, d.wsizes(), d_master_biases,
+                      d_b_grad, d_b_m, d_b_v, d.bsizes(), d.layers, a, mlp_stream);
+    graft::adam_hash(d_master_hashtable, d_fwd_hashtable, d_hashtable_grads, d_hash_m, d_hash_v,
+                     (size_t)m_totalHashElements, a, hash_stream);
+}
+
 // TinyMLPHashGrid.cu:394-455: raw MLPGridOptions header, fp32 table, then W, B per layer.
 void TinyMLPHashGrid::loadWeights(const std::string& filename)
 {

@@ -467,7 +467,8 @@ def main():
     roofline = {"bound": bound, "kernel": dom, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom),
                 "algorithmic_bytes_per_launch": int(algo), "avg_launch_ms": round(dom_ms, 4)}
-    mlp_ms = sum(st[k][0] for k in ("forward", "colorBwd", "densityBwd") if k in st)
+    # MLP stages: the fused forward, the dX chains (main stream) and the weight gradients (side stream)
+    mlp_ms = sum(st[k][0] for k in ("forward", "colorDx", "densityDx", "colorBwd", "densityBwd") if k in st)
     mfma_util = MLP_FLOP_PER_SAMPLE * n_prof / (mlp_ms * 1e-3) / 1e12 / FP16_PEAK_TFLOPS if mlp_ms else None
 
     out = {

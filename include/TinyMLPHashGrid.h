@@ -64,7 +64,13 @@ public:
     void loadHashgrid(const float* host_hashgrid);
     void saveHashgrid(float* host_hashgrid);
 
-    // ---- additions (no reference counterpart): introspection for tests ----
+    // ---- additions (no reference counterpart) ----
+    // step() with its two updates on two streams: the MLP layers on
+    // mlp_stream, the hash table on hash_stream (one Adam step count for both).
+    void stepSplit(float lr, float beta1, float beta2, float epsilon, float loss_scale, hipStream_t mlp_stream,
+                   hipStream_t hash_stream);
+
+    // introspection for tests
     struct Buffers {
         float* master_hashtable;
         half* fwd_hashtable;

@@ -481,13 +481,33 @@ def test_instant_nerf_step_matches_oracle_chain(dev):
     # colour backward (dX) and density gradient
     cgp = np.zeros((N, 8), np.float16)
     cgp[:, :3] = cg
-    h = [d2h(p, (N, 64), np.float16) for p in ptr_array(nerf.color.buffers().activations, 3)[1:]]
-    _, _, cdx_ref = orc.mlp_backward(cgp, cin, np.stack(h), cW.astype(np.float16), 32, 64, 8, 3)
+    cbuf = nerf.color.buffers()
+    h = [d2h(p, (N, 64), np.float16) for p in ptr_array(cbuf.activations, 3)[1:]]
+    cdW_ref, cdB_ref, cdx_ref = orc.mlp_backward(cgp, cin, np.stack(h), cW.astype(np.float16), 32, 64, 8, 3)
     cdx = d2h(b.color_dx, (N, 32), np.float16)
     scale = max(1.0, float(np.abs(cdx_ref.astype(np.float32)).max()))
     assert_close(cdx, cdx_ref, atol=2e-3 * scale, what="color dL/dinput")
-    np.testing.assert_array_equal(d2h(b.density_grad, (N, 16), np.float16).view(np.uint16),
-                                  orc.density_grad(got_ds, cdx).view(np.uint16))
+    # the colour head's weight gradients (computed beside the hash scatter)
+    sizes = [64 * 32, 64 * 64, 8 * 64]
+    cdW = np.concatenate([d2h(p, (n,), np.float32) for p, n in zip(ptr_array(cbuf.w_grad, 3), sizes)])
+    cdB = np.concatenate([d2h(p, (n,), np.float32) for p, n in zip(ptr_array(cbuf.b_grad, 3), [64, 64, 8])])
+    assert_close(cdW, cdW_ref, atol=2e-3 * max(1.0, float(np.abs(cdW_ref).max())), what="color dW")
+    assert_close(cdB, cdB_ref, atol=2e-3 * max(1.0, float(np.abs(cdB_ref).max())), what="color db")
+    dg = d2h(b.density_grad, (N, 16), np.float16)
+    np.testing.assert_array_equal(dg.view(np.uint16), orc.density_grad(got_ds, cdx).view(np.uint16))
+    # density head: dL/d(encoding) on the main stream, weight gradients beside the scatter
+    gbuf = nerf.density.buffers()
+    acts = ptr_array(gbuf.activations, 2)
+    enc = d2h(acts[0], (N, 32), np.float16)
+    h1 = d2h(acts[1], (N, 64), np.float16)
+    ddW_ref, ddB_ref, denc_ref = orc.mlp_backward(dg, enc, h1[None], dW.astype(np.float16), 32, 64, 16, 2)
+    denc = d2h(gbuf.dx_out, (N, 32), np.float16)
+    assert_close(denc, denc_ref, atol=2e-3 * max(1.0, float(np.abs(denc_ref.astype(np.float32)).max())),
+                 what="dL/d(encoding)")
+    ddW = np.concatenate([d2h(p, (n,), np.float32) for p, n in zip(ptr_array(gbuf.w_grad, 2), [64 * 32, 16 * 64])])
+    ddB = np.concatenate([d2h(p, (n,), np.float32) for p, n in zip(ptr_array(gbuf.b_grad, 2), [64, 16])])
+    assert_close(ddW, ddW_ref, atol=2e-3 * max(1.0, float(np.abs(ddW_ref).max())), what="density dW")
+    assert_close(ddB, ddB_ref, atol=2e-3 * max(1.0, float(np.abs(ddB_ref).max())), what="density db")
     # the step moved the parameters and kept them finite
     t2 = np.zeros_like(table)
     nerf.density.save_hashgrid(t2)
