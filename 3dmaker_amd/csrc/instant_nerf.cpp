@@ -23,6 +23,11 @@
 
 namespace {
 
+// Events that only order streams on this device: a device-scope release is
+// enough (the host never inspects them), and avoids the system-scope cache
+// writeback of a default event between the kernels it separates.
+constexpr unsigned kStreamEvent = hipEventDisableTiming | hipEventReleaseToDevice;
+
 struct StageTimer {
     const char* name;
     hipEvent_t a, b;
@@ -286,8 +291,8 @@ void InstantNerf::allocate()
         GRAFT_HIP_CHECK(hipMemset(S.result, 0, 2 * sizeof(uint32_t)));
         GRAFT_HIP_CHECK(hipHostMalloc((void**)&S.h_result, 2 * sizeof(uint32_t), hipHostMallocDefault));
         GRAFT_HIP_CHECK(hipEventCreateWithFlags(&S.ev_result, hipEventDisableTiming));
-        GRAFT_HIP_CHECK(hipEventCreateWithFlags(&S.ev_ready, hipEventDisableTiming));
-        GRAFT_HIP_CHECK(hipEventCreateWithFlags(&S.ev_free, hipEventDisableTiming));
+        GRAFT_HIP_CHECK(hipEventCreateWithFlags(&S.ev_ready, kStreamEvent));
+        GRAFT_HIP_CHECK(hipEventCreateWithFlags(&S.ev_free, kStreamEvent));
     }
     b.render_rgb = dalloc<float>(3 * R);
     b.render_depth = dalloc<float>(R);
@@ -308,13 +313,13 @@ void InstantNerf::allocate()
     b.active_list = dalloc<int>((size_t)N);
     b.active_count = dalloc<int>(1);
     b.list_scratch = dalloc<uint32_t>(graft::occ_list_scratch_words(N));
-    GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_fork, hipEventDisableTiming));
-    GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_join, hipEventDisableTiming));
-    GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_done, hipEventDisableTiming));
-    GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_done_occ, hipEventDisableTiming));
-    GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_params, hipEventDisableTiming));
-    GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_dl, hipEventDisableTiming));
-    GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_mlp, hipEventDisableTiming));
+    GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_fork, kStreamEvent));
+    GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_join, kStreamEvent));
+    GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_done, kStreamEvent));
+    GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_done_occ, kStreamEvent));
+    GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_params, kStreamEvent));
+    GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_dl, kStreamEvent));
+    GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_mlp, kStreamEvent));
     GRAFT_HIP_CHECK(hipStreamCreateWithFlags(&b.occ, hipStreamNonBlocking));
     GRAFT_HIP_CHECK(hipStreamCreateWithFlags(&b.side, hipStreamNonBlocking));
 
