@@ -522,17 +522,36 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         // The hash scatter waits only for dL/d(encoding): the main stream runs
         // the dX chain of both heads (dX-only kernels for the NeRF shapes) and
         // the side stream the weight gradients and MLP Adam beside the scatter.
+        graft::NerfBwdDxArgs bx;
+        bx.cshape = cshape;
+        bx.dshape = dshape;
+        bx.color_dy = cb.dloss;
+        bx.cacts = cb.activations;
+        bx.cW = cb.fwd_weights;
+        bx.dsigma = b.dsigma;
+        bx.dacts = db.activations;
+        bx.dW = db.fwd_weights;
+        bx.color_dx = b.color_dx;
+        bx.density_dy = db.dloss;
+        bx.denc = db.dx_out;
+        const bool fused_dx = graft::nerf_backward_dx(bx, 0, stream);  // shape check only (N = 0)
         const bool dx_only = graft::mlp_has_dx_kernel(cshape) && graft::mlp_has_dx_kernel(dshape);
-        if (dx_only) {
-            stage("colorDx", [&] {
-                graft::mlp_backward_dx(cshape, cb.dloss, cb.activations, cb.fwd_weights, b.color_dx, (int)Bn, stream,
-                                       d_hits);
-            });
-            stage("densityGrad", [&] { graft::density_grad(d_hits, Bn, b.dsigma, b.color_dx, db.dloss, stream); });
-            stage("densityDx", [&] {
-                graft::mlp_backward_dx(dshape, db.dloss, db.activations, db.fwd_weights, db.dx_out, (int)Bn, stream,
-                                       d_hits);
-            });
+        if (fused_dx || dx_only) {
+            if (fused_dx) {
+                // colour dX chain, density-gradient glue, density dX chain: one launch
+                stage("backwardDx", [&] { graft::nerf_backward_dx(bx, (int)Bn, stream, d_hits); });
+            } else {
+                stage("colorDx", [&] {
+                    graft::mlp_backward_dx(cshape, cb.dloss, cb.activations, cb.fwd_weights, b.color_dx, (int)Bn,
+                                           stream, d_hits);
+                });
+                stage("densityGrad",
+                      [&] { graft::density_grad(d_hits, Bn, b.dsigma, b.color_dx, db.dloss, stream); });
+                stage("densityDx", [&] {
+                    graft::mlp_backward_dx(dshape, db.dloss, db.activations, db.fwd_weights, db.dx_out, (int)Bn,
+                                           stream, d_hits);
+                });
+            }
             GRAFT_HIP_CHECK(hipEventRecord(b.ev_dl, stream));
             GRAFT_HIP_CHECK(hipStreamWaitEvent(b.side, b.ev_dl, 0));
             // this step's gradient overwrites the last one: no zero_grad pass

@@ -77,4 +77,23 @@ struct NerfFwdArgs {
 };
 void nerf_forward(const NerfFwdArgs& a, int N, hipStream_t stream, const uint32_t* d_n = nullptr);
 
+// The dX part of a NeRF step's backward in one launch: colour dL/dinput,
+// density dL/dy (colour dL/dinput[0..15] + d sigma on the logit, clamped) and
+// dL/d(encoding); bitwise equal to mlp_backward_dx(colour), density_grad,
+// mlp_backward_dx(density).  Only for the head shapes 32-64-64-8 and
+// 32-64-16; returns false for others.
+struct NerfBwdDxArgs {
+    MlpShape cshape, dshape;
+    const __half* color_dy = nullptr;       // [N x 8]
+    const __half* const* cacts = nullptr;
+    const __half* const* cW = nullptr;
+    const float* dsigma = nullptr;          // [N]
+    const __half* const* dacts = nullptr;
+    const __half* const* dW = nullptr;
+    __half* color_dx = nullptr;             // [N x 32]
+    __half* density_dy = nullptr;           // [N x 16]
+    __half* denc = nullptr;                 // [N x 32]
+};
+bool nerf_backward_dx(const NerfBwdDxArgs& a, int N, hipStream_t stream, const uint32_t* d_n = nullptr);
+
 }  // namespace graft

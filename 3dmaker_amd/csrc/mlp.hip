@@ -392,17 +392,6 @@ __device__ __forceinline__ h4 tile_transpose(h4 v, h4 id, bool exact_slow, int l
     return out;
 }
 
-template <int IN, int HID, int OUT, int LAYERS>
-struct HeadShape {
-    static constexpr int in_l(int l) { return l == 0 ? IN : HID; }
-    static constexpr int out_l(int l) { return l == LAYERS - 1 ? OUT : HID; }
-    static constexpr int ib(int l) { return (in_l(l) + 15) / 16; }
-    static constexpr int ob(int l) { return (out_l(l) + 15) / 16; }
-    static constexpr int acc_off(int l) { return l == 0 ? 0 : acc_off(l - 1) + ob(l - 1) * ib(l - 1); }
-    static constexpr int nacc() { return acc_off(LAYERS - 1) + ob(LAYERS - 1) * ib(LAYERS - 1); }
-    static constexpr int db_off(int l) { return l == 0 ? 0 : db_off(l - 1) + ob(l - 1); }
-    static constexpr int ndb() { return db_off(LAYERS - 1) + ob(LAYERS - 1); }
-};
 
 template <int IN, int HID, int OUT, int LAYERS>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void mlp_bwd_head_kernel(const BwdParams p)
@@ -556,7 +545,6 @@ template <int IN, int HID, int OUT, int LAYERS>
 __global__ __launch_bounds__(256) void mlp_bwd_dx_kernel(const BwdParams p)
 {
     using S = HeadShape<IN, HID, OUT, LAYERS>;
-    constexpr int MB = 4;
     extern __shared__ __align__(16) unsigned char smem[];
     _Float16* sfrag = reinterpret_cast<_Float16*>(smem);
     stage_fragments<true>(sfrag, p.W, IN, HID, OUT, LAYERS);
@@ -567,42 +555,17 @@ __global__ __launch_bounds__(256) void mlp_bwd_dx_kernel(const BwdParams p)
     for (int tile = blockIdx.x * 4 + wave; tile < ntiles; tile += gridDim.x * 4) {
         const int n = tile * 16 + r;
         const bool valid = n < N;
-        h4 G[MB];
+        h4 G[4];
 #pragma unroll
-        for (int ob = 0; ob < MB; ob++) {
+        for (int ob = 0; ob < 4; ob++) {
             const int col = 16 * ob + 4 * g;
             G[ob] = (ob < S::ob(LAYERS - 1) && valid && col < OUT) ? ld_h4(p.dy + (size_t)n * OUT + col) : h4zero();
         }
+        dx_chain<IN, HID, OUT, LAYERS>(G, sfrag, p.fragT_off, p.acts, n, valid, lane);
 #pragma unroll
-        for (int l = LAYERS - 1; l >= 0; l--) {
-            const int in_l = S::in_l(l);
-            const _Float16* fr = sfrag + p.fragT_off[l] + lane * 4;
-            h4 Gn[MB];
-#pragma unroll
-            for (int ib = 0; ib < MB; ib++) {
-                Gn[ib] = h4zero();
-                if (ib >= S::ib(l)) continue;
-                f4 d = f4zero();
-#pragma unroll
-                for (int ob = 0; ob < MB; ob++)
-                    if (ob < S::ob(l)) d = mfma16(*reinterpret_cast<const h4*>(fr + (ib * S::ob(l) + ob) * 256), G[ob], d);
-                h4 h;
-#pragma unroll
-                for (int j = 0; j < 4; j++) h[j] = to_h(d[j]);
-                const int col = 16 * ib + 4 * g;
-                if (l > 0) {
-                    // ReLU mask of this layer's input activation
-                    const h4 X = valid ? ld_h4(p.acts[l] + (size_t)n * in_l + col) : h4zero();
-#pragma unroll
-                    for (int j = 0; j < 4; j++)
-                        if (!((float)X[j] > 0.f)) h[j] = (_Float16)0.f;
-                } else if (valid && col < IN) {
-                    st_h4(p.dx + (size_t)n * IN + col, h);
-                }
-                Gn[ib] = h;
-            }
-#pragma unroll
-            for (int b = 0; b < MB; b++) G[b] = Gn[b];
+        for (int ib = 0; ib < S::ib(0); ib++) {
+            const int col = 16 * ib + 4 * g;
+            if (valid && col < IN) st_h4(p.dx + (size_t)n * IN + col, G[ib]);
         }
     }
 }

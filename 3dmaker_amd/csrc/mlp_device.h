@@ -1,4 +1,4 @@
-// Device building blocks of the fused MLP kernels (mlp.hip, nerf_fwd.hip).
+// Device building blocks of the fused MLP kernels (mlp.hip, nerf_fused.hip).
 //
 // Layout: activations travel as the B operand of v_mfma_f32_16x16x16f16 with
 // samples along N and features along K.  The D layout of one 16x16 MFMA (lane
@@ -86,6 +86,62 @@ __device__ __forceinline__ void stage_biases(float* __restrict__ sbias, const fl
         const int out_l = l == layers - 1 ? out : hid;
         for (int e = threadIdx.x; e < tiles16(out_l) * 16; e += blockDim.x)
             sbias[bias_off[l] + e] = e < out_l ? B[l][e] : 0.f;
+    }
+}
+
+// Compile-time layer shapes of a net whose widths are all <= 64 (at most four
+// 16-wide blocks per layer): ib/ob = input/output blocks of layer l.
+template <int IN, int HID, int OUT, int LAYERS>
+struct HeadShape {
+    static constexpr int in_l(int l) { return l == 0 ? IN : HID; }
+    static constexpr int out_l(int l) { return l == LAYERS - 1 ? OUT : HID; }
+    static constexpr int ib(int l) { return (in_l(l) + 15) / 16; }
+    static constexpr int ob(int l) { return (out_l(l) + 15) / 16; }
+    static constexpr int acc_off(int l) { return l == 0 ? 0 : acc_off(l - 1) + ob(l - 1) * ib(l - 1); }
+    static constexpr int nacc() { return acc_off(LAYERS - 1) + ob(LAYERS - 1) * ib(LAYERS - 1); }
+    static constexpr int db_off(int l) { return l == 0 ? 0 : db_off(l - 1) + ob(l - 1); }
+    static constexpr int ndb() { return db_off(LAYERS - 1) + ob(LAYERS - 1); }
+};
+
+// The dX chain of one 16-sample tile through a net whose transposed weight
+// fragments are staged (stage_fragments<true>): G holds dL/dy of the last
+// layer (S layout: lane (r, g) has features 4 g .. 4 g + 3 of K-block b of
+// sample r); on return G holds dL/dx of layer 0's input.  Each layer's dX is
+// rounded to fp16 and masked where that layer's input activation is <= 0
+// (not at layer 0).  acts is the device array of per-layer activations.
+template <int IN, int HID, int OUT, int LAYERS>
+__device__ __forceinline__ void dx_chain(h4 (&G)[4], const _Float16* sfrag, const int* fragT_off,
+                                         const _Float16* const* acts, int n, bool valid, int lane)
+{
+    using S = HeadShape<IN, HID, OUT, LAYERS>;
+    const int g = lane >> 4;
+#pragma unroll
+    for (int l = LAYERS - 1; l >= 0; l--) {
+        const int in_l = S::in_l(l);
+        const _Float16* fr = sfrag + fragT_off[l] + lane * 4;
+        h4 Gn[4];
+#pragma unroll
+        for (int ib = 0; ib < 4; ib++) {
+            Gn[ib] = h4zero();
+            if (ib >= S::ib(l)) continue;
+            f4 d = f4zero();
+#pragma unroll
+            for (int ob = 0; ob < 4; ob++)
+                if (ob < S::ob(l)) d = mfma16(*reinterpret_cast<const h4*>(fr + (ib * S::ob(l) + ob) * 256), G[ob], d);
+            h4 h;
+#pragma unroll
+            for (int j = 0; j < 4; j++) h[j] = to_h(d[j]);
+            if (l > 0) {
+                const int col = 16 * ib + 4 * g;
+                const h4 X = valid ? ld_h4(acts[l] + (size_t)n * in_l + col) : h4zero();
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    if (!((float)X[j] > 0.f)) h[j] = (_Float16)0.f;
+            }
+            Gn[ib] = h;
+        }
+#pragma unroll
+        for (int b = 0; b < 4; b++) G[b] = Gn[b];
     }
 }
 

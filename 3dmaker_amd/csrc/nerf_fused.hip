@@ -1,17 +1,23 @@
-// The forward half of a NeRF step in one kernel: hash encode + density MLP,
-// SH gather, colour MLP, per 16-sample tile in registers.
+// The two halves of a NeRF step that run per sample in one kernel each.
 //
-// The reference runs it as three launches with two HBM round trips
-// (networkFusionHashtable.cu:441-682, compute_SH_gather otherKernels.cu:
-// 156-273, networkFusion.cu:197-355).  Here the density head's output block,
-// already in the MFMA D layout that is the colour head's B layout for input
-// features 0..15, is sanitised and rounded to fp16 in place; each lane adds
-// the 4 SH coefficients of its sample it holds as features 16..31.  Every
-// value is produced by the same fp32 operations in the same order as the
-// three-launch chain, so the outputs are bitwise those of that chain.  The
-// saved buffers (density output, sigma, both heads' activations) are the
-// ones the backward reads; an inference caller passes nulls and keeps only
-// sigma and the colour output.
+// Forward: hash encode + density MLP, SH gather, colour MLP, per 16-sample
+// tile in registers.  The reference runs it as three launches with two HBM
+// round trips (networkFusionHashtable.cu:441-682, compute_SH_gather
+// otherKernels.cu:156-273, networkFusion.cu:197-355).  Here the density
+// head's output block, already in the MFMA D layout that is the colour head's
+// B layout for input features 0..15, is sanitised and rounded to fp16 in
+// place; each lane adds the 4 SH coefficients of its sample it holds as
+// features 16..31.  Every value is produced by the same fp32 operations in the
+// same order as the three-launch chain, so the outputs are bitwise those of
+// that chain.  The saved buffers (density output, sigma, both heads'
+// activations) are the ones the backward reads; an inference caller passes
+// nulls and keeps only sigma and the colour output.
+//
+// Backward, dX part: the colour head's dX chain, the density-gradient glue
+// (compute_density_grad, otherKernels.cu:506-562) and the density head's dX
+// chain, down to dL/d(encoding) for the hash scatter; bitwise the outputs of
+// the dX-only head kernels and density_grad_kernel.  The weight gradients are
+// computed apart (mlp_backward with dx = nullptr).
 #include "mlp_device.h"
 #include "nerf.h"
 
@@ -136,6 +142,72 @@ __global__ __launch_bounds__(256) void nerf_fwd_kernel(const NerfFwdParams p)
     }
 }
 
+struct NerfBwdDxParams {
+    const _Float16* cdy;              // [N x COUT] colour dL/dy (fp16)
+    const _Float16* const* cacts;     // colour activations
+    const _Float16* const* cW;
+    const float* dsigma;              // [N]
+    const _Float16* const* dacts;     // density activations
+    const _Float16* const* dW;
+    _Float16* cdx;                    // [N x 32] colour dL/dinput
+    _Float16* dloss;                  // [N x 16] density dL/dy
+    _Float16* denc;                   // [N x DIN] dL/d(encoding)
+    const uint32_t* d_n;
+    int N;
+    int c_fragT_off[kMaxLayers], d_fragT_off[kMaxLayers];
+    int d_frag_base;                  // LDS byte offset of the density fragments
+};
+
+template <int CIN, int CHID, int COUT, int CL, int DIN, int DHID, int DL>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void nerf_bwd_dx_kernel(const NerfBwdDxParams p)
+{
+    using CS = HeadShape<CIN, CHID, COUT, CL>;
+    using DS = HeadShape<DIN, DHID, 16, DL>;
+    extern __shared__ __align__(16) unsigned char smem[];
+    _Float16* cfrag = reinterpret_cast<_Float16*>(smem);
+    _Float16* dfrag = reinterpret_cast<_Float16*>(smem + p.d_frag_base);
+    stage_fragments<true>(cfrag, p.cW, CIN, CHID, COUT, CL);
+    stage_fragments<true>(dfrag, p.dW, DIN, DHID, 16, DL);
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, r = lane & 15;
+    const int N = p.d_n ? min((int)*p.d_n, p.N) : p.N;
+    const int ntiles = (N + 15) >> 4;
+    for (int tile = blockIdx.x * 4 + wave; tile < ntiles; tile += gridDim.x * 4) {
+        const int n = tile * 16 + r;
+        const bool valid = n < N;
+        h4 G[4];
+#pragma unroll
+        for (int ob = 0; ob < 4; ob++) {
+            const int col = 16 * ob + 4 * g;
+            G[ob] = (ob < CS::ob(CL - 1) && valid && col < COUT) ? ld_h4(p.cdy + (size_t)n * COUT + col) : h4zero();
+        }
+        dx_chain<CIN, CHID, COUT, CL>(G, cfrag, p.c_fragT_off, p.cacts, n, valid, lane);
+        if (valid) {
+#pragma unroll
+            for (int ib = 0; ib < CS::ib(0); ib++) st_h4(p.cdx + (size_t)n * CIN + 16 * ib + 4 * g, G[ib]);
+        }
+        // density dL/dy = colour dL/dinput[0..15] with d sigma added to the
+        // logit, clamped to the fp16 range, NaN -> 0 (density_grad_kernel)
+        h4 D;
+        const float ds = (valid && g == 0) ? p.dsigma[n] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            float f = (float)G[0][j];
+            if (g == 0 && j == 0) f += ds;
+            f = clamp_half_range(f);
+            if (f != f) f = 0.0f;
+            D[j] = to_h(f);
+        }
+        if (valid) st_h4(p.dloss + (size_t)n * 16 + 4 * g, D);
+        h4 E[4] = {D, h4zero(), h4zero(), h4zero()};
+        dx_chain<DIN, DHID, 16, DL>(E, dfrag, p.d_fragT_off, p.dacts, n, valid, lane);
+        if (valid) {
+#pragma unroll
+            for (int ib = 0; ib < DS::ib(0); ib++) st_h4(p.denc + (size_t)n * DIN + 16 * ib + 4 * g, E[ib]);
+        }
+    }
+}
+
 int pick_nt(int d)
 {
     if (d <= 32) return 2;  // the colour input alone is 32 wide
@@ -224,6 +296,45 @@ void nerf_forward(const NerfFwdArgs& a, int N, hipStream_t stream, const uint32_
     }
 #undef GRAFT_NERF_FWD
     GRAFT_LAUNCH_CHECK();
+}
+
+bool nerf_backward_dx(const NerfBwdDxArgs& a, int N, hipStream_t stream, const uint32_t* d_n)
+{
+    const bool shapes = a.cshape.in == 32 && a.cshape.hid == 64 && a.cshape.out == 8 && a.cshape.layers == 3 &&
+                        a.dshape.in == 32 && a.dshape.hid == 64 && a.dshape.out == 16 && a.dshape.layers == 2;
+    if (!shapes) return false;
+    if (N <= 0) return true;
+    NerfBwdDxParams p{};
+    p.cdy = reinterpret_cast<const _Float16*>(a.color_dy);
+    p.cacts = reinterpret_cast<const _Float16* const*>(a.cacts);
+    p.cW = reinterpret_cast<const _Float16* const*>(a.cW);
+    p.dsigma = a.dsigma;
+    p.dacts = reinterpret_cast<const _Float16* const*>(a.dacts);
+    p.dW = reinterpret_cast<const _Float16* const*>(a.dW);
+    p.cdx = reinterpret_cast<_Float16*>(a.color_dx);
+    p.dloss = reinterpret_cast<_Float16*>(a.density_dy);
+    p.denc = reinterpret_cast<_Float16*>(a.denc);
+    p.d_n = d_n;
+    p.N = N;
+    int ch = 0, dh = 0;
+    for (int l = 0; l < a.cshape.layers; l++) {
+        p.c_fragT_off[l] = ch;
+        ch += tiles16(a.cshape.out_l(l)) * tiles16(a.cshape.in_l(l)) * 256;
+    }
+    for (int l = 0; l < a.dshape.layers; l++) {
+        p.d_fragT_off[l] = dh;
+        dh += tiles16(a.dshape.out_l(l)) * tiles16(a.dshape.in_l(l)) * 256;
+    }
+    p.d_frag_base = (ch * 2 + 15) & ~15;
+    const int lds = p.d_frag_base + dh * 2;
+    const auto kern = nerf_bwd_dx_kernel<32, 64, 8, 3, 32, 64, 2>;
+    int per_cu = 0;
+    GRAFT_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, lds));
+    const int ntiles = (N + 15) / 16;
+    const int blocks = std::max(1, std::min((ntiles + 3) / 4, num_cus() * std::max(1, per_cu)));
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), lds, stream, p);
+    GRAFT_LAUNCH_CHECK();
+    return true;
 }
 
 }  // namespace graft
