@@ -125,6 +125,10 @@ __global__ __launch_bounds__(256) void hash_scatter_kernel(const GridKernelArgs 
                                                            const _Float16* __restrict__ denc,
                                                            float* __restrict__ grads)
 {
+    // This kernel's waves issue ahead of other kernels' waves on the same
+    // SIMD (the side stream's work runs beside it): its atomic stream is the
+    // step's critical path.
+    __builtin_amdgcn_s_setprio(3);
     __shared__ float ss[kMaxLevels];
     __shared__ int sr[kMaxLevels];
     stage_meta(a, ss, sr);
