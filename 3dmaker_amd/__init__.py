@@ -121,6 +121,8 @@ SIGNATURES = {
     "launchAdamHashGridOptim": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _f, _f, _f, _f, _f, _f, _f, _vp]),
     "launchHashEncodeKernel": (None, [_vp, _vp, _vp, _i, _vp, _i, _vp]),
     "tinymlp_last_error": (_i, []),
+    # include/graft_diag.h (bench support)
+    "graft_diag_atomic_line_rate": (_i, [_vp, C.c_size_t, _i, C.POINTER(C.c_double), _vp]),
     "tinymlp_last_error_message": (C.c_char_p, []),
     # include/tinymlp_capi.h (flat handle API)
     "tmlp_grid_create": (_vp, [C.POINTER(MLPGridOptions), _i, _i, _u, _i]),

@@ -65,6 +65,7 @@ SCATTER_BYTES_PER_SAMPLE = 16 + 2 * L * 2 + L * 8 * 2 * 8               # 2,128 
 ADAM_BYTES_PER_PARAM = 34
 MLP_FLOP_PER_SAMPLE = 3 * (2 * (32 * 64 + 64 * 16) + 2 * (32 * 64 + 64 * 64 + 64 * 3))  # 56,448 fwd + bwd
 COPY_BYTES = 256 << 20         # copy-calibration kernel of the PMC runs (read and write each)
+SCATTER_DWORDS_PER_REQUEST = 4  # the scatter's atomics: 4 lanes (x-corner pair x 2 features) share a line
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
 
@@ -76,6 +77,73 @@ def measured_traffic(kernel):
         return t["kernels"][kernel]["hbm_bytes_per_launch"]
     except (OSError, KeyError, ValueError):
         return None
+
+
+def d2h(ptr, shape, dtype):
+    """Copy a device buffer (raw pointer) into a new numpy array."""
+    hip = C.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    hip.hipMemcpy.restype = C.c_int
+    out = np.empty(shape, dtype)
+    if out.nbytes and hip.hipMemcpy(out.ctypes.data, int(ptr), out.nbytes, 2) != 0:
+        raise RuntimeError("hipMemcpy device-to-host failed")
+    return out
+
+
+def scatter_line_requests(pos):
+    """64-byte-line atomic requests one hash-scatter launch issues for samples `pos` [N x >=3] (float32).
+
+    Follows the kernel's schedule: a wave takes 16 consecutive samples at one level; per (y, z) corner
+    pair it issues one atomic instruction over lanes (sample, x-corner, feature), after merging runs of
+    equal addresses over consecutive samples (only run tails stay active).  A request is one distinct
+    64-byte line among the active lanes of an instruction."""
+    n = pos.shape[0]
+    if n == 0:
+        return 0
+    w = 16
+    m = (n + w - 1) // w * w
+    p = np.zeros((m, 3), np.float32)
+    p[:n] = pos[:, :3]
+    valid = np.arange(m) < n
+    inner = (np.float32(TBL) ** (1.0 / 3.0) - 1.0) / BASE
+    dense_start = max(0, min(int(math.floor(math.log2(inner) / math.log2(GROWTH))) + 1, L))
+    total = 0
+    for lvl in range(L):
+        s = np.float32(BASE * GROWTH ** lvl)
+        res = int(math.floor(s))
+        x0 = np.clip(np.floor(p * s).astype(np.int64), 0, res - 1)
+        x1 = np.minimum(x0 + 1, res)
+        cx = [x0[:, 0], x1[:, 0]]
+        for q in range(4):
+            cy = x1[:, 1] if q & 1 else x0[:, 1]
+            cz = x1[:, 2] if q & 2 else x0[:, 2]
+            ent = []
+            for xs in range(2):
+                if lvl < dense_start:
+                    e = cx[xs] + cy * (res + 1) + cz * (res + 1) ** 2
+                else:
+                    e = ((cx[xs].astype(np.uint32) ^ (cy.astype(np.uint32) * np.uint32(2654435761))
+                          ^ (cz.astype(np.uint32) * np.uint32(805459861))) & np.uint32(TBL - 1)).astype(np.int64)
+                e = e.reshape(-1, w)
+                v = valid.reshape(-1, w)
+                nxt = np.concatenate([e[:, 1:], np.full((e.shape[0], 1), -1)], axis=1)
+                tail = v & (e != nxt)
+                ent.append(np.where(tail, e // 8, -1))  # 8 entries of 2 floats per 64-byte line
+            lines = np.sort(np.concatenate(ent, axis=1), axis=1)
+            distinct = (np.diff(lines, axis=1) != 0).sum(axis=1) + 1 - (lines[:, 0] == -1)
+            total += int(distinct.sum())
+    return total
+
+
+def atomic_ceiling(P, torch):
+    """Measured ceiling of fp32 atomic line requests per second (include/graft_diag.h)."""
+    buf = torch.zeros(L * TBL * F, dtype=torch.float32, device="cuda:0")  # the size of the gradient table
+    rate = C.c_double(0.0)
+    stream = torch.cuda.current_stream().cuda_stream
+    P.check(P.lib().graft_diag_atomic_line_rate(buf.data_ptr(), buf.numel() * 4, SCATTER_DWORDS_PER_REQUEST,
+                                                C.byref(rate), stream))
+    del buf
+    return rate.value
 
 
 def parse():
@@ -467,6 +535,19 @@ def main():
     roofline = {"bound": bound, "kernel": dom, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom),
                 "algorithmic_bytes_per_launch": int(algo), "avg_launch_ms": round(dom_ms, 4)}
+    if dom == "hashScatter":
+        # The scatter's own ceiling: atomic line requests per second (measured), against the requests
+        # the last profiled step's samples make the kernel issue, scaled to the window's mean batch.
+        sb = nerf.step_buffers()
+        n_last = int(d2h(sb.result, (2,), np.uint32)[1])
+        req_per_sample = scatter_line_requests(d2h(sb.positions, (n_last, 4), np.float32)) / max(n_last, 1)
+        ceiling = atomic_ceiling(P, torch)
+        req_rate = req_per_sample * n_prof / (dom_ms * 1e-3)
+        roofline["atomic_requests"] = {"requests_per_sample": round(req_per_sample, 3),
+                                       "achieved_per_s": round(req_rate, 1), "ceiling_per_s": round(ceiling, 1),
+                                       "frac": round(req_rate / ceiling, 4),
+                                       "ceiling": f"fp32 atomic adds to random 64-byte lines, "
+                                                  f"{SCATTER_DWORDS_PER_REQUEST} dwords per line request"}
     # MLP stages: the fused forward, the dX chains (main stream) and the weight gradients (side stream)
     mlp_ms = sum(st[k][0] for k in ("forward", "backwardDx", "colorDx", "densityDx", "colorBwd", "densityBwd")
                  if k in st)
