@@ -100,9 +100,7 @@ struct NerfBuffers {
     // `occ` runs the occupancy refresh.
     hipStream_t side = nullptr, occ = nullptr;
     hipEvent_t ev_fork = nullptr, ev_join = nullptr, ev_done = nullptr, ev_done_occ = nullptr;
-    hipEvent_t ev_params = nullptr;  // main: the last step's hash-table Adam is done
     hipEvent_t ev_dl = nullptr;      // main: this step's MLP output gradients are written
-    hipEvent_t ev_mlp = nullptr;     // side: this step's MLP Adam is done
     std::vector<StageTimer> pending;
     std::map<std::string, std::pair<double, long>> stats;
 };
@@ -195,9 +193,7 @@ void InstantNerf::freeBuffers()
         if (b.ev_join) (void)hipEventDestroy(b.ev_join);
         if (b.ev_done) (void)hipEventDestroy(b.ev_done);
         if (b.ev_done_occ) (void)hipEventDestroy(b.ev_done_occ);
-        if (b.ev_params) (void)hipEventDestroy(b.ev_params);
         if (b.ev_dl) (void)hipEventDestroy(b.ev_dl);
-        if (b.ev_mlp) (void)hipEventDestroy(b.ev_mlp);
         if (b.occ) (void)hipStreamDestroy(b.occ);
         if (b.side) (void)hipStreamDestroy(b.side);
         for (auto& t : b.pending) {
@@ -317,9 +313,7 @@ void InstantNerf::allocate()
     GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_join, kStreamEvent));
     GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_done, kStreamEvent));
     GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_done_occ, kStreamEvent));
-    GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_params, kStreamEvent));
     GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_dl, kStreamEvent));
-    GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_mlp, kStreamEvent));
     GRAFT_HIP_CHECK(hipStreamCreateWithFlags(&b.occ, hipStreamNonBlocking));
     GRAFT_HIP_CHECK(hipStreamCreateWithFlags(&b.side, hipStreamNonBlocking));
 
@@ -429,29 +423,9 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         m_windowStart = raysDone;
         b.last_set = k;
 
-        // InstantNerf.cu:488-494: the refresh changes only the grid that later
-        // batches march and reads only the density head, so it runs on its
-        // own stream beside this step's forward/backward, on the parameters
-        // the previous step's Adam left; this step's Adam updates and the
-        // next batch's march wait for it, so every kernel sees the same
-        // parameters and grid as in the serial order.
-        const bool refresh = (m_trainSteps % 16 == 0);
-        if (refresh) {
-            if (i > 0) {
-                GRAFT_HIP_CHECK(hipStreamWaitEvent(b.occ, b.ev_params, 0));
-                GRAFT_HIP_CHECK(hipStreamWaitEvent(b.occ, b.ev_mlp, 0));
-            }
-            stage_on(b.occ, "occupancy", [&] {
-                if (m_trainSteps < 256) earlyOccupancyGridUpdate(b.occ);
-                else lateOccupancyGridUpdate(b.occ);
-            });
-            GRAFT_HIP_CHECK(hipEventRecord(b.ev_join, b.occ));
-        }
-
+        // S was compacted on the side stream after the previous step's MLP
+        // Adam: once it is ready, the weights this forward uses are updated
         GRAFT_HIP_CHECK(hipStreamWaitEvent(stream, S.ev_ready, 0));
-        // the previous step's MLP weight gradients have been read and its Adam
-        // has updated the weights this forward uses
-        if (i > 0) GRAFT_HIP_CHECK(hipStreamWaitEvent(stream, b.ev_mlp, 0));
         // hash encode + density head, SH gather (into the colour head's
         // activation 0), colour head: one launch, activations saved
         stage("forward", [&] {
@@ -576,6 +550,22 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
             GRAFT_HIP_CHECK(hipEventRecord(b.ev_dl, stream));
             GRAFT_HIP_CHECK(hipStreamWaitEvent(b.side, b.ev_dl, 0));
         }
+        // InstantNerf.cu:488-494: the refresh changes only the grid that later
+        // batches march and reads only the density head, so it runs on its
+        // own stream beside the scatter (which leaves most of every CU free),
+        // forked after this step's dX chain: by then the main stream has seen
+        // the previous step's Adam updates of both heads and the table.  This
+        // step's Adam updates and the next batch's march wait for it, so every
+        // kernel sees the same parameters and grid as in the serial order.
+        const bool refresh = (m_trainSteps % 16 == 0);
+        if (refresh) {
+            GRAFT_HIP_CHECK(hipStreamWaitEvent(b.occ, b.ev_dl, 0));
+            stage_on(b.occ, "occupancy", [&] {
+                if (m_trainSteps < 256) earlyOccupancyGridUpdate(b.occ);
+                else lateOccupancyGridUpdate(b.occ);
+            });
+            GRAFT_HIP_CHECK(hipEventRecord(b.ev_join, b.occ));
+        }
         stage("hashScatter", [&] {
             graft::hash_scatter(b.meta, db.dx_out, reinterpret_cast<const float*>(S.positions), 4, db.hashtable_grads,
                                 (int)Bn, stream, d_hits);
@@ -593,8 +583,6 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         stage("densityOpt", [&] {
             m_densityMLP->stepSplit(o.learningRate, o.beta1, o.beta2, o.epsilon, o.lossScale, b.side, stream);
         });
-        GRAFT_HIP_CHECK(hipEventRecord(b.ev_params, stream));
-        GRAFT_HIP_CHECK(hipEventRecord(b.ev_mlp, b.side));
 
         trainStepCount++;
         m_trainSteps++;
