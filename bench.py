@@ -457,6 +457,23 @@ def components(P, torch, stream, sp):
     t_march = timed(march)
     out.update({"march_compact_ms_2p18_rays": round(t_march, 4), "march_rays_per_s": round(R4 / (t_march * 1e-3), 1),
                 "march_samples": int(total.value)})
+    del t_o, t_d, t_bits, di, nr, fr, cnt, offs, posb, rib, tsb
+
+    # Achievable bandwidth in the same run: a streaming copy far larger than the 256 MB MALL, and one
+    # of the fp16 table's size (32 MiB, cache-resident); bytes = read + write.
+    for tag, nbytes in (("1gib", 1 << 30), ("32mib", 32 << 20)):
+        src = torch.empty(nbytes // 4, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        t_cp = timed(lambda: dst.copy_(src), reps=10)
+        out[f"copy_gbs_{tag}"] = round(2 * nbytes / (t_cp * 1e-3) / 1e9, 1)
+        del src, dst
+    # fp16 dense MFMA peak recomputed on the box: CUs x clock x 4,096 flop/clock/CU (gfx950 dense fp16)
+    hip = C.CDLL("libamdhip64.so")
+    clk = C.c_int(0)
+    if hip.hipDeviceGetAttribute(C.byref(clk), 5, 0) == 0 and clk.value > 0:  # 5 = hipDeviceAttributeClockRate (kHz)
+        cus = torch.cuda.get_device_properties(0).multi_processor_count
+        out["fp16_mfma_peak_tflops_from_clock"] = round(cus * clk.value * 1e3 * 4096 / 1e12, 1)
+        out["cus"], out["clock_mhz"] = cus, round(clk.value / 1e3)
     return out
 
 
