@@ -67,40 +67,50 @@ __device__ __forceinline__ void stage_meta(const GridKernelArgs& a, float* ss, i
     __syncthreads();
 }
 
-__global__ __launch_bounds__(256) void hash_encode_kernel(const GridKernelArgs a,
-                                                          const float* __restrict__ pos,
+// gfx950 dispatches workgroup i to XCD i mod 8, and each XCD has its own 4 MB
+// L2.  The encode gives each XCD its own levels, so that its L2 holds only
+// those levels' fp16 tables (2 MiB per hashed level at T = 2^19) instead of
+// cycling all 32 MiB through every L2: levels are dealt to XCDs in snake
+// order, l -> l mod 8 for even l / 8 and 7 - l mod 8 for odd, which pairs
+// level l with level 15 - l (a small dense level with a hashed one).
+constexpr int kXcds = 8;
+
+// Each workgroup encodes, for every sample of its stride, the levels of its
+// XCD, 16 k + x and 16 k + 15 - x; both are computed unconditionally (an
+// out-of-range level reads level 0 and is not stored) so that their gathers
+// are in flight together.  Output: PLANAR, enc[l][plane] feature pairs; else
+// row-major enc[n][2L].
+template <bool PLANAR>
+__global__ __launch_bounds__(256) void hash_encode_kernel(const GridKernelArgs a, const float* __restrict__ pos,
                                                           const _Float16* __restrict__ table,
-                                                          _Float16* __restrict__ enc)
+                                                          _Float16* __restrict__ enc, int plane)
 {
     __shared__ float ss[kMaxLevels];
     __shared__ int sr[kMaxLevels];
     stage_meta(a, ss, sr);
-    const int G = (a.L + 3) >> 2;
     const uint32_t mask = (uint32_t)a.T - 1u;
+    const int N = a.d_n ? min((int)*a.d_n, a.N) : a.N;
+    const int x = blockIdx.x % kXcds, nb = gridDim.x / kXcds;
     const int D = 2 * a.L;
-    for (long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x; t < (long long)a.N * G;
-         t += (long long)gridDim.x * blockDim.x) {
-        const int n = (int)(t / G), g = (int)(t - (long long)n * G);
+    for (int n = (blockIdx.x / kXcds) * blockDim.x + threadIdx.x; n < N; n += nb * blockDim.x) {
         const float* pp = pos + (size_t)n * a.pos_stride;
         const float px = pp[0], py = pp[1], pz = pp[2];
-        _Float16 v[8];
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const int l = 4 * g + k;
-            float2 e = make_float2(0.f, 0.f);
-            if (l < a.L)
-                e = encode_level(px, py, pz, ss[l], sr[l], l < a.dense_start, mask,
-                                 table + (size_t)l * a.T * 2);
-            v[2 * k] = to_h(e.x);
-            v[2 * k + 1] = to_h(e.y);
-        }
-        _Float16* dst = enc + (size_t)n * D + 8 * g;
-        const int cnt = min(8, D - 8 * g);
-        if (cnt == 8) {
-            *reinterpret_cast<h4*>(dst) = h4{v[0], v[1], v[2], v[3]};
-            *reinterpret_cast<h4*>(dst + 4) = h4{v[4], v[5], v[6], v[7]};
-        } else {
-            for (int k = 0; k < cnt; k++) dst[k] = v[k];
+        for (int base = 0; base < a.L; base += 2 * kXcds) {
+            const int la = base + x, lb = base + 2 * kXcds - 1 - x;
+            const bool va = la < a.L, vb = lb < a.L;
+            const int ca = va ? la : 0, cb = vb ? lb : 0;
+            const float2 ea = encode_level(px, py, pz, ss[ca], sr[ca], ca < a.dense_start, mask,
+                                           table + (size_t)ca * a.T * 2);
+            const float2 eb = encode_level(px, py, pz, ss[cb], sr[cb], cb < a.dense_start, mask,
+                                           table + (size_t)cb * a.T * 2);
+            const h2 ha{to_h(ea.x), to_h(ea.y)}, hb{to_h(eb.x), to_h(eb.y)};
+            if constexpr (PLANAR) {
+                if (va) *reinterpret_cast<h2*>(enc + ((size_t)la * plane + n) * 2) = ha;
+                if (vb) *reinterpret_cast<h2*>(enc + ((size_t)lb * plane + n) * 2) = hb;
+            } else {
+                if (va) *reinterpret_cast<h2*>(enc + (size_t)n * D + 2 * la) = ha;
+                if (vb) *reinterpret_cast<h2*>(enc + (size_t)n * D + 2 * lb) = hb;
+            }
         }
     }
 }
@@ -189,23 +199,37 @@ GridKernelArgs grid_args(const GridMeta& m, int N, int pos_stride)
     return a;
 }
 
-int grid_blocks(long long threads)
+// kXcds workgroups per 256 samples, at most 256 per XCD; at least one per XCD
+// so that every level has a workgroup.
+int encode_blocks(int N)
 {
-    long long b = (threads + 255) / 256;
-    return (int)std::max(1LL, std::min(b, (long long)num_cus() * 16));
+    return kXcds * std::max(1, std::min((N + 255) / 256, 256));
 }
 
 }  // namespace
 
 void hash_encode(const GridMeta& m, const __half* table, const float* pos, int pos_stride,
-                 __half* enc, int N, hipStream_t stream)
+                 __half* enc, int N, hipStream_t stream, const uint32_t* d_n)
 {
     if (N <= 0) return;
     if (pos_stride < 3) throw std::runtime_error("hash encode: position stride must be >= 3");
-    const GridKernelArgs a = grid_args(m, N, pos_stride);
-    const long long threads = (long long)N * ((m.numLevels + 3) / 4);
-    hipLaunchKernelGGL(hash_encode_kernel, dim3(grid_blocks(threads)), dim3(256), 0, stream, a, pos,
-                       reinterpret_cast<const _Float16*>(table), reinterpret_cast<_Float16*>(enc));
+    GridKernelArgs a = grid_args(m, N, pos_stride);
+    a.d_n = d_n;
+    hipLaunchKernelGGL(hash_encode_kernel<false>, dim3(encode_blocks(N)), dim3(256), 0, stream, a, pos,
+                       reinterpret_cast<const _Float16*>(table), reinterpret_cast<_Float16*>(enc), 0);
+    GRAFT_LAUNCH_CHECK();
+}
+
+void hash_encode_planar(const GridMeta& m, const __half* table, const float* pos, int pos_stride,
+                        __half* enc, int plane, int N, hipStream_t stream, const uint32_t* d_n)
+{
+    if (N <= 0) return;
+    if (pos_stride < 3) throw std::runtime_error("hash encode: position stride must be >= 3");
+    if (plane < N) throw std::runtime_error("hash encode: plane stride below the sample count");
+    GridKernelArgs a = grid_args(m, N, pos_stride);
+    a.d_n = d_n;
+    hipLaunchKernelGGL(hash_encode_kernel<true>, dim3(encode_blocks(N)), dim3(256), 0, stream, a, pos,
+                       reinterpret_cast<const _Float16*>(table), reinterpret_cast<_Float16*>(enc), plane);
     GRAFT_LAUNCH_CHECK();
 }
 

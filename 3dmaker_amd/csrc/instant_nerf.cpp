@@ -70,10 +70,12 @@ struct NerfBuffers {
     float* dw = nullptr;
     float* dsigma = nullptr;
     __half* color_dx = nullptr;
+    __half* enc_planar = nullptr;    // [L][Bn] feature pairs: the step's encodings, level-major
     // occupancy
     float* tmp_grid = nullptr;
     float4* occ_samples = nullptr;
     float* occ_density = nullptr;
+    __half* occ_enc = nullptr;       // [capacity x 2L] encodings of the refresh samples
     float* partials = nullptr;
     float* sum = nullptr;
     int* active_list = nullptr;
@@ -173,9 +175,11 @@ void InstantNerf::freeBuffers()
         dfree(b.dw);
         dfree(b.dsigma);
         dfree(b.color_dx);
+        dfree(b.enc_planar);
         dfree(b.tmp_grid);
         dfree(b.occ_samples);
         dfree(b.occ_density);
+        dfree(b.occ_enc);
         dfree(b.partials);
         dfree(b.sum);
         dfree(b.active_list);
@@ -304,6 +308,7 @@ void InstantNerf::allocate()
     b.occ_capacity = std::max(G, halfN / std::max(1, m_opts.numCascades));
     b.occ_samples = dalloc<float4>((size_t)b.occ_capacity);
     b.occ_density = dalloc<float>((size_t)b.occ_capacity * 16);
+    b.occ_enc = dalloc<__half>((size_t)b.occ_capacity * 2 * m_opts.numLevels);
     b.partials = dalloc<float>(1024);
     b.sum = dalloc<float>(1);
     b.active_list = dalloc<int>((size_t)N);
@@ -323,6 +328,7 @@ void InstantNerf::allocate()
     GRAFT_HIP_CHECK(hipMemcpy(&acts0, cb.activations, sizeof(acts0), hipMemcpyDeviceToHost));
     b.color_in = acts0;
     b.meta = graft::make_grid_meta(m_opts.hashTableSize, m_opts.numLevels, m_opts.growthFactor, m_opts.baseResolution);
+    b.enc_planar = dalloc<__half>((size_t)2 * b.meta.numLevels * Bn);
 }
 
 // InstantNerf.cu:341-359.  The mode picks the hit batch of the render path
@@ -450,6 +456,8 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
             fa.cacts = cb.activations;
             fa.color_in = b.color_in;
             fa.color_out = cb.padded_outputs;
+            fa.enc_scratch = b.enc_planar;
+            fa.enc_plane = (int)Bn;
             graft::nerf_forward(fa, (int)Bn, stream, d_hits);
         });
 
@@ -656,6 +664,25 @@ void InstantNerf::updateOccupancy(hipStream_t stream)
     else lateOccupancyGridUpdate(stream);
 }
 
+namespace {
+
+// Density logits of the n refresh samples in b.occ_samples: the encode runs
+// as its own launch (each XCD's L2 holding only its levels' tables; the
+// samples are spread over the whole grid, so the fused encode + MLP kernel
+// would cycle all 32 MiB of table through every L2), then the density head
+// on the encodings.
+void occupancy_density(NerfBuffers& b, const TinyMLPHashGrid::Buffers& db, const graft::MlpShape& dshape, int n,
+                       hipStream_t stream)
+{
+    graft::hash_encode(b.meta, db.fwd_hashtable, reinterpret_cast<const float*>(b.occ_samples), 4, b.occ_enc, n,
+                       stream);
+    graft::FwdInput in;
+    in.x = b.occ_enc;
+    graft::mlp_forward(dshape, in, db.fwd_weights, db.master_biases, nullptr, b.occ_density, n, OUT_ACT_NONE, stream);
+}
+
+}  // namespace
+
 // InstantNerf.cu:1108-1171: one jittered sample per cell of every cascade.
 void InstantNerf::earlyOccupancyGridUpdate(hipStream_t stream)
 {
@@ -669,13 +696,7 @@ void InstantNerf::earlyOccupancyGridUpdate(hipStream_t stream)
         graft::occ_sample(b.occ_samples, G, graft::kSampleEveryCell, G, c * G, nullptr, nullptr,
                           (uint64_t)m_trainSteps + (uint64_t)c, m_opts.gridResolution, m_opts.aabbMin, m_opts.aabbMax,
                           stream);
-        graft::FwdInput in;
-        in.pos = reinterpret_cast<const float*>(b.occ_samples);
-        in.pos_stride = 4;
-        in.table = db.fwd_hashtable;
-        in.meta = &b.meta;
-        graft::mlp_forward(dshape, in, db.fwd_weights, db.master_biases, nullptr, b.occ_density, G, OUT_ACT_NONE,
-                           stream);
+        occupancy_density(b, db, dshape, G, stream);
         graft::occ_tmp_max(b.occ_samples, b.occ_density, b.tmp_grid, m_opts.densityBias, G, stream);
     }
     finishOccupancyUpdate(stream);
@@ -704,13 +725,7 @@ void InstantNerf::lateOccupancyGridUpdate(hipStream_t stream)
         graft::occ_sample(b.occ_samples + occPer, uniPer, graft::kSampleRandomCell, N, 0, nullptr, nullptr, seed + 1,
                           m_opts.gridResolution, m_opts.aabbMin, m_opts.aabbMax, stream);
         const int cnt = occPer + uniPer;
-        graft::FwdInput in;
-        in.pos = reinterpret_cast<const float*>(b.occ_samples);
-        in.pos_stride = 4;
-        in.table = db.fwd_hashtable;
-        in.meta = &b.meta;
-        graft::mlp_forward(dshape, in, db.fwd_weights, db.master_biases, nullptr, b.occ_density, cnt, OUT_ACT_NONE,
-                           stream);
+        occupancy_density(b, db, dshape, cnt, stream);
         graft::occ_tmp_max(b.occ_samples, b.occ_density, b.tmp_grid, m_opts.densityBias, cnt, stream);
     }
     finishOccupancyUpdate(stream);

@@ -74,6 +74,11 @@ struct NerfFwdArgs {
     __half* const* cacts = nullptr;  // device array; entries 1.. receive the hidden activations
     __half* color_in = nullptr;      // [N x 32] logits | SH (the colour head's activation 0)
     float* color_out = nullptr;      // [N x cshape.out]
+    // Nullable: [L][enc_plane] feature pairs (enc_plane >= N).  When set, the
+    // encode runs first as its own launch (hash_encode_planar, each XCD's L2
+    // holding only its levels' tables) and the network kernel reads it.
+    __half* enc_scratch = nullptr;
+    int enc_plane = 0;
 };
 void nerf_forward(const NerfFwdArgs& a, int N, hipStream_t stream, const uint32_t* d_n = nullptr);
 

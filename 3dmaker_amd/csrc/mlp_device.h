@@ -154,6 +154,16 @@ struct NetView {
     int in, hid, out, layers;
 };
 
+// Row n of the layer-0 activation [N x in]: the lane's 4 features of K-block
+// ks (2 when the row ends mid-quad).
+__device__ __forceinline__ void store_act0(_Float16* act0, int in, int n, int ks, int g, h4 x)
+{
+    const int col = 16 * ks + 4 * g;
+    _Float16* dst = act0 + (size_t)n * in + col;
+    if (col + 4 <= in) st_h4(dst, x);
+    else if (col + 2 <= in) *reinterpret_cast<h2*>(dst) = h2{x.x, x.y};
+}
+
 // Hash encode of one 16-sample tile straight into the layer-0 B operand:
 // lane (r = sample, g) holds levels 8 ks + 2 g and 8 ks + 2 g + 1 of K-block
 // ks.  act0 (nullable) receives the fp16 encoding [N x in].
@@ -175,12 +185,30 @@ __device__ __forceinline__ void encode_tile(h4 (&X)[NT], float px, float py, flo
             if (valid && lb < L)
                 eb = encode_level(px, py, pz, sscale[lb], sres[lb], lb < dense_start, mask, table + (size_t)lb * T * 2);
             X[ks] = h4{to_h(ea.x), to_h(ea.y), to_h(eb.x), to_h(eb.y)};
-            if (act0 != nullptr && valid) {
-                const int col = 16 * ks + 4 * g;
-                _Float16* dst = act0 + (size_t)n * in + col;
-                if (col + 4 <= in) st_h4(dst, X[ks]);
-                else if (col + 2 <= in) *reinterpret_cast<h2*>(dst) = h2{X[ks].x, X[ks].y};
-            }
+            if (act0 != nullptr && valid) store_act0(act0, in, n, ks, g, X[ks]);
+        }
+    }
+}
+
+// The same operand from encodings stored level-major, enc[l][plane] feature
+// pairs (hash_encode_planar): lane (r, g) loads levels 8 ks + 2 g and
+// 8 ks + 2 g + 1 of its sample; the 16 lanes of a level read 64 contiguous
+// bytes.  act0 (nullable) receives the row-major encoding as above.
+template <int NT>
+__device__ __forceinline__ void load_encoded_tile(h4 (&X)[NT], const _Float16* __restrict__ enc, int plane, int L,
+                                                  int in, _Float16* act0, int n, bool valid, int g)
+{
+    const int KS0 = tiles16(in);
+#pragma unroll
+    for (int ks = 0; ks < NT; ks++) {
+        X[ks] = h4zero();
+        if (ks < KS0) {
+            const int la = 8 * ks + 2 * g, lb = la + 1;
+            h2 ea{(_Float16)0.f, (_Float16)0.f}, eb{(_Float16)0.f, (_Float16)0.f};
+            if (valid && la < L) ea = *reinterpret_cast<const h2*>(enc + ((size_t)la * plane + n) * 2);
+            if (valid && lb < L) eb = *reinterpret_cast<const h2*>(enc + ((size_t)lb * plane + n) * 2);
+            X[ks] = h4{ea.x, ea.y, eb.x, eb.y};
+            if (act0 != nullptr && valid) store_act0(act0, in, n, ks, g, X[ks]);
         }
     }
 }

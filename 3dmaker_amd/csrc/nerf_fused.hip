@@ -18,6 +18,7 @@
 // chain, down to dL/d(encoding) for the hash scatter; bitwise the outputs of
 // the dX-only head kernels and density_grad_kernel.  The weight gradients are
 // computed apart (mlp_backward with dx = nullptr).
+#include "hashgrid.h"
 #include "mlp_device.h"
 #include "nerf.h"
 
@@ -30,6 +31,8 @@ namespace {
 struct NerfFwdParams {
     const float* pos;
     const _Float16* table;
+    const _Float16* enc;      // level-major encodings (PLANAR kernels)
+    int plane;
     const _Float16* const* dW;
     const float* const* dB;
     _Float16* const* dacts;   // nullable
@@ -55,7 +58,7 @@ struct NerfFwdParams {
     int res[kMaxLevels];
 };
 
-template <int NT, int OUT_ACT>
+template <int NT, int OUT_ACT, bool PLANAR>
 __global__ __launch_bounds__(256) void nerf_fwd_kernel(const NerfFwdParams p)
 {
     extern __shared__ __align__(16) unsigned char smem[];
@@ -86,17 +89,21 @@ __global__ __launch_bounds__(256) void nerf_fwd_kernel(const NerfFwdParams p)
     for (int tile = blockIdx.x * 4 + wave; tile < ntiles; tile += gridDim.x * 4) {
         const int n = tile * 16 + r;
         const bool valid = n < N;
-        float px = 0.f, py = 0.f, pz = 0.f;
         float3 dir = make_float3(0.f, 0.f, 0.f);
-        if (valid) {
-            const float* pp = p.pos + (size_t)n * p.pos_stride;
-            px = pp[0];
-            py = pp[1];
-            pz = pp[2];
-            dir = p.dirs[p.ray_idx[n]];
-        }
+        if (valid) dir = p.dirs[p.ray_idx[n]];
         h4 X[NT];
-        encode_tile<NT>(X, px, py, pz, sscale, sres, p.L, p.T, p.dense_start, p.table, p.d_in, act0, n, valid, g);
+        if constexpr (PLANAR) {
+            load_encoded_tile<NT>(X, p.enc, p.plane, p.L, p.d_in, act0, n, valid, g);
+        } else {
+            float px = 0.f, py = 0.f, pz = 0.f;
+            if (valid) {
+                const float* pp = p.pos + (size_t)n * p.pos_stride;
+                px = pp[0];
+                py = pp[1];
+                pz = pp[2];
+            }
+            encode_tile<NT>(X, px, py, pz, sscale, sres, p.L, p.T, p.dense_start, p.table, p.d_in, act0, n, valid, g);
+        }
 
         // density head -> colour input features 0..15 (sanitised logits), sigma
         h4 C[NT];
@@ -229,10 +236,17 @@ void nerf_forward(const NerfFwdArgs& a, int N, hipStream_t stream, const uint32_
     const GridMeta& m = *a.meta;
     if (2 * m.numLevels != a.dshape.in) throw std::runtime_error("NeRF forward: density input must be 2 * numLevels");
 
+    const bool planar = a.enc_scratch != nullptr;
+    if (planar) {
+        if (a.enc_plane < N) throw std::runtime_error("NeRF forward: encoding plane stride below the sample count");
+        hash_encode_planar(m, a.table, a.pos, a.pos_stride, a.enc_scratch, a.enc_plane, N, stream, d_n);
+    }
     NerfFwdParams p{};
     p.pos = a.pos;
     p.pos_stride = a.pos_stride;
     p.table = reinterpret_cast<const _Float16*>(a.table);
+    p.enc = reinterpret_cast<const _Float16*>(a.enc_scratch);
+    p.plane = a.enc_plane;
     p.dW = reinterpret_cast<const _Float16* const*>(a.dW);
     p.dB = a.dB;
     p.dacts = reinterpret_cast<_Float16* const*>(a.dacts);
@@ -284,10 +298,17 @@ void nerf_forward(const NerfFwdArgs& a, int N, hipStream_t stream, const uint32_
     const int ntiles = (N + 15) / 16;
     const int blocks = std::max(1, std::min((ntiles + 3) / 4, num_cus() * 8));
     const int nt = pick_nt(std::max(a.dshape.maxd(), a.cshape.maxd()));
+#define GRAFT_NERF_FWD_P(NTV, PL)                                                                             \
+    do {                                                                                                      \
+        if (a.out_act == 1)                                                                                   \
+            hipLaunchKernelGGL((nerf_fwd_kernel<NTV, 1, PL>), dim3(blocks), dim3(256), lds, stream, p);       \
+        else                                                                                                  \
+            hipLaunchKernelGGL((nerf_fwd_kernel<NTV, 0, PL>), dim3(blocks), dim3(256), lds, stream, p);       \
+    } while (0)
 #define GRAFT_NERF_FWD(NTV)                                                                                   \
     do {                                                                                                      \
-        if (a.out_act == 1) hipLaunchKernelGGL((nerf_fwd_kernel<NTV, 1>), dim3(blocks), dim3(256), lds, stream, p); \
-        else hipLaunchKernelGGL((nerf_fwd_kernel<NTV, 0>), dim3(blocks), dim3(256), lds, stream, p);         \
+        if (planar) GRAFT_NERF_FWD_P(NTV, true);                                                              \
+        else GRAFT_NERF_FWD_P(NTV, false);                                                                    \
     } while (0)
     switch (nt) {
         case 2: GRAFT_NERF_FWD(2); break;
@@ -295,6 +316,7 @@ void nerf_forward(const NerfFwdArgs& a, int N, hipStream_t stream, const uint32_
         default: GRAFT_NERF_FWD(8); break;
     }
 #undef GRAFT_NERF_FWD
+#undef GRAFT_NERF_FWD_P
     GRAFT_LAUNCH_CHECK();
 }
 
