@@ -44,7 +44,7 @@ struct StepSet {
     float* t_sorted = nullptr;     // [batchSize]
     uint32_t* result = nullptr;    // [2] active rays, compacted samples
     uint32_t* h_result = nullptr;  // pinned copy of result
-    hipEvent_t ev_result = nullptr, ev_ready = nullptr, ev_free = nullptr;
+    hipEvent_t ev_result = nullptr, ev_ready = nullptr;
     uint32_t raysDone = 0;         // first ray of the batch in the call's rays
 };
 
@@ -164,7 +164,6 @@ void InstantNerf::freeBuffers()
             if (S.h_result) (void)hipHostFree(S.h_result);
             if (S.ev_result) (void)hipEventDestroy(S.ev_result);
             if (S.ev_ready) (void)hipEventDestroy(S.ev_ready);
-            if (S.ev_free) (void)hipEventDestroy(S.ev_free);
         }
         dfree(b.render_rgb);
         dfree(b.render_depth);
@@ -292,7 +291,6 @@ void InstantNerf::allocate()
         GRAFT_HIP_CHECK(hipHostMalloc((void**)&S.h_result, 2 * sizeof(uint32_t), hipHostMallocDefault));
         GRAFT_HIP_CHECK(hipEventCreateWithFlags(&S.ev_result, hipEventDisableTiming));
         GRAFT_HIP_CHECK(hipEventCreateWithFlags(&S.ev_ready, kStreamEvent));
-        GRAFT_HIP_CHECK(hipEventCreateWithFlags(&S.ev_free, kStreamEvent));
     }
     b.render_rgb = dalloc<float>(3 * R);
     b.render_depth = dalloc<float>(R);
@@ -377,14 +375,13 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
     // processRaysHitLinear (processRays.cu:931-1040) for the hit batch that
     // starts at ray raysDone, into step set k, on the side stream: the window
     // is marched only when it is not covered by the cached march on the
-    // current grid; the set is reused once the main stream has finished the
-    // step that last read it.
+    // current grid.  The set's previous step has finished reading it by
+    // then: this runs after the side stream's wait on a later step's ev_dl.
     auto compact = [&](int k, uint32_t raysDone) {
         StepSet& S = b.set[k];
         const uint32_t R = std::min<uint32_t>((uint32_t)o.rayChunkSize, numRays - raysDone);
         const float3* co = d_rays_o + raysDone;
         const float3* cd = d_rays_d + raysDone;
-        GRAFT_HIP_CHECK(hipStreamWaitEvent(b.side, S.ev_free, 0));
         if (b.cache_version != m_gridVersion || raysDone < b.cache_c0 || raysDone + R > b.cache_c1) {
             stage_on(b.side, "rayAabb", [&] {
                 graft::ray_aabb_inv(R, co, cd, o.aabbMin, o.aabbMax, o.numCascades, b.d_inv, b.nears, b.fars,
@@ -534,17 +531,6 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
                                            stream, d_hits);
                 });
             }
-            GRAFT_HIP_CHECK(hipEventRecord(b.ev_dl, stream));
-            GRAFT_HIP_CHECK(hipStreamWaitEvent(b.side, b.ev_dl, 0));
-            // this step's gradient overwrites the last one: no zero_grad pass
-            stage_on(b.side, "colorBwd", [&] {
-                graft::mlp_backward(cshape, cb.dloss, cb.activations, cb.fwd_weights, cb.w_grad, cb.b_grad, nullptr,
-                                    (int)Bn, b.side, d_hits, /*accumulate=*/false);
-            });
-            stage_on(b.side, "densityBwd", [&] {
-                graft::mlp_backward(dshape, db.dloss, db.activations, db.fwd_weights, db.w_grad, db.b_grad, nullptr,
-                                    (int)Bn, b.side, d_hits, /*accumulate=*/false);
-            });
         } else {
             stage("colorBwd", [&] {
                 graft::mlp_backward(cshape, cb.dloss, cb.activations, cb.fwd_weights, cb.w_grad, cb.b_grad,
@@ -555,8 +541,30 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
                 graft::mlp_backward(dshape, db.dloss, db.activations, db.fwd_weights, db.w_grad, db.b_grad,
                                     db.dx_out, (int)Bn, stream, d_hits, /*accumulate=*/false);
             });
-            GRAFT_HIP_CHECK(hipEventRecord(b.ev_dl, stream));
-            GRAFT_HIP_CHECK(hipStreamWaitEvent(b.side, b.ev_dl, 0));
+        }
+        GRAFT_HIP_CHECK(hipEventRecord(b.ev_dl, stream));
+        // The scatter is the step's critical path: it is enqueued before the
+        // side streams' work, so that the host's launches of that work never
+        // delay it.
+        stage("hashScatter", [&] {
+            graft::hash_scatter(b.meta, db.dx_out, reinterpret_cast<const float*>(S.positions), 4, db.hashtable_grads,
+                                (int)Bn, stream, d_hits);
+        });
+        // Beside it: the weight gradients (this step's gradient overwrites the
+        // last one: no zero_grad pass).  The side stream's wait on ev_dl also
+        // orders every read of this step set by the main stream before the
+        // compaction that refills the set two steps later (it is enqueued on
+        // the side stream after the next step's wait on ev_dl).
+        GRAFT_HIP_CHECK(hipStreamWaitEvent(b.side, b.ev_dl, 0));
+        if (fused_dx || dx_only) {
+            stage_on(b.side, "colorBwd", [&] {
+                graft::mlp_backward(cshape, cb.dloss, cb.activations, cb.fwd_weights, cb.w_grad, cb.b_grad, nullptr,
+                                    (int)Bn, b.side, d_hits, /*accumulate=*/false);
+            });
+            stage_on(b.side, "densityBwd", [&] {
+                graft::mlp_backward(dshape, db.dloss, db.activations, db.fwd_weights, db.w_grad, db.b_grad, nullptr,
+                                    (int)Bn, b.side, d_hits, /*accumulate=*/false);
+            });
         }
         // InstantNerf.cu:488-494: the refresh changes only the grid that later
         // batches march and reads only the density head, so it runs on its
@@ -574,11 +582,6 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
             });
             GRAFT_HIP_CHECK(hipEventRecord(b.ev_join, b.occ));
         }
-        stage("hashScatter", [&] {
-            graft::hash_scatter(b.meta, db.dx_out, reinterpret_cast<const float*>(S.positions), 4, db.hashtable_grads,
-                                (int)Bn, stream, d_hits);
-        });
-        GRAFT_HIP_CHECK(hipEventRecord(S.ev_free, stream));  // the last read of this set
         // Adam: MLP layers of both heads on the side stream, the hash table on
         // the main stream; both after the refresh has read the parameters
         if (refresh) {
