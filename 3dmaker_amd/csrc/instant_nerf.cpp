@@ -616,8 +616,9 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
     GRAFT_HIP_CHECK(hipStreamWaitEvent(stream, b.ev_done_occ, 0));
 
     if (o.isProfiling && !b.pending.empty()) {
-        GRAFT_HIP_CHECK(hipEventSynchronize(b.pending.back().b));
         for (auto& t : b.pending) {
+            // stages on the side streams may end after the last one recorded
+            GRAFT_HIP_CHECK(hipEventSynchronize(t.b));
             float ms = 0.f;
             GRAFT_HIP_CHECK(hipEventElapsedTime(&ms, t.a, t.b));
             auto& s = b.stats[t.name];
