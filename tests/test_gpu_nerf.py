@@ -535,6 +535,33 @@ def test_instant_nerf_trains_over_many_batches(dev):
     nerf.close()
 
 
+def test_instant_nerf_stage_timers_cover_every_stream(dev):
+    """Per-stage timers of a profiled call: main-stream, side-stream (weight
+    gradients, compaction) and occupancy-stream stages all report positive
+    times, and the same call unprofiled trains the same number of steps."""
+    P = pkg()
+    opts = small_options(P, batch=1 << 13, chunk=2048)
+    nerf = P.Nerf(opts)
+    R = 20000
+    o, d = scenes.rays_c4(R, n_cams=30, seed=16)
+    gt = scenes.SphereScene(seed=3).render(o, d, steps=64)
+    d_o, d_d, d_gt = T(o, dev), T(d, dev), T(gt, dev)
+    nerf.set_profiling(True)
+    steps, _ = nerf.train(d_o, d_d, d_gt, R)
+    torch.cuda.synchronize()
+    st = nerf.stats()
+    nerf.set_profiling(False)
+    for stage in ("forward", "renderGrad", "hashScatter", "densityOpt", "colorBwd", "densityBwd", "colorOpt",
+                  "compaction", "occupancy"):
+        assert stage in st, (stage, sorted(st))
+        ms, calls = st[stage]
+        assert calls >= 1 and ms > 0.0, (stage, st[stage])
+    assert st["hashScatter"][1] == steps
+    nerf.reset_stats()
+    assert nerf.stats() == {}
+    nerf.close()
+
+
 def test_instant_nerf_cached_window_steps_match_oracle(dev):
     """Later hit batches of one call re-compact the stored march; the last one
     must equal a fresh oracle march of its window on the grid it used."""
