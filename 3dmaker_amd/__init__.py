@@ -185,6 +185,7 @@ SIGNATURES = {
     "inerf_destroy": (None, [_vp]),
     "inerf_train": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, C.POINTER(_i), _vp, _vp, _vp]),
     "inerf_set_learning_rate": (_i, [_vp, _f]),
+    "inerf_set_next_rays": (_i, [_vp, _vp, _vp, _u32]),
     "inerf_set_bg_color": (_i, [_vp, _f, _f, _f]),
     "inerf_set_profiling": (_i, [_vp, _i]),
     "inerf_print_stats": (_i, [_vp]),
@@ -478,6 +479,11 @@ class Nerf:
 
     def set_learning_rate(self, lr):
         self._c(self._L.inerf_set_learning_rate(self.h, float(lr)))
+
+    def set_next_rays(self, rays_o, rays_d, num_rays):
+        """setNextRays: the rays of the next train() call, already written; their first hit batch is
+        compacted beside this call's last step."""
+        self._c(self._L.inerf_set_next_rays(self.h, ptr(rays_o), ptr(rays_d), int(num_rays)))
 
     def set_bg_color(self, r, g, b):
         self._c(self._L.inerf_set_bg_color(self.h, float(r), float(g), float(b)))

@@ -60,6 +60,21 @@ struct NerfBuffers {
     uint32_t* block_sums = nullptr;
     StepSet set[2];
     int last_set = 0;                // set of the last training step
+    // Rays of the next trainWithRaysHit call (setNextRays), and the first hit
+    // batch of those rays, compacted beside the last step of the call before.
+    struct Ahead {
+        const float3* o = nullptr;
+        const float3* d = nullptr;
+        uint32_t n = 0;
+    } next;
+    struct Prefetched {
+        bool valid = false;
+        const float3* o = nullptr;
+        const float3* d = nullptr;
+        uint32_t n = 0;
+        int set = 0;
+        long version = -1;           // grid version it was marched on
+    } pre;
     float* render_rgb = nullptr;
     float* render_depth = nullptr;
     float* phi = nullptr;
@@ -338,6 +353,13 @@ void InstantNerf::setMemoryMode(MemoryMode mode)
     m_memMode = mode;
 }
 
+void InstantNerf::setNextRays(const float3* d_rays_o, const float3* d_rays_d, uint32_t numRays)
+{
+    if (!m_init) throw std::runtime_error("InstantNerf: init() must be called before setNextRays()");
+    if (numRays && (!d_rays_o || !d_rays_d)) throw std::runtime_error("InstantNerf: setNextRays needs ray buffers");
+    B(m_buf).next = numRays ? NerfBuffers::Ahead{d_rays_o, d_rays_d, numRays} : NerfBuffers::Ahead{};
+}
+
 // InstantNerf.cu:359-583
 void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_d, const float* d_rays_depth,
                                    const float* d_rays_sigma, const float* d_rgb_true, uint32_t numRays,
@@ -377,11 +399,11 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
     // is marched only when it is not covered by the cached march on the
     // current grid.  The set's previous step has finished reading it by
     // then: this runs after the side stream's wait on a later step's ev_dl.
-    auto compact = [&](int k, uint32_t raysDone) {
+    auto compact_rays = [&](int k, uint32_t raysDone, const float3* rays_o, const float3* rays_d, uint32_t nRays) {
         StepSet& S = b.set[k];
-        const uint32_t R = std::min<uint32_t>((uint32_t)o.rayChunkSize, numRays - raysDone);
-        const float3* co = d_rays_o + raysDone;
-        const float3* cd = d_rays_d + raysDone;
+        const uint32_t R = std::min<uint32_t>((uint32_t)o.rayChunkSize, nRays - raysDone);
+        const float3* co = rays_o + raysDone;
+        const float3* cd = rays_d + raysDone;
         if (b.cache_version != m_gridVersion || raysDone < b.cache_c0 || raysDone + R > b.cache_c1) {
             stage_on(b.side, "rayAabb", [&] {
                 graft::ray_aabb_inv(R, co, cd, o.aabbMin, o.aabbMax, o.numCascades, b.d_inv, b.nears, b.fars,
@@ -406,14 +428,26 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         GRAFT_HIP_CHECK(hipEventRecord(S.ev_ready, b.side));
         S.raysDone = raysDone;
     };
+    auto compact = [&](int k, uint32_t raysDone) { compact_rays(k, raysDone, d_rays_o, d_rays_d, numRays); };
 
     // the side streams start after everything the caller queued (rays, grid)
     GRAFT_HIP_CHECK(hipEventRecord(b.ev_fork, stream));
     GRAFT_HIP_CHECK(hipStreamWaitEvent(b.side, b.ev_fork, 0));
     GRAFT_HIP_CHECK(hipStreamWaitEvent(b.occ, b.ev_fork, 0));
-    b.cache_version = -1;  // new rays: nothing cached
+    // The first hit batch: compacted beside the previous call's last step
+    // when that call was told these rays (same buffers, same grid), else now.
+    const bool prefetched = b.pre.valid && b.pre.o == d_rays_o && b.pre.d == d_rays_d && b.pre.n == numRays &&
+                            b.pre.version == m_gridVersion;
+    b.pre.valid = false;
+    const NerfBuffers::Ahead next = b.next;
+    b.next = NerfBuffers::Ahead{};
     int k = 0, i = 0;
-    compact(k, 0);
+    if (prefetched) {
+        k = b.pre.set;
+    } else {
+        b.cache_version = -1;  // new rays: nothing cached
+        compact(k, 0);
+    }
     while (true) {
         StepSet& S = b.set[k];
         const uint32_t raysDone = S.raysDone;
@@ -605,7 +639,17 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         if (active == 0) throw std::runtime_error("InstantNerf: no ray fits the batch");
         if (hitCounts) hitCounts[i] = hits;
         i++;
-        if (raysDone + active >= numRays) break;
+        if (raysDone + active >= numRays) {
+            if (next.n) {
+                // the next call's first hit batch, beside this last step; the
+                // march store is keyed by ray index, so it holds this call's rays
+                k ^= 1;
+                b.cache_version = -1;
+                compact_rays(k, 0, next.o, next.d, next.n);
+                b.pre = NerfBuffers::Prefetched{true, next.o, next.d, next.n, k, m_gridVersion};
+            }
+            break;
+        }
         k ^= 1;
         compact(k, raysDone + active);
     }
@@ -840,6 +884,7 @@ void InstantNerf::renderImageHit(const float3* d_rays_o, const float3* d_rays_d,
     const uint32_t* d_rays = S.result;
     const uint32_t* d_hits = S.result + 1;
     b.cache_version = -1;  // the march store is reused below
+    b.pre.valid = false;   // and so is step set 0
 
     for (uint32_t c0 = 0; c0 < numRays; c0 += (uint32_t)o.rayChunkSize) {
         const uint32_t R = std::min<uint32_t>((uint32_t)o.rayChunkSize, numRays - c0);

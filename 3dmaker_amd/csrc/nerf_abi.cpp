@@ -367,6 +367,12 @@ int inerf_train(Inerf* h, const float* rays_o, const float* rays_d, const float*
 }
 
 int inerf_set_learning_rate(Inerf* h, float lr) { return NERF_CALL("inerf_set_learning_rate", h->nerf.setLearningRate(lr)); }
+int inerf_set_next_rays(Inerf* h, const float* rays_o, const float* rays_d, uint32_t num_rays)
+{
+    return NERF_CALL("inerf_set_next_rays",
+                     h->nerf.setNextRays(reinterpret_cast<const float3*>(rays_o),
+                                         reinterpret_cast<const float3*>(rays_d), num_rays));
+}
 int inerf_set_bg_color(Inerf* h, float r, float g, float b)
 {
     return NERF_CALL("inerf_set_bg_color", h->nerf.setBgColor(make_float3(r, g, b)));

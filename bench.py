@@ -190,56 +190,79 @@ def cosine_lr(step):
 
 
 class RayFeed:
-    """Device-resident RGBA8 views + launchFetchRayChunk (DataLoader.cu:548-679)."""
+    """Device-resident RGBA8 views + launchFetchRayChunk (DataLoader.cu:548-679), into one of two chunk
+    slots (the trainer fills the next chunk's slot while the current one trains); o, d, rgb, dense and
+    sigma name the current slot."""
 
     def __init__(self, P, torch, imgs, transforms, width, height, focal, chunk):
         dev = imgs.device
         self.P, self.imgs, self.w, self.h, self.focal, self.chunk = P, imgs, width, height, focal, chunk
         self.T = torch.from_numpy(transforms).to(dev)
         self.total = int(imgs.shape[0]) * width * height
-        self.o = torch.empty((chunk, 3), device=dev)
-        self.d = torch.empty((chunk, 3), device=dev)
-        self.rgb = torch.empty((chunk, 3), device=dev)
-        self.dense = torch.empty(chunk, device=dev)
-        self.sigma = torch.empty(chunk, device=dev)
+        self.slots = [{k: torch.empty((chunk, 3) if k in ("o", "d", "rgb") else chunk, device=dev)
+                       for k in ("o", "d", "rgb", "dense", "sigma")} for _ in range(2)]
+        self.slot = 0
 
-    def fetch(self, offset, size, seed, bg, stream, sequential=False):
+    def __getattr__(self, k):
+        if k in ("o", "d", "rgb", "dense", "sigma"):
+            return self.slots[self.slot][k]
+        raise AttributeError(k)
+
+    def fetch(self, offset, size, seed, bg, stream, sequential=False, slot=None):
+        b = self.slots[self.slot if slot is None else slot]
         self.P.lib().launchFetchRayChunk(int(offset), int(size), self.total, int(seed) & 0xffffffff,
                                          0 if sequential else 1, self.w, self.h, float(self.focal),
-                                         self.T.data_ptr(), self.imgs.data_ptr(), self.o.data_ptr(),
-                                         self.d.data_ptr(), self.rgb.data_ptr(), self.dense.data_ptr(),
-                                         self.sigma.data_ptr(), None, None, None, None, None, 0, 0.0, 1.0, 1.0,
+                                         self.T.data_ptr(), self.imgs.data_ptr(), b["o"].data_ptr(),
+                                         b["d"].data_ptr(), b["rgb"].data_ptr(), b["dense"].data_ptr(),
+                                         b["sigma"].data_ptr(), None, None, None, None, None, 0, 0.0, 1.0, 1.0,
                                          self.P.Float3(*map(float, bg)), 0, stream)
 
 
 class Trainer:
     """INerfTrainer::trainOneChunk (NerfTrainer.cu:137-179): per call a 2^16-ray
     chunk drawn by the ray feed with the epoch's seed, a random background
-    colour (the reference's random-bg augmentation), cosine LR, trainWithRaysHit."""
+    colour (the reference's random-bg augmentation), cosine LR, trainWithRaysHit.
+
+    The next chunk is drawn (same draw order: epoch seed at cursor 0, then the
+    background) and fetched into the other feed slot before the current chunk
+    trains, and handed to setNextRays, so that its first hit batch is compacted
+    beside the current chunk's last step."""
 
     def __init__(self, nerf, feed, stream):
         self.nerf, self.feed, self.stream = nerf, feed, stream
         self.rng = np.random.default_rng(42)
-        self.cursor = 0
+        self.cursor = 0      # first ray of the next chunk to draw
         self.step = 0
         self.epoch_seed = 0
+        self.ahead = None    # (offset, size, bg, slot) of the chunk fetched ahead
+
+    def _draw_and_fetch(self, slot):
+        f = self.feed
+        if self.cursor >= f.total:
+            self.cursor = 0
+        if self.cursor == 0:
+            self.epoch_seed = int(self.rng.integers(0, 1 << 32))
+        size = min(RAYS_PER_CALL, f.total - self.cursor)
+        bg = self.rng.random(3)
+        f.fetch(self.cursor, size, self.epoch_seed, bg, self.stream, slot=slot)
+        chunk = (self.cursor, size, bg, slot)
+        self.cursor += size
+        return chunk
 
     def run(self, nsteps):
         hits = []
         f = self.feed
         while len(hits) < nsteps:
-            if self.cursor >= f.total:
-                self.cursor = 0
-            if self.cursor == 0:
-                self.epoch_seed = int(self.rng.integers(0, 1 << 32))
-            size = min(RAYS_PER_CALL, f.total - self.cursor)
+            cur = self.ahead if self.ahead is not None else self._draw_and_fetch(f.slot)
+            _, size, bg, slot = cur
+            self.ahead = self._draw_and_fetch(slot ^ 1)
+            nb = f.slots[slot ^ 1]
+            self.nerf.set_next_rays(nb["o"], nb["d"], self.ahead[1])
+            f.slot = slot
             self.nerf.set_learning_rate(cosine_lr(self.step))
-            bg = self.rng.random(3)
             self.nerf.set_bg_color(*map(float, bg))
-            f.fetch(self.cursor, size, self.epoch_seed, bg, self.stream)
             n, h = self.nerf.train(f.o, f.d, f.rgb, size, rays_depth=f.dense, rays_sigma=f.sigma,
                                    stream=self.stream)
-            self.cursor += size
             self.step += n
             hits.extend(h)
         return hits

@@ -106,6 +106,15 @@ public:
     void setBgColor(float3 c) { m_opts.bgColor = c; }
     void setProfiling(bool p) { m_opts.isProfiling = p; }
     void setMemoryMode(MemoryMode mode);
+    // Addition (no reference counterpart): the rays of the NEXT
+    // trainWithRaysHit call, already written (queued on that call's stream)
+    // before the current call.  The current call then compacts their first
+    // hit batch on its side stream beside its last step, and the next call
+    // with exactly these buffers and count starts training at once instead of
+    // marching first.  The buffers must stay unchanged until that call; a call
+    // with other rays, a render or an occupancy change in between discards the
+    // prefetch (the call compacts as usual).  numRays = 0 clears.
+    void setNextRays(const float3* d_rays_o, const float3* d_rays_d, uint32_t numRays);
 
     // InstantNerf.cu:359-583.  d_rays_depth / d_rays_sigma may be null (depth
     // supervision off), d_rgb_true must be set, hitCounts (host, nullable)

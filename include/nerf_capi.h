@@ -67,6 +67,9 @@ int inerf_train(Inerf* h, const float* rays_o, const float* rays_d, const float*
                 const float* rgb_true, uint32_t num_rays, int* train_step_count, uint32_t* hit_counts,
                 float* rgb_out, hipStream_t stream);
 int inerf_set_learning_rate(Inerf* h, float lr);
+/* InstantNerf::setNextRays (no reference counterpart): rays of the next
+ * inerf_train call, compacted beside the current call's last step. */
+int inerf_set_next_rays(Inerf* h, const float* rays_o, const float* rays_d, uint32_t num_rays);
 int inerf_set_bg_color(Inerf* h, float r, float g, float b);
 int inerf_set_profiling(Inerf* h, int on);
 int inerf_print_stats(Inerf* h);
