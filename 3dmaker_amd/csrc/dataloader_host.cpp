@@ -8,6 +8,7 @@
 
 #include <cmath>
 #include <stdexcept>
+#include <utility>
 
 namespace {
 
@@ -89,6 +90,11 @@ void DataLoader::freeVRAM()
     dfree(d_chunk_rgb_true);
     dfree(d_chunk_rays_dense);
     dfree(d_chunk_rays_sigma);
+    dfree(d_ahead_rays_o);
+    dfree(d_ahead_rays_d);
+    dfree(d_ahead_rgb_true);
+    dfree(d_ahead_rays_dense);
+    dfree(d_ahead_rays_sigma);
     dfree(d_rec_frame);
     dfree(d_rec_u);
     dfree(d_rec_v);
@@ -122,6 +128,39 @@ void DataLoader::setDepthPriors(const int* frame, const float* u, const float* v
 void DataLoader::fetchRayChunk(int offset, int size, uint32_t seed, float3 bg_color, hipStream_t stream,
                                bool forceSequential, int holdout_every)
 {
+    fetch_into(d_chunk_rays_o, d_chunk_rays_d, d_chunk_rgb_true, d_chunk_rays_dense, d_chunk_rays_sigma, offset, size,
+               seed, bg_color, stream, forceSequential, holdout_every);
+}
+
+void DataLoader::fetchRayChunkAhead(int offset, int size, uint32_t seed, float3 bg_color, hipStream_t stream,
+                                    bool forceSequential, int holdout_every)
+{
+    if (!d_images_rgba) throw std::runtime_error("DataLoader: data freed");
+    if (!d_ahead_rays_o) {
+        d_ahead_rays_o = dcopy<float3>(nullptr, m_chunk);
+        d_ahead_rays_d = dcopy<float3>(nullptr, m_chunk);
+        d_ahead_rgb_true = dcopy<float>(nullptr, (size_t)m_chunk * 3);
+        d_ahead_rays_dense = dcopy<float>(nullptr, m_chunk);
+        d_ahead_rays_sigma = dcopy<float>(nullptr, m_chunk);
+    }
+    fetch_into(d_ahead_rays_o, d_ahead_rays_d, d_ahead_rgb_true, d_ahead_rays_dense, d_ahead_rays_sigma, offset, size,
+               seed, bg_color, stream, forceSequential, holdout_every);
+}
+
+void DataLoader::advanceChunk()
+{
+    if (!d_ahead_rays_o) throw std::runtime_error("DataLoader: no chunk fetched ahead");
+    std::swap(d_chunk_rays_o, d_ahead_rays_o);
+    std::swap(d_chunk_rays_d, d_ahead_rays_d);
+    std::swap(d_chunk_rgb_true, d_ahead_rgb_true);
+    std::swap(d_chunk_rays_dense, d_ahead_rays_dense);
+    std::swap(d_chunk_rays_sigma, d_ahead_rays_sigma);
+}
+
+void DataLoader::fetch_into(float3* o, float3* d, float* rgb, float* dense, float* sigma, int offset, int size,
+                            uint32_t seed, float3 bg_color, hipStream_t stream, bool forceSequential,
+                            int holdout_every)
+{
     if (!d_images_rgba) throw std::runtime_error("DataLoader: data freed");
     if (size < 0 || (uint32_t)size > m_chunk) throw std::runtime_error("DataLoader: chunk larger than ray_chunk_size");
     graft::RayFeedArgs a{};
@@ -135,11 +174,11 @@ void DataLoader::fetchRayChunk(int offset, int size, uint32_t seed, float3 bg_co
     a.focal = focal;
     a.transforms = d_transforms;
     a.images_rgba = d_images_rgba;
-    a.rays_o = d_chunk_rays_o;
-    a.rays_d = d_chunk_rays_d;
-    a.rgb = d_chunk_rgb_true;
-    a.dense = d_chunk_rays_dense;
-    a.sigma = d_chunk_rays_sigma;
+    a.rays_o = o;
+    a.rays_d = d;
+    a.rgb = rgb;
+    a.dense = dense;
+    a.sigma = sigma;
     a.rec_frame = d_rec_frame;
     a.rec_u = d_rec_u;
     a.rec_v = d_rec_v;

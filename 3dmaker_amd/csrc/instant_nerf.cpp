@@ -118,6 +118,7 @@ struct NerfBuffers {
     hipStream_t side = nullptr, occ = nullptr;
     hipEvent_t ev_fork = nullptr, ev_join = nullptr, ev_done = nullptr, ev_done_occ = nullptr;
     hipEvent_t ev_dl = nullptr;      // main: this step's MLP output gradients are written
+    hipEvent_t ev_occ_fork = nullptr;  // main: a refresh step's parameters are final (step start)
     std::vector<StageTimer> pending;
     std::map<std::string, std::pair<double, long>> stats;
 };
@@ -212,6 +213,7 @@ void InstantNerf::freeBuffers()
         if (b.ev_done) (void)hipEventDestroy(b.ev_done);
         if (b.ev_done_occ) (void)hipEventDestroy(b.ev_done_occ);
         if (b.ev_dl) (void)hipEventDestroy(b.ev_dl);
+        if (b.ev_occ_fork) (void)hipEventDestroy(b.ev_occ_fork);
         if (b.occ) (void)hipStreamDestroy(b.occ);
         if (b.side) (void)hipStreamDestroy(b.side);
         for (auto& t : b.pending) {
@@ -332,6 +334,7 @@ void InstantNerf::allocate()
     GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_done, kStreamEvent));
     GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_done_occ, kStreamEvent));
     GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_dl, kStreamEvent));
+    GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_occ_fork, kStreamEvent));
     GRAFT_HIP_CHECK(hipStreamCreateWithFlags(&b.occ, hipStreamNonBlocking));
     GRAFT_HIP_CHECK(hipStreamCreateWithFlags(&b.side, hipStreamNonBlocking));
 
@@ -463,6 +466,23 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         // S was compacted on the side stream after the previous step's MLP
         // Adam: once it is ready, the weights this forward uses are updated
         GRAFT_HIP_CHECK(hipStreamWaitEvent(stream, S.ev_ready, 0));
+        // InstantNerf.cu:488-494: the refresh reads only the density head's
+        // parameters -- the ones this step's forward reads, final once S is
+        // ready -- and changes only the grid that later batches march, so it
+        // runs on its own stream beside the whole step: forward, backward and
+        // scatter.  The density head's Adam updates and the next batch's march
+        // wait for it, so every kernel sees the parameters and grid of the
+        // serial order.
+        const bool refresh = (m_trainSteps % 16 == 0);
+        if (refresh) {
+            GRAFT_HIP_CHECK(hipEventRecord(b.ev_occ_fork, stream));
+            GRAFT_HIP_CHECK(hipStreamWaitEvent(b.occ, b.ev_occ_fork, 0));
+            stage_on(b.occ, "occupancy", [&] {
+                if (m_trainSteps < 256) earlyOccupancyGridUpdate(b.occ);
+                else lateOccupancyGridUpdate(b.occ);
+            });
+            GRAFT_HIP_CHECK(hipEventRecord(b.ev_join, b.occ));
+        }
         // hash encode + density head, SH gather (into the colour head's
         // activation 0), colour head: one launch, activations saved
         stage("forward", [&] {
@@ -600,31 +620,18 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
                                     (int)Bn, b.side, d_hits, /*accumulate=*/false);
             });
         }
-        // InstantNerf.cu:488-494: the refresh changes only the grid that later
-        // batches march and reads only the density head, so it runs on its
-        // own stream beside the scatter (which leaves most of every CU free),
-        // forked after this step's dX chain: by then the main stream has seen
-        // the previous step's Adam updates of both heads and the table.  This
-        // step's Adam updates and the next batch's march wait for it, so every
-        // kernel sees the same parameters and grid as in the serial order.
-        const bool refresh = (m_trainSteps % 16 == 0);
-        if (refresh) {
-            GRAFT_HIP_CHECK(hipStreamWaitEvent(b.occ, b.ev_dl, 0));
-            stage_on(b.occ, "occupancy", [&] {
-                if (m_trainSteps < 256) earlyOccupancyGridUpdate(b.occ);
-                else lateOccupancyGridUpdate(b.occ);
-            });
-            GRAFT_HIP_CHECK(hipEventRecord(b.ev_join, b.occ));
-        }
         // Adam: MLP layers of both heads on the side stream, the hash table on
-        // the main stream; both after the refresh has read the parameters
+        // the main stream.  The colour head's needs nothing of the refresh;
+        // the density head's (and, after it on the side stream, the next
+        // batch's march) waits until the refresh has read the parameters and
+        // written the grid.
+        stage_on(b.side, "colorOpt", [&] {
+            m_colorMLP->step(o.learningRate, o.beta1, o.beta2, o.epsilon, o.lossScale, b.side);
+        });
         if (refresh) {
             GRAFT_HIP_CHECK(hipStreamWaitEvent(stream, b.ev_join, 0));
             GRAFT_HIP_CHECK(hipStreamWaitEvent(b.side, b.ev_join, 0));
         }
-        stage_on(b.side, "colorOpt", [&] {
-            m_colorMLP->step(o.learningRate, o.beta1, o.beta2, o.epsilon, o.lossScale, b.side);
-        });
         stage("densityOpt", [&] {
             m_densityMLP->stepSplit(o.learningRate, o.beta1, o.beta2, o.epsilon, o.lossScale, b.side, stream);
         });

@@ -106,6 +106,7 @@ void INerfTrainer::loadDataset(const uint8_t* host_rgba, const float* host_trans
                                int height, float focal)
 {
     if (m_masterConfig.rayChunkSize <= 0) throw std::runtime_error("INerfTrainer: init() first");
+    dropAheadChunk();
     delete m_dataloader;
     m_dataloader = nullptr;
     m_dataloader = new DataLoader(host_rgba, host_transforms, numImages, width, height, focal,
@@ -140,20 +141,58 @@ float INerfTrainer::chunkMse(const float* d_pred, const float* d_target, int n)
     return h;
 }
 
+// The chunk fetched ahead is not used (the cursor moved or the data changed):
+// forget it and rewind the draws made for it, so that the chunk sequence stays
+// the one of the serial driver.
+void INerfTrainer::dropAheadChunk()
+{
+    if (!m_ahead.valid) return;
+    m_rng = m_ahead.rng_before;
+    m_ahead.valid = false;
+}
+
 // NerfTrainer.cu:137-179: one ray chunk from the epoch's seed with a random
 // background, all of its hit batches, optionally the chunk's colour MSE.
+// The next chunk is drawn (epoch seed when the cursor wraps, then the
+// background: the order the next call would draw them in) and fetched into
+// the loader's second slot before this one trains, so that its first hit
+// batch is compacted beside this chunk's last step.
 float INerfTrainer::trainOneChunk(bool computeLoss)
 {
     const uint32_t rayChunk = (uint32_t)m_masterConfig.rayChunkSize;
     if (m_rayCursor >= m_total_rays) m_rayCursor = 0;
-    if (m_rayCursor == 0) m_epochSeed = m_seed_dist(m_rng);
-    const int chunkSize = (int)std::min(rayChunk, m_total_rays - m_rayCursor);
+    int chunkSize = 0;
+    float3 bg{};
+    if (m_ahead.valid && m_ahead.cursor == m_rayCursor) {
+        m_dataloader->advanceChunk();
+        m_epochSeed = m_ahead.seed;
+        chunkSize = m_ahead.size;
+        bg = m_ahead.bg;
+        m_ahead.valid = false;
+    } else {
+        dropAheadChunk();
+        if (m_rayCursor == 0) m_epochSeed = m_seed_dist(m_rng);
+        chunkSize = (int)std::min(rayChunk, m_total_rays - m_rayCursor);
+        bg = make_float3(m_dist(m_rng), m_dist(m_rng), m_dist(m_rng));
+        m_dataloader->fetchRayChunk((int)m_rayCursor, chunkSize, m_epochSeed, bg, 0, false, (int)m_holdout_every);
+    }
+
+    AheadChunk next;
+    next.rng_before = m_rng;
+    next.cursor = m_rayCursor + (uint32_t)chunkSize;
+    if (next.cursor >= m_total_rays) next.cursor = 0;
+    next.seed = (next.cursor == 0) ? m_seed_dist(m_rng) : m_epochSeed;
+    next.size = (int)std::min(rayChunk, m_total_rays - next.cursor);
+    next.bg = make_float3(m_dist(m_rng), m_dist(m_rng), m_dist(m_rng));
+    next.valid = true;
+    m_dataloader->fetchRayChunkAhead((int)next.cursor, next.size, next.seed, next.bg, 0, false,
+                                     (int)m_holdout_every);
+    m_ahead = next;
 
     m_nerf->setLearningRate(currentLR());
     m_nerf->setMemoryMode(TRAINING);
-    const float3 bg = make_float3(m_dist(m_rng), m_dist(m_rng), m_dist(m_rng));
     m_nerf->setBgColor(bg);
-    m_dataloader->fetchRayChunk((int)m_rayCursor, chunkSize, m_epochSeed, bg, 0, false, (int)m_holdout_every);
+    m_nerf->setNextRays(m_dataloader->getAheadRaysO(), m_dataloader->getAheadRaysD(), (uint32_t)next.size);
 
     std::vector<uint32_t> hitCounts((size_t)chunkSize, 0);
     m_nerf->trainWithRaysHit(m_dataloader->getChunkRaysO(), m_dataloader->getChunkRaysD(),
@@ -168,6 +207,7 @@ float INerfTrainer::trainOneChunk(bool computeLoss)
 
 void INerfTrainer::beginTraining(int totalSteps)
 {
+    dropAheadChunk();
     m_targetSteps = std::max(1, totalSteps);
     m_globalStep = 0;
     m_rayCursor = 0;

@@ -46,6 +46,15 @@ public:
     // pcg_hash from seed (training), skipping every holdout_every-th image.
     void fetchRayChunk(int offset, int size, uint32_t seed, float3 bg_color = make_float3(1.0f, 1.0f, 1.0f),
                        hipStream_t stream = 0, bool forceSequential = false, int holdout_every = 0);
+    // Additions (no reference counterpart): a second chunk slot, so the next
+    // chunk can be fetched while the current one trains.  fetchRayChunkAhead
+    // fills the second slot (allocated on first use); advanceChunk swaps the
+    // slots, making the fetched-ahead chunk the current one.
+    void fetchRayChunkAhead(int offset, int size, uint32_t seed, float3 bg_color = make_float3(1.0f, 1.0f, 1.0f),
+                            hipStream_t stream = 0, bool forceSequential = false, int holdout_every = 0);
+    void advanceChunk();
+    const float3* getAheadRaysO() const { return d_ahead_rays_o; }
+    const float3* getAheadRaysD() const { return d_ahead_rays_d; }
     void freeVRAM();
 
     uint32_t getTotalRays() const { return total_rays; }
@@ -75,6 +84,13 @@ private:
     float* d_chunk_rgb_true = nullptr;
     float* d_chunk_rays_dense = nullptr;
     float* d_chunk_rays_sigma = nullptr;
+    float3* d_ahead_rays_o = nullptr;
+    float3* d_ahead_rays_d = nullptr;
+    float* d_ahead_rgb_true = nullptr;
+    float* d_ahead_rays_dense = nullptr;
+    float* d_ahead_rays_sigma = nullptr;
+    void fetch_into(float3* o, float3* d, float* rgb, float* dense, float* sigma, int offset, int size, uint32_t seed,
+                    float3 bg_color, hipStream_t stream, bool forceSequential, int holdout_every);
     int* d_rec_frame = nullptr;
     float* d_rec_u = nullptr;
     float* d_rec_v = nullptr;

@@ -108,6 +108,7 @@ public:
 private:
     void buildModel();
     float trainOneChunk(bool computeLoss);
+    void dropAheadChunk();
     float currentLR() const;
     Image renderC2W(const float c2w[16], float focal, int width, int height);
     float chunkMse(const float* d_pred, const float* d_target, int n);
@@ -142,4 +143,17 @@ private:
     std::mt19937 m_rng{42};
     std::uniform_real_distribution<float> m_dist{0.0f, 1.0f};
     std::uniform_int_distribution<uint32_t> m_seed_dist{0u, 0xFFFFFFFFu};
+
+    // The next chunk, drawn and fetched into the loader's second slot while
+    // the current one trains (InstantNerf::setNextRays compacts its first hit
+    // batch beside the current chunk's last step).  rng_before is the draw
+    // state before its draws, restored when the chunk is dropped unused.
+    struct AheadChunk {
+        bool valid = false;
+        uint32_t cursor = 0;
+        int size = 0;
+        uint32_t seed = 0;
+        float3 bg{};
+        std::mt19937 rng_before;
+    } m_ahead;
 };
