@@ -1,0 +1,587 @@
+// Binned hash-grid gradient scatter for gfx950: the table gradient of
+// hashTableScatter_Backward (networkFusionBackwardHashtable.cu:783-910),
+// grads[l][idx][f] += dL/denc[n][2l+f] * w_c over the 8 corners of every
+// (sample, level), backward clamp.
+//
+// The reference issues one global fp32 atomic per product.  On gfx950 those
+// atomics execute beyond the L2 and are priced per 64-byte line request, so a
+// 2^18-sample batch at T = 2^19 is bound by about 10 M line requests.  This
+// path sorts the products by table slice instead and sums every slice in LDS:
+//
+//  count       per round of kRound samples: how many corner-pair records fall
+//              into each bin (level, kSlice-entry slice of the level) and the
+//              largest |dL/denc| of each level;
+//  prefix      per bin: exclusive prefix of the counts over the rounds, and
+//              the bin's total;
+//  distribute  per round: every corner pair becomes one 16-byte record
+//              {x0 slot | x1 slot << 16, g0 * wyz, g1 * wyz, wx} written at its
+//              bin's cursor (bin base + round prefix + LDS rank); workgroup 0
+//              also writes the chunk table (<= kChunk records per chunk);
+//  accumulate  per chunk: the slice's sums in LDS as int64 fixed point
+//              (ds_add_u64), then one store per table entry.  A bin of several
+//              chunks adds its partial sums into an int64 staging slice with
+//              global 64-bit atomics, and its last chunk converts the slice.
+//
+// A corner pair is the two x-neighbour corners of one (y, z) corner.  Dense
+// levels index them x0 and x0 + 1 of one (y, z) row, and a dense slice is a
+// whole number of rows; hashed levels index them x0 ^ H and (x0 + 1) ^ H,
+// which differ only below bit bitlen(x0 + 1) <= 12, so both lie in one
+// 4096-entry aligned slice.
+//
+// Fixed point: a product c of level l has |c| <= max|g| of the level
+// < 2^(E+1) (the corner weights are <= 1); it adds rint(c * 2^e) with
+// e = 60 - E - ceil(log2(records of the bin)), so no partial or total sum of
+// the bin reaches 2^62.  Integer addition is exact and order-free: the result
+// is the exactly summed fixed-point products rounded once to fp32, whatever
+// the record order, chunking or scheduling (deterministic).  Non-finite
+// products take an fp32 atomic instead, so NaN/Inf reach the entry as they do
+// through the reference's atomics.
+#include "scatter.h"
+
+#include "hashgrid.h"
+
+#include <algorithm>
+#include <cmath>
+#include <map>
+#include <mutex>
+#include <utility>
+
+namespace graft {
+
+namespace {
+
+constexpr int kSlice = 4096;  // table entries (feature pairs) per bin
+constexpr int kSliceShift = 12;
+constexpr int kBinThreads = 256;
+constexpr int kSamplesPerThread = 2;
+constexpr int kRound = kBinThreads * kSamplesPerThread;
+constexpr uint32_t kChunk = 32768;  // records per accumulate workgroup
+constexpr int kAccThreads = 512;
+constexpr int kMaxBins = 8192;
+
+struct ScatterArgs {
+    const uint32_t* d_n;  // nullable device-side sample count (<= N)
+    int L, T, dense_start, pos_stride, N, bins, rounds;
+    uint32_t mask;
+    float scale[kMaxLevels];
+    int res[kMaxLevels];
+    int bin_base[kMaxLevels + 1];   // bins of level l: [bin_base[l], bin_base[l + 1])
+    int rows_per_slice[kMaxLevels]; // dense levels: (y, z) rows of N_l + 1 entries per slice
+};
+
+// The four (y, z) corner pairs of one sample at level l, with the backward
+// clamp and the weights of level_corners<true> (hash_encode.h); pair q holds
+// corners (y_{q&1}, z_{q>>1}).
+struct Pairs {
+    int bin[4];
+    uint32_t key[4];  // slot of x0 within the slice | slot of x1 << 16
+    float wyz[4];
+    float wx;         // weight of the x0 corner
+};
+
+__device__ __forceinline__ void level_pairs(const ScatterArgs& a, int l, float px, float py, float pz, Pairs& p)
+{
+    const float s = a.scale[l];
+    const int N_l = a.res[l];
+    const float x_l = px * s, y_l = py * s, z_l = pz * s;
+    const float fx = floorf(x_l), fy = floorf(y_l), fz = floorf(z_l);
+    const int hi = N_l - 1;
+    const int x0 = max(0, min((int)fx, hi));
+    const int y0 = max(0, min((int)fy, hi));
+    const int z0 = max(0, min((int)fz, hi));
+    const int x1 = min(x0 + 1, N_l), y1 = min(y0 + 1, N_l), z1 = min(z0 + 1, N_l);
+    const float wx1 = (1.0f - x_l) + fx;
+    const float wy1 = (1.0f - y_l) + fy;
+    const float wz1 = (1.0f - z_l) + fz;
+    const float uy = 1.0f - wy1, uz = 1.0f - wz1;
+    p.wx = wx1;
+    p.wyz[0] = wy1 * wz1;
+    p.wyz[1] = uy * wz1;
+    p.wyz[2] = wy1 * uz;
+    p.wyz[3] = uy * uz;
+    const int base = a.bin_base[l];
+    if (l < a.dense_start) {
+        const int st = N_l + 1;
+        const int rps = a.rows_per_slice[l];
+        const int rows[4] = {y0 + z0 * st, y1 + z0 * st, y0 + z1 * st, y1 + z1 * st};
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int sl = rows[q] / rps;
+            const uint32_t s0 = (uint32_t)((rows[q] - sl * rps) * st + x0);
+            p.bin[q] = base + sl;
+            p.key[q] = s0 | ((s0 + (uint32_t)(x1 - x0)) << 16);
+        }
+    } else {
+        const uint32_t hy0 = (uint32_t)y0 * 2654435761u, hy1 = (uint32_t)y1 * 2654435761u;
+        const uint32_t hz0 = (uint32_t)z0 * 805459861u, hz1 = (uint32_t)z1 * 805459861u;
+        const uint32_t h[4] = {hy0 ^ hz0, hy1 ^ hz0, hy0 ^ hz1, hy1 ^ hz1};
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const uint32_t s0 = ((uint32_t)x0 ^ h[q]) & a.mask;
+            const uint32_t s1 = ((uint32_t)x1 ^ h[q]) & a.mask;
+            p.bin[q] = base + (int)(s0 >> kSliceShift);
+            p.key[q] = (s0 & (kSlice - 1)) | ((s1 & (kSlice - 1)) << 16);
+        }
+    }
+}
+
+__device__ __forceinline__ int sample_count(const ScatterArgs& a) { return a.d_n ? min((int)*a.d_n, a.N) : a.N; }
+
+// |dL/denc| of a level's feature pair: the larger fp16 magnitude, as bits.
+__device__ __forceinline__ uint32_t pair_mag(uint32_t gb) { return max(gb & 0x7fffu, (gb >> 16) & 0x7fffu); }
+
+__global__ __launch_bounds__(kBinThreads) void scatter_count_kernel(const ScatterArgs a, const float* __restrict__ pos,
+                                                                    const _Float16* __restrict__ denc,
+                                                                    uint32_t* __restrict__ counts,
+                                                                    uint32_t* __restrict__ lvlmax)
+{
+    extern __shared__ uint32_t sh[];
+    uint32_t* hist = sh;
+    uint32_t* lmax = sh + a.bins;
+    for (int i = threadIdx.x; i < a.bins + a.L; i += kBinThreads) sh[i] = 0u;
+    __syncthreads();
+    const int N = sample_count(a);
+    for (int k = 0; k < kSamplesPerThread; k++) {
+        const int n = blockIdx.x * kRound + k * kBinThreads + threadIdx.x;
+        if (n >= N) break;
+        const float* pp = pos + (size_t)n * a.pos_stride;
+        const float px = pp[0], py = pp[1], pz = pp[2];
+        const uint32_t* grow = reinterpret_cast<const uint32_t*>(denc + (size_t)n * 2 * a.L);
+        for (int l = 0; l < a.L; l++) {
+            const uint32_t gb = grow[l];
+            if ((gb & 0x7fff7fffu) == 0u) continue;  // both features +-0: no product is nonzero
+            atomicMax(&lmax[l], pair_mag(gb));
+            Pairs p;
+            level_pairs(a, l, px, py, pz, p);
+#pragma unroll
+            for (int q = 0; q < 4; q++) atomicAdd(&hist[p.bin[q]], 1u);
+        }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < a.bins; i += kBinThreads) counts[(size_t)blockIdx.x * a.bins + i] = hist[i];
+    for (int i = threadIdx.x; i < a.L; i += kBinThreads) lvlmax[(size_t)blockIdx.x * a.L + i] = lmax[i];
+}
+
+// Lanes = 64 consecutive bins, the 4 waves = quarters of the rounds.
+// counts[r][b] <- sum over r' < r of counts[r'][b]; totals[b]; block 0 also
+// reduces the per-round level maxima.
+__global__ __launch_bounds__(256) void scatter_prefix_kernel(const ScatterArgs a, uint32_t* __restrict__ counts,
+                                                             uint32_t* __restrict__ totals,
+                                                             const uint32_t* __restrict__ lvlmax,
+                                                             uint32_t* __restrict__ lvlmax_out)
+{
+    __shared__ uint32_t part[4][64];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int b = blockIdx.x * 64 + lane;
+    const int R = a.rounds;
+    const int q = (R + 3) / 4;
+    const int r0 = min(R, w * q), r1 = min(R, r0 + q);
+    uint32_t s = 0;
+    if (b < a.bins)
+        for (int r = r0; r < r1; r++) s += counts[(size_t)r * a.bins + b];
+    part[w][lane] = s;
+    __syncthreads();
+    uint32_t run = 0;
+    for (int k = 0; k < w; k++) run += part[k][lane];
+    if (b < a.bins) {
+        for (int r = r0; r < r1; r++) {
+            const size_t i = (size_t)r * a.bins + b;
+            const uint32_t c = counts[i];
+            counts[i] = run;
+            run += c;
+        }
+        if (w == 3) totals[b] = run;
+    }
+    if (blockIdx.x == 0) {
+        for (int l = threadIdx.x; l < a.L; l += 256) {
+            uint32_t m = 0;
+            for (int r = 0; r < R; r++) m = max(m, lvlmax[(size_t)r * a.L + l]);
+            lvlmax_out[l] = m;
+        }
+    }
+}
+
+// Exclusive prefix sum of in[0, n) into out[0, n) (in == out allowed: every
+// thread reads and writes only its own segment); returns the total.  Every
+// thread of the 256-thread block calls it; wsum is 4 words of LDS.
+__device__ uint32_t block_exclusive_scan(const uint32_t* in, uint32_t* out, int n, uint32_t* wsum)
+{
+    const int per = (n + 255) / 256;
+    const int b0 = min(n, (int)threadIdx.x * per), b1 = min(n, b0 + per);
+    uint32_t s = 0;
+    for (int i = b0; i < b1; i++) s += in[i];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    uint32_t x = s;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t y = __shfl_up(x, d, 64);
+        if (lane >= d) x += y;
+    }
+    if (lane == 63) wsum[w] = x;
+    __syncthreads();
+    uint32_t run = x - s;
+    for (int k = 0; k < w; k++) run += wsum[k];
+    const uint32_t total = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+    for (int i = b0; i < b1; i++) {
+        const uint32_t v = in[i];
+        out[i] = run;
+        run += v;
+    }
+    __syncthreads();
+    return total;
+}
+
+// Chunk table entry: bin, first record, end record, (chunks of the bin) |
+// (staging slot of a multi-chunk bin) << 16.
+__global__ __launch_bounds__(kBinThreads) void scatter_distribute_kernel(
+    const ScatterArgs a, const float* __restrict__ pos, const _Float16* __restrict__ denc,
+    const uint32_t* __restrict__ prefix, const uint32_t* __restrict__ totals, float4* __restrict__ rec,
+    uint4* __restrict__ chunks, uint32_t* __restrict__ nchunks)
+{
+    extern __shared__ uint32_t sh[];
+    uint32_t* cur = sh;               // [bins]
+    uint32_t* aux = sh + a.bins;      // [bins] (block 0: chunk starts), then [bins] staging slots
+    __shared__ uint32_t wsum[4];
+    block_exclusive_scan(totals, cur, a.bins, wsum);
+    if (blockIdx.x == 0) {
+        uint32_t* kst = aux;
+        uint32_t* sst = aux + a.bins;
+        for (int b = threadIdx.x; b < a.bins; b += kBinThreads) {
+            const uint32_t k = (totals[b] + kChunk - 1) / kChunk;
+            kst[b] = k;
+            sst[b] = k > 1 ? 1u : 0u;
+        }
+        __syncthreads();
+        const uint32_t nch = block_exclusive_scan(kst, kst, a.bins, wsum);
+        block_exclusive_scan(sst, sst, a.bins, wsum);
+        for (int b = threadIdx.x; b < a.bins; b += kBinThreads) {
+            const uint32_t t = totals[b];
+            const uint32_t k = (t + kChunk - 1) / kChunk;
+            for (uint32_t j = 0; j < k; j++)
+                chunks[kst[b] + j] = make_uint4((uint32_t)b, cur[b] + j * kChunk, cur[b] + min((j + 1) * kChunk, t),
+                                                k | (sst[b] << 16));
+        }
+        if (threadIdx.x == 0) *nchunks = nch;
+    }
+    for (int b = threadIdx.x; b < a.bins; b += kBinThreads) cur[b] += prefix[(size_t)blockIdx.x * a.bins + b];
+    __syncthreads();
+    const int N = sample_count(a);
+    for (int k = 0; k < kSamplesPerThread; k++) {
+        const int n = blockIdx.x * kRound + k * kBinThreads + threadIdx.x;
+        if (n >= N) break;
+        const float* pp = pos + (size_t)n * a.pos_stride;
+        const float px = pp[0], py = pp[1], pz = pp[2];
+        const h2* grow = reinterpret_cast<const h2*>(denc + (size_t)n * 2 * a.L);
+        for (int l = 0; l < a.L; l++) {
+            const h2 gh = grow[l];
+            const uint32_t gb = __builtin_bit_cast(uint32_t, gh);
+            if ((gb & 0x7fff7fffu) == 0u) continue;
+            const float g0 = (float)gh.x, g1 = (float)gh.y;
+            Pairs p;
+            level_pairs(a, l, px, py, pz, p);
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const uint32_t at = atomicAdd(&cur[p.bin[q]], 1u);
+                rec[at] = make_float4(__uint_as_float(p.key[q]), g0 * p.wyz[q], g1 * p.wyz[q], p.wx);
+            }
+        }
+    }
+}
+
+__device__ __forceinline__ void add_fixed(unsigned long long* acc, float* gl, int i, float c, int e, int* flag)
+{
+    if (isfinite(c)) {
+        const long long q = (long long)rintf(ldexpf(c, e));
+        if (q != 0)
+            __hip_atomic_fetch_add(acc + i, (unsigned long long)q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    } else {
+        atomic_add_f32(gl + i, c);
+        *flag = 1;
+    }
+}
+
+__global__ __launch_bounds__(kAccThreads) void scatter_accumulate_kernel(
+    const ScatterArgs a, const float4* __restrict__ rec, const uint4* __restrict__ chunks,
+    const uint32_t* __restrict__ nchunks, const uint32_t* __restrict__ totals, const uint32_t* __restrict__ lvlmax,
+    float* __restrict__ grads, unsigned long long* __restrict__ stage, uint32_t* __restrict__ done, int grads_zero)
+{
+    __shared__ unsigned long long acc[2 * kSlice];
+    __shared__ int s_flag, s_last;
+    if (blockIdx.x >= *nchunks) return;
+    const uint4 ch = chunks[blockIdx.x];
+    const int bin = (int)ch.x;
+    const uint32_t kb = ch.w & 0xffffu, slot = ch.w >> 16;
+    int l = 0;
+    while (l + 1 < a.L && a.bin_base[l + 1] <= bin) l++;
+    const int sl = bin - a.bin_base[l];
+    int elem0, slots;
+    if (l < a.dense_start) {
+        const int st = a.res[l] + 1, rps = a.rows_per_slice[l];
+        const int row0 = sl * rps;
+        elem0 = row0 * st;
+        slots = min(rps, st * st - row0) * st;
+    } else {
+        elem0 = sl * kSlice;
+        slots = min(kSlice, a.T);
+    }
+    const uint32_t hb = lvlmax[l];
+    const int ex = (int)((hb >> 10) & 31u);
+    const int E = ex == 0 ? -15 : min(ex - 15, 15);
+    const uint32_t tot = totals[bin];
+    const int lg = tot <= 1u ? 0 : 32 - __clz(tot - 1u);
+    const int e = 60 - E - lg;
+    float* gl = grads + ((size_t)l * a.T + elem0) * 2;
+    for (int i = threadIdx.x; i < 2 * slots; i += kAccThreads) acc[i] = 0ull;
+    if (threadIdx.x == 0) s_flag = 0;
+    __syncthreads();
+    for (uint32_t i = ch.y + threadIdx.x; i < ch.z; i += kAccThreads) {
+        const float4 r = rec[i];
+        const uint32_t key = __float_as_uint(r.x);
+        const int s0 = (int)(key & 0xffffu), s1 = (int)(key >> 16);
+        const float ux = 1.0f - r.w;
+        add_fixed(acc, gl, 2 * s0, r.y * r.w, e, &s_flag);
+        add_fixed(acc, gl, 2 * s0 + 1, r.z * r.w, e, &s_flag);
+        add_fixed(acc, gl, 2 * s1, r.y * ux, e, &s_flag);
+        add_fixed(acc, gl, 2 * s1 + 1, r.z * ux, e, &s_flag);
+    }
+    __syncthreads();
+    if (kb == 1) {
+        // sole owner of the slice
+        const bool atomic = s_flag != 0;
+        for (int s = threadIdx.x; s < slots; s += kAccThreads) {
+            const long long q0 = (long long)acc[2 * s], q1 = (long long)acc[2 * s + 1];
+            const float v0 = ldexpf((float)q0, -e), v1 = ldexpf((float)q1, -e);
+            float2* gp = reinterpret_cast<float2*>(gl) + s;
+            if (atomic) {
+                if (q0) atomic_add_f32(gl + 2 * s, v0);
+                if (q1) atomic_add_f32(gl + 2 * s + 1, v1);
+            } else if (grads_zero) {
+                *gp = make_float2(v0, v1);
+            } else if (q0 | q1) {
+                float2 o = *gp;
+                o.x += v0;
+                o.y += v1;
+                *gp = o;
+            }
+        }
+        return;
+    }
+    unsigned long long* sg = stage + (size_t)slot * (2 * kSlice);
+    for (int i = threadIdx.x; i < 2 * slots; i += kAccThreads) {
+        const unsigned long long q = acc[i];
+        if (q) __hip_atomic_fetch_add(sg + i, q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0)
+        s_last = __hip_atomic_fetch_add(done + slot, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == kb - 1;
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+    for (int i = threadIdx.x; i < 2 * slots; i += kAccThreads) {
+        const long long q = (long long)__hip_atomic_load(sg + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (q) {
+            atomic_add_f32(gl + i, ldexpf((float)q, -e));
+            sg[i] = 0ull;
+        }
+    }
+    if (threadIdx.x == 0) done[slot] = 0u;
+}
+
+}  // namespace
+
+struct ScatterPlan {
+    int maxN = 0;
+    int max_chunks = 0;
+    int max_multi = 0;
+    GridMeta meta{};
+    ScatterArgs args{};
+    void* mem = nullptr;
+    float4* rec = nullptr;
+    uint32_t* counts = nullptr;
+    uint32_t* totals = nullptr;
+    uint32_t* lvlmax = nullptr;
+    uint32_t* lvlmax_final = nullptr;
+    uint4* chunks = nullptr;
+    uint32_t* nchunks = nullptr;
+    unsigned long long* stage = nullptr;
+    uint32_t* done = nullptr;
+};
+
+namespace {
+
+bool same_meta(const GridMeta& a, const GridMeta& b)
+{
+    if (a.numLevels != b.numLevels || a.tableSize != b.tableSize || a.denseLevelStart != b.denseLevelStart)
+        return false;
+    for (int l = 0; l < a.numLevels; l++)
+        if (a.scale[l] != b.scale[l] || a.res[l] != b.res[l]) return false;
+    return true;
+}
+
+// Bins of every level; false if the configuration is outside the binned
+// path's limits.
+bool layout(const GridMeta& m, ScatterArgs& a)
+{
+    a = ScatterArgs{};
+    a.L = m.numLevels;
+    a.T = m.tableSize;
+    a.dense_start = m.denseLevelStart;
+    a.mask = (uint32_t)m.tableSize - 1u;
+    int bins = 0;
+    for (int l = 0; l < m.numLevels; l++) {
+        a.scale[l] = m.scale[l];
+        a.res[l] = m.res[l];
+        a.bin_base[l] = bins;
+        if (m.res[l] < 1) return false;
+        if (l < m.denseLevelStart) {
+            const long long st = (long long)m.res[l] + 1;
+            if (st > kSlice) return false;
+            const int rps = (int)(kSlice / st);
+            a.rows_per_slice[l] = rps;
+            bins += (int)((st * st + rps - 1) / rps);
+        } else {
+            // x0 and x0 + 1 <= N_l must differ only below bit 12
+            if (m.res[l] >= kSlice) return false;
+            bins += std::max(1, m.tableSize / kSlice);
+        }
+        if (bins > kMaxBins) return false;
+    }
+    a.bin_base[m.numLevels] = bins;
+    a.bins = bins;
+    return true;
+}
+
+size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
+
+}  // namespace
+
+ScatterPlan* scatter_plan_create(const GridMeta& m, int maxN)
+{
+    ScatterArgs a;
+    if (maxN < 1 || !layout(m, a)) return nullptr;
+    const unsigned long long recs = 4ull * (unsigned long long)m.numLevels * (unsigned long long)maxN;
+    if (recs >= (1ull << 31)) return nullptr;
+    a.rounds = (maxN + kRound - 1) / kRound;
+    auto* p = new ScatterPlan();
+    p->maxN = maxN;
+    p->meta = m;
+    p->args = a;
+    p->max_chunks = (int)(recs / kChunk) + a.bins + 1;
+    p->max_multi = (int)std::min<unsigned long long>(recs / kChunk + 1, (unsigned long long)a.bins);
+    size_t off = 0;
+    const size_t o_rec = off; off = align_up(off + recs * sizeof(float4));
+    const size_t o_cnt = off; off = align_up(off + (size_t)a.rounds * a.bins * 4);
+    const size_t o_tot = off; off = align_up(off + (size_t)a.bins * 4);
+    const size_t o_lmx = off; off = align_up(off + (size_t)a.rounds * a.L * 4);
+    const size_t o_lmf = off; off = align_up(off + (size_t)a.L * 4);
+    const size_t o_chk = off; off = align_up(off + (size_t)p->max_chunks * sizeof(uint4));
+    const size_t o_nch = off; off = align_up(off + 4);
+    const size_t o_stg = off; off = align_up(off + (size_t)p->max_multi * 2 * kSlice * 8);
+    const size_t o_don = off; off = align_up(off + (size_t)p->max_multi * 4);
+    const size_t zero_from = o_stg;
+    hipError_t e = hipMalloc(&p->mem, off);
+    if (e != hipSuccess) {
+        delete p;
+        GRAFT_HIP_CHECK(e);
+    }
+    char* base = static_cast<char*>(p->mem);
+    p->rec = reinterpret_cast<float4*>(base + o_rec);
+    p->counts = reinterpret_cast<uint32_t*>(base + o_cnt);
+    p->totals = reinterpret_cast<uint32_t*>(base + o_tot);
+    p->lvlmax = reinterpret_cast<uint32_t*>(base + o_lmx);
+    p->lvlmax_final = reinterpret_cast<uint32_t*>(base + o_lmf);
+    p->chunks = reinterpret_cast<uint4*>(base + o_chk);
+    p->nchunks = reinterpret_cast<uint32_t*>(base + o_nch);
+    p->stage = reinterpret_cast<unsigned long long*>(base + o_stg);
+    p->done = reinterpret_cast<uint32_t*>(base + o_don);
+    // the staging slices and their counters start (and are left) zero
+    e = hipMemset(base + zero_from, 0, off - zero_from);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        (void)hipFree(p->mem);
+        delete p;
+        GRAFT_HIP_CHECK(e);
+    }
+    return p;
+}
+
+void scatter_plan_destroy(ScatterPlan* p)
+{
+    if (!p) return;
+    if (p->mem) (void)hipFree(p->mem);
+    delete p;
+}
+
+int scatter_plan_max_samples(const ScatterPlan* p) { return p ? p->maxN : 0; }
+
+void hash_scatter_binned(ScatterPlan* p, const GridMeta& m, const __half* denc, const float* pos, int pos_stride,
+                         float* grads, int N, hipStream_t stream, const uint32_t* d_n, bool grads_zero)
+{
+    if (N <= 0) return;
+    if (!p) throw std::runtime_error("hash scatter: no scatter plan");
+    if (pos_stride < 3) throw std::runtime_error("hash scatter: position stride must be >= 3");
+    if (N > p->maxN) throw std::runtime_error("hash scatter: batch exceeds the plan's sample capacity");
+    if (!same_meta(p->meta, m)) throw std::runtime_error("hash scatter: plan built for another grid");
+    ScatterArgs a = p->args;
+    a.d_n = d_n;
+    a.N = N;
+    a.pos_stride = pos_stride;
+    a.rounds = (N + kRound - 1) / kRound;
+    const auto* dh = reinterpret_cast<const _Float16*>(denc);
+    const size_t lds_count = (size_t)(a.bins + a.L) * 4;
+    const size_t lds_dist = (size_t)(3 * a.bins) * 4;
+    hipLaunchKernelGGL(scatter_count_kernel, dim3(a.rounds), dim3(kBinThreads), lds_count, stream, a, pos, dh,
+                       p->counts, p->lvlmax);
+    GRAFT_LAUNCH_CHECK();
+    hipLaunchKernelGGL(scatter_prefix_kernel, dim3((a.bins + 63) / 64), dim3(256), 0, stream, a, p->counts,
+                       p->totals, p->lvlmax, p->lvlmax_final);
+    GRAFT_LAUNCH_CHECK();
+    hipLaunchKernelGGL(scatter_distribute_kernel, dim3(a.rounds), dim3(kBinThreads), lds_dist, stream, a, pos, dh,
+                       p->counts, p->totals, p->rec, p->chunks, p->nchunks);
+    GRAFT_LAUNCH_CHECK();
+    const unsigned long long recs = 4ull * (unsigned long long)a.L * (unsigned long long)N;
+    const int grid = (int)std::min<unsigned long long>(recs / kChunk + a.bins + 1, (unsigned long long)p->max_chunks);
+    hipLaunchKernelGGL(scatter_accumulate_kernel, dim3(grid), dim3(kAccThreads), 0, stream, a, p->rec, p->chunks,
+                       p->nchunks, p->totals, p->lvlmax_final, grads, p->stage, p->done, grads_zero ? 1 : 0);
+    GRAFT_LAUNCH_CHECK();
+}
+
+namespace {
+
+// Scratch of the stateless launchers, one plan per (device, stream): two
+// streams never share one.  A plan is replaced (after its stream drains) when
+// a call needs more samples or another grid.  Plans live until the process
+// ends.
+std::mutex g_plans_mu;
+std::map<std::pair<int, hipStream_t>, ScatterPlan*> g_plans;
+
+ScatterPlan* plan_for_stream(const GridMeta& m, int N, hipStream_t stream)
+{
+    int dev = 0;
+    GRAFT_HIP_CHECK(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lk(g_plans_mu);
+    ScatterPlan*& p = g_plans[{dev, stream}];
+    if (p && (p->maxN < N || !same_meta(p->meta, m))) {
+        GRAFT_HIP_CHECK(hipStreamSynchronize(stream));
+        scatter_plan_destroy(p);
+        p = nullptr;
+    }
+    if (!p) p = scatter_plan_create(m, N);
+    return p;
+}
+
+}  // namespace
+
+void hash_scatter(const GridMeta& m, const __half* denc, const float* pos, int pos_stride, float* grads, int N,
+                  hipStream_t stream, const uint32_t* d_n)
+{
+    if (N <= 0) return;
+    ScatterPlan* p = plan_for_stream(m, N, stream);
+    if (p)
+        hash_scatter_binned(p, m, denc, pos, pos_stride, grads, N, stream, d_n, /*grads_zero=*/false);
+    else
+        hash_scatter_atomic(m, denc, pos, pos_stride, grads, N, stream, d_n);
+}
+
+}  // namespace graft

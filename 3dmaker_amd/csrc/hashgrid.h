@@ -17,7 +17,13 @@ void hash_encode_planar(const GridMeta& m, const __half* table, const float* pos
 
 // grads [L][T][2] += scatter of denc [N x 2L] (backward clamp).
 // d_n (nullable): device-side sample count (<= N), as for the MLP kernels.
+// The binned path (scatter.h) with scratch cached per (device, stream), or,
+// for configurations outside its limits, hash_scatter_atomic.
 void hash_scatter(const GridMeta& m, const __half* denc, const float* pos, int pos_stride,
                   float* grads, int N, hipStream_t stream, const uint32_t* d_n = nullptr);
+
+// The same sum with one fp32 global atomic per run of equal corners.
+void hash_scatter_atomic(const GridMeta& m, const __half* denc, const float* pos, int pos_stride,
+                         float* grads, int N, hipStream_t stream, const uint32_t* d_n = nullptr);
 
 }  // namespace graft

@@ -233,8 +233,8 @@ void hash_encode_planar(const GridMeta& m, const __half* table, const float* pos
     GRAFT_LAUNCH_CHECK();
 }
 
-void hash_scatter(const GridMeta& m, const __half* denc, const float* pos, int pos_stride,
-                  float* grads, int N, hipStream_t stream, const uint32_t* d_n)
+void hash_scatter_atomic(const GridMeta& m, const __half* denc, const float* pos, int pos_stride,
+                         float* grads, int N, hipStream_t stream, const uint32_t* d_n)
 {
     if (N <= 0) return;
     if (pos_stride < 3) throw std::runtime_error("hash scatter: position stride must be >= 3");

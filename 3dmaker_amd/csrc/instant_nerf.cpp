@@ -8,6 +8,7 @@
 #include "InstantNerf.h"
 
 #include "hashgrid.h"
+#include "scatter.h"
 #include "mlp.h"
 #include "nerf.h"
 #include "nerf_math.h"
@@ -601,8 +602,15 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         // side streams' work, so that the host's launches of that work never
         // delay it.
         stage("hashScatter", [&] {
-            graft::hash_scatter(b.meta, db.dx_out, reinterpret_cast<const float*>(S.positions), 4, db.hashtable_grads,
-                                (int)Bn, stream, d_hits);
+            // the table gradient is all zero here: the previous step's Adam
+            // cleared every entry it consumed
+            if (db.scatter_plan)
+                graft::hash_scatter_binned(static_cast<graft::ScatterPlan*>(db.scatter_plan), b.meta, db.dx_out,
+                                           reinterpret_cast<const float*>(S.positions), 4, db.hashtable_grads,
+                                           (int)Bn, stream, d_hits, /*grads_zero=*/true);
+            else
+                graft::hash_scatter_atomic(b.meta, db.dx_out, reinterpret_cast<const float*>(S.positions), 4,
+                                           db.hashtable_grads, (int)Bn, stream, d_hits);
         });
         // Beside it: the weight gradients (this step's gradient overwrites the
         // last one: no zero_grad pass).  The side stream's wait on ev_dl also

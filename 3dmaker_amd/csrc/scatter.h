@@ -1,0 +1,30 @@
+// Internal interface of the binned hash-grid gradient scatter (hash_scatter.hip).
+#pragma once
+
+#include "common.h"
+
+namespace graft {
+
+// Device scratch of the binned scatter, sized once for a grid configuration
+// and a maximum sample count; one per owner (a TinyMLPHashGrid instance, or
+// the launchers' per-stream cache), so that scatters driven from different
+// owners never share it.
+struct ScatterPlan;
+
+// nullptr when the configuration is outside the binned path's limits (then
+// hash_scatter falls back to the per-corner atomic kernel).
+ScatterPlan* scatter_plan_create(const GridMeta& m, int maxN);
+void scatter_plan_destroy(ScatterPlan* p);
+int scatter_plan_max_samples(const ScatterPlan* p);
+
+// grads [L][T][2] += scatter of denc [N x 2L] (backward clamp), as the
+// atomic hash_scatter, with the table sums formed in fixed point (exact
+// integer addition, one rounding to fp32 per entry): deterministic.
+// grads_zero: the caller guarantees that grads is all zero on entry (the
+// training step: Adam clears every gradient it consumes); the entries of the
+// bins the batch touches are then stored instead of read-modify-written.
+void hash_scatter_binned(ScatterPlan* p, const GridMeta& m, const __half* denc, const float* pos,
+                         int pos_stride, float* grads, int N, hipStream_t stream, const uint32_t* d_n,
+                         bool grads_zero);
+
+}  // namespace graft

@@ -9,6 +9,7 @@
 #include "hashgrid.h"
 #include "mlp.h"
 #include "optimizer.h"
+#include "scatter.h"
 
 #include <algorithm>
 #include <cmath>
@@ -595,6 +596,7 @@ void TinyMLPHashGrid::allocate_memory()
         d_b_m = TT.bm.dev<float>();
         d_b_v = TT.bv.dev<float>();
         d_activations = TT.acts.dev<half>();
+        if (!m_scatter) m_scatter = graft::scatter_plan_create(META, m_maxBatchSize);
     }
 }
 
@@ -609,6 +611,8 @@ void TinyMLPHashGrid::free_training_state()
     }
     destroy_training_tables(TT);
     TT.acts.destroy();
+    graft::scatter_plan_destroy(static_cast<graft::ScatterPlan*>(m_scatter));
+    m_scatter = nullptr;
     d_w_grad = d_b_grad = d_w_m = d_w_v = d_b_m = d_b_v = nullptr;
     d_activations = nullptr;
     d_current_inputs_backward = nullptr;
@@ -734,7 +738,13 @@ void TinyMLPHashGrid::run_backward(int batchSize, hipStream_t stream)
     if (batchSize <= 0) return;
     graft::mlp_backward(shape_of(mlp_opt), d_dLoss_internal, d_activations, d_fwd_weights, d_w_grad, d_b_grad,
                         d_dx_out, batchSize, stream);
-    graft::hash_scatter(META, d_dx_out, d_current_inputs_backward, 4, d_hashtable_grads, batchSize, stream);
+    if (m_scatter)
+        graft::hash_scatter_binned(static_cast<graft::ScatterPlan*>(m_scatter), META, d_dx_out,
+                                   d_current_inputs_backward, 4, d_hashtable_grads, batchSize, stream, nullptr,
+                                   /*grads_zero=*/false);
+    else
+        graft::hash_scatter_atomic(META, d_dx_out, d_current_inputs_backward, 4, d_hashtable_grads, batchSize,
+                                   stream);
 }
 
 // TinyMLPHashGrid.cu:336-377 (split and fused scatter are one path here).
@@ -868,5 +878,7 @@ TinyMLPHashGrid::Buffers TinyMLPHashGrid::buffers() const
     b.padded_outputs = d_padded_outputs_float;
     b.hw = hw_opt;
     b.step = current_step;
+    b.scatter_plan = m_scatter;
+    b.scatter_plan = m_scatter;
     return b;
 }

@@ -89,6 +89,7 @@ public:
         float* padded_outputs;
         MLPGridOptions hw;
         int step;
+        void* scatter_plan;       // binned-scatter scratch (opaque); null: per-corner atomic scatter
     };
     Buffers buffers() const;
 
@@ -129,6 +130,7 @@ private:
     float** d_b_v = nullptr;
     void* h_ptrs = nullptr;
     void* m_meta = nullptr;   // hash-grid level table (opaque)
+    void* m_scatter = nullptr; // binned-scatter scratch of this instance (opaque)
 
     void allocate_memory();
     void free_training_state();

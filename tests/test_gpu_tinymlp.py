@@ -45,6 +45,7 @@ def edge_positions(n, seed):
 
 
 @pytest.mark.parametrize("N,T_,b,L", [(4096, 1 << 14, 1.447, 16), (1 << 18, 1 << 19, (2048 / 16) ** (1 / 15), 16),
+                                      (1 << 20, 1 << 19, (2048 / 16) ** (1 / 15), 16),   # BASELINE C2, second size
                                       (1000, 1 << 12, 1.5, 7), (1, 1 << 14, 1.447, 16)])
 def test_encode_bit_exact(dev, N, T_, b, L):
     P = pkg()
@@ -62,6 +63,8 @@ def test_encode_bit_exact(dev, N, T_, b, L):
 
 @pytest.mark.parametrize("N,T_,L,b,dist", [
     (1 << 18, 1 << 19, 16, (2048 / 16) ** (1 / 15), "uniform"),   # BASELINE C2 backward
+    (1 << 20, 1 << 19, 16, (2048 / 16) ** (1 / 15), "uniform"),   # BASELINE C2, second size
+    (1 << 18, 1 << 19, 16, 1.3819, "clustered"),                  # multi-chunk bins at every dense level
     (1 << 16, 1 << 14, 16, 1.447, "clustered"),                   # collision-heavy dense levels
     (3000, 1 << 19, 16, 1.3819, "uniform"),                        # small, ragged batch
     (1 << 16, 1 << 19, 16, 1.3819, "rays"),                        # ray-ordered: merged runs
@@ -89,6 +92,55 @@ def test_scatter_matches_oracle(dev, N, T_, L, b, dist):
     got = grads.cpu().numpy()
     scale = np.abs(want - 0.5).max()
     assert_close(got, want, atol=2e-6 * scale + 1e-6, rtol=1e-5, what="hash grads")
+
+
+def _scatter_inputs(N, L, seed, dist):
+    rng = np.random.default_rng(seed)
+    pos = positions(N, seed + 1)
+    if dist == "clustered":
+        pos[:, :3] = (0.5 + 0.02 * rng.normal(size=(N, 3))).clip(0, 1).astype(np.float32)
+    denc = rng.normal(0, 1, (N, 2 * L)).astype(np.float16)
+    return pos, denc
+
+
+def test_scatter_is_deterministic(dev):
+    """Fixed-point sums: bitwise equal results run to run, also for bins split over several chunks."""
+    P = pkg()
+    N, T_, L, b = 1 << 18, 1 << 19, 16, 1.3819
+    pos, denc = _scatter_inputs(N, L, 31, "clustered")
+    d_pos, d_denc = T(pos, dev), T(denc, dev)
+    outs = []
+    for _ in range(2):
+        grads = torch.zeros(L * T_ * 2, dtype=torch.float32, device=dev)
+        P.launch("launchHashTableBackwardKernel", d_denc, d_pos, grads, N, T_, L, b, 16, 2, None)
+        torch.cuda.synchronize()
+        outs.append(grads.cpu().numpy())
+    np.testing.assert_array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    want = orc.hash_scatter(pos, denc, T_, L, 16, b)
+    assert_close(outs[0], want, atol=2e-6 * np.abs(want).max() + 1e-6, rtol=1e-5, what="hash grads")
+
+
+def test_scatter_nonfinite_inputs_propagate(dev):
+    """Inf / NaN upstream gradients reach exactly the entries the oracle's sums make non-finite."""
+    P = pkg()
+    N, T_, L, b = 20000, 1 << 19, 16, 1.3819
+    pos, denc = _scatter_inputs(N, L, 41, "uniform")
+    denc[5, 3] = np.float16(np.inf)
+    denc[77, 20] = np.float16(-np.inf)
+    denc[900, 31] = np.float16(np.nan)
+    denc[1234, 0] = np.float16(65504.0)  # largest finite magnitude sets the level's fixed-point scale
+    grads = torch.zeros(L * T_ * 2, dtype=torch.float32, device=dev)
+    P.launch("launchHashTableBackwardKernel", T(denc, dev), T(pos, dev), grads, N, T_, L, b, 16, 2, None)
+    torch.cuda.synchronize()
+    got = grads.cpu().numpy()
+    with np.errstate(invalid="ignore"):
+        want = orc.hash_scatter(pos, denc, T_, L, 16, b)
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(want))
+    np.testing.assert_array_equal(np.isposinf(got), np.isposinf(want))
+    np.testing.assert_array_equal(np.isneginf(got), np.isneginf(want))
+    fin = np.isfinite(want)
+    assert fin.sum() < fin.size and (~fin).sum() >= 3
+    assert_close(got[fin], want[fin], atol=2e-6 * np.abs(want[fin]).max() + 1e-6, rtol=1e-5, what="finite grads")
 
 
 def test_encode_stride3(dev):
