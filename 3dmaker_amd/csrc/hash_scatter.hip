@@ -30,8 +30,9 @@
 //
 // Fixed point: a product c of level l has |c| <= max|g| of the level
 // < 2^(E+1) (the corner weights are <= 1); it adds rint(c * 2^e) with
-// e = 60 - E - ceil(log2(records of the bin)), so no partial or total sum of
-// the bin reaches 2^62.  Integer addition is exact and order-free: the result
+// e = min(49, 60 - ceil(log2(records of the bin))) - E, so every product is
+// below 2^50 (the fp64 rounding trick of fixed_of needs < 2^51) and no
+// partial or total sum of the bin reaches 2^62.  Integer addition is exact and order-free: the result
 // is the exactly summed fixed-point products rounded once to fp32, whatever
 // the record order, chunking or scheduling (deterministic).  Non-finite
 // products take an fp32 atomic instead, so NaN/Inf reach the entry as they do
@@ -130,6 +131,60 @@ __device__ __forceinline__ int sample_count(const ScatterArgs& a) { return a.d_n
 // |dL/denc| of a level's feature pair: the larger fp16 magnitude, as bits.
 __device__ __forceinline__ uint32_t pair_mag(uint32_t gb) { return max(gb & 0x7fffu, (gb >> 16) & 0x7fffu); }
 
+// dL/denc of levels [l0, l0 + kLevelGroup) of one sample's row, loaded
+// together (16-byte loads when the row is 16-byte aligned); zero past L.
+constexpr int kLevelGroup = 16;
+
+__device__ __forceinline__ void load_levels(const uint32_t* grow, int l0, int L, bool vec,
+                                            uint32_t (&g)[kLevelGroup])
+{
+    if (vec && l0 + kLevelGroup <= L) {
+        const uint4* v = reinterpret_cast<const uint4*>(grow + l0);
+#pragma unroll
+        for (int j = 0; j < kLevelGroup / 4; j++) {
+            const uint4 t = v[j];
+            g[4 * j] = t.x;
+            g[4 * j + 1] = t.y;
+            g[4 * j + 2] = t.z;
+            g[4 * j + 3] = t.w;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < kLevelGroup; j++) g[j] = l0 + j < L ? grow[l0 + j] : 0u;
+    }
+}
+
+// Lanes whose bin equals the first active lane's add together (one LDS
+// atomic): dense levels map most of a wave's samples to a handful of bins.
+__device__ __forceinline__ void bin_add(uint32_t* hist, int bin)
+{
+    const uint64_t act = __ballot(1);
+    const int first = __ffsll((unsigned long long)act) - 1;
+    const int b0 = __shfl(bin, first, 64);
+    const uint64_t same = __ballot(bin == b0);
+    if (bin != b0)
+        atomicAdd(&hist[bin], 1u);
+    else if ((int)(threadIdx.x & 63) == first)
+        atomicAdd(&hist[b0], (uint32_t)__popcll(same));
+}
+
+// The same with each lane's rank: the slot it takes at its bin's cursor.
+__device__ __forceinline__ uint32_t bin_take(uint32_t* cur, int bin)
+{
+    const uint64_t act = __ballot(1);
+    const int first = __ffsll((unsigned long long)act) - 1;
+    const int b0 = __shfl(bin, first, 64);
+    const uint64_t same = __ballot(bin == b0);
+    uint32_t at = 0;
+    if (bin != b0) {
+        at = atomicAdd(&cur[bin], 1u);
+    } else {
+        if ((int)(threadIdx.x & 63) == first) at = atomicAdd(&cur[b0], (uint32_t)__popcll(same));
+        at = __shfl(at, first, 64) + (uint32_t)__popcll(same & __lanemask_lt());
+    }
+    return at;
+}
+
 __global__ __launch_bounds__(kBinThreads) void scatter_count_kernel(const ScatterArgs a, const float* __restrict__ pos,
                                                                     const _Float16* __restrict__ denc,
                                                                     uint32_t* __restrict__ counts,
@@ -141,20 +196,40 @@ __global__ __launch_bounds__(kBinThreads) void scatter_count_kernel(const Scatte
     for (int i = threadIdx.x; i < a.bins + a.L; i += kBinThreads) sh[i] = 0u;
     __syncthreads();
     const int N = sample_count(a);
+    const bool vec = (a.L & 3) == 0;
     for (int k = 0; k < kSamplesPerThread; k++) {
         const int n = blockIdx.x * kRound + k * kBinThreads + threadIdx.x;
-        if (n >= N) break;
-        const float* pp = pos + (size_t)n * a.pos_stride;
-        const float px = pp[0], py = pp[1], pz = pp[2];
-        const uint32_t* grow = reinterpret_cast<const uint32_t*>(denc + (size_t)n * 2 * a.L);
-        for (int l = 0; l < a.L; l++) {
-            const uint32_t gb = grow[l];
-            if ((gb & 0x7fff7fffu) == 0u) continue;  // both features +-0: no product is nonzero
-            atomicMax(&lmax[l], pair_mag(gb));
-            Pairs p;
-            level_pairs(a, l, px, py, pz, p);
+        const bool valid = n < N;
+        float px = 0.f, py = 0.f, pz = 0.f;
+        const uint32_t* grow = reinterpret_cast<const uint32_t*>(denc + (size_t)(valid ? n : 0) * 2 * a.L);
+        if (valid) {
+            const float* pp = pos + (size_t)n * a.pos_stride;
+            px = pp[0];
+            py = pp[1];
+            pz = pp[2];
+        }
+        for (int l0 = 0; l0 < a.L; l0 += kLevelGroup) {
+            uint32_t gv[kLevelGroup];
+            load_levels(grow, l0, a.L, vec, gv);
 #pragma unroll
-            for (int q = 0; q < 4; q++) atomicAdd(&hist[p.bin[q]], 1u);
+            for (int j = 0; j < kLevelGroup; j++) {
+                const int l = l0 + j;
+                if (l >= a.L) break;
+                const uint32_t gb = valid ? gv[j] : 0u;
+                const bool live = (gb & 0x7fff7fffu) != 0u;  // else both features +-0: no product is nonzero
+                const uint32_t m = __ockl_wfred_max_u32(pair_mag(gb));
+                if ((threadIdx.x & 63) == 0 && m) atomicMax(&lmax[l], m);
+                if (!live) continue;
+                Pairs p;
+                level_pairs(a, l, px, py, pz, p);
+                if (l < a.dense_start) {
+#pragma unroll
+                    for (int q = 0; q < 4; q++) bin_add(hist, p.bin[q]);
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 4; q++) atomicAdd(&hist[p.bin[q]], 1u);
+                }
+            }
         }
     }
     __syncthreads();
@@ -162,51 +237,63 @@ __global__ __launch_bounds__(kBinThreads) void scatter_count_kernel(const Scatte
     for (int i = threadIdx.x; i < a.L; i += kBinThreads) lvlmax[(size_t)blockIdx.x * a.L + i] = lmax[i];
 }
 
-// Lanes = 64 consecutive bins, the 4 waves = quarters of the rounds.
-// counts[r][b] <- sum over r' < r of counts[r'][b]; totals[b]; block 0 also
-// reduces the per-round level maxima.
-__global__ __launch_bounds__(256) void scatter_prefix_kernel(const ScatterArgs a, uint32_t* __restrict__ counts,
-                                                             uint32_t* __restrict__ totals,
-                                                             const uint32_t* __restrict__ lvlmax,
-                                                             uint32_t* __restrict__ lvlmax_out)
+// Threads = kPrefixBins consecutive bins x kPrefixGroups groups of rounds.
+// counts[r][b] <- sum over r' < r of counts[r'][b]; totals[b].  Block x < L
+// also reduces level x's per-round maxima.
+constexpr int kPrefixBins = 8;
+constexpr int kPrefixGroups = 32;
+constexpr int kPrefixThreads = kPrefixBins * kPrefixGroups;
+
+__global__ __launch_bounds__(kPrefixThreads) void scatter_prefix_kernel(const ScatterArgs a, uint32_t* __restrict__ counts,
+                                                              uint32_t* __restrict__ totals,
+                                                              const uint32_t* __restrict__ lvlmax,
+                                                              uint32_t* __restrict__ lvlmax_out)
 {
-    __shared__ uint32_t part[4][64];
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int b = blockIdx.x * 64 + lane;
+    __shared__ uint32_t part[kPrefixGroups][kPrefixBins];
+    __shared__ uint32_t wmax[kPrefixThreads / 64];
+    const int bl = threadIdx.x % kPrefixBins, g = threadIdx.x / kPrefixBins;
+    const int b = blockIdx.x * kPrefixBins + bl;
     const int R = a.rounds;
-    const int q = (R + 3) / 4;
-    const int r0 = min(R, w * q), r1 = min(R, r0 + q);
+    const int per = (R + kPrefixGroups - 1) / kPrefixGroups;
+    const int r0 = min(R, g * per), r1 = min(R, r0 + per);
+    const bool vb = b < a.bins;
     uint32_t s = 0;
-    if (b < a.bins)
+    if (vb)
         for (int r = r0; r < r1; r++) s += counts[(size_t)r * a.bins + b];
-    part[w][lane] = s;
+    part[g][bl] = s;
+    if ((int)blockIdx.x < a.L) {
+        uint32_t m = 0;
+        for (int r = threadIdx.x; r < R; r += kPrefixThreads) m = max(m, lvlmax[(size_t)r * a.L + blockIdx.x]);
+        m = __ockl_wfred_max_u32(m);
+        if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
+    }
     __syncthreads();
+    if ((int)blockIdx.x < a.L && threadIdx.x == 0) {
+        uint32_t m = 0;
+        for (int w = 0; w < kPrefixThreads / 64; w++) m = max(m, wmax[w]);
+        lvlmax_out[blockIdx.x] = m;
+    }
     uint32_t run = 0;
-    for (int k = 0; k < w; k++) run += part[k][lane];
-    if (b < a.bins) {
+    for (int k = 0; k < g; k++) run += part[k][bl];
+    if (vb) {
         for (int r = r0; r < r1; r++) {
             const size_t i = (size_t)r * a.bins + b;
             const uint32_t c = counts[i];
             counts[i] = run;
             run += c;
         }
-        if (w == 3) totals[b] = run;
-    }
-    if (blockIdx.x == 0) {
-        for (int l = threadIdx.x; l < a.L; l += 256) {
-            uint32_t m = 0;
-            for (int r = 0; r < R; r++) m = max(m, lvlmax[(size_t)r * a.L + l]);
-            lvlmax_out[l] = m;
-        }
+        if (g == kPrefixGroups - 1) totals[b] = run;
     }
 }
 
 // Exclusive prefix sum of in[0, n) into out[0, n) (in == out allowed: every
 // thread reads and writes only its own segment); returns the total.  Every
-// thread of the 256-thread block calls it; wsum is 4 words of LDS.
+// thread of the kBinThreads-thread block calls it; wsum is kBinThreads / 64
+// words of LDS.
 __device__ uint32_t block_exclusive_scan(const uint32_t* in, uint32_t* out, int n, uint32_t* wsum)
 {
-    const int per = (n + 255) / 256;
+    constexpr int kWaves = kBinThreads / 64;
+    const int per = (n + kBinThreads - 1) / kBinThreads;
     const int b0 = min(n, (int)threadIdx.x * per), b1 = min(n, b0 + per);
     uint32_t s = 0;
     for (int i = b0; i < b1; i++) s += in[i];
@@ -219,9 +306,11 @@ __device__ uint32_t block_exclusive_scan(const uint32_t* in, uint32_t* out, int 
     }
     if (lane == 63) wsum[w] = x;
     __syncthreads();
-    uint32_t run = x - s;
-    for (int k = 0; k < w; k++) run += wsum[k];
-    const uint32_t total = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+    uint32_t run = x - s, total = 0;
+    for (int k = 0; k < kWaves; k++) {
+        if (k < w) run += wsum[k];
+        total += wsum[k];
+    }
     for (int i = b0; i < b1; i++) {
         const uint32_t v = in[i];
         out[i] = run;
@@ -236,12 +325,12 @@ __device__ uint32_t block_exclusive_scan(const uint32_t* in, uint32_t* out, int 
 __global__ __launch_bounds__(kBinThreads) void scatter_distribute_kernel(
     const ScatterArgs a, const float* __restrict__ pos, const _Float16* __restrict__ denc,
     const uint32_t* __restrict__ prefix, const uint32_t* __restrict__ totals, float4* __restrict__ rec,
-    uint4* __restrict__ chunks, uint32_t* __restrict__ nchunks)
+    uint32_t cap, uint4* __restrict__ chunks, uint32_t* __restrict__ nchunks)
 {
     extern __shared__ uint32_t sh[];
     uint32_t* cur = sh;               // [bins]
     uint32_t* aux = sh + a.bins;      // [bins] (block 0: chunk starts), then [bins] staging slots
-    __shared__ uint32_t wsum[4];
+    __shared__ uint32_t wsum[kBinThreads / 64];
     block_exclusive_scan(totals, cur, a.bins, wsum);
     if (blockIdx.x == 0) {
         uint32_t* kst = aux;
@@ -266,39 +355,65 @@ __global__ __launch_bounds__(kBinThreads) void scatter_distribute_kernel(
     for (int b = threadIdx.x; b < a.bins; b += kBinThreads) cur[b] += prefix[(size_t)blockIdx.x * a.bins + b];
     __syncthreads();
     const int N = sample_count(a);
+    const bool vec = (a.L & 3) == 0;
     for (int k = 0; k < kSamplesPerThread; k++) {
         const int n = blockIdx.x * kRound + k * kBinThreads + threadIdx.x;
         if (n >= N) break;
         const float* pp = pos + (size_t)n * a.pos_stride;
         const float px = pp[0], py = pp[1], pz = pp[2];
-        const h2* grow = reinterpret_cast<const h2*>(denc + (size_t)n * 2 * a.L);
-        for (int l = 0; l < a.L; l++) {
-            const h2 gh = grow[l];
-            const uint32_t gb = __builtin_bit_cast(uint32_t, gh);
-            if ((gb & 0x7fff7fffu) == 0u) continue;
-            const float g0 = (float)gh.x, g1 = (float)gh.y;
-            Pairs p;
-            level_pairs(a, l, px, py, pz, p);
+        const uint32_t* grow = reinterpret_cast<const uint32_t*>(denc + (size_t)n * 2 * a.L);
+        for (int l0 = 0; l0 < a.L; l0 += kLevelGroup) {
+            uint32_t gv[kLevelGroup];
+            load_levels(grow, l0, a.L, vec, gv);
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const uint32_t at = atomicAdd(&cur[p.bin[q]], 1u);
-                rec[at] = make_float4(__uint_as_float(p.key[q]), g0 * p.wyz[q], g1 * p.wyz[q], p.wx);
+            for (int j = 0; j < kLevelGroup; j++) {
+                const int l = l0 + j;
+                if (l >= a.L) break;
+                const uint32_t gb = gv[j];
+                if ((gb & 0x7fff7fffu) == 0u) continue;
+                const h2 gh = __builtin_bit_cast(h2, gb);
+                const float g0 = (float)gh.x, g1 = (float)gh.y;
+                Pairs p;
+                level_pairs(a, l, px, py, pz, p);
+                const bool dense = l < a.dense_start;
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const uint32_t at = dense ? bin_take(cur, p.bin[q]) : atomicAdd(&cur[p.bin[q]], 1u);
+                    if (at < cap)
+                        rec[at] = make_float4(__uint_as_float(p.key[q]), g0 * p.wyz[q], g1 * p.wyz[q], p.wx);
+                }
             }
         }
     }
 }
 
-__device__ __forceinline__ void add_fixed(unsigned long long* acc, float* gl, int i, float c, int e, int* flag)
+// rint(c * 2^e) as an int64 for |c * 2^e| < 2^51: adding 1.5 * 2^52 to the
+// fp64 value leaves the rounded integer (two's complement) in the low
+// mantissa bits.
+__device__ __forceinline__ long long fixed_of(float c, int e)
+{
+    const double y = ldexp((double)c, e) + 6755399441055744.0;
+    return __double_as_longlong(y) - 0x4338000000000000LL;
+}
+
+__device__ __forceinline__ void lds_add(unsigned long long* acc, int i, long long q)
+{
+    __hip_atomic_fetch_add(acc + i, (unsigned long long)q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// A product that may be non-finite: fixed point if finite, else an fp32
+// atomic on the table entry (and the slice is then flushed with atomics).
+__device__ __forceinline__ void add_checked(unsigned long long* acc, float* gl, int i, float c, int e, int* flag)
 {
     if (isfinite(c)) {
-        const long long q = (long long)rintf(ldexpf(c, e));
-        if (q != 0)
-            __hip_atomic_fetch_add(acc + i, (unsigned long long)q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        lds_add(acc, i, fixed_of(c, e));
     } else {
         atomic_add_f32(gl + i, c);
         *flag = 1;
     }
 }
+
+__device__ __forceinline__ bool finite_bits(float x) { return (__float_as_uint(x) & 0x7f800000u) != 0x7f800000u; }
 
 __global__ __launch_bounds__(kAccThreads) void scatter_accumulate_kernel(
     const ScatterArgs a, const float4* __restrict__ rec, const uint4* __restrict__ chunks,
@@ -329,39 +444,72 @@ __global__ __launch_bounds__(kAccThreads) void scatter_accumulate_kernel(
     const int E = ex == 0 ? -15 : min(ex - 15, 15);
     const uint32_t tot = totals[bin];
     const int lg = tot <= 1u ? 0 : 32 - __clz(tot - 1u);
-    const int e = 60 - E - lg;
+    const int e = min(49, 60 - lg) - E;
     float* gl = grads + ((size_t)l * a.T + elem0) * 2;
     for (int i = threadIdx.x; i < 2 * slots; i += kAccThreads) acc[i] = 0ull;
     if (threadIdx.x == 0) s_flag = 0;
     __syncthreads();
-    for (uint32_t i = ch.y + threadIdx.x; i < ch.z; i += kAccThreads) {
-        const float4 r = rec[i];
-        const uint32_t key = __float_as_uint(r.x);
-        const int s0 = (int)(key & 0xffffu), s1 = (int)(key >> 16);
-        const float ux = 1.0f - r.w;
-        add_fixed(acc, gl, 2 * s0, r.y * r.w, e, &s_flag);
-        add_fixed(acc, gl, 2 * s0 + 1, r.z * r.w, e, &s_flag);
-        add_fixed(acc, gl, 2 * s1, r.y * ux, e, &s_flag);
-        add_fixed(acc, gl, 2 * s1 + 1, r.z * ux, e, &s_flag);
+    // kBatch records per thread in flight before their LDS adds
+    constexpr int kBatch = 4;
+    for (uint32_t i0 = ch.y + threadIdx.x; i0 < ch.z; i0 += kBatch * kAccThreads) {
+        float4 r[kBatch];
+#pragma unroll
+        for (int k = 0; k < kBatch; k++) {
+            const uint32_t i = i0 + k * kAccThreads;
+            r[k] = i < ch.z ? rec[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int k = 0; k < kBatch; k++) {
+            if (i0 + k * kAccThreads >= ch.z) break;
+            const uint32_t key = __float_as_uint(r[k].x);
+            const int s0 = (int)(key & 0xffffu), s1 = (int)(key >> 16);
+            const float v0 = r[k].y, v1 = r[k].z, wx = r[k].w, ux = 1.0f - wx;
+            if (finite_bits(v0) & finite_bits(v1) & finite_bits(wx)) {
+                // |v| <= 65504 and wx, ux in [0, 1]: every product is finite
+                lds_add(acc, 2 * s0, fixed_of(v0 * wx, e));
+                lds_add(acc, 2 * s0 + 1, fixed_of(v1 * wx, e));
+                lds_add(acc, 2 * s1, fixed_of(v0 * ux, e));
+                lds_add(acc, 2 * s1 + 1, fixed_of(v1 * ux, e));
+            } else {
+                add_checked(acc, gl, 2 * s0, v0 * wx, e, &s_flag);
+                add_checked(acc, gl, 2 * s0 + 1, v1 * wx, e, &s_flag);
+                add_checked(acc, gl, 2 * s1, v0 * ux, e, &s_flag);
+                add_checked(acc, gl, 2 * s1 + 1, v1 * ux, e, &s_flag);
+            }
+        }
     }
     __syncthreads();
     if (kb == 1) {
         // sole owner of the slice
         const bool atomic = s_flag != 0;
-        for (int s = threadIdx.x; s < slots; s += kAccThreads) {
-            const long long q0 = (long long)acc[2 * s], q1 = (long long)acc[2 * s + 1];
-            const float v0 = ldexpf((float)q0, -e), v1 = ldexpf((float)q1, -e);
-            float2* gp = reinterpret_cast<float2*>(gl) + s;
-            if (atomic) {
-                if (q0) atomic_add_f32(gl + 2 * s, v0);
-                if (q1) atomic_add_f32(gl + 2 * s + 1, v1);
-            } else if (grads_zero) {
-                *gp = make_float2(v0, v1);
-            } else if (q0 | q1) {
-                float2 o = *gp;
-                o.x += v0;
-                o.y += v1;
-                *gp = o;
+        float2* g2 = reinterpret_cast<float2*>(gl);
+        if (atomic || grads_zero) {
+            for (int s = threadIdx.x; s < slots; s += kAccThreads) {
+                const long long q0 = (long long)acc[2 * s], q1 = (long long)acc[2 * s + 1];
+                const float v0 = ldexpf((float)q0, -e), v1 = ldexpf((float)q1, -e);
+                if (atomic) {
+                    if (q0) atomic_add_f32(gl + 2 * s, v0);
+                    if (q1) atomic_add_f32(gl + 2 * s + 1, v1);
+                } else {
+                    g2[s] = make_float2(v0, v1);
+                }
+            }
+        } else {
+            // read-modify-write, kBatch entries per thread in flight
+            for (int s0 = threadIdx.x; s0 < slots; s0 += kBatch * kAccThreads) {
+                float2 o[kBatch];
+#pragma unroll
+                for (int k = 0; k < kBatch; k++) {
+                    const int s = s0 + k * kAccThreads;
+                    o[k] = s < slots ? g2[s] : make_float2(0.f, 0.f);
+                }
+#pragma unroll
+                for (int k = 0; k < kBatch; k++) {
+                    const int s = s0 + k * kAccThreads;
+                    if (s >= slots) break;
+                    const long long q0 = (long long)acc[2 * s], q1 = (long long)acc[2 * s + 1];
+                    if (q0 | q1) g2[s] = make_float2(o[k].x + ldexpf((float)q0, -e), o[k].y + ldexpf((float)q1, -e));
+                }
             }
         }
         return;
@@ -534,11 +682,13 @@ void hash_scatter_binned(ScatterPlan* p, const GridMeta& m, const __half* denc, 
     hipLaunchKernelGGL(scatter_count_kernel, dim3(a.rounds), dim3(kBinThreads), lds_count, stream, a, pos, dh,
                        p->counts, p->lvlmax);
     GRAFT_LAUNCH_CHECK();
-    hipLaunchKernelGGL(scatter_prefix_kernel, dim3((a.bins + 63) / 64), dim3(256), 0, stream, a, p->counts,
-                       p->totals, p->lvlmax, p->lvlmax_final);
+    const int prefix_blocks = std::max((a.bins + kPrefixBins - 1) / kPrefixBins, a.L);
+    hipLaunchKernelGGL(scatter_prefix_kernel, dim3(prefix_blocks), dim3(kPrefixThreads), 0, stream, a, p->counts, p->totals,
+                       p->lvlmax, p->lvlmax_final);
     GRAFT_LAUNCH_CHECK();
+    const uint32_t cap = (uint32_t)(4ull * (unsigned long long)a.L * (unsigned long long)p->maxN);
     hipLaunchKernelGGL(scatter_distribute_kernel, dim3(a.rounds), dim3(kBinThreads), lds_dist, stream, a, pos, dh,
-                       p->counts, p->totals, p->rec, p->chunks, p->nchunks);
+                       p->counts, p->totals, p->rec, cap, p->chunks, p->nchunks);
     GRAFT_LAUNCH_CHECK();
     const unsigned long long recs = 4ull * (unsigned long long)a.L * (unsigned long long)N;
     const int grid = (int)std::min<unsigned long long>(recs / kChunk + a.bins + 1, (unsigned long long)p->max_chunks);
