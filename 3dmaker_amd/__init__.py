@@ -118,6 +118,7 @@ SIGNATURES = {
     "launchNetworkFusionHashTableBackwardKernel": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp]),
     "launchNetworkFusionScatterBackwardKernel": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp]),
     "launchHashTableBackwardKernel": (None, [_vp, _vp, _vp, _i, _i, _i, _f, _i, _i, _vp]),
+    "launchHashTableBackwardKernelNoAlloc": (None, [_vp, _vp, _vp, _i, _i, _i, _f, _i, _i, _vp]),
     "launchAdamHashGridOptim": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _f, _f, _f, _f, _f, _f, _f, _vp]),
     "launchHashEncodeKernel": (None, [_vp, _vp, _vp, _i, _vp, _i, _vp]),
     "tinymlp_last_error": (_i, []),

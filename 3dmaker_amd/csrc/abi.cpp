@@ -13,6 +13,7 @@
 #include "hashgrid.h"
 #include "mlp.h"
 #include "optimizer.h"
+#include "scatter.h"
 
 #include <cstdio>
 #include <string>
@@ -213,6 +214,17 @@ void launchHashTableBackwardKernel(half* d_dx_out, float* d_inputs, float* d_has
         if (featuresLevel != 2) throw std::runtime_error("featuresLevel must be 2");
         const graft::GridMeta m = graft::make_grid_meta(tableSize, numLevels, b, lowestSize);
         graft::hash_scatter(m, d_dx_out, d_inputs, 4, d_hashtable_grads, batchSize, stream);
+    });
+}
+
+void launchHashTableBackwardKernelNoAlloc(half* d_dx_out, float* d_inputs, float* d_hashtable_grads, int batchSize,
+                                          int tableSize, int numLevels, float b, int lowestSize, int featuresLevel,
+                                          hipStream_t stream)
+{
+    guarded("launchHashTableBackwardKernelNoAlloc", [&] {
+        if (featuresLevel != 2) throw std::runtime_error("featuresLevel must be 2");
+        const graft::GridMeta m = graft::make_grid_meta(tableSize, numLevels, b, lowestSize);
+        graft::hash_scatter_noalloc(m, d_dx_out, d_inputs, 4, d_hashtable_grads, batchSize, stream);
     });
 }
 

@@ -604,50 +604,79 @@ size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
 
 }  // namespace
 
-ScatterPlan* scatter_plan_create(const GridMeta& m, int maxN)
+namespace {
+
+// Byte offsets of a plan's buffers.  The int64 staging slices of multi-chunk
+// bins and their counters come first: kernels leave them zero after every
+// call, so a region that starts zero stays zero whatever the configuration.
+struct PlanLayout {
+    size_t o_stg, o_don, o_rec, o_cnt, o_tot, o_lmx, o_lmf, o_chk, o_nch, zero_end, bytes;
+};
+
+bool plan_shape(const GridMeta& m, int maxN, ScatterPlan& p, PlanLayout& lay, int max_multi_cap = 0)
 {
     ScatterArgs a;
-    if (maxN < 1 || !layout(m, a)) return nullptr;
+    if (maxN < 1 || !layout(m, a)) return false;
     const unsigned long long recs = 4ull * (unsigned long long)m.numLevels * (unsigned long long)maxN;
-    if (recs >= (1ull << 31)) return nullptr;
+    if (recs >= (1ull << 31)) return false;
     a.rounds = (maxN + kRound - 1) / kRound;
-    auto* p = new ScatterPlan();
-    p->maxN = maxN;
-    p->meta = m;
-    p->args = a;
-    p->max_chunks = (int)(recs / kChunk) + a.bins + 1;
-    p->max_multi = (int)std::min<unsigned long long>(recs / kChunk + 1, (unsigned long long)a.bins);
+    p.maxN = maxN;
+    p.meta = m;
+    p.args = a;
+    p.max_chunks = (int)(recs / kChunk) + a.bins + 1;
+    p.max_multi = (int)std::min<unsigned long long>(recs / kChunk + 1, (unsigned long long)a.bins);
+    const int multi = std::max(p.max_multi, max_multi_cap);
     size_t off = 0;
-    const size_t o_rec = off; off = align_up(off + recs * sizeof(float4));
-    const size_t o_cnt = off; off = align_up(off + (size_t)a.rounds * a.bins * 4);
-    const size_t o_tot = off; off = align_up(off + (size_t)a.bins * 4);
-    const size_t o_lmx = off; off = align_up(off + (size_t)a.rounds * a.L * 4);
-    const size_t o_lmf = off; off = align_up(off + (size_t)a.L * 4);
-    const size_t o_chk = off; off = align_up(off + (size_t)p->max_chunks * sizeof(uint4));
-    const size_t o_nch = off; off = align_up(off + 4);
-    const size_t o_stg = off; off = align_up(off + (size_t)p->max_multi * 2 * kSlice * 8);
-    const size_t o_don = off; off = align_up(off + (size_t)p->max_multi * 4);
-    const size_t zero_from = o_stg;
-    hipError_t e = hipMalloc(&p->mem, off);
+    lay.o_stg = off; off = align_up(off + (size_t)multi * 2 * kSlice * 8);
+    lay.o_don = off; off = align_up(off + (size_t)multi * 4);
+    lay.zero_end = off;
+    lay.o_rec = off; off = align_up(off + recs * sizeof(float4));
+    lay.o_cnt = off; off = align_up(off + (size_t)a.rounds * a.bins * 4);
+    lay.o_tot = off; off = align_up(off + (size_t)a.bins * 4);
+    lay.o_lmx = off; off = align_up(off + (size_t)a.rounds * a.L * 4);
+    lay.o_lmf = off; off = align_up(off + (size_t)a.L * 4);
+    lay.o_chk = off; off = align_up(off + (size_t)p.max_chunks * sizeof(uint4));
+    lay.o_nch = off; off = align_up(off + 4);
+    lay.bytes = off;
+    return true;
+}
+
+void plan_bind(ScatterPlan& p, char* base, const PlanLayout& lay)
+{
+    p.mem = base;
+    p.rec = reinterpret_cast<float4*>(base + lay.o_rec);
+    p.counts = reinterpret_cast<uint32_t*>(base + lay.o_cnt);
+    p.totals = reinterpret_cast<uint32_t*>(base + lay.o_tot);
+    p.lvlmax = reinterpret_cast<uint32_t*>(base + lay.o_lmx);
+    p.lvlmax_final = reinterpret_cast<uint32_t*>(base + lay.o_lmf);
+    p.chunks = reinterpret_cast<uint4*>(base + lay.o_chk);
+    p.nchunks = reinterpret_cast<uint32_t*>(base + lay.o_nch);
+    p.stage = reinterpret_cast<unsigned long long*>(base + lay.o_stg);
+    p.done = reinterpret_cast<uint32_t*>(base + lay.o_don);
+}
+
+}  // namespace
+
+ScatterPlan* scatter_plan_create(const GridMeta& m, int maxN)
+{
+    auto* p = new ScatterPlan();
+    PlanLayout lay;
+    if (!plan_shape(m, maxN, *p, lay)) {
+        delete p;
+        return nullptr;
+    }
+    void* mem = nullptr;
+    hipError_t e = hipMalloc(&mem, lay.bytes);
     if (e != hipSuccess) {
         delete p;
         GRAFT_HIP_CHECK(e);
     }
-    char* base = static_cast<char*>(p->mem);
-    p->rec = reinterpret_cast<float4*>(base + o_rec);
-    p->counts = reinterpret_cast<uint32_t*>(base + o_cnt);
-    p->totals = reinterpret_cast<uint32_t*>(base + o_tot);
-    p->lvlmax = reinterpret_cast<uint32_t*>(base + o_lmx);
-    p->lvlmax_final = reinterpret_cast<uint32_t*>(base + o_lmf);
-    p->chunks = reinterpret_cast<uint4*>(base + o_chk);
-    p->nchunks = reinterpret_cast<uint32_t*>(base + o_nch);
-    p->stage = reinterpret_cast<unsigned long long*>(base + o_stg);
-    p->done = reinterpret_cast<uint32_t*>(base + o_don);
+    plan_bind(*p, static_cast<char*>(mem), lay);
     // the staging slices and their counters start (and are left) zero
-    e = hipMemset(base + zero_from, 0, off - zero_from);
+    e = hipMemset(mem, 0, lay.zero_end);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
-        (void)hipFree(p->mem);
+        (void)hipFree(mem);
         delete p;
         GRAFT_HIP_CHECK(e);
     }
@@ -732,6 +761,85 @@ void hash_scatter(const GridMeta& m, const __half* denc, const float* pos, int p
         hash_scatter_binned(p, m, denc, pos, pos_stride, grads, N, stream, d_n, /*grads_zero=*/false);
     else
         hash_scatter_atomic(m, denc, pos, pos_stride, grads, N, stream, d_n);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free variant.  The scratch is one file-scope device array per
+// GPU (kNoAllocBytes; each GPU the library runs on keeps it until the process
+// ends).  Its staging region (offset 0, sized for the most multi-chunk bins a
+// sub-batch can have) starts zero and every call leaves it zero; the rest is
+// rewritten by every call.  Batches above one sub-batch run as consecutive
+// sub-batches on the caller's stream.  All calls on one GPU share the array:
+// calls that overlap on one GPU (two streams, or two threads) race.
+// ---------------------------------------------------------------------------
+
+namespace {
+
+constexpr size_t kNoAllocBytes = (size_t)40 << 20;
+constexpr unsigned long long kNoAllocRecords = 1ull << 21;  // corner-pair records per sub-batch
+constexpr size_t kNoAllocCountWords = (size_t)1 << 20;       // rounds x bins per sub-batch
+constexpr int kNoAllocMulti = (int)(kNoAllocRecords / kChunk) + 1;
+constexpr int kMaxDevices = 64;
+
+static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
+
+char* g_noalloc_base[kMaxDevices];
+std::mutex g_noalloc_mu;
+
+__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* p, size_t n)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = 0u;
+}
+
+// The array's device address on the current GPU (looked up, and its staging
+// region cleared on the caller's stream, on the first call on each GPU).
+char* noalloc_base(hipStream_t stream, size_t zero_bytes)
+{
+    int dev = 0;
+    GRAFT_HIP_CHECK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) throw std::runtime_error("hash scatter (no-alloc): device index out of range");
+    std::lock_guard<std::mutex> lk(g_noalloc_mu);
+    if (!g_noalloc_base[dev]) {
+        void* ptr = nullptr;
+        GRAFT_HIP_CHECK(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+        if (!ptr) throw std::runtime_error("hash scatter (no-alloc): no device address for the scratch array");
+        hipLaunchKernelGGL(zero_words_kernel, dim3(256), dim3(256), 0, stream, static_cast<uint32_t*>(ptr),
+                           zero_bytes / 4);
+        GRAFT_LAUNCH_CHECK();
+        g_noalloc_base[dev] = static_cast<char*>(ptr);
+    }
+    return g_noalloc_base[dev];
+}
+
+}  // namespace
+
+size_t scatter_noalloc_bytes() { return kNoAllocBytes; }
+
+void hash_scatter_noalloc(const GridMeta& m, const __half* denc, const float* pos, int pos_stride, float* grads,
+                          int N, hipStream_t stream)
+{
+    if (N <= 0) return;
+    if (pos_stride < 3) throw std::runtime_error("hash scatter: position stride must be >= 3");
+    ScatterArgs a;
+    if (!layout(m, a))
+        throw std::runtime_error("hash scatter (no-alloc): grid beyond the fixed scratch (more than 8192 bins of "
+                                 "4096 entries, or a hashed level's resolution above 4095)");
+    const long long by_rec = (long long)(kNoAllocRecords / (4ull * (unsigned long long)m.numLevels));
+    const long long by_cnt = (long long)(kNoAllocCountWords / (size_t)a.bins) * kRound;
+    const int sub = (int)(std::min(by_rec, by_cnt) / kRound * kRound);
+    if (sub < kRound) throw std::runtime_error("hash scatter (no-alloc): grid beyond the fixed scratch");
+    ScatterPlan plan;
+    PlanLayout lay;
+    if (!plan_shape(m, sub, plan, lay, kNoAllocMulti) || plan.max_multi > kNoAllocMulti || lay.bytes > kNoAllocBytes)
+        throw std::runtime_error("hash scatter (no-alloc): grid beyond the fixed scratch");
+    plan_bind(plan, noalloc_base(stream, lay.zero_end), lay);
+    const int D = 2 * m.numLevels;
+    for (int off = 0; off < N; off += sub) {
+        const int n = std::min(sub, N - off);
+        hash_scatter_binned(&plan, m, denc + (size_t)off * D, pos + (size_t)off * pos_stride, pos_stride, grads, n,
+                            stream, nullptr, /*grads_zero=*/false);
+    }
 }
 
 }  // namespace graft

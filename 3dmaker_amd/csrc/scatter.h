@@ -27,4 +27,12 @@ void hash_scatter_binned(ScatterPlan* p, const GridMeta& m, const __half* denc, 
                          int pos_stride, float* grads, int N, hipStream_t stream, const uint32_t* d_n,
                          bool grads_zero);
 
+// hash_scatter_binned's sum (grads +=) with the scratch in a fixed static
+// device array instead of allocated memory: no allocation on any call.  The
+// batch runs in sub-batches that fit the array; grids beyond its bin capacity
+// throw.  Calls that overlap on one GPU race (they share the array).
+void hash_scatter_noalloc(const GridMeta& m, const __half* denc, const float* pos, int pos_stride, float* grads,
+                          int N, hipStream_t stream);
+size_t scatter_noalloc_bytes();
+
 }  // namespace graft

@@ -140,6 +140,20 @@ void launchHashTableBackwardKernel(GRAFT_HALF* d_dx_out, float* d_inputs, float*
                                    int batchSize, int tableSize, int numLevels, float b,
                                    int lowestSize, int featuresLevel, hipStream_t stream);
 
+/* No counterpart in the reference.  launchHashTableBackwardKernel for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc): the same sum
+ * (d_hashtable_grads += scatter of d_dx_out, within the scatter's tolerance)
+ * with its scratch in a fixed 40 MiB static device array instead of
+ * library-allocated memory; it calls no hipMalloc/hipFree.  Any batch size
+ * (large batches run as consecutive sub-batches on `stream`); grids with more
+ * than 8192 slices of 4096 entries, or a hashed level's resolution above 4095,
+ * are rejected through tinymlp_last_error().  All calls on one GPU share the
+ * array: calls that overlap on one GPU race. */
+void launchHashTableBackwardKernelNoAlloc(GRAFT_HALF* d_dx_out, float* d_inputs, float* d_hashtable_grads,
+                                          int batchSize, int tableSize, int numLevels, float b,
+                                          int lowestSize, int featuresLevel, hipStream_t stream);
+
 /* TinyMLPHashGrid.h:241-255: Adam over the fp32 master table; skips entries
  * whose gradient is exactly 0 and zeroes each gradient it consumes. */
 void launchAdamHashGridOptim(MLPGridOptions* opt, float* master_hash, GRAFT_HALF* fwd_hash,
