@@ -100,6 +100,11 @@ class StepBuffers(C.Structure):
         "result")] + [("trainSteps", C.c_int), ("windowStart", C.c_uint32)]
 
 
+class RefreshBuffers(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("samples", "density_out", "tmp_grid", "active_list", "active_count")] + \
+        [("last_count", C.c_int)]
+
+
 _vp, _i, _f, _u = C.c_void_p, C.c_int, C.c_float, C.c_uint
 _u32 = C.c_uint32
 
@@ -204,6 +209,7 @@ SIGNATURES = {
     "inerf_set_occupancy": (_i, [_vp, _vp]),
     "inerf_get_master_grid": (_i, [_vp, _vp]),
     "inerf_step_buffers": (_i, [_vp, C.POINTER(StepBuffers)]),
+    "inerf_refresh_buffers": (_i, [_vp, C.POINTER(RefreshBuffers)]),
     "inerf_save": (_i, [_vp, C.c_char_p]),
     "inerf_load": (_i, [_vp, C.c_char_p]),
     "inerf_get_options": (_i, [_vp, C.POINTER(NerfOptions)]),
@@ -565,6 +571,11 @@ class Nerf:
     def step_buffers(self) -> StepBuffers:
         b = StepBuffers()
         self._c(self._L.inerf_step_buffers(self.h, C.byref(b)))
+        return b
+
+    def refresh_buffers(self) -> RefreshBuffers:
+        b = RefreshBuffers()
+        self._c(self._L.inerf_refresh_buffers(self.h, C.byref(b)))
         return b
 
 

@@ -98,6 +98,7 @@ struct NerfBuffers {
     int* active_count = nullptr;
     uint32_t* list_scratch = nullptr;
     int occ_capacity = 0;
+    int occ_last_count = 0;   // samples of the last refresh's last chunk
     // inference render / queries (allocated on first use, sized to the hit batch)
     struct Render {
         uint32_t cap = 0;
@@ -762,6 +763,7 @@ void InstantNerf::earlyOccupancyGridUpdate(hipStream_t stream)
         occupancy_density(b, db, dshape, G, stream);
         graft::occ_tmp_max(b.occ_samples, b.occ_density, b.tmp_grid, m_opts.densityBias, G, stream);
     }
+    b.occ_last_count = G;
     finishOccupancyUpdate(stream);
 }
 
@@ -790,6 +792,7 @@ void InstantNerf::lateOccupancyGridUpdate(hipStream_t stream)
         const int cnt = occPer + uniPer;
         occupancy_density(b, db, dshape, cnt, stream);
         graft::occ_tmp_max(b.occ_samples, b.occ_density, b.tmp_grid, m_opts.densityBias, cnt, stream);
+        b.occ_last_count = cnt;
     }
     finishOccupancyUpdate(stream);
 }
@@ -815,6 +818,20 @@ void InstantNerf::setOccupancyBits(const uint8_t* host_bits)
     if (!m_init) throw std::runtime_error("InstantNerf: init() first");
     GRAFT_HIP_CHECK(hipMemcpy(d_occupancyGrid, host_bits, m_occupancyBytes, hipMemcpyHostToDevice));
     m_gridVersion++;
+}
+
+InstantNerf::RefreshBuffers InstantNerf::refreshBuffers() const
+{
+    if (!m_buf) throw std::runtime_error("InstantNerf: init() first");
+    const NerfBuffers& b = *static_cast<const NerfBuffers*>(m_buf);
+    RefreshBuffers r{};
+    r.samples = b.occ_samples;
+    r.density_out = b.occ_density;
+    r.tmp_grid = b.tmp_grid;
+    r.active_list = b.active_list;
+    r.active_count = b.active_count;
+    r.lastCount = b.occ_last_count;
+    return r;
 }
 
 InstantNerf::StepBuffers InstantNerf::stepBuffers() const

@@ -447,6 +447,18 @@ int inerf_get_master_grid(Inerf* h, float* host_cells)
         GRAFT_HIP_CHECK(hipMemcpy(host_cells, h->nerf.masterOccupancyGrid(), n * sizeof(float), hipMemcpyDeviceToHost));
     });
 }
+int inerf_refresh_buffers(Inerf* h, InerfRefreshBuffers* out)
+{
+    return NERF_CALL("inerf_refresh_buffers", {
+        const InstantNerf::RefreshBuffers r = h->nerf.refreshBuffers();
+        out->samples = reinterpret_cast<float*>(r.samples);
+        out->density_out = r.density_out;
+        out->tmp_grid = r.tmp_grid;
+        out->active_list = r.active_list;
+        out->active_count = r.active_count;
+        out->last_count = r.lastCount;
+    });
+}
 int inerf_step_buffers(Inerf* h, InerfStepBuffers* out)
 {
     return NERF_CALL("inerf_step_buffers", {

@@ -177,6 +177,19 @@ public:
     };
     StepBuffers stepBuffers() const;
 
+    // Buffers of the last occupancy refresh (introspection for tests): the
+    // sample buffer holds its last chunk (lastCount samples: the last cascade
+    // of an early refresh, the last cascade chunk of a late one).
+    struct RefreshBuffers {
+        float4* samples;          // [lastCount]: contracted position, cell id (int bits)
+        float* density_out;       // [lastCount x 16]
+        float* tmp_grid;          // [numCascades x cells]
+        int* active_list;         // occupied cells in cell order (late refresh)
+        int* active_count;        // [1]
+        int lastCount;
+    };
+    RefreshBuffers refreshBuffers() const;
+
 private:
     void allocate();
     void freeBuffers();

@@ -59,6 +59,16 @@ typedef struct InerfStepBuffers {
     uint32_t windowStart;   /* first ray of the last step within the last call's rays */
 } InerfStepBuffers;
 
+/* InstantNerf::refreshBuffers (introspection, no reference counterpart). */
+typedef struct InerfRefreshBuffers {
+    float* samples;         /* float4 [last_count]: contracted position, cell id bits */
+    float* density_out;     /* [last_count x 16] */
+    float* tmp_grid;        /* [cascades x cells] */
+    int* active_list;
+    int* active_count;
+    int last_count;
+} InerfRefreshBuffers;
+
 void inerf_default_options(InerfOptions* out);
 size_t inerf_options_size(void);
 Inerf* inerf_create(const InerfOptions* opts);
@@ -97,6 +107,7 @@ int inerf_get_occupancy(Inerf* h, uint8_t* host_bits);
 int inerf_set_occupancy(Inerf* h, const uint8_t* host_bits);
 int inerf_get_master_grid(Inerf* h, float* host_cells);
 int inerf_step_buffers(Inerf* h, InerfStepBuffers* out);
+int inerf_refresh_buffers(Inerf* h, InerfRefreshBuffers* out);
 /* InstantNerf::save / load (InstantNerf.h:333-334): the reference's .inerf
  * format ("INERF1", raw NerfOptions, hash table, density and colour weights,
  * master occupancy grid, bitfield).  load re-initialises the model with the

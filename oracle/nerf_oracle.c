@@ -566,6 +566,73 @@ void orc_build_mipmaps(uint8_t* bits, const uint32_t* res, int L, int C)
     }
 }
 
+/* ---- occupancy refresh sampling (otherKernels.cu:591-675, 852-888) ---- */
+void orc_philox4x32_10(uint32_t c[4], uint32_t k0, uint32_t k1)
+{
+    for (int r = 0; r < 10; r++) {
+        const uint64_t p0 = (uint64_t)0xD2511F53u * c[0];
+        const uint64_t p1 = (uint64_t)0xCD9E8D57u * c[2];
+        const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c[1] ^ k0;
+        const uint32_t n2 = (uint32_t)(p0 >> 32) ^ c[3] ^ k1;
+        c[1] = (uint32_t)p1;
+        c[3] = (uint32_t)p0;
+        c[0] = n0;
+        c[2] = n2;
+        k0 += 0x9E3779B9u;
+        k1 += 0xBB67AE85u;
+    }
+}
+
+static float unit_of(uint32_t u) { return (float)(u >> 8) * 5.9604645e-8f + 2.9802322e-8f; }
+
+void orc_occ_sample(float* out4, int N, int mode, int total_cells, int cell_offset, const int* list, int list_count,
+                    uint64_t seed, const uint32_t* res3, const float* mn, const float* mx)
+{
+    const int G = (int)(res3[0] * res3[1] * res3[2]);
+    for (int idx = 0; idx < N; idx++) {
+        uint32_t c[4] = {(uint32_t)idx, 0u, (uint32_t)seed, (uint32_t)(seed >> 32)};
+        orc_philox4x32_10(c, 0x3DA3ACB5u, 0xA79C5F42u);
+        const float r[3] = {unit_of(c[0]), unit_of(c[1]), unit_of(c[2])};
+        const float rw = unit_of(c[3]);
+        int cell;
+        if (mode == 0) {
+            if (list_count == 0) continue;
+            int k = (int)(rw * (float)list_count);
+            cell = list[k < list_count - 1 ? k : list_count - 1];
+        } else if (mode == 1) {
+            cell = cell_offset + idx;
+        } else {
+            int k = (int)(rw * (float)total_cells);
+            cell = cell_offset + (k < total_cells - 1 ? k : total_cells - 1);
+        }
+        const int cas = cell / G, local = cell % G;
+        const int g[3] = {local % (int)res3[0], (local / (int)res3[0]) % (int)res3[1],
+                          local / (int)(res3[0] * res3[1])};
+        const float cs = ldexpf(1.0f, cas);
+        float p[3], q[3];
+        for (int k = 0; k < 3; k++) {
+            const float lo = mn[k] * cs, hi = mx[k] * cs;
+            const float size = (hi - lo) / (float)res3[k];
+            p[k] = lo + ((float)g[k] + r[k]) * size;
+        }
+        orc_contract_pos(p, mn, mx, q);
+        out4[4 * (size_t)idx] = q[0];
+        out4[4 * (size_t)idx + 1] = q[1];
+        out4[4 * (size_t)idx + 2] = q[2];
+        memcpy(&out4[4 * (size_t)idx + 3], &cell, 4);
+    }
+}
+
+void orc_occ_tmp_max(const float* samples4, const float* density_out, float* tmp, float bias, int N)
+{
+    for (int idx = 0; idx < N; idx++) {
+        int cell;
+        memcpy(&cell, &samples4[4 * (size_t)idx + 3], 4);
+        const float sigma = orc_expf(fminf(density_out[16 * (size_t)idx] - bias, 8.0f));
+        if (sigma > tmp[cell]) tmp[cell] = sigma;
+    }
+}
+
 /* ---- training ray feed (DataLoader.cu:542-661) ---- */
 
 uint32_t orc_pcg_hash(uint32_t input)

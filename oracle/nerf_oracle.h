@@ -114,6 +114,26 @@ void orc_update_occupancy_bits(uint8_t* bits, const float* master, float sum, in
 /* buildMipmaps + bitfield_max_pool (InstantNerf.cu:1177-1204, otherKernels.cu:752-807). */
 void orc_build_mipmaps(uint8_t* bits, const uint32_t* res3, int mip_levels, int num_cascades);
 
+/* Philox4x32-10 (Salmon, Moraes, Dror, Shaw, SC'11, "Parallel random numbers:
+ * as easy as 1, 2, 3"): the occupancy refresh's generator in this build (the
+ * reference draws from cuRAND's Philox state, whose counter/key use is not
+ * reproducible here).  c[4] is the counter in, the block out. */
+void orc_philox4x32_10(uint32_t c[4], uint32_t k0, uint32_t k1);
+
+/* sampleAABB (otherKernels.cu:591-648; modes 1 every cell of
+ * [cell_offset, cell_offset + N), 2 a random cell of [cell_offset,
+ * cell_offset + total_cells)) and sampleOccupiedAABB (:852-888; mode 0, a
+ * random entry of list[0, list_count)) with this build's draws: sample idx
+ * takes the Philox4x32-10 block of counter (idx, 0, seed lo, seed hi) under key
+ * (0x3DA3ACB5, 0xA79C5F42), each output u as (u >> 8) 2^-24 + 2^-25; out4
+ * [N][4] = contracted position, cell id (int bits). */
+void orc_occ_sample(float* out4, int N, int mode, int total_cells, int cell_offset, const int* list, int list_count,
+                    uint64_t seed, const uint32_t* res3, const float* mn, const float* mx);
+
+/* updateTmpGrid (otherKernels.cu:650-675): tmp[cell] = max(tmp[cell],
+ * e^min(logit - bias, 8)) with logit = density_out[16 idx] (orc_expf). */
+void orc_occ_tmp_max(const float* samples4, const float* density_out, float* tmp, float bias, int N);
+
 /* pcg_hash (DataLoader.cu:542-546). */
 uint32_t orc_pcg_hash(uint32_t input);
 

@@ -77,6 +77,9 @@ def lib():
                                       _u16p, _f32p, f, f, C.c_uint32]),
             "orc_density_grad": (None, [C.c_uint32, _f32p, _u16p, _u16p]),
             "orc_update_master_grid": (None, [_f32p, _f32p, f, C.c_uint32]),
+            "orc_philox4x32_10": (None, [_u32p, C.c_uint32, C.c_uint32]),
+            "orc_occ_sample": (None, [_f32p, i, i, i, i, C.c_void_p, i, C.c_uint64, _u32p, _f32p, _f32p]),
+            "orc_occ_tmp_max": (None, [_f32p, _f32p, _f32p, f, i]),
             "orc_update_occupancy_bits": (None, [_u8p, _f32p, f, i, i, i, f, f]),
             "orc_build_mipmaps": (None, [_u8p, _u32p, i, i]),
             "orc_pcg_hash": (C.c_uint32, [C.c_uint32]),
@@ -381,6 +384,61 @@ def update_occupancy_bits(bits, master, total_sum, G, S, min_optical, base_voxel
 def build_mipmaps(bits, res, L, cascades):
     lib().orc_build_mipmaps(bits, np.ascontiguousarray(res, np.uint32), int(L), int(cascades))
     return bits
+
+
+def philox4x32_10(ctr, key):
+    c = np.ascontiguousarray(ctr, np.uint32).copy()
+    lib().orc_philox4x32_10(c, int(key[0]) & 0xffffffff, int(key[1]) & 0xffffffff)
+    return c
+
+
+# occ_sample modes (otherKernels.cu:591-648, 852-888)
+OCC_FROM_LIST, OCC_EVERY_CELL, OCC_RANDOM_CELL = 0, 1, 2
+
+
+def occ_sample(N, mode, total_cells, cell_offset, seed, res, aabb_min, aabb_max, cell_list=None):
+    """-> (positions float32 [N][3] contracted, cells int32 [N]); rows of an empty list stay zero."""
+    out = np.zeros((N, 4), np.float32)
+    lst = None if cell_list is None else np.ascontiguousarray(cell_list, np.int32)
+    lib().orc_occ_sample(out, int(N), int(mode), int(total_cells), int(cell_offset),
+                         None if lst is None else lst.ctypes.data, 0 if lst is None else int(lst.size),
+                         int(seed) & 0xffffffffffffffff, np.ascontiguousarray(res, np.uint32), _f3(aabb_min),
+                         _f3(aabb_max))
+    return out, out[:, 3].copy().view(np.int32)
+
+
+def occ_tmp_max(samples4, density_out, tmp, bias):
+    lib().orc_occ_tmp_max(np.ascontiguousarray(samples4, np.float32), np.ascontiguousarray(density_out, np.float32),
+                          tmp, float(bias), int(samples4.shape[0]))
+    return tmp
+
+
+def active_cells(bits, G, S, cascades):
+    """Cells (cascade * G + local) whose level-0 bit is set, in cell order (extractActiveCells,
+    otherKernels.cu:809-834; the reference appends with an atomic counter, this build in order)."""
+    b = np.unpackbits(np.ascontiguousarray(bits, np.uint8), bitorder="little")
+    cells = []
+    for c in range(cascades):
+        lvl0 = b[c * S: c * S + G]
+        cells.append(np.nonzero(lvl0)[0].astype(np.int64) + c * G)
+    return np.concatenate(cells).astype(np.int32)
+
+
+def refresh_schedule(train_steps, cascades, G):
+    """The occupancy refresh's sampling calls (InstantNerf.cu:1009-1171): a list of chunks, each a list of
+    (mode, N, total_cells, cell_offset, seed); early (< 256 steps) = every cell of each cascade, late = half
+    the cells' worth per refresh split over `cascades` chunks, half from the occupied list, half uniform."""
+    if train_steps < 256:
+        return [[(OCC_EVERY_CELL, G, G, c * G, train_steps + c)] for c in range(cascades)]
+    N = cascades * G
+    per = (N // 2) // cascades
+    occ = per // 2
+    uni = per - occ
+    out = []
+    for ch in range(cascades):
+        seed = train_steps * (2 * cascades) + 2 * ch
+        out.append([(OCC_FROM_LIST, occ, 0, 0, seed), (OCC_RANDOM_CELL, uni, N, 0, seed + 1)])
+    return out
 
 
 def pcg_hash(x):

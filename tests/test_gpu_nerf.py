@@ -672,3 +672,109 @@ def test_instant_nerf_next_rays_prefetch(dev):
     assert all(len(h) >= 1 for h in (ha, ha2, ha3, ha4, hb, hb2, hb3, hb4))
     A.close()
     Bn.close()
+
+
+# --------------------------------------------------------------------------- occupancy refresh (f1)
+
+
+def _refresh_oracle_chunks(nerf, opts, steps, bits, G, S, Cc, res, table, dW, dB):
+    """The refresh's sampling calls on the oracle: per chunk (samples [n, 4], oracle density logits [n, 16])."""
+    T_ = opts.hashTableSize
+    active = orc.active_cells(bits, G, S, Cc)
+    chunks = []
+    for calls in orc.refresh_schedule(steps, Cc, G):
+        parts = []
+        for mode, n, total, off, seed in calls:
+            pos, cells = orc.occ_sample(n, mode, total, off, seed, [res] * 3, MN, MX,
+                                        cell_list=active if mode == orc.OCC_FROM_LIST else None)
+            parts.append(np.concatenate([pos[:, :3], cells.view(np.float32)[:, None]], 1))
+        smp = np.ascontiguousarray(np.concatenate(parts), np.float32)
+        enc = orc.hash_encode(smp, table.astype(np.float16), T_, opts.numLevels, opts.baseResolution,
+                              opts.growthFactor)
+        y, _ = orc.mlp_forward(enc, dW.astype(np.float16), dB, 32, 64, 16, 2, save_acts=False)
+        chunks.append((smp, y))
+    return chunks
+
+
+@pytest.mark.parametrize("late", [False, True])
+def test_occupancy_refresh_matches_oracle(dev, late):
+    """updateOccupancy: sample positions and cells bit-exact on this build's Philox draws, density within the
+    MLP tolerance, tmp grid bit-exact on the GPU's own densities, EMA master grid bit-exact, bits."""
+    P = pkg()
+    opts = small_options(P, batch=1 << 14)
+    nerf = P.Nerf(opts)
+    res, Cc, L = 32, 2, 4
+    G, S = res ** 3, orc.pyramid_cells([res] * 3, L)
+    if late:   # 256 one-step calls: the next refresh samples occupied cells (InstantNerf.cu:1009-1106)
+        rng = np.random.default_rng(21)
+        o, d = scenes.rays_c4(1000, n_cams=20, seed=22)
+        d_o, d_d = T(o, dev), T(d, dev)
+        d_gt = T(rng.random((1000, 3)).astype(np.float32), dev)
+        done = 0
+        while done < 256:
+            n, _ = nerf.train(d_o, d_d, d_gt, 1000)
+            done += n
+        torch.cuda.synchronize()
+        # a sparse grid, so that the occupied-cell list is a proper subset
+        lv = [rng.random((res,) * 3) < (0.2 if c == 0 else 0.05) for c in range(Cc)]
+        nerf.set_occupancy(scenes.pack_grid(lv, L))
+    steps = nerf.step_buffers().trainSteps
+    print(f"[refresh] late={late} trainSteps={steps}", flush=True)
+    assert (steps >= 256) == late
+    table = np.zeros(16 * (1 << 14) * 2, np.float32)
+    nerf.density.save_hashgrid(table)
+    dW = np.zeros(64 * 32 + 16 * 64, np.float32)
+    dB = np.zeros(64 + 16, np.float32)
+    nerf.density.save_weights(dW, dB)
+    bits = nerf.occupancy()
+    master0 = nerf.master_grid()
+    nerf.update_occupancy()
+    torch.cuda.synchronize()
+    rb = nerf.refresh_buffers()
+    n_last = rb.last_count
+    g_smp = d2h(rb.samples, (n_last, 4), np.float32)
+    g_den = d2h(rb.density_out, (n_last, 16), np.float32)
+    g_tmp = d2h(rb.tmp_grid, (Cc * G,), np.float32)
+    if late:   # the occupied-cell list, in cell order
+        want_list = orc.active_cells(bits, G, S, Cc)
+        n_act = int(d2h(rb.active_count, (1,), np.int32)[0])
+        assert 0 < n_act == want_list.size < Cc * G
+        np.testing.assert_array_equal(d2h(rb.active_list, (n_act,), np.int32), want_list)
+    master1 = nerf.master_grid()
+    bits1 = nerf.occupancy()
+
+    chunks = _refresh_oracle_chunks(nerf, opts, steps, bits, G, S, Cc, res, table, dW, dB)
+    smp, y = chunks[-1]
+    assert smp.shape[0] == n_last
+    np.testing.assert_array_equal(g_smp.view(np.uint32), smp.view(np.uint32))  # positions and cell ids
+    assert_close(g_den, y, what="refresh density logits")
+    # tmp grid: the earlier chunks from the oracle's densities, the last one from the GPU's own
+    tmp = np.zeros(Cc * G, np.float32)
+    for s_, y_ in chunks[:-1]:
+        orc.occ_tmp_max(s_, y_, tmp, opts.densityBias)
+    last_only = np.zeros(Cc * G, bool)
+    last_only[smp[:, 3].view(np.int32)] = True
+    for s_, _ in chunks[:-1]:
+        last_only[s_[:, 3].view(np.int32)] = False
+    orc.occ_tmp_max(smp, g_den, tmp, opts.densityBias)
+    bits_eq(g_tmp[last_only], tmp[last_only])
+    early = ~last_only
+    np.testing.assert_array_equal(g_tmp[early] > 0, tmp[early] > 0)   # sampled cells (sigma > 0)
+    hit = early & (tmp > 0)
+    # sigma = e^logit: the density head's tolerance, in logit space
+    assert_close(np.log(g_tmp[hit]), np.log(tmp[hit]), what="tmp grid of the earlier chunks (log sigma)")
+    # EMA-max on the GPU's tmp grid: bit-exact
+    bits_eq(master1, orc.update_master_grid(g_tmp, master0.copy(), opts.decayValue))
+    # bits from the master grid (threshold min(0.01 / voxel / 2^c, mean)); cells at the threshold excepted
+    want = bits1.copy()
+    mean = np.float32(master1.astype(np.float64).sum())
+    orc.update_occupancy_bits(want, master1, mean, G, S, opts.minDensityThreshold, 3.0 / res)
+    orc.build_mipmaps(want, [res] * 3, L, Cc)
+    thr = np.minimum((opts.minDensityThreshold / (3.0 / res)) / 2.0 ** (np.arange(Cc * G) // G),
+                     master1.astype(np.float64).mean())
+    near = np.abs(master1 - thr) <= 1e-5 * np.abs(thr)
+    got_l0 = np.concatenate([np.unpackbits(bits1, bitorder="little")[c * S: c * S + G] for c in range(Cc)])
+    want_l0 = np.concatenate([np.unpackbits(want, bitorder="little")[c * S: c * S + G] for c in range(Cc)])
+    np.testing.assert_array_equal(got_l0[~near], want_l0[~near])
+    assert got_l0.any()
+    nerf.close()

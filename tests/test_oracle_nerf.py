@@ -574,3 +574,108 @@ def test_fetch_ray_chunk_depth_prior_rays():
         pxi, pyi = min(max(int(px + 0.5), 0), w - 1), min(max(int(py + 0.5), 0), h - 1)
         a = imgs[f, pyi, pxi].astype(np.float64) / 255
         np.testing.assert_allclose(r["rgb"][sel][0], a[:3] * a[3] + (1 - a[3]), atol=1e-6)
+
+
+# --------------------------------------------------------------------------- occupancy refresh sampling
+
+# Random123 known-answer vectors for philox4x32_10 (Salmon et al., SC'11; kat_vectors of the distribution)
+PHILOX_KATS = [
+    ((0, 0, 0, 0), (0, 0), (0x6627e8d5, 0xe169c58d, 0xbc57ac4c, 0x9b00dbd8)),
+    ((0xffffffff,) * 4, (0xffffffff, 0xffffffff), (0x408f276d, 0x41c83b0e, 0xa20bc7c6, 0x6d5451fd)),
+    ((0x243f6a88, 0x85a308d3, 0x13198a2e, 0x03707344), (0xa4093822, 0x299f31d0),
+     (0xd16cfe09, 0x94fdcceb, 0x5001e420, 0x24126ea1)),
+]
+
+
+@pytest.mark.parametrize("ctr,key,want", PHILOX_KATS)
+def test_oracle_philox_known_answers(ctr, key, want):
+    assert tuple(int(x) for x in orc.philox4x32_10(ctr, key)) == want
+
+
+def test_oracle_philox_matches_the_library_host_generator():
+    import ctypes as C
+    P = importlib.import_module("3dmaker_amd")
+    rng = np.random.default_rng(3)
+    for _ in range(200):
+        ctr = rng.integers(0, 1 << 32, 4, dtype=np.uint64).astype(np.uint32)
+        key = rng.integers(0, 1 << 32, 2, dtype=np.uint64).astype(np.uint32)
+        c = (C.c_uint32 * 4)(*[int(x) for x in ctr])
+        P.lib().inerf_philox4x32_10(c, int(key[0]), int(key[1]))
+        assert tuple(c) == tuple(int(x) for x in orc.philox4x32_10(ctr, key))
+
+
+def _uncontract(q, mn, mx):
+    """World position of a contracted coordinate (the inverse of contract_pos, processRays.cu:21-46)."""
+    c = 4.0 * q.astype(np.float64) - 2.0
+    n = np.where(np.abs(c) <= 1.0, c, np.sign(c) / (2.0 - np.abs(c)))
+    return mn + (n + 1.0) * 0.5 * (mx - mn)
+
+
+def _draws(N, seed):
+    """The four unit draws of each sample: Philox block of (idx, 0, seed lo, seed hi) under the sampler's key,
+    each output u as (u >> 8) * 2^-24 + 2^-25 in fp32 (the sum rounds to even above 0.5)."""
+    out = np.zeros((N, 4), np.float32)
+    for i in range(N):
+        u = orc.philox4x32_10((i, 0, seed & 0xffffffff, seed >> 32), (0x3DA3ACB5, 0xA79C5F42))
+        out[i] = (u >> 8).astype(np.float32) * np.float32(2.0 ** -24) + np.float32(2.0 ** -25)
+    return out
+
+
+def test_occ_sample_every_cell_mode_places_each_sample_in_its_cell():
+    res, mn, mx, C_ = np.array([8, 6, 4]), np.float32([-1.5] * 3), np.float32([1.5] * 3), 3
+    G = int(np.prod(res))
+    for c in range(C_):
+        seed = 1000 + c
+        pos, cells = orc.occ_sample(G, orc.OCC_EVERY_CELL, G, c * G, seed, res, mn, mx)
+        np.testing.assert_array_equal(cells, np.arange(G) + c * G)
+        local = cells - c * G
+        g = np.stack([local % res[0], (local // res[0]) % res[1], local // (res[0] * res[1])], 1)
+        lo, hi = mn * 2.0 ** c, mx * 2.0 ** c
+        size = (hi - lo) / res
+        p = np.stack([_uncontract(pos[:, k], mn[k], mx[k]) for k in range(3)], 1)
+        jit = (p - lo) / size - g                                 # position within its cell, in cells
+        assert (jit > -1e-3).all() and (jit < 1 + 1e-3).all()
+        np.testing.assert_allclose(jit, _draws(G, seed)[:, :3], atol=2e-3 if c else 1e-5)
+
+
+def test_occ_sample_random_cell_and_list_modes():
+    res, mn, mx = np.array([8, 8, 8]), np.float32([-1.0] * 3), np.float32([1.0] * 3)
+    G, N = 512, 20000
+    _, cells = orc.occ_sample(N, orc.OCC_RANDOM_CELL, 2 * G, 0, 77, res, mn, mx)
+    w = np.floor(_draws(N, 77)[:, 3] * np.float32(2 * G)).astype(np.int64)
+    np.testing.assert_array_equal(cells, np.minimum(w, 2 * G - 1))   # cell = floor(w * total), clamped
+    counts = np.bincount(cells, minlength=2 * G)
+    assert counts.min() > 0 and abs(counts.mean() - N / (2 * G)) < 1e-9
+    lst = np.array([5, 17, 600, 1023], np.int32)
+    _, cl = orc.occ_sample(4000, orc.OCC_FROM_LIST, 0, 0, 78, res, mn, mx, cell_list=lst)
+    assert set(np.unique(cl)) == set(lst.tolist())
+    empty, ce = orc.occ_sample(10, orc.OCC_FROM_LIST, 0, 0, 79, res, mn, mx, cell_list=np.zeros(0, np.int32))
+    assert not empty.any() and not ce.any()
+
+
+def test_occ_tmp_max_is_the_per_cell_max_of_sigma():
+    rng = np.random.default_rng(5)
+    N, cells_n = 5000, 300
+    samples = np.zeros((N, 4), np.float32)
+    cells = rng.integers(0, cells_n, N).astype(np.int32)
+    samples[:, 3] = cells.view(np.float32)
+    dout = rng.normal(0, 4, (N, 16)).astype(np.float32)
+    tmp = orc.occ_tmp_max(samples, dout, np.zeros(cells_n, np.float32), 0.5)
+    want = np.zeros(cells_n)
+    sig = np.exp(np.minimum(dout[:, 0].astype(np.float64) - 0.5, 8.0))
+    np.maximum.at(want, cells, sig)
+    np.testing.assert_allclose(tmp, want, rtol=3e-7)
+
+
+def test_refresh_schedule_sample_budget():
+    G, C_ = 4096, 5
+    early = orc.refresh_schedule(100, C_, G)
+    assert [len(ch) for ch in early] == [1] * C_
+    assert [(m, n, off, seed) for ((m, n, _, off, seed),) in early] == \
+        [(orc.OCC_EVERY_CELL, G, c * G, 100 + c) for c in range(C_)]
+    late = orc.refresh_schedule(300, C_, G)
+    assert len(late) == C_
+    per = (C_ * G // 2) // C_
+    for ch, ((m0, n0, _, _, s0), (m1, n1, t1, _, s1)) in enumerate(late):
+        assert (m0, m1) == (orc.OCC_FROM_LIST, orc.OCC_RANDOM_CELL) and n0 + n1 == per and n0 == per // 2
+        assert t1 == C_ * G and s0 == 300 * 2 * C_ + 2 * ch and s1 == s0 + 1
