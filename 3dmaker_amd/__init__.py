@@ -44,13 +44,15 @@ class GridBuffers(C.Structure):
     _fields_ = [(n, C.c_void_p) for n in (
         "master_hashtable", "fwd_hashtable", "hashtable_grads", "hash_m", "hash_v",
         "master_weights", "master_biases", "fwd_weights", "w_grad", "b_grad", "activations",
-        "dx_out", "dloss", "padded_inputs", "padded_outputs")] + [("hw", MLPGridOptions), ("step", C.c_int)]
+        "dx_out", "dloss", "padded_inputs", "padded_outputs")] + [("hw", MLPGridOptions), ("step", C.c_int)] + \
+        [(n, C.c_void_p) for n in ("w_m", "w_v", "b_m", "b_v")]
 
 
 class NetBuffers(C.Structure):
     _fields_ = [(n, C.c_void_p) for n in (
         "master_weights", "master_biases", "fwd_weights", "w_grad", "b_grad", "activations",
-        "dloss", "padded_outputs")] + [("hw", MLPOption), ("step", C.c_int)]
+        "dloss", "padded_outputs")] + [("hw", MLPOption), ("step", C.c_int)] + \
+        [(n, C.c_void_p) for n in ("w_m", "w_v", "b_m", "b_v")]
 
 
 class Float3(C.Structure):

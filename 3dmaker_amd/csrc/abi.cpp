@@ -330,6 +330,10 @@ int tmlp_grid_buffers(TmlpGrid* h, TmlpGridBuffers* out)
         out->padded_outputs = b.padded_outputs;
         out->hw = b.hw;
         out->step = b.step;
+        out->w_m = b.w_m;
+        out->w_v = b.w_v;
+        out->b_m = b.b_m;
+        out->b_v = b.b_v;
     });
 }
 
@@ -399,6 +403,10 @@ int tmlp_net_buffers(TmlpNet* h, TmlpNetBuffers* out)
         out->padded_outputs = b.padded_outputs;
         out->hw = b.hw;
         out->step = b.step;
+        out->w_m = b.w_m;
+        out->w_v = b.w_v;
+        out->b_m = b.b_m;
+        out->b_v = b.b_v;
     });
 }
 

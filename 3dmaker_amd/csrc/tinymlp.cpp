@@ -490,6 +490,10 @@ TinyMLP::Buffers TinyMLP::buffers() const
     b.padded_outputs = d_padded_outputs_float;
     b.hw = hw_opt;
     b.step = current_step;
+    b.w_m = d_w_m;
+    b.w_v = d_w_v;
+    b.b_m = d_b_m;
+    b.b_v = d_b_v;
     return b;
 }
 
@@ -880,5 +884,9 @@ TinyMLPHashGrid::Buffers TinyMLPHashGrid::buffers() const
     b.step = current_step;
     b.scatter_plan = m_scatter;
     b.scatter_plan = m_scatter;
+    b.w_m = d_w_m;
+    b.w_v = d_w_v;
+    b.b_m = d_b_m;
+    b.b_v = d_b_v;
     return b;
 }

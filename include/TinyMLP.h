@@ -67,6 +67,10 @@ public:
         float* padded_outputs;    // fp32 [maxBatch x hw out]
         MLPOption hw;
         int step;
+        float** w_m;              // Adam moments (device arrays of per-layer pointers)
+        float** w_v;
+        float** b_m;
+        float** b_v;
     };
     Buffers buffers() const;
 

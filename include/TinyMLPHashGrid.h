@@ -90,6 +90,10 @@ public:
         MLPGridOptions hw;
         int step;
         void* scatter_plan;       // binned-scatter scratch (opaque); null: per-corner atomic scatter
+        float** w_m;              // MLP Adam moments (device arrays of per-layer pointers)
+        float** w_v;
+        float** b_m;
+        float** b_v;
     };
     Buffers buffers() const;
 

@@ -37,6 +37,10 @@ typedef struct TmlpGridBuffers {
     float* padded_outputs;
     MLPGridOptions hw;
     int step;
+    float** w_m;            /* MLP Adam moments, per layer */
+    float** w_v;
+    float** b_m;
+    float** b_v;
 } TmlpGridBuffers;
 
 typedef struct TmlpNetBuffers {
@@ -50,6 +54,10 @@ typedef struct TmlpNetBuffers {
     float* padded_outputs;
     MLPOption hw;
     int step;
+    float** w_m;            /* Adam moments, per layer */
+    float** w_v;
+    float** b_m;
+    float** b_v;
 } TmlpNetBuffers;
 
 /* ---- TinyMLPHashGrid ---- */
