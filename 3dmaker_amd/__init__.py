@@ -129,8 +129,6 @@ SIGNATURES = {
     "launchAdamHashGridOptim": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _f, _f, _f, _f, _f, _f, _f, _vp]),
     "launchHashEncodeKernel": (None, [_vp, _vp, _vp, _i, _vp, _i, _vp]),
     "tinymlp_last_error": (_i, []),
-    # include/graft_diag.h (bench support)
-    "graft_diag_atomic_line_rate": (_i, [_vp, C.c_size_t, _i, C.POINTER(C.c_double), _vp]),
     "tinymlp_last_error_message": (C.c_char_p, []),
     # include/tinymlp_capi.h (flat handle API)
     "tmlp_grid_create": (_vp, [C.POINTER(MLPGridOptions), _i, _i, _u, _i]),
@@ -195,6 +193,8 @@ SIGNATURES = {
     "inerf_set_learning_rate": (_i, [_vp, _f]),
     "inerf_set_next_rays": (_i, [_vp, _vp, _vp, _u32]),
     "inerf_set_bg_color": (_i, [_vp, _f, _f, _f]),
+    "inerf_set_step_limit": (_i, [_vp, _i]),
+    "inerf_last_rays_trained": (_u32, [_vp]),
     "inerf_set_profiling": (_i, [_vp, _i]),
     "inerf_print_stats": (_i, [_vp]),
     "inerf_stats": (_i, [_vp, C.c_char_p, _i]),
@@ -493,6 +493,13 @@ class Nerf:
         """setNextRays: the rays of the next train() call, already written; their first hit batch is
         compacted beside this call's last step."""
         self._c(self._L.inerf_set_next_rays(self.h, ptr(rays_o), ptr(rays_d), int(num_rays)))
+
+    def set_step_limit(self, n):
+        """At most n optimizer steps per train() call (0: no limit)."""
+        self._c(self._L.inerf_set_step_limit(self.h, int(n)))
+
+    def last_rays_trained(self):
+        return int(self._L.inerf_last_rays_trained(self.h))
 
     def set_bg_color(self, r, g, b):
         self._c(self._L.inerf_set_bg_color(self.h, float(r), float(g), float(b)))

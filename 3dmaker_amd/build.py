@@ -68,6 +68,24 @@ def build(verbose: bool = False) -> str:
     return LIB
 
 
+PROBES_SRC = os.path.join(ROOT, "bench_probes.hip")
+PROBES_LIB = os.path.join(ROOT, "bench_probes.so")
+
+
+def build_probes(verbose: bool = False) -> str:
+    """bench.py's device-ceiling probes, a shared library of their own (not part of the product library)."""
+    tmp = PROBES_LIB + ".tmp"
+    cmd = [HIPCC, *COMMON, "-shared", "-o", tmp, PROBES_SRC]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {PROBES_SRC}:\n{r.stderr}")
+    os.replace(tmp, PROBES_LIB)
+    if verbose:
+        print(f"built {PROBES_LIB}")
+    return PROBES_LIB
+
+
 if __name__ == "__main__":
     build(verbose=True)
+    build_probes(verbose=True)
     sys.exit(0)

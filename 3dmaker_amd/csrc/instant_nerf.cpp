@@ -652,11 +652,31 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         // cursor; the next batch's compaction then runs beside this step.
         GRAFT_HIP_CHECK(hipEventSynchronize(S.ev_result));
         const uint32_t active = S.h_result[0], hits = S.h_result[1];
-        if (active == 0) throw std::runtime_error("InstantNerf: no ray fits the batch");
+        if (active == 0) {
+            // unreachable with batchSize >= one ray's sample cap; leave no work
+            // of this call on the side streams and no timers behind
+            GRAFT_HIP_CHECK(hipEventRecord(b.ev_done, b.side));
+            GRAFT_HIP_CHECK(hipStreamWaitEvent(stream, b.ev_done, 0));
+            GRAFT_HIP_CHECK(hipEventRecord(b.ev_done_occ, b.occ));
+            GRAFT_HIP_CHECK(hipStreamWaitEvent(stream, b.ev_done_occ, 0));
+            GRAFT_HIP_CHECK(hipStreamSynchronize(stream));
+            for (auto& t : b.pending) {
+                (void)hipEventDestroy(t.a);
+                (void)hipEventDestroy(t.b);
+            }
+            b.pending.clear();
+            b.pre.valid = false;
+            throw std::runtime_error("InstantNerf: no ray fits the batch");
+        }
         if (hitCounts) hitCounts[i] = hits;
         i++;
-        if (raysDone + active >= numRays) {
-            if (next.n) {
+        m_lastRaysTrained = raysDone + active;
+        const bool all_rays = raysDone + active >= numRays;
+        if (all_rays || (m_stepLimit > 0 && i >= m_stepLimit)) {
+            // the next call's rays are compacted ahead only when they are
+            // other buffers than this call's (a caller refilling these buffers
+            // in place for the next call would otherwise train on stale rays)
+            if (all_rays && next.n && next.o != d_rays_o && next.d != d_rays_d) {
                 // the next call's first hit batch, beside this last step; the
                 // march store is keyed by ray index, so it holds this call's rays
                 k ^= 1;

@@ -373,6 +373,11 @@ int inerf_set_next_rays(Inerf* h, const float* rays_o, const float* rays_d, uint
                      h->nerf.setNextRays(reinterpret_cast<const float3*>(rays_o),
                                          reinterpret_cast<const float3*>(rays_d), num_rays));
 }
+int inerf_set_step_limit(Inerf* h, int max_steps)
+{
+    return NERF_CALL("inerf_set_step_limit", h->nerf.setStepLimit(max_steps));
+}
+uint32_t inerf_last_rays_trained(Inerf* h) { return h ? h->nerf.lastRaysTrained() : 0u; }
 int inerf_set_bg_color(Inerf* h, float r, float g, float b)
 {
     return NERF_CALL("inerf_set_bg_color", h->nerf.setBgColor(make_float3(r, g, b)));

@@ -115,6 +115,12 @@ public:
     // with other rays, a render or an occupancy change in between discards the
     // prefetch (the call compacts as usual).  numRays = 0 clears.
     void setNextRays(const float3* d_rays_o, const float3* d_rays_d, uint32_t numRays);
+    // Addition: at most maxSteps optimizer steps per trainWithRaysHit call
+    // (0: no limit, the reference's behaviour); the call then returns after
+    // training the rays [0, lastRaysTrained()), and the caller continues with
+    // the rest.
+    void setStepLimit(int maxSteps) { m_stepLimit = maxSteps > 0 ? maxSteps : 0; }
+    uint32_t lastRaysTrained() const { return m_lastRaysTrained; }
 
     // InstantNerf.cu:359-583.  d_rays_depth / d_rays_sigma may be null (depth
     // supervision off), d_rgb_true must be set, hitCounts (host, nullable)
@@ -206,6 +212,8 @@ private:
     int m_trainSteps = 0;
     long m_gridVersion = 0;  // bumped whenever the occupancy bitfield changes
     uint32_t m_windowStart = 0;
+    int m_stepLimit = 0;
+    uint32_t m_lastRaysTrained = 0;
 
     uint8_t* d_occupancyGrid = nullptr;
     size_t m_occupancyBytes = 0;

@@ -81,6 +81,10 @@ int inerf_set_learning_rate(Inerf* h, float lr);
  * inerf_train call, compacted beside the current call's last step. */
 int inerf_set_next_rays(Inerf* h, const float* rays_o, const float* rays_d, uint32_t num_rays);
 int inerf_set_bg_color(Inerf* h, float r, float g, float b);
+/* InstantNerf::setStepLimit / lastRaysTrained (no reference counterpart): at
+ * most max_steps optimizer steps per inerf_train call (0: no limit). */
+int inerf_set_step_limit(Inerf* h, int max_steps);
+uint32_t inerf_last_rays_trained(Inerf* h);
 int inerf_set_profiling(Inerf* h, int on);
 int inerf_print_stats(Inerf* h);
 /* Per-stage profiling means as "stage:mean_ms:calls;..." into buf (NUL-terminated,
