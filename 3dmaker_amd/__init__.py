@@ -168,6 +168,17 @@ SIGNATURES = {
     # include/nerf_abi.h (NeRF launchers)
     "processRaysHitLinear": (_i, [_u32, _vp, _vp, _vp, _vp, _vp, _vp, Uint3, Float3, Float3, _i, _i, _i, _i,
                                   C.POINTER(_u32), _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "launchMarchRaysDDA": (None, [_u32, _vp, _vp, _vp, _vp, _vp, _vp, Uint3, Float3, Float3, _i, _i, _i, _vp, _vp,
+                                  _vp, _vp]),
+    "processRaysChunk": (None, [_u32, _vp, _vp, _vp, _vp, _vp, _vp, Uint3, Float3, Float3, _i, _i, _i, _vp, _vp, _vp,
+                                _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "processRaysChunkLinear": (None, [_u32, _vp, _vp, _vp, _vp, _vp, _vp, Uint3, Float3, Float3, _i, _i, _i, _vp,
+                                      _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "processRaysHitData": (None, [_u32, _vp, _vp, _vp, _vp, _vp, _vp, Uint3, Float3, Float3, _i, _i, _i, _vp, _vp,
+                                  _vp, _vp]),
+    "processRaysHitPositions": (_i, [_u32, _vp, _vp, _vp, _vp, _vp, _vp, Uint3, Float3, Float3, _i, _i, _i, _u32, _i,
+                                     C.POINTER(_u32), C.POINTER(_u32), _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "launchComputeRealSHDegree3": (None, [_u32, _vp, _vp, _vp]),
     "launchVolumeRendering": (None, [_u32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f, _f,
                                      Float3, _u32, _u32, _vp]),
     "launchComputeRayAabbInv": (None, [_u32, _vp, _vp, Float3, Float3, _i, _vp, _vp, _vp, _vp]),

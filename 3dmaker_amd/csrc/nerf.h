@@ -60,6 +60,51 @@ void march_compact_stored(uint32_t R, const float3* o, const float3* d, const Oc
                           float* t_out, uint32_t* ray_idx, float4* pos_out, const MarchScratch& scratch,
                           hipStream_t s, uint32_t* counts_out = nullptr);
 
+// march_rays_dda_calc_hits (processRays.cu:626-737): per-ray sample counts only.
+void march_count(uint32_t R, const float3* o, const float3* d, const float3* d_inv, const float* nears,
+                 const float* fars, const OccGrid& g, int K, uint32_t* counts, hipStream_t s);
+// march_rays_dda_kernel (processRays.cu:96-226): the per-ray ("sparse")
+// layout, sample k of ray i at t_sparse[i * kMaxHits + k] and, when morton is
+// set, the 30-bit Morton code of its level-0 cell at morton[i * kMaxHits + k].
+void march_sparse(uint32_t R, const float3* o, const float3* d, const float3* d_inv, const float* nears,
+                  const float* fars, const OccGrid& g, int K, uint32_t* counts, float* t_sparse, uint32_t* morton,
+                  hipStream_t s);
+// Exclusive scan of counts [R] into offsets (uint32 wrap-around, as
+// custom_exclusive_sum, processRays.cu:486-549) and the cutoff at batch:
+// scratch.result = {rays whose samples fit in batch, their samples}; batch =
+// UINT32_MAX gives {R, all samples}.
+void scan_counts(uint32_t R, const uint32_t* counts, uint32_t batch, uint32_t* offsets, const MarchScratch& scratch,
+                 hipStream_t s, uint32_t* counts_out = nullptr);
+// find_cutoff_ray_from_kernel (processRays.cu:771-799) over rays [rays_done,
+// R): result[4] = {batch rays, their samples, base = offsets[rays_done],
+// rays_done + batch rays}, all zero (and *next_done zero) when the first ray
+// does not fit or rays_done >= R; *next_done (nullable) = result[3].
+void cutoff_from(uint32_t R, const uint32_t* offsets, const uint32_t* counts, uint32_t batch, uint32_t rays_done,
+                 uint32_t* next_done, uint32_t* result, hipStream_t s);
+// Samples j < result[1] of rays [0, result[0]) whose samples start at
+// offsets[i] - base, from a march store holding those rays from row 0:
+// t_out[j], ray_idx[j] (ray-local), pos_out[j] (contracted, w = 0).
+void gather_stored(uint32_t max_samples, const float3* o, const float3* d, const OccGrid& g, const uint32_t* offsets,
+                   uint32_t base, const float* t_scratch, const uint32_t* result, float* t_out, uint32_t* ray_idx,
+                   float4* pos_out, hipStream_t s);
+// compact_hits(_linear)_kernel (processRays.cu:297-318, 466-483) over the
+// result[1] samples of rays [0, R): sparse_idx[j] = ray * kMaxHits + k, keys[j]
+// (nullable) = morton[sparse_idx[j]].
+void compact_sparse(uint32_t R, const uint32_t* offsets, const uint32_t* result, uint32_t max_samples,
+                    const uint32_t* morton, uint32_t* keys, uint32_t* sparse_idx, hipStream_t s);
+// generate_mlp_batch_kernel (processRays.cu:320-356) over result[1] samples.
+void sparse_batch(const uint32_t* result, uint32_t max_samples, const uint32_t* sparse_idx, const float* t_sparse,
+                  const float3* o, const float3* d, float3 aabb_min, float3 aabb_max, float4* pos_out,
+                  uint32_t* ray_idx, float* t_out, hipStream_t s);
+// compute_real_sh_degree_3_kernel (otherKernels.cu:18-64): out [n][16]
+// (16-byte aligned).
+void sh_degree3(uint32_t n, const float3* dirs, float* out, hipStream_t s);
+// Stable ascending sort of n (key, value) pairs of 32-bit keys (rocPRIM's
+// LSD radix sort; library-owned temporary storage grown on demand).  Blocks
+// until the sort has finished.
+void sort_pairs_u32(const uint32_t* keys_in, uint32_t* keys_out, const uint32_t* values_in, uint32_t* values_out,
+                    uint32_t n, hipStream_t s);
+
 // compute_SH_gather (otherKernels.cu:156-273).
 void sh_gather(const float3* dirs, const uint32_t* ray_idx, const uint32_t* d_n, uint32_t n_max, float bias,
                const float* density_out, __half* color_in, float* sigma, hipStream_t s);

@@ -16,6 +16,7 @@
 #include <algorithm>
 #include <cstring>
 #include <mutex>
+#include <string>
 
 using graft::guarded;
 
@@ -63,6 +64,65 @@ float* march_tstore(size_t floats)
     return g_tstore;
 }
 
+graft::OccGrid occ_grid(const uint8_t* bits, uint3 res, float3 mn, float3 mx, int cascades, int mips)
+{
+    graft::OccGrid g{};
+    g.bits = bits;
+    g.res = res;
+    g.aabb_min = mn;
+    g.aabb_max = mx;
+    g.cascades = cascades;
+    g.mip_levels = mips;
+    return g;
+}
+
+// float4 stores need 16-byte alignment (the reference's vector stores do too).
+void require_aligned16(const void* p, const char* what)
+{
+    if (reinterpret_cast<uintptr_t>(p) % 16 != 0)
+        throw std::runtime_error(std::string(what) + " must be 16-byte aligned");
+}
+
+// Exclusive scan of counts into offsets with the library's scratch; returns
+// the scratch (result = {R, total samples}) and writes the total to *total.
+graft::MarchScratch scan_all(uint32_t R, const uint32_t* counts, uint32_t* offsets, hipStream_t s, uint32_t* total)
+{
+    const size_t words = graft::march_scratch_words(R);
+    uint32_t* sc = march_scratch(words);
+    graft::MarchScratch ms{sc, sc + (words - 2)};
+    graft::scan_counts(R, counts, 0xffffffffu, offsets, ms, s);
+    if (total) {
+        uint32_t h[2] = {0, 0};
+        GRAFT_HIP_CHECK(hipMemcpyAsync(h, ms.result, sizeof(h), hipMemcpyDeviceToHost, s));
+        GRAFT_HIP_CHECK(hipStreamSynchronize(s));
+        *total = h[1];
+    }
+    return ms;
+}
+
+// processRaysChunk / processRaysChunkLinear (processRays.cu:357-464, 551-624):
+// sparse march, scan, compaction (Morton-sorted when keys are given), batch.
+void chunk_pipeline(uint32_t R, const float3* o, const float3* d, const float3* di, const float* nears,
+                    const float* fars, const graft::OccGrid& g, int K, uint32_t* morton, float* t_sparse,
+                    uint32_t* counts, uint32_t* offsets, uint32_t* keys_in, uint32_t* idx_in, uint32_t* keys_out,
+                    uint32_t* idx_out, float* pos, uint32_t* ridx, float* t_sorted, hipStream_t s)
+{
+    if (R == 0) return;
+    require_aligned16(pos, "d_mlp_positions_batch");
+    graft::march_sparse(R, o, d, di, nears, fars, g, K, counts, t_sparse, morton, s);
+    uint32_t total = 0;
+    const graft::MarchScratch ms = scan_all(R, counts, offsets, s, &total);
+    if (total == 0) return;
+    graft::compact_sparse(R, offsets, ms.result, total, morton, keys_in, idx_in, s);
+    const uint32_t* order = idx_in;
+    if (keys_in) {
+        graft::sort_pairs_u32(keys_in, keys_out, idx_in, idx_out, total, s);
+        order = idx_out;
+    }
+    graft::sparse_batch(ms.result, total, order, t_sparse, o, d, g.aabb_min, g.aabb_max,
+                        reinterpret_cast<float4*>(pos), ridx, t_sorted, s);
+}
+
 float* reduce_partials()
 {
     static float* p = nullptr;
@@ -93,13 +153,9 @@ int processRaysHitLinear(const uint32_t num_rays, const float3* rays_o, const fl
     int active = 0;
     guarded("processRaysHitLinear", [&] {
         if (batchSize < 0) throw std::runtime_error("batchSize must be >= 0");
-        graft::OccGrid g{};
-        g.bits = occupancy_grid;
-        g.res = grid_resolution;
-        g.aabb_min = aabb_min;
-        g.aabb_max = aabb_max;
-        g.cascades = numCascades;
-        g.mip_levels = mipmapLevels;
+        require_aligned16(d_mlp_positions_batch, "d_mlp_positions_batch");
+        const graft::OccGrid g =
+            occ_grid(occupancy_grid, grid_resolution, aabb_min, aabb_max, numCascades, mipmapLevels);
         const size_t words = graft::march_scratch_words(num_rays);
         (void)d_block_sums;  // sized (R + 1023) / 1024 by reference callers: too small, not used
         uint32_t* sc = march_scratch(words);
@@ -119,6 +175,132 @@ int processRaysHitLinear(const uint32_t num_rays, const float3* rays_o, const fl
         active = (int)h[0];
     });
     return active;
+}
+
+void processRaysHitData(const uint32_t num_rays, const float3* rays_o, const float3* rays_d, const float3* rays_d_inv,
+                        const float* nears, const float* fars, const uint8_t* occupancy_grid,
+                        const uint3 grid_resolution, const float3 aabb_min, const float3 aabb_max,
+                        const int numCascades, const int mipmapLevels, const int samplesPerVoxel,
+                        uint32_t* d_num_steps, uint32_t* d_ray_offsets, uint32_t* d_block_sums, hipStream_t stream)
+{
+    guarded("processRaysHitData", [&] {
+        (void)d_block_sums;  // sized (R + 1023) / 1024 by reference callers; the library's scratch is used
+        if (num_rays == 0) return;
+        const graft::OccGrid g =
+            occ_grid(occupancy_grid, grid_resolution, aabb_min, aabb_max, numCascades, mipmapLevels);
+        graft::march_count(num_rays, rays_o, rays_d, rays_d_inv, nears, fars, g, samplesPerVoxel, d_num_steps,
+                           stream);
+        scan_all(num_rays, d_num_steps, d_ray_offsets, stream, nullptr);
+    });
+}
+
+int processRaysHitPositions(const uint32_t num_rays, const float3* rays_o, const float3* rays_d,
+                            const float3* rays_d_inv, const float* nears, const float* fars,
+                            const uint8_t* occupancy_grid, const uint3 grid_resolution, const float3 aabb_min,
+                            const float3 aabb_max, const int numCascades, const int mipmapLevels,
+                            const int samplesPerVoxel, const uint32_t rays_done, const int batchSize,
+                            uint32_t* totalHits, uint32_t* out_base, uint32_t* d_num_steps, uint32_t* d_ray_offsets,
+                            float* d_mlp_positions_batch, uint32_t* d_ray_indices, uint32_t* d_active_rays_count,
+                            float* d_t_sorted, uint32_t* d_block_sums, hipStream_t stream)
+{
+    int active = 0;
+    guarded("processRaysHitPositions", [&] {
+        (void)d_block_sums;
+        if (batchSize < 0) throw std::runtime_error("batchSize must be >= 0");
+        if (!totalHits || !out_base) throw std::runtime_error("totalHits and out_base must not be NULL");
+        require_aligned16(d_mlp_positions_batch, "d_mlp_positions_batch");
+        const graft::OccGrid g =
+            occ_grid(occupancy_grid, grid_resolution, aabb_min, aabb_max, numCascades, mipmapLevels);
+        const uint32_t left = rays_done < num_rays ? num_rays - rays_done : 0u;
+        // scratch: the re-marched rays' counts [left], then the cutoff result [4]
+        uint32_t* sc = march_scratch((size_t)left + 4);
+        uint32_t* res = sc + left;
+        graft::cutoff_from(num_rays, d_ray_offsets, d_num_steps, (uint32_t)batchSize, rays_done,
+                           d_active_rays_count, res, stream);
+        uint32_t h[4] = {0, 0, 0, 0};
+        GRAFT_HIP_CHECK(hipMemcpyAsync(h, res, sizeof(h), hipMemcpyDeviceToHost, stream));
+        GRAFT_HIP_CHECK(hipStreamSynchronize(stream));
+        if (h[3] <= rays_done) {  // the first ray does not fit (or no rays are left)
+            *totalHits = 0;
+            return;
+        }
+        const uint32_t batch_rays = h[0], total = h[1], base = h[2];
+        *out_base = base;
+        *totalHits = total;
+        // march_rays_dda_offset (processRays.cu:801-929) re-marches the batch's
+        // rays; here they are marched into the store and gathered per sample
+        float* ts = march_tstore(graft::march_store_floats(batch_rays));
+        const size_t r0 = rays_done;
+        graft::march_store(batch_rays, rays_o + r0, rays_d + r0, rays_d_inv + r0, nears + r0, fars + r0, g,
+                           samplesPerVoxel, sc, ts, stream);
+        graft::gather_stored(total, rays_o + r0, rays_d + r0, g, d_ray_offsets + r0, base, ts, res, d_t_sorted,
+                             d_ray_indices, reinterpret_cast<float4*>(d_mlp_positions_batch), stream);
+        active = (int)batch_rays;
+    });
+    return active;
+}
+
+void launchMarchRaysDDA(const uint32_t num_rays, const float3* rays_o, const float3* rays_d, const float3* rays_d_inv,
+                        const float* nears, const float* fars, const uint8_t* occupancy_grid,
+                        const uint3 grid_resolution, const float3 aabb_min, const float3 aabb_max,
+                        const int numCascades, const int mipmapLevels, const int samplesPerVoxel,
+                        uint32_t* packed_coords_out, float* t_hits_out, uint32_t* num_steps_per_ray,
+                        hipStream_t stream)
+{
+    guarded("launchMarchRaysDDA", [&] {
+        const graft::OccGrid g =
+            occ_grid(occupancy_grid, grid_resolution, aabb_min, aabb_max, numCascades, mipmapLevels);
+        graft::march_sparse(num_rays, rays_o, rays_d, rays_d_inv, nears, fars, g, samplesPerVoxel,
+                            num_steps_per_ray, t_hits_out, packed_coords_out, stream);
+    });
+}
+
+void processRaysChunk(const uint32_t num_rays, const float3* rays_o, const float3* rays_d, const float3* rays_d_inv,
+                      const float* nears, const float* fars, const uint8_t* occupancy_grid,
+                      const uint3 grid_resolution, const float3 aabb_min, const float3 aabb_max,
+                      const int numCascades, const int mipmapLevels, const int samplesPerVoxel,
+                      uint32_t* d_sparse_morton, float* d_sparse_ts, uint32_t* d_num_steps, uint32_t* d_ray_offsets,
+                      uint32_t* d_dense_morton_keys_in, uint32_t* d_dense_sparse_indices_in,
+                      uint32_t* d_dense_morton_keys_out, uint32_t* d_dense_sparse_indices_out,
+                      float* d_mlp_positions_batch, uint32_t* d_ray_indices, float* d_t_sorted, hipStream_t stream)
+{
+    guarded("processRaysChunk", [&] {
+        if (!d_sparse_morton || !d_dense_morton_keys_in || !d_dense_morton_keys_out || !d_dense_sparse_indices_out)
+            throw std::runtime_error("the Morton key and sorted index buffers must not be NULL");
+        const graft::OccGrid g =
+            occ_grid(occupancy_grid, grid_resolution, aabb_min, aabb_max, numCascades, mipmapLevels);
+        chunk_pipeline(num_rays, rays_o, rays_d, rays_d_inv, nears, fars, g, samplesPerVoxel, d_sparse_morton,
+                       d_sparse_ts, d_num_steps, d_ray_offsets, d_dense_morton_keys_in, d_dense_sparse_indices_in,
+                       d_dense_morton_keys_out, d_dense_sparse_indices_out, d_mlp_positions_batch, d_ray_indices,
+                       d_t_sorted, stream);
+    });
+}
+
+void processRaysChunkLinear(const uint32_t num_rays, const float3* rays_o, const float3* rays_d,
+                            const float3* rays_d_inv, const float* nears, const float* fars,
+                            const uint8_t* occupancy_grid, const uint3 grid_resolution, const float3 aabb_min,
+                            const float3 aabb_max, const int numCascades, const int mipmapLevels,
+                            const int samplesPerVoxel, float* d_sparse_ts, uint32_t* d_num_steps,
+                            uint32_t* d_ray_offsets, uint32_t* d_dense_sparse_indices, float* d_mlp_positions_batch,
+                            uint32_t* d_ray_indices, float* d_t_sorted, hipStream_t stream)
+{
+    guarded("processRaysChunkLinear", [&] {
+        const graft::OccGrid g =
+            occ_grid(occupancy_grid, grid_resolution, aabb_min, aabb_max, numCascades, mipmapLevels);
+        chunk_pipeline(num_rays, rays_o, rays_d, rays_d_inv, nears, fars, g, samplesPerVoxel, nullptr, d_sparse_ts,
+                       d_num_steps, d_ray_offsets, nullptr, d_dense_sparse_indices, nullptr, nullptr,
+                       d_mlp_positions_batch, d_ray_indices, d_t_sorted, stream);
+    });
+}
+
+void launchComputeRealSHDegree3(const uint32_t total_hits, const float3* d_directions, float* d_out_sh,
+                                hipStream_t stream)
+{
+    guarded("launchComputeRealSHDegree3", [&] {
+        if (total_hits == 0) return;
+        require_aligned16(d_out_sh, "d_out_sh");
+        graft::sh_degree3(total_hits, d_directions, d_out_sh, stream);
+    });
 }
 
 void launchVolumeRendering(const uint32_t num_rays, const uint32_t* d_ray_offsets, const uint32_t* d_num_steps,

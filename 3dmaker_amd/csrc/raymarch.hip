@@ -56,8 +56,8 @@ struct MarchArgs {
     int shift_levels;            // res divisible by 2^(L-1): level-l cells are level-0 cells >> l
 };
 
-// Marches ray i and stores its sample t values at t_out[march_store_index(i, k)];
-// returns the sample count.
+// Marches ray i, hands sample k (its t value and the level-0 cell it lies in)
+// to sink(k, t, ix, iy, iz), and returns the sample count.
 //
 // The reference loop (processRays.cu:660-733) spends one iteration per mip
 // level: at a t it starts at level L-1 and descends while the cell is
@@ -70,8 +70,8 @@ struct MarchArgs {
 // bit-identical; `it` counts the reference's iterations, descents included.
 // The voxel size uses (e * 2^c) / r == 2^c * (e / r), exact for powers of two,
 // with e / r precomputed per level.
-template <int MAXL>
-__device__ uint32_t march_ray(const MarchArgs& a, uint32_t i, float* __restrict__ t_out)
+template <int MAXL, class Sink>
+__device__ uint32_t march_ray(const MarchArgs& a, uint32_t i, Sink&& sink)
 {
     const float3 o = a.o[i], d = a.d[i], di = a.di[i];
     float t = a.nears[i];
@@ -153,7 +153,7 @@ __device__ uint32_t march_ray(const MarchArgs& a, uint32_t i, float* __restrict_
             const float span = next_t - t;
             for (int k = 0; k < a.K; ++k) {
                 if (hit >= (uint32_t)kMaxHits) break;
-                t_out[march_store_index(i, hit)] = t + ((float)k + 0.5f) / (float)a.K * span;
+                sink(hit, t + ((float)k + 0.5f) / (float)a.K * span, vix, viy, viz);
                 hit++;
             }
         }
@@ -281,7 +281,47 @@ __global__ __launch_bounds__(256) void march_store_kernel(const MarchArgs a, uin
                                                           float* __restrict__ t_scratch)
 {
     const uint32_t i = blockIdx.x * 256 + threadIdx.x;
-    if (i < a.R) counts[i] = march_ray<MAXL>(a, i, t_scratch);
+    if (i < a.R)
+        counts[i] = march_ray<MAXL>(a, i, [&](uint32_t k, float t, int, int, int) {
+            t_scratch[march_store_index(i, k)] = t;
+        });
+}
+
+// march_rays_dda_calc_hits (processRays.cu:626-737): counts only.
+template <int MAXL>
+__global__ __launch_bounds__(256) void march_count_kernel(const MarchArgs a, uint32_t* __restrict__ counts)
+{
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i < a.R) counts[i] = march_ray<MAXL>(a, i, [](uint32_t, float, int, int, int) {});
+}
+
+// 30-bit Morton code of a cell: bit b of x, y, z goes to bit 3b, 3b + 1,
+// 3b + 2; coordinates are taken mod 2^10 (expand_bits_3d / morton3d,
+// processRays.cu:71-82).
+__device__ __forceinline__ uint32_t morton30(uint32_t x, uint32_t y, uint32_t z)
+{
+    uint32_t m = 0;
+#pragma unroll
+    for (int b = 0; b < 10; b++)
+        m |= (((x >> b) & 1u) << (3 * b)) | (((y >> b) & 1u) << (3 * b + 1)) | (((z >> b) & 1u) << (3 * b + 2));
+    return m;
+}
+
+// march_rays_dda_kernel (processRays.cu:96-226): sample k of ray i at
+// t_sparse[i * kMaxHits + k], its cell's Morton code at the same index of
+// morton (nullable).
+template <int MAXL>
+__global__ __launch_bounds__(256) void march_sparse_kernel(const MarchArgs a, uint32_t* __restrict__ counts,
+                                                           float* __restrict__ t_sparse,
+                                                           uint32_t* __restrict__ morton)
+{
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= a.R) return;
+    const size_t row = (size_t)i * kMaxHits;
+    counts[i] = march_ray<MAXL>(a, i, [&](uint32_t k, float t, int x, int y, int z) {
+        t_sparse[row + k] = t;
+        if (morton != nullptr) morton[row + k] = morton30((uint32_t)x, (uint32_t)y, (uint32_t)z);
+    });
 }
 
 __global__ __launch_bounds__(256) void block_sums_kernel(const uint32_t* __restrict__ counts, uint32_t n,
@@ -311,14 +351,30 @@ __global__ __launch_bounds__(256) void offsets_kernel(const uint32_t* __restrict
     }
 }
 
-// One thread per compacted sample j < result[1]: its ray is the last active
-// ray whose offset is <= j (rays without samples share the next ray's offset);
-// t comes from the stored march, the position is contracted as in the fill.
+// The ray of compacted sample j: the last of rays [0, active) whose offset
+// (less base) is <= j; rays without samples share the next ray's offset.
+__device__ __forceinline__ uint32_t ray_of_sample(const uint32_t* __restrict__ offsets, uint32_t base,
+                                                  uint32_t active, uint32_t j)
+{
+    uint32_t lo = 0, hi = active - 1;
+    while (lo < hi) {
+        const uint32_t mid = (lo + hi + 1) >> 1;
+        if (offsets[mid] - base <= j) lo = mid;
+        else hi = mid - 1;
+    }
+    return lo;
+}
+
+// One thread per compacted sample j < result[1] of rays [0, result[0]); t
+// comes from the stored march, the position is contracted as in the fill.
+// The sample index within the ray is clamped to the store's row, so offsets
+// that disagree with the stored march cannot read outside it.
 struct GatherArgs {
     const float3* o;
     const float3* d;
     float3 mn, mx;
     const uint32_t* offsets;
+    uint32_t base;           // subtracted from every offset
     const float* t_scratch;
     uint32_t ray_base;
     const uint32_t* result;
@@ -331,13 +387,8 @@ __global__ __launch_bounds__(256) void gather_samples_kernel(const GatherArgs g)
 {
     const uint32_t active = g.result[0], total = g.result[1];
     for (uint32_t j = blockIdx.x * 256 + threadIdx.x; j < total; j += gridDim.x * 256) {
-        uint32_t lo = 0, hi = active - 1;
-        while (lo < hi) {
-            const uint32_t mid = (lo + hi + 1) >> 1;
-            if (g.offsets[mid] <= j) lo = mid;
-            else hi = mid - 1;
-        }
-        const uint32_t k = j - g.offsets[lo];
+        const uint32_t lo = ray_of_sample(g.offsets, g.base, active, j);
+        const uint32_t k = min(j - (g.offsets[lo] - g.base), (uint32_t)kMaxHits - 1u);
         const float tk = g.t_scratch[march_store_index(g.ray_base + lo, k)];
         const float3 o = g.o[lo], d = g.d[lo];
         g.t_out[j] = tk;
@@ -346,6 +397,84 @@ __global__ __launch_bounds__(256) void gather_samples_kernel(const GatherArgs g)
                                    contract_axis(o.y + tk * d.y, g.mn.y, g.mx.y),
                                    contract_axis(o.z + tk * d.z, g.mn.z, g.mx.z), 0.0f);
     }
+}
+
+// find_cutoff_ray_from_kernel (processRays.cu:771-799): the rays from
+// rays_done whose samples fit in batch.  The boundary ray i (the last that
+// fits) writes result = {i + 1 - rays_done, its inclusive sample count past
+// base, base, i + 1} and *next_done = i + 1; result and *next_done stay zero
+// when the first ray does not fit.
+__global__ __launch_bounds__(256) void cutoff_from_kernel(uint32_t R, const uint32_t* __restrict__ offsets,
+                                                          const uint32_t* __restrict__ counts, uint32_t batch,
+                                                          uint32_t rays_done, uint32_t* __restrict__ next_done,
+                                                          uint32_t* __restrict__ result)
+{
+    const uint32_t base = offsets[rays_done];
+    for (uint32_t i = rays_done + blockIdx.x * 256 + threadIdx.x; i < R; i += gridDim.x * 256) {
+        const uint32_t incl = offsets[i] + counts[i] - base;
+        if (incl > batch) continue;
+        if (i + 1 < R && offsets[i + 1] + counts[i + 1] - base <= batch) continue;
+        result[0] = i + 1 - rays_done;
+        result[1] = incl;
+        result[2] = base;
+        result[3] = i + 1;
+        if (next_done != nullptr) *next_done = i + 1;
+    }
+}
+
+// compact_hits_kernel / compact_hits_linear_kernel (processRays.cu:297-318,
+// 466-483), one thread per compacted sample j < result[1] of rays [0, R):
+// sparse_idx[j] = ray * kMaxHits + k for sample k of its ray, keys[j] (nullable)
+// that sample's Morton code.
+__global__ __launch_bounds__(256) void compact_sparse_kernel(uint32_t R, const uint32_t* __restrict__ offsets,
+                                                             const uint32_t* __restrict__ result,
+                                                             const uint32_t* __restrict__ morton,
+                                                             uint32_t* __restrict__ keys,
+                                                             uint32_t* __restrict__ sparse_idx)
+{
+    const uint32_t total = result[1];
+    for (uint32_t j = blockIdx.x * 256 + threadIdx.x; j < total; j += gridDim.x * 256) {
+        const uint32_t ray = ray_of_sample(offsets, 0u, R, j);
+        const uint32_t k = min(j - offsets[ray], (uint32_t)kMaxHits - 1u);
+        const uint32_t idx = ray * (uint32_t)kMaxHits + k;
+        sparse_idx[j] = idx;
+        if (keys != nullptr) keys[j] = morton[idx];
+    }
+}
+
+// generate_mlp_batch_kernel (processRays.cu:320-356): sample j < result[1]
+// is sparse sample sparse_idx[j] of ray sparse_idx[j] / kMaxHits.
+__global__ __launch_bounds__(256) void sparse_batch_kernel(const uint32_t* __restrict__ result,
+                                                           const uint32_t* __restrict__ sparse_idx,
+                                                           const float* __restrict__ t_sparse,
+                                                           const float3* __restrict__ O, const float3* __restrict__ D,
+                                                           float3 mn, float3 mx, float4* __restrict__ pos_out,
+                                                           uint32_t* __restrict__ ridx, float* __restrict__ t_out)
+{
+    const uint32_t total = result[1];
+    for (uint32_t j = blockIdx.x * 256 + threadIdx.x; j < total; j += gridDim.x * 256) {
+        const uint32_t idx = sparse_idx[j];
+        const uint32_t ray = idx / (uint32_t)kMaxHits;
+        const float tk = t_sparse[idx];
+        const float3 o = O[ray], d = D[ray];
+        pos_out[j] = make_float4(contract_axis(o.x + tk * d.x, mn.x, mx.x), contract_axis(o.y + tk * d.y, mn.y, mx.y),
+                                 contract_axis(o.z + tk * d.z, mn.z, mx.z), 0.0f);
+        ridx[j] = ray;
+        t_out[j] = tk;
+    }
+}
+
+// compute_real_sh_degree_3_kernel (otherKernels.cu:18-64): out[n][16].
+__global__ __launch_bounds__(256) void sh_degree3_kernel(uint32_t n, const float3* __restrict__ dirs,
+                                                         float4* __restrict__ out)
+{
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const float3 d = dirs[i];
+    float sh[16];
+    sh_basis16(d.x, d.y, d.z, sh);
+#pragma unroll
+    for (int q = 0; q < 4; q++) out[4 * (size_t)i + q] = make_float4(sh[4 * q], sh[4 * q + 1], sh[4 * q + 2], sh[4 * q + 3]);
 }
 
 MarchArgs march_args(uint32_t R, const float3* o, const float3* d, const float3* di, const float* nears,
@@ -399,22 +528,43 @@ void ray_aabb_inv(uint32_t R, const float3* o, const float3* d, float3 mn, float
 
 size_t march_scratch_words(uint32_t R) { return (size_t)(R + 255) / 256 + 2; }
 
+// Launches kernel<MAXL> for the smallest MAXL >= the mip level count.
+#define GRAFT_MARCH_LAUNCH(kernel, a, s, ...)                                                               \
+    do {                                                                                                    \
+        const dim3 grid_((a.R + 255) / 256);                                                                \
+        if (a.L <= 4) hipLaunchKernelGGL(kernel<4>, grid_, dim3(256), 0, s, a, __VA_ARGS__);                \
+        else if (a.L <= 8) hipLaunchKernelGGL(kernel<8>, grid_, dim3(256), 0, s, a, __VA_ARGS__);           \
+        else hipLaunchKernelGGL(kernel<kMaxMip>, grid_, dim3(256), 0, s, a, __VA_ARGS__);                   \
+        GRAFT_LAUNCH_CHECK();                                                                               \
+    } while (0)
+
 void march_store(uint32_t R, const float3* o, const float3* d, const float3* d_inv, const float* nears,
                  const float* fars, const OccGrid& g, int K, uint32_t* counts, float* t_scratch, hipStream_t s)
 {
     if (R == 0) return;
     const MarchArgs a = march_args(R, o, d, d_inv, nears, fars, g, K);
-    const dim3 grid((R + 255) / 256);
-    if (a.L <= 4) hipLaunchKernelGGL(march_store_kernel<4>, grid, dim3(256), 0, s, a, counts, t_scratch);
-    else if (a.L <= 8) hipLaunchKernelGGL(march_store_kernel<8>, grid, dim3(256), 0, s, a, counts, t_scratch);
-    else hipLaunchKernelGGL(march_store_kernel<kMaxMip>, grid, dim3(256), 0, s, a, counts, t_scratch);
-    GRAFT_LAUNCH_CHECK();
+    GRAFT_MARCH_LAUNCH(march_store_kernel, a, s, counts, t_scratch);
 }
 
-void march_compact_stored(uint32_t R, const float3* o, const float3* d, const OccGrid& g, uint32_t batch,
-                          const uint32_t* counts, const float* t_scratch, uint32_t ray_base, uint32_t* offsets,
-                          float* t_out, uint32_t* ray_idx, float4* pos_out, const MarchScratch& sc, hipStream_t s,
-                          uint32_t* counts_out)
+void march_count(uint32_t R, const float3* o, const float3* d, const float3* d_inv, const float* nears,
+                 const float* fars, const OccGrid& g, int K, uint32_t* counts, hipStream_t s)
+{
+    if (R == 0) return;
+    const MarchArgs a = march_args(R, o, d, d_inv, nears, fars, g, K);
+    GRAFT_MARCH_LAUNCH(march_count_kernel, a, s, counts);
+}
+
+void march_sparse(uint32_t R, const float3* o, const float3* d, const float3* d_inv, const float* nears,
+                  const float* fars, const OccGrid& g, int K, uint32_t* counts, float* t_sparse, uint32_t* morton,
+                  hipStream_t s)
+{
+    if (R == 0) return;
+    const MarchArgs a = march_args(R, o, d, d_inv, nears, fars, g, K);
+    GRAFT_MARCH_LAUNCH(march_sparse_kernel, a, s, counts, t_sparse, morton);
+}
+
+void scan_counts(uint32_t R, const uint32_t* counts, uint32_t batch, uint32_t* offsets, const MarchScratch& sc,
+                 hipStream_t s, uint32_t* counts_out)
 {
     if (R == 0) {
         GRAFT_HIP_CHECK(hipMemsetAsync(sc.result, 0, 2 * sizeof(uint32_t), s));
@@ -427,9 +577,68 @@ void march_compact_stored(uint32_t R, const float3* o, const float3* d, const Oc
     GRAFT_LAUNCH_CHECK();
     hipLaunchKernelGGL(offsets_kernel, dim3(nb), dim3(256), 0, s, counts, R, sc.block_sums, offsets, counts_out);
     GRAFT_LAUNCH_CHECK();
-    GatherArgs ga{o, d, g.aabb_min, g.aabb_max, offsets, t_scratch, ray_base, sc.result, t_out, ray_idx, pos_out};
-    const int gblocks = (int)std::max<uint32_t>(1, std::min<uint32_t>((batch + 255) / 256, 4096));
-    hipLaunchKernelGGL(gather_samples_kernel, dim3(gblocks), dim3(256), 0, s, ga);
+}
+
+static int sample_blocks(uint32_t n) { return (int)std::max<uint32_t>(1, std::min<uint32_t>((n + 255) / 256, 4096)); }
+
+void march_compact_stored(uint32_t R, const float3* o, const float3* d, const OccGrid& g, uint32_t batch,
+                          const uint32_t* counts, const float* t_scratch, uint32_t ray_base, uint32_t* offsets,
+                          float* t_out, uint32_t* ray_idx, float4* pos_out, const MarchScratch& sc, hipStream_t s,
+                          uint32_t* counts_out)
+{
+    scan_counts(R, counts, batch, offsets, sc, s, counts_out);
+    if (R == 0) return;
+    GatherArgs ga{o, d, g.aabb_min, g.aabb_max, offsets, 0u, t_scratch, ray_base, sc.result, t_out, ray_idx, pos_out};
+    hipLaunchKernelGGL(gather_samples_kernel, dim3(sample_blocks(batch)), dim3(256), 0, s, ga);
+    GRAFT_LAUNCH_CHECK();
+}
+
+void cutoff_from(uint32_t R, const uint32_t* offsets, const uint32_t* counts, uint32_t batch, uint32_t rays_done,
+                 uint32_t* next_done, uint32_t* result, hipStream_t s)
+{
+    GRAFT_HIP_CHECK(hipMemsetAsync(result, 0, 4 * sizeof(uint32_t), s));
+    if (next_done) GRAFT_HIP_CHECK(hipMemsetAsync(next_done, 0, sizeof(uint32_t), s));
+    if (rays_done >= R) return;
+    const int blocks = (int)std::min<uint32_t>((R - rays_done + 255) / 256, 1024);
+    hipLaunchKernelGGL(cutoff_from_kernel, dim3(blocks), dim3(256), 0, s, R, offsets, counts, batch, rays_done,
+                       next_done, result);
+    GRAFT_LAUNCH_CHECK();
+}
+
+void gather_stored(uint32_t max_samples, const float3* o, const float3* d, const OccGrid& g, const uint32_t* offsets,
+                   uint32_t base, const float* t_scratch, const uint32_t* result, float* t_out, uint32_t* ray_idx,
+                   float4* pos_out, hipStream_t s)
+{
+    if (max_samples == 0) return;
+    GatherArgs ga{o, d, g.aabb_min, g.aabb_max, offsets, base, t_scratch, 0u, result, t_out, ray_idx, pos_out};
+    hipLaunchKernelGGL(gather_samples_kernel, dim3(sample_blocks(max_samples)), dim3(256), 0, s, ga);
+    GRAFT_LAUNCH_CHECK();
+}
+
+void compact_sparse(uint32_t R, const uint32_t* offsets, const uint32_t* result, uint32_t max_samples,
+                    const uint32_t* morton, uint32_t* keys, uint32_t* sparse_idx, hipStream_t s)
+{
+    if (R == 0 || max_samples == 0) return;
+    hipLaunchKernelGGL(compact_sparse_kernel, dim3(sample_blocks(max_samples)), dim3(256), 0, s, R, offsets, result,
+                       morton, keys, sparse_idx);
+    GRAFT_LAUNCH_CHECK();
+}
+
+void sparse_batch(const uint32_t* result, uint32_t max_samples, const uint32_t* sparse_idx, const float* t_sparse,
+                  const float3* o, const float3* d, float3 aabb_min, float3 aabb_max, float4* pos_out,
+                  uint32_t* ray_idx, float* t_out, hipStream_t s)
+{
+    if (max_samples == 0) return;
+    hipLaunchKernelGGL(sparse_batch_kernel, dim3(sample_blocks(max_samples)), dim3(256), 0, s, result, sparse_idx,
+                       t_sparse, o, d, aabb_min, aabb_max, pos_out, ray_idx, t_out);
+    GRAFT_LAUNCH_CHECK();
+}
+
+void sh_degree3(uint32_t n, const float3* dirs, float* out, hipStream_t s)
+{
+    if (n == 0) return;
+    hipLaunchKernelGGL(sh_degree3_kernel, dim3((n + 255) / 256), dim3(256), 0, s, n, dirs,
+                       reinterpret_cast<float4*>(out));
     GRAFT_LAUNCH_CHECK();
 }
 

@@ -22,8 +22,99 @@
 
 #ifdef __cplusplus
 #include <hip/hip_vector_types.h>
+/* the reference's default arguments (C++ callers only) */
+#define GRAFT_DEFAULT(v) = v
 extern "C" {
+#else
+#define GRAFT_DEFAULT(v)
 #endif
+
+/* ---- the hierarchical DDA march and its compactions ----
+ * Every march below is the reference's (march_rays_dda_calc_hits /
+ * march_rays_dda_offset / march_rays_dda_kernel, processRays.cu:96-226,
+ * 626-737, 801-929): the same cells, sample t values and per-ray cap of 1024
+ * samples (MAX_HITS, InstantNerf.h:24), bit for bit.  Positions are written as
+ * float4 (x, y, z, 0) and need 16-byte alignment. */
+
+/* launchMarchRaysDDA (processRays.cu:228-265, declared InstantNerf.h:385-403).
+ * The per-ray layout: sample k of ray i at t_hits_out[i * 1024 + k], the
+ * 30-bit Morton code of its level-0 cell (coordinates mod 1024) at
+ * packed_coords_out[i * 1024 + k] (nullable here), the count at
+ * num_steps_per_ray[i]. */
+void launchMarchRaysDDA(const uint32_t num_rays, const float3* rays_o, const float3* rays_d,
+                        const float3* rays_d_inv, const float* nears, const float* fars,
+                        const uint8_t* occupancy_grid, const uint3 grid_resolution, const float3 aabb_min,
+                        const float3 aabb_max, const int numCascades, const int mipmapLevels,
+                        const int samplesPerVoxel, uint32_t* packed_coords_out, float* t_hits_out,
+                        uint32_t* num_steps_per_ray, hipStream_t stream);
+
+/* processRaysChunk (processRays.cu:357-464, declared InstantNerf.h:405-434).
+ * launchMarchRaysDDA into d_sparse_*, exclusive scan of the counts into
+ * d_ray_offsets, then every sample of every ray compacted (no batch cutoff:
+ * the outputs hold all samples) and stably sorted by Morton code: keys_in /
+ * indices_in hold the ray-major compaction, keys_out / indices_out the sorted
+ * one (index = ray * 1024 + k), and positions, ray indices and t follow the
+ * sorted order.  Blocks the calling thread (one read of the sample count,
+ * and the sort). */
+void processRaysChunk(const uint32_t num_rays, const float3* rays_o, const float3* rays_d,
+                      const float3* rays_d_inv, const float* nears, const float* fars,
+                      const uint8_t* occupancy_grid, const uint3 grid_resolution, const float3 aabb_min,
+                      const float3 aabb_max, const int numCascades, const int mipmapLevels,
+                      const int samplesPerVoxel, uint32_t* d_sparse_morton, float* d_sparse_ts,
+                      uint32_t* d_num_steps, uint32_t* d_ray_offsets, uint32_t* d_dense_morton_keys_in,
+                      uint32_t* d_dense_sparse_indices_in, uint32_t* d_dense_morton_keys_out,
+                      uint32_t* d_dense_sparse_indices_out, float* d_mlp_positions_batch,
+                      uint32_t* d_ray_indices, float* d_t_sorted, hipStream_t stream);
+
+/* processRaysChunkLinear (processRays.cu:551-624, declared InstantNerf.h:436-460):
+ * processRaysChunk without the Morton keys and the sort; the outputs are in
+ * ray-major order.  Blocks the calling thread (one read of the sample count). */
+void processRaysChunkLinear(const uint32_t num_rays, const float3* rays_o, const float3* rays_d,
+                            const float3* rays_d_inv, const float* nears, const float* fars,
+                            const uint8_t* occupancy_grid, const uint3 grid_resolution, const float3 aabb_min,
+                            const float3 aabb_max, const int numCascades, const int mipmapLevels,
+                            const int samplesPerVoxel, float* d_sparse_ts, uint32_t* d_num_steps,
+                            uint32_t* d_ray_offsets, uint32_t* d_dense_sparse_indices,
+                            float* d_mlp_positions_batch, uint32_t* d_ray_indices, float* d_t_sorted,
+                            hipStream_t stream);
+
+/* processRaysHitData (processRays.cu:1042-1081, declared InstantNerf.h:521-539).
+ * Per-ray sample counts into d_num_steps and their exclusive scan (uint32
+ * wrap-around) into d_ray_offsets; asynchronous.  d_block_sums is accepted
+ * for signature compatibility and not used; it may be NULL. */
+void processRaysHitData(const uint32_t num_rays, const float3* rays_o, const float3* rays_d,
+                        const float3* rays_d_inv, const float* nears, const float* fars,
+                        const uint8_t* occupancy_grid, const uint3 grid_resolution, const float3 aabb_min,
+                        const float3 aabb_max, const int numCascades, const int mipmapLevels,
+                        const int samplesPerVoxel, uint32_t* d_num_steps, uint32_t* d_ray_offsets,
+                        uint32_t* d_block_sums, hipStream_t stream);
+
+/* processRaysHitPositions (processRays.cu:1083-1174, declared InstantNerf.h:541-568).
+ * After processRaysHitData on the same rays and grid: the rays from rays_done
+ * whose samples fit in batchSize (find_cutoff_ray_from_kernel, :771-799).
+ * Returns their number B (0 when the first does not fit or no rays are left),
+ * writes rays_done + B to *d_active_rays_count (0 in those cases),
+ * offsets[rays_done] to *out_base and their sample count to *totalHits
+ * (host pointers; *out_base is left alone when B is 0), and fills sample j of
+ * the batch at index d_ray_offsets[rays_done + r] - base + k: t, the
+ * batch-local ray index r, the contracted position.  Blocks the calling thread
+ * for the cutoff; the fill is asynchronous.  d_block_sums is not used. */
+int processRaysHitPositions(const uint32_t num_rays, const float3* rays_o, const float3* rays_d,
+                            const float3* rays_d_inv, const float* nears, const float* fars,
+                            const uint8_t* occupancy_grid, const uint3 grid_resolution, const float3 aabb_min,
+                            const float3 aabb_max, const int numCascades, const int mipmapLevels,
+                            const int samplesPerVoxel, const uint32_t rays_done, const int batchSize,
+                            uint32_t* totalHits, uint32_t* out_base, uint32_t* d_num_steps,
+                            uint32_t* d_ray_offsets, float* d_mlp_positions_batch, uint32_t* d_ray_indices,
+                            uint32_t* d_active_rays_count, float* d_t_sorted, uint32_t* d_block_sums,
+                            hipStream_t stream);
+
+/* launchComputeRealSHDegree3 (otherKernels.cu:66-83, declared InstantNerf.h:491-496).
+ * d_out_sh [total_hits][16] (16-byte aligned): the real spherical harmonics
+ * of degree <= 3 of each direction (taken as given, not normalised), in the
+ * order and sign convention of the colour head's input. */
+void launchComputeRealSHDegree3(const uint32_t total_hits, const float3* d_directions, float* d_out_sh,
+                                hipStream_t stream GRAFT_DEFAULT(0));
 
 /* processRays.cu:931-1040 (declared InstantNerf.h:509-533).  Count pass,
  * exclusive scan and cutoff at batchSize, fill pass; returns the number of
@@ -52,8 +143,10 @@ void launchVolumeRendering(const uint32_t num_rays, const uint32_t* d_ray_offset
                            const float* d_t_sorted, const float* d_density_sigma, const float* d_depth_chunk,
                            const float* d_sigma_chunk, const float* d_rgb_output, const float* d_rgb_true,
                            float* d_render_rgb, float* d_render_depth, float* d_phi_out, float* d_dw_out,
-                           float* d_weight_sum, float lambda_dist, float lambda_depth, float3 bg_color,
-                           uint32_t base, uint32_t raysDone, hipStream_t stream);
+                           float* d_weight_sum, float lambda_dist, float lambda_depth,
+                           float3 bg_color GRAFT_DEFAULT(make_float3(1.0f, 1.0f, 1.0f)),
+                           uint32_t base GRAFT_DEFAULT(0), uint32_t raysDone GRAFT_DEFAULT(0),
+                           hipStream_t stream GRAFT_DEFAULT(0));
 
 /* fetchRayChunkStreamingKernel (DataLoader.cu:548-661) as launched by
  * DataLoader::fetchRayChunk (:663-679): size rays from offset (randomize = 0)
@@ -132,4 +225,5 @@ void nerf_abi_echo_vec(float3 a, uint3 b, float* out);
 #ifdef __cplusplus
 }
 #endif
+#undef GRAFT_DEFAULT
 #endif

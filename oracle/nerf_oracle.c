@@ -135,12 +135,29 @@ void orc_ray_aabb_inv(uint32_t R, const float* O, const float* D, const float* m
     }
 }
 
-/* ---- the hierarchical DDA of march_rays_dda_calc_hits / _offset ----------
- * processRays.cu:626-737 (count) and 801-929 (fill).  fill = 0 counts only. */
+/* expand_bits_3d / morton3d (processRays.cu:71-82): bit b of x, y, z to bits
+ * 3b, 3b+1, 3b+2 of the result, coordinates taken mod 2^10. */
+uint32_t orc_morton30(uint32_t x, uint32_t y, uint32_t z)
+{
+    uint32_t m = 0;
+    for (int b = 0; b < 10; b++) {
+        m |= ((x >> b) & 1u) << (3 * b);
+        m |= ((y >> b) & 1u) << (3 * b + 1);
+        m |= ((z >> b) & 1u) << (3 * b + 2);
+    }
+    return m;
+}
+
+/* ---- the hierarchical DDA of march_rays_dda_calc_hits / _offset / _kernel -
+ * processRays.cu:626-737 (count), 801-929 (fill) and 96-226 (per-ray
+ * layout).  fill = 0 counts only; fill = 1 writes sample `hit` at
+ * out_base + hit (t, ray index i, contracted position); fill = 2 writes it at
+ * i * ORC_MAX_HITS + hit (t, and the Morton code of its level-0 cell when
+ * morton is set). */
 static uint32_t march_one(uint32_t i, const float* O, const float* D, const float* DI, float t_min,
                           float t_max, const uint8_t* bits, const uint32_t* res, const float* mn,
                           const float* mx, int C, int L, int K, int fill, uint32_t out_base,
-                          float* t_out, uint32_t* ridx, float* pos_out)
+                          float* t_out, uint32_t* ridx, float* pos_out, uint32_t* morton)
 {
     const float* o = O + 3 * i;
     const float* d = D + 3 * i;
@@ -193,6 +210,13 @@ static uint32_t march_one(uint32_t i, const float* O, const float* D, const floa
                 for (int k = 0; k < K; ++k) {
                     if (hit >= ORC_MAX_HITS) break;
                     const float tk = t + ((float)k + 0.5f) / (float)K * span;
+                    if (fill == 2) {
+                        const size_t w = (size_t)i * ORC_MAX_HITS + hit;
+                        t_out[w] = tk;
+                        if (morton) morton[w] = orc_morton30((uint32_t)vi[0], (uint32_t)vi[1], (uint32_t)vi[2]);
+                        hit++;
+                        continue;
+                    }
                     const uint32_t w = out_base + hit;
                     t_out[w] = tk;
                     ridx[w] = i;
@@ -226,7 +250,7 @@ void orc_march_count(uint32_t R, const float* O, const float* D, const float* DI
 #pragma omp parallel for schedule(dynamic, 256)
     for (long long i = 0; i < (long long)R; i++)
         counts[i] = march_one((uint32_t)i, O, D, DI, nears[i], fars[i], bits, res, mn, mx, C, L, K, 0, 0,
-                              NULL, NULL, NULL);
+                              NULL, NULL, NULL, NULL);
 }
 
 uint32_t orc_march_hits(uint32_t R, const float* O, const float* D, const float* DI, const float* nears,
@@ -256,8 +280,48 @@ uint32_t orc_march_hits(uint32_t R, const float* O, const float* D, const float*
 #pragma omp parallel for schedule(dynamic, 256)
     for (long long i = 0; i < (long long)active; i++)
         march_one((uint32_t)i, O, D, DI, nears[i], fars[i], bits, res, mn, mx, C, L, K, 1, offsets[i], t_out,
-                  ridx, pos_out);
+                  ridx, pos_out, NULL);
     return active;
+}
+
+void orc_march_fill(uint32_t R, const float* O, const float* D, const float* DI, const float* nears,
+                    const float* fars, const uint8_t* bits, const uint32_t* res, const float* mn,
+                    const float* mx, int C, int L, int K, const uint32_t* out_base, float* t_out,
+                    uint32_t* ridx, float* pos_out)
+{
+#pragma omp parallel for schedule(dynamic, 256)
+    for (long long i = 0; i < (long long)R; i++)
+        march_one((uint32_t)i, O, D, DI, nears[i], fars[i], bits, res, mn, mx, C, L, K, 1, out_base[i], t_out,
+                  ridx, pos_out, NULL);
+}
+
+void orc_sparse_batch(uint32_t N, const uint32_t* sparse_idx, const float* t_sparse, const float* O,
+                      const float* D, const float* mn, const float* mx, float* pos_out, uint32_t* ridx,
+                      float* t_out)
+{
+#pragma omp parallel for schedule(static)
+    for (long long j = 0; j < (long long)N; j++) {
+        const uint32_t idx = sparse_idx[j];
+        const uint32_t ray = idx / ORC_MAX_HITS;
+        const float t = t_sparse[idx];
+        float q[3], cq[3];
+        for (int a = 0; a < 3; a++) q[a] = O[3 * (size_t)ray + a] + t * D[3 * (size_t)ray + a];
+        orc_contract_pos(q, mn, mx, cq);
+        for (int a = 0; a < 3; a++) pos_out[4 * (size_t)j + a] = cq[a];
+        pos_out[4 * (size_t)j + 3] = 0.0f;
+        ridx[j] = ray;
+        t_out[j] = t;
+    }
+}
+
+void orc_march_sparse(uint32_t R, const float* O, const float* D, const float* DI, const float* nears,
+                      const float* fars, const uint8_t* bits, const uint32_t* res, const float* mn,
+                      const float* mx, int C, int L, int K, uint32_t* counts, float* t_sparse, uint32_t* morton)
+{
+#pragma omp parallel for schedule(dynamic, 256)
+    for (long long i = 0; i < (long long)R; i++)
+        counts[i] = march_one((uint32_t)i, O, D, DI, nears[i], fars[i], bits, res, mn, mx, C, L, K, 2, 0, t_sparse,
+                              NULL, NULL, morton);
 }
 
 /* ---- compute_SH_gather (otherKernels.cu:156-273) -------------------------- */
@@ -267,31 +331,44 @@ static float sanitize_logit(float v)
     return (v != v) ? 0.0f : v;
 }
 
+/* The 16 real SH of compute_SH_gather and compute_real_sh_degree_3_kernel
+ * (otherKernels.cu:24-51, 182-200; one expression list in both). */
+static void sh16(const float* d, float* sh)
+{
+    const float x = d[0], y = d[1], z = d[2];
+    const float x2 = x * x, y2 = y * y, z2 = z * z;
+    sh[0] = 0.28209479f;
+    sh[1] = -0.48860251f * y;
+    sh[2] = 0.48860251f * z;
+    sh[3] = -0.48860251f * x;
+    sh[4] = 1.09254843f * x * y;
+    sh[5] = -1.09254843f * y * z;
+    sh[6] = 0.31539156f * (3.0f * z2 - 1.0f);
+    sh[7] = -1.09254843f * x * z;
+    sh[8] = 0.54627421f * (x2 - y2);
+    sh[9] = -0.59004359f * y * (3.0f * x2 - y2);
+    sh[10] = 2.89061144f * x * y * z;
+    sh[11] = -0.45704580f * y * (5.0f * z2 - 1.0f);
+    sh[12] = 0.37317633f * z * (5.0f * z2 - 3.0f);
+    sh[13] = -0.45704580f * x * (5.0f * z2 - 1.0f);
+    sh[14] = 1.44530572f * z * (x2 - y2);
+    sh[15] = -0.59004359f * x * (x2 - 3.0f * y2);
+}
+
+/* compute_real_sh_degree_3_kernel (otherKernels.cu:18-64): out [N][16]. */
+void orc_sh_degree3(uint32_t N, const float* dirs, float* out)
+{
+#pragma omp parallel for schedule(static)
+    for (long long n = 0; n < (long long)N; n++) sh16(dirs + 3 * (size_t)n, out + 16 * (size_t)n);
+}
+
 void orc_sh_gather(uint32_t N, const float* dirs, const uint32_t* ray_idx, float bias, const float* dout,
                    uint16_t* color_in, float* sigma)
 {
 #pragma omp parallel for schedule(static)
     for (long long n = 0; n < (long long)N; n++) {
-        const float* d = dirs + 3 * (size_t)ray_idx[n];
-        const float x = d[0], y = d[1], z = d[2];
-        const float x2 = x * x, y2 = y * y, z2 = z * z;
         float sh[16];
-        sh[0] = 0.28209479f;
-        sh[1] = -0.48860251f * y;
-        sh[2] = 0.48860251f * z;
-        sh[3] = -0.48860251f * x;
-        sh[4] = 1.09254843f * x * y;
-        sh[5] = -1.09254843f * y * z;
-        sh[6] = 0.31539156f * (3.0f * z2 - 1.0f);
-        sh[7] = -1.09254843f * x * z;
-        sh[8] = 0.54627421f * (x2 - y2);
-        sh[9] = -0.59004359f * y * (3.0f * x2 - y2);
-        sh[10] = 2.89061144f * x * y * z;
-        sh[11] = -0.45704580f * y * (5.0f * z2 - 1.0f);
-        sh[12] = 0.37317633f * z * (5.0f * z2 - 3.0f);
-        sh[13] = -0.45704580f * x * (5.0f * z2 - 1.0f);
-        sh[14] = 1.44530572f * z * (x2 - y2);
-        sh[15] = -0.59004359f * x * (x2 - 3.0f * y2);
+        sh16(dirs + 3 * (size_t)ray_idx[n], sh);
         float lg[16];
         for (int k = 0; k < 16; k++) lg[k] = sanitize_logit(dout[16 * (size_t)n + k]);
         sigma[n] = orc_expf(fminf(lg[0] - bias, 8.0f));

@@ -66,6 +66,40 @@ uint32_t orc_march_hits(uint32_t R, const float* rays_o, const float* rays_d, co
                         uint32_t* counts, uint32_t* offsets, uint32_t* total_hits,
                         float* t_out, uint32_t* ray_idx_out, float* pos_out);
 
+/* processRaysHitPositions' fill (march_rays_dda_offset, processRays.cu:801-929,
+ * called at :1150-1170 on the batch's rays): ray i of the R given (pointers
+ * already offset to the batch's first ray) writes its samples at
+ * out_base[i] + k with the ray index i (batch-local). */
+void orc_march_fill(uint32_t R, const float* rays_o, const float* rays_d, const float* d_inv,
+                    const float* nears, const float* fars, const uint8_t* bits,
+                    const uint32_t* res3, const float* aabb_min, const float* aabb_max,
+                    int num_cascades, int mip_levels, int K, const uint32_t* out_base, float* t_out,
+                    uint32_t* ray_idx_out, float* pos_out);
+
+/* march_rays_dda_kernel (processRays.cu:96-226): the per-ray layout, sample k
+ * of ray i at t_sparse[i * ORC_MAX_HITS + k] and, when morton is set, the
+ * Morton code of its level-0 cell at morton[i * ORC_MAX_HITS + k]; counts [R]. */
+void orc_march_sparse(uint32_t R, const float* rays_o, const float* rays_d, const float* d_inv,
+                      const float* nears, const float* fars, const uint8_t* bits,
+                      const uint32_t* res3, const float* aabb_min, const float* aabb_max,
+                      int num_cascades, int mip_levels, int K, uint32_t* counts, float* t_sparse,
+                      uint32_t* morton);
+
+/* generate_mlp_batch_kernel (processRays.cu:320-356): sample j is sparse
+ * sample sparse_idx[j] of ray sparse_idx[j] / ORC_MAX_HITS: its contracted
+ * position (float4, w = 0), ray index and t. */
+void orc_sparse_batch(uint32_t N, const uint32_t* sparse_idx, const float* t_sparse, const float* rays_o,
+                      const float* rays_d, const float* aabb_min, const float* aabb_max, float* pos_out,
+                      uint32_t* ray_idx_out, float* t_out);
+
+/* morton3d / expand_bits_3d (processRays.cu:71-82): 30-bit interleave of the
+ * low 10 bits of x (bit 3b), y (3b + 1), z (3b + 2). */
+uint32_t orc_morton30(uint32_t x, uint32_t y, uint32_t z);
+
+/* compute_real_sh_degree_3_kernel (otherKernels.cu:18-64): out [N][16], the
+ * basis of compute_SH_gather below at each direction as given. */
+void orc_sh_degree3(uint32_t N, const float* dirs, float* out);
+
 /* compute_SH_gather (otherKernels.cu:156-273): color input fp16 [N][32] =
  * [16 sanitised density logits | 16 real SH (degree <= 3) of the ray direction],
  * sigma [N] = exp(min(logit0 - bias, 8)). */

@@ -67,6 +67,13 @@ def lib():
             "orc_march_hits": (C.c_uint32, [C.c_uint32, _f32p, _f32p, _f32p, _f32p, _f32p, _u8p, _u32p, _f32p,
                                             _f32p, i, i, i, C.c_uint32, _u32p, _u32p, C.POINTER(C.c_uint32),
                                             _f32p, _u32p, _f32p]),
+            "orc_march_fill": (None, [C.c_uint32, _f32p, _f32p, _f32p, _f32p, _f32p, _u8p, _u32p, _f32p,
+                                      _f32p, i, i, i, _u32p, _f32p, _u32p, _f32p]),
+            "orc_march_sparse": (None, [C.c_uint32, _f32p, _f32p, _f32p, _f32p, _f32p, _u8p, _u32p, _f32p,
+                                        _f32p, i, i, i, _u32p, _f32p, C.c_void_p]),
+            "orc_morton30": (C.c_uint32, [C.c_uint32, C.c_uint32, C.c_uint32]),
+            "orc_sparse_batch": (None, [C.c_uint32, _u32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _u32p, _f32p]),
+            "orc_sh_degree3": (None, [C.c_uint32, _f32p, _f32p]),
             "orc_sh_gather": (None, [C.c_uint32, _f32p, _u32p, f, _f32p, _u16p, _f32p]),
             "orc_composite_distortion": (None, [C.c_uint32, _u32p, _u32p, _f32p, _f32p, C.c_void_p, C.c_void_p,
                                                 _f32p, C.c_void_p, _f32p, _f32p, C.c_void_p, _f32p, _f32p, f, f,
@@ -302,6 +309,113 @@ def march_hits(o, d, di, nears, fars, bits, res, aabb_min, aabb_max, cascades, L
     n = tot.value
     return dict(active=int(act), total=int(n), counts=cnt, offsets=off, t=t[:n], ray_idx=ri[:n],
                 pos=pos.reshape(-1, 4)[:n])
+
+
+def exclusive_scan_u32(counts):
+    """custom_exclusive_sum (processRays.cu:486-549): exclusive prefix sums, uint32 wrap-around."""
+    c = np.ascontiguousarray(counts, np.uint32)
+    out = np.zeros_like(c)
+    if c.size > 1:
+        out[1:] = np.cumsum(c[:-1], dtype=np.uint64).astype(np.uint32)
+    return out
+
+
+def hit_data(o, d, di, nears, fars, bits, res, aabb_min, aabb_max, cascades, L, K):
+    """processRaysHitData (processRays.cu:1042-1081) -> (counts, offsets) over all rays."""
+    cnt = march_count(o, d, di, nears, fars, bits, res, aabb_min, aabb_max, cascades, L, K)
+    return cnt, exclusive_scan_u32(cnt)
+
+
+def hit_positions(o, d, di, nears, fars, bits, res, aabb_min, aabb_max, cascades, L, K, counts, offsets,
+                  rays_done, batch):
+    """processRaysHitPositions (processRays.cu:1083-1174) after hit_data.
+
+    -> dict(rays, next_done, total, base, t, ray_idx (batch-local), pos [total, 4]); rays = 0 (and
+    base None) when the first ray from rays_done does not fit or no rays are left.  The cutoff is
+    find_cutoff_ray_from_kernel (:771-799): the boundary ray i >= rays_done is the one whose inclusive
+    sample count past base fits and whose successor's does not (or that is the last ray)."""
+    R = int(np.asarray(counts).size)
+    rd = int(rays_done)
+    counts = np.ascontiguousarray(counts, np.uint32)
+    offsets = np.ascontiguousarray(offsets, np.uint32)
+    empty = dict(rays=0, next_done=0, total=0, base=None, t=np.zeros(0, np.float32),
+                 ray_idx=np.zeros(0, np.uint32), pos=np.zeros((0, 4), np.float32))
+    if rd >= R:
+        return empty
+    base = offsets[rd]
+    incl = (offsets[rd:] + counts[rd:] - base).astype(np.uint32)   # uint32 arithmetic, as on the device
+    fits = incl <= np.uint32(batch)
+    nxt = np.append(~fits[1:], True)      # successor does not fit, or i is the last ray
+    bnd = np.nonzero(fits & nxt)[0]
+    if bnd.size == 0:
+        return empty
+    nb = int(bnd.max()) + 1                # batch rays
+    total = int(incl[nb - 1])
+    sl = slice(rd, rd + nb)
+    t = np.zeros(max(total, 1), np.float32)
+    ri = np.zeros(max(total, 1), np.uint32)
+    pos = np.zeros(4 * max(total, 1), np.float32)
+    ob = (offsets[sl] - base).astype(np.uint32)
+    lib().orc_march_fill(nb, _f3(np.asarray(o)[sl]), _f3(np.asarray(d)[sl]), _f3(np.asarray(di)[sl]),
+                         _f3(np.asarray(nears)[sl]), _f3(np.asarray(fars)[sl]), np.ascontiguousarray(bits, np.uint8),
+                         np.ascontiguousarray(res, np.uint32), _f3(aabb_min), _f3(aabb_max), int(cascades), int(L),
+                         int(K), ob, t, ri, pos)
+    return dict(rays=nb, next_done=rd + nb, total=total, base=int(base), t=t[:total], ray_idx=ri[:total],
+                pos=pos.reshape(-1, 4)[:total])
+
+
+def march_sparse(o, d, di, nears, fars, bits, res, aabb_min, aabb_max, cascades, L, K, morton=True):
+    """launchMarchRaysDDA (processRays.cu:96-265) -> (counts [R], t [R, 1024], morton [R, 1024] or None);
+    entries past a ray's count are zero."""
+    R = _f3(o).size // 3
+    cnt = np.zeros(R, np.uint32)
+    t = np.zeros(R * MAX_HITS, np.float32)
+    m = np.zeros(R * MAX_HITS, np.uint32) if morton else None
+    lib().orc_march_sparse(R, _f3(o), _f3(d), _f3(di), _f3(nears), _f3(fars), np.ascontiguousarray(bits, np.uint8),
+                           np.ascontiguousarray(res, np.uint32), _f3(aabb_min), _f3(aabb_max), int(cascades),
+                           int(L), int(K), cnt, t, None if m is None else m.ctypes.data_as(C.c_void_p))
+    return cnt, t.reshape(R, MAX_HITS), None if m is None else m.reshape(R, MAX_HITS)
+
+
+def morton30(x, y, z):
+    return int(lib().orc_morton30(int(x), int(y), int(z)))
+
+
+def process_chunk(o, d, di, nears, fars, bits, res, aabb_min, aabb_max, cascades, L, K, sort=True):
+    """processRaysChunk (sort, processRays.cu:357-464) / processRaysChunkLinear (:551-624).
+
+    -> dict(counts, offsets, t_sparse, morton, dense_idx (ray-major, ray * 1024 + k), keys_in,
+    sorted_idx, keys_out, pos [N, 4], ray_idx, t): every sample of every ray, in ray-major order, or
+    stably sorted by Morton code (cub::DeviceRadixSort::SortPairs over 32 bits) when sort."""
+    cnt, ts, mor = march_sparse(o, d, di, nears, fars, bits, res, aabb_min, aabb_max, cascades, L, K, morton=sort)
+    off = exclusive_scan_u32(cnt)
+    rows = np.repeat(np.arange(cnt.size, dtype=np.uint64), cnt.astype(np.int64))
+    ks = np.arange(rows.size, dtype=np.uint64) - np.repeat(off.astype(np.uint64), cnt.astype(np.int64))
+    dense = (rows * MAX_HITS + ks).astype(np.uint32)
+    out = dict(counts=cnt, offsets=off, t_sparse=ts, morton=mor, dense_idx=dense)
+    order = dense
+    if sort:
+        keys = mor.reshape(-1)[dense]
+        perm = np.argsort(keys, kind="stable")
+        out.update(keys_in=keys, keys_out=keys[perm], sorted_idx=dense[perm])
+        order = dense[perm]
+    N = int(order.size)
+    pos = np.zeros(4 * max(N, 1), np.float32)
+    ray = np.zeros(max(N, 1), np.uint32)
+    t = np.zeros(max(N, 1), np.float32)
+    lib().orc_sparse_batch(N, np.ascontiguousarray(order, np.uint32), np.ascontiguousarray(ts.reshape(-1)), _f3(o),
+                           _f3(d), _f3(aabb_min), _f3(aabb_max), pos, ray, t)
+    out.update(pos=pos.reshape(-1, 4)[:N], ray_idx=ray[:N], t=t[:N])
+    return out
+
+
+def sh_degree3(dirs):
+    """compute_real_sh_degree_3_kernel (otherKernels.cu:18-64) -> [N, 16]."""
+    dd = _f3(dirs)
+    N = dd.size // 3
+    out = np.zeros(16 * max(N, 1), np.float32)
+    lib().orc_sh_degree3(N, dd, out)
+    return out[:16 * N].reshape(N, 16)
 
 
 def sh_gather(dirs, ray_idx, density_out, bias=0.0):

@@ -45,6 +45,26 @@ def test_reference_launchers_present():
               "launchNetworkFusionHashTableBackwardKernel", "launchNetworkFusionScatterBackwardKernel",
               "launchHashTableBackwardKernel", "launchAdamHashGridOptim"]:
         assert n in names
+    # the extern "C" launchers of modules/NeRF/InstantNerf.h:385-568
+    names = declared_c_functions(os.path.join(INCLUDE, "nerf_abi.h"))
+    for n in ["launchMarchRaysDDA", "processRaysChunk", "processRaysChunkLinear", "processRaysHitLinear",
+              "launchComputeRealSHDegree3", "launchVolumeRendering", "processRaysHitData", "processRaysHitPositions"]:
+        assert n in names
+
+
+def test_launcher_argument_errors_without_gpu():
+    """Argument errors of the march / SH launchers are reported before any device call."""
+    P = pkg()
+    L = P.lib()
+    L.launchComputeRealSHDegree3(4, 16, 20, None)     # output not 16-byte aligned
+    assert L.tinymlp_last_error() != 0 and b"aligned" in L.tinymlp_last_error_message()
+    L.launchComputeRealSHDegree3(0, None, None, None)  # nothing to do
+    assert L.tinymlp_last_error() == 0
+    args = [None] * 6 + [P.Uint3(16, 16, 16), P.Float3(-1, -1, -1), P.Float3(1, 1, 1), 1, 1, 1]
+    L.processRaysHitPositions(8, *args, 0, 64, None, None, None, None, None, None, None, None, None, None)
+    assert L.tinymlp_last_error() != 0 and b"NULL" in L.tinymlp_last_error_message()
+    L.processRaysChunk(8, *args, None, None, None, None, None, None, None, None, None, None, None, None)
+    assert L.tinymlp_last_error() != 0 and b"NULL" in L.tinymlp_last_error_message()
 
 
 def test_python_bindings_cover_the_headers():

@@ -219,6 +219,141 @@ def test_march_k_subsamples_and_contraction():
         assert r["pos"][j, 3] == 0.0
 
 
+def _deinterleave(m):
+    """Inverse of the 30-bit Morton interleave, bit by bit."""
+    x = y = z = 0
+    for b in range(10):
+        x |= ((m >> (3 * b)) & 1) << b
+        y |= ((m >> (3 * b + 1)) & 1) << b
+        z |= ((m >> (3 * b + 2)) & 1) << b
+    return x, y, z
+
+
+def test_morton30_known_values_and_inverse():
+    assert orc.morton30(0, 0, 0) == 0
+    assert (orc.morton30(1, 0, 0), orc.morton30(0, 1, 0), orc.morton30(0, 0, 1)) == (1, 2, 4)
+    assert orc.morton30(2, 0, 0) == 8 and orc.morton30(3, 3, 3) == 63
+    assert orc.morton30(1023, 1023, 1023) == (1 << 30) - 1
+    assert orc.morton30(1024 + 5, 2048 + 6, 7) == orc.morton30(5, 6, 7)   # coordinates mod 2^10
+    rng = np.random.default_rng(0)
+    for x, y, z in rng.integers(0, 1 << 12, (200, 3)):
+        assert _deinterleave(orc.morton30(x, y, z)) == (x & 1023, y & 1023, z & 1023)
+    # order: the code of the cell z-major sub-cube precedes every cell of the next one
+    assert orc.morton30(1, 1, 1) < orc.morton30(0, 0, 2) < orc.morton30(1, 1, 3)
+
+
+def _march_scene(R=1500, res=32, C=3, L=4, p=0.2, seed=5):
+    bits, per = small_grid(res, C, L, p=p, seed=seed)
+    rng = np.random.default_rng(seed + 1)
+    o = rng.uniform(-2, 2, (R, 3)).astype(np.float32)
+    d = rng.normal(size=(R, 3)).astype(np.float32)
+    d /= np.linalg.norm(d, axis=1, keepdims=True)
+    di, nr, fr = orc.ray_aabb_inv(o, d, AABB_MIN, AABB_MAX, C)
+    return dict(o=o, d=d, di=di, nr=nr, fr=fr, bits=bits, per=per, res=res, C=C, L=L)
+
+
+def _margs(sc, K):
+    return (sc["o"], sc["d"], sc["di"], sc["nr"], sc["fr"], sc["bits"], [sc["res"]] * 3, AABB_MIN, AABB_MAX,
+            sc["C"], sc["L"], K)
+
+
+def test_march_sparse_layout_equals_the_compacted_march_and_codes_its_cells():
+    sc = _march_scene()
+    K = 2
+    full = orc.march_hits(*_margs(sc, K), 1 << 30)
+    cnt, ts, mor = orc.march_sparse(*_margs(sc, K))
+    np.testing.assert_array_equal(cnt, full["counts"])
+    R = cnt.size
+    for i in range(R):
+        a, n = int(full["offsets"][i]), int(cnt[i])
+        np.testing.assert_array_equal(ts[i, :n], full["t"][a:a + n])
+        assert not ts[i, n:].any() and not mor[i, n:].any()
+    # each sample's code is the level-0 cell holding it (fp64 position; on a
+    # face, either side), and that cell is occupied
+    res, C, per = sc["res"], sc["C"], sc["per"]
+    total = 0
+    for i in range(0, R, 7):
+        for k in range(int(cnt[i])):
+            x, y, z = _deinterleave(int(mor[i, k]))
+            c, _, _, _ = occupied_cell_of(sc["o"][i], sc["d"][i], float(ts[i, k]), per, res, C)
+            p = sc["o"][i].astype(np.float64) + float(ts[i, k]) * sc["d"][i].astype(np.float64)
+            f = [(p[a] + 1.5 * 2 ** c) / (3.0 * 2 ** c) * res for a in range(3)]
+            for a, v in enumerate((x, y, z)):
+                w = min(max(math.floor(f[a]), 0), res - 1)
+                assert v == w or (abs(v - w) == 1 and abs(f[a] - round(f[a])) < 1e-5), (i, k)
+            assert per[c][z, y, x]
+            total += 1
+    assert total > 1000
+    # counts only
+    cnt2, ts2, none = orc.march_sparse(*_margs(sc, K), morton=False)
+    assert none is None
+    np.testing.assert_array_equal(cnt2, cnt)
+    np.testing.assert_array_equal(ts2, ts)
+
+
+def test_process_chunk_linear_and_sorted():
+    sc = _march_scene(R=800)
+    K = 1
+    full = orc.march_hits(*_margs(sc, K), 1 << 30)
+    lin = orc.process_chunk(*_margs(sc, K), sort=False)
+    np.testing.assert_array_equal(lin["offsets"], full["offsets"])
+    np.testing.assert_array_equal(lin["t"], full["t"])
+    np.testing.assert_array_equal(lin["ray_idx"], full["ray_idx"])
+    np.testing.assert_array_equal(lin["pos"], full["pos"])
+    np.testing.assert_array_equal(lin["dense_idx"] // 1024, full["ray_idx"])
+    srt = orc.process_chunk(*_margs(sc, K), sort=True)
+    keys, idx = srt["keys_out"], srt["sorted_idx"]
+    assert (np.diff(keys.astype(np.int64)) >= 0).all()
+    np.testing.assert_array_equal(np.sort(idx), lin["dense_idx"])
+    # stable: equal keys keep the ray-major order
+    same = keys[1:] == keys[:-1]
+    assert same.any() and (idx[1:][same] > idx[:-1][same]).all()
+    np.testing.assert_array_equal(srt["keys_in"], srt["morton"].reshape(-1)[lin["dense_idx"]])
+    # the sorted batch is the linear batch permuted
+    perm = np.searchsorted(lin["dense_idx"], idx)
+    np.testing.assert_array_equal(srt["t"], lin["t"][perm])
+    np.testing.assert_array_equal(srt["pos"], lin["pos"][perm])
+    np.testing.assert_array_equal(srt["ray_idx"], lin["ray_idx"][perm])
+
+
+def test_hit_positions_batches_tile_the_full_march():
+    sc = _march_scene(R=1200)
+    K = 2
+    full = orc.march_hits(*_margs(sc, K), 1 << 30)
+    cnt, off = orc.hit_data(*_margs(sc, K))
+    np.testing.assert_array_equal(cnt, full["counts"])
+    np.testing.assert_array_equal(off, full["offsets"])
+    batch = int(cnt.max()) * 5 + 3
+    done, pieces, nb = 0, [], 0
+    while done < cnt.size:
+        r = orc.hit_positions(*_margs(sc, K), cnt, off, done, batch)
+        assert r["rays"] > 0 and r["next_done"] == done + r["rays"] and r["base"] == off[done]
+        assert r["total"] <= batch
+        if r["next_done"] < cnt.size:   # the next ray would not fit
+            assert r["total"] + int(cnt[r["next_done"]]) > batch
+        if done == 0:   # the first batch is processRaysHitLinear's
+            first = orc.march_hits(*_margs(sc, K), batch)
+            assert first["active"] == r["rays"] and first["total"] == r["total"]
+            np.testing.assert_array_equal(first["t"], r["t"])
+            np.testing.assert_array_equal(first["pos"], r["pos"])
+        pieces.append((done, r))
+        done = r["next_done"]
+        nb += 1
+    assert nb > 5
+    t = np.concatenate([r["t"] for _, r in pieces])
+    pos = np.concatenate([r["pos"] for _, r in pieces])
+    ridx = np.concatenate([r["ray_idx"].astype(np.int64) + d0 for d0, r in pieces])
+    np.testing.assert_array_equal(t, full["t"])
+    np.testing.assert_array_equal(pos, full["pos"])
+    np.testing.assert_array_equal(ridx, full["ray_idx"].astype(np.int64))
+    # the first ray from rays_done does not fit; no rays left
+    i0 = int(np.argmax(cnt > 0))
+    z = orc.hit_positions(*_margs(sc, K), cnt, off, i0, int(cnt[i0]) - 1)
+    assert z["rays"] == 0 and z["total"] == 0 and z["base"] is None
+    z = orc.hit_positions(*_margs(sc, K), cnt, off, cnt.size, batch)
+    assert z["rays"] == 0 and z["total"] == 0
+
+
 # --------------------------------------------------------------------------- bitfield
 
 
@@ -309,6 +444,24 @@ def test_sh_gather_matches_textbook_real_sh_and_sanitises():
     assert sig[1] == orc.expf(np.float32([8.0]))[0]
     arg = np.minimum(logits[2:, 0] - np.float32(0.5), np.float32(8)).astype(np.float64)
     np.testing.assert_allclose(sig[2:], np.exp(arg), rtol=2e-7)
+
+
+def test_sh_degree3_matches_textbook_real_sh_and_the_gather_basis():
+    rng = np.random.default_rng(11)
+    d = rng.normal(size=(400, 3))
+    d /= np.linalg.norm(d, axis=1, keepdims=True)
+    d32 = d.astype(np.float32)
+    got = orc.sh_degree3(d32)
+    assert got.shape == (400, 16) and got.dtype == np.float32
+    np.testing.assert_allclose(got, real_sh_scipy(d32.astype(np.float64)), atol=2e-6)
+    # the colour head's input basis (compute_SH_gather) is the same basis, in fp16
+    cin, _ = orc.sh_gather(d32, np.arange(400, dtype=np.uint32), np.zeros((400, 16), np.float32))
+    np.testing.assert_array_equal(cin[:, 16:], got.astype(np.float16))
+    # directions are taken as given: a scaled direction scales each degree-l term by s^l (l <= 1 exact)
+    g2 = orc.sh_degree3(2 * d32[:4])
+    np.testing.assert_array_equal(g2[:, 0], got[:4, 0])
+    np.testing.assert_allclose(g2[:, 1:4], 2 * got[:4, 1:4], rtol=1e-6)
+    assert orc.sh_degree3(np.zeros((0, 3), np.float32)).shape == (0, 16)
 
 
 # --------------------------------------------------------------------------- compositing + distortion
