@@ -79,9 +79,28 @@ __device__ __forceinline__ uint32_t dense_index(int cx, int cy, int cz, int N_l)
     return (uint32_t)(cx + cy * (N_l + 1) + cz * (N_l + 1) * (N_l + 1));
 }
 
-// Library-owned device workspace (grown on demand, never shrunk).  One per
-// process; the API is single-stream like the reference.
-void* workspace(size_t bytes);
+// Device scratch of one owner (an MLP instance, or one stream of the
+// extern "C" launchers): grown on demand, never shrunk, freed with the owner.
+// Kernels of one owner run in stream order, so they never share it with
+// another owner's work in flight.  Growing frees the old buffer with
+// hipFree, which waits for the device first.
+class Workspace {
+public:
+    Workspace() = default;
+    ~Workspace();
+    Workspace(const Workspace&) = delete;
+    Workspace& operator=(const Workspace&) = delete;
+    void* get(size_t bytes);
+    size_t size() const { return bytes_; }
+
+private:
+    void* p_ = nullptr;
+    size_t bytes_ = 0;
+};
+
+// The workspace of (current device, stream), for callers without an owner of
+// their own (the extern "C" launchers); kept until the process ends.
+Workspace& stream_workspace(hipStream_t s);
 
 int num_cus();
 

@@ -14,6 +14,8 @@
 
 #include <algorithm>
 #include <cmath>
+#include <map>
+#include <memory>
 #include <mutex>
 
 namespace graft {
@@ -257,8 +259,6 @@ void hash_scatter_atomic(const GridMeta& m, const __half* denc, const float* pos
 
 namespace {
 std::mutex g_ws_mu;
-void* g_ws = nullptr;
-size_t g_ws_bytes = 0;
 int g_cus = 0;
 int g_lds = 0;
 }  // namespace
@@ -276,17 +276,34 @@ int max_lds_per_block()
     return g_lds;
 }
 
-void* workspace(size_t bytes)
+Workspace::~Workspace()
 {
-    std::lock_guard<std::mutex> lk(g_ws_mu);
-    if (bytes > g_ws_bytes) {
-        if (g_ws) GRAFT_HIP_CHECK(hipFree(g_ws));
-        g_ws = nullptr;
-        size_t nb = std::max(bytes, (size_t)1 << 20);
-        GRAFT_HIP_CHECK(hipMalloc(&g_ws, nb));
-        g_ws_bytes = nb;
+    if (p_) (void)hipFree(p_);
+}
+
+void* Workspace::get(size_t bytes)
+{
+    if (bytes > bytes_) {
+        if (p_) GRAFT_HIP_CHECK(hipFree(p_));
+        p_ = nullptr;
+        bytes_ = 0;
+        const size_t nb = std::max(bytes, (size_t)1 << 16);
+        GRAFT_HIP_CHECK(hipMalloc(&p_, nb));
+        bytes_ = nb;
     }
-    return g_ws;
+    return p_;
+}
+
+Workspace& stream_workspace(hipStream_t s)
+{
+    int dev = 0;
+    GRAFT_HIP_CHECK(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    static std::map<std::pair<int, hipStream_t>, std::unique_ptr<Workspace>>* cache =
+        new std::map<std::pair<int, hipStream_t>, std::unique_ptr<Workspace>>();  // outlives static destructors
+    auto& w = (*cache)[{dev, s}];
+    if (!w) w.reset(new Workspace());
+    return *w;
 }
 
 int num_cus()

@@ -590,12 +590,14 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         } else {
             stage("colorBwd", [&] {
                 graft::mlp_backward(cshape, cb.dloss, cb.activations, cb.fwd_weights, cb.w_grad, cb.b_grad,
-                                    b.color_dx, (int)Bn, stream, d_hits, /*accumulate=*/false);
+                                    b.color_dx, (int)Bn, stream, d_hits, /*accumulate=*/false,
+                                    static_cast<graft::Workspace*>(cb.workspace));
             });
             stage("densityGrad", [&] { graft::density_grad(d_hits, Bn, b.dsigma, b.color_dx, db.dloss, stream); });
             stage("densityBwd", [&] {
                 graft::mlp_backward(dshape, db.dloss, db.activations, db.fwd_weights, db.w_grad, db.b_grad,
-                                    db.dx_out, (int)Bn, stream, d_hits, /*accumulate=*/false);
+                                    db.dx_out, (int)Bn, stream, d_hits, /*accumulate=*/false,
+                                    static_cast<graft::Workspace*>(db.workspace));
             });
         }
         GRAFT_HIP_CHECK(hipEventRecord(b.ev_dl, stream));
@@ -622,11 +624,13 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         if (fused_dx || dx_only) {
             stage_on(b.side, "colorBwd", [&] {
                 graft::mlp_backward(cshape, cb.dloss, cb.activations, cb.fwd_weights, cb.w_grad, cb.b_grad, nullptr,
-                                    (int)Bn, b.side, d_hits, /*accumulate=*/false);
+                                    (int)Bn, b.side, d_hits, /*accumulate=*/false,
+                                    static_cast<graft::Workspace*>(cb.workspace));
             });
             stage_on(b.side, "densityBwd", [&] {
                 graft::mlp_backward(dshape, db.dloss, db.activations, db.fwd_weights, db.w_grad, db.b_grad, nullptr,
-                                    (int)Bn, b.side, d_hits, /*accumulate=*/false);
+                                    (int)Bn, b.side, d_hits, /*accumulate=*/false,
+                                    static_cast<graft::Workspace*>(db.workspace));
             });
         }
         // Adam: MLP layers of both heads on the side stream, the hash table on

@@ -37,10 +37,12 @@ void mlp_forward(const MlpShape& s, const FwdInput& in, const __half* const* W,
 
 // dW/dB (device arrays of per-layer pointers) are accumulated (+=), or
 // overwritten with this batch's gradient when accumulate is false; dx may be
-// nullptr (then layer 0's dX is skipped).
+// nullptr (then layer 0's dX is skipped).  ws holds the per-block partial
+// sums (nullptr: the stream's workspace).
 void mlp_backward(const MlpShape& s, const __half* dy, const __half* const* acts,
                   const __half* const* W, float* const* dW, float* const* dB, __half* dx, int N,
-                  hipStream_t stream, const uint32_t* d_n = nullptr, bool accumulate = true);
+                  hipStream_t stream, const uint32_t* d_n = nullptr, bool accumulate = true,
+                  Workspace* ws = nullptr);
 
 // dx = dL/dx alone, bitwise the dx of mlp_backward, for the NeRF head shapes
 // (32-64-16, 2 layers; 32-64-8, 3 layers); returns false for other shapes.

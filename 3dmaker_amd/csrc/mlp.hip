@@ -777,7 +777,7 @@ bool mlp_backward_dx(const MlpShape& s, const __half* dy, const __half* const* a
 
 void mlp_backward(const MlpShape& s, const __half* dy, const __half* const* acts,
                   const __half* const* W, float* const* dW, float* const* dB, __half* dx, int N,
-                  hipStream_t stream, const uint32_t* d_n, bool accumulate)
+                  hipStream_t stream, const uint32_t* d_n, bool accumulate, Workspace* ws)
 {
     s.validate();
     if (N <= 0) return;
@@ -820,7 +820,7 @@ void mlp_backward(const MlpShape& s, const __half* dy, const __half* const* acts
         int per_cu = 0;
         GRAFT_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, lds));
         const int blocks = std::max(1, std::min((ntiles + 3) / 4, num_cus() * std::max(1, per_cu)));
-        p.ws = static_cast<float*>(workspace((size_t)blocks * p.P * sizeof(float)));
+        p.ws = static_cast<float*>((ws ? *ws : stream_workspace(stream)).get((size_t)blocks * p.P * sizeof(float)));
         hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), lds, stream, p);
         GRAFT_LAUNCH_CHECK();
         ReduceParams rp{};
@@ -850,7 +850,7 @@ void mlp_backward(const MlpShape& s, const __half* dy, const __half* const* acts
     p.nchunks = (N + kBwdChunk - 1) / kBwdChunk;
     const int per_cu = reg ? std::max(1, std::min(4, max_lds_per_block() / std::max(lds, 1))) : 2;
     const int blocks = std::max(1, std::min(p.nchunks, num_cus() * per_cu));
-    p.ws = static_cast<float*>(workspace((size_t)blocks * p.P * sizeof(float)));
+    p.ws = static_cast<float*>((ws ? *ws : stream_workspace(stream)).get((size_t)blocks * p.P * sizeof(float)));
 
     if (reg) {
         switch (maxd) {

@@ -15,6 +15,8 @@
 #include <cstddef>
 #include <algorithm>
 #include <cstring>
+#include <map>
+#include <memory>
 #include <mutex>
 #include <string>
 
@@ -30,38 +32,35 @@ static_assert(offsetof(InerfOptions, isProfiling) == offsetof(NerfOptions, isPro
 
 namespace {
 
-// Library-owned compaction scratch for processRaysHitLinear callers that pass
-// no block-sum buffer (grown on demand, one per process, single stream).
+// Scratch of the launchers, one set per (device, stream): the compactions'
+// block sums and results, the march store (kMaxHits floats per ray) and the
+// sum's partials; grown on demand, kept until the process ends.  Calls on one
+// stream run in order and share a set; calls on different streams never do.
+struct LauncherScratch {
+    graft::Workspace words, tstore, partials;
+};
+
 std::mutex g_mu;
-uint32_t* g_scratch = nullptr;
-size_t g_scratch_words = 0;
 
-float* g_tstore = nullptr;
-size_t g_tstore_floats = 0;
-
-uint32_t* march_scratch(size_t words)
+LauncherScratch& scratch_of(hipStream_t s)
 {
+    int dev = 0;
+    GRAFT_HIP_CHECK(hipGetDevice(&dev));
     std::lock_guard<std::mutex> lk(g_mu);
-    if (words > g_scratch_words) {
-        if (g_scratch) GRAFT_HIP_CHECK(hipFree(g_scratch));
-        g_scratch = nullptr;
-        GRAFT_HIP_CHECK(hipMalloc(&g_scratch, words * sizeof(uint32_t)));
-        g_scratch_words = words;
-    }
-    return g_scratch;
+    static auto* sets = new std::map<std::pair<int, hipStream_t>, std::unique_ptr<LauncherScratch>>();
+    auto& p = (*sets)[{dev, s}];
+    if (!p) p.reset(new LauncherScratch());
+    return *p;
 }
 
-// Per-ray sample store of the one-pass march (MAX_HITS floats per ray).
-float* march_tstore(size_t floats)
+uint32_t* march_scratch(hipStream_t s, size_t words)
 {
-    std::lock_guard<std::mutex> lk(g_mu);
-    if (floats > g_tstore_floats) {
-        if (g_tstore) GRAFT_HIP_CHECK(hipFree(g_tstore));
-        g_tstore = nullptr;
-        GRAFT_HIP_CHECK(hipMalloc(&g_tstore, floats * sizeof(float)));
-        g_tstore_floats = floats;
-    }
-    return g_tstore;
+    return static_cast<uint32_t*>(scratch_of(s).words.get(words * sizeof(uint32_t)));
+}
+
+float* march_tstore(hipStream_t s, size_t floats)
+{
+    return static_cast<float*>(scratch_of(s).tstore.get(floats * sizeof(float)));
 }
 
 graft::OccGrid occ_grid(const uint8_t* bits, uint3 res, float3 mn, float3 mx, int cascades, int mips)
@@ -88,7 +87,7 @@ void require_aligned16(const void* p, const char* what)
 graft::MarchScratch scan_all(uint32_t R, const uint32_t* counts, uint32_t* offsets, hipStream_t s, uint32_t* total)
 {
     const size_t words = graft::march_scratch_words(R);
-    uint32_t* sc = march_scratch(words);
+    uint32_t* sc = march_scratch(s, words);
     graft::MarchScratch ms{sc, sc + (words - 2)};
     graft::scan_counts(R, counts, 0xffffffffu, offsets, ms, s);
     if (total) {
@@ -123,12 +122,9 @@ void chunk_pipeline(uint32_t R, const float3* o, const float3* d, const float3* 
                         reinterpret_cast<float4*>(pos), ridx, t_sorted, s);
 }
 
-float* reduce_partials()
+float* reduce_partials(hipStream_t s)
 {
-    static float* p = nullptr;
-    std::lock_guard<std::mutex> lk(g_mu);
-    if (!p) GRAFT_HIP_CHECK(hipMalloc(&p, 1024 * sizeof(float)));
-    return p;
+    return static_cast<float*>(scratch_of(s).partials.get(1024 * sizeof(float)));
 }
 
 }  // namespace
@@ -158,9 +154,9 @@ int processRaysHitLinear(const uint32_t num_rays, const float3* rays_o, const fl
             occ_grid(occupancy_grid, grid_resolution, aabb_min, aabb_max, numCascades, mipmapLevels);
         const size_t words = graft::march_scratch_words(num_rays);
         (void)d_block_sums;  // sized (R + 1023) / 1024 by reference callers: too small, not used
-        uint32_t* sc = march_scratch(words);
+        uint32_t* sc = march_scratch(stream, words);
         graft::MarchScratch ms{sc, sc + (words - 2)};
-        float* ts = march_tstore(graft::march_store_floats(std::max<uint32_t>(num_rays, 1)));
+        float* ts = march_tstore(stream, graft::march_store_floats(std::max<uint32_t>(num_rays, 1)));
         graft::march_store(num_rays, rays_o, rays_d, rays_d_inv, nears, fars, g, samplesPerVoxel, d_num_steps, ts,
                            stream);
         graft::march_compact_stored(num_rays, rays_o, rays_d, g, (uint32_t)batchSize, d_num_steps, ts, 0, d_ray_offsets,
@@ -213,7 +209,7 @@ int processRaysHitPositions(const uint32_t num_rays, const float3* rays_o, const
             occ_grid(occupancy_grid, grid_resolution, aabb_min, aabb_max, numCascades, mipmapLevels);
         const uint32_t left = rays_done < num_rays ? num_rays - rays_done : 0u;
         // scratch: the re-marched rays' counts [left], then the cutoff result [4]
-        uint32_t* sc = march_scratch((size_t)left + 4);
+        uint32_t* sc = march_scratch(stream, (size_t)left + 4);
         uint32_t* res = sc + left;
         graft::cutoff_from(num_rays, d_ray_offsets, d_num_steps, (uint32_t)batchSize, rays_done,
                            d_active_rays_count, res, stream);
@@ -229,7 +225,7 @@ int processRaysHitPositions(const uint32_t num_rays, const float3* rays_o, const
         *totalHits = total;
         // march_rays_dda_offset (processRays.cu:801-929) re-marches the batch's
         // rays; here they are marched into the store and gathered per sample
-        float* ts = march_tstore(graft::march_store_floats(batch_rays));
+        float* ts = march_tstore(stream, graft::march_store_floats(batch_rays));
         const size_t r0 = rays_done;
         graft::march_store(batch_rays, rays_o + r0, rays_d + r0, rays_d_inv + r0, nears + r0, fars + r0, g,
                            samplesPerVoxel, sc, ts, stream);
@@ -471,7 +467,7 @@ void launchReduceSum(const float* d_in, int n, float* d_out, hipStream_t stream)
 {
     guarded("launchReduceSum", [&] {
         if (n < 0) throw std::runtime_error("negative size");
-        graft::reduce_sum(d_in, (uint32_t)n, reduce_partials(), d_out, stream);
+        graft::reduce_sum(d_in, (uint32_t)n, reduce_partials(stream), d_out, stream);
     });
 }
 

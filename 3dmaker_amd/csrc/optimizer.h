@@ -32,8 +32,9 @@ void zero_layers(float* const* a, float* const* b, const LayerSizes& sa, const L
                  hipStream_t stream);
 
 // *total += sum of squared error; dloss = fp16(diff * 2/(N*valid) * scale [* sigmoid']).
+// ws holds the per-block partial sums (nullptr: the stream's workspace).
 void mse_loss_grad(const float* pred, const __half* tgt, __half* dloss, float* total, int N, int padded,
-                   int valid, float loss_scale, int out_act, hipStream_t stream);
+                   int valid, float loss_scale, int out_act, hipStream_t stream, Workspace* ws = nullptr);
 
 void pad_f32(const float* src, float* dst, long long rows, int udim, int pdim, hipStream_t s);
 void pad_f16(const __half* src, __half* dst, long long rows, int udim, int pdim, hipStream_t s);

@@ -260,7 +260,7 @@ void zero_layers(float* const* a, float* const* b, const LayerSizes& sa, const L
 }
 
 void mse_loss_grad(const float* pred, const __half* tgt, __half* dloss, float* total, int N, int padded,
-                   int valid, float loss_scale, int out_act, hipStream_t stream)
+                   int valid, float loss_scale, int out_act, hipStream_t stream, Workspace* ws)
 {
     if (N <= 0) return;
     if (padded % 2) throw std::runtime_error("MSE: padded dimension must be even");
@@ -269,7 +269,7 @@ void mse_loss_grad(const float* pred, const __half* tgt, __half* dloss, float* t
     const int blocks = blocks_for(n2);
     const _Float16* t = reinterpret_cast<const _Float16*>(tgt);
     _Float16* d = reinterpret_cast<_Float16*>(dloss);
-    float* partials = static_cast<float*>(workspace((size_t)blocks * sizeof(float)));
+    float* partials = static_cast<float*>((ws ? *ws : stream_workspace(stream)).get((size_t)blocks * sizeof(float)));
     if (out_act == 1)
         hipLaunchKernelGGL(mse_kernel<1>, dim3(blocks), dim3(256), 0, stream, pred, t, d, partials, n2, padded, valid,
                            grad_scale);

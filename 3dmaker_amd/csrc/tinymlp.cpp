@@ -272,11 +272,14 @@ void TinyMLP::allocate_memory()
         d_b_m = TT.bm.dev<float>();
         d_b_v = TT.bv.dev<float>();
         d_activations = TT.acts.dev<half>();
+        if (!m_workspace) m_workspace = new graft::Workspace();
     }
 }
 
 void TinyMLP::free_training_state()
 {
+    delete static_cast<graft::Workspace*>(m_workspace);
+    m_workspace = nullptr;
     dfree(d_padded_targets);
     d_padded_targets = nullptr;
     dfree(d_dLoss_internal);
@@ -390,7 +393,8 @@ float TinyMLP::calculate_loss_and_grad(const half* d_unpadded_targets, int batch
         tg = d_padded_targets;
     }
     graft::mse_loss_grad(d_padded_outputs_float, tg, d_dLoss_internal, d_total_loss, batchSize, hw_opt.outputDim,
-                         user_opt.outputDim, loss_scale, hw_opt.outputActivation, stream);
+                         user_opt.outputDim, loss_scale, hw_opt.outputActivation, stream,
+                         static_cast<graft::Workspace*>(m_workspace));
     if (fetch_loss) {
         float h = 0.f;
         GRAFT_HIP_CHECK(hipMemcpyAsync(&h, d_total_loss, sizeof(float), hipMemcpyDeviceToHost, stream));
@@ -412,7 +416,8 @@ void TinyMLP::run_backward(const half* custom, bool have_custom, half* dx, int b
             GRAFT_HIP_CHECK(hipMemcpyAsync(d_dLoss_internal, custom, (size_t)batchSize * hw_opt.outputDim * sizeof(half),
                                            hipMemcpyDeviceToDevice, s));
     }
-    graft::mlp_backward(shape_of(hw_opt), d_dLoss_internal, d_activations, d_fwd_weights, d_w_grad, d_b_grad, dx, batchSize, s);
+    graft::mlp_backward(shape_of(hw_opt), d_dLoss_internal, d_activations, d_fwd_weights, d_w_grad, d_b_grad, dx,
+                        batchSize, s, nullptr, true, static_cast<graft::Workspace*>(m_workspace));
 }
 
 // TinyMLP.cu:354-390
@@ -494,6 +499,7 @@ TinyMLP::Buffers TinyMLP::buffers() const
     b.w_v = d_w_v;
     b.b_m = d_b_m;
     b.b_v = d_b_v;
+    b.workspace = m_workspace;
     return b;
 }
 
@@ -601,6 +607,7 @@ void TinyMLPHashGrid::allocate_memory()
         d_b_v = TT.bv.dev<float>();
         d_activations = TT.acts.dev<half>();
         if (!m_scatter) m_scatter = graft::scatter_plan_create(META, m_maxBatchSize);
+        if (!m_workspace) m_workspace = new graft::Workspace();
     }
 }
 
@@ -617,6 +624,8 @@ void TinyMLPHashGrid::free_training_state()
     TT.acts.destroy();
     graft::scatter_plan_destroy(static_cast<graft::ScatterPlan*>(m_scatter));
     m_scatter = nullptr;
+    delete static_cast<graft::Workspace*>(m_workspace);
+    m_workspace = nullptr;
     d_w_grad = d_b_grad = d_w_m = d_w_v = d_b_m = d_b_v = nullptr;
     d_activations = nullptr;
     d_current_inputs_backward = nullptr;
@@ -725,7 +734,8 @@ float TinyMLPHashGrid::calculate_loss_and_grad(const half* d_unpadded_targets, i
         tg = d_padded_targets;
     }
     graft::mse_loss_grad(d_padded_outputs_float, tg, d_dLoss_internal, d_total_loss, batchSize, hw_opt.outputDim,
-                         user_opt.outputDim, loss_scale, OUT_ACT_NONE, stream);
+                         user_opt.outputDim, loss_scale, OUT_ACT_NONE, stream,
+                         static_cast<graft::Workspace*>(m_workspace));
     if (fetch_loss) {
         float h = 0.f;
         GRAFT_HIP_CHECK(hipMemcpyAsync(&h, d_total_loss, sizeof(float), hipMemcpyDeviceToHost, stream));
@@ -741,7 +751,7 @@ void TinyMLPHashGrid::run_backward(int batchSize, hipStream_t stream)
     if (batchSize > m_maxBatchSize) throw std::runtime_error("batchSize exceeds maxBatchSize");
     if (batchSize <= 0) return;
     graft::mlp_backward(shape_of(mlp_opt), d_dLoss_internal, d_activations, d_fwd_weights, d_w_grad, d_b_grad,
-                        d_dx_out, batchSize, stream);
+                        d_dx_out, batchSize, stream, nullptr, true, static_cast<graft::Workspace*>(m_workspace));
     if (m_scatter)
         graft::hash_scatter_binned(static_cast<graft::ScatterPlan*>(m_scatter), META, d_dx_out,
                                    d_current_inputs_backward, 4, d_hashtable_grads, batchSize, stream, nullptr,
@@ -883,7 +893,7 @@ TinyMLPHashGrid::Buffers TinyMLPHashGrid::buffers() const
     b.hw = hw_opt;
     b.step = current_step;
     b.scatter_plan = m_scatter;
-    b.scatter_plan = m_scatter;
+    b.workspace = m_workspace;
     b.w_m = d_w_m;
     b.w_v = d_w_v;
     b.b_m = d_b_m;

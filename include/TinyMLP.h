@@ -71,6 +71,7 @@ public:
         float** w_v;
         float** b_m;
         float** b_v;
+        void* workspace;          // partial-sum workspace of this instance (opaque)
     };
     Buffers buffers() const;
 
@@ -101,6 +102,7 @@ private:
     float** d_b_m = nullptr;
     float** d_b_v = nullptr;
     void* h_ptrs = nullptr;   // host-side pointer tables (opaque)
+    void* m_workspace = nullptr;  // partial-sum workspace of the loss and backward (opaque)
 
     void allocate_memory();
     void free_training_state();

@@ -94,6 +94,7 @@ public:
         float** w_v;
         float** b_m;
         float** b_v;
+        void* workspace;          // partial-sum workspace of this instance (opaque)
     };
     Buffers buffers() const;
 
@@ -135,6 +136,7 @@ private:
     void* h_ptrs = nullptr;
     void* m_meta = nullptr;   // hash-grid level table (opaque)
     void* m_scatter = nullptr; // binned-scatter scratch of this instance (opaque)
+    void* m_workspace = nullptr;  // partial-sum workspace of the loss and backward (opaque)
 
     void allocate_memory();
     void free_training_state();

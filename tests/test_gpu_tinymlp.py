@@ -389,6 +389,56 @@ def test_net_forward_backward(dev, inD, hid, outD, nl, act, N):
     assert_close(dx, dx_ref, atol=2e-3 * max(1.0, np.abs(dx_ref.astype(np.float32)).max()), what="dx")
 
 
+def _net_grads(net, nl):
+    bufs = net.buffers()
+    hw = bufs.hw
+    hi, hh, ho = hw.inputDim, hw.hiddenDim, hw.outputDim
+    wg, bg = ptr_array(bufs.w_grad, nl), ptr_array(bufs.b_grad, nl)
+    outs = [ho if l == nl - 1 else hh for l in range(nl)]
+    ins = [hi if l == 0 else hh for l in range(nl)]
+    return np.concatenate([d2h(wg[l], (outs[l] * ins[l],), np.float32) for l in range(nl)] +
+                          [d2h(bg[l], (outs[l],), np.float32) for l in range(nl)])
+
+
+def test_two_instances_on_two_streams_match_serial_runs(dev):
+    """Each TinyMLP instance owns the partial-sum workspace of its loss and backward: two instances
+    trained at once on two streams give the gradients of serial runs, bit for bit (the reductions
+    are fixed-order)."""
+    P = pkg()
+    N = 1 << 18
+    shapes = [(32, 64, 16, 2, 0), (32, 64, 3, 3, 1)]   # the density and colour head shapes
+    nets = [P.Net(P.MLPOption(inputDim=i, hiddenDim=h, outputDim=o, numLayers=nl, activationType=0,
+                              outputActivation=a), N, seed=11 + k)
+            for k, (i, h, o, nl, a) in enumerate(shapes)]
+    rng = np.random.default_rng(12)
+    xs = [T(rng.standard_normal((N, sh[0])).astype(np.float16), dev) for sh in shapes]
+    ts = [T(rng.random((N, sh[2]), dtype=np.float32).astype(np.float16), dev) for sh in shapes]
+
+    def phases(k, stream):
+        n = nets[k]
+        return [lambda: n.zero_grad(stream), lambda: n.forward(xs[k], None, N, stream),
+                lambda: n.calculate_loss_and_grad(ts[k], N, 128.0, stream=stream),
+                lambda: n.backward(N, stream=stream)]
+
+    serial = []
+    for k in range(2):
+        for f in phases(k, 0):
+            f()
+        torch.cuda.synchronize()
+        serial.append(_net_grads(nets[k], shapes[k][3]))
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for rep in range(3):
+        pa, pb = phases(0, streams[0].cuda_stream), phases(1, streams[1].cuda_stream)
+        for fa, fb in zip(pa, pb):   # interleaved: the two backwards run at the same time
+            fa()
+            fb()
+        torch.cuda.synchronize()
+        for k in range(2):
+            np.testing.assert_array_equal(_net_grads(nets[k], shapes[k][3]), serial[k], err_msg=f"rep {rep} net {k}")
+    for n in nets:
+        n.close()
+
+
 def test_net_custom_grad_and_accumulation(dev):
     """backward(custom) twice accumulates dW exactly 2x (deterministic reduction)."""
     P = pkg()
