@@ -18,7 +18,6 @@ namespace {
 
 constexpr float kPI = 3.14159265359f;
 constexpr char kSceneMagic[4] = {'S', 'C', 'N', '1'};
-constexpr std::streamoff kSceneFooterBytes = 4 + 8 * (std::streamoff)sizeof(float);
 
 template <class T>
 T* dalloc(size_t n)
@@ -26,6 +25,42 @@ T* dalloc(size_t n)
     void* p = nullptr;
     GRAFT_HIP_CHECK(hipMalloc(&p, std::max<size_t>(n, 1) * sizeof(T)));
     return static_cast<T*>(p);
+}
+
+// Peak signal-to-noise ratio of a mean squared error on [0, 1] colours, with
+// the error floored at 1e-8 (80 dB).
+float psnr_db(float mse) { return -10.0f * log10f(fmaxf(mse, 1e-8f)); }
+
+// Smoothed wall time per step: the first measurement as is, each later one
+// pulls the estimate 30 % of the way towards itself.
+double smoothed_ms(double estimate, double measured)
+{
+    return estimate > 0.0 ? estimate + 0.30 * (measured - estimate) : measured;
+}
+
+// The scene footer appended to a saved model: "SCN1", then the scene centre,
+// up vector, scale and horizontal field of view (radians) as 8 floats.
+struct SceneFooter {
+    float center[3];
+    float up[3];
+    float scale;
+    float angle_x;
+};
+static_assert(sizeof(SceneFooter) == 8 * sizeof(float), "footer layout");
+constexpr std::streamoff kSceneFooterBytes = sizeof(kSceneMagic) + sizeof(SceneFooter);
+
+bool read_scene_footer(const std::string& path, SceneFooter& f)
+{
+    std::ifstream in(path, std::ios::binary | std::ios::ate);
+    if (!in) return false;
+    const std::streamoff bytes = in.tellg();
+    if (bytes < kSceneFooterBytes) return false;
+    char tail[kSceneFooterBytes];
+    in.seekg(bytes - kSceneFooterBytes);
+    if (!in.read(tail, kSceneFooterBytes)) return false;
+    if (std::memcmp(tail, kSceneMagic, sizeof(kSceneMagic)) != 0) return false;
+    std::memcpy(&f, tail + sizeof(kSceneMagic), sizeof(f));
+    return true;
 }
 
 }  // namespace
@@ -205,50 +240,53 @@ float INerfTrainer::trainOneChunk(bool computeLoss)
     return chunkMse(m_d_chunkRgb, m_dataloader->getChunkRgbTrue(), chunkSize) / (float)std::max(1, chunkSize);
 }
 
+// Starts a schedule of totalSteps (at least 1) optimizer steps from step 0,
+// the first ray of the feed and no loss or timing history
+// (NerfTrainer.cu:181-188).
 void INerfTrainer::beginTraining(int totalSteps)
 {
     dropAheadChunk();
-    m_targetSteps = std::max(1, totalSteps);
-    m_globalStep = 0;
-    m_rayCursor = 0;
-    m_raysSeen = 0.0;
-    m_emaMsPerStep = 0.0;
     m_lossHistory.clear();
+    m_emaMsPerStep = 0.0;
+    m_raysSeen = 0.0;
+    m_rayCursor = 0;
+    m_globalStep = 0;
+    m_targetSteps = totalSteps > 1 ? totalSteps : 1;
 }
 
+// Trains whole ray chunks until at least nSteps more optimizer steps have run
+// or the schedule is complete (a 20000-step schedule is begun when none was);
+// the first chunk of the call also measures its colour MSE
+// (NerfTrainer.cu:190-225).  Without a model and dataset it does nothing and
+// returns zeroed stats.
 TrainStats INerfTrainer::trainSteps(int nSteps)
 {
-    TrainStats s;
-    if (!m_nerf || !m_dataloader || m_total_rays == 0) return s;
+    if (!m_nerf || !m_dataloader || m_total_rays == 0) return TrainStats{};
     if (m_targetSteps == 0) beginTraining(20000);
-    const int target = std::min(m_globalStep + std::max(1, nSteps), m_targetSteps);
-    const int startStep = m_globalStep;
-    const auto t0 = std::chrono::high_resolution_clock::now();
-    float mse = -1.0f;
-    bool first = true;
-    while (m_globalStep < target) {
-        const float chunkMse_ = trainOneChunk(first);
-        if (chunkMse_ > 0.0f) mse = chunkMse_;
-        first = false;
+    const int from = m_globalStep;
+    const int until = std::min(m_targetSteps, from + std::max(nSteps, 1));
+    const auto started = std::chrono::high_resolution_clock::now();
+    float measured = -1.0f;  // this call's chunk MSE, when one was measured
+    for (int chunk = 0; m_globalStep < until; chunk++) {
+        const float mse = trainOneChunk(chunk == 0);
+        if (mse > 0.0f) measured = mse;
     }
     GRAFT_HIP_CHECK(hipDeviceSynchronize());
-    const auto t1 = std::chrono::high_resolution_clock::now();
-    const int stepsDone = m_globalStep - startStep;
-    if (stepsDone > 0) {
-        const double ms = std::chrono::duration<double, std::milli>(t1 - t0).count() / stepsDone;
-        m_emaMsPerStep = (m_emaMsPerStep > 0.0) ? (0.70 * m_emaMsPerStep + 0.30 * ms) : ms;
-    }
-    if (mse > 0.0f) m_lossHistory.push_back(mse);
-    const int remaining = std::max(0, m_targetSteps - m_globalStep);
-    s.step = m_globalStep;
-    s.targetSteps = m_targetSteps;
-    s.loss = (mse > 0.0f) ? mse : (m_lossHistory.empty() ? 0.0f : m_lossHistory.back());
-    s.psnr = (s.loss > 0.0f) ? -10.0f * log10f(fmaxf(s.loss, 1e-8f)) : 0.0f;
-    s.lr = currentLR();
-    s.epochs = epochs();
-    s.msPerStep = (float)m_emaMsPerStep;
-    s.etaSeconds = (float)(m_emaMsPerStep * remaining / 1000.0);
-    return s;
+    const double wall_ms =
+        std::chrono::duration<double, std::milli>(std::chrono::high_resolution_clock::now() - started).count();
+    if (m_globalStep > from) m_emaMsPerStep = smoothed_ms(m_emaMsPerStep, wall_ms / (m_globalStep - from));
+    if (measured > 0.0f) m_lossHistory.push_back(measured);
+
+    TrainStats st;
+    st.step = m_globalStep;
+    st.targetSteps = m_targetSteps;
+    st.loss = measured > 0.0f ? measured : (m_lossHistory.empty() ? 0.0f : m_lossHistory.back());
+    st.psnr = st.loss > 0.0f ? psnr_db(st.loss) : 0.0f;
+    st.lr = currentLR();
+    st.epochs = epochs();
+    st.msPerStep = (float)m_emaMsPerStep;
+    st.etaSeconds = (float)(m_emaMsPerStep * 1e-3 * std::max(0, m_targetSteps - m_globalStep));
+    return st;
 }
 
 // NerfTrainer.cu:228-252: progress bar on stdout.
@@ -355,82 +393,77 @@ Image INerfTrainer::renderTrainView(int index, int width, int height)
     return renderC2W(c2w, focal, width, height);
 }
 
-// NerfTrainer.cu:373-408: held-out views (every 8th image) in sequential
-// tiles of rayChunkSize rays, ground truth composited over white, mean over
-// pixels of (r^2 + g^2 + b^2) / 3.  As in the reference, the model renders
-// with its current background colour (the last training chunk's).
+// PSNR over the held-out views (the images training skips: every 8th),
+// rendered in tiles of rayChunkSize rays against ground truth composited
+// over white, from the per-pixel error (r^2 + g^2 + b^2) / 3 averaged over
+// all their pixels (NerfTrainer.cu:378-409).  The model keeps its current
+// background colour, the last training chunk's.
 float INerfTrainer::validate()
 {
     if (!m_nerf || !m_dataloader) return 0.0f;
-    const int HOLDOUT = 8;
-    const int pixels = m_dataloader->getWidth() * m_dataloader->getHeight();
+    const long long pixels = (long long)m_dataloader->getWidth() * m_dataloader->getHeight();
     if (pixels <= 0) return 0.0f;
-    const int numImgs = m_dataloader->getNumImages();
-    const int tile = m_masterConfig.rayChunkSize;
+    constexpr int kHeldOutEvery = 8;
+    const long long tile = m_masterConfig.rayChunkSize;
+    const float3 white = make_float3(1.0f, 1.0f, 1.0f);
+    double squared = 0.0;
+    long long seen = 0;
     m_nerf->setMemoryMode(INFERENCE);
-    const float3 valBg = make_float3(1.0f, 1.0f, 1.0f);
-    double se = 0.0;
-    long long totalPixels = 0;
-    for (int i = 0; i < numImgs; ++i) {
-        if (i % HOLDOUT != 0) continue;
-        for (int off = 0; off < pixels; off += tile) {
-            const int count = std::min(tile, pixels - off);
-            m_dataloader->fetchRayChunk(i * pixels + off, count, 0, valBg, 0, true, 0);
-            m_nerf->renderImageHit(m_dataloader->getChunkRaysO(), m_dataloader->getChunkRaysD(), (uint32_t)count,
+    for (int view = 0; view < m_dataloader->getNumImages(); view += kHeldOutEvery) {
+        for (long long px = 0; px < pixels; px += tile) {
+            const int n = (int)std::min(tile, pixels - px);
+            m_dataloader->fetchRayChunk((int)(view * pixels + px), n, 0, white, 0, true, 0);
+            m_nerf->renderImageHit(m_dataloader->getChunkRaysO(), m_dataloader->getChunkRaysD(), (uint32_t)n,
                                    m_d_chunkRgb, 0);
-            se += chunkMse(m_d_chunkRgb, m_dataloader->getChunkRgbTrue(), count);
-            totalPixels += count;
+            squared += chunkMse(m_d_chunkRgb, m_dataloader->getChunkRgbTrue(), n);
+            seen += n;
         }
     }
     m_nerf->setMemoryMode(TRAINING);
-    const float mse = (float)(se / (double)std::max(1LL, totalPixels));
-    return -10.0f * log10f(fmaxf(mse, 1e-8f));
+    return psnr_db((float)(squared / (double)(seen > 0 ? seen : 1)));
 }
 
+// Views in the feed: its rays over the pixels of one view.
 int INerfTrainer::numTrainViews() const
 {
     if (!m_dataloader) return 0;
-    const int px = m_dataloader->getWidth() * m_dataloader->getHeight();
-    return px > 0 ? (int)(m_total_rays / (uint32_t)px) : 0;
+    const uint32_t per_view = (uint32_t)std::max(0, m_dataloader->getWidth() * m_dataloader->getHeight());
+    return per_view ? (int)(m_total_rays / per_view) : 0;
 }
 
-// NerfTrainer.cu:269-300
+// The model file (InstantNerf::save), then the scene footer (NerfTrainer.cu:262-278).
 void INerfTrainer::save(const std::string& path)
 {
     if (!m_nerf) return;
     m_nerf->save(path);
+    SceneFooter f{{m_sceneCenter.x, m_sceneCenter.y, m_sceneCenter.z},
+                  {m_sceneUp.x, m_sceneUp.y, m_sceneUp.z},
+                  m_sceneScale,
+                  m_cameraAngleX};
     std::ofstream out(path, std::ios::binary | std::ios::app);
+    out.write(kSceneMagic, sizeof(kSceneMagic));
+    out.write(reinterpret_cast<const char*>(&f), sizeof(f));
     if (!out) throw std::runtime_error("INerfTrainer::save: cannot append the scene footer to " + path);
-    const float buf[8] = {m_sceneCenter.x, m_sceneCenter.y, m_sceneCenter.z, m_sceneUp.x,
-                          m_sceneUp.y,     m_sceneUp.z,     m_sceneScale,    m_cameraAngleX};
-    out.write(kSceneMagic, 4);
-    out.write(reinterpret_cast<const char*>(buf), sizeof(buf));
 }
 
+// The model (its options become the trainer's), and the scene fields when the
+// file ends with a footer (NerfTrainer.cu:280-300).
 void INerfTrainer::load(const std::string& path)
 {
     if (!m_nerf) m_nerf = new InstantNerf();
     m_nerf->load(path);
     m_masterConfig = m_nerf->options();
+    const size_t chunk = (size_t)m_masterConfig.rayChunkSize;
     (void)hipFree(m_d_chunkRgb);
     (void)hipFree(m_d_err);
-    m_d_chunkRgb = dalloc<float>((size_t)m_masterConfig.rayChunkSize * 3);
-    m_d_err = dalloc<float>((size_t)m_masterConfig.rayChunkSize);
+    m_d_chunkRgb = dalloc<float>(chunk * 3);
+    m_d_err = dalloc<float>(chunk);
     if (!m_d_loss) m_d_loss = dalloc<float>(1);
     if (!m_d_partials) m_d_partials = dalloc<float>(1024);
-    std::ifstream in(path, std::ios::binary | std::ios::ate);
-    if (!in) return;
-    const std::streamoff size = in.tellg();
-    if (size < kSceneFooterBytes) return;
-    in.seekg(size - kSceneFooterBytes, std::ios::beg);
-    char magic[4];
-    in.read(magic, 4);
-    if (std::memcmp(magic, kSceneMagic, 4) != 0) return;
-    float buf[8];
-    in.read(reinterpret_cast<char*>(buf), sizeof(buf));
-    if (!in) return;
-    m_sceneCenter = {buf[0], buf[1], buf[2]};
-    m_sceneUp = {buf[3], buf[4], buf[5]};
-    m_sceneScale = buf[6];
-    m_cameraAngleX = buf[7];
+    SceneFooter f;
+    if (!read_scene_footer(path, f)) return;
+    m_sceneCenter = {f.center[0], f.center[1], f.center[2]};
+    m_sceneUp = {f.up[0], f.up[1], f.up[2]};
+    m_sceneScale = f.scale;
+    m_cameraAngleX = f.angle_x;
 }
