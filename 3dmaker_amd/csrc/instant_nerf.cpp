@@ -11,6 +11,7 @@
 #include "scatter.h"
 #include "mlp.h"
 #include "nerf.h"
+#include "nerf_heads.h"
 #include "nerf_math.h"
 #include "occupancy.h"
 #include "optimizer.h"
@@ -87,6 +88,7 @@ struct NerfBuffers {
     float* dsigma = nullptr;
     __half* color_dx = nullptr;
     __half* enc_planar = nullptr;    // [L][Bn] feature pairs: the step's encodings, level-major
+    void* heads_packed = nullptr;    // both heads' weights packed for nerf_heads.hip (null: other shapes)
     // occupancy
     float* tmp_grid = nullptr;
     float4* occ_samples = nullptr;
@@ -193,6 +195,7 @@ void InstantNerf::freeBuffers()
         dfree(b.dsigma);
         dfree(b.color_dx);
         dfree(b.enc_planar);
+        dfree(b.heads_packed);
         dfree(b.tmp_grid);
         dfree(b.occ_samples);
         dfree(b.occ_density);
@@ -347,6 +350,10 @@ void InstantNerf::allocate()
     b.color_in = acts0;
     b.meta = graft::make_grid_meta(m_opts.hashTableSize, m_opts.numLevels, m_opts.growthFactor, m_opts.baseResolution);
     b.enc_planar = dalloc<__half>((size_t)2 * b.meta.numLevels * Bn);
+    const TinyMLPHashGrid::Buffers dbuf = m_densityMLP->buffers();
+    const graft::MlpShape dsh{2 * m_opts.numLevels, dbuf.hw.hiddenDim, dbuf.hw.outputDim, dbuf.hw.numLayers};
+    const graft::MlpShape csh = shape_of(cb.hw);
+    if (graft::nerf_heads_supported(dsh, csh)) b.heads_packed = dalloc<unsigned char>(graft::nerf_heads_packed_bytes());
 }
 
 // InstantNerf.cu:341-359.  The mode picks the hit batch of the render path
@@ -496,7 +503,8 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
             fa.meta = &b.meta;
             fa.dW = db.fwd_weights;
             fa.dB = db.master_biases;
-            fa.dacts = db.activations;
+            // the 16x16x32 heads store no activations: the backward recomputes them
+            fa.dacts = b.heads_packed ? nullptr : db.activations;
             fa.density_out = b.density_out;
             fa.dirs = cd;
             fa.ray_idx = S.ray_idx;
@@ -506,11 +514,12 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
             fa.out_act = cb.hw.outputActivation;
             fa.cW = cb.fwd_weights;
             fa.cB = cb.master_biases;
-            fa.cacts = cb.activations;
+            fa.cacts = b.heads_packed ? nullptr : cb.activations;
             fa.color_in = b.color_in;
             fa.color_out = cb.padded_outputs;
             fa.enc_scratch = b.enc_planar;
             fa.enc_plane = (int)Bn;
+            fa.heads_packed = b.heads_packed;
             graft::nerf_forward(fa, (int)Bn, stream, d_hits);
         });
 
@@ -569,9 +578,24 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         bx.color_dx = b.color_dx;
         bx.density_dy = db.dloss;
         bx.denc = db.dx_out;
-        const bool fused_dx = graft::nerf_backward_dx(bx, 0, stream);  // shape check only (N = 0)
-        const bool dx_only = graft::mlp_has_dx_kernel(cshape) && graft::mlp_has_dx_kernel(dshape);
-        if (fused_dx || dx_only) {
+        graft::NerfHeadsBwd hb;
+        hb.packed = b.heads_packed;
+        hb.enc = b.enc_planar;
+        hb.enc_plane = (int)Bn;
+        hb.levels = b.meta.numLevels;
+        hb.color_in = b.color_in;
+        hb.color_dy = cb.dloss;
+        hb.dsigma = b.dsigma;
+        hb.denc = db.dx_out;
+        hb.density_dy = db.dloss;
+        hb.color_dx = b.color_dx;
+        const bool heads = b.heads_packed != nullptr;
+        const bool fused_dx = !heads && graft::nerf_backward_dx(bx, 0, stream);  // shape check only (N = 0)
+        const bool dx_only = !heads && graft::mlp_has_dx_kernel(cshape) && graft::mlp_has_dx_kernel(dshape);
+        if (heads) {
+            // recomputed activations: colour dX chain, glue, density dX chain
+            stage("backwardDx", [&] { graft::nerf_heads_dx(hb, (int)Bn, stream, d_hits); });
+        } else if (fused_dx || dx_only) {
             if (fused_dx) {
                 // colour dX chain, density-gradient glue, density dX chain: one launch
                 stage("backwardDx", [&] { graft::nerf_backward_dx(bx, (int)Bn, stream, d_hits); });
@@ -621,7 +645,12 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         // compaction that refills the set two steps later (it is enqueued on
         // the side stream after the next step's wait on ev_dl).
         GRAFT_HIP_CHECK(hipStreamWaitEvent(b.side, b.ev_dl, 0));
-        if (fused_dx || dx_only) {
+        if (heads) {
+            stage_on(b.side, "headsBwd", [&] {
+                graft::nerf_heads_dw(hb, graft::NerfHeadsGrads{db.w_grad, db.b_grad, cb.w_grad, cb.b_grad}, (int)Bn,
+                                     b.side, d_hits, static_cast<graft::Workspace*>(db.workspace));
+            });
+        } else if (fused_dx || dx_only) {
             stage_on(b.side, "colorBwd", [&] {
                 graft::mlp_backward(cshape, cb.dloss, cb.activations, cb.fwd_weights, cb.w_grad, cb.b_grad, nullptr,
                                     (int)Bn, b.side, d_hits, /*accumulate=*/false,
@@ -883,6 +912,9 @@ InstantNerf::StepBuffers InstantNerf::stepBuffers() const
     s.result = S.result;
     s.trainSteps = m_trainSteps;
     s.windowStart = m_windowStart;
+    s.encodings = reinterpret_cast<half*>(b.enc_planar);
+    s.encodingPlane = (uint32_t)std::max(1, m_opts.batchSize);
+    s.activationsSaved = b.heads_packed ? 0 : 1;
     return s;
 }
 

@@ -51,6 +51,12 @@ bool mlp_backward_dx(const MlpShape& s, const __half* dy, const __half* const* a
                      __half* dx, int N, hipStream_t stream, const uint32_t* d_n = nullptr);
 bool mlp_has_dx_kernel(const MlpShape& s);
 
+// Fixed-order sum of nparts block partials ws [nparts][P] of one net's
+// gradients (W of every layer row-major [out][in], then b of every layer)
+// into dW / dB (device arrays of per-layer pointers), added when accumulate.
+void mlp_grad_reduce(const MlpShape& s, const float* ws, int nparts, float* const* dW, float* const* dB,
+                     bool accumulate, hipStream_t stream);
+
 // The forward of a NeRF step (hash encode + density head, SH gather, colour
 // head) in one launch; bitwise equal to mlp_forward(density), sh_gather,
 // mlp_forward(colour).  dacts / density_out / cacts / color_in may be null
@@ -81,6 +87,12 @@ struct NerfFwdArgs {
     // holding only its levels' tables) and the network kernel reads it.
     __half* enc_scratch = nullptr;
     int enc_plane = 0;
+    // Nullable: a buffer of nerf_heads_packed_bytes().  With it, the planar
+    // encodings and the head shapes nerf_heads_supported() accepts, and no
+    // activations asked for (dacts, cacts null), the heads run as the
+    // 16x16x32 MFMA kernels of nerf_heads.hip after packing the weights into
+    // this buffer.
+    void* heads_packed = nullptr;
 };
 void nerf_forward(const NerfFwdArgs& a, int N, hipStream_t stream, const uint32_t* d_n = nullptr);
 

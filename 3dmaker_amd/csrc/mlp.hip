@@ -885,4 +885,30 @@ void mlp_backward(const MlpShape& s, const __half* dy, const __half* const* acts
     GRAFT_LAUNCH_CHECK();
 }
 
+void mlp_grad_reduce(const MlpShape& s, const float* ws, int nparts, float* const* dW, float* const* dB,
+                     bool accumulate, hipStream_t stream)
+{
+    s.validate();
+    ReduceParams rp{};
+    rp.ws = ws;
+    rp.dW = dW;
+    rp.dB = dB;
+    rp.nparts = nparts;
+    rp.layers = s.layers;
+    rp.accumulate = accumulate ? 1 : 0;
+    int tot = 0;
+    for (int l = 0; l < s.layers; l++) {
+        rp.wofs[l] = tot;
+        tot += s.in_l(l) * s.out_l(l);
+    }
+    rp.wtot = tot;
+    for (int l = 0; l < s.layers; l++) {
+        rp.bofs[l] = tot;
+        tot += s.out_l(l);
+    }
+    rp.P = tot;
+    hipLaunchKernelGGL(mlp_grad_reduce_kernel, dim3((rp.P + 63) / 64), dim3(1024), 0, stream, rp);
+    GRAFT_LAUNCH_CHECK();
+}
+
 }  // namespace graft

@@ -665,6 +665,9 @@ int inerf_step_buffers(Inerf* h, InerfStepBuffers* out)
         out->result = b.result;
         out->trainSteps = b.trainSteps;
         out->windowStart = b.windowStart;
+        out->encodings = b.encodings;
+        out->encodingPlane = b.encodingPlane;
+        out->activationsSaved = b.activationsSaved;
     });
 }
 int inerf_save(Inerf* h, const char* path)

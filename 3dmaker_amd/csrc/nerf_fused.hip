@@ -21,6 +21,7 @@
 #include "hashgrid.h"
 #include "mlp_device.h"
 #include "nerf.h"
+#include "nerf_heads.h"
 
 #include <algorithm>
 
@@ -240,6 +241,25 @@ void nerf_forward(const NerfFwdArgs& a, int N, hipStream_t stream, const uint32_
     if (planar) {
         if (a.enc_plane < N) throw std::runtime_error("NeRF forward: encoding plane stride below the sample count");
         hash_encode_planar(m, a.table, a.pos, a.pos_stride, a.enc_scratch, a.enc_plane, N, stream, d_n);
+    }
+    if (planar && a.heads_packed != nullptr && a.dacts == nullptr && a.cacts == nullptr &&
+        nerf_heads_supported(a.dshape, a.cshape)) {
+        nerf_heads_pack(NerfHeadsWeights{a.dW, a.dB, a.cW, a.cB}, a.heads_packed, stream);
+        NerfHeadsFwd h;
+        h.packed = a.heads_packed;
+        h.enc = a.enc_scratch;
+        h.enc_plane = a.enc_plane;
+        h.levels = m.numLevels;
+        h.dirs = a.dirs;
+        h.ray_idx = a.ray_idx;
+        h.density_bias = a.density_bias;
+        h.out_act = a.out_act;
+        h.sigma = a.sigma;
+        h.density_out = a.density_out;
+        h.color_out = a.color_out;
+        h.color_in = a.color_in;
+        nerf_heads_forward(h, N, stream, d_n);
+        return;
     }
     NerfFwdParams p{};
     p.pos = a.pos;

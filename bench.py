@@ -671,8 +671,8 @@ def main():
                 "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom),
                 "algorithmic_bytes_per_launch": int(algo), "avg_launch_ms": round(dom_ms, 4)}
     # MLP stages: the fused forward, the dX chains (main stream) and the weight gradients (side stream)
-    mlp_ms = sum(st[k][0] for k in ("forward", "backwardDx", "colorDx", "densityDx", "colorBwd", "densityBwd")
-                 if k in st)
+    mlp_ms = sum(st[k][0] for k in ("forward", "backwardDx", "colorDx", "densityDx", "colorBwd", "densityBwd",
+                                    "headsBwd") if k in st)
     mfma_util = MLP_FLOP_PER_SAMPLE * n_prof / (mlp_ms * 1e-3) / 1e12 / FP16_PEAK_TFLOPS if mlp_ms else None
 
     out = {

@@ -180,6 +180,11 @@ public:
         uint32_t* result;         // [2]: active rays, compacted samples of the last step
         int trainSteps;
         uint32_t windowStart;     // index of the last step's first ray in the last call's rays
+        half* encodings;          // [numLevels][encodingPlane] feature pairs of the last step
+        uint32_t encodingPlane;
+        int activationsSaved;     // 0: the heads' hidden activations are recomputed, not kept in
+                                  // the TinyMLP activation buffers; color_dx then holds only the
+                                  // logit features (the SH features are 0)
     };
     StepBuffers stepBuffers() const;
 

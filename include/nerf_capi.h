@@ -57,6 +57,9 @@ typedef struct InerfStepBuffers {
     uint32_t* result;       /* [2] active rays, compacted samples */
     int trainSteps;
     uint32_t windowStart;   /* first ray of the last step within the last call's rays */
+    GRAFT_HALF* encodings;  /* [numLevels][encodingPlane] feature pairs of the last step */
+    uint32_t encodingPlane;
+    int activationsSaved;   /* 0: hidden activations recomputed, not stored; color_dx holds the logit features only */
 } InerfStepBuffers;
 
 /* InstantNerf::refreshBuffers (introspection, no reference counterpart). */
