@@ -120,9 +120,12 @@ struct NerfBuffers {
     // of the next hit batch and the MLP weight gradients and Adam updates;
     // `occ` runs the occupancy refresh.
     hipStream_t side = nullptr, occ = nullptr;
+    hipStream_t cmp = nullptr;  // ray setup, march and compaction of the next hit batch
     hipEvent_t ev_fork = nullptr, ev_join = nullptr, ev_done = nullptr, ev_done_occ = nullptr;
+    hipEvent_t ev_done_cmp = nullptr;
     hipEvent_t ev_dl = nullptr;      // main: this step's MLP output gradients are written
     hipEvent_t ev_occ_fork = nullptr;  // main: a refresh step's parameters are final (step start)
+    hipEvent_t ev_opt = nullptr;       // side: the step's MLP Adam updates are done
     std::vector<StageTimer> pending;
     std::map<std::string, std::pair<double, long>> stats;
 };
@@ -219,8 +222,11 @@ void InstantNerf::freeBuffers()
         if (b.ev_done_occ) (void)hipEventDestroy(b.ev_done_occ);
         if (b.ev_dl) (void)hipEventDestroy(b.ev_dl);
         if (b.ev_occ_fork) (void)hipEventDestroy(b.ev_occ_fork);
+        if (b.ev_opt) (void)hipEventDestroy(b.ev_opt);
+        if (b.ev_done_cmp) (void)hipEventDestroy(b.ev_done_cmp);
         if (b.occ) (void)hipStreamDestroy(b.occ);
         if (b.side) (void)hipStreamDestroy(b.side);
+        if (b.cmp) (void)hipStreamDestroy(b.cmp);
         for (auto& t : b.pending) {
             (void)hipEventDestroy(t.a);
             (void)hipEventDestroy(t.b);
@@ -340,8 +346,11 @@ void InstantNerf::allocate()
     GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_done_occ, kStreamEvent));
     GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_dl, kStreamEvent));
     GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_occ_fork, kStreamEvent));
+    GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_opt, kStreamEvent));
+    GRAFT_HIP_CHECK(hipEventCreateWithFlags(&b.ev_done_cmp, kStreamEvent));
     GRAFT_HIP_CHECK(hipStreamCreateWithFlags(&b.occ, hipStreamNonBlocking));
     GRAFT_HIP_CHECK(hipStreamCreateWithFlags(&b.side, hipStreamNonBlocking));
+    GRAFT_HIP_CHECK(hipStreamCreateWithFlags(&b.cmp, hipStreamNonBlocking));
 
     // The color head's activation-0 buffer receives the SH gather output directly.
     const TinyMLP::Buffers cb = m_colorMLP->buffers();
@@ -407,37 +416,39 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
     auto stage = [&](const char* name, auto&& fn) { stage_on(stream, name, fn); };
 
     // processRaysHitLinear (processRays.cu:931-1040) for the hit batch that
-    // starts at ray raysDone, into step set k, on the side stream: the window
-    // is marched only when it is not covered by the cached march on the
+    // starts at ray raysDone, into step set k, on the compaction stream: the
+    // window is marched only when it is not covered by the cached march on the
     // current grid.  The set's previous step has finished reading it by
-    // then: this runs after the side stream's wait on a later step's ev_dl.
+    // then: the compaction stream waits for a later step's ev_dl first.
     auto compact_rays = [&](int k, uint32_t raysDone, const float3* rays_o, const float3* rays_d, uint32_t nRays) {
         StepSet& S = b.set[k];
         const uint32_t R = std::min<uint32_t>((uint32_t)o.rayChunkSize, nRays - raysDone);
         const float3* co = rays_o + raysDone;
         const float3* cd = rays_d + raysDone;
         if (b.cache_version != m_gridVersion || raysDone < b.cache_c0 || raysDone + R > b.cache_c1) {
-            stage_on(b.side, "rayAabb", [&] {
+            stage_on(b.cmp, "rayAabb", [&] {
                 graft::ray_aabb_inv(R, co, cd, o.aabbMin, o.aabbMax, o.numCascades, b.d_inv, b.nears, b.fars,
-                                    b.side);
+                                    b.cmp);
             });
-            stage_on(b.side, "march", [&] {
+            stage_on(b.cmp, "march", [&] {
                 graft::march_store(R, co, cd, b.d_inv, b.nears, b.fars, g, o.samplesPerVoxel, b.counts, b.t_scratch,
-                                   b.side);
+                                   b.cmp);
             });
             b.cache_c0 = raysDone;
             b.cache_c1 = raysDone + R;
             b.cache_version = m_gridVersion;
         }
         const uint32_t woff = raysDone - b.cache_c0;
-        stage_on(b.side, "compaction", [&] {
+        stage_on(b.cmp, "compaction", [&] {
             graft::march_compact_stored(R, co, cd, g, Bn, b.counts + woff, b.t_scratch, woff, S.offsets, S.t_sorted,
-                                        S.ray_idx, S.positions, graft::MarchScratch{b.block_sums, S.result}, b.side,
+                                        S.ray_idx, S.positions, graft::MarchScratch{b.block_sums, S.result}, b.cmp,
                                         S.counts);
         });
-        GRAFT_HIP_CHECK(hipMemcpyAsync(S.h_result, S.result, 2 * sizeof(uint32_t), hipMemcpyDeviceToHost, b.side));
-        GRAFT_HIP_CHECK(hipEventRecord(S.ev_result, b.side));
-        GRAFT_HIP_CHECK(hipEventRecord(S.ev_ready, b.side));
+        // the main stream needs the set on the device only: ready before the
+        // 8-byte copy to the host, whose latency stays off the step's path
+        GRAFT_HIP_CHECK(hipEventRecord(S.ev_ready, b.cmp));
+        GRAFT_HIP_CHECK(hipMemcpyAsync(S.h_result, S.result, 2 * sizeof(uint32_t), hipMemcpyDeviceToHost, b.cmp));
+        GRAFT_HIP_CHECK(hipEventRecord(S.ev_result, b.cmp));
         S.raysDone = raysDone;
     };
     auto compact = [&](int k, uint32_t raysDone) { compact_rays(k, raysDone, d_rays_o, d_rays_d, numRays); };
@@ -445,6 +456,7 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
     // the side streams start after everything the caller queued (rays, grid)
     GRAFT_HIP_CHECK(hipEventRecord(b.ev_fork, stream));
     GRAFT_HIP_CHECK(hipStreamWaitEvent(b.side, b.ev_fork, 0));
+    GRAFT_HIP_CHECK(hipStreamWaitEvent(b.cmp, b.ev_fork, 0));
     GRAFT_HIP_CHECK(hipStreamWaitEvent(b.occ, b.ev_fork, 0));
     // The first hit batch: compacted beside the previous call's last step
     // when that call was told these rays (same buffers, same grid), else now.
@@ -454,6 +466,7 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
     const NerfBuffers::Ahead next = b.next;
     b.next = NerfBuffers::Ahead{};
     int k = 0, i = 0;
+    bool opt_recorded = false;  // ev_opt holds a step of this call
     if (prefetched) {
         k = b.pre.set;
     } else {
@@ -473,8 +486,10 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         b.last_set = k;
 
         // S was compacted on the side stream after the previous step's MLP
-        // Adam: once it is ready, the weights this forward uses are updated
+        // S on the device, and the previous step's MLP Adam (side stream):
+        // then the weights this forward uses are updated
         GRAFT_HIP_CHECK(hipStreamWaitEvent(stream, S.ev_ready, 0));
+        if (opt_recorded) GRAFT_HIP_CHECK(hipStreamWaitEvent(stream, b.ev_opt, 0));
         // InstantNerf.cu:488-494: the refresh reads only the density head's
         // parameters -- the ones this step's forward reads, final once S is
         // ready -- and changes only the grid that later batches march, so it
@@ -645,6 +660,42 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         // compaction that refills the set two steps later (it is enqueued on
         // the side stream after the next step's wait on ev_dl).
         GRAFT_HIP_CHECK(hipStreamWaitEvent(b.side, b.ev_dl, 0));
+
+        // The only host read of the step: its active-ray count (computed a
+        // step ago), to advance the cursor.  The next batch is compacted on
+        // the side stream first, beside this step's scatter (after the
+        // refresh instead when this step refreshes the grid).
+        GRAFT_HIP_CHECK(hipEventSynchronize(S.ev_result));
+        const uint32_t active = S.h_result[0], hits = S.h_result[1];
+        if (active == 0) {
+            // unreachable with batchSize >= one ray's sample cap; leave no work
+            // of this call on the side streams and no timers behind
+            GRAFT_HIP_CHECK(hipEventRecord(b.ev_done, b.side));
+            GRAFT_HIP_CHECK(hipStreamWaitEvent(stream, b.ev_done, 0));
+            GRAFT_HIP_CHECK(hipEventRecord(b.ev_done_occ, b.occ));
+            GRAFT_HIP_CHECK(hipStreamWaitEvent(stream, b.ev_done_occ, 0));
+            GRAFT_HIP_CHECK(hipEventRecord(b.ev_done_cmp, b.cmp));
+            GRAFT_HIP_CHECK(hipStreamWaitEvent(stream, b.ev_done_cmp, 0));
+            GRAFT_HIP_CHECK(hipStreamSynchronize(stream));
+            for (auto& t : b.pending) {
+                (void)hipEventDestroy(t.a);
+                (void)hipEventDestroy(t.b);
+            }
+            b.pending.clear();
+            b.pre.valid = false;
+            throw std::runtime_error("InstantNerf: no ray fits the batch");
+        }
+        if (hitCounts) hitCounts[i] = hits;
+        i++;
+        m_lastRaysTrained = raysDone + active;
+        const bool all_rays = raysDone + active >= numRays;
+        const bool stop = all_rays || (m_stepLimit > 0 && i >= m_stepLimit);
+        // the compaction stream: after this step's reads of the set it refills
+        // (ev_dl) and, on a refresh step, after the refresh (ev_join)
+        GRAFT_HIP_CHECK(hipStreamWaitEvent(b.cmp, b.ev_dl, 0));
+        if (refresh) GRAFT_HIP_CHECK(hipStreamWaitEvent(b.cmp, b.ev_join, 0));
+        if (!stop) compact(k ^ 1, raysDone + active);
+
         if (heads) {
             stage_on(b.side, "headsBwd", [&] {
                 graft::nerf_heads_dw(hb, graft::NerfHeadsGrads{db.w_grad, db.b_grad, cb.w_grad, cb.b_grad}, (int)Bn,
@@ -677,35 +728,12 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         stage("densityOpt", [&] {
             m_densityMLP->stepSplit(o.learningRate, o.beta1, o.beta2, o.epsilon, o.lossScale, b.side, stream);
         });
+        GRAFT_HIP_CHECK(hipEventRecord(b.ev_opt, b.side));
+        opt_recorded = true;
 
         trainStepCount++;
         m_trainSteps++;
-
-        // The only host read of the step: its active-ray count, to advance the
-        // cursor; the next batch's compaction then runs beside this step.
-        GRAFT_HIP_CHECK(hipEventSynchronize(S.ev_result));
-        const uint32_t active = S.h_result[0], hits = S.h_result[1];
-        if (active == 0) {
-            // unreachable with batchSize >= one ray's sample cap; leave no work
-            // of this call on the side streams and no timers behind
-            GRAFT_HIP_CHECK(hipEventRecord(b.ev_done, b.side));
-            GRAFT_HIP_CHECK(hipStreamWaitEvent(stream, b.ev_done, 0));
-            GRAFT_HIP_CHECK(hipEventRecord(b.ev_done_occ, b.occ));
-            GRAFT_HIP_CHECK(hipStreamWaitEvent(stream, b.ev_done_occ, 0));
-            GRAFT_HIP_CHECK(hipStreamSynchronize(stream));
-            for (auto& t : b.pending) {
-                (void)hipEventDestroy(t.a);
-                (void)hipEventDestroy(t.b);
-            }
-            b.pending.clear();
-            b.pre.valid = false;
-            throw std::runtime_error("InstantNerf: no ray fits the batch");
-        }
-        if (hitCounts) hitCounts[i] = hits;
-        i++;
-        m_lastRaysTrained = raysDone + active;
-        const bool all_rays = raysDone + active >= numRays;
-        if (all_rays || (m_stepLimit > 0 && i >= m_stepLimit)) {
+        if (stop) {
             // the next call's rays are compacted ahead only when they are
             // other buffers than this call's (a caller refilling these buffers
             // in place for the next call would otherwise train on stale rays)
@@ -720,13 +748,14 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
             break;
         }
         k ^= 1;
-        compact(k, raysDone + active);
     }
     // nothing of this call stays on the side streams past the return
     GRAFT_HIP_CHECK(hipEventRecord(b.ev_done, b.side));
     GRAFT_HIP_CHECK(hipStreamWaitEvent(stream, b.ev_done, 0));
     GRAFT_HIP_CHECK(hipEventRecord(b.ev_done_occ, b.occ));
     GRAFT_HIP_CHECK(hipStreamWaitEvent(stream, b.ev_done_occ, 0));
+    GRAFT_HIP_CHECK(hipEventRecord(b.ev_done_cmp, b.cmp));
+    GRAFT_HIP_CHECK(hipStreamWaitEvent(stream, b.ev_done_cmp, 0));
 
     if (o.isProfiling && !b.pending.empty()) {
         for (auto& t : b.pending) {

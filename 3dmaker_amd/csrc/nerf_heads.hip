@@ -913,7 +913,7 @@ void nerf_heads_dw(const NerfHeadsBwd& a, const NerfHeadsGrads& out, int N, hipS
     BwdParams p = bwd_params(a, N, d_n);
     const int lds = (int)std::max(kTrBytes + kFwdBytes, (size_t)PC * sizeof(float));
     // one block per CU for each head (the colour head's has the more work)
-    const int cb = num_cus(), db = num_cus();
+    const int cb = num_cus() / 2, db = num_cus() / 2;
     Workspace& w = ws ? *ws : stream_workspace(s);
     float* part = static_cast<float*>(w.get(((size_t)cb * PC + (size_t)db * PD) * sizeof(float)));
     p.ws_c = part;
