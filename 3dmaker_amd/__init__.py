@@ -142,6 +142,8 @@ SIGNATURES = {
     "tmlp_grid_backward": (_i, [_vp, _vp, _i, _vp]),
     "tmlp_grid_set_split_scatter": (_i, [_vp, _i]),
     "tmlp_grid_step": (_i, [_vp, _f, _f, _f, _f, _f, _vp]),
+    "tmlp_grid_scatter_adam_table": (_i, [_vp, _vp, _vp, _i, _i, _f, _f, _f, _f, _f, _vp]),
+    "tmlp_grid_step_mlp": (_i, [_vp, _f, _f, _f, _f, _f, _vp]),
     "tmlp_grid_reset_step": (_i, [_vp]),
     "tmlp_grid_load_weights": (_i, [_vp, _vp, _vp]),
     "tmlp_grid_save_weights": (_i, [_vp, _vp, _vp]),
@@ -195,6 +197,11 @@ SIGNATURES = {
     "launchReduceSum": (None, [_vp, _i, _vp, _vp]),
     "launchUpdateOccupancyGrid": (None, [_vp, _vp, _vp, _i, _i, _i, _f, _f, _vp]),
     "launchBuildMipmaps": (None, [_vp, Uint3, _i, _i, _vp]),
+    "nerfHeadsPackedBytes": (C.c_size_t, []),
+    "launchNerfHeadsPack": (None, [_vp, _vp, _vp, _vp, _vp, _vp]),
+    "launchNerfHeadsForward": (None, [_vp, _vp, _i, _i, _vp, _vp, _i, _f, _i, _vp, _vp, _vp, _vp, _vp]),
+    "launchNerfHeadsBackward": (None, [_vp, _vp, _i, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp]),
+    "launchNerfHeadsWeightGrads": (None, [_vp, _vp, _i, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp]),
     "nerf_abi_echo_vec": (None, [Float3, Uint3, C.POINTER(_f)]),
     # include/nerf_capi.h (InstantNerf handle API)
     "inerf_default_options": (None, [C.POINTER(NerfOptions)]),
@@ -340,6 +347,15 @@ class HashGrid:
 
     def step(self, lr=3e-4, beta1=0.9, beta2=0.999, eps=1e-8, loss_scale=65536.0, stream=0):
         self._c(self._L.tmlp_grid_step(self.h, lr, beta1, beta2, eps, loss_scale, stream))
+
+    def scatter_adam_table(self, dx, positions, n, pos_stride=4, lr=3e-4, beta1=0.9, beta2=0.999, eps=1e-8,
+                           loss_scale=65536.0, stream=0):
+        """The table half of the next step, fused into the scatter of dx (TinyMLPHashGrid::scatterAdamTable)."""
+        self._c(self._L.tmlp_grid_scatter_adam_table(self.h, ptr(dx), ptr(positions), pos_stride, n, lr, beta1, beta2,
+                                                     eps, loss_scale, stream))
+
+    def step_mlp(self, lr=3e-4, beta1=0.9, beta2=0.999, eps=1e-8, loss_scale=65536.0, stream=0):
+        self._c(self._L.tmlp_grid_step_mlp(self.h, lr, beta1, beta2, eps, loss_scale, stream))
 
     def reset_step(self):
         self._c(self._L.tmlp_grid_reset_step(self.h))

@@ -21,6 +21,10 @@
 //              (ds_add_u64), then one store per table entry.  A bin of several
 //              chunks adds its partial sums into an int64 staging slice with
 //              global 64-bit atomics, and its last chunk converts the slice.
+//              The training step's variant applies Adam to every entry the
+//              sums reach instead of storing a gradient (the table half of
+//              the optimizer step, optimizerKernel.cu:16-167, fused in): the
+//              update sees the gradient the stored path would have stored.
 //
 // A corner pair is the two x-neighbour corners of one (y, z) corner.  Dense
 // levels index them x0 and x0 + 1 of one (y, z) row, and a dense slice is a
@@ -39,6 +43,7 @@
 // through the reference's atomics.
 #include "scatter.h"
 
+#include "adam_math.h"
 #include "hashgrid.h"
 
 #include <algorithm>
@@ -53,12 +58,13 @@ namespace {
 
 constexpr int kSlice = 4096;  // table entries (feature pairs) per bin
 constexpr int kSliceShift = 12;
-constexpr int kBinThreads = 256;
-constexpr int kSamplesPerThread = 2;
+constexpr int kBinThreads = 512;
+constexpr int kSamplesPerThread = 1;
 constexpr int kRound = kBinThreads * kSamplesPerThread;
 constexpr uint32_t kChunk = 32768;  // records per accumulate workgroup
 constexpr int kAccThreads = 512;
 constexpr int kMaxBins = 8192;
+constexpr int kDenseBins = 64;  // target bins per dense level
 
 struct ScatterArgs {
     const uint32_t* d_n;  // nullable device-side sample count (<= N)
@@ -237,52 +243,73 @@ __global__ __launch_bounds__(kBinThreads) void scatter_count_kernel(const Scatte
     for (int i = threadIdx.x; i < a.L; i += kBinThreads) lvlmax[(size_t)blockIdx.x * a.L + i] = lmax[i];
 }
 
-// Threads = kPrefixBins consecutive bins x kPrefixGroups groups of rounds.
-// counts[r][b] <- sum over r' < r of counts[r'][b]; totals[b].  Block x < L
-// also reduces level x's per-round maxima.
-constexpr int kPrefixBins = 8;
-constexpr int kPrefixGroups = 32;
-constexpr int kPrefixThreads = kPrefixBins * kPrefixGroups;
+// Block x: bins [64 x, 64 x + 64), one per lane, and kPrefixWaves waves, each
+// over a contiguous range of rounds (every wave load is one 256-byte row
+// segment).  counts[r][b] <- sum over r' < r of counts[r'][b]; totals[b].
+// Block x < L also reduces level x's per-round maxima.
+constexpr int kPrefixWaves = 16;
+constexpr int kPrefixThreads = 64 * kPrefixWaves;
+constexpr int kPrefixUnroll = 8;
 
 __global__ __launch_bounds__(kPrefixThreads) void scatter_prefix_kernel(const ScatterArgs a, uint32_t* __restrict__ counts,
                                                               uint32_t* __restrict__ totals,
                                                               const uint32_t* __restrict__ lvlmax,
                                                               uint32_t* __restrict__ lvlmax_out)
 {
-    __shared__ uint32_t part[kPrefixGroups][kPrefixBins];
-    __shared__ uint32_t wmax[kPrefixThreads / 64];
-    const int bl = threadIdx.x % kPrefixBins, g = threadIdx.x / kPrefixBins;
-    const int b = blockIdx.x * kPrefixBins + bl;
+    __shared__ uint32_t part[kPrefixWaves][64];
+    __shared__ uint32_t wmax[kPrefixWaves];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int b = blockIdx.x * 64 + lane;
     const int R = a.rounds;
-    const int per = (R + kPrefixGroups - 1) / kPrefixGroups;
-    const int r0 = min(R, g * per), r1 = min(R, r0 + per);
+    const int per = (R + kPrefixWaves - 1) / kPrefixWaves;
+    const int r0 = min(R, w * per), r1 = min(R, r0 + per);
     const bool vb = b < a.bins;
     uint32_t s = 0;
-    if (vb)
-        for (int r = r0; r < r1; r++) s += counts[(size_t)r * a.bins + b];
-    part[g][bl] = s;
+    if (vb) {
+        int r = r0;
+        for (; r + kPrefixUnroll <= r1; r += kPrefixUnroll) {
+            uint32_t c[kPrefixUnroll];
+#pragma unroll
+            for (int k = 0; k < kPrefixUnroll; k++) c[k] = counts[(size_t)(r + k) * a.bins + b];
+#pragma unroll
+            for (int k = 0; k < kPrefixUnroll; k++) s += c[k];
+        }
+        for (; r < r1; r++) s += counts[(size_t)r * a.bins + b];
+    }
+    part[w][lane] = s;
     if ((int)blockIdx.x < a.L) {
         uint32_t m = 0;
         for (int r = threadIdx.x; r < R; r += kPrefixThreads) m = max(m, lvlmax[(size_t)r * a.L + blockIdx.x]);
         m = __ockl_wfred_max_u32(m);
-        if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
+        if (lane == 0) wmax[w] = m;
     }
     __syncthreads();
     if ((int)blockIdx.x < a.L && threadIdx.x == 0) {
         uint32_t m = 0;
-        for (int w = 0; w < kPrefixThreads / 64; w++) m = max(m, wmax[w]);
+        for (int k = 0; k < kPrefixWaves; k++) m = max(m, wmax[k]);
         lvlmax_out[blockIdx.x] = m;
     }
     uint32_t run = 0;
-    for (int k = 0; k < g; k++) run += part[k][bl];
+    for (int k = 0; k < w; k++) run += part[k][lane];
     if (vb) {
-        for (int r = r0; r < r1; r++) {
+        int r = r0;
+        for (; r + kPrefixUnroll <= r1; r += kPrefixUnroll) {
+            uint32_t c[kPrefixUnroll];
+#pragma unroll
+            for (int k = 0; k < kPrefixUnroll; k++) c[k] = counts[(size_t)(r + k) * a.bins + b];
+#pragma unroll
+            for (int k = 0; k < kPrefixUnroll; k++) {
+                counts[(size_t)(r + k) * a.bins + b] = run;
+                run += c[k];
+            }
+        }
+        for (; r < r1; r++) {
             const size_t i = (size_t)r * a.bins + b;
             const uint32_t c = counts[i];
             counts[i] = run;
             run += c;
         }
-        if (g == kPrefixGroups - 1) totals[b] = run;
+        if (w == kPrefixWaves - 1) totals[b] = run;
     }
 }
 
@@ -320,8 +347,9 @@ __device__ uint32_t block_exclusive_scan(const uint32_t* in, uint32_t* out, int 
     return total;
 }
 
-// Chunk table entry: bin, first record, end record, (chunks of the bin) |
-// (staging slot of a multi-chunk bin) << 16.
+// Chunk table entry: bin | (chunk index within the bin) << 16, first record,
+// end record, (chunks of the bin) | (first partial slice of a multi-chunk
+// bin) << 16.
 __global__ __launch_bounds__(kBinThreads) void scatter_distribute_kernel(
     const ScatterArgs a, const float* __restrict__ pos, const _Float16* __restrict__ denc,
     const uint32_t* __restrict__ prefix, const uint32_t* __restrict__ totals, float4* __restrict__ rec,
@@ -329,7 +357,7 @@ __global__ __launch_bounds__(kBinThreads) void scatter_distribute_kernel(
 {
     extern __shared__ uint32_t sh[];
     uint32_t* cur = sh;               // [bins]
-    uint32_t* aux = sh + a.bins;      // [bins] (block 0: chunk starts), then [bins] staging slots
+    uint32_t* aux = sh + a.bins;      // [bins] (block 0: chunk starts), then [bins] partial-slice bases
     __shared__ uint32_t wsum[kBinThreads / 64];
     block_exclusive_scan(totals, cur, a.bins, wsum);
     if (blockIdx.x == 0) {
@@ -338,7 +366,7 @@ __global__ __launch_bounds__(kBinThreads) void scatter_distribute_kernel(
         for (int b = threadIdx.x; b < a.bins; b += kBinThreads) {
             const uint32_t k = (totals[b] + kChunk - 1) / kChunk;
             kst[b] = k;
-            sst[b] = k > 1 ? 1u : 0u;
+            sst[b] = k > 1 ? k : 0u;
         }
         __syncthreads();
         const uint32_t nch = block_exclusive_scan(kst, kst, a.bins, wsum);
@@ -347,8 +375,8 @@ __global__ __launch_bounds__(kBinThreads) void scatter_distribute_kernel(
             const uint32_t t = totals[b];
             const uint32_t k = (t + kChunk - 1) / kChunk;
             for (uint32_t j = 0; j < k; j++)
-                chunks[kst[b] + j] = make_uint4((uint32_t)b, cur[b] + j * kChunk, cur[b] + min((j + 1) * kChunk, t),
-                                                k | (sst[b] << 16));
+                chunks[kst[b] + j] = make_uint4((uint32_t)b | (j << 16), cur[b] + j * kChunk,
+                                                cur[b] + min((j + 1) * kChunk, t), k | (sst[b] << 16));
         }
         if (threadIdx.x == 0) *nchunks = nch;
     }
@@ -413,19 +441,101 @@ __device__ __forceinline__ void add_checked(unsigned long long* acc, float* gl, 
     }
 }
 
+// The fused update's form: a non-finite product marks its gradient
+// non-finite (one bit per gradient of the slice) instead of adding.  Adam
+// takes any non-finite gradient as 0 (finite_or_zero), and the sum the
+// stored path forms from such a product is non-finite whatever else it adds,
+// so the bit is all the update needs.
+__device__ __forceinline__ void add_or_mark(unsigned long long* acc, uint32_t* nf, int i, float c, int e)
+{
+    if (isfinite(c)) lds_add(acc, i, fixed_of(c, e));
+    else atomicOr(&nf[i >> 5], 1u << (i & 31));
+}
+
 __device__ __forceinline__ bool finite_bits(float x) { return (__float_as_uint(x) & 0x7f800000u) != 0x7f800000u; }
 
-__global__ __launch_bounds__(kAccThreads) void scatter_accumulate_kernel(
+
+// Parameters of the fused table update (ADAM): the table [L][T][2] (fp32
+// master, fp16 copy) and its moments.
+struct TableAdamArgs {
+    float* w;
+    _Float16* w16;
+    float* m;
+    float* v;
+    AdamArgs a;
+};
+
+constexpr int kNfWords = 2 * kSlice / 32;  // non-finite bits of one slice
+
+// Adam on entries [s0, s0 + kAdamBatch * kAccThreads) step kAccThreads of one
+// slice (entry elem = base + s): gradient f of entry s is ldexpf(q[2 s + f],
+// -e), or non-finite where its bit is set; entries with neither a nonzero
+// sum nor the bit keep every word (the stored path's zero gradients, which
+// Adam skips).  Only touched features' words are stored.
+constexpr int kAdamBatch = 8;  // entries per thread in flight in the update pass
+
+template <class Q>
+__device__ __forceinline__ void table_adam_batch(const TableAdamArgs& t, size_t base, int s0, int slots, Q&& q,
+                                                 const uint32_t* nfw, int e)
+{
+    constexpr int kBatch = kAdamBatch;
+    bool t0[kBatch], t1[kBatch];
+    float g0[kBatch], g1[kBatch];
+    float2 w[kBatch], m[kBatch], v[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; k++) {
+        const int s = s0 + k * kAccThreads;
+        t0[k] = t1[k] = false;
+        g0[k] = g1[k] = 0.f;
+        if (s < slots) {
+            const long long q0 = q(2 * s), q1 = q(2 * s + 1);
+            const uint32_t bits = nfw[(2 * s) >> 5] >> ((2 * s) & 31);  // 2 s even: both bits in one word
+            const bool n0 = bits & 1u, n1 = (bits >> 1) & 1u;
+            t0[k] = (q0 != 0) | n0;
+            t1[k] = (q1 != 0) | n1;
+            g0[k] = n0 ? __builtin_nanf("") : ldexpf((float)q0, -e);
+            g1[k] = n1 ? __builtin_nanf("") : ldexpf((float)q1, -e);
+        }
+        if (t0[k] | t1[k]) {
+            const size_t i = base + (size_t)s;
+            w[k] = reinterpret_cast<const float2*>(t.w)[i];
+            m[k] = reinterpret_cast<const float2*>(t.m)[i];
+            v[k] = reinterpret_cast<const float2*>(t.v)[i];
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kBatch; k++) {
+        if (!(t0[k] | t1[k])) continue;
+        const size_t i = base + (size_t)(s0 + k * kAccThreads);
+        float2 wk = w[k], mk = m[k], vk = v[k];
+        if (t0[k]) adam_update(g0[k], mk.x, vk.x, wk.x, t.a);
+        if (t1[k]) adam_update(g1[k], mk.y, vk.y, wk.y, t.a);
+        reinterpret_cast<float2*>(t.w)[i] = wk;
+        reinterpret_cast<float2*>(t.m)[i] = mk;
+        reinterpret_cast<float2*>(t.v)[i] = vk;
+        if (t0[k] & t1[k]) {
+            reinterpret_cast<h2*>(t.w16)[i] = h2{to_h(wk.x), to_h(wk.y)};
+        } else {
+            t.w16[2 * i + (t0[k] ? 0 : 1)] = to_h(t0[k] ? wk.x : wk.y);
+        }
+    }
+}
+
+// Two blocks per CU (the LDS holds two slices): at most 128 VGPRs.
+template <bool ADAM>
+__global__ __launch_bounds__(kAccThreads) __attribute__((amdgpu_waves_per_eu(4))) void scatter_accumulate_kernel(
     const ScatterArgs a, const float4* __restrict__ rec, const uint4* __restrict__ chunks,
     const uint32_t* __restrict__ nchunks, const uint32_t* __restrict__ totals, const uint32_t* __restrict__ lvlmax,
-    float* __restrict__ grads, unsigned long long* __restrict__ stage, uint32_t* __restrict__ done, int grads_zero)
+    float* __restrict__ grads, unsigned long long* __restrict__ part, uint32_t* __restrict__ done, int grads_zero,
+    uint32_t* __restrict__ part_nf, const TableAdamArgs ta)
 {
     __shared__ unsigned long long acc[2 * kSlice];
+    __shared__ uint32_t nf[ADAM ? kNfWords : 1];
     __shared__ int s_flag, s_last;
     if (blockIdx.x >= *nchunks) return;
     const uint4 ch = chunks[blockIdx.x];
-    const int bin = (int)ch.x;
-    const uint32_t kb = ch.w & 0xffffu, slot = ch.w >> 16;
+    const int bin = (int)(ch.x & 0xffffu);
+    const uint32_t kb = ch.w & 0xffffu, pbase = ch.w >> 16, pj = ch.x >> 16;
     int l = 0;
     while (l + 1 < a.L && a.bin_base[l + 1] <= bin) l++;
     const int sl = bin - a.bin_base[l];
@@ -445,12 +555,83 @@ __global__ __launch_bounds__(kAccThreads) void scatter_accumulate_kernel(
     const uint32_t tot = totals[bin];
     const int lg = tot <= 1u ? 0 : 32 - __clz(tot - 1u);
     const int e = min(49, 60 - lg) - E;
-    float* gl = grads + ((size_t)l * a.T + elem0) * 2;
+    float* gl = ADAM ? nullptr : grads + ((size_t)l * a.T + elem0) * 2;
+    const size_t ebase = (size_t)l * a.T + elem0;  // first table entry of the slice
     for (int i = threadIdx.x; i < 2 * slots; i += kAccThreads) acc[i] = 0ull;
+    if constexpr (ADAM)
+        for (int i = threadIdx.x; i < kNfWords; i += kAccThreads) nf[i] = 0u;
     if (threadIdx.x == 0) s_flag = 0;
     __syncthreads();
-    // kBatch records per thread in flight before their LDS adds
-    constexpr int kBatch = 4;
+    // records per thread in flight before their LDS adds (hashed bins)
+    constexpr int kBatch = 8;
+    if (l < a.dense_start) {
+        // Dense bins: the distribute pass leaves the records of consecutive
+        // samples of a ray in consecutive slots, and those share corner
+        // pairs.  Each lane takes kRun consecutive records (one 64-byte
+        // piece of the wave's contiguous span) and adds the fixed-point
+        // values of a run of equal keys in registers (exact: integer sums in
+        // any order), with one LDS add per run it holds.
+        constexpr int kRun = 4;
+        constexpr int kGroups = 4;  // runs per lane in flight
+        const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+        constexpr int kWaveSpan = 64 * kRun;
+        for (uint32_t b0 = ch.y + (uint32_t)wv * kWaveSpan; b0 < ch.z;
+             b0 += (uint32_t)kGroups * kAccThreads * kRun) {
+            float4 r[kGroups][kRun];
+#pragma unroll
+            for (int gi = 0; gi < kGroups; gi++)
+#pragma unroll
+                for (int k = 0; k < kRun; k++) {
+                    const uint32_t i = b0 + (uint32_t)gi * kAccThreads * kRun + (uint32_t)(lane * kRun + k);
+                    r[gi][k] = i < ch.z ? rec[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+                }
+#pragma unroll
+            for (int gi = 0; gi < kGroups; gi++) {
+                uint32_t cur = 0xffffffffu;
+                long long q[4] = {0, 0, 0, 0};
+                auto flush = [&]() {
+                    if (cur == 0xffffffffu) return;
+                    const int s0 = (int)(cur & 0xffffu), s1 = (int)(cur >> 16);
+                    if (q[0]) lds_add(acc, 2 * s0, q[0]);
+                    if (q[1]) lds_add(acc, 2 * s0 + 1, q[1]);
+                    if (q[2]) lds_add(acc, 2 * s1, q[2]);
+                    if (q[3]) lds_add(acc, 2 * s1 + 1, q[3]);
+                };
+#pragma unroll
+                for (int k = 0; k < kRun; k++) {
+                    const uint32_t i = b0 + (uint32_t)gi * kAccThreads * kRun + (uint32_t)(lane * kRun + k);
+                    if (i >= ch.z) break;
+                    const uint32_t key = __float_as_uint(r[gi][k].x);
+                    if (key != cur) {
+                        flush();
+                        cur = key;
+                        q[0] = q[1] = q[2] = q[3] = 0;
+                    }
+                    const int s0 = (int)(key & 0xffffu), s1 = (int)(key >> 16);
+                    const float v0 = r[gi][k].y, v1 = r[gi][k].z, wx = r[gi][k].w, ux = 1.0f - wx;
+                    const float c[4] = {v0 * wx, v1 * wx, v0 * ux, v1 * ux};
+                    const int at[4] = {2 * s0, 2 * s0 + 1, 2 * s1, 2 * s1 + 1};
+                    if (finite_bits(v0) & finite_bits(v1) & finite_bits(wx)) {
+#pragma unroll
+                        for (int j = 0; j < 4; j++) q[j] += fixed_of(c[j], e);
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < 4; j++) {
+                            if (isfinite(c[j])) {
+                                q[j] += fixed_of(c[j], e);
+                            } else if constexpr (ADAM) {
+                                atomicOr(&nf[at[j] >> 5], 1u << (at[j] & 31));
+                            } else {
+                                atomic_add_f32(gl + at[j], c[j]);
+                                s_flag = 1;
+                            }
+                        }
+                    }
+                }
+                flush();
+            }
+        }
+    } else
     for (uint32_t i0 = ch.y + threadIdx.x; i0 < ch.z; i0 += kBatch * kAccThreads) {
         float4 r[kBatch];
 #pragma unroll
@@ -470,6 +651,11 @@ __global__ __launch_bounds__(kAccThreads) void scatter_accumulate_kernel(
                 lds_add(acc, 2 * s0 + 1, fixed_of(v1 * wx, e));
                 lds_add(acc, 2 * s1, fixed_of(v0 * ux, e));
                 lds_add(acc, 2 * s1 + 1, fixed_of(v1 * ux, e));
+            } else if constexpr (ADAM) {
+                add_or_mark(acc, nf, 2 * s0, v0 * wx, e);
+                add_or_mark(acc, nf, 2 * s0 + 1, v1 * wx, e);
+                add_or_mark(acc, nf, 2 * s1, v0 * ux, e);
+                add_or_mark(acc, nf, 2 * s1 + 1, v1 * ux, e);
             } else {
                 add_checked(acc, gl, 2 * s0, v0 * wx, e, &s_flag);
                 add_checked(acc, gl, 2 * s0 + 1, v1 * wx, e, &s_flag);
@@ -479,8 +665,66 @@ __global__ __launch_bounds__(kAccThreads) void scatter_accumulate_kernel(
         }
     }
     __syncthreads();
-    if (kb == 1) {
-        // sole owner of the slice
+    if (kb > 1) {
+        // A bin of several chunks: every chunk stores its sums (and non-finite
+        // bits) as a partial slice; the last one to finish adds them all up
+        // (exact integer sums) and finishes the bin as its sole owner.
+        unsigned long long* mine = part + (size_t)(pbase + pj) * (2 * kSlice);
+        for (int i = threadIdx.x; i < 2 * slots; i += kAccThreads) mine[i] = acc[i];
+        if constexpr (ADAM) {
+            uint32_t* mnf = part_nf + (size_t)(pbase + pj) * kNfWords;
+            for (int i = threadIdx.x; i < kNfWords; i += kAccThreads) mnf[i] = nf[i];
+        }
+        // done[bin]: chunks finished; done[kMaxBins + bin]: non-finite atomics seen
+        if (!ADAM && threadIdx.x == 0 && s_flag)
+            __hip_atomic_fetch_or(done + kMaxBins + bin, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __threadfence();
+        __syncthreads();
+        if (threadIdx.x == 0)
+            s_last = __hip_atomic_fetch_add(done + bin, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == kb - 1;
+        __syncthreads();
+        if (!s_last) return;
+        __threadfence();  // acquire: the other chunks' partial slices are visible
+        // the other chunks' sums onto this one's (still in LDS): each thread
+        // adds the words it owns, kMergeBatch loads in flight
+        constexpr int kMergeBatch = 2 * kSlice / kAccThreads;
+        for (uint32_t c = 0; c < kb; c++) {
+            if (c == pj) continue;
+            const unsigned long long* other = part + (size_t)(pbase + c) * (2 * kSlice);
+            unsigned long long t[kMergeBatch];
+#pragma unroll
+            for (int k = 0; k < kMergeBatch; k++) {
+                const int i = threadIdx.x + k * kAccThreads;
+                t[k] = i < 2 * slots ? other[i] : 0ull;
+            }
+#pragma unroll
+            for (int k = 0; k < kMergeBatch; k++) {
+                const int i = threadIdx.x + k * kAccThreads;
+                if (i < 2 * slots) acc[i] += t[k];
+            }
+            if constexpr (ADAM) {
+                const uint32_t* onf = part_nf + (size_t)(pbase + c) * kNfWords;
+                for (int i = threadIdx.x; i < kNfWords; i += kAccThreads) nf[i] |= onf[i];
+            }
+        }
+        if (threadIdx.x == 0) {
+            if (!ADAM && __hip_atomic_load(done + kMaxBins + bin, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+                s_flag = 1;
+            done[bin] = 0u;
+            done[kMaxBins + bin] = 0u;
+        }
+        __syncthreads();
+    }
+    // the sole owner of the slice's sums
+    if constexpr (ADAM) {
+        // update every entry the sums reached
+        for (int s0 = threadIdx.x; s0 < slots; s0 += kAdamBatch * kAccThreads)
+            table_adam_batch(ta, ebase, s0, slots, [&](int i) { return (long long)acc[i]; }, nf, e);
+        return;
+    }
+    {
+        // non-finite products went to the entries by fp32 atomics: then the
+        // sums follow by atomics too
         const bool atomic = s_flag != 0;
         float2* g2 = reinterpret_cast<float2*>(gl);
         if (atomic || grads_zero) {
@@ -512,28 +756,7 @@ __global__ __launch_bounds__(kAccThreads) void scatter_accumulate_kernel(
                 }
             }
         }
-        return;
     }
-    unsigned long long* sg = stage + (size_t)slot * (2 * kSlice);
-    for (int i = threadIdx.x; i < 2 * slots; i += kAccThreads) {
-        const unsigned long long q = acc[i];
-        if (q) __hip_atomic_fetch_add(sg + i, q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0)
-        s_last = __hip_atomic_fetch_add(done + slot, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == kb - 1;
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    for (int i = threadIdx.x; i < 2 * slots; i += kAccThreads) {
-        const long long q = (long long)__hip_atomic_load(sg + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (q) {
-            atomic_add_f32(gl + i, ldexpf((float)q, -e));
-            sg[i] = 0ull;
-        }
-    }
-    if (threadIdx.x == 0) done[slot] = 0u;
 }
 
 }  // namespace
@@ -552,8 +775,9 @@ struct ScatterPlan {
     uint32_t* lvlmax_final = nullptr;
     uint4* chunks = nullptr;
     uint32_t* nchunks = nullptr;
-    unsigned long long* stage = nullptr;
-    uint32_t* done = nullptr;
+    unsigned long long* part = nullptr;  // partial slices of the chunks of multi-chunk bins
+    uint32_t* done = nullptr;            // [2 kMaxBins]: chunks finished, non-finite atomics seen
+    uint32_t* part_nf = nullptr;         // non-finite bits of the partial slices (fused table update)
 };
 
 namespace {
@@ -585,7 +809,12 @@ bool layout(const GridMeta& m, ScatterArgs& a)
         if (l < m.denseLevelStart) {
             const long long st = (long long)m.res[l] + 1;
             if (st > kSlice) return false;
-            const int rps = (int)(kSlice / st);
+            // about kDenseBins bins per level (at most kSlice entries each): a
+            // coarse level's few entries take a contribution from nearly
+            // every sample, so its records are spread over as many blocks
+            // as a fine level's
+            const long long rows = st * st;
+            const int rps = (int)std::max(1LL, std::min((long long)(kSlice / st), (rows + kDenseBins - 1) / kDenseBins));
             a.rows_per_slice[l] = rps;
             bins += (int)((st * st + rps - 1) / rps);
         } else {
@@ -606,30 +835,38 @@ size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
 
 namespace {
 
-// Byte offsets of a plan's buffers.  The int64 staging slices of multi-chunk
-// bins and their counters come first: kernels leave them zero after every
-// call, so a region that starts zero stays zero whatever the configuration.
+// Byte offsets of a plan's buffers.  The per-bin counters come first:
+// kernels leave them zero after every call, so a region that starts zero
+// stays zero whatever the configuration.
 struct PlanLayout {
-    size_t o_stg, o_don, o_rec, o_cnt, o_tot, o_lmx, o_lmf, o_chk, o_nch, zero_end, bytes;
+    size_t o_don, o_prt, o_pnf, o_rec, o_cnt, o_tot, o_lmx, o_lmf, o_chk, o_nch, zero_end, bytes;
 };
 
-bool plan_shape(const GridMeta& m, int maxN, ScatterPlan& p, PlanLayout& lay, int max_multi_cap = 0)
+// Partial slices: every chunk of a multi-chunk bin has one; a bin of t > kChunk
+// records has ceil(t / kChunk) < t / kChunk + 1 chunks and there are fewer
+// than recs / kChunk such bins, so 2 recs / kChunk + 1 slices suffice.
+// with_nf: room for the fused table update's non-finite bits of every
+// partial slice (plans of the training step; the allocation-free plan has
+// none).
+bool plan_shape(const GridMeta& m, int maxN, ScatterPlan& p, PlanLayout& lay, int max_multi_cap = 0,
+                bool with_nf = false)
 {
     ScatterArgs a;
     if (maxN < 1 || !layout(m, a)) return false;
     const unsigned long long recs = 4ull * (unsigned long long)m.numLevels * (unsigned long long)maxN;
-    if (recs >= (1ull << 31)) return false;
+    if (recs >= (1ull << 30)) return false;  // chunk and partial indices stay below 2^16
     a.rounds = (maxN + kRound - 1) / kRound;
     p.maxN = maxN;
     p.meta = m;
     p.args = a;
     p.max_chunks = (int)(recs / kChunk) + a.bins + 1;
-    p.max_multi = (int)std::min<unsigned long long>(recs / kChunk + 1, (unsigned long long)a.bins);
+    p.max_multi = (int)(2 * (recs / kChunk) + 1);
     const int multi = std::max(p.max_multi, max_multi_cap);
     size_t off = 0;
-    lay.o_stg = off; off = align_up(off + (size_t)multi * 2 * kSlice * 8);
-    lay.o_don = off; off = align_up(off + (size_t)multi * 4);
+    lay.o_don = off; off = align_up(off + (size_t)2 * kMaxBins * 4);
     lay.zero_end = off;
+    lay.o_prt = off; off = align_up(off + (size_t)multi * 2 * kSlice * 8);
+    lay.o_pnf = off; off = align_up(off + (with_nf ? (size_t)multi * kNfWords * 4 : 0));
     lay.o_rec = off; off = align_up(off + recs * sizeof(float4));
     lay.o_cnt = off; off = align_up(off + (size_t)a.rounds * a.bins * 4);
     lay.o_tot = off; off = align_up(off + (size_t)a.bins * 4);
@@ -651,8 +888,9 @@ void plan_bind(ScatterPlan& p, char* base, const PlanLayout& lay)
     p.lvlmax_final = reinterpret_cast<uint32_t*>(base + lay.o_lmf);
     p.chunks = reinterpret_cast<uint4*>(base + lay.o_chk);
     p.nchunks = reinterpret_cast<uint32_t*>(base + lay.o_nch);
-    p.stage = reinterpret_cast<unsigned long long*>(base + lay.o_stg);
+    p.part = reinterpret_cast<unsigned long long*>(base + lay.o_prt);
     p.done = reinterpret_cast<uint32_t*>(base + lay.o_don);
+    p.part_nf = lay.o_pnf < lay.o_rec ? reinterpret_cast<uint32_t*>(base + lay.o_pnf) : nullptr;
 }
 
 }  // namespace
@@ -661,7 +899,7 @@ ScatterPlan* scatter_plan_create(const GridMeta& m, int maxN)
 {
     auto* p = new ScatterPlan();
     PlanLayout lay;
-    if (!plan_shape(m, maxN, *p, lay)) {
+    if (!plan_shape(m, maxN, *p, lay, 0, /*with_nf=*/true)) {
         delete p;
         return nullptr;
     }
@@ -672,7 +910,7 @@ ScatterPlan* scatter_plan_create(const GridMeta& m, int maxN)
         GRAFT_HIP_CHECK(e);
     }
     plan_bind(*p, static_cast<char*>(mem), lay);
-    // the staging slices and their counters start (and are left) zero
+    // the per-bin counters start (and are left) zero
     e = hipMemset(mem, 0, lay.zero_end);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
@@ -692,14 +930,20 @@ void scatter_plan_destroy(ScatterPlan* p)
 
 int scatter_plan_max_samples(const ScatterPlan* p) { return p ? p->maxN : 0; }
 
-void hash_scatter_binned(ScatterPlan* p, const GridMeta& m, const __half* denc, const float* pos, int pos_stride,
-                         float* grads, int N, hipStream_t stream, const uint32_t* d_n, bool grads_zero)
+namespace {
+
+// count, prefix, distribute, then (after wait_before, when given) accumulate:
+// into grads, or (ta) as the fused table update.
+void scatter_launch(ScatterPlan* p, const GridMeta& m, const __half* denc, const float* pos, int pos_stride,
+                    float* grads, int N, hipStream_t stream, const uint32_t* d_n, bool grads_zero,
+                    const TableAdamArgs* ta, hipEvent_t wait_before)
 {
     if (N <= 0) return;
     if (!p) throw std::runtime_error("hash scatter: no scatter plan");
     if (pos_stride < 3) throw std::runtime_error("hash scatter: position stride must be >= 3");
     if (N > p->maxN) throw std::runtime_error("hash scatter: batch exceeds the plan's sample capacity");
     if (!same_meta(p->meta, m)) throw std::runtime_error("hash scatter: plan built for another grid");
+    if (ta && !p->part_nf) throw std::runtime_error("hash scatter: plan without the fused update's scratch");
     ScatterArgs a = p->args;
     a.d_n = d_n;
     a.N = N;
@@ -711,7 +955,7 @@ void hash_scatter_binned(ScatterPlan* p, const GridMeta& m, const __half* denc, 
     hipLaunchKernelGGL(scatter_count_kernel, dim3(a.rounds), dim3(kBinThreads), lds_count, stream, a, pos, dh,
                        p->counts, p->lvlmax);
     GRAFT_LAUNCH_CHECK();
-    const int prefix_blocks = std::max((a.bins + kPrefixBins - 1) / kPrefixBins, a.L);
+    const int prefix_blocks = std::max((a.bins + 63) / 64, a.L);
     hipLaunchKernelGGL(scatter_prefix_kernel, dim3(prefix_blocks), dim3(kPrefixThreads), 0, stream, a, p->counts, p->totals,
                        p->lvlmax, p->lvlmax_final);
     GRAFT_LAUNCH_CHECK();
@@ -719,11 +963,34 @@ void hash_scatter_binned(ScatterPlan* p, const GridMeta& m, const __half* denc, 
     hipLaunchKernelGGL(scatter_distribute_kernel, dim3(a.rounds), dim3(kBinThreads), lds_dist, stream, a, pos, dh,
                        p->counts, p->totals, p->rec, cap, p->chunks, p->nchunks);
     GRAFT_LAUNCH_CHECK();
+    if (wait_before) GRAFT_HIP_CHECK(hipStreamWaitEvent(stream, wait_before, 0));
     const unsigned long long recs = 4ull * (unsigned long long)a.L * (unsigned long long)N;
     const int grid = (int)std::min<unsigned long long>(recs / kChunk + a.bins + 1, (unsigned long long)p->max_chunks);
-    hipLaunchKernelGGL(scatter_accumulate_kernel, dim3(grid), dim3(kAccThreads), 0, stream, a, p->rec, p->chunks,
-                       p->nchunks, p->totals, p->lvlmax_final, grads, p->stage, p->done, grads_zero ? 1 : 0);
+    if (ta)
+        hipLaunchKernelGGL(scatter_accumulate_kernel<true>, dim3(grid), dim3(kAccThreads), 0, stream, a, p->rec,
+                           p->chunks, p->nchunks, p->totals, p->lvlmax_final, nullptr, p->part, p->done, 0,
+                           p->part_nf, *ta);
+    else
+        hipLaunchKernelGGL(scatter_accumulate_kernel<false>, dim3(grid), dim3(kAccThreads), 0, stream, a, p->rec,
+                           p->chunks, p->nchunks, p->totals, p->lvlmax_final, grads, p->part, p->done,
+                           grads_zero ? 1 : 0, nullptr, TableAdamArgs{});
     GRAFT_LAUNCH_CHECK();
+}
+
+}  // namespace
+
+void hash_scatter_binned(ScatterPlan* p, const GridMeta& m, const __half* denc, const float* pos, int pos_stride,
+                         float* grads, int N, hipStream_t stream, const uint32_t* d_n, bool grads_zero)
+{
+    scatter_launch(p, m, denc, pos, pos_stride, grads, N, stream, d_n, grads_zero, nullptr, nullptr);
+}
+
+void hash_scatter_adam(ScatterPlan* p, const GridMeta& m, const __half* denc, const float* pos, int pos_stride, int N,
+                       const TableAdam& t, hipStream_t stream, const uint32_t* d_n, hipEvent_t wait_before_update)
+{
+    if (!t.w || !t.w16 || !t.m || !t.v) throw std::runtime_error("hash scatter: null table or moment array");
+    const TableAdamArgs ta{t.w, reinterpret_cast<_Float16*>(t.w16), t.m, t.v, t.a};
+    scatter_launch(p, m, denc, pos, pos_stride, nullptr, N, stream, d_n, false, &ta, wait_before_update);
 }
 
 namespace {
@@ -766,19 +1033,18 @@ void hash_scatter(const GridMeta& m, const __half* denc, const float* pos, int p
 // ---------------------------------------------------------------------------
 // Allocation-free variant.  The scratch is one file-scope device array per
 // GPU (kNoAllocBytes; each GPU the library runs on keeps it until the process
-// ends).  Its staging region (offset 0, sized for the most multi-chunk bins a
-// sub-batch can have) starts zero and every call leaves it zero; the rest is
-// rewritten by every call.  Batches above one sub-batch run as consecutive
+// ends).  Its per-bin counters (offset 0) start zero and every call leaves
+// them zero; the rest is rewritten by every call.  Batches above one sub-batch run as consecutive
 // sub-batches on the caller's stream.  All calls on one GPU share the array:
 // calls that overlap on one GPU (two streams, or two threads) race.
 // ---------------------------------------------------------------------------
 
 namespace {
 
-constexpr size_t kNoAllocBytes = (size_t)40 << 20;
+constexpr size_t kNoAllocBytes = (size_t)48 << 20;
 constexpr unsigned long long kNoAllocRecords = 1ull << 21;  // corner-pair records per sub-batch
 constexpr size_t kNoAllocCountWords = (size_t)1 << 20;       // rounds x bins per sub-batch
-constexpr int kNoAllocMulti = (int)(kNoAllocRecords / kChunk) + 1;
+constexpr int kNoAllocMulti = (int)(2 * (kNoAllocRecords / kChunk)) + 1;  // partial slices per sub-batch
 constexpr int kMaxDevices = 64;
 
 static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
@@ -792,7 +1058,7 @@ __global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* p, size_t n)
         p[i] = 0u;
 }
 
-// The array's device address on the current GPU (looked up, and its staging
+// The array's device address on the current GPU (looked up, and its counter
 // region cleared on the caller's stream, on the first call on each GPU).
 char* noalloc_base(hipStream_t stream, size_t zero_bytes)
 {

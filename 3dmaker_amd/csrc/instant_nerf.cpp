@@ -643,14 +643,19 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         // The scatter is the step's critical path: it is enqueued before the
         // side streams' work, so that the host's launches of that work never
         // delay it.
+        // With the binned scatter the table's Adam update is fused into it
+        // (every entry the batch reaches is updated as its sum completes; no
+        // gradient array).  The update waits for a refresh of this step, which
+        // reads the table.
+        const bool fused_table = db.scatter_plan != nullptr;
         stage("hashScatter", [&] {
-            // the table gradient is all zero here: the previous step's Adam
-            // cleared every entry it consumed
-            if (db.scatter_plan)
-                graft::hash_scatter_binned(static_cast<graft::ScatterPlan*>(db.scatter_plan), b.meta, db.dx_out,
-                                           reinterpret_cast<const float*>(S.positions), 4, db.hashtable_grads,
-                                           (int)Bn, stream, d_hits, /*grads_zero=*/true);
+            if (fused_table)
+                m_densityMLP->scatterAdamTable(db.dx_out, reinterpret_cast<const float*>(S.positions), 4, (int)Bn,
+                                               d_hits, o.learningRate, o.beta1, o.beta2, o.epsilon, o.lossScale,
+                                               stream, refresh ? b.ev_join : nullptr);
             else
+                // the table gradient is all zero here: the previous step's
+                // Adam cleared every entry it consumed
                 graft::hash_scatter_atomic(b.meta, db.dx_out, reinterpret_cast<const float*>(S.positions), 4,
                                            db.hashtable_grads, (int)Bn, stream, d_hits);
         });
@@ -714,7 +719,8 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
             });
         }
         // Adam: MLP layers of both heads on the side stream, the hash table on
-        // the main stream.  The colour head's needs nothing of the refresh;
+        // the main stream (in the scatter above when that is the binned one).
+        // The colour head's needs nothing of the refresh;
         // the density head's (and, after it on the side stream, the next
         // batch's march) waits until the refresh has read the parameters and
         // written the grid.
@@ -725,9 +731,14 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
             GRAFT_HIP_CHECK(hipStreamWaitEvent(stream, b.ev_join, 0));
             GRAFT_HIP_CHECK(hipStreamWaitEvent(b.side, b.ev_join, 0));
         }
-        stage("densityOpt", [&] {
-            m_densityMLP->stepSplit(o.learningRate, o.beta1, o.beta2, o.epsilon, o.lossScale, b.side, stream);
-        });
+        if (fused_table)
+            stage_on(b.side, "densityOpt", [&] {
+                m_densityMLP->stepMlp(o.learningRate, o.beta1, o.beta2, o.epsilon, o.lossScale, b.side);
+            });
+        else
+            stage("densityOpt", [&] {
+                m_densityMLP->stepSplit(o.learningRate, o.beta1, o.beta2, o.epsilon, o.lossScale, b.side, stream);
+            });
         GRAFT_HIP_CHECK(hipEventRecord(b.ev_opt, b.side));
         opt_recorded = true;
 

@@ -9,6 +9,7 @@
 #include "abi_error.h"
 #include "capi_handles.h"
 #include "nerf.h"
+#include "nerf_heads.h"
 #include "nerf_math.h"
 #include "occupancy.h"
 
@@ -296,6 +297,92 @@ void launchComputeRealSHDegree3(const uint32_t total_hits, const float3* d_direc
         if (total_hits == 0) return;
         require_aligned16(d_out_sh, "d_out_sh");
         graft::sh_degree3(total_hits, d_directions, d_out_sh, stream);
+    });
+}
+
+size_t nerfHeadsPackedBytes(void) { return graft::nerf_heads_packed_bytes(); }
+
+void launchNerfHeadsPack(const GRAFT_HALF* const* d_density_w, const float* const* d_density_b,
+                         const GRAFT_HALF* const* d_color_w, const float* const* d_color_b, void* d_packed,
+                         hipStream_t stream)
+{
+    guarded("launchNerfHeadsPack", [&] {
+        if (!d_density_w || !d_density_b || !d_color_w || !d_color_b || !d_packed)
+            throw std::runtime_error("null argument");
+        graft::nerf_heads_pack(graft::NerfHeadsWeights{d_density_w, d_density_b, d_color_w, d_color_b}, d_packed,
+                               stream);
+    });
+}
+
+void launchNerfHeadsForward(const void* d_packed, const GRAFT_HALF* d_enc, int enc_plane, int levels,
+                            const float3* d_dirs, const uint32_t* d_ray_indices, int num_samples,
+                            float density_bias, int color_activation, float* d_sigma, float* d_density_out,
+                            float* d_color_out, GRAFT_HALF* d_color_in, hipStream_t stream)
+{
+    guarded("launchNerfHeadsForward", [&] {
+        if (num_samples < 0) throw std::runtime_error("num_samples must be >= 0");
+        if (!d_packed || !d_enc || !d_dirs || !d_ray_indices || !d_sigma || !d_color_out)
+            throw std::runtime_error("null argument");
+        graft::NerfHeadsFwd h;
+        h.packed = d_packed;
+        h.enc = d_enc;
+        h.enc_plane = enc_plane;
+        h.levels = levels;
+        h.dirs = d_dirs;
+        h.ray_idx = d_ray_indices;
+        h.density_bias = density_bias;
+        h.out_act = color_activation;
+        h.sigma = d_sigma;
+        h.density_out = d_density_out;
+        h.color_out = d_color_out;
+        h.color_in = d_color_in;
+        graft::nerf_heads_forward(h, num_samples, stream);
+    });
+}
+
+static graft::NerfHeadsBwd heads_bwd(const void* d_packed, const GRAFT_HALF* d_enc, int enc_plane, int levels,
+                                     const GRAFT_HALF* d_color_in, const GRAFT_HALF* d_color_dy, const float* d_dsigma)
+{
+    if (!d_packed || !d_enc || !d_color_in || !d_color_dy || !d_dsigma) throw std::runtime_error("null argument");
+    graft::NerfHeadsBwd h;
+    h.packed = d_packed;
+    h.enc = d_enc;
+    h.enc_plane = enc_plane;
+    h.levels = levels;
+    h.color_in = d_color_in;
+    h.color_dy = d_color_dy;
+    h.dsigma = d_dsigma;
+    return h;
+}
+
+void launchNerfHeadsBackward(const void* d_packed, const GRAFT_HALF* d_enc, int enc_plane, int levels,
+                             const GRAFT_HALF* d_color_in, const GRAFT_HALF* d_color_dy, const float* d_dsigma,
+                             int num_samples, GRAFT_HALF* d_denc, GRAFT_HALF* d_density_dy, GRAFT_HALF* d_color_dx,
+                             hipStream_t stream)
+{
+    guarded("launchNerfHeadsBackward", [&] {
+        if (num_samples < 0) throw std::runtime_error("num_samples must be >= 0");
+        if (!d_denc) throw std::runtime_error("null argument");
+        graft::NerfHeadsBwd h = heads_bwd(d_packed, d_enc, enc_plane, levels, d_color_in, d_color_dy, d_dsigma);
+        h.denc = d_denc;
+        h.density_dy = d_density_dy;
+        h.color_dx = d_color_dx;
+        graft::nerf_heads_dx(h, num_samples, stream);
+    });
+}
+
+void launchNerfHeadsWeightGrads(const void* d_packed, const GRAFT_HALF* d_enc, int enc_plane, int levels,
+                                const GRAFT_HALF* d_color_in, const GRAFT_HALF* d_color_dy, const float* d_dsigma,
+                                int num_samples, float* const* d_density_dw, float* const* d_density_db,
+                                float* const* d_color_dw, float* const* d_color_db, hipStream_t stream)
+{
+    guarded("launchNerfHeadsWeightGrads", [&] {
+        if (num_samples < 0) throw std::runtime_error("num_samples must be >= 0");
+        if (!d_density_dw || !d_density_db || !d_color_dw || !d_color_db) throw std::runtime_error("null argument");
+        const graft::NerfHeadsBwd h =
+            heads_bwd(d_packed, d_enc, enc_plane, levels, d_color_in, d_color_dy, d_dsigma);
+        graft::nerf_heads_dw(h, graft::NerfHeadsGrads{d_density_dw, d_density_db, d_color_dw, d_color_db},
+                             num_samples, stream);
     });
 }
 

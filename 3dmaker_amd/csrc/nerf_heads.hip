@@ -909,7 +909,8 @@ void nerf_heads_dx(const NerfHeadsBwd& a, int N, hipStream_t s, const uint32_t* 
 void nerf_heads_dw(const NerfHeadsBwd& a, const NerfHeadsGrads& out, int N, hipStream_t s, const uint32_t* d_n,
                    Workspace* ws)
 {
-    if (N <= 0) return;
+    // N = 0 still runs: the gradients are overwritten with zeros
+    if (N < 0) return;
     BwdParams p = bwd_params(a, N, d_n);
     const int lds = (int)std::max(kTrBytes + kFwdBytes, (size_t)PC * sizeof(float));
     // one block per CU for each head (the colour head's has the more work)

@@ -11,28 +11,13 @@
 // exactly 0.0f skip the m/v/w reads, every consumed gradient is zeroed.
 #include "optimizer.h"
 
+#include "adam_math.h"
+
 #include <algorithm>
 
 namespace graft {
 
 namespace {
-
-__device__ __forceinline__ float finite_or_zero(float x) { return isfinite(x) ? x : 0.0f; }
-
-__device__ __forceinline__ void adam_update(float graw, float& m, float& v, float& w, const AdamArgs& a)
-{
-    const float g = finite_or_zero(graw * a.inv_scale);
-    const float mv = a.b1 * finite_or_zero(m) + (1.0f - a.b1) * g;
-    const float vv = a.b2 * finite_or_zero(v) + ((1.0f - a.b2) * g) * g;
-    const float mh = mv / a.bc1;
-    const float vh = vv / a.bc2;
-    float wv = isfinite(w) ? w : 0.0f;
-    wv = wv - ((a.lr * mh) / (sqrtf(vh) + a.eps));
-    if (!isfinite(wv)) wv = 0.0f;
-    m = mv;
-    v = vv;
-    w = wv;
-}
 
 __global__ __launch_bounds__(256) void adam_hash_kernel(float* __restrict__ w, _Float16* __restrict__ w16,
                                                         float* __restrict__ g, float* __restrict__ m,

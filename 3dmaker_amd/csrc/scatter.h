@@ -2,6 +2,7 @@
 #pragma once
 
 #include "common.h"
+#include "optimizer.h"
 
 namespace graft {
 
@@ -26,6 +27,24 @@ int scatter_plan_max_samples(const ScatterPlan* p);
 void hash_scatter_binned(ScatterPlan* p, const GridMeta& m, const __half* denc, const float* pos,
                          int pos_stride, float* grads, int N, hipStream_t stream, const uint32_t* d_n,
                          bool grads_zero);
+
+// The table half of the training step's optimizer step fused into the
+// scatter: every table entry [L][T][2] the scatter of denc reaches takes its
+// Adam update (adam_hash's arithmetic) from the gradient hash_scatter_binned
+// with grads_zero would have stored, in the same pass; no gradient array is
+// read or written, entries the batch does not reach keep every word (the
+// zero gradients adam_hash skips).  The update waits for wait_before_update
+// (nullable) after the sorting passes, before its first table read.
+struct TableAdam {
+    float* w;       // fp32 master table
+    __half* w16;    // fp16 copy the encode reads
+    float* m;
+    float* v;
+    AdamArgs a;
+};
+void hash_scatter_adam(ScatterPlan* p, const GridMeta& m, const __half* denc, const float* pos, int pos_stride, int N,
+                       const TableAdam& t, hipStream_t stream, const uint32_t* d_n = nullptr,
+                       hipEvent_t wait_before_update = nullptr);
 
 // hash_scatter_binned's sum (grads +=) with the scratch in a fixed static
 // device array instead of allocated memory: no allocation on any call.  The

@@ -810,6 +810,30 @@ void TinyMLPHashGrid::stepSplit(float lr, float beta1, float beta2, float epsilo
                      (size_t)m_totalHashElements, a, hash_stream);
 }
 
+void TinyMLPHashGrid::scatterAdamTable(const half* d_dx_out, const float* d_positions, int pos_stride, int N,
+                                       const uint32_t* d_n, float lr, float beta1, float beta2, float epsilon,
+                                       float loss_scale, hipStream_t stream, hipEvent_t wait_before_update)
+{
+    if (!m_isTraining) throw std::runtime_error("step called while in inference mode!");
+    if (!m_scatter) throw std::runtime_error("scatterAdamTable: this grid has no binned scatter");
+    // the step count the next stepMlp() takes
+    const int next = current_step < 50000 ? current_step + 1 : current_step;
+    const graft::TableAdam t{d_master_hashtable, d_fwd_hashtable, d_hash_m, d_hash_v,
+                             adam_args(next, lr, beta1, beta2, epsilon, loss_scale)};
+    graft::hash_scatter_adam(static_cast<graft::ScatterPlan*>(m_scatter), META, d_dx_out, d_positions, pos_stride, N,
+                             t, stream, d_n, wait_before_update);
+}
+
+void TinyMLPHashGrid::stepMlp(float lr, float beta1, float beta2, float epsilon, float loss_scale, hipStream_t stream)
+{
+    if (!m_isTraining) throw std::runtime_error("step called while in inference mode!");
+    if (current_step < 50000) current_step++;
+    const AdamArgs a = adam_args(current_step, lr, beta1, beta2, epsilon, loss_scale);
+    const Dims d = dims_of(mlp_opt);
+    graft::adam_dense(d_master_weights, d_fwd_weights, d_w_grad, d_w_m, d_w_v, d.wsizes(), d_master_biases,
+                      d_b_grad, d_b_m, d_b_v, d.bsizes(), d.layers, a, stream);
+}
+
 // TinyMLPHashGrid.cu:394-455: raw MLPGridOptions header, fp32 table, then W, B per layer.
 void TinyMLPHashGrid::loadWeights(const std::string& filename)
 {

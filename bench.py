@@ -65,6 +65,8 @@ ENC_BYTES_PER_SAMPLE = 16 + L * 8 * 4 + 2 * L * 2                    # 592
 SCATTER_BYTES_PER_SAMPLE = 16 + 2 * L * 2 + L * 8 * 2 * 8               # 2,128 (pos 16 + denc 64 + RMW 2,048)
 ADAM_BYTES_PER_PARAM = 34
 MLP_FLOP_PER_SAMPLE = 3 * (2 * (32 * 64 + 64 * 16) + 2 * (32 * 64 + 64 * 64 + 64 * 3))  # 56,448 fwd + bwd
+# the same minus the colour head's dL/d(SH features), which nothing consumes: 54,400
+HEADS_FLOP_PER_SAMPLE = MLP_FLOP_PER_SAMPLE - 2 * 16 * 64
 COPY_BYTES = 256 << 20         # copy-calibration kernel of the PMC runs (read and write each)
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
@@ -416,6 +418,75 @@ def five_cascades(P, torch, feed, hfeed, sp):
     return out
 
 
+def heads_components(P, torch, dev, rng, x, d_dirs, ridx, sp, timed):
+    """The training step's heads (launchNerfHeads*: density 32-64-16 and colour 32-64-64-3 on the 16x16x32
+    MFMA, hidden activations recomputed in the backward) at 2^18, on the same inputs as the TinyMLP leg:
+    forward, dX chains, weight gradients, each alone and the three in sequence."""
+    lib = P.lib()
+
+    def layers(shape, seed):
+        inD, hid, outD, nl = shape
+        r = np.random.default_rng(seed)
+        ws, bs = [], []
+        for l in range(nl):
+            o, i = (outD if l == nl - 1 else hid), (inD if l == 0 else hid)
+            ws.append(torch.from_numpy(r.uniform(-1, 1, o * i).astype(np.float16) * np.float16(np.sqrt(6 / (o + i))))
+                      .to(dev))
+            bs.append(torch.zeros(o, device=dev))
+        ptrs = lambda ts: torch.tensor([t.data_ptr() for t in ts], dtype=torch.int64, device=dev)  # noqa: E731
+        gw = [torch.empty(t.numel(), device=dev) for t in ws]
+        gb = [torch.empty(t.numel(), device=dev) for t in bs]
+        return (ws, bs, gw, gb), ptrs(ws), ptrs(bs), ptrs(gw), ptrs(gb)
+
+    dkeep, dW, dB, dgW, dgB = layers((32, 64, 16, 2), 1)
+    ckeep, cW, cB, cgW, cgB = layers((32, 64, 8, 3), 2)
+    packed = torch.empty(lib.nerfHeadsPackedBytes(), dtype=torch.uint8, device=dev)
+    lib.launchNerfHeadsPack(dW.data_ptr(), dB.data_ptr(), cW.data_ptr(), cB.data_ptr(), packed.data_ptr(), sp)
+    P.check()
+    enc = x.view(BATCH, L, 2).transpose(0, 1).contiguous()  # [L][N][2]
+    sig = torch.empty(BATCH, device=dev)
+    dout = torch.empty((BATCH, 16), device=dev)
+    cout = torch.empty((BATCH, 8), device=dev)
+    cin = torch.empty((BATCH, 32), dtype=torch.float16, device=dev)
+    cdy = torch.zeros((BATCH, 8), dtype=torch.float16, device=dev)
+    cdy[:, :3] = torch.from_numpy(rng.normal(0, 0.1, (BATCH, 3)).astype(np.float16)).to(dev)
+    ds = torch.from_numpy(rng.normal(0, 0.1, BATCH).astype(np.float32)).to(dev)
+    denc = torch.empty((BATCH, 32), dtype=torch.float16, device=dev)
+
+    def fwd():
+        lib.launchNerfHeadsForward(packed.data_ptr(), enc.data_ptr(), BATCH, L, d_dirs.data_ptr(), ridx.data_ptr(),
+                                   BATCH, 0.0, 1, sig.data_ptr(), None, cout.data_ptr(), cin.data_ptr(), sp)
+
+    def dx():
+        lib.launchNerfHeadsBackward(packed.data_ptr(), enc.data_ptr(), BATCH, L, cin.data_ptr(), cdy.data_ptr(),
+                                    ds.data_ptr(), BATCH, denc.data_ptr(), None, None, sp)
+
+    def dw():
+        lib.launchNerfHeadsWeightGrads(packed.data_ptr(), enc.data_ptr(), BATCH, L, cin.data_ptr(), cdy.data_ptr(),
+                                       ds.data_ptr(), BATCH, dgW.data_ptr(), dgB.data_ptr(), cgW.data_ptr(),
+                                       cgB.data_ptr(), sp)
+
+    def step():
+        lib.launchNerfHeadsPack(dW.data_ptr(), dB.data_ptr(), cW.data_ptr(), cB.data_ptr(), packed.data_ptr(), sp)
+        fwd()
+        dx()
+        dw()
+
+    t_f, t_x, t_w, t_all = timed(fwd), timed(dx), timed(dw), timed(step)
+    P.check()
+    fl_f = 2 * (32 * 64 + 64 * 16 + 32 * 64 + 64 * 64 + 64 * 3)          # 18,816
+    fl_w = fl_f
+    fl_x = HEADS_FLOP_PER_SAMPLE - fl_f - fl_w                           # 16,768
+    util = lambda fl, ms: round(fl * BATCH / (ms * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 5)  # noqa: E731
+    del dkeep, ckeep
+    return {"mlp_fwd_bwd_ms_2p18": round(t_all, 4),
+            "mlp_tflops": round(HEADS_FLOP_PER_SAMPLE * BATCH / (t_all * 1e-3) / 1e12, 2),
+            "mlp_mfma_util": util(HEADS_FLOP_PER_SAMPLE, t_all),
+            "heads_forward_ms_2p18": round(t_f, 4), "heads_forward_mfma_util": util(fl_f, t_f),
+            "heads_dx_ms_2p18": round(t_x, 4), "heads_dx_mfma_util": util(fl_x, t_x),
+            "heads_dw_ms_2p18": round(t_w, 4), "heads_dw_mfma_util": util(fl_w, t_w)}
+
+
 def components(P, torch, stream, sp):
     """Stand-alone launches at BASELINE configs[1]/[2] shapes: encode, scatter, hash Adam (HIP events)."""
     dev = torch.device("cuda:0")
@@ -519,9 +590,10 @@ def components(P, torch, stream, sp):
 
     t_mlp = timed(mlp_step)
     flops = MLP_FLOP_PER_SAMPLE * BATCH
-    out.update({"mlp_fwd_bwd_ms_2p18": round(t_mlp, 4),
-                "mlp_tflops": round(flops / (t_mlp * 1e-3) / 1e12, 2),
-                "mlp_mfma_util": round(flops / (t_mlp * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 5)})
+    out.update({"tinymlp_fwd_bwd_ms_2p18": round(t_mlp, 4),
+                "tinymlp_tflops": round(flops / (t_mlp * 1e-3) / 1e12, 2),
+                "tinymlp_mfma_util": round(flops / (t_mlp * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 5)})
+    out.update(heads_components(P, torch, dev, rng, x, d_dirs, ridx, sp, timed))
     # Adam over both heads and the dense table gradient (a fresh copy per launch: consumed grads are cleared)
     n_tab = L * TBL * F
     master = torch.from_numpy(rng.uniform(-1e-4, 1e-4, n_tab).astype(np.float32)).to(dev)

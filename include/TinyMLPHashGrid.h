@@ -69,6 +69,19 @@ public:
     // mlp_stream, the hash table on hash_stream (one Adam step count for both).
     void stepSplit(float lr, float beta1, float beta2, float epsilon, float loss_scale, hipStream_t mlp_stream,
                    hipStream_t hash_stream);
+    // The table half of the next step() fused into the scatter of the
+    // backward: d_dx_out [N x 2L] (N, or *d_n when given, samples at
+    // d_positions with pos_stride floats each) is scattered and every table
+    // entry it reaches takes that step's Adam update in the same pass, with
+    // the gradient the scatter would have stored (no gradient array).  The
+    // step count is not advanced: stepMlp(), which follows, does that.
+    // wait_before_update (nullable) is waited on before the first table
+    // write.  Needs the binned scatter (scatter_plan non-null).
+    void scatterAdamTable(const half* d_dx_out, const float* d_positions, int pos_stride, int N, const uint32_t* d_n,
+                          float lr, float beta1, float beta2, float epsilon, float loss_scale, hipStream_t stream,
+                          hipEvent_t wait_before_update);
+    // The MLP half of step(): advances the step count, updates the layers.
+    void stepMlp(float lr, float beta1, float beta2, float epsilon, float loss_scale, hipStream_t stream);
 
     // introspection for tests
     struct Buffers {

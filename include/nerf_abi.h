@@ -219,6 +219,54 @@ void launchUpdateOccupancyGrid(uint32_t* d_occupancy_grid, const float* d_master
 void launchBuildMipmaps(uint8_t* d_grid, uint3 grid_resolution, int mipmapLevels, int numCascades,
                         hipStream_t stream);
 
+/* ---- the NeRF step's two heads on the 16x16x32 fp16 MFMA (no single
+ * reference counterpart: the reference runs each head's forward and backward
+ * as separate launches, networkFusionHashtable.cu:441-682,
+ * networkFusion.cu:197-355, networkFusionBackward.cu:49-646,
+ * networkFusionBackwardHashtable.cu:71-781, with compute_SH_gather and
+ * compute_density_grad between them).  Shapes: density 32-64-16 and colour
+ * 32-64-64-8 (TinyMLP's hardware shapes of the 32-64-64-3 head), ReLU.
+ * Weights are device arrays of per-layer device pointers as the TinyMLP
+ * classes keep them (fp16 W [out][in], fp32 b).  Encodings are level-major:
+ * d_enc[l][enc_plane] fp16 feature pairs, l < levels <= 16, enc_plane >=
+ * num_samples.  Unsupported shapes are reported through tinymlp_last_error. */
+
+/* Bytes of the packed-weight buffer the launchers below take. */
+size_t nerfHeadsPackedBytes(void);
+
+/* Packs both heads' current weights and biases into d_packed. */
+void launchNerfHeadsPack(const GRAFT_HALF* const* d_density_w, const float* const* d_density_b,
+                         const GRAFT_HALF* const* d_color_w, const float* const* d_color_b, void* d_packed,
+                         hipStream_t stream);
+
+/* Density head -> sigma = e^min(sanitised logit 0 - density_bias, 8), the
+ * colour input [logits sanitised to +-64, NaN -> 0 | SH of the sample's ray
+ * direction] (fp16 [N][32], d_color_in; the backward's input), colour head
+ * (sigmoid when color_activation = 1) -> d_color_out fp32 [N][8];
+ * d_density_out (fp32 [N][16], the logits before sanitising) is nullable. */
+void launchNerfHeadsForward(const void* d_packed, const GRAFT_HALF* d_enc, int enc_plane, int levels,
+                            const float3* d_dirs, const uint32_t* d_ray_indices, int num_samples,
+                            float density_bias, int color_activation, float* d_sigma, float* d_density_out,
+                            float* d_color_out, GRAFT_HALF* d_color_in, hipStream_t stream);
+
+/* Recomputes the heads' hidden layers from d_enc and d_color_in, then the
+ * colour dX chain from d_color_dy (fp16 [N][8]), the density-gradient glue
+ * with d_dsigma and the density dX chain: d_denc fp16 [N][32] = dL/d(encoding);
+ * d_density_dy (fp16 [N][16]) and d_color_dx (fp16 [N][32], the logit
+ * features; the SH features are written as 0) are nullable. */
+void launchNerfHeadsBackward(const void* d_packed, const GRAFT_HALF* d_enc, int enc_plane, int levels,
+                             const GRAFT_HALF* d_color_in, const GRAFT_HALF* d_color_dy, const float* d_dsigma,
+                             int num_samples, GRAFT_HALF* d_denc, GRAFT_HALF* d_density_dy, GRAFT_HALF* d_color_dx,
+                             hipStream_t stream);
+
+/* The weight gradients of every layer of both heads for the same inputs,
+ * stored (not added) into the per-layer fp32 arrays (device arrays of device
+ * pointers); the block partials are summed in a fixed order. */
+void launchNerfHeadsWeightGrads(const void* d_packed, const GRAFT_HALF* d_enc, int enc_plane, int levels,
+                                const GRAFT_HALF* d_color_in, const GRAFT_HALF* d_color_dy, const float* d_dsigma,
+                                int num_samples, float* const* d_density_dw, float* const* d_density_db,
+                                float* const* d_color_dw, float* const* d_color_db, hipStream_t stream);
+
 /* ABI self-check (no reference counterpart): writes a.xyz, b.xyz to out[0..6). */
 void nerf_abi_echo_vec(float3 a, uint3 b, float* out);
 

@@ -144,7 +144,7 @@ void launchHashTableBackwardKernel(GRAFT_HALF* d_dx_out, float* d_inputs, float*
  * that cannot allocate device memory (code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc): the same sum
  * (d_hashtable_grads += scatter of d_dx_out, within the scatter's tolerance)
- * with its scratch in a fixed 40 MiB static device array instead of
+ * with its scratch in a fixed 48 MiB static device array instead of
  * library-allocated memory; it calls no hipMalloc/hipFree.  Any batch size
  * (large batches run as consecutive sub-batches on `stream`); grids with more
  * than 8192 slices of 4096 entries, or a hashed level's resolution above 4095,

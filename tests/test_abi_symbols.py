@@ -65,6 +65,20 @@ def test_launcher_argument_errors_without_gpu():
     assert L.tinymlp_last_error() != 0 and b"NULL" in L.tinymlp_last_error_message()
     L.processRaysChunk(8, *args, None, None, None, None, None, None, None, None, None, None, None, None)
     assert L.tinymlp_last_error() != 0 and b"NULL" in L.tinymlp_last_error_message()
+    assert L.nerfHeadsPackedBytes() > 0
+    fake = 1 << 20  # never dereferenced: every check below fails before a device call
+    L.launchNerfHeadsForward(fake, fake, 64, 16, fake, fake, -1, 0.0, 1, fake, None, fake, fake, None)
+    assert L.tinymlp_last_error() != 0 and b"num_samples" in L.tinymlp_last_error_message()
+    L.launchNerfHeadsForward(fake, fake, 16, 16, fake, fake, 64, 0.0, 1, fake, None, fake, fake, None)
+    assert L.tinymlp_last_error() != 0 and b"plane" in L.tinymlp_last_error_message()
+    L.launchNerfHeadsForward(fake, fake, 64, 17, fake, fake, 64, 0.0, 1, fake, None, fake, fake, None)
+    assert L.tinymlp_last_error() != 0 and b"levels" in L.tinymlp_last_error_message()
+    L.launchNerfHeadsBackward(fake, fake, 64, 16, None, fake, fake, 64, fake, None, None, None)
+    assert L.tinymlp_last_error() != 0 and b"null" in L.tinymlp_last_error_message()
+    L.launchNerfHeadsWeightGrads(fake, fake, 64, 16, fake, fake, fake, 64, None, fake, fake, fake, None)
+    assert L.tinymlp_last_error() != 0 and b"null" in L.tinymlp_last_error_message()
+    L.launchNerfHeadsPack(None, fake, fake, fake, fake, None)
+    assert L.tinymlp_last_error() != 0 and b"null" in L.tinymlp_last_error_message()
 
 
 def test_python_bindings_cover_the_headers():
