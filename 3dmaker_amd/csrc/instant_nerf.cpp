@@ -50,15 +50,25 @@ struct StepSet {
     uint32_t raysDone = 0;         // first ray of the batch in the call's rays
 };
 
-struct NerfBuffers {
-    // per step, rays
+// A marched window of rays: ray setup, per-ray sample counts and the march
+// store (march_store_floats(rayChunkSize)) of rays [c0, c1) of the buffers o, d.
+struct MarchStore {
     float3* d_inv = nullptr;
     float* nears = nullptr;
     float* fars = nullptr;
-    uint32_t* counts = nullptr;      // counts of the cached window [c0, c1)
-    float* t_scratch = nullptr;      // march store of the cached window (march_store_floats(rayChunkSize))
-    uint32_t cache_c0 = 0, cache_c1 = 0;
-    long cache_version = -1;         // grid version the cached counts were marched on
+    uint32_t* counts = nullptr;
+    float* t = nullptr;
+    uint32_t c0 = 0, c1 = 0;
+    long version = -1;               // grid version it was marched on (-1: nothing)
+    const float3* o = nullptr;
+    const float3* d = nullptr;
+};
+
+struct NerfBuffers {
+    // per step, rays: the current call's marched window, and the next call's
+    // first window marched ahead (setNextRays) in the other store
+    MarchStore ms[2];
+    int cur = 0;                     // store of the current call
     uint32_t* block_sums = nullptr;
     StepSet set[2];
     int last_set = 0;                // set of the last training step
@@ -75,6 +85,7 @@ struct NerfBuffers {
         const float3* d = nullptr;
         uint32_t n = 0;
         int set = 0;
+        int store = 0;               // march store of its window
         long version = -1;           // grid version it was marched on
     } pre;
     float* render_rgb = nullptr;
@@ -171,11 +182,13 @@ void InstantNerf::freeBuffers()
 {
     if (m_buf) {
         NerfBuffers& b = B(m_buf);
-        dfree(b.d_inv);
-        dfree(b.nears);
-        dfree(b.fars);
-        dfree(b.counts);
-        dfree(b.t_scratch);
+        for (MarchStore& M : b.ms) {
+            dfree(M.d_inv);
+            dfree(M.nears);
+            dfree(M.fars);
+            dfree(M.counts);
+            dfree(M.t);
+        }
         dfree(b.block_sums);
         for (StepSet& S : b.set) {
             dfree(S.offsets);
@@ -302,11 +315,13 @@ void InstantNerf::allocate()
     const size_t R = (size_t)m_opts.rayChunkSize, Bn = (size_t)m_opts.batchSize;
     const int G = grid_cells(m_opts);
     const int N = m_opts.numCascades * G;
-    b.d_inv = dalloc<float3>(R);
-    b.nears = dalloc<float>(R);
-    b.fars = dalloc<float>(R);
-    b.counts = dalloc<uint32_t>(R);
-    b.t_scratch = dalloc<float>(graft::march_store_floats((uint32_t)R));
+    for (MarchStore& M : b.ms) {
+        M.d_inv = dalloc<float3>(R);
+        M.nears = dalloc<float>(R);
+        M.fars = dalloc<float>(R);
+        M.counts = dalloc<uint32_t>(R);
+        M.t = dalloc<float>(graft::march_store_floats((uint32_t)R));
+    }
     b.block_sums = dalloc<uint32_t>(graft::march_scratch_words((uint32_t)R));
     for (StepSet& S : b.set) {
         S.offsets = dalloc<uint32_t>(R);
@@ -420,27 +435,39 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
     // window is marched only when it is not covered by the cached march on the
     // current grid.  The set's previous step has finished reading it by
     // then: the compaction stream waits for a later step's ev_dl first.
-    auto compact_rays = [&](int k, uint32_t raysDone, const float3* rays_o, const float3* rays_d, uint32_t nRays) {
+    // the window of rays [raysDone, raysDone + rayChunkSize) marched into
+    // store si on the current grid, unless that store holds it already
+    auto march_window = [&](int si, uint32_t raysDone, const float3* rays_o, const float3* rays_d, uint32_t nRays) {
+        MarchStore& M = b.ms[si];
+        const uint32_t R = std::min<uint32_t>((uint32_t)o.rayChunkSize, nRays - raysDone);
+        if (M.version == m_gridVersion && M.o == rays_o && M.d == rays_d && raysDone >= M.c0 &&
+            raysDone + R <= M.c1)
+            return;
+        const float3* co = rays_o + raysDone;
+        const float3* cd = rays_d + raysDone;
+        stage_on(b.cmp, "rayAabb", [&] {
+            graft::ray_aabb_inv(R, co, cd, o.aabbMin, o.aabbMax, o.numCascades, M.d_inv, M.nears, M.fars, b.cmp);
+        });
+        stage_on(b.cmp, "march", [&] {
+            graft::march_store(R, co, cd, M.d_inv, M.nears, M.fars, g, o.samplesPerVoxel, M.counts, M.t, b.cmp);
+        });
+        M.c0 = raysDone;
+        M.c1 = raysDone + R;
+        M.version = m_gridVersion;
+        M.o = rays_o;
+        M.d = rays_d;
+    };
+    auto compact_rays = [&](int k, int si, uint32_t raysDone, const float3* rays_o, const float3* rays_d,
+                            uint32_t nRays) {
         StepSet& S = b.set[k];
         const uint32_t R = std::min<uint32_t>((uint32_t)o.rayChunkSize, nRays - raysDone);
         const float3* co = rays_o + raysDone;
         const float3* cd = rays_d + raysDone;
-        if (b.cache_version != m_gridVersion || raysDone < b.cache_c0 || raysDone + R > b.cache_c1) {
-            stage_on(b.cmp, "rayAabb", [&] {
-                graft::ray_aabb_inv(R, co, cd, o.aabbMin, o.aabbMax, o.numCascades, b.d_inv, b.nears, b.fars,
-                                    b.cmp);
-            });
-            stage_on(b.cmp, "march", [&] {
-                graft::march_store(R, co, cd, b.d_inv, b.nears, b.fars, g, o.samplesPerVoxel, b.counts, b.t_scratch,
-                                   b.cmp);
-            });
-            b.cache_c0 = raysDone;
-            b.cache_c1 = raysDone + R;
-            b.cache_version = m_gridVersion;
-        }
-        const uint32_t woff = raysDone - b.cache_c0;
+        march_window(si, raysDone, rays_o, rays_d, nRays);
+        const MarchStore& M = b.ms[si];
+        const uint32_t woff = raysDone - M.c0;
         stage_on(b.cmp, "compaction", [&] {
-            graft::march_compact_stored(R, co, cd, g, Bn, b.counts + woff, b.t_scratch, woff, S.offsets, S.t_sorted,
+            graft::march_compact_stored(R, co, cd, g, Bn, M.counts + woff, M.t, woff, S.offsets, S.t_sorted,
                                         S.ray_idx, S.positions, graft::MarchScratch{b.block_sums, S.result}, b.cmp,
                                         S.counts);
         });
@@ -451,7 +478,7 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         GRAFT_HIP_CHECK(hipEventRecord(S.ev_result, b.cmp));
         S.raysDone = raysDone;
     };
-    auto compact = [&](int k, uint32_t raysDone) { compact_rays(k, raysDone, d_rays_o, d_rays_d, numRays); };
+    auto compact = [&](int k, uint32_t raysDone) { compact_rays(k, b.cur, raysDone, d_rays_o, d_rays_d, numRays); };
 
     // the side streams start after everything the caller queued (rays, grid)
     GRAFT_HIP_CHECK(hipEventRecord(b.ev_fork, stream));
@@ -469,10 +496,22 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
     bool opt_recorded = false;  // ev_opt holds a step of this call
     if (prefetched) {
         k = b.pre.set;
+        b.cur = b.pre.store;
     } else {
-        b.cache_version = -1;  // new rays: nothing cached
+        // new rays (the buffers may hold other rays than a store marched)
+        b.ms[0].version = b.ms[1].version = -1;
         compact(k, 0);
     }
+    // The next call's first window, marched ahead into the other store on
+    // the grid of now (again after every refresh of this call): its first
+    // hit batch, compacted beside this call's last step, then needs no march
+    // at the end of the call unless the grid changed after the last one.
+    // (Not now when the first step refreshes the grid.)
+    const bool ahead = next.n && next.o != d_rays_o && next.d != d_rays_d;
+    auto march_next = [&] {
+        if (ahead) march_window(b.cur ^ 1, 0, next.o, next.d, next.n);
+    };
+    if (m_trainSteps % 16 != 0) march_next();
     while (true) {
         StepSet& S = b.set[k];
         const uint32_t raysDone = S.raysDone;
@@ -700,6 +739,7 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         GRAFT_HIP_CHECK(hipStreamWaitEvent(b.cmp, b.ev_dl, 0));
         if (refresh) GRAFT_HIP_CHECK(hipStreamWaitEvent(b.cmp, b.ev_join, 0));
         if (!stop) compact(k ^ 1, raysDone + active);
+        if (refresh && !stop) march_next();
 
         if (heads) {
             stage_on(b.side, "headsBwd", [&] {
@@ -748,13 +788,12 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
             // the next call's rays are compacted ahead only when they are
             // other buffers than this call's (a caller refilling these buffers
             // in place for the next call would otherwise train on stale rays)
-            if (all_rays && next.n && next.o != d_rays_o && next.d != d_rays_d) {
-                // the next call's first hit batch, beside this last step; the
-                // march store is keyed by ray index, so it holds this call's rays
+            if (all_rays && ahead) {
+                // the next call's first hit batch, beside this last step, from
+                // the other store (marched ahead unless the grid has changed)
                 k ^= 1;
-                b.cache_version = -1;
-                compact_rays(k, 0, next.o, next.d, next.n);
-                b.pre = NerfBuffers::Prefetched{true, next.o, next.d, next.n, k, m_gridVersion};
+                compact_rays(k, b.cur ^ 1, 0, next.o, next.d, next.n);
+                b.pre = NerfBuffers::Prefetched{true, next.o, next.d, next.n, k, b.cur ^ 1, m_gridVersion};
             }
             break;
         }
@@ -1011,18 +1050,19 @@ void InstantNerf::renderImageHit(const float3* d_rays_o, const float3* d_rays_d,
     StepSet& S = b.set[0];  // the render path runs on the caller's stream only
     const uint32_t* d_rays = S.result;
     const uint32_t* d_hits = S.result + 1;
-    b.cache_version = -1;  // the march store is reused below
-    b.pre.valid = false;   // and so is step set 0
+    MarchStore& M = b.ms[b.cur];
+    b.ms[0].version = b.ms[1].version = -1;  // the march store is reused below
+    b.pre.valid = false;                     // and so is step set 0
 
     for (uint32_t c0 = 0; c0 < numRays; c0 += (uint32_t)o.rayChunkSize) {
         const uint32_t R = std::min<uint32_t>((uint32_t)o.rayChunkSize, numRays - c0);
         const float3* co = d_rays_o + c0;
         const float3* cd = d_rays_d + c0;
-        graft::ray_aabb_inv(R, co, cd, o.aabbMin, o.aabbMax, o.numCascades, b.d_inv, b.nears, b.fars, stream);
-        graft::march_store(R, co, cd, b.d_inv, b.nears, b.fars, g, o.samplesPerVoxel, b.counts, b.t_scratch, stream);
+        graft::ray_aabb_inv(R, co, cd, o.aabbMin, o.aabbMax, o.numCascades, M.d_inv, M.nears, M.fars, stream);
+        graft::march_store(R, co, cd, M.d_inv, M.nears, M.fars, g, o.samplesPerVoxel, M.counts, M.t, stream);
         uint32_t done = 0;
         while (done < R) {
-            graft::march_compact_stored(R - done, co + done, cd + done, g, hitBatch, b.counts + done, b.t_scratch, done,
+            graft::march_compact_stored(R - done, co + done, cd + done, g, hitBatch, M.counts + done, M.t, done,
                                         S.offsets, b.render.t, b.render.ray_idx, b.render.positions,
                                         graft::MarchScratch{b.block_sums, S.result}, stream);
             GRAFT_HIP_CHECK(hipMemcpyAsync(S.h_result, S.result, 2 * sizeof(uint32_t), hipMemcpyDeviceToHost, stream));
@@ -1047,7 +1087,7 @@ void InstantNerf::renderImageHit(const float3* d_rays_o, const float3* d_rays_d,
             graft::nerf_forward(fa, (int)hitBatch, stream, d_hits);
             graft::CompositeArgs ca{};
             ca.offsets = S.offsets;
-            ca.counts = b.counts + done;
+            ca.counts = M.counts + done;
             ca.t = b.render.t;
             ca.sigma = b.render.sigma;
             ca.rgb = b.render.rgb;
