@@ -494,11 +494,15 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
     b.next = NerfBuffers::Ahead{};
     int k = 0, i = 0;
     bool opt_recorded = false;  // ev_opt holds a step of this call
+    // A store is valid only for rays not rewritten since it was marched:
+    // within a call, or from the call before under the setNextRays contract.
+    // Callers refill ray buffers between calls (two feed slots taking turns),
+    // so the same pointers may hold other rays now.
     if (prefetched) {
         k = b.pre.set;
         b.cur = b.pre.store;
+        b.ms[b.cur ^ 1].version = -1;
     } else {
-        // new rays (the buffers may hold other rays than a store marched)
         b.ms[0].version = b.ms[1].version = -1;
         compact(k, 0);
     }

@@ -379,8 +379,9 @@ void launchNerfHeadsWeightGrads(const void* d_packed, const GRAFT_HALF* d_enc, i
     guarded("launchNerfHeadsWeightGrads", [&] {
         if (num_samples < 0) throw std::runtime_error("num_samples must be >= 0");
         if (!d_density_dw || !d_density_db || !d_color_dw || !d_color_db) throw std::runtime_error("null argument");
-        const graft::NerfHeadsBwd h =
-            heads_bwd(d_packed, d_enc, enc_plane, levels, d_color_in, d_color_dy, d_dsigma);
+        graft::NerfHeadsBwd h = heads_bwd(d_packed, d_enc, enc_plane, levels, d_color_in, d_color_dy, d_dsigma);
+        // the whole GPU: two blocks per CU (one of each head)
+        h.dw_blocks = graft::num_cus();
         graft::nerf_heads_dw(h, graft::NerfHeadsGrads{d_density_dw, d_density_db, d_color_dw, d_color_db},
                              num_samples, stream);
     });

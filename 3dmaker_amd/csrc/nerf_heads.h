@@ -45,6 +45,8 @@ struct NerfHeadsBwd {
     __half* denc = nullptr;            // [N x 32] dL/d(encoding) (nerf_heads_dx)
     __half* density_dy = nullptr;      // nullable [N x 16]
     __half* color_dx = nullptr;        // nullable [N x 32]: logit features; the SH features are not computed (0)
+    int dw_blocks = 0;                 // weight-gradient blocks per head (0: half the CUs each, so that the
+                                       // kernel leaves room beside the scatter it runs with)
 };
 
 // Per-layer fp32 gradient arrays (device arrays of device pointers); the

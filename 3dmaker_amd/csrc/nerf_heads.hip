@@ -913,8 +913,8 @@ void nerf_heads_dw(const NerfHeadsBwd& a, const NerfHeadsGrads& out, int N, hipS
     if (N < 0) return;
     BwdParams p = bwd_params(a, N, d_n);
     const int lds = (int)std::max(kTrBytes + kFwdBytes, (size_t)PC * sizeof(float));
-    // one block per CU for each head (the colour head's has the more work)
-    const int cb = num_cus() / 2, db = num_cus() / 2;
+    const int per_head = a.dw_blocks > 0 ? a.dw_blocks : std::max(1, num_cus() / 2);
+    const int cb = per_head, db = per_head;
     Workspace& w = ws ? *ws : stream_workspace(s);
     float* part = static_cast<float*>(w.get(((size_t)cb * PC + (size_t)db * PD) * sizeof(float)));
     p.ws_c = part;

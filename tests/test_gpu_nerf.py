@@ -684,6 +684,52 @@ def test_instant_nerf_next_rays_prefetch(dev):
     Bn.close()
 
 
+def test_instant_nerf_prefetch_with_refilled_ray_slots(dev):
+    """A driver that refills two ray buffers in turn, as the trainer's feed does (chunk c in slot c % 2,
+    chunk c + 1 written and named with setNextRays before chunk c trains): every call trains the same
+    compacted batches as plain calls on fresh buffers, so nothing marched for a slot's earlier rays is
+    ever reused for the rays written there since."""
+    P = pkg()
+    opts = small_options(P, batch=8192, chunk=2048)
+    A, Bn = P.Nerf(opts), P.Nerf(opts)
+    sizes = [300, 300, 300, 300, 300, 40]
+    chunks = []
+    for i, R in enumerate(sizes):
+        o, d = scenes.rays_c4(R, n_cams=20, seed=70 + i)
+        gt = np.random.default_rng(80 + i).random((R, 3)).astype(np.float32)
+        chunks.append((o, d, gt, R))
+    slots = [{k: torch.empty((300, 3), dtype=torch.float32, device=dev) for k in ("o", "d", "gt")} for _ in range(2)]
+
+    def write(i):
+        o, d, gt, R = chunks[i]
+        sl = slots[i % 2]
+        sl["o"][:R].copy_(torch.from_numpy(o))
+        sl["d"][:R].copy_(torch.from_numpy(d))
+        sl["gt"][:R].copy_(torch.from_numpy(gt))
+
+    hits_a, hits_b = [], []
+    write(0)
+    for i, (o, d, gt, R) in enumerate(chunks):
+        if i + 1 < len(chunks):
+            write(i + 1)
+            nxt = slots[(i + 1) % 2]
+            Bn.set_next_rays(nxt["o"], nxt["d"], chunks[i + 1][3])
+        sl = slots[i % 2]
+        hits_b.append(Bn.train(sl["o"], sl["d"], sl["gt"], R)[1])
+        hits_a.append(A.train(T(o, dev), T(d, dev), T(gt, dev), R)[1])
+        torch.cuda.synchronize()
+    assert sum(len(h) for h in hits_a) <= 16
+    assert hits_a == hits_b
+    sa, sb = A.step_buffers(), Bn.step_buffers()
+    R, n = sizes[-1], hits_a[-1][-1]
+    for name, shape, dt in (("num_steps", (R,), np.uint32), ("ray_offsets", (R,), np.uint32),
+                            ("ray_indices", (n,), np.uint32), ("t_sorted", (n,), np.float32),
+                            ("positions", (n, 4), np.float32)):
+        bits_eq(d2h(getattr(sb, name), shape, dt), d2h(getattr(sa, name), shape, dt))
+    A.close()
+    Bn.close()
+
+
 # --------------------------------------------------------------------------- occupancy refresh (f1)
 
 
