@@ -516,6 +516,14 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         if (ahead) march_window(b.cur ^ 1, 0, next.o, next.d, next.n);
     };
     if (m_trainSteps % 16 != 0) march_next();
+    // both heads' current weights (they may have been loaded or changed
+    // since the last call) for the first step's forward
+    auto pack_heads = [&](hipStream_t s) {
+        graft::nerf_heads_pack(
+            graft::NerfHeadsWeights{db.fwd_weights, db.master_biases, cb.fwd_weights, cb.master_biases},
+            b.heads_packed, s);
+    };
+    if (b.heads_packed) pack_heads(stream);
     while (true) {
         StepSet& S = b.set[k];
         const uint32_t raysDone = S.raysDone;
@@ -578,6 +586,7 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
             fa.enc_scratch = b.enc_planar;
             fa.enc_plane = (int)Bn;
             fa.heads_packed = b.heads_packed;
+            fa.heads_prepacked = true;  // packed at the call's start and after every step's layer Adam
             graft::nerf_forward(fa, (int)Bn, stream, d_hits);
         });
 
@@ -783,6 +792,8 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
             stage("densityOpt", [&] {
                 m_densityMLP->stepSplit(o.learningRate, o.beta1, o.beta2, o.epsilon, o.lossScale, b.side, stream);
             });
+        // the next step's weights, packed beside this step's scatter
+        if (b.heads_packed) pack_heads(b.side);
         GRAFT_HIP_CHECK(hipEventRecord(b.ev_opt, b.side));
         opt_recorded = true;
 

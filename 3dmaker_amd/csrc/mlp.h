@@ -91,8 +91,9 @@ struct NerfFwdArgs {
     // encodings and the head shapes nerf_heads_supported() accepts, and no
     // activations asked for (dacts, cacts null), the heads run as the
     // 16x16x32 MFMA kernels of nerf_heads.hip after packing the weights into
-    // this buffer.
+    // this buffer (heads_prepacked: the caller packed the current weights).
     void* heads_packed = nullptr;
+    bool heads_prepacked = false;
 };
 void nerf_forward(const NerfFwdArgs& a, int N, hipStream_t stream, const uint32_t* d_n = nullptr);
 

@@ -244,7 +244,7 @@ void nerf_forward(const NerfFwdArgs& a, int N, hipStream_t stream, const uint32_
     }
     if (planar && a.heads_packed != nullptr && a.dacts == nullptr && a.cacts == nullptr &&
         nerf_heads_supported(a.dshape, a.cshape)) {
-        nerf_heads_pack(NerfHeadsWeights{a.dW, a.dB, a.cW, a.cB}, a.heads_packed, stream);
+        if (!a.heads_prepacked) nerf_heads_pack(NerfHeadsWeights{a.dW, a.dB, a.cW, a.cB}, a.heads_packed, stream);
         NerfHeadsFwd h;
         h.packed = a.heads_packed;
         h.enc = a.enc_scratch;
