@@ -28,6 +28,9 @@ COMMON = [
     "-ffp-contract=off",
     "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA sources and results in ordinary VGPRs: no accumulation-register
+    # copies between a layer's MFMAs and its epilogue
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall", "-Wno-unused-result", "-Wno-unused-function",
     f"-I{INCLUDE}", f"-I{CSRC}",
 ]

@@ -80,28 +80,42 @@ __device__ __forceinline__ h8 cat(h4 lo, h4 hi) { return h8{lo[0], lo[1], lo[2],
 __device__ __forceinline__ h4 lo4(h8 v) { return h4{v[0], v[1], v[2], v[3]}; }
 __device__ __forceinline__ h4 hi4(h8 v) { return h4{v[4], v[5], v[6], v[7]}; }
 
-// ReLU(acc + bias) of one output block, rounded to fp16
-__device__ __forceinline__ h4 relu_h4(f4 a, f4 b)
+typedef short s4 __attribute__((ext_vector_type(4)));
+
+// four fp32 values rounded to fp16 (to nearest even), two per instruction
+__device__ __forceinline__ h4 round_h4(f4 d) { return __builtin_convertvector(d, h4); }
+
+// ReLU of one output block whose accumulator started from the bias, rounded
+// to fp16: rounding first, then the integer max of the fp16 bits with 0, which
+// turns every negative value and -0 into +0 and keeps the others.
+__device__ __forceinline__ h4 relu_h4(f4 acc)
 {
-    h4 r;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const float x = a[j] + b[j];
-        r[j] = to_h(x > 0.f ? x : 0.f);
-    }
-    return r;
+    const s4 b = __builtin_bit_cast(s4, round_h4(acc));
+    return __builtin_bit_cast(h4, __builtin_elementwise_max(b, (s4)0));
+}
+
+// Two halves of v (fp16 bits) kept where the matching half of x (the fp16
+// bits of a ReLU output: +0 or positive) is not 0, else 0: min(x, 1) per
+// half is the 0/1 mask and the 16-bit integer product applies it.  The mask
+// instruction is written out so that the compiler does not trace it back to
+// a float compare and select per half; the product stays compiler-visible
+// (it feeds MFMAs, whose operand hazards the compiler tracks).
+__device__ __forceinline__ uint32_t keep_where_positive(uint32_t v, uint32_t x)
+{
+    typedef unsigned short u2 __attribute__((ext_vector_type(2)));
+    uint32_t m;
+    __asm__("v_pk_min_u16 %0, %1, 1 op_sel_hi:[1,0]" : "=v"(m) : "v"(x));
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u2, v) * __builtin_bit_cast(u2, m));
 }
 
 // dX block rounded to fp16, zero where the layer's input activation is not > 0
 __device__ __forceinline__ h4 mask_h4(f4 d, h4 x)
 {
-    h4 r;
-#pragma unroll
-    for (int j = 0; j < 4; j++) r[j] = (float)x[j] > 0.f ? to_h(d[j]) : (_Float16)0.f;
-    return r;
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 m = __builtin_bit_cast(u32x2, x);
+    const u32x2 v = __builtin_bit_cast(u32x2, round_h4(d));
+    return __builtin_bit_cast(h4, u32x2{keep_where_positive(v[0], m[0]), keep_where_positive(v[1], m[1])});
 }
-
-__device__ __forceinline__ h4 round_h4(f4 d) { return h4{to_h(d[0]), to_h(d[1]), to_h(d[2]), to_h(d[3])}; }
 
 // Placed at the top of a tile loop: the LDS-staged fragments and biases are
 // read where they are used instead of being hoisted into registers for the
@@ -258,20 +272,16 @@ __device__ __forceinline__ h4 sh_quad(float x, float y, float z, int g)
 __device__ __forceinline__ void forward_tile(const Weights& w, const f4* __restrict__ sbias, const TileIn& in,
                                              int g, Acts& a)
 {
-    const f4 z = f4zero();
     a.enc = in.enc;
     // density L0 (32 -> 64)
     f4 d0[4];
 #pragma unroll
-    for (int mt = 0; mt < 4; mt++) d0[mt] = mfma32(w.F[FD0 + mt], in.enc, z);
-    a.hd[0] = cat(relu_h4(d0[0], sbias[(BD0 + 0) * 4 + g]), relu_h4(d0[1], sbias[(BD0 + 1) * 4 + g]));
-    a.hd[1] = cat(relu_h4(d0[2], sbias[(BD0 + 2) * 4 + g]), relu_h4(d0[3], sbias[(BD0 + 3) * 4 + g]));
+    for (int mt = 0; mt < 4; mt++) d0[mt] = mfma32(w.F[FD0 + mt], in.enc, sbias[(BD0 + mt) * 4 + g]);
+    a.hd[0] = cat(relu_h4(d0[0]), relu_h4(d0[1]));
+    a.hd[1] = cat(relu_h4(d0[2]), relu_h4(d0[3]));
     // density L1 (64 -> 16)
-    f4 y = mfma32(w.F[FD1 + 0], a.hd[0], z);
+    f4 y = mfma32(w.F[FD1 + 0], a.hd[0], sbias[BD1 * 4 + g]);
     y = mfma32(w.F[FD1 + 1], a.hd[1], y);
-    const f4 b1 = sbias[BD1 * 4 + g];
-#pragma unroll
-    for (int j = 0; j < 4; j++) y[j] = y[j] + b1[j];
     a.y = y;
     h4 lg;
 #pragma unroll
@@ -280,24 +290,21 @@ __device__ __forceinline__ void forward_tile(const Weights& w, const f4* __restr
     // colour L0 (32 -> 64)
     f4 c0[4];
 #pragma unroll
-    for (int mt = 0; mt < 4; mt++) c0[mt] = mfma32(w.F[FC0 + mt], a.cin, z);
-    a.h1[0] = cat(relu_h4(c0[0], sbias[(BC0 + 0) * 4 + g]), relu_h4(c0[1], sbias[(BC0 + 1) * 4 + g]));
-    a.h1[1] = cat(relu_h4(c0[2], sbias[(BC0 + 2) * 4 + g]), relu_h4(c0[3], sbias[(BC0 + 3) * 4 + g]));
+    for (int mt = 0; mt < 4; mt++) c0[mt] = mfma32(w.F[FC0 + mt], a.cin, sbias[(BC0 + mt) * 4 + g]);
+    a.h1[0] = cat(relu_h4(c0[0]), relu_h4(c0[1]));
+    a.h1[1] = cat(relu_h4(c0[2]), relu_h4(c0[3]));
     // colour L1 (64 -> 64)
     f4 c1[4];
 #pragma unroll
     for (int mt = 0; mt < 4; mt++) {
-        c1[mt] = mfma32(w.F[FC1 + 2 * mt], a.h1[0], z);
+        c1[mt] = mfma32(w.F[FC1 + 2 * mt], a.h1[0], sbias[(BC1 + mt) * 4 + g]);
         c1[mt] = mfma32(w.F[FC1 + 2 * mt + 1], a.h1[1], c1[mt]);
     }
-    a.h2[0] = cat(relu_h4(c1[0], sbias[(BC1 + 0) * 4 + g]), relu_h4(c1[1], sbias[(BC1 + 1) * 4 + g]));
-    a.h2[1] = cat(relu_h4(c1[2], sbias[(BC1 + 2) * 4 + g]), relu_h4(c1[3], sbias[(BC1 + 3) * 4 + g]));
+    a.h2[0] = cat(relu_h4(c1[0]), relu_h4(c1[1]));
+    a.h2[1] = cat(relu_h4(c1[2]), relu_h4(c1[3]));
     // colour L2 (64 -> 8)
-    f4 o = mfma32(w.F[FC2 + 0], a.h2[0], z);
+    f4 o = mfma32(w.F[FC2 + 0], a.h2[0], sbias[BC2 * 4 + g]);
     o = mfma32(w.F[FC2 + 1], a.h2[1], o);
-    const f4 b2 = sbias[BC2 * 4 + g];
-#pragma unroll
-    for (int j = 0; j < 4; j++) o[j] = o[j] + b2[j];
     a.rgb[0] = o;
 }
 
@@ -309,27 +316,26 @@ template <class FW>
 __device__ __forceinline__ void recompute_tile(const FW& w, const f4* __restrict__ sbias, h8 enc, h8 cin, int g,
                                                Acts& a)
 {
-    const f4 z = f4zero();
     a.enc = enc;
     a.cin = cin;
     f4 d0[4];
 #pragma unroll
-    for (int mt = 0; mt < 4; mt++) d0[mt] = mfma32(w.F[FD0 + mt], enc, z);
-    a.hd[0] = cat(relu_h4(d0[0], sbias[(BD0 + 0) * 4 + g]), relu_h4(d0[1], sbias[(BD0 + 1) * 4 + g]));
-    a.hd[1] = cat(relu_h4(d0[2], sbias[(BD0 + 2) * 4 + g]), relu_h4(d0[3], sbias[(BD0 + 3) * 4 + g]));
+    for (int mt = 0; mt < 4; mt++) d0[mt] = mfma32(w.F[FD0 + mt], enc, sbias[(BD0 + mt) * 4 + g]);
+    a.hd[0] = cat(relu_h4(d0[0]), relu_h4(d0[1]));
+    a.hd[1] = cat(relu_h4(d0[2]), relu_h4(d0[3]));
     f4 c0[4];
 #pragma unroll
-    for (int mt = 0; mt < 4; mt++) c0[mt] = mfma32(w.F[FC0 + mt], cin, z);
-    a.h1[0] = cat(relu_h4(c0[0], sbias[(BC0 + 0) * 4 + g]), relu_h4(c0[1], sbias[(BC0 + 1) * 4 + g]));
-    a.h1[1] = cat(relu_h4(c0[2], sbias[(BC0 + 2) * 4 + g]), relu_h4(c0[3], sbias[(BC0 + 3) * 4 + g]));
+    for (int mt = 0; mt < 4; mt++) c0[mt] = mfma32(w.F[FC0 + mt], cin, sbias[(BC0 + mt) * 4 + g]);
+    a.h1[0] = cat(relu_h4(c0[0]), relu_h4(c0[1]));
+    a.h1[1] = cat(relu_h4(c0[2]), relu_h4(c0[3]));
     f4 c1[4];
 #pragma unroll
     for (int mt = 0; mt < 4; mt++) {
-        c1[mt] = mfma32(w.F[FC1 + 2 * mt], a.h1[0], z);
+        c1[mt] = mfma32(w.F[FC1 + 2 * mt], a.h1[0], sbias[(BC1 + mt) * 4 + g]);
         c1[mt] = mfma32(w.F[FC1 + 2 * mt + 1], a.h1[1], c1[mt]);
     }
-    a.h2[0] = cat(relu_h4(c1[0], sbias[(BC1 + 0) * 4 + g]), relu_h4(c1[1], sbias[(BC1 + 1) * 4 + g]));
-    a.h2[1] = cat(relu_h4(c1[2], sbias[(BC1 + 2) * 4 + g]), relu_h4(c1[3], sbias[(BC1 + 3) * 4 + g]));
+    a.h2[0] = cat(relu_h4(c1[0]), relu_h4(c1[1]));
+    a.h2[1] = cat(relu_h4(c1[2]), relu_h4(c1[3]));
 }
 
 // The inputs of one tile's backward, all indexed by the sample.
