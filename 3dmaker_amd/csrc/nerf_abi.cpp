@@ -373,13 +373,16 @@ void launchNerfHeadsBackward(const void* d_packed, const GRAFT_HALF* d_enc, int 
 
 void launchNerfHeadsWeightGrads(const void* d_packed, const GRAFT_HALF* d_enc, int enc_plane, int levels,
                                 const GRAFT_HALF* d_color_in, const GRAFT_HALF* d_color_dy, const float* d_dsigma,
-                                int num_samples, float* const* d_density_dw, float* const* d_density_db,
-                                float* const* d_color_dw, float* const* d_color_db, hipStream_t stream)
+                                const GRAFT_HALF* d_density_dy, int num_samples, float* const* d_density_dw,
+                                float* const* d_density_db, float* const* d_color_dw, float* const* d_color_db,
+                                hipStream_t stream)
 {
     guarded("launchNerfHeadsWeightGrads", [&] {
         if (num_samples < 0) throw std::runtime_error("num_samples must be >= 0");
         if (!d_density_dw || !d_density_db || !d_color_dw || !d_color_db) throw std::runtime_error("null argument");
         graft::NerfHeadsBwd h = heads_bwd(d_packed, d_enc, enc_plane, levels, d_color_in, d_color_dy, d_dsigma);
+        // read only: the density dL/dy launchNerfHeadsBackward stored for these inputs
+        h.density_dy = const_cast<__half*>(reinterpret_cast<const __half*>(d_density_dy));
         // the whole GPU: two blocks per CU (one of each head)
         h.dw_blocks = graft::num_cus();
         graft::nerf_heads_dw(h, graft::NerfHeadsGrads{d_density_dw, d_density_db, d_color_dw, d_color_db},

@@ -650,25 +650,49 @@ __device__ __forceinline__ void color_dw_tile(ColorAcc& A, const h8* T, int lane
     }
 }
 
-// The density head's dW / db of one tile: the whole dX chain down to the
-// density dY0 (backward_tile's operations), then the two updates.
+// The density head's dW / db of one tile from its dL/dy (d1) and hidden
+// layer (hd): dY0 = (W1^T d1 masked by hd > 0), then the two updates.
+__device__ __forceinline__ void density_dw_update(DensityAcc& A, const h8* T, int lane, const h8* hd, h8 enc, h4 d1,
+                                                  h4 ident)
+{
+    const f4 z = f4zero();
+    const h8 gd1 = cat(d1, h4zero());
+    h4 d0[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; mt++) d0[mt] = mask_h4(mfma32(T[(TD1 + mt) * 64 + lane], gd1, z), blk(hd, mt));
+    {  // L1: dY1 x hd
+        const h4 Y = tblk(d1, ident, &A.b1);
+#pragma unroll
+        for (int mi = 0; mi < 4; mi++) A.d1[mi] = mfma16t(Y, tblk(blk(hd, mi), ident), A.d1[mi]);
+    }
+    const h4 X0 = tblk(lo4(enc), ident), X1 = tblk(hi4(enc), ident);
+#pragma unroll
+    for (int mo = 0; mo < 4; mo++) {  // L0: dY0 x enc
+        const h4 Y = tblk(d0[mo], ident, &A.b0[mo]);
+        A.d0[mo][0] = mfma16t(Y, X0, A.d0[mo][0]);
+        A.d0[mo][1] = mfma16t(Y, X1, A.d0[mo][1]);
+    }
+}
+
+// The density head's dW / db of one tile when its dL/dy is not stored: the
+// whole dX chain down to it (backward_tile's operations, so the same bits).
 __device__ __forceinline__ void density_dw_tile(DensityAcc& A, const h8* T, int lane, const Acts& a, h4 cdy, float ds,
                                                 h4 ident)
 {
     Grads gr;
     backward_tile<false>(T, lane, a, cat(cdy, h4zero()), ds, gr);
-    {  // L1: dY1 x hd
-        const h4 Y = tblk(gr.d1, ident, &A.b1);
+    density_dw_update(A, T, lane, a.hd, a.enc, gr.d1, ident);
+}
+
+// The density hidden layer of one tile (recompute_tile's operations for it)
+template <class FW>
+__device__ __forceinline__ void recompute_density(const FW& w, const f4* __restrict__ sbias, h8 enc, int g, h8* hd)
+{
+    f4 d0[4];
 #pragma unroll
-        for (int mi = 0; mi < 4; mi++) A.d1[mi] = mfma16t(Y, tblk(blk(a.hd, mi), ident), A.d1[mi]);
-    }
-    const h4 X0 = tblk(lo4(a.enc), ident), X1 = tblk(hi4(a.enc), ident);
-#pragma unroll
-    for (int mo = 0; mo < 4; mo++) {  // L0: dY0 x enc
-        const h4 Y = tblk(gr.d0[mo], ident, &A.b0[mo]);
-        A.d0[mo][0] = mfma16t(Y, X0, A.d0[mo][0]);
-        A.d0[mo][1] = mfma16t(Y, X1, A.d0[mo][1]);
-    }
+    for (int mt = 0; mt < 4; mt++) d0[mt] = mfma32(w.F[FD0 + mt], enc, sbias[(BD0 + mt) * 4 + g]);
+    hd[0] = cat(relu_h4(d0[0]), relu_h4(d0[1]));
+    hd[1] = cat(relu_h4(d0[2]), relu_h4(d0[3]));
 }
 
 // db: the four lane groups of a feature hold partial sums
@@ -738,13 +762,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void h
             A.b0[i] = A.b1[i] = 0.f;
         }
         A.b2 = 0.f;
-        for (int tile = rb * waves + wave; tile < ntiles; tile += nb * waves) {
+        const int stride = nb * waves;
+        int tile = rb * waves + wave;
+        // invalid samples: zero dL/dy; the next tile's inputs are in flight
+        // while this one computes
+        BwdIn in = load_bwd(p, tile * 16 + r, tile < ntiles && tile * 16 + r < N, g);
+        for (; tile < ntiles; tile += stride) {
             reload_fence();
-            const int n = tile * 16 + r;
-            const BwdIn in = load_bwd(p, n, n < N, g);  // invalid samples: zero dL/dy
+            const int nt = tile + stride;
+            const BwdIn nxt = load_bwd(p, nt * 16 + r, nt < ntiles && nt * 16 + r < N, g);
             Acts a;
             recompute_tile(w, sbias, in.enc, in.cin, g, a);
             color_dw_tile(A, str, lane, a, lo4(in.cdy), ident);
+            in = nxt;
         }
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -779,13 +809,43 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void h
             A.b0[i] = 0.f;
         }
         A.b1 = 0.f;
-        for (int tile = rb * waves + wave; tile < ntiles; tile += nb * waves) {
-            reload_fence();
-            const int n = tile * 16 + r;
-            const BwdIn in = load_bwd(p, n, n < N, g);
-            Acts a;
-            recompute_tile(w, sbias, in.enc, in.cin, g, a);
-            density_dw_tile(A, str, lane, a, lo4(in.cdy), in.ds, ident);
+        const int stride = nb * waves;
+        int tile = rb * waves + wave;
+        if (p.dloss) {
+            // the density dL/dy the dX kernel stored for these inputs: no
+            // colour chain; the next tile's inputs are in flight while this
+            // one computes
+            auto load = [&](int t, h8& enc, h4& d1) {
+                const int n = t * 16 + r;
+                const bool valid = t < ntiles && n < N;
+                enc = load_enc(p.enc, p.plane, p.L, n, valid, g);
+                d1 = valid ? ld_h4(p.dloss + (size_t)n * DOUT + 4 * g) : h4zero();
+            };
+            h8 enc;
+            h4 d1;
+            load(tile, enc, d1);
+            for (; tile < ntiles; tile += stride) {
+                reload_fence();
+                h8 enc_n;
+                h4 d1_n;
+                load(tile + stride, enc_n, d1_n);
+                h8 hd[2];
+                recompute_density(w, sbias, enc, g, hd);
+                density_dw_update(A, str, lane, hd, enc, d1, ident);
+                enc = enc_n;
+                d1 = d1_n;
+            }
+        } else {
+            BwdIn in = load_bwd(p, tile * 16 + r, tile < ntiles && tile * 16 + r < N, g);
+            for (; tile < ntiles; tile += stride) {
+                reload_fence();
+                const int nt = tile + stride;
+                const BwdIn nxt = load_bwd(p, nt * 16 + r, nt < ntiles && nt * 16 + r < N, g);
+                Acts a;
+                recompute_tile(w, sbias, in.enc, in.cin, g, a);
+                density_dw_tile(A, str, lane, a, lo4(in.cdy), in.ds, ident);
+                in = nxt;
+            }
         }
 #pragma unroll
         for (int i = 0; i < 4; i++) A.b0[i] = gsum(A.b0[i]);
@@ -920,6 +980,8 @@ void nerf_heads_dw(const NerfHeadsBwd& a, const NerfHeadsGrads& out, int N, hipS
     BwdParams p = bwd_params(a, N, d_n);
     const int lds = (int)std::max(kTrBytes + kFwdBytes, (size_t)PC * sizeof(float));
     const int per_head = a.dw_blocks > 0 ? a.dw_blocks : std::max(1, num_cus() / 2);
+    // an even split also when the density dL/dy is stored (measured against
+    // 70/30, 40/60 and 30/70 colour/density splits beside the scatter)
     const int cb = per_head, db = per_head;
     Workspace& w = ws ? *ws : stream_workspace(s);
     float* part = static_cast<float*>(w.get(((size_t)cb * PC + (size_t)db * PD) * sizeof(float)));

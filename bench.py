@@ -452,6 +452,7 @@ def heads_components(P, torch, dev, rng, x, d_dirs, ridx, sp, timed):
     cdy[:, :3] = torch.from_numpy(rng.normal(0, 0.1, (BATCH, 3)).astype(np.float16)).to(dev)
     ds = torch.from_numpy(rng.normal(0, 0.1, BATCH).astype(np.float32)).to(dev)
     denc = torch.empty((BATCH, 32), dtype=torch.float16, device=dev)
+    ddy = torch.empty((BATCH, 16), dtype=torch.float16, device=dev)  # density dL/dy: dX kernel -> dW kernel
 
     def fwd():
         lib.launchNerfHeadsForward(packed.data_ptr(), enc.data_ptr(), BATCH, L, d_dirs.data_ptr(), ridx.data_ptr(),
@@ -459,12 +460,12 @@ def heads_components(P, torch, dev, rng, x, d_dirs, ridx, sp, timed):
 
     def dx():
         lib.launchNerfHeadsBackward(packed.data_ptr(), enc.data_ptr(), BATCH, L, cin.data_ptr(), cdy.data_ptr(),
-                                    ds.data_ptr(), BATCH, denc.data_ptr(), None, None, sp)
+                                    ds.data_ptr(), BATCH, denc.data_ptr(), ddy.data_ptr(), None, sp)
 
     def dw():
         lib.launchNerfHeadsWeightGrads(packed.data_ptr(), enc.data_ptr(), BATCH, L, cin.data_ptr(), cdy.data_ptr(),
-                                       ds.data_ptr(), BATCH, dgW.data_ptr(), dgB.data_ptr(), cgW.data_ptr(),
-                                       cgB.data_ptr(), sp)
+                                       ds.data_ptr(), ddy.data_ptr(), BATCH, dgW.data_ptr(), dgB.data_ptr(),
+                                       cgW.data_ptr(), cgB.data_ptr(), sp)
 
     def step():
         lib.launchNerfHeadsPack(dW.data_ptr(), dB.data_ptr(), cW.data_ptr(), cB.data_ptr(), packed.data_ptr(), sp)

@@ -261,11 +261,15 @@ void launchNerfHeadsBackward(const void* d_packed, const GRAFT_HALF* d_enc, int 
 
 /* The weight gradients of every layer of both heads for the same inputs,
  * stored (not added) into the per-layer fp32 arrays (device arrays of device
- * pointers); the block partials are summed in a fixed order. */
+ * pointers); the block partials are summed in a fixed order.  d_density_dy
+ * (nullable) is the density dL/dy launchNerfHeadsBackward stored for the same
+ * inputs: given, the density head's gradients start from it instead of
+ * running the colour dX chain again (same values). */
 void launchNerfHeadsWeightGrads(const void* d_packed, const GRAFT_HALF* d_enc, int enc_plane, int levels,
                                 const GRAFT_HALF* d_color_in, const GRAFT_HALF* d_color_dy, const float* d_dsigma,
-                                int num_samples, float* const* d_density_dw, float* const* d_density_db,
-                                float* const* d_color_dw, float* const* d_color_db, hipStream_t stream);
+                                const GRAFT_HALF* d_density_dy, int num_samples, float* const* d_density_dw,
+                                float* const* d_density_db, float* const* d_color_dw, float* const* d_color_db,
+                                hipStream_t stream);
 
 /* ABI self-check (no reference counterpart): writes a.xyz, b.xyz to out[0..6). */
 void nerf_abi_echo_vec(float3 a, uint3 b, float* out);

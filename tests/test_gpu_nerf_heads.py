@@ -93,7 +93,7 @@ def make_case(N, levels, plane_pad, seed, dev):
 
 
 class Run:
-    def __init__(self, case, dh, ch, dev, bias=0.5, act=1):
+    def __init__(self, case, dh, ch, dev, bias=0.5, act=1, stored_dy=False):
         P = pkg()
         self.L = L = P.lib()
         N = case["N"]
@@ -123,8 +123,10 @@ class Run:
                                   self.cin.data_ptr(), self.cdy.data_ptr(), self.dsig.data_ptr(), N,
                                   self.denc.data_ptr(), self.ddy.data_ptr(), self.cdx.data_ptr(), None)
         check(L, "backward")
+        # stored_dy: the density head's gradients start from the density dL/dy the backward stored
         L.launchNerfHeadsWeightGrads(self.packed.data_ptr(), self.enc.data_ptr(), case["plane"], case["levels"],
-                                     self.cin.data_ptr(), self.cdy.data_ptr(), self.dsig.data_ptr(), N,
+                                     self.cin.data_ptr(), self.cdy.data_ptr(), self.dsig.data_ptr(),
+                                     self.ddy.data_ptr() if stored_dy else None, N,
                                      dh.pgw.data_ptr(), dh.pgb.data_ptr(), ch.pgw.data_ptr(), ch.pgb.data_ptr(), None)
         check(L, "weight grads")
         torch.cuda.synchronize()
@@ -167,13 +169,30 @@ def check_against_oracle(run, dh, ch):
     big_close(cdB, cdB_ref, "colour db")
 
 
-@pytest.mark.parametrize("N,levels,pad,act", [(1, 16, 0, 1), (17, 16, 5, 1), (5003, 16, 0, 1), (4096, 16, 64, 0),
-                                              (3001, 9, 3, 1), (40000, 16, 0, 1)])
-def test_heads_match_oracle(dev, N, levels, pad, act):
-    print(f"heads N={N} levels={levels} pad={pad} act={act}", flush=True)
+@pytest.mark.parametrize("N,levels,pad,act,stored_dy", [(1, 16, 0, 1, False), (17, 16, 5, 1, True),
+                                                        (5003, 16, 0, 1, False), (5003, 16, 0, 1, True),
+                                                        (4096, 16, 64, 0, True), (3001, 9, 3, 1, True),
+                                                        (40000, 16, 0, 1, False), (40000, 16, 0, 1, True)])
+def test_heads_match_oracle(dev, N, levels, pad, act, stored_dy):
+    print(f"heads N={N} levels={levels} pad={pad} act={act} stored_dy={stored_dy}", flush=True)
     dh, ch = Head(DSHAPE, 11, dev), Head(CSHAPE, 12, dev)
-    run = Run(make_case(N, levels, pad, 100 + N, dev), dh, ch, dev, act=act)
+    run = Run(make_case(N, levels, pad, 100 + N, dev), dh, ch, dev, act=act, stored_dy=stored_dy)
     check_against_oracle(run, dh, ch)
+
+
+def test_heads_density_grads_from_stored_dy_match_the_recomputed_ones(dev):
+    """The density head's dW/db from the stored density dL/dy equal those of the recomputed colour chain
+    (the dX kernel's operations: the same per-sample values); the two paths split the blocks between the
+    heads differently, so the fixed-order sums of the block partials agree to fp32 rounding."""
+    case = make_case(20011, 16, 0, 13, dev)
+    dh, ch = Head(DSHAPE, 41, dev), Head(CSHAPE, 42, dev)
+    Run(case, dh, ch, dev, stored_dy=False)
+    rec = dh.grads() + ch.grads()
+    dh2, ch2 = Head(DSHAPE, 41, dev), Head(CSHAPE, 42, dev)
+    Run(case, dh2, ch2, dev, stored_dy=True)
+    got = dh2.grads() + ch2.grads()
+    for a, b, what in zip(rec, got, ("density dW", "density db", "colour dW", "colour db")):
+        np.testing.assert_allclose(b, a, rtol=0, atol=1e-5 * float(np.abs(a).max()), err_msg=what)
 
 
 def test_heads_zero_samples_store_zero_gradients(dev):
@@ -194,7 +213,7 @@ def test_heads_weight_grads_are_deterministic_and_overwrite(dev):
         t.fill_(123.0)
     L = run.L
     L.launchNerfHeadsWeightGrads(run.packed.data_ptr(), run.enc.data_ptr(), case["plane"], case["levels"],
-                                 run.cin.data_ptr(), run.cdy.data_ptr(), run.dsig.data_ptr(), case["N"],
+                                 run.cin.data_ptr(), run.cdy.data_ptr(), run.dsig.data_ptr(), None, case["N"],
                                  dh.pgw.data_ptr(), dh.pgb.data_ptr(), ch.pgw.data_ptr(), ch.pgb.data_ptr(), None)
     check(L, "weight grads")
     second = dh.grads() + ch.grads()
