@@ -105,7 +105,7 @@ class StepBuffers(C.Structure):
 
 class RefreshBuffers(C.Structure):
     _fields_ = [(n, C.c_void_p) for n in ("samples", "density_out", "tmp_grid", "active_list", "active_count")] + \
-        [("last_count", C.c_int)]
+        [("last_count", C.c_int), ("density_stride", C.c_int), ("density_order", C.c_void_p)]
 
 
 _vp, _i, _f, _u = C.c_void_p, C.c_int, C.c_float, C.c_uint

@@ -104,7 +104,14 @@ struct NerfBuffers {
     float* tmp_grid = nullptr;
     float4* occ_samples = nullptr;
     float* occ_density = nullptr;
-    __half* occ_enc = nullptr;       // [capacity x 2L] encodings of the refresh samples
+    __half* occ_enc = nullptr;       // [capacity x 2L] encodings of the refresh samples (level-major with the heads)
+    // the refresh with the 16x16x32 density head: its own packed fragments
+    // (packed at the refresh's start), the samples in spatial order
+    void* occ_packed = nullptr;
+    float4* occ_sorted = nullptr;
+    uint32_t* occ_perm = nullptr;
+    graft::OccSortScratch occ_sort{};
+    bool occ_last_sorted = false;  // the last chunk's densities are in occ_perm's order
     float* partials = nullptr;
     float* sum = nullptr;
     int* active_list = nullptr;
@@ -216,6 +223,14 @@ void InstantNerf::freeBuffers()
         dfree(b.occ_samples);
         dfree(b.occ_density);
         dfree(b.occ_enc);
+        dfree(b.occ_packed);
+        dfree(b.occ_sorted);
+        dfree(b.occ_perm);
+        dfree(b.occ_sort.counts);
+        dfree(b.occ_sort.offsets);
+        dfree(b.occ_sort.block_sums);
+        dfree(b.occ_sort.result);
+        dfree(b.occ_sort.rank);
         dfree(b.partials);
         dfree(b.sum);
         dfree(b.active_list);
@@ -348,6 +363,9 @@ void InstantNerf::allocate()
     const int halfN = N / 2;
     b.occ_capacity = std::max(G, halfN / std::max(1, m_opts.numCascades));
     b.occ_samples = dalloc<float4>((size_t)b.occ_capacity);
+    // a late refresh with no occupied cell leaves its list samples as they
+    // were: zeros here (cell 0) until a refresh writes them
+    GRAFT_HIP_CHECK(hipMemset(b.occ_samples, 0, (size_t)b.occ_capacity * sizeof(float4)));
     b.occ_density = dalloc<float>((size_t)b.occ_capacity * 16);
     b.occ_enc = dalloc<__half>((size_t)b.occ_capacity * 2 * m_opts.numLevels);
     b.partials = dalloc<float>(1024);
@@ -377,7 +395,18 @@ void InstantNerf::allocate()
     const TinyMLPHashGrid::Buffers dbuf = m_densityMLP->buffers();
     const graft::MlpShape dsh{2 * m_opts.numLevels, dbuf.hw.hiddenDim, dbuf.hw.outputDim, dbuf.hw.numLayers};
     const graft::MlpShape csh = shape_of(cb.hw);
-    if (graft::nerf_heads_supported(dsh, csh)) b.heads_packed = dalloc<unsigned char>(graft::nerf_heads_packed_bytes());
+    if (graft::nerf_heads_supported(dsh, csh)) {
+        b.heads_packed = dalloc<unsigned char>(graft::nerf_heads_packed_bytes());
+        b.occ_packed = dalloc<unsigned char>(graft::nerf_heads_packed_bytes());
+        b.occ_sorted = dalloc<float4>((size_t)b.occ_capacity);
+        b.occ_perm = dalloc<uint32_t>((size_t)b.occ_capacity);
+        const size_t keys = graft::occ_sort_keys(m_opts.numCascades, m_opts.gridResolution);
+        b.occ_sort.counts = dalloc<uint32_t>(keys);
+        b.occ_sort.offsets = dalloc<uint32_t>(keys);
+        b.occ_sort.block_sums = dalloc<uint32_t>(graft::march_scratch_words((uint32_t)keys));
+        b.occ_sort.result = dalloc<uint32_t>(2);
+        b.occ_sort.rank = dalloc<uint32_t>((size_t)b.occ_capacity);
+    }
 }
 
 // InstantNerf.cu:341-359.  The mode picks the hit batch of the render path
@@ -549,15 +578,19 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         // wait for it, so every kernel sees the parameters and grid of the
         // serial order.
         const bool refresh = (m_trainSteps % 16 == 0);
-        if (refresh) {
-            GRAFT_HIP_CHECK(hipEventRecord(b.ev_occ_fork, stream));
+        if (refresh) GRAFT_HIP_CHECK(hipEventRecord(b.ev_occ_fork, stream));
+        // The refresh's launches are enqueued after the forward and the dX
+        // chain (the host's launch time then overlaps them), forked from the
+        // step's start all the same.
+        auto enqueue_refresh = [&] {
+            if (!refresh) return;
             GRAFT_HIP_CHECK(hipStreamWaitEvent(b.occ, b.ev_occ_fork, 0));
             stage_on(b.occ, "occupancy", [&] {
                 if (m_trainSteps < 256) earlyOccupancyGridUpdate(b.occ);
                 else lateOccupancyGridUpdate(b.occ);
             });
             GRAFT_HIP_CHECK(hipEventRecord(b.ev_join, b.occ));
-        }
+        };
         // hash encode + density head, SH gather (into the colour head's
         // activation 0), colour head: one launch, activations saved
         stage("forward", [&] {
@@ -692,6 +725,7 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
             });
         }
         GRAFT_HIP_CHECK(hipEventRecord(b.ev_dl, stream));
+        enqueue_refresh();
         // The scatter is the step's critical path: it is enqueued before the
         // side streams' work, so that the host's launches of that work never
         // delay it.
@@ -877,22 +911,61 @@ void InstantNerf::updateOccupancy(hipStream_t stream)
 
 namespace {
 
-// Density logits of the n refresh samples in b.occ_samples: the encode runs
-// as its own launch (each XCD's L2 holding only its levels' tables; the
-// samples are spread over the whole grid, so the fused encode + MLP kernel
-// would cycle all 32 MiB of table through every L2), then the density head
-// on the encodings.
-void occupancy_density(NerfBuffers& b, const TinyMLPHashGrid::Buffers& db, const graft::MlpShape& dshape, int n,
-                       hipStream_t stream)
+// The per-cell maximum of sigma over the n refresh samples in b.occ_samples,
+// into b.tmp_grid, with each sample's density logit 0 in b.occ_density
+// (stride refresh_density_stride; in b.occ_perm's order when sorted).  The encode runs as its own launch (each
+// XCD's L2 holding only its levels' tables; the samples are spread over the
+// whole grid, so an encode fused with the head would cycle all 32 MiB of table
+// through every L2).  With the 16x16x32 heads: the samples are first put in a
+// spatial order when spread at random (spatial_sort), so that a wave's
+// gathers share table lines, then the density head runs on the level-major
+// encodings with the maximum fused in (b.occ_packed holds the density
+// head's fragments, packed at the refresh's start); otherwise the TinyMLP
+// density forward, then the maximum.
+void occupancy_density_max(NerfBuffers& b, const TinyMLPHashGrid::Buffers& db, const graft::MlpShape& dshape, int n,
+                           bool spatial_sort, bool one_per_cell, const NerfOptions& o, hipStream_t stream)
 {
+    if (b.occ_packed) {
+        const float4* src = b.occ_samples;
+        if (spatial_sort) {
+            graft::occ_sort_samples(b.occ_samples, n, o.numCascades, o.gridResolution, b.occ_sort, b.occ_sorted,
+                                    b.occ_perm, stream);
+            src = b.occ_sorted;
+        }
+        graft::hash_encode_planar(b.meta, db.fwd_hashtable, reinterpret_cast<const float*>(src), 4, b.occ_enc, n, n,
+                                  stream);
+        graft::NerfDensityMax a;
+        a.packed = b.occ_packed;
+        a.enc = b.occ_enc;
+        a.enc_plane = n;
+        a.levels = b.meta.numLevels;
+        a.samples = src;
+        a.density_bias = o.densityBias;
+        a.logit = b.occ_density;
+        a.tmp = b.tmp_grid;
+        a.one_per_cell = one_per_cell;
+        graft::nerf_density_max(a, n, stream);
+        b.occ_last_sorted = spatial_sort;
+        return;
+    }
+    b.occ_last_sorted = false;
     graft::hash_encode(b.meta, db.fwd_hashtable, reinterpret_cast<const float*>(b.occ_samples), 4, b.occ_enc, n,
                        stream);
     graft::FwdInput in;
     in.x = b.occ_enc;
     graft::mlp_forward(dshape, in, db.fwd_weights, db.master_biases, nullptr, b.occ_density, n, OUT_ACT_NONE, stream);
+    graft::occ_tmp_max(b.occ_samples, b.occ_density, b.tmp_grid, o.densityBias, n, stream);
 }
 
-}  // namespace
+int refresh_density_stride(const NerfBuffers& b) { return b.occ_packed ? 1 : 16; }
+
+// the density head's current weights for the refresh's own fragments
+void pack_refresh(NerfBuffers& b, const TinyMLPHashGrid::Buffers& db, hipStream_t stream)
+{
+    if (b.occ_packed)
+        graft::nerf_heads_pack_density(graft::NerfHeadsWeights{db.fwd_weights, db.master_biases, nullptr, nullptr},
+                                       b.occ_packed, stream);
+}}  // namespace
 
 // InstantNerf.cu:1108-1171: one jittered sample per cell of every cascade.
 void InstantNerf::earlyOccupancyGridUpdate(hipStream_t stream)
@@ -902,13 +975,16 @@ void InstantNerf::earlyOccupancyGridUpdate(hipStream_t stream)
     const int N = m_opts.numCascades * G;
     const TinyMLPHashGrid::Buffers db = m_densityMLP->buffers();
     const graft::MlpShape dshape{2 * m_opts.numLevels, db.hw.hiddenDim, db.hw.outputDim, db.hw.numLayers};
-    GRAFT_HIP_CHECK(hipMemsetAsync(b.tmp_grid, 0, (size_t)N * sizeof(float), stream));
+    // with the density head of the 16x16x32 heads, each cell's one sample
+    // stores its sigma; else the maximum starts from zero
+    if (!b.occ_packed) GRAFT_HIP_CHECK(hipMemsetAsync(b.tmp_grid, 0, (size_t)N * sizeof(float), stream));
+    pack_refresh(b, db, stream);
     for (int c = 0; c < m_opts.numCascades; ++c) {
         graft::occ_sample(b.occ_samples, G, graft::kSampleEveryCell, G, c * G, nullptr, nullptr,
                           (uint64_t)m_trainSteps + (uint64_t)c, m_opts.gridResolution, m_opts.aabbMin, m_opts.aabbMax,
                           stream);
-        occupancy_density(b, db, dshape, G, stream);
-        graft::occ_tmp_max(b.occ_samples, b.occ_density, b.tmp_grid, m_opts.densityBias, G, stream);
+        // every cell in cell order: already spatial
+        occupancy_density_max(b, db, dshape, G, false, true, m_opts, stream);
     }
     b.occ_last_count = G;
     finishOccupancyUpdate(stream);
@@ -924,8 +1000,10 @@ void InstantNerf::lateOccupancyGridUpdate(hipStream_t stream)
     const int S = (int)graft::mip_offset(m_opts.gridResolution, m_opts.levelsMipmap);
     const TinyMLPHashGrid::Buffers db = m_densityMLP->buffers();
     const graft::MlpShape dshape{2 * m_opts.numLevels, db.hw.hiddenDim, db.hw.outputDim, db.hw.numLayers};
-    GRAFT_HIP_CHECK(hipMemsetAsync(b.tmp_grid, 0, (size_t)N * sizeof(float), stream));
-    graft::occ_active_list(d_occupancyGrid, N, G, S, b.active_list, b.active_count, b.list_scratch, stream);
+    pack_refresh(b, db, stream);
+    // the list's pass over every cell also clears the tmp grid
+    graft::occ_active_list(d_occupancyGrid, N, G, S, b.active_list, b.active_count, b.list_scratch, stream,
+                           b.tmp_grid);
     const int chunks = m_opts.numCascades;
     const int perChunk = (N / 2) / chunks;
     const int occPer = perChunk / 2;
@@ -937,8 +1015,7 @@ void InstantNerf::lateOccupancyGridUpdate(hipStream_t stream)
         graft::occ_sample(b.occ_samples + occPer, uniPer, graft::kSampleRandomCell, N, 0, nullptr, nullptr, seed + 1,
                           m_opts.gridResolution, m_opts.aabbMin, m_opts.aabbMax, stream);
         const int cnt = occPer + uniPer;
-        occupancy_density(b, db, dshape, cnt, stream);
-        graft::occ_tmp_max(b.occ_samples, b.occ_density, b.tmp_grid, m_opts.densityBias, cnt, stream);
+        occupancy_density_max(b, db, dshape, cnt, true, false, m_opts, stream);
         b.occ_last_count = cnt;
     }
     finishOccupancyUpdate(stream);
@@ -974,6 +1051,8 @@ InstantNerf::RefreshBuffers InstantNerf::refreshBuffers() const
     RefreshBuffers r{};
     r.samples = b.occ_samples;
     r.density_out = b.occ_density;
+    r.densityStride = refresh_density_stride(b);
+    r.densityOrder = b.occ_last_sorted ? b.occ_perm : nullptr;
     r.tmp_grid = b.tmp_grid;
     r.active_list = b.active_list;
     r.active_count = b.active_count;

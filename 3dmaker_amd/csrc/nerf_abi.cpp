@@ -731,6 +731,8 @@ int inerf_refresh_buffers(Inerf* h, InerfRefreshBuffers* out)
         out->active_list = r.active_list;
         out->active_count = r.active_count;
         out->last_count = r.lastCount;
+        out->density_stride = r.densityStride;
+        out->density_order = r.densityOrder;
     });
 }
 int inerf_step_buffers(Inerf* h, InerfStepBuffers* out)

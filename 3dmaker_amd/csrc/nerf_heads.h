@@ -58,10 +58,31 @@ struct NerfHeadsGrads {
     float* const* cB;
 };
 
+// The occupancy refresh's use of the density head: per sample j of samples[]
+// (w = cell index bits) sigma = e^min(logit 0 - density_bias, 8) maxed into
+// tmp[cell] (integer max on the float bits) and, when logit is given, logit 0
+// stored at logit[j].
+struct NerfDensityMax {
+    const void* packed;            // nerf_heads_pack or nerf_heads_pack_density output
+    const __half* enc = nullptr;   // [levels][enc_plane] feature pairs of samples[] (hash_encode_planar)
+    int enc_plane = 0;
+    int levels = 16;
+    const float4* samples = nullptr;
+    float density_bias = 0.0f;
+    float* logit = nullptr;
+    float* tmp = nullptr;
+    // the samples cover every cell they reach exactly once (the early refresh):
+    // sigma is stored, which is the maximum over a zeroed cell
+    bool one_per_cell = false;
+};
+
 bool nerf_heads_supported(const MlpShape& density, const MlpShape& color);
 size_t nerf_heads_packed_bytes();
 // Packs both heads' fp16 weights and fp32 biases for the kernels below.
 void nerf_heads_pack(const NerfHeadsWeights& w, void* packed, hipStream_t s);
+// The density head's fragments and biases only (the colour head's are left as they are).
+void nerf_heads_pack_density(const NerfHeadsWeights& w, void* packed, hipStream_t s);
+void nerf_density_max(const NerfDensityMax& a, int N, hipStream_t s);
 void nerf_heads_forward(const NerfHeadsFwd& a, int N, hipStream_t s, const uint32_t* d_n = nullptr);
 // dL/d(encoding) (and the optional density / colour dL arrays).
 void nerf_heads_dx(const NerfHeadsBwd& a, int N, hipStream_t s, const uint32_t* d_n = nullptr);

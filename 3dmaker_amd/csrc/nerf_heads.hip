@@ -134,6 +134,7 @@ struct PackParams {
     h8* fwd;   // [kFwdFrags][64]
     h8* tr;    // [kTrFrags][64]
     f4* bias;  // [kBiasBlocks][4]
+    bool density_only;  // the density head's forward fragments and biases only
 };
 
 // element (row, col) of W_l [out][in], 0 outside
@@ -146,6 +147,7 @@ __global__ __launch_bounds__(256) void pack_kernel(const PackParams p)
 {
     const int t = blockIdx.x * 256 + threadIdx.x;
     const int nf = (kFwdFrags + kTrFrags) * 64;
+    if (p.density_only && (t < nf ? (t >> 6) >= FC0 : ((t - nf) >> 2) >= BC0)) return;
     if (t < nf) {
         const int lane = t & 63, f = t >> 6, m = lane & 15, g = lane >> 4;
         h8 v;
@@ -506,6 +508,68 @@ __global__ __launch_bounds__(256) void heads_fwd_kernel(const FwdParams p)
             }
             *reinterpret_cast<f4*>(p.cout + (size_t)n * COUT + 4 * g) = v;
         }
+    }
+}
+
+// The density head alone over samples in an arbitrary order (the occupancy
+// refresh): sigma = e^min(logit 0 - bias, 8) of each sample maxed into its
+// cell of tmp as an integer max on the float bits (sigma >= 0: the float max,
+// whatever the order), and logit 0 stored in the same order.
+struct DensityMaxParams {
+    const h8* fwd;
+    const f4* bias;
+    const _Float16* enc;
+    int plane, L;
+    const float4* samples;  // w = cell index bits
+    int N;
+    float density_bias;
+    float* logit;           // nullable [N]
+    float* tmp;
+    bool one_per_cell;      // every cell of tmp gets exactly one sample: stored, not maxed
+};
+
+__global__ __launch_bounds__(256) void density_max_kernel(const DensityMaxParams p)
+{
+    __shared__ f4 sbias[kBiasBlocks * 4];
+    stage_bias(sbias, p.bias);
+    const int lane = threadIdx.x & 63, g = lane >> 4, r = lane & 15;
+    h8 F[6];
+#pragma unroll
+    for (int q = 0; q < 6; q++) F[q] = p.fwd[(FD0 + q) * 64 + lane];
+    const int ntiles = (p.N + 15) >> 4;
+    const int nw = gridDim.x * (blockDim.x >> 6);
+    int tile = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    // the next tile's encodings and cell are in flight while this one computes
+    auto load = [&](int t, h8& enc, int& cell) {
+        const int n = t * 16 + r;
+        const bool valid = t < ntiles && n < p.N;
+        enc = load_enc(p.enc, p.plane, p.L, n, valid, g);
+        cell = (valid && g == 0) ? __float_as_int(p.samples[n].w) : 0;
+    };
+    h8 enc;
+    int cell;
+    load(tile, enc, cell);
+    for (; tile < ntiles; tile += nw) {
+        h8 enc_n;
+        int cell_n;
+        load(tile + nw, enc_n, cell_n);
+        const int n = tile * 16 + r;
+        f4 d0[4];
+#pragma unroll
+        for (int mt = 0; mt < 4; mt++) d0[mt] = mfma32(F[mt], enc, sbias[(BD0 + mt) * 4 + g]);
+        const h8 hd0 = cat(relu_h4(d0[0]), relu_h4(d0[1]));
+        const h8 hd1 = cat(relu_h4(d0[2]), relu_h4(d0[3]));
+        f4 y = mfma32(F[4], hd0, sbias[BD1 * 4 + g]);
+        y = mfma32(F[5], hd1, y);
+        if (n < p.N && g == 0) {
+            const float sigma = nerf_expf(fminf(y[0] - p.density_bias, 8.0f));
+            int* dst = reinterpret_cast<int*>(p.tmp) + cell;
+            if (p.one_per_cell) *dst = __float_as_int(sigma);  // the max over one sample
+            else atomicMax(dst, __float_as_int(sigma));
+            if (p.logit) p.logit[n] = y[0];
+        }
+        enc = enc_n;
+        cell = cell_n;
     }
 }
 
@@ -905,6 +969,44 @@ void nerf_heads_pack(const NerfHeadsWeights& w, void* packed, hipStream_t s)
     p.bias = reinterpret_cast<f4*>(base + kFwdBytes + kTrBytes);
     const int threads = (kFwdFrags + kTrFrags) * 64 + kBiasBlocks * 4;
     hipLaunchKernelGGL(pack_kernel, dim3((threads + 255) / 256), dim3(256), 0, s, p);
+    GRAFT_LAUNCH_CHECK();
+}
+
+void nerf_heads_pack_density(const NerfHeadsWeights& w, void* packed, hipStream_t s)
+{
+    PackParams p{};
+    p.dW = reinterpret_cast<const _Float16* const*>(w.dW);
+    p.dB = w.dB;
+    unsigned char* base = static_cast<unsigned char*>(packed);
+    p.fwd = reinterpret_cast<h8*>(base);
+    p.tr = reinterpret_cast<h8*>(base + kFwdBytes);
+    p.bias = reinterpret_cast<f4*>(base + kFwdBytes + kTrBytes);
+    p.density_only = true;
+    const int threads = (kFwdFrags + kTrFrags) * 64 + kBiasBlocks * 4;
+    hipLaunchKernelGGL(pack_kernel, dim3((threads + 255) / 256), dim3(256), 0, s, p);
+    GRAFT_LAUNCH_CHECK();
+}
+
+void nerf_density_max(const NerfDensityMax& a, int N, hipStream_t s)
+{
+    if (N <= 0) return;
+    if (a.enc_plane < N) throw std::runtime_error("NeRF heads: encoding plane stride below the sample count");
+    if (a.levels < 1 || a.levels > 16) throw std::runtime_error("NeRF heads: the density input is 16 levels x 2");
+    DensityMaxParams p{};
+    const unsigned char* base = static_cast<const unsigned char*>(a.packed);
+    p.fwd = reinterpret_cast<const h8*>(base);
+    p.bias = reinterpret_cast<const f4*>(base + kFwdBytes + kTrBytes);
+    p.enc = reinterpret_cast<const _Float16*>(a.enc);
+    p.plane = a.enc_plane;
+    p.L = a.levels;
+    p.samples = a.samples;
+    p.N = N;
+    p.density_bias = a.density_bias;
+    p.logit = a.logit;
+    p.tmp = a.tmp;
+    p.one_per_cell = a.one_per_cell;
+    const int blocks = grid_for((const void*)density_max_kernel, 0, (N + 15) / 16, 4);
+    hipLaunchKernelGGL(density_max_kernel, dim3(blocks), dim3(256), 0, s, p);
     GRAFT_LAUNCH_CHECK();
 }
 

@@ -117,9 +117,10 @@ __device__ __forceinline__ bool cell_occupied(const uint8_t* bits, int cell, int
 }
 
 __global__ __launch_bounds__(256) void occ_count_kernel(const uint8_t* __restrict__ bits, int total, int G, int S,
-                                                        uint32_t* __restrict__ block_counts)
+                                                        uint32_t* __restrict__ block_counts, float* __restrict__ zero)
 {
     const int cell = blockIdx.x * 256 + threadIdx.x;
+    if (zero && cell < total) zero[cell] = 0.0f;
     const bool occ = cell < total && cell_occupied(bits, cell, G, S);
     const int n = __syncthreads_count(occ);
     if (threadIdx.x == 0) block_counts[blockIdx.x] = (uint32_t)n;
@@ -169,7 +170,78 @@ __global__ __launch_bounds__(256) void occ_write_kernel(const uint8_t* __restric
     if (occ) list[before + (uint32_t)__popcll(below)] = cell;
 }
 
+// Spatial key of a sample's cell for the refresh's evaluation order: the
+// cascade, then the Morton code of the cell's 4x4x4 block (bit b of the block
+// coordinates x, y, z at bits 3b, 3b + 1, 3b + 2).
+struct SortKeyArgs {
+    int G;
+    uint3 res;
+    uint32_t per_cascade;  // P^3, P = blocks per axis rounded up to a power of two
+};
+
+__device__ __forceinline__ uint32_t spread3(uint32_t v)
+{
+    uint32_t m = 0;
+#pragma unroll
+    for (int b = 0; b < 10; b++) m |= ((v >> b) & 1u) << (3 * b);
+    return m;
+}
+
+__device__ __forceinline__ uint32_t occ_sort_key(const SortKeyArgs& k, int cell)
+{
+    const int cascade = cell / k.G, local = cell - cascade * k.G;
+    const uint32_t gx = (uint32_t)(local % (int)k.res.x);
+    const uint32_t gy = (uint32_t)((local / (int)k.res.x) % (int)k.res.y);
+    const uint32_t gz = (uint32_t)(local / (int)(k.res.x * k.res.y));
+    return (uint32_t)cascade * k.per_cascade + (spread3(gx >> 2) | (spread3(gy >> 2) << 1) | (spread3(gz >> 2) << 2));
+}
+
+// The counting key of sample i: its spatial key in one of kSortCopies key
+// ranges, picked by the sample index, so that the many samples of one block
+// of occupied cells spread their counter atomics over that many cache lines.
+// The order is then (copy, cascade, block): a handful of spatial sweeps.
+constexpr uint32_t kSortCopies = 8;
+
+__device__ __forceinline__ uint32_t occ_count_key(const SortKeyArgs& k, uint32_t keys, int i, int cell)
+{
+    return ((uint32_t)i & (kSortCopies - 1)) * keys + occ_sort_key(k, cell);
+}
+
+// rank[i] = the sample's place among the samples of its key (in the order the
+// atomics land: any order serves, the per-cell maximum does not depend on it)
+__global__ __launch_bounds__(256) void occ_rank_kernel(const float4* __restrict__ samples, int N, const SortKeyArgs k,
+                                                       uint32_t keys, uint32_t* __restrict__ counts,
+                                                       uint32_t* __restrict__ rank)
+{
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= N) return;
+    rank[i] = atomicAdd(counts + occ_count_key(k, keys, i, __float_as_int(samples[i].w)), 1u);
+}
+
+__global__ __launch_bounds__(256) void occ_place_kernel(const float4* __restrict__ samples, int N, const SortKeyArgs k,
+                                                        uint32_t keys, const uint32_t* __restrict__ offsets,
+                                                        const uint32_t* __restrict__ rank, float4* __restrict__ sorted,
+                                                        uint32_t* __restrict__ perm)
+{
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= N) return;
+    const float4 v = samples[i];
+    const uint32_t j = offsets[occ_count_key(k, keys, i, __float_as_int(v.w))] + rank[i];
+    sorted[j] = v;
+    perm[j] = (uint32_t)i;
+}
+
 int nblocks(int n) { return std::max(1, (n + 255) / 256); }
+
+SortKeyArgs sort_key_args(int cascades, uint3 res, uint32_t* keys)
+{
+    uint32_t P = 1;
+    const uint32_t m = std::max({(res.x + 3) / 4, (res.y + 3) / 4, (res.z + 3) / 4});
+    while (P < m) P <<= 1;
+    SortKeyArgs k{(int)(res.x * res.y * res.z), res, P * P * P};
+    if (keys) *keys = (uint32_t)cascades * k.per_cascade;
+    return k;
+}
 
 }  // namespace
 
@@ -203,11 +275,34 @@ void occ_tmp_max(const float4* samples, const float* density_out, float* tmp, fl
 
 size_t occ_list_scratch_words(int total) { return (size_t)nblocks(total); }
 
+size_t occ_sort_keys(int cascades, uint3 res)
+{
+    uint32_t keys = 0;
+    sort_key_args(cascades, res, &keys);
+    return (size_t)keys * kSortCopies;
+}
+
+void occ_sort_samples(const float4* samples, int N, int cascades, uint3 res, const OccSortScratch& sc, float4* sorted,
+                      uint32_t* perm, hipStream_t s)
+{
+    if (N <= 0) return;
+    uint32_t keys = 0;
+    const SortKeyArgs k = sort_key_args(cascades, res, &keys);
+    const uint32_t all = keys * kSortCopies;
+    GRAFT_HIP_CHECK(hipMemsetAsync(sc.counts, 0, (size_t)all * sizeof(uint32_t), s));
+    hipLaunchKernelGGL(occ_rank_kernel, dim3(nblocks(N)), dim3(256), 0, s, samples, N, k, keys, sc.counts, sc.rank);
+    GRAFT_LAUNCH_CHECK();
+    scan_counts(all, sc.counts, 0xffffffffu, sc.offsets, MarchScratch{sc.block_sums, sc.result}, s);
+    hipLaunchKernelGGL(occ_place_kernel, dim3(nblocks(N)), dim3(256), 0, s, samples, N, k, keys, sc.offsets, sc.rank,
+                       sorted, perm);
+    GRAFT_LAUNCH_CHECK();
+}
+
 void occ_active_list(const uint8_t* bits, int total, int G, int S, int* list, int* d_count, uint32_t* scratch,
-                     hipStream_t s)
+                     hipStream_t s, float* zero)
 {
     const int nb = nblocks(total);
-    hipLaunchKernelGGL(occ_count_kernel, dim3(nb), dim3(256), 0, s, bits, total, G, S, scratch);
+    hipLaunchKernelGGL(occ_count_kernel, dim3(nb), dim3(256), 0, s, bits, total, G, S, scratch, zero);
     GRAFT_LAUNCH_CHECK();
     hipLaunchKernelGGL(occ_scan_kernel, dim3(1), dim3(1024), 0, s, scratch, nb, d_count);
     GRAFT_LAUNCH_CHECK();

@@ -193,11 +193,13 @@ public:
     // of an early refresh, the last cascade chunk of a late one).
     struct RefreshBuffers {
         float4* samples;          // [lastCount]: contracted position, cell id (int bits)
-        float* density_out;       // [lastCount x 16]
+        float* density_out;       // [lastCount x densityStride]: density logit 0 first
         float* tmp_grid;          // [numCascades x cells]
         int* active_list;         // occupied cells in cell order (late refresh)
         int* active_count;        // [1]
         int lastCount;
+        int densityStride;        // 1 (the logit alone) or 16 (the density head's whole output)
+        const uint32_t* densityOrder;  // nullable: density_out row j is sample densityOrder[j]
     };
     RefreshBuffers refreshBuffers() const;
 

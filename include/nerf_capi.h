@@ -65,11 +65,13 @@ typedef struct InerfStepBuffers {
 /* InstantNerf::refreshBuffers (introspection, no reference counterpart). */
 typedef struct InerfRefreshBuffers {
     float* samples;         /* float4 [last_count]: contracted position, cell id bits */
-    float* density_out;     /* [last_count x 16] */
+    float* density_out;     /* [last_count x density_stride]: density logit 0 first */
     float* tmp_grid;        /* [cascades x cells] */
     int* active_list;
     int* active_count;
     int last_count;
+    int density_stride;     /* 1 or 16 */
+    const uint32_t* density_order; /* nullable: density_out row j is sample density_order[j] */
 } InerfRefreshBuffers;
 
 void inerf_default_options(InerfOptions* out);

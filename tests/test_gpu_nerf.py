@@ -789,7 +789,16 @@ def test_occupancy_refresh_matches_oracle(dev, late):
     rb = nerf.refresh_buffers()
     n_last = rb.last_count
     g_smp = d2h(rb.samples, (n_last, 4), np.float32)
-    g_den = d2h(rb.density_out, (n_last, 16), np.float32)
+    # the density logit 0 of each sample (the refresh's MFMA density head stores only it, in the order it
+    # evaluated the samples: density_order, the spatial sort of a late refresh)
+    g_den = d2h(rb.density_out, (n_last, rb.density_stride), np.float32)[:, 0]
+    if rb.density_order:
+        order = d2h(rb.density_order, (n_last,), np.uint32)
+        assert np.array_equal(np.sort(order), np.arange(n_last)), "the evaluation order is a permutation"
+        unsorted = np.empty_like(g_den)
+        unsorted[order] = g_den
+        g_den = unsorted
+    assert bool(rb.density_order) == (late and rb.density_stride == 1)
     g_tmp = d2h(rb.tmp_grid, (Cc * G,), np.float32)
     if late:   # the occupied-cell list, in cell order
         want_list = orc.active_cells(bits, G, S, Cc)
@@ -803,7 +812,7 @@ def test_occupancy_refresh_matches_oracle(dev, late):
     smp, y = chunks[-1]
     assert smp.shape[0] == n_last
     np.testing.assert_array_equal(g_smp.view(np.uint32), smp.view(np.uint32))  # positions and cell ids
-    assert_close(g_den, y, what="refresh density logits")
+    assert_close(g_den, y[:, 0], what="refresh density logit 0")
     # tmp grid: the earlier chunks from the oracle's densities, the last one from the GPU's own
     tmp = np.zeros(Cc * G, np.float32)
     for s_, y_ in chunks[:-1]:
@@ -812,7 +821,9 @@ def test_occupancy_refresh_matches_oracle(dev, late):
     last_only[smp[:, 3].view(np.int32)] = True
     for s_, _ in chunks[:-1]:
         last_only[s_[:, 3].view(np.int32)] = False
-    orc.occ_tmp_max(smp, g_den, tmp, opts.densityBias)
+    g_y = np.zeros((n_last, 16), np.float32)
+    g_y[:, 0] = g_den
+    orc.occ_tmp_max(smp, g_y, tmp, opts.densityBias)
     bits_eq(g_tmp[last_only], tmp[last_only])
     early = ~last_only
     np.testing.assert_array_equal(g_tmp[early] > 0, tmp[early] > 0)   # sampled cells (sigma > 0)
