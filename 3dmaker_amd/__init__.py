@@ -200,8 +200,8 @@ SIGNATURES = {
     "nerfHeadsPackedBytes": (C.c_size_t, []),
     "launchNerfHeadsPack": (None, [_vp, _vp, _vp, _vp, _vp, _vp]),
     "launchNerfHeadsForward": (None, [_vp, _vp, _i, _i, _vp, _vp, _i, _f, _i, _vp, _vp, _vp, _vp, _vp]),
-    "launchNerfHeadsBackward": (None, [_vp, _vp, _i, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp]),
-    "launchNerfHeadsWeightGrads": (None, [_vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp]),
+    "launchNerfHeadsBackward": (None, [_vp, _vp, _i, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp]),
+    "launchNerfHeadsWeightGrads": (None, [_vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp]),
     "nerf_abi_echo_vec": (None, [Float3, Uint3, C.POINTER(_f)]),
     # include/nerf_capi.h (InstantNerf handle API)
     "inerf_default_options": (None, [C.POINTER(NerfOptions)]),

@@ -100,6 +100,7 @@ struct NerfBuffers {
     __half* color_dx = nullptr;
     __half* enc_planar = nullptr;    // [L][Bn] feature pairs: the step's encodings, level-major
     void* heads_packed = nullptr;    // both heads' weights packed for nerf_heads.hip (null: other shapes)
+    uint32_t* tile_live = nullptr;   // [Bn / 16 + 1]: 16-sample tiles with a nonzero gradient (dX -> dW)
     // occupancy
     float* tmp_grid = nullptr;
     float4* occ_samples = nullptr;
@@ -219,6 +220,7 @@ void InstantNerf::freeBuffers()
         dfree(b.color_dx);
         dfree(b.enc_planar);
         dfree(b.heads_packed);
+        dfree(b.tile_live);
         dfree(b.tmp_grid);
         dfree(b.occ_samples);
         dfree(b.occ_density);
@@ -397,6 +399,7 @@ void InstantNerf::allocate()
     const graft::MlpShape csh = shape_of(cb.hw);
     if (graft::nerf_heads_supported(dsh, csh)) {
         b.heads_packed = dalloc<unsigned char>(graft::nerf_heads_packed_bytes());
+        b.tile_live = dalloc<uint32_t>((size_t)Bn / 16 + 1);
         b.occ_packed = dalloc<unsigned char>(graft::nerf_heads_packed_bytes());
         b.occ_sorted = dalloc<float4>((size_t)b.occ_capacity);
         b.occ_perm = dalloc<uint32_t>((size_t)b.occ_capacity);
@@ -689,6 +692,7 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         hb.denc = db.dx_out;
         hb.density_dy = db.dloss;
         hb.color_dx = b.color_dx;
+        hb.tile_live = b.tile_live;
         const bool heads = b.heads_packed != nullptr;
         const bool fused_dx = !heads && graft::nerf_backward_dx(bx, 0, stream);  // shape check only (N = 0)
         const bool dx_only = !heads && graft::mlp_has_dx_kernel(cshape) && graft::mlp_has_dx_kernel(dshape);

@@ -358,7 +358,7 @@ static graft::NerfHeadsBwd heads_bwd(const void* d_packed, const GRAFT_HALF* d_e
 void launchNerfHeadsBackward(const void* d_packed, const GRAFT_HALF* d_enc, int enc_plane, int levels,
                              const GRAFT_HALF* d_color_in, const GRAFT_HALF* d_color_dy, const float* d_dsigma,
                              int num_samples, GRAFT_HALF* d_denc, GRAFT_HALF* d_density_dy, GRAFT_HALF* d_color_dx,
-                             hipStream_t stream)
+                             uint32_t* d_tile_live, hipStream_t stream)
 {
     guarded("launchNerfHeadsBackward", [&] {
         if (num_samples < 0) throw std::runtime_error("num_samples must be >= 0");
@@ -367,15 +367,16 @@ void launchNerfHeadsBackward(const void* d_packed, const GRAFT_HALF* d_enc, int 
         h.denc = d_denc;
         h.density_dy = d_density_dy;
         h.color_dx = d_color_dx;
+        h.tile_live = d_tile_live;
         graft::nerf_heads_dx(h, num_samples, stream);
     });
 }
 
 void launchNerfHeadsWeightGrads(const void* d_packed, const GRAFT_HALF* d_enc, int enc_plane, int levels,
                                 const GRAFT_HALF* d_color_in, const GRAFT_HALF* d_color_dy, const float* d_dsigma,
-                                const GRAFT_HALF* d_density_dy, int num_samples, float* const* d_density_dw,
-                                float* const* d_density_db, float* const* d_color_dw, float* const* d_color_db,
-                                hipStream_t stream)
+                                const GRAFT_HALF* d_density_dy, const uint32_t* d_tile_live, int num_samples,
+                                float* const* d_density_dw, float* const* d_density_db, float* const* d_color_dw,
+                                float* const* d_color_db, hipStream_t stream)
 {
     guarded("launchNerfHeadsWeightGrads", [&] {
         if (num_samples < 0) throw std::runtime_error("num_samples must be >= 0");
@@ -383,6 +384,7 @@ void launchNerfHeadsWeightGrads(const void* d_packed, const GRAFT_HALF* d_enc, i
         graft::NerfHeadsBwd h = heads_bwd(d_packed, d_enc, enc_plane, levels, d_color_in, d_color_dy, d_dsigma);
         // read only: the density dL/dy launchNerfHeadsBackward stored for these inputs
         h.density_dy = const_cast<__half*>(reinterpret_cast<const __half*>(d_density_dy));
+        h.tile_live = const_cast<uint32_t*>(d_tile_live);  // read only here
         // the whole GPU: two blocks per CU (one of each head)
         h.dw_blocks = graft::num_cus();
         graft::nerf_heads_dw(h, graft::NerfHeadsGrads{d_density_dw, d_density_db, d_color_dw, d_color_db},

@@ -45,6 +45,10 @@ struct NerfHeadsBwd {
     __half* denc = nullptr;            // [N x 32] dL/d(encoding) (nerf_heads_dx)
     __half* density_dy = nullptr;      // nullable [N x 16]
     __half* color_dx = nullptr;        // nullable [N x 32]: logit features; the SH features are not computed (0)
+    // nullable [ceil(N / 16)]: nerf_heads_dx stores per 16-sample tile whether
+    // any gradient through the heads is nonzero; nerf_heads_dw given the same
+    // array (of the same inputs) skips the others (they add nothing)
+    uint32_t* tile_live = nullptr;
     int dw_blocks = 0;                 // weight-gradient blocks per head (0: half the CUs each, so that the
                                        // kernel leaves room beside the scatter it runs with)
 };

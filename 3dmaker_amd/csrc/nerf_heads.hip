@@ -589,6 +589,8 @@ struct BwdParams {
     _Float16* cdx;         // nullable [N x 32] colour dL/d(input): logit features, SH features 0
     float* ws_d;           // [gridDim.x][PD] (weight-gradient kernel)
     float* ws_c;           // [gridDim.x][PC]
+    uint32_t* tile_live;   // nullable [tiles]: the dX kernel stores which tiles have a nonzero gradient, the
+                           // weight-gradient kernel then visits only those
 };
 
 __device__ __forceinline__ BwdIn load_bwd(const BwdParams& p, int n, bool valid, int g)
@@ -604,6 +606,43 @@ __device__ __forceinline__ BwdIn load_bwd(const BwdParams& p, int n, bool valid,
     in.cdy = load_cdy(p.cdy, n, valid, g);
     in.ds = (valid && g == 0) ? p.dsigma[n] : 0.0f;
     return in;
+}
+
+// A tile whose colour dL/dy is zero in every sample, and whose density dL/dy
+// (the glue of a zero colour dL/dx and d sigma) rounds to zero as well, has
+// zero gradients through both heads: every dL/d(encoding), dW and db term of
+// it is 0 (samples past a ray's saturated transmittance; about half the tiles
+// of a converged scene).  The kernels below skip such tiles wave-uniformly;
+// the dX kernel stores what the chain would (zeros, and the glue of +0).
+
+// density dL/dy slot 0 of a sample whose colour dL/dx is +0 (the glue)
+__device__ __forceinline__ _Float16 glue_of_zero(float ds)
+{
+    float f = 0.0f + ds;
+    f = clamp_half_range(f);
+    if (f != f) f = 0.0f;
+    return to_h(f);
+}
+
+__device__ __forceinline__ bool h8_nonzero(h8 v)
+{
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 b = __builtin_bit_cast(u32x4, v);
+    return ((b[0] | b[1] | b[2] | b[3]) & 0x7fff7fffu) != 0u;
+}
+
+__device__ __forceinline__ bool h4_nonzero(h4 v)
+{
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 b = __builtin_bit_cast(u32x2, v);
+    return ((b[0] | b[1]) & 0x7fff7fffu) != 0u;
+}
+
+// the whole wave's tile has some nonzero colour dL/dy or density dL/dy
+__device__ __forceinline__ bool tile_live(h8 cdy, float ds, int g)
+{
+    const bool mine = h8_nonzero(cdy) || (g == 0 && (__builtin_bit_cast(uint16_t, glue_of_zero(ds)) & 0x7fffu) != 0u);
+    return __ballot(mine) != 0ull;
 }
 
 __global__ __launch_bounds__(256) void heads_dx_kernel(const BwdParams p)
@@ -627,10 +666,18 @@ __global__ __launch_bounds__(256) void heads_dx_kernel(const BwdParams p)
         // the next tile's inputs are in flight while this one computes
         const int nt = tile + nw;
         const BwdIn nxt = load_bwd(p, nt * 16 + r, nt < ntiles && nt * 16 + r < N, g);
-        Acts a;
-        recompute_tile(w, sbias, cur.enc, cur.cin, g, a);
         Grads gr;
-        backward_tile<true>(str, lane, a, cur.cdy, cur.ds, gr);
+        const bool live = tile_live(cur.cdy, cur.ds, g);
+        if (p.tile_live && lane == 0) p.tile_live[tile] = live ? 1u : 0u;
+        if (live) {
+            Acts a;
+            recompute_tile(w, sbias, cur.enc, cur.cin, g, a);
+            backward_tile<true>(str, lane, a, cur.cdy, cur.ds, gr);
+        } else {
+            gr.denc[0] = gr.denc[1] = gr.cx = h4zero();
+            gr.d1 = h4zero();
+            if (g == 0) gr.d1[0] = glue_of_zero(cur.ds);
+        }
         if (valid) {
             st_h4(p.denc + (size_t)n * DIN + 4 * g, gr.denc[0]);
             st_h4(p.denc + (size_t)n * DIN + 16 + 4 * g, gr.denc[1]);
@@ -793,6 +840,20 @@ __device__ __forceinline__ void put_b(float* s, int bofs, int mo, float v, int r
 // Blocks [0, color_blocks) accumulate the colour head's gradients over every
 // tile, the others the density head's: each block partial is one head's row
 // of the workspace.
+// The first live tile of t, t + stride, t + 2 stride, ... (ntiles if none):
+// 64 candidates per step, one per lane; wave-uniform.
+__device__ __forceinline__ int next_live(const uint32_t* __restrict__ live, int t, int stride, int ntiles, int lane)
+{
+    for (; t < ntiles; t += 64 * stride) {
+        const int c = t + lane * stride;
+        const uint64_t m = __ballot(c < ntiles && live[c] != 0u);
+        if (m) return t + (__ffsll((unsigned long long)m) - 1) * stride;
+    }
+    return ntiles;
+}
+
+// LIVE: p.tile_live holds the dX kernel's flags and only live tiles are visited
+template <bool LIVE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void heads_dw_kernel(const BwdParams p,
                                                                                                int color_blocks)
 {
@@ -827,18 +888,37 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void h
         }
         A.b2 = 0.f;
         const int stride = nb * waves;
-        int tile = rb * waves + wave;
-        // invalid samples: zero dL/dy; the next tile's inputs are in flight
-        // while this one computes
-        BwdIn in = load_bwd(p, tile * 16 + r, tile < ntiles && tile * 16 + r < N, g);
-        for (; tile < ntiles; tile += stride) {
-            reload_fence();
-            const int nt = tile + stride;
-            const BwdIn nxt = load_bwd(p, nt * 16 + r, nt < ntiles && nt * 16 + r < N, g);
-            Acts a;
-            recompute_tile(w, sbias, in.enc, in.cin, g, a);
-            color_dw_tile(A, str, lane, a, lo4(in.cdy), ident);
-            in = nxt;
+        if constexpr (LIVE) {
+            // this wave's live tiles (every stride-th tile; the dead ones add
+            // nothing), in order
+            // invalid samples: zero dL/dy; the next live tile's inputs are in
+            // flight while this one computes
+            int tile = next_live(p.tile_live, rb * waves + wave, stride, ntiles, lane);
+            BwdIn in = load_bwd(p, tile * 16 + r, tile < ntiles && tile * 16 + r < N, g);
+            while (tile < ntiles) {
+                reload_fence();
+                const int nt = next_live(p.tile_live, tile + stride, stride, ntiles, lane);
+                const BwdIn nxt = load_bwd(p, nt * 16 + r, nt < ntiles && nt * 16 + r < N, g);
+                Acts a;
+                recompute_tile(w, sbias, in.enc, in.cin, g, a);
+                color_dw_tile(A, str, lane, a, lo4(in.cdy), ident);
+                in = nxt;
+                tile = nt;
+            }
+        } else {
+            int tile = rb * waves + wave;
+            // invalid samples: zero dL/dy; the next tile's inputs are in
+            // flight while this one computes
+            BwdIn in = load_bwd(p, tile * 16 + r, tile < ntiles && tile * 16 + r < N, g);
+            for (; tile < ntiles; tile += stride) {
+                reload_fence();
+                const int nt = tile + stride;
+                const BwdIn nxt = load_bwd(p, nt * 16 + r, nt < ntiles && nt * 16 + r < N, g);
+                Acts a;
+                recompute_tile(w, sbias, in.enc, in.cin, g, a);
+                color_dw_tile(A, str, lane, a, lo4(in.cdy), ident);
+                in = nxt;
+            }
         }
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -885,19 +965,39 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void h
                 enc = load_enc(p.enc, p.plane, p.L, n, valid, g);
                 d1 = valid ? ld_h4(p.dloss + (size_t)n * DOUT + 4 * g) : h4zero();
             };
-            h8 enc;
-            h4 d1;
-            load(tile, enc, d1);
-            for (; tile < ntiles; tile += stride) {
-                reload_fence();
-                h8 enc_n;
-                h4 d1_n;
-                load(tile + stride, enc_n, d1_n);
-                h8 hd[2];
-                recompute_density(w, sbias, enc, g, hd);
-                density_dw_update(A, str, lane, hd, enc, d1, ident);
-                enc = enc_n;
-                d1 = d1_n;
+            if constexpr (LIVE) {
+                int t = next_live(p.tile_live, tile, stride, ntiles, lane);
+                h8 enc;
+                h4 d1;
+                load(t, enc, d1);
+                while (t < ntiles) {
+                    reload_fence();
+                    const int nt = next_live(p.tile_live, t + stride, stride, ntiles, lane);
+                    h8 enc_n;
+                    h4 d1_n;
+                    load(nt, enc_n, d1_n);
+                    h8 hd[2];
+                    recompute_density(w, sbias, enc, g, hd);
+                    density_dw_update(A, str, lane, hd, enc, d1, ident);
+                    enc = enc_n;
+                    d1 = d1_n;
+                    t = nt;
+                }
+            } else {
+                h8 enc;
+                h4 d1;
+                load(tile, enc, d1);
+                for (; tile < ntiles; tile += stride) {
+                    reload_fence();
+                    h8 enc_n;
+                    h4 d1_n;
+                    load(tile + stride, enc_n, d1_n);
+                    h8 hd[2];
+                    recompute_density(w, sbias, enc, g, hd);
+                    density_dw_update(A, str, lane, hd, enc, d1, ident);
+                    enc = enc_n;
+                    d1 = d1_n;
+                }
             }
         } else {
             BwdIn in = load_bwd(p, tile * 16 + r, tile < ntiles && tile * 16 + r < N, g);
@@ -1061,6 +1161,7 @@ static BwdParams bwd_params(const NerfHeadsBwd& a, int N, const uint32_t* d_n)
     p.denc = reinterpret_cast<_Float16*>(a.denc);
     p.dloss = reinterpret_cast<_Float16*>(a.density_dy);
     p.cdx = reinterpret_cast<_Float16*>(a.color_dx);
+    p.tile_live = a.tile_live;
     return p;
 }
 
@@ -1089,7 +1190,8 @@ void nerf_heads_dw(const NerfHeadsBwd& a, const NerfHeadsGrads& out, int N, hipS
     float* part = static_cast<float*>(w.get(((size_t)cb * PC + (size_t)db * PD) * sizeof(float)));
     p.ws_c = part;
     p.ws_d = part + (size_t)cb * PC;
-    hipLaunchKernelGGL(heads_dw_kernel, dim3(cb + db), dim3(256), lds, s, p, cb);
+    if (p.tile_live) hipLaunchKernelGGL(heads_dw_kernel<true>, dim3(cb + db), dim3(256), lds, s, p, cb);
+    else hipLaunchKernelGGL(heads_dw_kernel<false>, dim3(cb + db), dim3(256), lds, s, p, cb);
     GRAFT_LAUNCH_CHECK();
     const MlpShape ds{DIN, DHID, DOUT, 2}, cs{CIN, CHID, COUT, 3};
     mlp_grad_reduce(ds, p.ws_d, db, out.dW, out.dB, false, s);

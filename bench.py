@@ -453,6 +453,7 @@ def heads_components(P, torch, dev, rng, x, d_dirs, ridx, sp, timed):
     ds = torch.from_numpy(rng.normal(0, 0.1, BATCH).astype(np.float32)).to(dev)
     denc = torch.empty((BATCH, 32), dtype=torch.float16, device=dev)
     ddy = torch.empty((BATCH, 16), dtype=torch.float16, device=dev)  # density dL/dy: dX kernel -> dW kernel
+    live = torch.empty(BATCH // 16 + 1, dtype=torch.int32, device=dev)  # tiles with a nonzero gradient
 
     def fwd():
         lib.launchNerfHeadsForward(packed.data_ptr(), enc.data_ptr(), BATCH, L, d_dirs.data_ptr(), ridx.data_ptr(),
@@ -460,11 +461,11 @@ def heads_components(P, torch, dev, rng, x, d_dirs, ridx, sp, timed):
 
     def dx():
         lib.launchNerfHeadsBackward(packed.data_ptr(), enc.data_ptr(), BATCH, L, cin.data_ptr(), cdy.data_ptr(),
-                                    ds.data_ptr(), BATCH, denc.data_ptr(), ddy.data_ptr(), None, sp)
+                                    ds.data_ptr(), BATCH, denc.data_ptr(), ddy.data_ptr(), None, live.data_ptr(), sp)
 
     def dw():
         lib.launchNerfHeadsWeightGrads(packed.data_ptr(), enc.data_ptr(), BATCH, L, cin.data_ptr(), cdy.data_ptr(),
-                                       ds.data_ptr(), ddy.data_ptr(), BATCH, dgW.data_ptr(), dgB.data_ptr(),
+                                       ds.data_ptr(), ddy.data_ptr(), live.data_ptr(), BATCH, dgW.data_ptr(), dgB.data_ptr(),
                                        cgW.data_ptr(), cgB.data_ptr(), sp)
 
     def step():

@@ -253,23 +253,28 @@ void launchNerfHeadsForward(const void* d_packed, const GRAFT_HALF* d_enc, int e
  * colour dX chain from d_color_dy (fp16 [N][8]), the density-gradient glue
  * with d_dsigma and the density dX chain: d_denc fp16 [N][32] = dL/d(encoding);
  * d_density_dy (fp16 [N][16]) and d_color_dx (fp16 [N][32], the logit
- * features; the SH features are written as 0) are nullable. */
+ * features; the SH features are written as 0) are nullable.  16-sample tiles
+ * whose colour dL/dy is zero and whose density dL/dy rounds to +-0 skip the
+ * chain (their outputs are the chain's: zeros and the glue of +0);
+ * d_tile_live (nullable, uint32 [ceil(N / 16)]) receives 1 for the others. */
 void launchNerfHeadsBackward(const void* d_packed, const GRAFT_HALF* d_enc, int enc_plane, int levels,
                              const GRAFT_HALF* d_color_in, const GRAFT_HALF* d_color_dy, const float* d_dsigma,
                              int num_samples, GRAFT_HALF* d_denc, GRAFT_HALF* d_density_dy, GRAFT_HALF* d_color_dx,
-                             hipStream_t stream);
+                             uint32_t* d_tile_live, hipStream_t stream);
 
 /* The weight gradients of every layer of both heads for the same inputs,
  * stored (not added) into the per-layer fp32 arrays (device arrays of device
  * pointers); the block partials are summed in a fixed order.  d_density_dy
  * (nullable) is the density dL/dy launchNerfHeadsBackward stored for the same
  * inputs: given, the density head's gradients start from it instead of
- * running the colour dX chain again (same values). */
+ * running the colour dX chain again (same values).  d_tile_live (nullable)
+ * is that call's tile flags: only the flagged tiles are visited (the others
+ * add nothing). */
 void launchNerfHeadsWeightGrads(const void* d_packed, const GRAFT_HALF* d_enc, int enc_plane, int levels,
                                 const GRAFT_HALF* d_color_in, const GRAFT_HALF* d_color_dy, const float* d_dsigma,
-                                const GRAFT_HALF* d_density_dy, int num_samples, float* const* d_density_dw,
-                                float* const* d_density_db, float* const* d_color_dw, float* const* d_color_db,
-                                hipStream_t stream);
+                                const GRAFT_HALF* d_density_dy, const uint32_t* d_tile_live, int num_samples,
+                                float* const* d_density_dw, float* const* d_density_db, float* const* d_color_dw,
+                                float* const* d_color_db, hipStream_t stream);
 
 /* ABI self-check (no reference counterpart): writes a.xyz, b.xyz to out[0..6). */
 void nerf_abi_echo_vec(float3 a, uint3 b, float* out);

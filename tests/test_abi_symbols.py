@@ -73,9 +73,9 @@ def test_launcher_argument_errors_without_gpu():
     assert L.tinymlp_last_error() != 0 and b"plane" in L.tinymlp_last_error_message()
     L.launchNerfHeadsForward(fake, fake, 64, 17, fake, fake, 64, 0.0, 1, fake, None, fake, fake, None)
     assert L.tinymlp_last_error() != 0 and b"levels" in L.tinymlp_last_error_message()
-    L.launchNerfHeadsBackward(fake, fake, 64, 16, None, fake, fake, 64, fake, None, None, None)
+    L.launchNerfHeadsBackward(fake, fake, 64, 16, None, fake, fake, 64, fake, None, None, None, None)
     assert L.tinymlp_last_error() != 0 and b"null" in L.tinymlp_last_error_message()
-    L.launchNerfHeadsWeightGrads(fake, fake, 64, 16, fake, fake, fake, None, 64, None, fake, fake, fake, None)
+    L.launchNerfHeadsWeightGrads(fake, fake, 64, 16, fake, fake, fake, None, None, 64, None, fake, fake, fake, None)
     assert L.tinymlp_last_error() != 0 and b"null" in L.tinymlp_last_error_message()
     L.launchNerfHeadsPack(None, fake, fake, fake, fake, None)
     assert L.tinymlp_last_error() != 0 and b"null" in L.tinymlp_last_error_message()

@@ -74,7 +74,7 @@ def big_close(got, want, what):
     assert_close(got, want, atol=2e-3 * max(1.0, float(np.abs(want).max())), what=what)
 
 
-def make_case(N, levels, plane_pad, seed, dev):
+def make_case(N, levels, plane_pad, seed, dev, zero_tiles=False):
     rng = np.random.default_rng(seed)
     R = max(1, N // 7)
     enc = np.zeros((N, 32), np.float16)
@@ -89,11 +89,24 @@ def make_case(N, levels, plane_pad, seed, dev):
     cdy = np.zeros((n1, 8), np.float16)
     cdy[:, :3] = rng.uniform(-0.5, 0.5, (n1, 3)).astype(np.float16)
     dsig = rng.uniform(-1, 1, n1).astype(np.float32)
+    if zero_tiles:
+        # tiles past a saturated transmittance: zero colour dL/dy and a d sigma that rounds to +-0 in fp16
+        # (skipped tiles); tiles with zero colour dL/dy but one live d sigma; a zero run across a tile edge
+        for t in range((n1 + 15) // 16):
+            sl = slice(16 * t, min(16 * t + 16, n1))
+            if t % 3 == 0:
+                cdy[sl] = 0
+                dsig[sl] = rng.choice([0.0, -0.0, 1e-30, -1e-30, 2e-8, -2e-8], sl.stop - sl.start).astype(np.float32)
+            elif t % 3 == 1:
+                cdy[sl] = 0
+                dsig[sl] = 0.0
+                dsig[16 * t] = 0.25
+        cdy[8:24] = 0
     return dict(N=N, levels=levels, plane=plane, enc=enc, planar=planar, dirs=dirs, ridx=ridx, cdy=cdy, dsig=dsig)
 
 
 class Run:
-    def __init__(self, case, dh, ch, dev, bias=0.5, act=1, stored_dy=False):
+    def __init__(self, case, dh, ch, dev, bias=0.5, act=1, stored_dy=False, tile_flags=False):
         P = pkg()
         self.L = L = P.lib()
         N = case["N"]
@@ -119,14 +132,18 @@ class Run:
         self.denc = torch.full((n1, 32), float("nan"), dtype=torch.float16, device=dev)
         self.ddy = torch.full((n1, 16), float("nan"), dtype=torch.float16, device=dev)
         self.cdx = torch.full((n1, 32), float("nan"), dtype=torch.float16, device=dev)
+        # tile_flags: the backward flags the tiles with a nonzero gradient, the weight gradients visit those
+        self.live = torch.full(((n1 + 15) // 16,), 7, dtype=torch.int32, device=dev)
         L.launchNerfHeadsBackward(self.packed.data_ptr(), self.enc.data_ptr(), case["plane"], case["levels"],
                                   self.cin.data_ptr(), self.cdy.data_ptr(), self.dsig.data_ptr(), N,
-                                  self.denc.data_ptr(), self.ddy.data_ptr(), self.cdx.data_ptr(), None)
+                                  self.denc.data_ptr(), self.ddy.data_ptr(), self.cdx.data_ptr(),
+                                  self.live.data_ptr() if tile_flags else None, None)
         check(L, "backward")
         # stored_dy: the density head's gradients start from the density dL/dy the backward stored
         L.launchNerfHeadsWeightGrads(self.packed.data_ptr(), self.enc.data_ptr(), case["plane"], case["levels"],
                                      self.cin.data_ptr(), self.cdy.data_ptr(), self.dsig.data_ptr(),
-                                     self.ddy.data_ptr() if stored_dy else None, N,
+                                     self.ddy.data_ptr() if stored_dy else None,
+                                     self.live.data_ptr() if tile_flags else None, N,
                                      dh.pgw.data_ptr(), dh.pgb.data_ptr(), ch.pgw.data_ptr(), ch.pgb.data_ptr(), None)
         check(L, "weight grads")
         torch.cuda.synchronize()
@@ -180,6 +197,30 @@ def test_heads_match_oracle(dev, N, levels, pad, act, stored_dy):
     check_against_oracle(run, dh, ch)
 
 
+@pytest.mark.parametrize("stored_dy,tile_flags", [(False, False), (True, False), (False, True), (True, True)])
+def test_heads_skip_zero_gradient_tiles(dev, stored_dy, tile_flags):
+    """Tiles whose colour dL/dy is zero and whose density dL/dy rounds to +-0 are skipped by the dX kernel and,
+    with its tile flags, by the weight-gradient kernel: same results as the chain (zero dL/d(encoding), the
+    glue of +0 and d sigma, zero dW terms), against the oracle; the flags mark exactly the live tiles."""
+    dh, ch = Head(DSHAPE, 51, dev), Head(CSHAPE, 52, dev)
+    case = make_case(3001, 16, 7, 77, dev, zero_tiles=True)
+    run = Run(case, dh, ch, dev, stored_dy=stored_dy, tile_flags=tile_flags)
+    check_against_oracle(run, dh, ch)
+    g = run.host()
+    ntiles = (3001 + 15) // 16
+    cdy = np.zeros((ntiles * 16, 8), np.float16)
+    cdy[:3001] = case["cdy"][:3001]
+    glue = np.zeros(ntiles * 16, np.float16)
+    glue[:3001] = np.clip(np.nan_to_num(np.float32(0.0) + case["dsig"][:3001], nan=0.0), -65504, 65504)
+    live = ((cdy.view(np.uint16) & 0x7fff).reshape(ntiles, -1).any(1) |
+            (glue.view(np.uint16) & 0x7fff).reshape(ntiles, 16).any(1))
+    assert (~live).sum() > ntiles // 4
+    rows = np.concatenate([np.arange(16 * t, min(16 * t + 16, 3001)) for t in np.nonzero(~live)[0]])
+    assert not (g["denc"][rows].view(np.uint16) & 0x7fff).any()
+    if tile_flags:
+        np.testing.assert_array_equal(run.live.cpu().numpy() != 0, live)
+
+
 def test_heads_density_grads_from_stored_dy_match_the_recomputed_ones(dev):
     """The density head's dW/db from the stored density dL/dy equal those of the recomputed colour chain
     (the dX kernel's operations: the same per-sample values); the two paths split the blocks between the
@@ -213,7 +254,7 @@ def test_heads_weight_grads_are_deterministic_and_overwrite(dev):
         t.fill_(123.0)
     L = run.L
     L.launchNerfHeadsWeightGrads(run.packed.data_ptr(), run.enc.data_ptr(), case["plane"], case["levels"],
-                                 run.cin.data_ptr(), run.cdy.data_ptr(), run.dsig.data_ptr(), None, case["N"],
+                                 run.cin.data_ptr(), run.cdy.data_ptr(), run.dsig.data_ptr(), None, None, case["N"],
                                  dh.pgw.data_ptr(), dh.pgb.data_ptr(), ch.pgw.data_ptr(), ch.pgb.data_ptr(), None)
     check(L, "weight grads")
     second = dh.grads() + ch.grads()
