@@ -142,7 +142,7 @@ SIGNATURES = {
     "tmlp_grid_backward": (_i, [_vp, _vp, _i, _vp]),
     "tmlp_grid_set_split_scatter": (_i, [_vp, _i]),
     "tmlp_grid_step": (_i, [_vp, _f, _f, _f, _f, _f, _vp]),
-    "tmlp_grid_scatter_adam_table": (_i, [_vp, _vp, _vp, _i, _i, _f, _f, _f, _f, _f, _vp]),
+    "tmlp_grid_scatter_adam_table": (_i, [_vp, _vp, _vp, _i, _i, _f, _f, _f, _f, _f, _vp, _vp]),
     "tmlp_grid_step_mlp": (_i, [_vp, _f, _f, _f, _f, _f, _vp]),
     "tmlp_grid_reset_step": (_i, [_vp]),
     "tmlp_grid_load_weights": (_i, [_vp, _vp, _vp]),
@@ -349,10 +349,11 @@ class HashGrid:
         self._c(self._L.tmlp_grid_step(self.h, lr, beta1, beta2, eps, loss_scale, stream))
 
     def scatter_adam_table(self, dx, positions, n, pos_stride=4, lr=3e-4, beta1=0.9, beta2=0.999, eps=1e-8,
-                           loss_scale=65536.0, stream=0):
-        """The table half of the next step, fused into the scatter of dx (TinyMLPHashGrid::scatterAdamTable)."""
+                           loss_scale=65536.0, stream=0, tile_live=None):
+        """The table half of the next step, fused into the scatter of dx (TinyMLPHashGrid::scatterAdamTable);
+        tile_live: optional uint32 per 16 rows of dx, 0 where the rows are all +-0 (skipped)."""
         self._c(self._L.tmlp_grid_scatter_adam_table(self.h, ptr(dx), ptr(positions), pos_stride, n, lr, beta1, beta2,
-                                                     eps, loss_scale, stream))
+                                                     eps, loss_scale, ptr(tile_live), stream))
 
     def step_mlp(self, lr=3e-4, beta1=0.9, beta2=0.999, eps=1e-8, loss_scale=65536.0, stream=0):
         self._c(self._L.tmlp_grid_step_mlp(self.h, lr, beta1, beta2, eps, loss_scale, stream))

@@ -303,13 +303,14 @@ int tmlp_grid_step(TmlpGrid* h, float lr, float b1, float b2, float eps, float l
     return GRID_CALL("step", h->g->step(lr, b1, b2, eps, loss_scale, s));
 }
 int tmlp_grid_scatter_adam_table(TmlpGrid* h, const GRAFT_HALF* dx, const float* positions, int pos_stride, int N,
-                                 float lr, float b1, float b2, float eps, float loss_scale, hipStream_t s)
+                                 float lr, float b1, float b2, float eps, float loss_scale, const uint32_t* tile_live,
+                                 hipStream_t s)
 {
     return GRID_CALL("scatterAdamTable", {
         if (N < 0) throw std::runtime_error("N must be >= 0");
         if (N > 0 && (!dx || !positions)) throw std::runtime_error("null argument");
         h->g->scatterAdamTable(reinterpret_cast<const half*>(dx), positions, pos_stride, N, nullptr, lr, b1, b2, eps,
-                               loss_scale, s, nullptr);
+                               loss_scale, s, nullptr, tile_live);
     });
 }
 int tmlp_grid_step_mlp(TmlpGrid* h, float lr, float b1, float b2, float eps, float loss_scale, hipStream_t s)

@@ -68,6 +68,9 @@ constexpr int kDenseBins = 64;  // target bins per dense level
 
 struct ScatterArgs {
     const uint32_t* d_n;  // nullable device-side sample count (<= N)
+    // nullable, per 16-sample tile: 0 where every dL/denc of the tile is +-0
+    // (they add no record; their rows are not read)
+    const uint32_t* tile_live;
     int L, T, dense_start, pos_stride, N, bins, rounds;
     uint32_t mask;
     float scale[kMaxLevels];
@@ -205,7 +208,7 @@ __global__ __launch_bounds__(kBinThreads) void scatter_count_kernel(const Scatte
     const bool vec = (a.L & 3) == 0;
     for (int k = 0; k < kSamplesPerThread; k++) {
         const int n = blockIdx.x * kRound + k * kBinThreads + threadIdx.x;
-        const bool valid = n < N;
+        const bool valid = n < N && (!a.tile_live || a.tile_live[n >> 4] != 0u);
         float px = 0.f, py = 0.f, pz = 0.f;
         const uint32_t* grow = reinterpret_cast<const uint32_t*>(denc + (size_t)(valid ? n : 0) * 2 * a.L);
         if (valid) {
@@ -387,6 +390,7 @@ __global__ __launch_bounds__(kBinThreads) void scatter_distribute_kernel(
     for (int k = 0; k < kSamplesPerThread; k++) {
         const int n = blockIdx.x * kRound + k * kBinThreads + threadIdx.x;
         if (n >= N) break;
+        if (a.tile_live && a.tile_live[n >> 4] == 0u) continue;  // no record: every product is +-0
         const float* pp = pos + (size_t)n * a.pos_stride;
         const float px = pp[0], py = pp[1], pz = pp[2];
         const uint32_t* grow = reinterpret_cast<const uint32_t*>(denc + (size_t)n * 2 * a.L);
@@ -936,7 +940,7 @@ namespace {
 // into grads, or (ta) as the fused table update.
 void scatter_launch(ScatterPlan* p, const GridMeta& m, const __half* denc, const float* pos, int pos_stride,
                     float* grads, int N, hipStream_t stream, const uint32_t* d_n, bool grads_zero,
-                    const TableAdamArgs* ta, hipEvent_t wait_before)
+                    const TableAdamArgs* ta, hipEvent_t wait_before, const uint32_t* tile_live = nullptr)
 {
     if (N <= 0) return;
     if (!p) throw std::runtime_error("hash scatter: no scatter plan");
@@ -946,6 +950,7 @@ void scatter_launch(ScatterPlan* p, const GridMeta& m, const __half* denc, const
     if (ta && !p->part_nf) throw std::runtime_error("hash scatter: plan without the fused update's scratch");
     ScatterArgs a = p->args;
     a.d_n = d_n;
+    a.tile_live = tile_live;
     a.N = N;
     a.pos_stride = pos_stride;
     a.rounds = (N + kRound - 1) / kRound;
@@ -986,11 +991,12 @@ void hash_scatter_binned(ScatterPlan* p, const GridMeta& m, const __half* denc, 
 }
 
 void hash_scatter_adam(ScatterPlan* p, const GridMeta& m, const __half* denc, const float* pos, int pos_stride, int N,
-                       const TableAdam& t, hipStream_t stream, const uint32_t* d_n, hipEvent_t wait_before_update)
+                       const TableAdam& t, hipStream_t stream, const uint32_t* d_n, hipEvent_t wait_before_update,
+                       const uint32_t* tile_live)
 {
     if (!t.w || !t.w16 || !t.m || !t.v) throw std::runtime_error("hash scatter: null table or moment array");
     const TableAdamArgs ta{t.w, reinterpret_cast<_Float16*>(t.w16), t.m, t.v, t.a};
-    scatter_launch(p, m, denc, pos, pos_stride, nullptr, N, stream, d_n, false, &ta, wait_before_update);
+    scatter_launch(p, m, denc, pos, pos_stride, nullptr, N, stream, d_n, false, &ta, wait_before_update, tile_live);
 }
 
 namespace {

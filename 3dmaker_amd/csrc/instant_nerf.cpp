@@ -742,7 +742,7 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
             if (fused_table)
                 m_densityMLP->scatterAdamTable(db.dx_out, reinterpret_cast<const float*>(S.positions), 4, (int)Bn,
                                                d_hits, o.learningRate, o.beta1, o.beta2, o.epsilon, o.lossScale,
-                                               stream, refresh ? b.ev_join : nullptr);
+                                               stream, refresh ? b.ev_join : nullptr, heads ? b.tile_live : nullptr);
             else
                 // the table gradient is all zero here: the previous step's
                 // Adam cleared every entry it consumed

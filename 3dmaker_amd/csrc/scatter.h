@@ -35,6 +35,8 @@ void hash_scatter_binned(ScatterPlan* p, const GridMeta& m, const __half* denc, 
 // read or written, entries the batch does not reach keep every word (the
 // zero gradients adam_hash skips).  The update waits for wait_before_update
 // (nullable) after the sorting passes, before its first table read.
+// tile_live (nullable): per 16-sample tile of denc, 0 where every value of
+// the tile is +-0 (nerf_heads_dx's flags); those rows are not read.
 struct TableAdam {
     float* w;       // fp32 master table
     __half* w16;    // fp16 copy the encode reads
@@ -44,7 +46,7 @@ struct TableAdam {
 };
 void hash_scatter_adam(ScatterPlan* p, const GridMeta& m, const __half* denc, const float* pos, int pos_stride, int N,
                        const TableAdam& t, hipStream_t stream, const uint32_t* d_n = nullptr,
-                       hipEvent_t wait_before_update = nullptr);
+                       hipEvent_t wait_before_update = nullptr, const uint32_t* tile_live = nullptr);
 
 // hash_scatter_binned's sum (grads +=) with the scratch in a fixed static
 // device array instead of allocated memory: no allocation on any call.  The

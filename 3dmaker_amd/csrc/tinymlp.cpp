@@ -812,7 +812,8 @@ void TinyMLPHashGrid::stepSplit(float lr, float beta1, float beta2, float epsilo
 
 void TinyMLPHashGrid::scatterAdamTable(const half* d_dx_out, const float* d_positions, int pos_stride, int N,
                                        const uint32_t* d_n, float lr, float beta1, float beta2, float epsilon,
-                                       float loss_scale, hipStream_t stream, hipEvent_t wait_before_update)
+                                       float loss_scale, hipStream_t stream, hipEvent_t wait_before_update,
+                                       const uint32_t* d_tile_live)
 {
     if (!m_isTraining) throw std::runtime_error("step called while in inference mode!");
     if (!m_scatter) throw std::runtime_error("scatterAdamTable: this grid has no binned scatter");
@@ -821,7 +822,7 @@ void TinyMLPHashGrid::scatterAdamTable(const half* d_dx_out, const float* d_posi
     const graft::TableAdam t{d_master_hashtable, d_fwd_hashtable, d_hash_m, d_hash_v,
                              adam_args(next, lr, beta1, beta2, epsilon, loss_scale)};
     graft::hash_scatter_adam(static_cast<graft::ScatterPlan*>(m_scatter), META, d_dx_out, d_positions, pos_stride, N,
-                             t, stream, d_n, wait_before_update);
+                             t, stream, d_n, wait_before_update, d_tile_live);
 }
 
 void TinyMLPHashGrid::stepMlp(float lr, float beta1, float beta2, float epsilon, float loss_scale, hipStream_t stream)

@@ -76,10 +76,12 @@ public:
     // the gradient the scatter would have stored (no gradient array).  The
     // step count is not advanced: stepMlp(), which follows, does that.
     // wait_before_update (nullable) is waited on before the first table
-    // write.  Needs the binned scatter (scatter_plan non-null).
+    // write.  Needs the binned scatter (scatter_plan non-null).  d_tile_live
+    // (nullable): per 16-sample tile of d_dx_out, 0 where the whole tile is
+    // +-0 (those rows are skipped: they add nothing).
     void scatterAdamTable(const half* d_dx_out, const float* d_positions, int pos_stride, int N, const uint32_t* d_n,
                           float lr, float beta1, float beta2, float epsilon, float loss_scale, hipStream_t stream,
-                          hipEvent_t wait_before_update);
+                          hipEvent_t wait_before_update, const uint32_t* d_tile_live = nullptr);
     // The MLP half of step(): advances the step count, updates the layers.
     void stepMlp(float lr, float beta1, float beta2, float epsilon, float loss_scale, hipStream_t stream);
 

@@ -76,9 +76,11 @@ int tmlp_grid_set_split_scatter(TmlpGrid* h, int enabled);
 int tmlp_grid_step(TmlpGrid* h, float lr, float b1, float b2, float eps, float loss_scale, hipStream_t s);
 /* TinyMLPHashGrid::scatterAdamTable (no reference counterpart): scatter of dx [N x 2L] at positions
  * (pos_stride floats each) with the table's Adam update of the next step fused in; then
- * tmlp_grid_step_mlp (TinyMLPHashGrid::stepMlp) advances the step and updates the MLP layers. */
+ * tmlp_grid_step_mlp (TinyMLPHashGrid::stepMlp) advances the step and updates the MLP layers.
+ * tile_live (nullable, uint32 per 16 rows of dx): 0 where all 16 rows are +-0 (skipped). */
 int tmlp_grid_scatter_adam_table(TmlpGrid* h, const GRAFT_HALF* dx, const float* positions, int pos_stride, int N,
-                                 float lr, float b1, float b2, float eps, float loss_scale, hipStream_t s);
+                                 float lr, float b1, float b2, float eps, float loss_scale, const uint32_t* tile_live,
+                                 hipStream_t s);
 int tmlp_grid_step_mlp(TmlpGrid* h, float lr, float b1, float b2, float eps, float loss_scale, hipStream_t s);
 int tmlp_grid_reset_step(TmlpGrid* h);
 int tmlp_grid_load_weights(TmlpGrid* h, const float* host_w, const float* host_b);

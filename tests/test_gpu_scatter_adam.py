@@ -52,10 +52,16 @@ def bits(a):
     return a.view(np.uint16 if a.dtype == np.float16 else np.uint32)
 
 
-@pytest.mark.parametrize("T_,L,b,N,steps", [(1 << 14, 16, 1.447, 1 << 16, 3), (1 << 19, 16, 1.3819, 3001, 2),
-                                            (1 << 19, 16, 1.3819, 1 << 17, 2), (1 << 12, 8, 2.0, 777, 2)])
-def test_fused_table_update_equals_scatter_then_step(dev, T_, L, b, N, steps):
-    print(f"[scatter adam] T={T_} L={L} N={N}", flush=True)
+@pytest.mark.parametrize("T_,L,b,N,steps,flags", [(1 << 14, 16, 1.447, 1 << 16, 3, False),
+                                                  (1 << 19, 16, 1.3819, 3001, 2, False),
+                                                  (1 << 19, 16, 1.3819, 1 << 17, 2, False),
+                                                  (1 << 12, 8, 2.0, 777, 2, False),
+                                                  (1 << 19, 16, 1.3819, 1 << 17, 2, True),
+                                                  (1 << 14, 16, 1.447, 3001, 2, True)])
+def test_fused_table_update_equals_scatter_then_step(dev, T_, L, b, N, steps, flags):
+    """flags: whole 16-row tiles of dx are +-0 and flagged dead (the dX kernel's tile flags): skipped rows,
+    same table."""
+    print(f"[scatter adam] T={T_} L={L} N={N} flags={flags}", flush=True)
     P = pkg()
     ga, gb = make_grid(T_, L, b, N, 5), make_grid(T_, L, b, N, 5)
     n = L * T_ * 2
@@ -70,6 +76,14 @@ def test_fused_table_update_equals_scatter_then_step(dev, T_, L, b, N, steps):
         dx[rng.random((N, 2 * L)) < 0.3] = 0  # zero gradients: entries no product reaches
         if step == steps - 1 and N > 40:
             dx[5, 0], dx[17, 3], dx[33, 2 * L - 1] = np.inf, -np.inf, np.nan
+        live = None
+        if flags:
+            ntiles = (N + 15) // 16
+            dead = rng.random(ntiles) < 0.5
+            dead[:3] = False
+            for t in np.nonzero(dead)[0]:
+                dx[16 * t:16 * t + 16] = np.where(rng.random(dx[16 * t:16 * t + 16].shape) < 0.5, -0.0, 0.0)
+            live = T((~dead).astype(np.uint32), dev)
         d_pos, d_dx = T(pos, dev), T(dx, dev)
         # stored path: scatter into the zero gradient array, then the optimizer step
         ga.zero_grad()
@@ -77,7 +91,7 @@ def test_fused_table_update_equals_scatter_then_step(dev, T_, L, b, N, steps):
         ga.step(LR, B1, B2, EPS, SCALE)
         # fused path
         gb.zero_grad()
-        gb.scatter_adam_table(d_dx, d_pos, N, 4, LR, B1, B2, EPS, SCALE)
+        gb.scatter_adam_table(d_dx, d_pos, N, 4, LR, B1, B2, EPS, SCALE, tile_live=live)
         gb.step_mlp(LR, B1, B2, EPS, SCALE)
         torch.cuda.synchronize()
         sa, sb = state(ga, n), state(gb, n)
