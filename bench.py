@@ -57,6 +57,7 @@ RAYS_PER_CALL = 1 << 16
 N_VIEWS, N_HELDOUT, IMG_W, IMG_H, FOV_X = 100, 12, 800, 800, 50.0
 L, F, TBL, BASE, GROWTH = 16, 2, 1 << 19, 16, 1.3819
 LR_MAX, LR_MIN, ANNEAL = 1e-2, 1e-4, 2000
+C5_SEEDS = (1, 2, 3, 4, 5)    # further background-draw seeds of the 5-cascade run
 PRETRAIN_STEPS = 256           # optimizer steps before the warm-up (past the early occupancy phase)
 CPU_FEED_CHUNKS = 8            # feed chunks of rays available to the CPU-oracle leg (stops after ~10 s)
 
@@ -378,9 +379,11 @@ def heldout_psnr(P, torch, nerf, feed, sp):
 
 def five_cascades(P, torch, feed, hfeed, sp):
     """The same run at 5 occupancy cascades (the configs[3] grid): step time, held-out PSNR, the PSNR of
-    fresh training-view rays (training composite and renderImageHit), occupied cells per cascade.  The step
-    math matches the oracle at 5 cascades (tests/test_gpu_c5.py); the outer cascades stay occupied and the
-    model fits the training views but not the held-out ones."""
+    fresh training-view rays (training composite and renderImageHit), occupied cells per cascade; then the
+    held-out PSNR of the same training at other seeds of the trainer's background draws.  The step math
+    matches the oracle at 5 cascades (tests/test_gpu_c5.py); with random backgrounds the training is
+    bistable: at some seeds the outer cascades fill with a fog that follows the backgrounds (held-out PSNR
+    under 12 dB), at the others it converges as at one cascade."""
     scenes = importlib.import_module("3dmaker_amd.scenes")
     nerf = P.Nerf(options(P, 5))
     tr = Trainer(nerf, feed, sp)
@@ -415,6 +418,17 @@ def five_cascades(P, torch, feed, hfeed, sp):
     S, G = scenes.pyramid_cells(128, 4), 128 ** 3
     out["occupied_fraction_per_cascade"] = [round(float(bits[c * S: c * S + G].mean()), 4) for c in range(5)]
     nerf.close()
+    # the trainer's background draws at other seeds (the run above: 42)
+    seeds = {}
+    for seed in C5_SEEDS:
+        nerf = P.Nerf(options(P, 5))
+        tr = Trainer(nerf, feed, sp)
+        tr.rng = np.random.default_rng(seed)
+        tr.run(ANNEAL)
+        torch.cuda.synchronize()
+        seeds[str(seed)] = heldout_psnr(P, torch, nerf, hfeed, sp)["value"]
+        nerf.close()
+    out["psnr_heldout_by_seed"] = seeds
     return out
 
 
