@@ -594,8 +594,13 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
             });
             GRAFT_HIP_CHECK(hipEventRecord(b.ev_join, b.occ));
         };
-        // hash encode + density head, SH gather (into the colour head's
-        // activation 0), colour head: one launch, activations saved
+        // hash encode (its own stage with the 16x16x32 heads), then density
+        // head, SH gather and colour head
+        if (b.heads_packed)
+            stage("encode", [&] {
+                graft::hash_encode_planar(b.meta, db.fwd_hashtable, reinterpret_cast<const float*>(S.positions), 4,
+                                          b.enc_planar, (int)Bn, (int)Bn, stream, d_hits);
+            });
         stage("forward", [&] {
             graft::NerfFwdArgs fa;
             fa.dshape = dshape;
@@ -623,6 +628,7 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
             fa.enc_plane = (int)Bn;
             fa.heads_packed = b.heads_packed;
             fa.heads_prepacked = true;  // packed at the call's start and after every step's layer Adam
+            fa.enc_ready = b.heads_packed != nullptr;
             graft::nerf_forward(fa, (int)Bn, stream, d_hits);
         });
 

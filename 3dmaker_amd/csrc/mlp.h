@@ -87,6 +87,7 @@ struct NerfFwdArgs {
     // holding only its levels' tables) and the network kernel reads it.
     __half* enc_scratch = nullptr;
     int enc_plane = 0;
+    bool enc_ready = false;  // enc_scratch already holds these positions' encodings: no encode launch
     // Nullable: a buffer of nerf_heads_packed_bytes().  With it, the planar
     // encodings and the head shapes nerf_heads_supported() accepts, and no
     // activations asked for (dacts, cacts null), the heads run as the

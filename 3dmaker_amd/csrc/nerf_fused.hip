@@ -240,7 +240,7 @@ void nerf_forward(const NerfFwdArgs& a, int N, hipStream_t stream, const uint32_
     const bool planar = a.enc_scratch != nullptr;
     if (planar) {
         if (a.enc_plane < N) throw std::runtime_error("NeRF forward: encoding plane stride below the sample count");
-        hash_encode_planar(m, a.table, a.pos, a.pos_stride, a.enc_scratch, a.enc_plane, N, stream, d_n);
+        if (!a.enc_ready) hash_encode_planar(m, a.table, a.pos, a.pos_stride, a.enc_scratch, a.enc_plane, N, stream, d_n);
     }
     if (planar && a.heads_packed != nullptr && a.dacts == nullptr && a.cacts == nullptr &&
         nerf_heads_supported(a.dshape, a.cshape)) {

@@ -748,9 +748,11 @@ def main():
     # the stream each stage runs on)
     candidates = {
         "hashScatter": ("hbm", SCATTER_BYTES_PER_SAMPLE * n_prof),  # count, prefix, distribute, accumulate
-        "forward": ("hbm", ENC_BYTES_PER_SAMPLE * n_prof),  # encode + both heads' forward
+        "encode": ("hbm", ENC_BYTES_PER_SAMPLE * n_prof),  # the step's hash encode (16x16x32 heads)
         "densityOpt": ("hbm", ADAM_BYTES_PER_PARAM * (L * TBL * F)),
     }
+    if "encode" not in st:  # other head shapes: encode and heads in one stage
+        candidates["forward"] = ("hbm", ENC_BYTES_PER_SAMPLE * n_prof)
     dom = max((k for k in candidates if k in st), key=lambda k: st[k][0])
     bound, algo = candidates[dom]
     dom_ms = st[dom][0]
@@ -758,7 +760,8 @@ def main():
     roofline = {"bound": bound, "kernel": dom, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom),
                 "algorithmic_bytes_per_launch": int(algo), "avg_launch_ms": round(dom_ms, 4)}
-    # MLP stages: the fused forward, the dX chains (main stream) and the weight gradients (side stream)
+    # MLP stages: the heads' forward (the encode is a stage of its own with the 16x16x32 heads), the dX
+    # chains (main stream) and the weight gradients (side stream, beside the scatter)
     mlp_ms = sum(st[k][0] for k in ("forward", "backwardDx", "colorDx", "densityDx", "colorBwd", "densityBwd",
                                     "headsBwd") if k in st)
     mfma_util = MLP_FLOP_PER_SAMPLE * n_prof / (mlp_ms * 1e-3) / 1e12 / FP16_PEAK_TFLOPS if mlp_ms else None
@@ -785,7 +788,8 @@ def main():
                    "feed": "100 RGBA8 800x800 views in HBM, pcg_hash draws, random background per call"},
         "stage_ms": stage_ms,
         "stage_ms_per_step": stage_ms_per_step,
-        "forward_samples_per_s": round(n_prof / (st["forward"][0] * 1e-3), 1) if "forward" in st else None,
+        "forward_samples_per_s": round(n_prof / ((st["forward"][0] + st.get("encode", (0.0,))[0]) * 1e-3), 1)
+        if "forward" in st else None,
         "mfma_util": round(mfma_util, 5) if mfma_util else None,
         "roofline": roofline,
     }
