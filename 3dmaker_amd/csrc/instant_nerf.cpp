@@ -120,6 +120,10 @@ struct NerfBuffers {
     uint32_t* list_scratch = nullptr;
     int occ_capacity = 0;
     int occ_last_count = 0;   // samples of the last refresh's last chunk
+    // a late refresh's samples drawn a step ahead (one cascade): the step
+    // count and grid version they were drawn for (-1: none)
+    long drawn_steps = -1;
+    long drawn_version = -1;
     // inference render / queries (allocated on first use, sized to the hit batch)
     struct Render {
         uint32_t cap = 0;
@@ -631,6 +635,13 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
             fa.enc_ready = b.heads_packed != nullptr;
             graft::nerf_forward(fa, (int)Bn, stream, d_hits);
         });
+        // The next step's late refresh (one cascade): its samples are drawn
+        // beside the rest of this step, from the step after the forward.
+        if (!refresh && m_opts.numCascades == 1 && (m_trainSteps + 1) % 16 == 0 && m_trainSteps + 1 >= 256) {
+            GRAFT_HIP_CHECK(hipEventRecord(b.ev_occ_fork, stream));
+            GRAFT_HIP_CHECK(hipStreamWaitEvent(b.occ, b.ev_occ_fork, 0));
+            stage_on(b.occ, "occupancyDraw", [&] { drawLateRefresh((long)m_trainSteps + 1, b.occ); });
+        }
 
         float* final_rgb = d_rgb_out ? d_rgb_out + (size_t)raysDone * 3 : b.render_rgb;
         stage("renderGrad", [&] {
@@ -926,22 +937,17 @@ namespace {
 // (stride refresh_density_stride; in b.occ_perm's order when sorted).  The encode runs as its own launch (each
 // XCD's L2 holding only its levels' tables; the samples are spread over the
 // whole grid, so an encode fused with the head would cycle all 32 MiB of table
-// through every L2).  With the 16x16x32 heads: the samples are first put in a
-// spatial order when spread at random (spatial_sort), so that a wave's
-// gathers share table lines, then the density head runs on the level-major
-// encodings with the maximum fused in (b.occ_packed holds the density
-// head's fragments, packed at the refresh's start); otherwise the TinyMLP
-// density forward, then the maximum.
+// through every L2).  With the 16x16x32 heads: samples spread at random are
+// evaluated in the spatial order late_refresh_draw put them in (sorted: in
+// b.occ_sorted), so that a wave's gathers share table lines; the density
+// head runs on the level-major encodings with the maximum fused in
+// (b.occ_packed holds the density head's fragments, packed at the refresh's
+// start); otherwise the TinyMLP density forward, then the maximum.
 void occupancy_density_max(NerfBuffers& b, const TinyMLPHashGrid::Buffers& db, const graft::MlpShape& dshape, int n,
-                           bool spatial_sort, bool one_per_cell, const NerfOptions& o, hipStream_t stream)
+                           bool sorted, bool one_per_cell, const NerfOptions& o, hipStream_t stream)
 {
     if (b.occ_packed) {
-        const float4* src = b.occ_samples;
-        if (spatial_sort) {
-            graft::occ_sort_samples(b.occ_samples, n, o.numCascades, o.gridResolution, b.occ_sort, b.occ_sorted,
-                                    b.occ_perm, stream);
-            src = b.occ_sorted;
-        }
+        const float4* src = sorted ? b.occ_sorted : b.occ_samples;
         graft::hash_encode_planar(b.meta, db.fwd_hashtable, reinterpret_cast<const float*>(src), 4, b.occ_enc, n, n,
                                   stream);
         graft::NerfDensityMax a;
@@ -955,7 +961,7 @@ void occupancy_density_max(NerfBuffers& b, const TinyMLPHashGrid::Buffers& db, c
         a.tmp = b.tmp_grid;
         a.one_per_cell = one_per_cell;
         graft::nerf_density_max(a, n, stream);
-        b.occ_last_sorted = spatial_sort;
+        b.occ_last_sorted = sorted;
         return;
     }
     b.occ_last_sorted = false;
@@ -975,7 +981,40 @@ void pack_refresh(NerfBuffers& b, const TinyMLPHashGrid::Buffers& db, hipStream_
     if (b.occ_packed)
         graft::nerf_heads_pack_density(graft::NerfHeadsWeights{db.fwd_weights, db.master_biases, nullptr, nullptr},
                                        b.occ_packed, stream);
-}}  // namespace
+}
+
+// Samples of a late refresh's chunk ch (InstantNerf.cu:1009-1106): half from
+// the occupied-cell list in b.active_list, half uniform over all cells,
+// seeded by the refresh's step count; with the 16x16x32 heads also put in a
+// spatial order (b.occ_sorted, b.occ_perm).  They depend on the grid and the
+// step count only, not on any parameter.
+void late_refresh_draw(NerfBuffers& b, const NerfOptions& o, long steps, int ch, hipStream_t stream)
+{
+    const int N = o.numCascades * grid_cells(o);
+    const int chunks = o.numCascades;
+    const int perChunk = (N / 2) / chunks;
+    const int occPer = perChunk / 2;
+    const int uniPer = perChunk - occPer;
+    const uint64_t seed = (uint64_t)steps * (2ULL * chunks) + 2ULL * ch;
+    graft::occ_sample(b.occ_samples, occPer, graft::kSampleFromList, 0, 0, b.active_list, b.active_count, seed,
+                      o.gridResolution, o.aabbMin, o.aabbMax, stream);
+    graft::occ_sample(b.occ_samples + occPer, uniPer, graft::kSampleRandomCell, N, 0, nullptr, nullptr, seed + 1,
+                      o.gridResolution, o.aabbMin, o.aabbMax, stream);
+    if (b.occ_packed)
+        graft::occ_sort_samples(b.occ_samples, perChunk, o.numCascades, o.gridResolution, b.occ_sort, b.occ_sorted,
+                                b.occ_perm, stream);
+}
+
+// the occupied-cell list of the grid (its pass over every cell also clears
+// the tmp grid)
+void late_refresh_list(NerfBuffers& b, const NerfOptions& o, const uint8_t* grid, hipStream_t stream)
+{
+    const int G = grid_cells(o);
+    const int S = (int)graft::mip_offset(o.gridResolution, o.levelsMipmap);
+    graft::occ_active_list(grid, o.numCascades * G, G, S, b.active_list, b.active_count, b.list_scratch, stream,
+                           b.tmp_grid);
+}
+}  // namespace
 
 // InstantNerf.cu:1108-1171: one jittered sample per cell of every cascade.
 void InstantNerf::earlyOccupancyGridUpdate(hipStream_t stream)
@@ -994,7 +1033,7 @@ void InstantNerf::earlyOccupancyGridUpdate(hipStream_t stream)
                           (uint64_t)m_trainSteps + (uint64_t)c, m_opts.gridResolution, m_opts.aabbMin, m_opts.aabbMax,
                           stream);
         // every cell in cell order: already spatial
-        occupancy_density_max(b, db, dshape, G, false, true, m_opts, stream);
+        occupancy_density_max(b, db, dshape, G, /*sorted=*/false, true, m_opts, stream);
     }
     b.occ_last_count = G;
     finishOccupancyUpdate(stream);
@@ -1005,30 +1044,39 @@ void InstantNerf::earlyOccupancyGridUpdate(hipStream_t stream)
 void InstantNerf::lateOccupancyGridUpdate(hipStream_t stream)
 {
     NerfBuffers& b = B(m_buf);
-    const int G = grid_cells(m_opts);
-    const int N = m_opts.numCascades * G;
-    const int S = (int)graft::mip_offset(m_opts.gridResolution, m_opts.levelsMipmap);
+    const int N = m_opts.numCascades * grid_cells(m_opts);
     const TinyMLPHashGrid::Buffers db = m_densityMLP->buffers();
     const graft::MlpShape dshape{2 * m_opts.numLevels, db.hw.hiddenDim, db.hw.outputDim, db.hw.numLayers};
     pack_refresh(b, db, stream);
-    // the list's pass over every cell also clears the tmp grid
-    graft::occ_active_list(d_occupancyGrid, N, G, S, b.active_list, b.active_count, b.list_scratch, stream,
-                           b.tmp_grid);
+    // the samples of a one-chunk refresh may have been drawn a step ahead
+    // (drawLateRefresh) for this step count on this grid
+    const bool drawn = b.drawn_steps == (long)m_trainSteps && b.drawn_version == m_gridVersion;
+    b.drawn_steps = b.drawn_version = -1;
+    if (!drawn) late_refresh_list(b, m_opts, d_occupancyGrid, stream);
     const int chunks = m_opts.numCascades;
     const int perChunk = (N / 2) / chunks;
-    const int occPer = perChunk / 2;
-    const int uniPer = perChunk - occPer;
     for (int ch = 0; ch < chunks; ++ch) {
-        const uint64_t seed = (uint64_t)m_trainSteps * (2ULL * chunks) + 2ULL * ch;
-        graft::occ_sample(b.occ_samples, occPer, graft::kSampleFromList, 0, 0, b.active_list, b.active_count, seed,
-                          m_opts.gridResolution, m_opts.aabbMin, m_opts.aabbMax, stream);
-        graft::occ_sample(b.occ_samples + occPer, uniPer, graft::kSampleRandomCell, N, 0, nullptr, nullptr, seed + 1,
-                          m_opts.gridResolution, m_opts.aabbMin, m_opts.aabbMax, stream);
-        const int cnt = occPer + uniPer;
-        occupancy_density_max(b, db, dshape, cnt, true, false, m_opts, stream);
-        b.occ_last_count = cnt;
+        if (!drawn) late_refresh_draw(b, m_opts, (long)m_trainSteps, ch, stream);
+        occupancy_density_max(b, db, dshape, perChunk, /*sorted=*/b.occ_packed != nullptr, false, m_opts, stream);
+        b.occ_last_count = perChunk;
     }
     finishOccupancyUpdate(stream);
+}
+
+// The sample draw of the late refresh at step count `steps`, a step ahead of
+// it: the occupied-cell list, the samples and their spatial sort read only
+// the grid and the step count, so with one cascade (one chunk, whose samples
+// the refresh's density head then evaluates) they run beside the step before
+// the refresh instead of on the refresh's own path.  The refresh uses them
+// only if the grid has not changed since (m_gridVersion).
+void InstantNerf::drawLateRefresh(long steps, hipStream_t stream)
+{
+    NerfBuffers& b = B(m_buf);
+    if (m_opts.numCascades != 1 || steps < 256 || steps % 16 != 0) return;
+    late_refresh_list(b, m_opts, d_occupancyGrid, stream);
+    late_refresh_draw(b, m_opts, steps, 0, stream);
+    b.drawn_steps = steps;
+    b.drawn_version = m_gridVersion;
 }
 
 // EMA-max into the master grid, mean, level-0 bits, mip pyramid (InstantNerf.cu:1150-1171).

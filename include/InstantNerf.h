@@ -208,6 +208,7 @@ private:
     void freeBuffers();
     void earlyOccupancyGridUpdate(hipStream_t stream);
     void lateOccupancyGridUpdate(hipStream_t stream);
+    void drawLateRefresh(long steps, hipStream_t stream);
     void finishOccupancyUpdate(hipStream_t stream);
     uint32_t renderHitBatch() const;
 

@@ -753,28 +753,46 @@ def _refresh_oracle_chunks(nerf, opts, steps, bits, G, S, Cc, res, table, dW, dB
     return chunks
 
 
-@pytest.mark.parametrize("late", [False, True])
-def test_occupancy_refresh_matches_oracle(dev, late):
+@pytest.mark.parametrize("mode", ["early", "late", "late_drawn"])
+def test_occupancy_refresh_matches_oracle(dev, mode):
     """updateOccupancy: sample positions and cells bit-exact on this build's Philox draws, density within the
-    MLP tolerance, tmp grid bit-exact on the GPU's own densities, EMA master grid bit-exact, bits."""
+    MLP tolerance, tmp grid bit-exact on the GPU's own densities, EMA master grid bit-exact, bits.
+    late_drawn: one cascade, the refresh at step 272 with the samples its previous training step drew
+    beside itself (the occupied-cell list, the draw and its spatial sort, a step ahead)."""
     P = pkg()
     opts = small_options(P, batch=1 << 14)
+    late, drawn = mode != "early", mode == "late_drawn"
+    if drawn:
+        opts.numCascades = 1
     nerf = P.Nerf(opts)
-    res, Cc, L = 32, 2, 4
+    res, Cc, L = 32, int(opts.numCascades), 4
     G, S = res ** 3, orc.pyramid_cells([res] * 3, L)
     if late:   # 256 one-step calls: the next refresh samples occupied cells (InstantNerf.cu:1009-1106)
         rng = np.random.default_rng(21)
         o, d = scenes.rays_c4(1000, n_cams=20, seed=22)
         d_o, d_d = T(o, dev), T(d, dev)
         d_gt = T(rng.random((1000, 3)).astype(np.float32), dev)
+        target = 270 if drawn else 256
         done = 0
-        while done < 256:
+        while done < target:
+            nerf.set_step_limit(target - done)
             n, _ = nerf.train(d_o, d_d, d_gt, 1000)
             done += n
         torch.cuda.synchronize()
         # a sparse grid, so that the occupied-cell list is a proper subset
         lv = [rng.random((res,) * 3) < (0.2 if c == 0 else 0.05) for c in range(Cc)]
         nerf.set_occupancy(scenes.pack_grid(lv, L))
+        if drawn:   # steps 270 and 271 on that grid (one step a call); 271 draws the refresh's samples
+            for k in range(2):
+                nerf.set_step_limit(1)
+                nerf.set_profiling(k == 1)
+                nerf.reset_stats()
+                n, _ = nerf.train(d_o, d_d, d_gt, 1000)
+                torch.cuda.synchronize()
+                assert n == 1
+            assert nerf.stats()["occupancyDraw"][1] == 1, nerf.stats()
+            nerf.set_profiling(False)
+        nerf.set_step_limit(0)
     steps = nerf.step_buffers().trainSteps
     print(f"[refresh] late={late} trainSteps={steps}", flush=True)
     assert (steps >= 256) == late
@@ -800,6 +818,8 @@ def test_occupancy_refresh_matches_oracle(dev, late):
         unsorted[order] = g_den
         g_den = unsorted
     assert bool(rb.density_order) == (late and rb.density_stride == 1)
+    if drawn:
+        assert steps == 272
     g_tmp = d2h(rb.tmp_grid, (Cc * G,), np.float32)
     if late:   # the occupied-cell list, in cell order
         want_list = orc.active_cells(bits, G, S, Cc)
