@@ -253,19 +253,26 @@ __global__ __launch_bounds__(kBinThreads) void scatter_count_kernel(const Scatte
 constexpr int kPrefixWaves = 16;
 constexpr int kPrefixThreads = 64 * kPrefixWaves;
 constexpr int kPrefixUnroll = 8;
+constexpr int kPrefixBins = 32;  // bins per workgroup (a divisor of 64; 16 and 8 measured slower)
 
 __global__ __launch_bounds__(kPrefixThreads) void scatter_prefix_kernel(const ScatterArgs a, uint32_t* __restrict__ counts,
                                                               uint32_t* __restrict__ totals,
                                                               const uint32_t* __restrict__ lvlmax,
                                                               uint32_t* __restrict__ lvlmax_out)
 {
-    __shared__ uint32_t part[kPrefixWaves][64];
+    // kPrefixBins bins per workgroup, the rounds cut into kRanges ranges (one
+    // per group of kPrefixBins lanes): short dependent load chains per thread
+    constexpr int kSplit = 64 / kPrefixBins;
+    constexpr int kRanges = kSplit * kPrefixWaves;
+    __shared__ uint32_t part[kRanges][kPrefixBins];
     __shared__ uint32_t wmax[kPrefixWaves];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int b = blockIdx.x * 64 + lane;
+    const int q = kSplit * w + lane / kPrefixBins;  // this lane group's range of rounds
+    const int bl = lane % kPrefixBins;
+    const int b = blockIdx.x * kPrefixBins + bl;
     const int R = a.rounds;
-    const int per = (R + kPrefixWaves - 1) / kPrefixWaves;
-    const int r0 = min(R, w * per), r1 = min(R, r0 + per);
+    const int per = (R + kRanges - 1) / kRanges;
+    const int r0 = min(R, q * per), r1 = min(R, r0 + per);
     const bool vb = b < a.bins;
     uint32_t s = 0;
     if (vb) {
@@ -279,7 +286,7 @@ __global__ __launch_bounds__(kPrefixThreads) void scatter_prefix_kernel(const Sc
         }
         for (; r < r1; r++) s += counts[(size_t)r * a.bins + b];
     }
-    part[w][lane] = s;
+    part[q][bl] = s;
     if ((int)blockIdx.x < a.L) {
         uint32_t m = 0;
         for (int r = threadIdx.x; r < R; r += kPrefixThreads) m = max(m, lvlmax[(size_t)r * a.L + blockIdx.x]);
@@ -293,7 +300,7 @@ __global__ __launch_bounds__(kPrefixThreads) void scatter_prefix_kernel(const Sc
         lvlmax_out[blockIdx.x] = m;
     }
     uint32_t run = 0;
-    for (int k = 0; k < w; k++) run += part[k][lane];
+    for (int k = 0; k < q; k++) run += part[k][bl];
     if (vb) {
         int r = r0;
         for (; r + kPrefixUnroll <= r1; r += kPrefixUnroll) {
@@ -312,7 +319,7 @@ __global__ __launch_bounds__(kPrefixThreads) void scatter_prefix_kernel(const Sc
             counts[i] = run;
             run += c;
         }
-        if (w == kPrefixWaves - 1) totals[b] = run;
+        if (q == kRanges - 1) totals[b] = run;
     }
 }
 
@@ -960,7 +967,7 @@ void scatter_launch(ScatterPlan* p, const GridMeta& m, const __half* denc, const
     hipLaunchKernelGGL(scatter_count_kernel, dim3(a.rounds), dim3(kBinThreads), lds_count, stream, a, pos, dh,
                        p->counts, p->lvlmax);
     GRAFT_LAUNCH_CHECK();
-    const int prefix_blocks = std::max((a.bins + 63) / 64, a.L);
+    const int prefix_blocks = std::max((a.bins + kPrefixBins - 1) / kPrefixBins, a.L);
     hipLaunchKernelGGL(scatter_prefix_kernel, dim3(prefix_blocks), dim3(kPrefixThreads), 0, stream, a, p->counts, p->totals,
                        p->lvlmax, p->lvlmax_final);
     GRAFT_LAUNCH_CHECK();
