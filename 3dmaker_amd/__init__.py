@@ -510,10 +510,15 @@ class Nerf:
               max_steps=4096):
         """trainWithRaysHit; returns (steps taken, [compacted samples per step])."""
         cnt = C.c_int(0)
-        hits = (_u32 * max(int(max_steps), int(num_rays), 1))()  # one step consumes >= 1 ray
+        # one step consumes >= 1 ray: room for num_rays counts; the buffer is
+        # kept and grown, not allocated and zeroed on every call
+        need = max(int(max_steps), int(num_rays), 1)
+        if getattr(self, "_hits", None) is None or len(self._hits) < need:
+            self._hits = (_u32 * need)()
+        hits = self._hits
         self._c(self._L.inerf_train(self.h, ptr(rays_o), ptr(rays_d), ptr(rays_depth), ptr(rays_sigma),
                                     ptr(rgb_true), int(num_rays), C.byref(cnt), hits, ptr(rgb_out), stream))
-        return cnt.value, list(hits[:cnt.value])
+        return cnt.value, hits[:cnt.value]
 
     def set_learning_rate(self, lr):
         self._c(self._L.inerf_set_learning_rate(self.h, float(lr)))

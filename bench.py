@@ -284,8 +284,10 @@ class Trainer:
             self.nerf.set_bg_color(*map(float, bg))
             self.nerf.set_step_limit(nsteps - len(hits))
             b = f.slots[slot]
-            n, h = self.nerf.train(b["o"][done:], b["d"][done:], b["rgb"][done:], size - done,
-                                   rays_depth=b["dense"][done:], rays_sigma=b["sigma"][done:], stream=self.stream)
+            # the chunk's buffers from its first untrained ray, as device addresses (no tensor views per call)
+            at = lambda t, per: t.data_ptr() + done * per * t.element_size()  # noqa: E731
+            n, h = self.nerf.train(at(b["o"], 3), at(b["d"], 3), at(b["rgb"], 3), size - done,
+                                   rays_depth=at(b["dense"], 1), rays_sigma=at(b["sigma"], 1), stream=self.stream)
             self.calls += 1
             self.step += n
             hits.extend(h)
