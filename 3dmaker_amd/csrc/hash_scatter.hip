@@ -252,7 +252,7 @@ __global__ __launch_bounds__(kBinThreads) void scatter_count_kernel(const Scatte
 // Block x < L also reduces level x's per-round maxima.
 constexpr int kPrefixWaves = 16;
 constexpr int kPrefixThreads = 64 * kPrefixWaves;
-constexpr int kPrefixUnroll = 8;
+constexpr int kPrefixUnroll = 4;  // loads in flight per thread (2, 3, 8 and 16 measured slower)
 constexpr int kPrefixBins = 32;  // bins per workgroup (a divisor of 64; 16 and 8 measured slower)
 
 __global__ __launch_bounds__(kPrefixThreads) void scatter_prefix_kernel(const ScatterArgs a, uint32_t* __restrict__ counts,
