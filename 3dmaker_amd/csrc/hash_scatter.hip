@@ -583,7 +583,7 @@ __global__ __launch_bounds__(kAccThreads) __attribute__((amdgpu_waves_per_eu(4))
         // values of a run of equal keys in registers (exact: integer sums in
         // any order), with one LDS add per run it holds.
         constexpr int kRun = 4;
-        constexpr int kGroups = 4;  // runs per lane in flight
+        constexpr int kGroups = 2;  // runs per lane in flight (4 and 6 measured slower)
         const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
         constexpr int kWaveSpan = 64 * kRun;
         for (uint32_t b0 = ch.y + (uint32_t)wv * kWaveSpan; b0 < ch.z;
