@@ -14,9 +14,12 @@
 //  prefix      per bin: exclusive prefix of the counts over the rounds, and
 //              the bin's total;
 //  distribute  per round: every corner pair becomes one 16-byte record
-//              {x0 slot | x1 slot << 16, g0 * wyz, g1 * wyz, wx} written at its
-//              bin's cursor (bin base + round prefix + LDS rank); workgroup 0
-//              also writes the chunk table (<= kChunk records per chunk);
+//              {x0 slot | x1 slot << 16, (g0, g1) as fp16, w of the x0 corner,
+//              w of the x1 corner} written at its bin's cursor (bin base +
+//              round prefix + LDS rank); workgroup 0 also writes the chunk
+//              table (<= kChunk records per chunk).  The weights are the
+//              reference's products (wx * wy) * wz, so every product g * w is
+//              the reference's fp32 product bit for bit;
 //  accumulate  per chunk: the slice's sums in LDS as int64 fixed point
 //              (ds_add_u64), then one store per table entry.  A bin of several
 //              chunks adds its partial sums into an int64 staging slice with
@@ -41,6 +44,22 @@
 // the record order, chunking or scheduling (deterministic).  Non-finite
 // products take an fp32 atomic instead, so NaN/Inf reach the entry as they do
 // through the reference's atomics.
+//
+// Refinement: the level's quantum 2^-e is absolute, so a gradient whose sum
+// is tiny against the level's largest gradient keeps few significant bits, and
+// one whose products are each below half a quantum, or cancel at that
+// resolution, sums to 0 (and the fused update would skip it, where the
+// reference's fp32 sum is nonzero and Adam moves the entry).  In a training
+// step about a sixth of the touched gradients are such.  A gradient that took
+// a product below 2^24 quanta and whose sum is below 2^24 quanta is summed
+// again from the bin's records, 2^s times finer (s = min(26, 38 - lg): every
+// such product stays below 2^50 units and a sum of 2^lg of them below 2^62).
+// Rare cases take further passes: a gradient that also took a product of
+// 2^24 quanta or more (products cancelling) is summed at e again; one whose
+// finer sum is still below 2^24 units is summed at the scale its largest
+// |product| sets, the way the level maximum sets e.  Every other sum is at
+// least 2^24 units of its scale (each product within 2^-25 of the sum) or made
+// of products of at least 2^24 quanta (each within 2^-25 of the smallest).
 #include "scatter.h"
 
 #include "adam_math.h"
@@ -62,9 +81,12 @@ constexpr int kBinThreads = 512;
 constexpr int kSamplesPerThread = 1;
 constexpr int kRound = kBinThreads * kSamplesPerThread;
 constexpr uint32_t kChunk = 32768;  // records per accumulate workgroup
-constexpr int kAccThreads = 512;
 constexpr int kMaxBins = 8192;
 constexpr int kDenseBins = 64;  // target bins per dense level
+// word offset of a dense slice's finer sums (a dense slice holds at most
+// kSlice / 2 entries, so its 2 * entries words and their finer twins share
+// the LDS slice)
+constexpr int kFine = kSlice;
 
 struct ScatterArgs {
     const uint32_t* d_n;  // nullable device-side sample count (<= N)
@@ -85,8 +107,8 @@ struct ScatterArgs {
 struct Pairs {
     int bin[4];
     uint32_t key[4];  // slot of x0 within the slice | slot of x1 << 16
-    float wyz[4];
-    float wx;         // weight of the x0 corner
+    float w0[4];      // weight of the x0 corner, (wx * wy) * wz
+    float w1[4];      // weight of the x1 corner, ((1 - wx) * wy) * wz
 };
 
 __device__ __forceinline__ void level_pairs(const ScatterArgs& a, int l, float px, float py, float pz, Pairs& p)
@@ -103,12 +125,14 @@ __device__ __forceinline__ void level_pairs(const ScatterArgs& a, int l, float p
     const float wx1 = (1.0f - x_l) + fx;
     const float wy1 = (1.0f - y_l) + fy;
     const float wz1 = (1.0f - z_l) + fz;
-    const float uy = 1.0f - wy1, uz = 1.0f - wz1;
-    p.wx = wx1;
-    p.wyz[0] = wy1 * wz1;
-    p.wyz[1] = uy * wz1;
-    p.wyz[2] = wy1 * uz;
-    p.wyz[3] = uy * uz;
+    const float ux = 1.0f - wx1, uy = 1.0f - wy1, uz = 1.0f - wz1;
+    // networkFusionBackwardHashtable.cu:836-839: w = (x-factor * y-factor) * z-factor
+    const float ys[2] = {wy1, uy}, zs[2] = {wz1, uz};
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        p.w0[q] = (wx1 * ys[q & 1]) * zs[q >> 1];
+        p.w1[q] = (ux * ys[q & 1]) * zs[q >> 1];
+    }
     const int base = a.bin_base[l];
     if (l < a.dense_start) {
         const int st = N_l + 1;
@@ -410,8 +434,6 @@ __global__ __launch_bounds__(kBinThreads) void scatter_distribute_kernel(
                 if (l >= a.L) break;
                 const uint32_t gb = gv[j];
                 if ((gb & 0x7fff7fffu) == 0u) continue;
-                const h2 gh = __builtin_bit_cast(h2, gb);
-                const float g0 = (float)gh.x, g1 = (float)gh.y;
                 Pairs p;
                 level_pairs(a, l, px, py, pz, p);
                 const bool dense = l < a.dense_start;
@@ -419,7 +441,7 @@ __global__ __launch_bounds__(kBinThreads) void scatter_distribute_kernel(
                 for (int q = 0; q < 4; q++) {
                     const uint32_t at = dense ? bin_take(cur, p.bin[q]) : atomicAdd(&cur[p.bin[q]], 1u);
                     if (at < cap)
-                        rec[at] = make_float4(__uint_as_float(p.key[q]), g0 * p.wyz[q], g1 * p.wyz[q], p.wx);
+                        rec[at] = make_float4(__uint_as_float(p.key[q]), __uint_as_float(gb), p.w0[q], p.w1[q]);
                 }
             }
         }
@@ -465,6 +487,75 @@ __device__ __forceinline__ void add_or_mark(unsigned long long* acc, uint32_t* n
 
 __device__ __forceinline__ bool finite_bits(float x) { return (__float_as_uint(x) & 0x7f800000u) != 0x7f800000u; }
 
+// 0 < |c| < 2^(24 - e): a nonzero product of fewer than 2^24 quanta; thr_bits
+// is the fp32 pattern of 2^(24 - e) (the unsigned wrap excludes |c| == 0, and
+// non-finite patterns lie above every threshold).
+__device__ __forceinline__ bool small_product(float c, uint32_t thr_bits)
+{
+    return (__float_as_uint(c) & 0x7fffffffu) - 1u < thr_bits - 1u;
+}
+
+__device__ __forceinline__ void set_bit(uint32_t* w, int i) { atomicOr(&w[i >> 5], 1u << (i & 31)); }
+__device__ __forceinline__ void clear_bit(uint32_t* w, int i) { atomicAnd(&w[i >> 5], ~(1u << (i & 31))); }
+__device__ __forceinline__ bool get_bit(const uint32_t* w, int i) { return (w[i >> 5] >> (i & 31)) & 1u; }
+// the same while other threads may clear other bits of the word
+__device__ __forceinline__ bool get_bit_shared(uint32_t* w, int i)
+{
+    return (__hip_atomic_load(&w[i >> 5], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >> (i & 31)) & 1u;
+}
+
+// Sums below this many quanta carry fewer significant bits than fp32 and are
+// summed again at the entry's own scale.
+constexpr long long kFewBits = 1LL << 24;
+
+// The four products of a corner-pair record and the gradient words they add
+// to: g_f * w of the x0 corner, then of the x1 corner (the reference's
+// valX / valY = grads * weight, networkFusionBackwardHashtable.cu:864-865).
+struct RecProducts {
+    float c[4];
+    int at[4];
+};
+
+__device__ __forceinline__ RecProducts rec_products(const float4& r)
+{
+    const uint32_t key = __float_as_uint(r.x);
+    const int s0 = (int)(key & 0xffffu), s1 = (int)(key >> 16);
+    const h2 gh = __builtin_bit_cast(h2, __float_as_uint(r.y));
+    const float g0 = (float)gh.x, g1 = (float)gh.y, w0 = r.z, w1 = r.w;
+    return RecProducts{{g0 * w0, g1 * w0, g0 * w1, g1 * w1}, {2 * s0, 2 * s0 + 1, 2 * s1, 2 * s1 + 1}};
+}
+
+// Every product of the record is finite: both fp16 gradients and both weights
+// are (|g| <= 65504, weights in [0, 1]).
+__device__ __forceinline__ bool rec_finite(const float4& r)
+{
+    const uint32_t gb = __float_as_uint(r.y);
+    return ((gb & 0x7c00u) != 0x7c00u) & ((gb & 0x7c000000u) != 0x7c000000u) & finite_bits(r.z) & finite_bits(r.w);
+}
+
+constexpr int kAccThreads = 512;
+
+// f(products) over records [r0, r1) step kAccThreads, kRescan loads in flight
+// per thread (a dependent load per record would wait out the memory latency
+// each time).
+constexpr int kRescan = 8;
+
+template <class F>
+__device__ __forceinline__ void for_each_record(const float4* __restrict__ rec, uint32_t r0, uint32_t r1, F&& f)
+{
+    for (uint32_t i0 = r0 + threadIdx.x; i0 < r1; i0 += kRescan * kAccThreads) {
+        float4 r[kRescan];
+#pragma unroll
+        for (int k = 0; k < kRescan; k++) {
+            const uint32_t i = i0 + k * kAccThreads;
+            r[k] = i < r1 ? rec[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int k = 0; k < kRescan; k++)
+            if (i0 + k * kAccThreads < r1) f(rec_products(r[k]));
+    }
+}
+
 
 // Parameters of the fused table update (ADAM): the table [L][T][2] (fp32
 // master, fp16 copy) and its moments.
@@ -479,15 +570,16 @@ struct TableAdamArgs {
 constexpr int kNfWords = 2 * kSlice / 32;  // non-finite bits of one slice
 
 // Adam on entries [s0, s0 + kAdamBatch * kAccThreads) step kAccThreads of one
-// slice (entry elem = base + s): gradient f of entry s is ldexpf(q[2 s + f],
-// -e), or non-finite where its bit is set; entries with neither a nonzero
-// sum nor the bit keep every word (the stored path's zero gradients, which
-// Adam skips).  Only touched features' words are stored.
+// slice (entry elem = base + s): gradient f of entry s is grad_of(2 s + f)
+// (which also says whether its sum is nonzero), or non-finite where its bit
+// is set; entries with neither a nonzero sum nor the bit keep every word (the
+// stored path's zero gradients, which Adam skips).  Only touched features'
+// words are stored.
 constexpr int kAdamBatch = 8;  // entries per thread in flight in the update pass (4 measured slower)
 
-template <class Q>
-__device__ __forceinline__ void table_adam_batch(const TableAdamArgs& t, size_t base, int s0, int slots, Q&& q,
-                                                 const uint32_t* nfw, int e)
+template <class G>
+__device__ __forceinline__ void table_adam_batch(const TableAdamArgs& t, size_t base, int s0, int slots,
+                                                 G&& grad_of, const uint32_t* nfw)
 {
     constexpr int kBatch = kAdamBatch;
     bool t0[kBatch], t1[kBatch];
@@ -499,13 +591,14 @@ __device__ __forceinline__ void table_adam_batch(const TableAdamArgs& t, size_t 
         t0[k] = t1[k] = false;
         g0[k] = g1[k] = 0.f;
         if (s < slots) {
-            const long long q0 = q(2 * s), q1 = q(2 * s + 1);
+            float a0, a1;
+            const bool z0 = grad_of(2 * s, a0), z1 = grad_of(2 * s + 1, a1);
             const uint32_t bits = nfw[(2 * s) >> 5] >> ((2 * s) & 31);  // 2 s even: both bits in one word
             const bool n0 = bits & 1u, n1 = (bits >> 1) & 1u;
-            t0[k] = (q0 != 0) | n0;
-            t1[k] = (q1 != 0) | n1;
-            g0[k] = n0 ? __builtin_nanf("") : ldexpf((float)q0, -e);
-            g1[k] = n1 ? __builtin_nanf("") : ldexpf((float)q1, -e);
+            t0[k] = z0 | n0;
+            t1[k] = z1 | n1;
+            g0[k] = n0 ? __builtin_nanf("") : a0;
+            g1[k] = n1 ? __builtin_nanf("") : a1;
         }
         if (t0[k] | t1[k]) {
             const size_t i = base + (size_t)s;
@@ -538,10 +631,14 @@ __global__ __launch_bounds__(kAccThreads) __attribute__((amdgpu_waves_per_eu(4))
     const ScatterArgs a, const float4* __restrict__ rec, const uint4* __restrict__ chunks,
     const uint32_t* __restrict__ nchunks, const uint32_t* __restrict__ totals, const uint32_t* __restrict__ lvlmax,
     float* __restrict__ grads, unsigned long long* __restrict__ part, uint32_t* __restrict__ done, int grads_zero,
-    uint32_t* __restrict__ part_nf, const TableAdamArgs ta)
+    uint32_t* __restrict__ part_nf, uint32_t* __restrict__ part_sus, const TableAdamArgs ta)
 {
     __shared__ unsigned long long acc[2 * kSlice];
     __shared__ uint32_t nf[ADAM ? kNfWords : 1];
+    __shared__ uint32_t sus[kNfWords];        // gradients summed again at a finer scale
+    __shared__ uint32_t aux[kNfWords];        // gradients with products cancelling
+    __shared__ uint32_t tny[kNfWords];        // gradients still below 2^24 units
+    __shared__ uint8_t ex_off[2 * kSlice];    // the refined gradients' exponent above e
     __shared__ int s_flag, s_last;
     if (blockIdx.x >= *nchunks) return;
     const uint4 ch = chunks[blockIdx.x];
@@ -566,13 +663,32 @@ __global__ __launch_bounds__(kAccThreads) __attribute__((amdgpu_waves_per_eu(4))
     const uint32_t tot = totals[bin];
     const int lg = tot <= 1u ? 0 : 32 - __clz(tot - 1u);
     const int e = min(49, 60 - lg) - E;
+    const uint32_t thr = (uint32_t)(127 + 24 - e) << 23;  // 2^(24 - e), 24 - e in [-40, 9]
+    // the finer scale e + sfine of small products: below 2^(24 + sfine) <= 2^50
+    // units each, 2^lg of them below 2^62
+    const int sfine = min(26, 38 - lg);
+    const bool dense = l < a.dense_start;
+    // words of the slice in use: a dense slice (at most kSlice / 2 entries)
+    // keeps its small products' sums at the finer scale in acc[kFine + i]
+    const int nw = dense ? kFine + 2 * slots : 2 * slots;
     float* gl = ADAM ? nullptr : grads + ((size_t)l * a.T + elem0) * 2;
     const size_t ebase = (size_t)l * a.T + elem0;  // first table entry of the slice
-    for (int i = threadIdx.x; i < 2 * slots; i += kAccThreads) acc[i] = 0ull;
-    if constexpr (ADAM)
-        for (int i = threadIdx.x; i < kNfWords; i += kAccThreads) nf[i] = 0u;
+    for (int i = threadIdx.x; i < nw; i += kAccThreads) acc[i] = 0ull;
+    for (int i = threadIdx.x; i < kNfWords; i += kAccThreads) {
+        sus[i] = aux[i] = tny[i] = 0u;
+        if constexpr (ADAM) nf[i] = 0u;
+    }
     if (threadIdx.x == 0) s_flag = 0;
     __syncthreads();
+    // the gradients a record adds a small product to (refined if their sums stay small)
+    auto mark_small = [&](const float (&c)[4], const int (&at)[4]) {
+        if (small_product(c[0], thr) | small_product(c[1], thr) | small_product(c[2], thr) |
+            small_product(c[3], thr)) {
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (small_product(c[j], thr)) set_bit(sus, at[j]);
+        }
+    };
     // records per thread in flight before their LDS adds (hashed bins)
     constexpr int kBatch = 8;
     if (l < a.dense_start) {
@@ -581,7 +697,8 @@ __global__ __launch_bounds__(kAccThreads) __attribute__((amdgpu_waves_per_eu(4))
         // pairs.  Each lane takes kRun consecutive records (one 64-byte
         // piece of the wave's contiguous span) and adds the fixed-point
         // values of a run of equal keys in registers (exact: integer sums in
-        // any order), with one LDS add per run it holds.
+        // any order), with one LDS add per run it holds: products below 2^24
+        // quanta at the finer scale into acc[kFine + i], the others at e.
         constexpr int kRun = 4;
         constexpr int kGroups = 2;  // runs per lane in flight (4 and 6 measured slower)
         const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -599,14 +716,18 @@ __global__ __launch_bounds__(kAccThreads) __attribute__((amdgpu_waves_per_eu(4))
 #pragma unroll
             for (int gi = 0; gi < kGroups; gi++) {
                 uint32_t cur = 0xffffffffu;
-                long long q[4] = {0, 0, 0, 0};
+                long long q[4] = {0, 0, 0, 0}, qf[4] = {0, 0, 0, 0};
+                uint32_t sm = 0;  // gradients of the run that took a small product
                 auto flush = [&]() {
                     if (cur == 0xffffffffu) return;
                     const int s0 = (int)(cur & 0xffffu), s1 = (int)(cur >> 16);
-                    if (q[0]) lds_add(acc, 2 * s0, q[0]);
-                    if (q[1]) lds_add(acc, 2 * s0 + 1, q[1]);
-                    if (q[2]) lds_add(acc, 2 * s1, q[2]);
-                    if (q[3]) lds_add(acc, 2 * s1 + 1, q[3]);
+                    const int at[4] = {2 * s0, 2 * s0 + 1, 2 * s1, 2 * s1 + 1};
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        if (q[j]) lds_add(acc, at[j], q[j]);
+                        if (qf[j]) lds_add(acc, kFine + at[j], qf[j]);
+                        if (sm & (1u << j)) set_bit(sus, at[j]);
+                    }
                 };
 #pragma unroll
                 for (int k = 0; k < kRun; k++) {
@@ -617,25 +738,24 @@ __global__ __launch_bounds__(kAccThreads) __attribute__((amdgpu_waves_per_eu(4))
                         flush();
                         cur = key;
                         q[0] = q[1] = q[2] = q[3] = 0;
+                        qf[0] = qf[1] = qf[2] = qf[3] = 0;
+                        sm = 0;
                     }
-                    const int s0 = (int)(key & 0xffffu), s1 = (int)(key >> 16);
-                    const float v0 = r[gi][k].y, v1 = r[gi][k].z, wx = r[gi][k].w, ux = 1.0f - wx;
-                    const float c[4] = {v0 * wx, v1 * wx, v0 * ux, v1 * ux};
-                    const int at[4] = {2 * s0, 2 * s0 + 1, 2 * s1, 2 * s1 + 1};
-                    if (finite_bits(v0) & finite_bits(v1) & finite_bits(wx)) {
+                    const RecProducts rp = rec_products(r[gi][k]);
+                    const bool fin = rec_finite(r[gi][k]);
 #pragma unroll
-                        for (int j = 0; j < 4; j++) q[j] += fixed_of(c[j], e);
-                    } else {
-#pragma unroll
-                        for (int j = 0; j < 4; j++) {
-                            if (isfinite(c[j])) {
-                                q[j] += fixed_of(c[j], e);
-                            } else if constexpr (ADAM) {
-                                atomicOr(&nf[at[j] >> 5], 1u << (at[j] & 31));
-                            } else {
-                                atomic_add_f32(gl + at[j], c[j]);
-                                s_flag = 1;
-                            }
+                    for (int j = 0; j < 4; j++) {
+                        const bool small = small_product(rp.c[j], thr);
+                        sm |= small ? 1u << j : 0u;
+                        if (small) {
+                            qf[j] += fixed_of(rp.c[j], e + sfine);
+                        } else if (fin || isfinite(rp.c[j])) {
+                            q[j] += fixed_of(rp.c[j], e);
+                        } else if constexpr (ADAM) {
+                            set_bit(nf, rp.at[j]);
+                        } else {
+                            atomic_add_f32(gl + rp.at[j], rp.c[j]);
+                            s_flag = 1;
                         }
                     }
                 }
@@ -653,26 +773,18 @@ __global__ __launch_bounds__(kAccThreads) __attribute__((amdgpu_waves_per_eu(4))
 #pragma unroll
         for (int k = 0; k < kBatch; k++) {
             if (i0 + k * kAccThreads >= ch.z) break;
-            const uint32_t key = __float_as_uint(r[k].x);
-            const int s0 = (int)(key & 0xffffu), s1 = (int)(key >> 16);
-            const float v0 = r[k].y, v1 = r[k].z, wx = r[k].w, ux = 1.0f - wx;
-            if (finite_bits(v0) & finite_bits(v1) & finite_bits(wx)) {
-                // |v| <= 65504 and wx, ux in [0, 1]: every product is finite
-                lds_add(acc, 2 * s0, fixed_of(v0 * wx, e));
-                lds_add(acc, 2 * s0 + 1, fixed_of(v1 * wx, e));
-                lds_add(acc, 2 * s1, fixed_of(v0 * ux, e));
-                lds_add(acc, 2 * s1 + 1, fixed_of(v1 * ux, e));
+            const RecProducts rp = rec_products(r[k]);
+            if (rec_finite(r[k])) {
+#pragma unroll
+                for (int j = 0; j < 4; j++) lds_add(acc, rp.at[j], fixed_of(rp.c[j], e));
             } else if constexpr (ADAM) {
-                add_or_mark(acc, nf, 2 * s0, v0 * wx, e);
-                add_or_mark(acc, nf, 2 * s0 + 1, v1 * wx, e);
-                add_or_mark(acc, nf, 2 * s1, v0 * ux, e);
-                add_or_mark(acc, nf, 2 * s1 + 1, v1 * ux, e);
+#pragma unroll
+                for (int j = 0; j < 4; j++) add_or_mark(acc, nf, rp.at[j], rp.c[j], e);
             } else {
-                add_checked(acc, gl, 2 * s0, v0 * wx, e, &s_flag);
-                add_checked(acc, gl, 2 * s0 + 1, v1 * wx, e, &s_flag);
-                add_checked(acc, gl, 2 * s1, v0 * ux, e, &s_flag);
-                add_checked(acc, gl, 2 * s1 + 1, v1 * ux, e, &s_flag);
+#pragma unroll
+                for (int j = 0; j < 4; j++) add_checked(acc, gl, rp.at[j], rp.c[j], e, &s_flag);
             }
+            mark_small(rp.c, rp.at);
         }
     }
     __syncthreads();
@@ -681,10 +793,11 @@ __global__ __launch_bounds__(kAccThreads) __attribute__((amdgpu_waves_per_eu(4))
         // bits) as a partial slice; the last one to finish adds them all up
         // (exact integer sums) and finishes the bin as its sole owner.
         unsigned long long* mine = part + (size_t)(pbase + pj) * (2 * kSlice);
-        for (int i = threadIdx.x; i < 2 * slots; i += kAccThreads) mine[i] = acc[i];
-        if constexpr (ADAM) {
-            uint32_t* mnf = part_nf + (size_t)(pbase + pj) * kNfWords;
-            for (int i = threadIdx.x; i < kNfWords; i += kAccThreads) mnf[i] = nf[i];
+        for (int i = threadIdx.x; i < nw; i += kAccThreads) mine[i] = acc[i];
+        uint32_t* msus = part_sus + (size_t)(pbase + pj) * kNfWords;
+        for (int i = threadIdx.x; i < kNfWords; i += kAccThreads) {
+            msus[i] = sus[i];
+            if constexpr (ADAM) part_nf[(size_t)(pbase + pj) * kNfWords + i] = nf[i];
         }
         // done[bin]: chunks finished; done[kMaxBins + bin]: non-finite atomics seen
         if (!ADAM && threadIdx.x == 0 && s_flag)
@@ -706,16 +819,17 @@ __global__ __launch_bounds__(kAccThreads) __attribute__((amdgpu_waves_per_eu(4))
 #pragma unroll
             for (int k = 0; k < kMergeBatch; k++) {
                 const int i = threadIdx.x + k * kAccThreads;
-                t[k] = i < 2 * slots ? other[i] : 0ull;
+                t[k] = i < nw ? other[i] : 0ull;
             }
 #pragma unroll
             for (int k = 0; k < kMergeBatch; k++) {
                 const int i = threadIdx.x + k * kAccThreads;
-                if (i < 2 * slots) acc[i] += t[k];
+                if (i < nw) acc[i] += t[k];
             }
-            if constexpr (ADAM) {
-                const uint32_t* onf = part_nf + (size_t)(pbase + c) * kNfWords;
-                for (int i = threadIdx.x; i < kNfWords; i += kAccThreads) nf[i] |= onf[i];
+            const uint32_t* osus = part_sus + (size_t)(pbase + c) * kNfWords;
+            for (int i = threadIdx.x; i < kNfWords; i += kAccThreads) {
+                sus[i] |= osus[i];
+                if constexpr (ADAM) nf[i] |= part_nf[(size_t)(pbase + c) * kNfWords + i];
             }
         }
         if (threadIdx.x == 0) {
@@ -726,11 +840,139 @@ __global__ __launch_bounds__(kAccThreads) __attribute__((amdgpu_waves_per_eu(4))
         }
         __syncthreads();
     }
-    // the sole owner of the slice's sums
+    // The sole owner of the slice's sums.  Refinement (see the file comment)
+    // over the records of the whole bin, [r0, r1).
+    const uint32_t r0 = ch.y - pj * kChunk, r1 = r0 + tot;
+    bool refine = false;  // hashed slice: some gradients summed again (pass 1)
+    bool tiny = false;    // gradients below 2^24 units of their finer scale
+    if (dense) {
+        // the two scales together, in units of the finer one
+        for (int i = threadIdx.x; i < 2 * slots; i += kAccThreads) {
+            if (!get_bit(sus, i)) continue;
+            const double c = ldexp((double)(long long)acc[i], sfine) + (double)(long long)acc[kFine + i];
+            if (fabs(c) < 0x1p24) {
+                set_bit(tny, i);
+                tiny = true;
+            }
+        }
+    } else {
+        // keep the marks of gradients whose sums stayed below 2^24 quanta
+        bool few = false;
+        for (int i = threadIdx.x; i < 2 * slots; i += kAccThreads) {
+            if (!get_bit_shared(sus, i)) continue;
+            const long long q = (long long)acc[i];
+            if (q > -kFewBits && q < kFewBits) few = true;
+            else clear_bit(sus, i);
+        }
+        refine = __syncthreads_or(few);
+    }
+    if (refine) {
+        // pass 1: the marked gradients' small products at scale e + sfine; a
+        // product of 2^24 quanta or more marks its gradient for pass 2
+        for (int i = threadIdx.x; i < 2 * slots; i += kAccThreads)
+            if (get_bit(sus, i)) {
+                acc[i] = 0ull;
+                ex_off[i] = (uint8_t)sfine;
+            }
+        __syncthreads();
+        bool big = false;
+        for_each_record(rec, r0, r1, [&](const RecProducts& rp) {
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (finite_bits(rp.c[j]) && rp.c[j] != 0.f && get_bit(sus, rp.at[j])) {
+                    if (small_product(rp.c[j], thr)) {
+                        lds_add(acc, rp.at[j], fixed_of(rp.c[j], e + sfine));
+                    } else {
+                        set_bit(aux, rp.at[j]);
+                        big = true;
+                    }
+                }
+        });
+        if (__syncthreads_or(big)) {
+            // pass 2 (products cancelling): those gradients at scale e again
+            for (int i = threadIdx.x; i < 2 * slots; i += kAccThreads)
+                if (get_bit(aux, i)) {
+                    acc[i] = 0ull;
+                    clear_bit(sus, i);
+                }
+            __syncthreads();
+            for_each_record(rec, r0, r1, [&](const RecProducts& rp) {
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    if (finite_bits(rp.c[j]) && get_bit(aux, rp.at[j])) lds_add(acc, rp.at[j], fixed_of(rp.c[j], e));
+            });
+            __syncthreads();
+        }
+        // gradients whose finer sums stay below 2^24 units (products of a few
+        // quanta at most)
+        for (int i = threadIdx.x; i < 2 * slots; i += kAccThreads) {
+            if (!get_bit(sus, i)) continue;
+            const long long q = (long long)acc[i];
+            if (q > -kFewBits && q < kFewBits) {
+                set_bit(tny, i);
+                tiny = true;
+            }
+        }
+    }
+    const bool any_tiny = __syncthreads_or(tiny);
+    if (any_tiny) {
+        // passes 3 and 4: the largest |product| of each (fp32 bit patterns of
+        // non-negative values order as the values), then the sums at the
+        // exponent it sets: |product| < 2^(Es + 1) gives min(49, 60 - lg) - Es,
+        // Es <= E, an offset over e of E - Es in [0, 164]; the sum lands in
+        // acc[i] (a dense slice's finer sum cleared)
+        for (int i = threadIdx.x; i < 2 * slots; i += kAccThreads)
+            if (get_bit(tny, i)) {
+                acc[i] = 0ull;
+                if (dense) acc[kFine + i] = 0ull;
+            }
+        __syncthreads();
+        for_each_record(rec, r0, r1, [&](const RecProducts& rp) {
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (finite_bits(rp.c[j]) && rp.c[j] != 0.f && get_bit(tny, rp.at[j]))
+                    __hip_atomic_fetch_max(acc + rp.at[j], (unsigned long long)(__float_as_uint(rp.c[j]) & 0x7fffffffu),
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        });
+        __syncthreads();
+        for (int i = threadIdx.x; i < 2 * slots; i += kAccThreads) {
+            if (!get_bit(tny, i)) continue;
+            const uint32_t mb = (uint32_t)acc[i];
+            const int Es = mb >= 0x800000u ? (int)(mb >> 23) - 127 : (mb ? 31 - __clz(mb) - 149 : E);
+            ex_off[i] = (uint8_t)min(255, max(0, E - Es));
+            acc[i] = 0ull;
+        }
+        __syncthreads();
+        for_each_record(rec, r0, r1, [&](const RecProducts& rp) {
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (finite_bits(rp.c[j]) && rp.c[j] != 0.f && get_bit(tny, rp.at[j]))
+                    lds_add(acc, rp.at[j], fixed_of(rp.c[j], e + ex_off[rp.at[j]]));
+        });
+        __syncthreads();
+    }
+    // gradient word i: its fp32 value (the exact fixed-point sum rounded once;
+    // a dense slice's two scales combined in fp64 first) and whether its sum
+    // is nonzero
+    auto grad_of = [&](int i, float& g) -> bool {
+        const long long q = (long long)acc[i];
+        if ((refine || any_tiny) && (get_bit(tny, i) || (refine && get_bit(sus, i)))) {
+            g = ldexpf((float)q, -(e + (int)ex_off[i]));
+            return q != 0;
+        }
+        if (dense) {
+            const long long f = (long long)acc[kFine + i];
+            if (f == 0) g = ldexpf((float)q, -e);
+            else if (q == 0) g = ldexpf((float)f, -(e + sfine));
+            else g = (float)(ldexp((double)q, -e) + ldexp((double)f, -(e + sfine)));
+            return (q | f) != 0;
+        }
+        g = ldexpf((float)q, -e);
+        return q != 0;
+    };
     if constexpr (ADAM) {
         // update every entry the sums reached
-        for (int s0 = threadIdx.x; s0 < slots; s0 += kAdamBatch * kAccThreads)
-            table_adam_batch(ta, ebase, s0, slots, [&](int i) { return (long long)acc[i]; }, nf, e);
+        for (int s0 = threadIdx.x; s0 < slots; s0 += kAdamBatch * kAccThreads) table_adam_batch(ta, ebase, s0, slots, grad_of, nf);
         return;
     }
     {
@@ -740,11 +982,11 @@ __global__ __launch_bounds__(kAccThreads) __attribute__((amdgpu_waves_per_eu(4))
         float2* g2 = reinterpret_cast<float2*>(gl);
         if (atomic || grads_zero) {
             for (int s = threadIdx.x; s < slots; s += kAccThreads) {
-                const long long q0 = (long long)acc[2 * s], q1 = (long long)acc[2 * s + 1];
-                const float v0 = ldexpf((float)q0, -e), v1 = ldexpf((float)q1, -e);
+                float v0, v1;
+                const bool z0 = grad_of(2 * s, v0), z1 = grad_of(2 * s + 1, v1);
                 if (atomic) {
-                    if (q0) atomic_add_f32(gl + 2 * s, v0);
-                    if (q1) atomic_add_f32(gl + 2 * s + 1, v1);
+                    if (z0) atomic_add_f32(gl + 2 * s, v0);
+                    if (z1) atomic_add_f32(gl + 2 * s + 1, v1);
                 } else {
                     g2[s] = make_float2(v0, v1);
                 }
@@ -762,8 +1004,9 @@ __global__ __launch_bounds__(kAccThreads) __attribute__((amdgpu_waves_per_eu(4))
                 for (int k = 0; k < kBatch; k++) {
                     const int s = s0 + k * kAccThreads;
                     if (s >= slots) break;
-                    const long long q0 = (long long)acc[2 * s], q1 = (long long)acc[2 * s + 1];
-                    if (q0 | q1) g2[s] = make_float2(o[k].x + ldexpf((float)q0, -e), o[k].y + ldexpf((float)q1, -e));
+                    float v0, v1;
+                    const bool z0 = grad_of(2 * s, v0), z1 = grad_of(2 * s + 1, v1);
+                    if (z0 | z1) g2[s] = make_float2(o[k].x + v0, o[k].y + v1);
                 }
             }
         }
@@ -789,6 +1032,7 @@ struct ScatterPlan {
     unsigned long long* part = nullptr;  // partial slices of the chunks of multi-chunk bins
     uint32_t* done = nullptr;            // [2 kMaxBins]: chunks finished, non-finite atomics seen
     uint32_t* part_nf = nullptr;         // non-finite bits of the partial slices (fused table update)
+    uint32_t* part_sus = nullptr;        // small-product marks of the partial slices
 };
 
 namespace {
@@ -819,13 +1063,15 @@ bool layout(const GridMeta& m, ScatterArgs& a)
         if (m.res[l] < 1) return false;
         if (l < m.denseLevelStart) {
             const long long st = (long long)m.res[l] + 1;
-            if (st > kSlice) return false;
-            // about kDenseBins bins per level (at most kSlice entries each): a
+            if (st > kSlice / 2) return false;
+            // about kDenseBins bins per level (at most kSlice / 2 entries each,
+            // the other half of the LDS slice holding their finer sums): a
             // coarse level's few entries take a contribution from nearly
             // every sample, so its records are spread over as many blocks
             // as a fine level's
             const long long rows = st * st;
-            const int rps = (int)std::max(1LL, std::min((long long)(kSlice / st), (rows + kDenseBins - 1) / kDenseBins));
+            const int rps =
+                (int)std::max(1LL, std::min((long long)(kSlice / 2 / st), (rows + kDenseBins - 1) / kDenseBins));
             a.rows_per_slice[l] = rps;
             bins += (int)((st * st + rps - 1) / rps);
         } else {
@@ -850,7 +1096,7 @@ namespace {
 // kernels leave them zero after every call, so a region that starts zero
 // stays zero whatever the configuration.
 struct PlanLayout {
-    size_t o_don, o_prt, o_pnf, o_rec, o_cnt, o_tot, o_lmx, o_lmf, o_chk, o_nch, zero_end, bytes;
+    size_t o_don, o_prt, o_pnf, o_psu, o_rec, o_cnt, o_tot, o_lmx, o_lmf, o_chk, o_nch, zero_end, bytes;
 };
 
 // Partial slices: every chunk of a multi-chunk bin has one; a bin of t > kChunk
@@ -878,6 +1124,7 @@ bool plan_shape(const GridMeta& m, int maxN, ScatterPlan& p, PlanLayout& lay, in
     lay.zero_end = off;
     lay.o_prt = off; off = align_up(off + (size_t)multi * 2 * kSlice * 8);
     lay.o_pnf = off; off = align_up(off + (with_nf ? (size_t)multi * kNfWords * 4 : 0));
+    lay.o_psu = off; off = align_up(off + (size_t)multi * kNfWords * 4);
     lay.o_rec = off; off = align_up(off + recs * sizeof(float4));
     lay.o_cnt = off; off = align_up(off + (size_t)a.rounds * a.bins * 4);
     lay.o_tot = off; off = align_up(off + (size_t)a.bins * 4);
@@ -901,7 +1148,8 @@ void plan_bind(ScatterPlan& p, char* base, const PlanLayout& lay)
     p.nchunks = reinterpret_cast<uint32_t*>(base + lay.o_nch);
     p.part = reinterpret_cast<unsigned long long*>(base + lay.o_prt);
     p.done = reinterpret_cast<uint32_t*>(base + lay.o_don);
-    p.part_nf = lay.o_pnf < lay.o_rec ? reinterpret_cast<uint32_t*>(base + lay.o_pnf) : nullptr;
+    p.part_nf = lay.o_pnf < lay.o_psu ? reinterpret_cast<uint32_t*>(base + lay.o_pnf) : nullptr;
+    p.part_sus = reinterpret_cast<uint32_t*>(base + lay.o_psu);
 }
 
 }  // namespace
@@ -981,11 +1229,11 @@ void scatter_launch(ScatterPlan* p, const GridMeta& m, const __half* denc, const
     if (ta)
         hipLaunchKernelGGL(scatter_accumulate_kernel<true>, dim3(grid), dim3(kAccThreads), 0, stream, a, p->rec,
                            p->chunks, p->nchunks, p->totals, p->lvlmax_final, nullptr, p->part, p->done, 0,
-                           p->part_nf, *ta);
+                           p->part_nf, p->part_sus, *ta);
     else
         hipLaunchKernelGGL(scatter_accumulate_kernel<false>, dim3(grid), dim3(kAccThreads), 0, stream, a, p->rec,
                            p->chunks, p->nchunks, p->totals, p->lvlmax_final, grads, p->part, p->done,
-                           grads_zero ? 1 : 0, nullptr, TableAdamArgs{});
+                           grads_zero ? 1 : 0, nullptr, p->part_sus, TableAdamArgs{});
     GRAFT_LAUNCH_CHECK();
 }
 

@@ -61,6 +61,13 @@ void orc_hash_scatter_bwd(const float* pos, int pos_stride, int N,
                           const uint16_t* denc, int T, int L, int lowestSize, float b,
                           float* grads);
 
+/* The same sums written to grads (not added), with per gradient word the sum
+ * of the products' magnitudes and the number of products: the inputs of an
+ * error bound for a reordered or fixed-point sum (test infrastructure). */
+void orc_hash_scatter_stats(const float* pos, int pos_stride, int N,
+                            const uint16_t* denc, int T, int L, int lowestSize, float b,
+                            float* grads, float* gabs, uint32_t* count);
+
 /* ---- fused MLP (networkFusion.cu:197-355, networkFusionHashtable.cu:572-682) --
  * Layer l maps in_l -> out_l with W_l fp16 row-major [out_l][in_l] and b_l fp32.
  * in_0 = inDim, out_{L-1} = outDim, all others hidDim.  Hidden activations are

@@ -47,6 +47,7 @@ def lib():
             "orc_hash_corners": (None, [_f32p, i, i, i, i, i, f, i, _u32p, _f32p]),
             "orc_hash_encode_fwd": (None, [_f32p, i, i, _u16p, i, i, i, f, _u16p]),
             "orc_hash_scatter_bwd": (None, [_f32p, i, i, _u16p, i, i, i, f, _f32p]),
+            "orc_hash_scatter_stats": (None, [_f32p, i, i, _u16p, i, i, i, f, _f32p, _f32p, _u32p]),
             "orc_mlp_forward": (None, [_u16p, i, i, i, i, i, _u16p, _f32p, i, C.c_void_p, _f32p]),
             "orc_mlp_backward": (None, [_u16p, _u16p, C.c_void_p, i, i, i, i, i, _u16p,
                                         _f32p, _f32p, C.c_void_p]),
@@ -166,6 +167,17 @@ def hash_scatter(pos, denc, T, L, base, b, grads=None):
     g = np.zeros(L * T * 2, np.float32) if grads is None else grads
     lib().orc_hash_scatter_bwd(pos, st, N, _h(denc).ravel(), T, L, base, float(b), g)
     return g
+
+
+def hash_scatter_stats(pos, denc, T, L, base, b):
+    """(grads, sum of |products|, product count) per gradient word, each [L * T * 2]."""
+    pos, st = _pos(pos)
+    N = pos.shape[0]
+    g = np.empty(L * T * 2, np.float32)
+    ga = np.empty(L * T * 2, np.float32)
+    cnt = np.empty(L * T * 2, np.uint32)
+    lib().orc_hash_scatter_stats(pos, st, N, _h(denc).ravel(), T, L, base, float(b), g, ga, cnt)
+    return g, ga, cnt
 
 
 def _layer_shapes(inD, hid, outD, nl):

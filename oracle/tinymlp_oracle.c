@@ -239,6 +239,61 @@ void orc_hash_scatter_bwd(const float* pos, int pos_stride, int N,
     }
 }
 
+/* The same sums as orc_hash_scatter_bwd (grads written, not added to) plus,
+ * per gradient word, the sum of the products' magnitudes (fp64 rounded to
+ * fp32) and the number of products (zero ones included): what an error bound
+ * of a reordered or fixed-point sum needs. */
+void orc_hash_scatter_stats(const float* pos, int pos_stride, int N,
+                            const uint16_t* denc, int T, int L, int lowestSize, float b,
+                            float* grads, float* gabs, uint32_t* count)
+{
+    float scale[64];
+    int res[64];
+    orc_level_scales(lowestSize, b, L, scale, res);
+    int dls = orc_dense_level_start(T, lowestSize, b, L);
+    /* fp64 sums of every level, kept between calls (repeated test calls
+     * would otherwise pay the first touch of fresh pages every time) */
+    static double* ws = NULL;
+    static size_t ws_words = 0;
+    size_t need = (size_t)L * T * 4;
+    if (need > ws_words) {
+        free(ws);
+        ws = (double*)malloc(need * sizeof(double));
+        ws_words = ws ? need : 0;
+        if (!ws) return;
+    }
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int l = 0; l < L; l++) {
+        size_t lev = (size_t)T * 2;
+        double* acc = ws + (size_t)l * 2 * lev;
+        memset(acc, 0, 2 * lev * sizeof(double));
+        double* aab = acc + lev;
+        uint32_t* cnt = count + (size_t)l * lev;
+        memset(cnt, 0, lev * sizeof(uint32_t));
+        for (int n = 0; n < N; n++) {
+            uint32_t idx[8];
+            float w[8];
+            corners_one(pos + (size_t)n * pos_stride, scale[l], res[l], l, T, l < dls, 1, idx, w);
+            float gx = orc_f16_to_f32(denc[(size_t)n * 2 * L + 2 * l]);
+            float gy = orc_f16_to_f32(denc[(size_t)n * 2 * L + 2 * l + 1]);
+            for (int c = 0; c < 8; c++) {
+                size_t o = idx[c] - (size_t)l * lev;
+                float px = gx * w[c], py = gy * w[c];
+                acc[o] += (double)px;
+                acc[o + 1] += (double)py;
+                aab[o] += fabs((double)px);
+                aab[o + 1] += fabs((double)py);
+                cnt[o]++;
+                cnt[o + 1]++;
+            }
+        }
+        for (size_t i = 0; i < lev; i++) {
+            grads[(size_t)l * lev + i] = (float)acc[i];
+            gabs[(size_t)l * lev + i] = (float)aab[i];
+        }
+    }
+}
+
 /* ------------------------------------------------------------------------ */
 /* fused MLP                                                                 */
 /* ------------------------------------------------------------------------ */

@@ -26,6 +26,56 @@ def assert_close(actual, expected, atol=ATOL, rtol=RTOL, what=""):
                              f"worst at {i}: got {a[i]!r} expected {e[i]!r}")
 
 
+def scatter_quantum(denc, L, T, N=None):
+    """Per gradient word [L * T * 2], an upper bound on the binned scatter's fixed-point quantum 2^-e of the
+    word's level: e = min(49, 60 - ceil(log2(records of the bin))) - E, E the exponent of the level's
+    largest fp16 |dL/denc| (non-finite ones count as 2^15), and a bin holds at most 4 records per sample."""
+    d = np.ascontiguousarray(denc, np.float16).reshape(-1, L, 2).view(np.uint16) & 0x7fff
+    ex = ((d.max(axis=(0, 2)) >> 10) & 31).astype(np.int64)
+    E = np.where(ex == 0, -15, np.minimum(ex - 15, 15))
+    n = d.shape[0] if N is None else N
+    lg = int(np.ceil(np.log2(max(4 * n, 2))))
+    return np.repeat(np.ldexp(1.0, E - min(49, 60 - lg)), 2 * T)
+
+
+def scatter_bound(g, gabs, cnt, quantum=None, extra_roundings=0):
+    """Per gradient word, the bound on |binned scatter - oracle| given the oracle's sum (g), sum of
+    |products| (gabs) and product count (cnt) of the word (pyoracle.hash_scatter_stats).  Both sides form
+    the reference's fp32 products g_f * ((wx * wy) * wz) bit for bit, so only the sums differ:
+
+    - each side rounds its sum to fp32 once: 2^-23 |g| (the oracle's fp64 sum of the products is exact to
+      cnt * 2^-52 gabs);
+    - the fixed-point sums, cnt / 2 times the smaller of the level's quantum (scatter_quantum; each
+      product is within half of it) and 2^-24 gabs (a sum of at least 2^24 quanta has each product within
+      2^-25 of the sum, products of at least 2^24 quanta each are within 2^-25 of the smallest; the other
+      sums are summed again at the word's own scale, where a product is within 2^-37 of the word's largest
+      product for bins of up to 2^22 records);
+    - extra_roundings fp32 roundings of gabs for additions the caller makes (sub-batches added one after
+      another).
+    """
+    ga = gabs.astype(np.float64)
+    per = np.ldexp(ga, -24)
+    if quantum is not None:
+        per = np.minimum(per, quantum)
+    c = cnt.astype(np.float64)
+    return (np.ldexp(np.abs(g.astype(np.float64)), -23) + np.ldexp(extra_roundings + c * 2.0 ** -28, -24) * ga
+            + 0.5 * c * per)
+
+
+def assert_scatter_close(got, want, bound, base=0.0, what=""):
+    """got / want: gradient arrays that held `base` before the scatter added to it; every word within its
+    bound (plus the fp32 rounding of the addition to a nonzero base)."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    allow = bound + (np.ldexp(np.abs(want), -23) if base else 0.0)
+    err = np.abs(got - want)
+    bad = err > allow
+    if bad.any():
+        i = int(np.argmax(np.where(bad, err / np.maximum(allow, 1e-300), 0)))
+        raise AssertionError(f"{what}: {int(bad.sum())} of {got.size} words outside the per-word bound; worst at "
+                             f"{i}: got {got[i]!r} expected {want[i]!r} bound {allow[i]!r}")
+
+
 def positions(n, seed, stride=4):
     rng = np.random.default_rng(seed)
     p = np.zeros((n, stride), np.float32)

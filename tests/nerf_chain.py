@@ -12,7 +12,7 @@ from __future__ import annotations
 import numpy as np
 
 import pyoracle as orc
-from helpers import assert_close, d2h, ptr_array
+from helpers import assert_close, d2h, ptr_array, scatter_bound, scatter_quantum
 
 MN = np.float32([-1.5, -1.5, -1.5])
 MX = np.float32([1.5, 1.5, 1.5])
@@ -232,37 +232,48 @@ def check_step(nerf, opts, st, march, o, d, gt, R, bg, lr, rgb_out):
     check_adam_head(D, gbuf, lr, opts)
     check_adam_head(Cs, cbuf, lr, opts)
     # hash table: scatter of the GPU's dL/d(encoding), then Adam from the state before
-    g_ref = orc.hash_scatter(pos, denc, T_, Lh, base, growth)
-    bc1, bc2 = orc.adam_bias_corrections(opts.beta1, opts.beta2, D.step + 1)
-    t_ref = st["table"].copy()
-    orc.adam_hash(t_ref, g_ref.copy(), st["hash_m"].copy(), st["hash_v"].copy(), lr, opts.beta1, opts.beta2,
-                  opts.epsilon, bc1, bc2, 1.0 / opts.lossScale, want_f16=False)
-    t_gpu = d2h(gbuf.master_hashtable, t_ref.shape, np.float32)
-    # entries no nonzero product reaches: skipped by Adam on both sides, bit-identical
-    g_abs = orc.hash_scatter(pos, np.abs(denc), T_, Lh, base, growth)
+    t_gpu = d2h(gbuf.master_hashtable, st["table"].shape, np.float32)
+    m_gpu = d2h(gbuf.hash_m, st["table"].shape, np.float32)
+    n_touched, n_ill = check_table_update(t_gpu, m_gpu, st["table"], st["hash_m"], st["hash_v"], pos, denc, T_, Lh,
+                                          base, growth, lr, opts, D.step + 1)
+    return {"samples": N, "loss": float(np.mean((comp["rgb"] - gt[:R]) ** 2)),
+            "loss_gpu": float(np.mean((rgb_out[:R] - gt[:R]) ** 2)), "touched": n_touched,
+            "ill_conditioned": n_ill}
+
+
+def check_table_update(t_gpu, m_gpu, w0, m0, v0, pos, denc, T_, L, base, growth, lr, opts, step):
+    """The fused scatter + Adam of the hash table (optimizerKernel.cu:116-167 on the gradient of
+    networkFusionBackwardHashtable.cu:783-910) against the oracle's scatter and Adam from the state before
+    (w0, m0, v0), on every touched entry:
+
+    - entries no nonzero product reaches: skipped, bit-identical;
+    - entries whose gradient is well conditioned (|g_ref| above 4x the per-word bound of the binned sum
+      against the oracle's): the reference updates them, so must the fused path, to the oracle's Adam
+      within 1e-6 rel / 1e-7 abs (m within 1e-5 rel);
+    - the ill-conditioned rest (products cancelling to within a few fp32 roundings of their magnitudes)
+      stays below 0.1 % of the touched entries.
+    Returns (touched, ill-conditioned) counts."""
+    g_ref, g_abs, cnt = orc.hash_scatter_stats(pos, denc, T_, L, base, growth)
+    bc1, bc2 = orc.adam_bias_corrections(opts.beta1, opts.beta2, step)
+    t_ref, m_ref, v_ref = w0.copy(), m0.copy(), v0.copy()
+    orc.adam_hash(t_ref, g_ref.copy(), m_ref, v_ref, lr, opts.beta1, opts.beta2, opts.epsilon, bc1, bc2,
+                  1.0 / opts.lossScale, want_f16=False)
     untouched = g_abs == 0
-    moved = np.nonzero(untouched & (t_gpu.view(np.uint32) != st["table"].view(np.uint32)))[0]
+    moved = np.nonzero(untouched & (t_gpu.view(np.uint32) != w0.view(np.uint32)))[0]
     if moved.size:
         lev = moved // (2 * T_)
         slot = (moved % (2 * T_)) // 2
         raise AssertionError(f"{moved.size} table entries without gradient moved: idx {moved[:8]} level {lev[:8]} "
-                             f"slot {slot[:8]} before {st['table'][moved[:8]]} after {t_gpu[moved[:8]]}")
-    # entries whose products cancel exactly in the oracle's product order (g * ((wx * wy) * wz)) but not
-    # necessarily in the GPU's ((g * wy wz) * wx): Adam skips them or applies a zero-gradient update
-    cancel = (g_abs != 0) & (g_ref == 0)
-    if cancel.any():
-        m0, v0, w0 = st["hash_m"][cancel], st["hash_v"][cancel], st["table"][cancel]
-        mh = (opts.beta1 * m0) / bc1
-        vh = (opts.beta2 * v0) / bc2
-        w_upd = w0 - (lr * mh) / (np.sqrt(vh) + opts.epsilon)
-        got = t_gpu[cancel]
-        ok = (got.view(np.uint32) == w0.view(np.uint32)) | (np.abs(got - w_upd) <= 1e-6 + 1e-5 * np.abs(w_upd))
-        assert ok.all(), f"{(~ok).sum()} cancelled-gradient entries neither skipped nor zero-gradient updated"
-    big = np.abs(g_ref) > 1e-4 * np.abs(g_ref).max()
-    assert_close(t_gpu[big], t_ref[big], atol=1e-6, rtol=1e-5, what="hash table after Adam")
-    return {"samples": N, "loss": float(np.mean((comp["rgb"] - gt[:R]) ** 2)),
-            "loss_gpu": float(np.mean((rgb_out[:R] - gt[:R]) ** 2)), "touched": int((~untouched).sum()),
-            "cancelled": int(cancel.sum())}
+                             f"slot {slot[:8]} before {w0[moved[:8]]} after {t_gpu[moved[:8]]}")
+    ill = ~untouched & (np.abs(g_ref) <= 4.0 * scatter_bound(g_ref, g_abs, cnt, scatter_quantum(denc, L, T_)))
+    well = ~untouched & ~ill
+    n_touched = int((~untouched).sum())
+    assert n_touched > 0
+    assert ill.sum() <= 1e-3 * n_touched, f"{int(ill.sum())} of {n_touched} touched entries ill-conditioned"
+    assert_close(t_gpu[well], t_ref[well], atol=1e-7, rtol=1e-6, what="hash table after Adam (every touched entry)")
+    assert_close(m_gpu[well], m_ref[well], atol=1e-7 * float(np.abs(m_ref).max()), rtol=1e-5,
+                 what="hash table Adam m (every touched entry)")
+    return n_touched, int(ill.sum())
 
 
 def refresh_oracle_chunks(opts, st):

@@ -137,7 +137,7 @@ def test_c5_full_scale_steps_match_oracle(views, cascades):
             refreshes += 1
         print(f"[c5 C={cascades}] step {st['train_steps']}: {R} rays, {out['samples']} samples, loss "
               f"{out['loss']:.5f} (gpu {out['loss_gpu']:.5f}), {out['touched']} table entries "
-              f"({out['cancelled']} cancelled)"
+              f"({out['ill_conditioned']} ill-conditioned)"
               + (f", refresh: {occupied} occupied cells" if refresh else ""), flush=True)
         assert abs(out["loss_gpu"] - out["loss"]) <= 1e-4 * out["loss"] + 1e-7
         first += R

@@ -52,16 +52,20 @@ def bits(a):
     return a.view(np.uint16 if a.dtype == np.float16 else np.uint32)
 
 
-@pytest.mark.parametrize("T_,L,b,N,steps,flags", [(1 << 14, 16, 1.447, 1 << 16, 3, False),
-                                                  (1 << 19, 16, 1.3819, 3001, 2, False),
-                                                  (1 << 19, 16, 1.3819, 1 << 17, 2, False),
-                                                  (1 << 12, 8, 2.0, 777, 2, False),
-                                                  (1 << 19, 16, 1.3819, 1 << 17, 2, True),
-                                                  (1 << 14, 16, 1.447, 3001, 2, True)])
-def test_fused_table_update_equals_scatter_then_step(dev, T_, L, b, N, steps, flags):
+@pytest.mark.parametrize("T_,L,b,N,steps,flags,skew", [(1 << 14, 16, 1.447, 1 << 16, 3, False, False),
+                                                       (1 << 19, 16, 1.3819, 3001, 2, False, False),
+                                                       (1 << 19, 16, 1.3819, 1 << 17, 2, False, False),
+                                                       (1 << 12, 8, 2.0, 777, 2, False, False),
+                                                       (1 << 19, 16, 1.3819, 1 << 17, 2, True, False),
+                                                       (1 << 14, 16, 1.447, 3001, 2, True, False),
+                                                       (1 << 14, 16, 1.447, 1 << 16, 2, False, True),
+                                                       (1 << 19, 16, 1.3819, 1 << 17, 2, False, True)])
+def test_fused_table_update_equals_scatter_then_step(dev, T_, L, b, N, steps, flags, skew):
     """flags: whole 16-row tiles of dx are +-0 and flagged dead (the dX kernel's tile flags): skipped rows,
-    same table."""
-    print(f"[scatter adam] T={T_} L={L} N={N} flags={flags}", flush=True)
+    same table.  skew: dx spread over seven decades with one row at 60000 (every level's quantum set by it)
+    and half the samples clustered (bins of several chunks): most sums are summed again at their own
+    scale, in the fused update as in the stored path."""
+    print(f"[scatter adam] T={T_} L={L} N={N} flags={flags} skew={skew}", flush=True)
     P = pkg()
     ga, gb = make_grid(T_, L, b, N, 5), make_grid(T_, L, b, N, 5)
     n = L * T_ * 2
@@ -74,6 +78,10 @@ def test_fused_table_update_equals_scatter_then_step(dev, T_, L, b, N, steps, fl
         pos[:32, :3] = rng.choice(np.float32([0.0, 1.0, 0.5, np.nextafter(np.float32(1), 0)]), (32, 3))
         dx = rng.normal(0, 0.5, (N, 2 * L)).astype(np.float16)
         dx[rng.random((N, 2 * L)) < 0.3] = 0  # zero gradients: entries no product reaches
+        if skew:
+            pos[: N // 2, :3] = (0.5 + 0.02 * rng.normal(size=(N // 2, 3))).clip(0, 1)
+            dx = (dx.astype(np.float32) * 10.0 ** rng.uniform(-7, 0, (N, 1))).astype(np.float16)
+            dx[N // 3] = np.float16(60000.0)
         if step == steps - 1 and N > 40:
             dx[5, 0], dx[17, 3], dx[33, 2 * L - 1] = np.inf, -np.inf, np.nan
         live = None

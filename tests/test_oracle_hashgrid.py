@@ -193,3 +193,24 @@ def test_scatter_clamp_differs_at_seam():
     N = int(res[0])
     assert idx[0, 0, 0] == orc.dense_index(N - 1, N - 1, N - 1, N) * 2
     assert w[0, 0, 0] == 1.0
+
+
+@pytest.mark.parametrize("T,b,L", [(1 << 10, 1.5, 4), (T14, 1.447, 16)])
+def test_scatter_stats_sums_magnitudes_and_counts(T, b, L):
+    """hash_scatter_stats: its sums are hash_scatter's bit for bit, its magnitudes are the scatter of |g|
+    (the corner weights are non-negative), and its counts are a bincount of the backward corner indices
+    (two words per corner, zero products included)."""
+    rng = np.random.default_rng(23)
+    N = 3000
+    pos = rng.random((N, 3)).astype(np.float32)
+    pos[:16] = rng.choice(np.float32([0.0, 1.0, 0.5]), (16, 3))
+    g = rng.standard_normal((N, 2 * L)).astype(np.float16)
+    g[rng.random((N, 2 * L)) < 0.2] = 0
+    s, sa, cnt = orc.hash_scatter_stats(pos, g, T, L, 16, b)
+    np.testing.assert_array_equal(s.view(np.uint32), orc.hash_scatter(pos, g, T, L, 16, b).view(np.uint32))
+    np.testing.assert_array_equal(sa.view(np.uint32), orc.hash_scatter(pos, np.abs(g), T, L, 16, b).view(np.uint32))
+    idx, w = orc.hash_corners(pos, T, L, 16, b, bwd_clamp=True)
+    assert (w >= 0).all()
+    want = np.bincount(idx.ravel().astype(np.int64), minlength=L * T * 2)
+    want[1:] += np.bincount(idx.ravel().astype(np.int64) + 1, minlength=L * T * 2)[1:L * T * 2]
+    np.testing.assert_array_equal(cnt, want[:L * T * 2])
