@@ -755,11 +755,19 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         // gradient array).  The update waits for a refresh of this step, which
         // reads the table.
         const bool fused_table = db.scatter_plan != nullptr;
+        // Profiling: the wait for the refresh comes before the stage's timer
+        // (then the whole scatter waits, not only its update), so that the
+        // stage times the scatter's kernels and not the refresh beside them.
+        hipEvent_t update_wait = refresh ? b.ev_join : nullptr;
+        if (o.isProfiling && update_wait) {
+            GRAFT_HIP_CHECK(hipStreamWaitEvent(stream, update_wait, 0));
+            update_wait = nullptr;
+        }
         stage("hashScatter", [&] {
             if (fused_table)
                 m_densityMLP->scatterAdamTable(db.dx_out, reinterpret_cast<const float*>(S.positions), 4, (int)Bn,
                                                d_hits, o.learningRate, o.beta1, o.beta2, o.epsilon, o.lossScale,
-                                               stream, refresh ? b.ev_join : nullptr, heads ? b.tile_live : nullptr);
+                                               stream, update_wait, heads ? b.tile_live : nullptr);
             else
                 // the table gradient is all zero here: the previous step's
                 // Adam cleared every entry it consumed

@@ -59,6 +59,10 @@ L, F, TBL, BASE, GROWTH = 16, 2, 1 << 19, 16, 1.3819
 LR_MAX, LR_MIN, ANNEAL = 1e-2, 1e-4, 2000
 C5_SEEDS = (1, 2, 3, 4, 5)    # further background-draw seeds of the 5-cascade run
 PRETRAIN_STEPS = 256           # optimizer steps before the warm-up (past the early occupancy phase)
+# The per-stage HIP-event window (the roofline's kernel times) and a steady-state window of whole refresh
+# periods, run after the timed steps: fixed so that the committed kernel trace covers the same steps
+# (rocprofv3 ... bench.py --warmup 384 --profile-steps 64: steps 640 .. 703).
+PROFILE_FROM, PROFILE_STEPS, STEADY_STEPS = 640, 64, 64
 CPU_FEED_CHUNKS = 8            # feed chunks of rays available to the CPU-oracle leg (stops after ~10 s)
 
 # Algorithmic counts per unit.
@@ -70,6 +74,17 @@ MLP_FLOP_PER_SAMPLE = 3 * (2 * (32 * 64 + 64 * 16) + 2 * (32 * 64 + 64 * 64 + 64
 HEADS_FLOP_PER_SAMPLE = MLP_FLOP_PER_SAMPLE - 2 * 16 * 64
 COPY_BYTES = 256 << 20         # copy-calibration kernel of the PMC runs (read and write each)
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+MFMA_FILE = os.path.join(ROOT, "profiles", "mfma_counters.json")
+L2_FILE = os.path.join(ROOT, "profiles", "encode_l2_requests.json")
+
+
+def profile_json(path):
+    """A committed counter summary (profiles/*.json), or None."""
+    try:
+        with open(path) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return None
 
 
 def measured_traffic(kernel):
@@ -298,12 +313,29 @@ class Trainer:
         return hits
 
 
-def cpu_baseline(P, nerf, o, d, gt, min_seconds=10.0, max_steps=64):
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(P, nerf, chunks, min_seconds=10.0, max_steps=64):
     """The C oracle on the host cores: full training steps of up to BATCH compacted
     samples each, chained (each step marches the next rays and trains the
-    parameters the previous step updated), until min_seconds have passed."""
+    parameters the previous step updated), until min_seconds have passed.
+    chunks: (o, d, rgb, background) per feed chunk, each composited over its own
+    random background as the GPU run's feed draws them; a step's rays stay in
+    one chunk and composite over its background."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import pyoracle as orc
+    bounds = np.cumsum([0] + [c[0].shape[0] for c in chunks])
+    o, d, gt = (np.concatenate([c[k] for c in chunks]) for k in range(3))
     bits = nerf.occupancy()
     casc = int(nerf.opts.numCascades)
     mn, mx = np.float32([-1.5] * 3), np.float32([1.5] * 3)
@@ -322,7 +354,10 @@ def cpu_baseline(P, nerf, o, d, gt, min_seconds=10.0, max_steps=64):
     ray0, steps, samples = 0, 0, 0
     t0 = time.perf_counter()
     while steps < max_steps and ray0 < len(o) and (steps == 0 or time.perf_counter() - t0 < min_seconds):
-        oo, dd, gg = o[ray0:ray0 + window], d[ray0:ray0 + window], gt[ray0:ray0 + window]
+        ci = int(np.searchsorted(bounds, ray0, side="right")) - 1
+        end = min(ray0 + window, int(bounds[ci + 1]))
+        bg = np.asarray(chunks[ci][3], np.float32)
+        oo, dd, gg = o[ray0:end], d[ray0:end], gt[ray0:end]
         di, nr, fr = orc.ray_aabb_inv(oo, dd, mn, mx, casc)
         m = orc.march_hits(oo, dd, di, nr, fr, bits, [128] * 3, mn, mx, casc, 4, 1, BATCH)
         N, act = m["total"], m["active"]
@@ -332,8 +367,7 @@ def cpu_baseline(P, nerf, o, d, gt, min_seconds=10.0, max_steps=64):
         cin, sig = orc.sh_gather(dd, m["ray_idx"], dout, 0.0)
         cout, cacts = orc.mlp_forward(cin, cW16, cB, 32, 64, 8, 3, out_act=1)
         rgb = np.ascontiguousarray(cout[:, :3])
-        comp = orc.composite(m["offsets"][:act], m["counts"][:act], m["t"], sig, rgb, gg[:act], 0.1,
-                             np.float32([1, 1, 1]))
+        comp = orc.composite(m["offsets"][:act], m["counts"][:act], m["t"], sig, rgb, gg[:act], 0.1, bg)
         cg, ds = orc.color_grad(m["counts"][:act], m["offsets"][:act], m["t"], dout, rgb, comp["phi"], comp["rgb"],
                                 comp["dw"], comp["weight_sum"], 128.0, 0.0, RAYS_PER_CALL)
         cgp = np.zeros((N, 8), np.float16)
@@ -351,9 +385,101 @@ def cpu_baseline(P, nerf, o, d, gt, min_seconds=10.0, max_steps=64):
         samples += N
     dt = time.perf_counter() - t0
     return {"value": round(samples / dt, 1), "unit": "samples/s", "cores": orc.num_threads(), "kind": "port",
+            "cpu_model": cpu_model(),
             "sample": f"{steps} chained full training steps (march, encode, both MLPs fwd/bwd, compositing, "
                       f"gradients, scatter, Adam over all 16.8 M table entries) on {ray0} feed rays = "
-                      f"{samples} compacted samples, same scene and model state as the GPU run, {dt:.1f} s"}
+                      f"{samples} compacted samples, same scene and model state as the GPU run, a random "
+                      f"background per 2^16-ray chunk as the GPU run's feed, {dt:.1f} s"}
+
+
+def cpu_components(gpu):
+    """BASELINE configs[0]-[3] on the oracle, each at its full shape: median of 5 runs after 1 warm-up
+    (time.perf_counter), beside the GPU's time of the same component from `gpu` (the components leg)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle as orc
+    scenes = importlib.import_module("3dmaker_amd.scenes")
+    rng = np.random.default_rng(7)
+    b1 = (2048 / 16) ** (1 / 15)
+
+    def med(fn, reps=5):
+        fn()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts)) * 1e3
+
+    rows = {}
+    # configs[0]: N = 4096, T = 2^14, b = 1.447: encode, density MLP forward, MSE, backward, scatter, Adam
+    n0, t0_ = 4096, 1 << 14
+    p0 = rng.random((n0, 3), dtype=np.float32)
+    tab0 = rng.uniform(-1e-4, 1e-4, L * t0_ * F).astype(np.float32)
+    w0 = np.concatenate([rng.uniform(-a, a, k) for a, k in ((math.sqrt(6 / 96), 64 * 32), (math.sqrt(6 / 80), 16 * 64))])
+    w0 = w0.astype(np.float32)
+    bias0 = np.zeros(80, np.float32)
+    tgt0 = rng.random((n0, 16)).astype(np.float16)
+    st0 = [np.zeros_like(tab0), np.zeros_like(tab0), np.zeros_like(w0), np.zeros_like(w0),
+           np.zeros_like(bias0), np.zeros_like(bias0)]
+
+    def c1_step():
+        enc = orc.hash_encode(p0, tab0.astype(np.float16), t0_, L, BASE, 1.447)
+        y, acts = orc.mlp_forward(enc, w0.astype(np.float16), bias0, 32, 64, 16, 2)
+        _, dy = orc.mse_loss_grad(y, tgt0, 16, 128.0)
+        gw, gb, dx = orc.mlp_backward(dy, enc, acts, w0.astype(np.float16), 32, 64, 16, 2)
+        g = orc.hash_scatter(p0, dx, t0_, L, BASE, 1.447)
+        bc1, bc2 = orc.adam_bias_corrections(0.9, 0.99, 1)
+        orc.adam_hash(tab0, g, st0[0], st0[1], 1e-2, 0.9, 0.99, 1e-15, bc1, bc2, 1 / 128.0, want_f16=False)
+        orc.adam_dense(w0, gw, st0[2], st0[3], 1e-2, 0.9, 0.99, 1e-15, bc1, bc2, 1 / 128.0)
+        orc.adam_dense(bias0, gb, st0[4], st0[5], 1e-2, 0.9, 0.99, 1e-15, bc1, bc2, 1 / 128.0)
+
+    rows["c1_train_step_4096_ms"] = med(c1_step)
+    # configs[1]: encode and scatter at 2^18 and 2^20, T = 2^19
+    tab = rng.uniform(-1e-4, 1e-4, L * TBL * F).astype(np.float16)
+    for tag, n in (("2p18", 1 << 18), ("2p20", 1 << 20)):
+        pos = rng.random((n, 3), dtype=np.float32)
+        denc = rng.normal(0, 1, (n, 2 * L)).astype(np.float16)
+        rows[f"c2_encode_{tag}_ms"] = med(lambda: orc.hash_encode(pos, tab, TBL, L, BASE, b1))
+        rows[f"c2_scatter_{tag}_ms"] = med(lambda: orc.hash_scatter(pos, denc, TBL, L, BASE, b1))
+    # configs[2]: both heads forward + backward at 2^18 (N(0,1) density inputs, SH of unit directions)
+    n2 = BATCH
+    x = rng.normal(0, 1, (n2, 32)).astype(np.float16)
+    dirs = rng.normal(size=(n2, 3)).astype(np.float32)
+    dirs /= np.linalg.norm(dirs, axis=1, keepdims=True)
+    wd = (rng.normal(0, 0.1, 64 * 32 + 16 * 64)).astype(np.float16)
+    bd = np.zeros(80, np.float32)
+    wc = (rng.normal(0, 0.1, 64 * 32 + 64 * 64 + 8 * 64)).astype(np.float16)
+    bc = np.zeros(136, np.float32)
+    ridx = np.arange(n2, dtype=np.uint32)
+    cdy = rng.normal(0, 1, (n2, 8)).astype(np.float16)
+    cdy[:, 3:] = 0
+
+    def heads():
+        dout, dacts = orc.mlp_forward(x, wd, bd, 32, 64, 16, 2)
+        cin, sig = orc.sh_gather(dirs, ridx, dout, 0.0)
+        cout, cacts = orc.mlp_forward(cin, wc, bc, 32, 64, 8, 3, out_act=1)
+        _, _, cdx = orc.mlp_backward(cdy, cin, cacts, wc, 32, 64, 8, 3)
+        dg = orc.density_grad(np.zeros(n2, np.float32), cdx)
+        orc.mlp_backward(dg, x, dacts, wd, 32, 64, 16, 2)
+
+    rows["c3_heads_fwd_bwd_2p18_ms"] = med(heads)
+    # configs[3]: DDA march + compaction of 2^18 camera rays over the 128^3 x 5 Bernoulli grid
+    bits = scenes.occupancy_c4(128, 5, 4, 0.1, 0.3, 1.5, seed=0)
+    o4, d4 = scenes.rays_c4(1 << 18, n_cams=100, seed=1)
+    mn, mx = np.float32([-1.5] * 3), np.float32([1.5] * 3)
+
+    def march():
+        di, nr, fr = orc.ray_aabb_inv(o4, d4, mn, mx, 5)
+        orc.march_hits(o4, d4, di, nr, fr, bits, [128] * 3, mn, mx, 5, 4, 1, BATCH)
+
+    rows["c4_march_2p18_rays_ms"] = med(march)
+    rows = {k: round(v, 2) for k, v in rows.items()}
+    pairs = {"c2_encode_2p18_ms": "hash_encode_ms_2p18", "c2_encode_2p20_ms": "hash_encode_ms_2p20",
+             "c2_scatter_2p18_ms": "hash_scatter_ms_2p18", "c3_heads_fwd_bwd_2p18_ms": "mlp_fwd_bwd_ms_2p18",
+             "c4_march_2p18_rays_ms": "march_compact_ms_2p18_rays"}
+    speedup = {k: round(rows[k] / gpu[g], 1) for k, g in pairs.items() if gpu.get(g)}
+    return {"components_ms": rows, "component_timing": "median of 5 runs after 1 warm-up, oracle at full shape",
+            "gpu_speedup": speedup}
 
 
 def heldout_psnr(P, torch, nerf, feed, sp):
@@ -734,10 +860,17 @@ def main():
     samples = int(np.sum(hits, dtype=np.int64))
     ms_step = wall * 1e3 / steps
 
-    # Per-stage HIP-event timings on the launch stream over a further profiled window.
+    # Untimed up to the fixed profiling window, then per-stage HIP-event timings on the launch stream over it
+    # (the library waits for a refresh before the scatter stage while profiling, so the stage times its
+    # kernels), then a steady-state window of whole refresh periods (timed, no events).
+    start = max(PROFILE_FROM, -(-tr.step // 16) * 16)
+    if tr.step < start:
+        tr.run(start - tr.step)
+    torch.cuda.synchronize()
+    prof_from = tr.step
     nerf.set_profiling(True)
     nerf.reset_stats()
-    prof_hits = tr.run(64)
+    prof_hits = tr.run(PROFILE_STEPS)
     torch.cuda.synchronize()
     nerf.set_profiling(False)
     st = nerf.stats()
@@ -745,6 +878,17 @@ def main():
     stage_ms = {k: round(v[0], 4) for k, v in st.items()}
     # per training step: mean per call x calls / steps (march and occupancy run less than once a step)
     stage_ms_per_step = {k: round(v[0] * v[1] / len(prof_hits), 4) for k, v in st.items()}
+    steady_from = tr.step
+    t1 = time.perf_counter()
+    steady_hits = tr.run(STEADY_STEPS)
+    torch.cuda.synchronize()
+    steady_wall = time.perf_counter() - t1
+    steady = {"window": [steady_from, steady_from + len(steady_hits)],
+              "refreshes": sum(1 for k in range(steady_from, steady_from + len(steady_hits)) if k % 16 == 0),
+              "ms_per_step": round(steady_wall * 1e3 / len(steady_hits), 4),
+              "samples_per_s": round(float(np.sum(steady_hits)) / steady_wall, 1),
+              "mean_samples_per_step": round(float(np.mean(steady_hits)), 1)}
+    timed_refreshes = sum(1 for k in range(timed_from, timed_from + steps) if k % 16 == 0)
 
     # roofline of the dominant stage of the step (per-call averages of the profiled window, HIP events on
     # the stream each stage runs on)
@@ -761,12 +905,14 @@ def main():
     ach = algo / (dom_ms * 1e-3) / 1e9
     roofline = {"bound": bound, "kernel": dom, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom),
-                "algorithmic_bytes_per_launch": int(algo), "avg_launch_ms": round(dom_ms, 4)}
+                "algorithmic_bytes_per_launch": int(algo), "avg_launch_ms": round(dom_ms, 4),
+                "window": [prof_from, prof_from + len(prof_hits)], "mean_samples": round(n_prof, 1)}
     # MLP stages: the heads' forward (the encode is a stage of its own with the 16x16x32 heads), the dX
     # chains (main stream) and the weight gradients (side stream, beside the scatter)
     mlp_ms = sum(st[k][0] for k in ("forward", "backwardDx", "colorDx", "densityDx", "colorBwd", "densityBwd",
                                     "headsBwd") if k in st)
     mfma_util = MLP_FLOP_PER_SAMPLE * n_prof / (mlp_ms * 1e-3) / 1e12 / FP16_PEAK_TFLOPS if mlp_ms else None
+    mc = profile_json(MFMA_FILE)
 
     out = {
         "metric": "training samples/sec (full NeRF training step, <= 2^18 compacted samples/step)",
@@ -793,6 +939,13 @@ def main():
         "forward_samples_per_s": round(n_prof / ((st["forward"][0] + st.get("encode", (0.0,))[0]) * 1e-3), 1)
         if "forward" in st else None,
         "mfma_util": round(mfma_util, 5) if mfma_util else None,
+        # the heads kernels' MFMA flop by counter (SQ_INSTS_VALU_MFMA_MOPS_F16 x 512, every MFMA issued) over
+        # their durations, from the committed counter passes: the step's window and the stand-alone 2^18 run
+        "mfma_util_counters": {"step_heads": mc["step"]["mfma_util_all_heads"],
+                               "standalone_heads_2p18": mc["components"]["mfma_util_heads"],
+                               "source": mc["source"]} if mc else None,
+        "timed_refreshes": timed_refreshes,
+        "steady_state": steady,
         "roofline": roofline,
     }
     # finish the cosine schedule (untimed), then PSNR on 12 held-out views
@@ -807,14 +960,16 @@ def main():
         del hfeed, himgs
     out["components"] = components(P, torch, stream, sp)
     if not args.no_cpu:
+        # the feed as the GPU run draws it: a random background per chunk, composited at fetch time
+        crng = np.random.default_rng(12345)
         chunks = []
         for k in range(CPU_FEED_CHUNKS):
-            feed.fetch(k * RAYS_PER_CALL, RAYS_PER_CALL, 12345, (1.0, 1.0, 1.0), sp)
+            bg = crng.random(3)
+            feed.fetch(k * RAYS_PER_CALL, RAYS_PER_CALL, 12345, bg, sp)
             torch.cuda.synchronize()
-            chunks.append((feed.o.cpu().numpy(), feed.d.cpu().numpy(), feed.rgb.cpu().numpy()))
-        nerf.set_bg_color(1.0, 1.0, 1.0)
-        o_h, d_h, g_h = (np.concatenate(c) for c in zip(*chunks))
-        out["cpu_baseline"] = cpu_baseline(P, nerf, o_h, d_h, g_h)
+            chunks.append((feed.o.cpu().numpy(), feed.d.cpu().numpy(), feed.rgb.cpu().numpy(), bg))
+        out["cpu_baseline"] = cpu_baseline(P, nerf, chunks)
+        out["cpu_baseline"].update(cpu_components(out["components"]))
     print(json.dumps(out))
 
 
