@@ -251,6 +251,8 @@ SIGNATURES = {
     "ntr_render_train_view": (_i, [_vp, _i, _i, _i, _vp]),
     "ntr_num_train_views": (_i, [_vp]),
     "ntr_step": (_i, [_vp]),
+    "ntr_num_cascades": (_i, [_vp]),
+    "ntr_estimate_num_cascades": (_i, [_vp, _i]),
     "tmlp_version": (C.c_char_p, []),
 }
 
@@ -697,3 +699,13 @@ class NerfTrainer:
 
     def step(self) -> int:
         return self._L.ntr_step(self.h)
+
+    def num_cascades(self) -> int:
+        return self._L.ntr_num_cascades(self.h)
+
+
+def estimate_num_cascades(transforms) -> int:
+    """DataLoader::getNumCascades on float32 [n, 16] row-major camera-to-world matrices (host only)."""
+    import numpy as np
+    tf = np.ascontiguousarray(transforms, np.float32).reshape(-1, 16)
+    return lib().ntr_estimate_num_cascades(tf.ctypes.data, tf.shape[0])

@@ -81,6 +81,83 @@ void DataLoader::getSceneOrientation(float3& center, float3& up) const
     up = len > 0 ? make_float3(ux / len, uy / len, uz / len) : make_float3(0, 0, 1);
 }
 
+namespace {
+
+double det3x3(const double (&m)[3][3])
+{
+    return m[0][0] * (m[1][1] * m[2][2] - m[1][2] * m[2][1]) - m[0][1] * (m[1][0] * m[2][2] - m[1][2] * m[2][0]) +
+           m[0][2] * (m[1][0] * m[2][1] - m[1][1] * m[2][0]);
+}
+
+float norm3f(float x, float y, float z) { return std::sqrt(x * x + y * y + z * z); }
+
+}  // namespace
+
+// DataLoader.cu:213-271 (the regime signals) and 367-377 (the estimate), with
+// the reference's precisions: view directions and the inwardness mean in
+// fp32, the normal equations in fp64.
+int DataLoader::estimateNumCascades(const float* tf, int n)
+{
+    if (!tf || n < 4) return 1;
+    std::vector<float3> dir((size_t)n), eye((size_t)n);
+    float3 mean_eye = make_float3(0, 0, 0);
+    // normal equations of the point nearest to every view ray:
+    // sum_i (I - f_i f_i^T) p = sum_i (I - f_i f_i^T) c_i
+    double A[3][3] = {{0, 0, 0}, {0, 0, 0}, {0, 0, 0}}, rhs[3] = {0, 0, 0};
+    for (int i = 0; i < n; i++) {
+        const float* m = tf + (size_t)i * 16;
+        float3 f = make_float3(-m[2], -m[6], -m[10]);  // the camera looks down its -z column
+        const float len = norm3f(f.x, f.y, f.z);
+        if (len > 1e-8f) f = make_float3(f.x / len, f.y / len, f.z / len);
+        const float3 c = make_float3(m[3], m[7], m[11]);
+        dir[(size_t)i] = f;
+        eye[(size_t)i] = c;
+        mean_eye = make_float3(mean_eye.x + c.x, mean_eye.y + c.y, mean_eye.z + c.z);
+        const double fv[3] = {f.x, f.y, f.z}, cv[3] = {c.x, c.y, c.z};
+        for (int r = 0; r < 3; r++)
+            for (int k = 0; k < 3; k++) {
+                const double a = (r == k ? 1.0 : 0.0) - fv[r] * fv[k];
+                A[r][k] += a;
+                rhs[r] += a * cv[k];
+            }
+    }
+    mean_eye = make_float3(mean_eye.x / n, mean_eye.y / n, mean_eye.z / n);
+    // (sum_i (I - f_i f_i^T)) / n loses an eigenvalue when the view directions
+    // are parallel: a determinant below 0.02 (about 0.3 for spread directions)
+    double An[3][3];
+    for (int r = 0; r < 3; r++)
+        for (int k = 0; k < 3; k++) An[r][k] = A[r][k] / n;
+    const bool parallel = std::fabs(det3x3(An)) < 0.02;
+    float3 p = mean_eye;  // where the rays do not converge: the mean camera position
+    const double d = det3x3(A);
+    if (!parallel && std::fabs(d) >= 1e-12) {
+        double x[3];
+        for (int col = 0; col < 3; col++) {  // Cramer's rule
+            double Ac[3][3];
+            for (int r = 0; r < 3; r++)
+                for (int k = 0; k < 3; k++) Ac[r][k] = k == col ? rhs[r] : A[r][k];
+            x[col] = det3x3(Ac) / d;
+        }
+        p = make_float3((float)x[0], (float)x[1], (float)x[2]);
+    }
+    // mean cosine between each view direction and the direction to p
+    float inward = 0.0f;
+    for (int i = 0; i < n; i++) {
+        float gx = p.x - eye[(size_t)i].x, gy = p.y - eye[(size_t)i].y, gz = p.z - eye[(size_t)i].z;
+        const float gl = norm3f(gx, gy, gz);
+        if (gl > 1e-8f) {
+            gx /= gl;
+            gy /= gl;
+            gz /= gl;
+        }
+        inward += dir[(size_t)i].x * gx + dir[(size_t)i].y * gy + dir[(size_t)i].z * gz;
+    }
+    inward /= (float)n;
+    if (parallel && std::fabs(inward) < 0.3f) return 4;  // forward-facing
+    if (inward < -0.3f) return 3;                         // outward panorama
+    return 1;                                             // bounded
+}
+
 void DataLoader::freeVRAM()
 {
     dfree(d_images_rgba);

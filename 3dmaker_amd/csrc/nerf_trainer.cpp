@@ -147,6 +147,9 @@ void INerfTrainer::loadDataset(const uint8_t* host_rgba, const float* host_trans
     m_dataloader = new DataLoader(host_rgba, host_transforms, numImages, width, height, focal,
                                   (uint32_t)m_masterConfig.rayChunkSize, true, m_config.depthFraction);
     m_total_rays = m_dataloader->getTotalRays();
+    // NerfTrainer.cu:113-114: numCascades 0 takes the loader's pose estimate
+    // (before the model exists; a model built by an earlier call keeps its grid)
+    if (m_config.numCascades <= 0) m_masterConfig.numCascades = std::max(1, m_dataloader->getNumCascades());
     buildModel();
     float3 c, up;
     m_dataloader->getSceneOrientation(c, up);

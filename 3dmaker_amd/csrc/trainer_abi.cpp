@@ -1,4 +1,5 @@
 // Flat C handle API over INerfTrainer (include/trainer_capi.h).
+#include "DataLoader.h"
 #include "NerfTrainer.h"
 #include "abi_error.h"
 #include "trainer_capi.h"
@@ -140,5 +141,10 @@ int ntr_render_train_view(Ntr* h, int index, int width, int height, float* host_
 }
 int ntr_num_train_views(Ntr* h) { return h ? h->t.numTrainViews() : 0; }
 int ntr_step(Ntr* h) { return h ? h->t.step() : 0; }
+int ntr_num_cascades(Ntr* h) { return h ? h->t.numCascades() : 0; }
+int ntr_estimate_num_cascades(const float* host_transforms, int n)
+{
+    return DataLoader::estimateNumCascades(host_transforms, n);
+}
 
 }  // extern "C"

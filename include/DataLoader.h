@@ -68,6 +68,16 @@ public:
     void getFramePose(int i, float out[16]) const;
     // DataLoader.h:49-68: mean camera position and normalised mean camera up axis.
     void getSceneOrientation(float3& center, float3& up) const;
+    // DataLoader.h:70: occupancy cascades for this pose set, from the
+    // reference's pose-only heuristic (DataLoader.cu:213-271, 367-377); see
+    // estimateNumCascades.
+    int getNumCascades() const { return estimateNumCascades(h_transforms.data(), num_images); }
+    // The heuristic on n row-major camera-to-world matrices: 4 where the view
+    // directions are (nearly) parallel and neither converge nor diverge
+    // (forward-facing), 3 where the cameras look away from the point their
+    // view rays pass closest to (outward panorama), else 1 (bounded: orbit or
+    // nadir).  Fewer than 4 poses: 1, the reference loader's default.
+    static int estimateNumCascades(const float* transforms, int n);
 
 private:
     int width = 0, height = 0, num_images = 0;

@@ -68,7 +68,8 @@ public:
     void loadDataset(const std::string& path);
     // The dataset in memory: numImages RGBA8 images (host, [n][h][w][4]) and
     // camera-to-world matrices (host, [n][16] row-major), focal in pixels.
-    // numCascades 0 in the config selects 1 cascade.
+    // numCascades 0 in the config takes the loader's estimate from the poses
+    // (DataLoader::getNumCascades), as NerfTrainer.cu:113-114 does.
     void loadDataset(const uint8_t* host_rgba, const float* host_transforms, int numImages, int width, int height,
                      float focal);
 
@@ -103,6 +104,7 @@ public:
 
     // ---- additions (no reference counterpart) ----
     InstantNerf* nerf() { return m_nerf; }
+    int numCascades() const { return m_masterConfig.numCascades; }
     DataLoader* dataloader() { return m_dataloader; }
 
 private:

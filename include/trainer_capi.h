@@ -53,6 +53,12 @@ int ntr_render_orbit(Ntr* h, float azimuth_deg, float elevation_deg, float radiu
 int ntr_render_train_view(Ntr* h, int index, int width, int height, float* host_rgb);
 int ntr_num_train_views(Ntr* h);
 int ntr_step(Ntr* h);
+/* Occupancy cascades of the trainer's model (its config's, or the loader's
+ * estimate when the config asks for 0). */
+int ntr_num_cascades(Ntr* h);
+/* DataLoader::getNumCascades (DataLoader.h:70) on n row-major camera-to-world
+ * matrices, without a loader or a GPU: 1, 3 or 4. */
+int ntr_estimate_num_cascades(const float* host_transforms, int n);
 
 #ifdef __cplusplus
 }

@@ -66,3 +66,23 @@ def test_trainer_loop_validate_save_load_render(dev, tmp_path):
     assert tr2.train_steps(1).step == 0  # no dataset on the loaded trainer: nothing to train (as the reference)
     tr.close()
     tr2.close()
+
+
+@pytest.mark.parametrize("kind,want", [("orbit", 1), ("forward", 4)])
+def test_trainer_takes_the_loaders_cascade_estimate(dev, kind, want):
+    # numCascades 0: the model is built with the loader's pose estimate (NerfTrainer.cu:113-114)
+    P = pkg()
+    n, W, H = 12, 16, 16
+    if kind == "orbit":
+        tf = np.asarray(scenes.cameras(n, 1.5, seed=3), np.float32).reshape(n, 16)
+    else:
+        tf = np.tile(np.eye(4, dtype=np.float32).reshape(16), (n, 1))
+        tf[:, 3] = np.linspace(-1.0, 1.0, n)   # a row of parallel cameras looking down -z
+        tf[:, 11] = 2.0
+    rgba = np.full((n, H, W, 4), 255, np.uint8)
+    cfg = P.NerfTrainer.default_config()
+    cfg.numCascades, cfg.batchSize, cfg.renderBatchSize = 0, 1 << 14, 1 << 14
+    tr = P.NerfTrainer(cfg)
+    tr.load_dataset(rgba, tf, scenes.focal_from_fov(W, 50.0))
+    assert tr.num_cascades() == want == P.estimate_num_cascades(tf)
+    tr.close()
