@@ -17,13 +17,16 @@
 //              {x0 slot | x1 slot << 16, (g0, g1) as fp16, w of the x0 corner,
 //              w of the x1 corner} written at its bin's cursor (bin base +
 //              round prefix + LDS rank); workgroup 0 also writes the chunk
-//              table (<= kChunk records per chunk).  The weights are the
-//              reference's products (wx * wy) * wz, so every product g * w is
-//              the reference's fp32 product bit for bit;
+//              table (bins of more than kSplit records cut into chunks of
+//              kChunk) and the list of bins of several chunks.  The weights are the reference's products
+//              (wx * wy) * wz, so every product g * w is the reference's fp32
+//              product bit for bit;
 //  accumulate  per chunk: the slice's sums in LDS as int64 fixed point
-//              (ds_add_u64), then one store per table entry.  A bin of several
-//              chunks adds its partial sums into an int64 staging slice with
-//              global 64-bit atomics, and its last chunk converts the slice.
+//              (ds_add_u64), then one store per table entry.  A chunk of a
+//              bin of several stores its sums as an int64 partial slice
+//              instead;
+//  merge       per bin of several chunks: the sum of its partial slices, then
+//              the same stores.
 //              The training step's variant applies Adam to every entry the
 //              sums reach instead of storing a gradient (the table half of
 //              the optimizer step, optimizerKernel.cu:16-167, fused in): the
@@ -80,7 +83,15 @@ constexpr int kSliceShift = 12;
 constexpr int kBinThreads = 512;
 constexpr int kSamplesPerThread = 1;
 constexpr int kRound = kBinThreads * kSamplesPerThread;
-constexpr uint32_t kChunk = 32768;  // records per accumulate workgroup
+// Accumulate chunks: a bin of more than kSplit records is cut into chunks of
+// kChunk records, summed by as many workgroups and merged after (the heaviest
+// bins, those of the coarse dense levels in a training step, then run on many
+// CUs at once); other bins are one chunk each.  The allocation-free entry
+// point splits bins of more than kChunkNoAlloc records into chunks of that
+// size (fewer partial slices).
+constexpr uint32_t kChunk = 8192;
+constexpr uint32_t kSplit = 3 * kChunk;
+constexpr uint32_t kChunkNoAlloc = 32768;
 constexpr int kMaxBins = 8192;
 constexpr int kDenseBins = 64;  // target bins per dense level
 // word offset of a dense slice's finer sums (a dense slice holds at most
@@ -95,6 +106,8 @@ struct ScatterArgs {
     const uint32_t* tile_live;
     int L, T, dense_start, pos_stride, N, bins, rounds;
     uint32_t mask;
+    uint32_t chunk;  // records per accumulate chunk of a split bin
+    uint32_t split;  // bins of more records are split into chunks
     float scale[kMaxLevels];
     int res[kMaxLevels];
     int bin_base[kMaxLevels + 1];   // bins of level l: [bin_base[l], bin_base[l + 1])
@@ -350,30 +363,32 @@ __global__ __launch_bounds__(kPrefixThreads) void scatter_prefix_kernel(const Sc
 // Exclusive prefix sum of in[0, n) into out[0, n) (in == out allowed: every
 // thread reads and writes only its own segment); returns the total.  Every
 // thread of the kBinThreads-thread block calls it; wsum is kBinThreads / 64
-// words of LDS.
-__device__ uint32_t block_exclusive_scan(const uint32_t* in, uint32_t* out, int n, uint32_t* wsum)
+// words of LDS.  T: uint32_t, or uint64_t for several counters packed in
+// bit fields that cannot carry into each other.
+template <class T>
+__device__ T block_exclusive_scan(const T* in, T* out, int n, T* wsum)
 {
     constexpr int kWaves = kBinThreads / 64;
     const int per = (n + kBinThreads - 1) / kBinThreads;
     const int b0 = min(n, (int)threadIdx.x * per), b1 = min(n, b0 + per);
-    uint32_t s = 0;
+    T s = 0;
     for (int i = b0; i < b1; i++) s += in[i];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    uint32_t x = s;
+    T x = s;
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
-        const uint32_t y = __shfl_up(x, d, 64);
+        const T y = __shfl_up(x, d, 64);
         if (lane >= d) x += y;
     }
     if (lane == 63) wsum[w] = x;
     __syncthreads();
-    uint32_t run = x - s, total = 0;
+    T run = x - s, total = 0;
     for (int k = 0; k < kWaves; k++) {
         if (k < w) run += wsum[k];
         total += wsum[k];
     }
     for (int i = b0; i < b1; i++) {
-        const uint32_t v = in[i];
+        const T v = in[i];
         out[i] = run;
         run += v;
     }
@@ -381,38 +396,77 @@ __device__ uint32_t block_exclusive_scan(const uint32_t* in, uint32_t* out, int 
     return total;
 }
 
-// Chunk table entry: bin | (chunk index within the bin) << 16, first record,
-// end record, (chunks of the bin) | (first partial slice of a multi-chunk
-// bin) << 16.
+// Chunk table entries (uint4): bin, first record, end record, and the
+// chunk's partial slice, or kSoleOwner for a bin of one chunk.  Merge list
+// entries: bin, the bin's first record, its first partial slice, its chunk
+// count.
+constexpr uint32_t kSoleOwner = 0xffffffffu;
+
+// Bins of one chunk finished in the accumulate's second phase, beside the
+// merges (about one block per block slot of the GPU, two per CU).
+constexpr uint32_t kLateChunks = 448;
+
+// Workgroup 0 also writes the chunk table and the merge list of the
+// accumulate pass (the heaviest work first): the chunks of the bins of more
+// than a.split records (cut into chunks of a.chunk records), then the other
+// bins of more than a.chunk records, then the remaining bins with records,
+// last level first (the fine levels' bins take the longest to finish);
+// nchunks[0] = chunks of the first phase, [1] = bins to merge, [2] = chunks
+// (the last min(kLateChunks, bins of at most a.chunk records) run in the
+// second phase).
 __global__ __launch_bounds__(kBinThreads) void scatter_distribute_kernel(
     const ScatterArgs a, const float* __restrict__ pos, const _Float16* __restrict__ denc,
     const uint32_t* __restrict__ prefix, const uint32_t* __restrict__ totals, float4* __restrict__ rec,
-    uint32_t cap, uint4* __restrict__ chunks, uint32_t* __restrict__ nchunks)
+    uint32_t cap, uint4* __restrict__ chunks, uint4* __restrict__ merges, uint32_t* __restrict__ nchunks)
 {
     extern __shared__ uint32_t sh[];
-    uint32_t* cur = sh;               // [bins]
-    uint32_t* aux = sh + a.bins;      // [bins] (block 0: chunk starts), then [bins] partial-slice bases
+    uint32_t* cur = sh;                        // [bins]
+    uint32_t* aux = sh + ((a.bins + 1) & ~1);  // [2 bins], 8-byte aligned (block 0: chunk table positions)
     __shared__ uint32_t wsum[kBinThreads / 64];
+    __shared__ uint64_t wsum64[kBinThreads / 64];
     block_exclusive_scan(totals, cur, a.bins, wsum);
     if (blockIdx.x == 0) {
-        uint32_t* kst = aux;
-        uint32_t* sst = aux + a.bins;
-        for (int b = threadIdx.x; b < a.bins; b += kBinThreads) {
-            const uint32_t k = (totals[b] + kChunk - 1) / kChunk;
-            kst[b] = k;
-            sst[b] = k > 1 ? k : 0u;
-        }
-        __syncthreads();
-        const uint32_t nch = block_exclusive_scan(kst, kst, a.bins, wsum);
-        block_exclusive_scan(sst, sst, a.bins, wsum);
+        const uint32_t C = a.chunk, S = a.split;
+        // per bin, four counters packed in one word and scanned together (no
+        // field's total carries into the next: chunks of split bins < 2^18,
+        // bins <= kMaxBins < 2^14): the chunks of a split bin (bits 0-17: its
+        // first chunk, also its first partial slice) and 1 for its merge entry
+        // (bits 46-59), or 1 for a large bin of one chunk (bits 18-31), or 1
+        // for a small one (bits 32-45)
+        uint64_t* pk = reinterpret_cast<uint64_t*>(aux);
         for (int b = threadIdx.x; b < a.bins; b += kBinThreads) {
             const uint32_t t = totals[b];
-            const uint32_t k = (t + kChunk - 1) / kChunk;
-            for (uint32_t j = 0; j < k; j++)
-                chunks[kst[b] + j] = make_uint4((uint32_t)b | (j << 16), cur[b] + j * kChunk,
-                                                cur[b] + min((j + 1) * kChunk, t), k | (sst[b] << 16));
+            uint64_t v = 0;
+            if (t > S) v = (uint64_t)((t + C - 1) / C) | (1ull << 46);
+            else if (t > C) v = 1ull << 18;
+            else if (t != 0u) v = 1ull << 32;
+            pk[b] = v;
         }
-        if (threadIdx.x == 0) *nchunks = nch;
+        __syncthreads();
+        const uint64_t tot = block_exclusive_scan(pk, pk, a.bins, wsum64);
+        const uint32_t nsplit = (uint32_t)(tot & 0x3ffffu), nlarge = (uint32_t)(tot >> 18) & 0x3fffu,
+                       nsmall = (uint32_t)(tot >> 32) & 0x3fffu, nmerge = (uint32_t)(tot >> 46) & 0x3fffu;
+        for (int b = threadIdx.x; b < a.bins; b += kBinThreads) {
+            const uint32_t t = totals[b];
+            const uint64_t v = pk[b];
+            if (t > S) {
+                const uint32_t first = (uint32_t)(v & 0x3ffffu), k = (t + C - 1) / C;
+                for (uint32_t j = 0; j < k; j++)
+                    chunks[first + j] = make_uint4((uint32_t)b, cur[b] + j * C, cur[b] + min((j + 1) * C, t), first + j);
+                merges[(uint32_t)(v >> 46) & 0x3fffu] = make_uint4((uint32_t)b, cur[b], first, k);
+            } else if (t > C) {
+                chunks[nsplit + ((uint32_t)(v >> 18) & 0x3fffu)] = make_uint4((uint32_t)b, cur[b], cur[b] + t, kSoleOwner);
+            } else if (t != 0u) {
+                const uint32_t back = nsmall - 1u - ((uint32_t)(v >> 32) & 0x3fffu);
+                chunks[nsplit + nlarge + back] = make_uint4((uint32_t)b, cur[b], cur[b] + t, kSoleOwner);
+            }
+        }
+        if (threadIdx.x == 0) {
+            const uint32_t all = nsplit + nlarge + nsmall;
+            nchunks[0] = all - min(nsmall, kLateChunks);
+            nchunks[1] = nmerge;
+            nchunks[2] = all;
+        }
     }
     for (int b = threadIdx.x; b < a.bins; b += kBinThreads) cur[b] += prefix[(size_t)blockIdx.x * a.bins + b];
     __syncthreads();
@@ -496,13 +550,7 @@ __device__ __forceinline__ bool small_product(float c, uint32_t thr_bits)
 }
 
 __device__ __forceinline__ void set_bit(uint32_t* w, int i) { atomicOr(&w[i >> 5], 1u << (i & 31)); }
-__device__ __forceinline__ void clear_bit(uint32_t* w, int i) { atomicAnd(&w[i >> 5], ~(1u << (i & 31))); }
 __device__ __forceinline__ bool get_bit(const uint32_t* w, int i) { return (w[i >> 5] >> (i & 31)) & 1u; }
-// the same while other threads may clear other bits of the word
-__device__ __forceinline__ bool get_bit_shared(uint32_t* w, int i)
-{
-    return (__hip_atomic_load(&w[i >> 5], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >> (i & 31)) & 1u;
-}
 
 // Sums below this many quanta carry fewer significant bits than fp32 and are
 // summed again at the entry's own scale.
@@ -534,6 +582,23 @@ __device__ __forceinline__ bool rec_finite(const float4& r)
 }
 
 constexpr int kAccThreads = 512;
+
+// f(i) for every set bit i < nbits of an LDS bitmap, each word visited by one
+// thread of the block.
+template <class F>
+__device__ __forceinline__ void for_each_bit(const uint32_t* w, int nbits, F&& f)
+{
+    const int nwords = (nbits + 31) >> 5;
+    for (int wi = threadIdx.x; wi < nwords; wi += kAccThreads) {
+        uint32_t m = w[wi];
+        while (m) {
+            const int b = __ffs(m) - 1;
+            m &= m - 1;
+            f(wi * 32 + b);
+        }
+    }
+}
+
 
 // f(products) over records [r0, r1) step kAccThreads, kRescan loads in flight
 // per thread (a dependent load per record would wait out the memory latency
@@ -607,91 +672,109 @@ __device__ __forceinline__ void table_adam_batch(const TableAdamArgs& t, size_t 
             v[k] = reinterpret_cast<const float2*>(t.v)[i];
         }
     }
+    // every update before the first store: a store between two entries'
+    // updates would make the next entry's wait for its loads also wait for
+    // that store to complete (one counter covers loads and stores)
+#pragma unroll
+    for (int k = 0; k < kBatch; k++) {
+        if (t0[k]) adam_update(g0[k], m[k].x, v[k].x, w[k].x, t.a);
+        if (t1[k]) adam_update(g1[k], m[k].y, v[k].y, w[k].y, t.a);
+    }
 #pragma unroll
     for (int k = 0; k < kBatch; k++) {
         if (!(t0[k] | t1[k])) continue;
         const size_t i = base + (size_t)(s0 + k * kAccThreads);
-        float2 wk = w[k], mk = m[k], vk = v[k];
-        if (t0[k]) adam_update(g0[k], mk.x, vk.x, wk.x, t.a);
-        if (t1[k]) adam_update(g1[k], mk.y, vk.y, wk.y, t.a);
-        reinterpret_cast<float2*>(t.w)[i] = wk;
-        reinterpret_cast<float2*>(t.m)[i] = mk;
-        reinterpret_cast<float2*>(t.v)[i] = vk;
+        reinterpret_cast<float2*>(t.w)[i] = w[k];
+        reinterpret_cast<float2*>(t.m)[i] = m[k];
+        reinterpret_cast<float2*>(t.v)[i] = v[k];
         if (t0[k] & t1[k]) {
-            reinterpret_cast<h2*>(t.w16)[i] = h2{to_h(wk.x), to_h(wk.y)};
+            reinterpret_cast<h2*>(t.w16)[i] = h2{to_h(w[k].x), to_h(w[k].y)};
         } else {
-            t.w16[2 * i + (t0[k] ? 0 : 1)] = to_h(t0[k] ? wk.x : wk.y);
+            t.w16[2 * i + (t0[k] ? 0 : 1)] = to_h(t0[k] ? w[k].x : w[k].y);
         }
     }
 }
 
-// Two blocks per CU (the LDS holds two slices): at most 128 VGPRs.
-template <bool ADAM>
-__global__ __launch_bounds__(kAccThreads) __attribute__((amdgpu_waves_per_eu(4))) void scatter_accumulate_kernel(
-    const ScatterArgs a, const float4* __restrict__ rec, const uint4* __restrict__ chunks,
-    const uint32_t* __restrict__ nchunks, const uint32_t* __restrict__ totals, const uint32_t* __restrict__ lvlmax,
-    float* __restrict__ grads, unsigned long long* __restrict__ part, uint32_t* __restrict__ done, int grads_zero,
-    uint32_t* __restrict__ part_nf, uint32_t* __restrict__ part_sus, const TableAdamArgs ta)
+// The slice of one bin: its level, its first table entry and entry count,
+// and the fixed-point scales of its sums.
+struct SliceCtx {
+    int l, slots, e, E, sfine;
+    bool dense;
+    uint32_t thr, tot;
+    size_t ebase;  // first table entry of the slice ([L][T] numbering)
+    // gradient words in use: [0, 2 slots), and for a dense slice (at most
+    // kSlice / 2 entries) the finer sums of its small products at
+    // [kFine, kFine + 2 slots)
+    __device__ int used() const { return dense ? 4 * slots : 2 * slots; }
+    __device__ int word(int k) const { return k < 2 * slots ? k : kFine + (k - 2 * slots); }
+};
+
+__device__ __forceinline__ SliceCtx slice_ctx(const ScatterArgs& a, int bin, const uint32_t* __restrict__ totals,
+                                              const uint32_t* __restrict__ lvlmax)
 {
-    __shared__ unsigned long long acc[2 * kSlice];
-    __shared__ uint32_t nf[ADAM ? kNfWords : 1];
-    __shared__ uint32_t sus[kNfWords];        // gradients summed again at a finer scale
-    __shared__ uint32_t aux[kNfWords];        // gradients with products cancelling
-    __shared__ uint32_t tny[kNfWords];        // gradients still below 2^24 units
-    __shared__ uint8_t ex_off[2 * kSlice];    // the refined gradients' exponent above e
-    __shared__ int s_flag, s_last;
-    if (blockIdx.x >= *nchunks) return;
-    const uint4 ch = chunks[blockIdx.x];
-    const int bin = (int)(ch.x & 0xffffu);
-    const uint32_t kb = ch.w & 0xffffu, pbase = ch.w >> 16, pj = ch.x >> 16;
+    SliceCtx c;
     int l = 0;
     while (l + 1 < a.L && a.bin_base[l + 1] <= bin) l++;
+    c.l = l;
     const int sl = bin - a.bin_base[l];
-    int elem0, slots;
-    if (l < a.dense_start) {
+    c.dense = l < a.dense_start;
+    int elem0;
+    if (c.dense) {
         const int st = a.res[l] + 1, rps = a.rows_per_slice[l];
         const int row0 = sl * rps;
         elem0 = row0 * st;
-        slots = min(rps, st * st - row0) * st;
+        c.slots = min(rps, st * st - row0) * st;
     } else {
         elem0 = sl * kSlice;
-        slots = min(kSlice, a.T);
+        c.slots = min(kSlice, a.T);
     }
+    c.ebase = (size_t)l * a.T + elem0;
     const uint32_t hb = lvlmax[l];
     const int ex = (int)((hb >> 10) & 31u);
-    const int E = ex == 0 ? -15 : min(ex - 15, 15);
-    const uint32_t tot = totals[bin];
-    const int lg = tot <= 1u ? 0 : 32 - __clz(tot - 1u);
-    const int e = min(49, 60 - lg) - E;
-    const uint32_t thr = (uint32_t)(127 + 24 - e) << 23;  // 2^(24 - e), 24 - e in [-40, 9]
+    c.E = ex == 0 ? -15 : min(ex - 15, 15);
+    c.tot = totals[bin];
+    const int lg = c.tot <= 1u ? 0 : 32 - __clz(c.tot - 1u);
+    c.e = min(49, 60 - lg) - c.E;
+    c.thr = (uint32_t)(127 + 24 - c.e) << 23;  // 2^(24 - e), 24 - e in [-40, 9]
     // the finer scale e + sfine of small products: below 2^(24 + sfine) <= 2^50
     // units each, 2^lg of them below 2^62
-    const int sfine = min(26, 38 - lg);
-    const bool dense = l < a.dense_start;
-    // words of the slice in use: a dense slice (at most kSlice / 2 entries)
-    // keeps its small products' sums at the finer scale in acc[kFine + i]
-    const int nw = dense ? kFine + 2 * slots : 2 * slots;
-    float* gl = ADAM ? nullptr : grads + ((size_t)l * a.T + elem0) * 2;
-    const size_t ebase = (size_t)l * a.T + elem0;  // first table entry of the slice
-    for (int i = threadIdx.x; i < nw; i += kAccThreads) acc[i] = 0ull;
-    for (int i = threadIdx.x; i < kNfWords; i += kAccThreads) {
-        sus[i] = aux[i] = tny[i] = 0u;
-        if constexpr (ADAM) nf[i] = 0u;
-    }
-    if (threadIdx.x == 0) s_flag = 0;
-    __syncthreads();
+    c.sfine = min(26, 38 - lg);
+    return c;
+}
+
+// A slice's sums in LDS (two blocks per CU: at most 80 KiB each).
+template <bool ADAM>
+struct SliceLds {
+    unsigned long long acc[2 * kSlice];
+    uint32_t nf[ADAM ? kNfWords : 1];  // non-finite products (fused update)
+    uint32_t sus[kNfWords];            // gradients that took a small product (summed again at a finer scale)
+    uint32_t aux[kNfWords];            // gradients with products cancelling
+    uint32_t tny[kNfWords];            // gradients still below 2^24 units
+    uint8_t ex_off[2 * kSlice];        // the refined gradients' exponent above e
+    int flag;                          // stored path: non-finite products went to the entries by fp32 atomics
+};
+
+// Sums of the records [r0, r1) of one bin into the cleared slice; ends with a
+// block barrier.  gl: the slice's gradient words (stored path), for the fp32
+// atomics of non-finite products.
+template <bool ADAM>
+__device__ __forceinline__ void sum_records(SliceLds<ADAM>& S, const SliceCtx& c, const float4* __restrict__ rec,
+                                            uint32_t r0, uint32_t r1, float* gl)
+{
+    const uint32_t thr = c.thr;
+    const int e = c.e, sfine = c.sfine;
     // the gradients a record adds a small product to (refined if their sums stay small)
-    auto mark_small = [&](const float (&c)[4], const int (&at)[4]) {
-        if (small_product(c[0], thr) | small_product(c[1], thr) | small_product(c[2], thr) |
-            small_product(c[3], thr)) {
+    auto mark_small = [&](const float (&cc)[4], const int (&at)[4]) {
+        if (small_product(cc[0], thr) | small_product(cc[1], thr) | small_product(cc[2], thr) |
+            small_product(cc[3], thr)) {
 #pragma unroll
             for (int j = 0; j < 4; j++)
-                if (small_product(c[j], thr)) set_bit(sus, at[j]);
+                if (small_product(cc[j], thr)) set_bit(S.sus, at[j]);
         }
     };
     // records per thread in flight before their LDS adds (hashed bins)
     constexpr int kBatch = 8;
-    if (l < a.dense_start) {
+    if (c.dense) {
         // Dense bins: the distribute pass leaves the records of consecutive
         // samples of a ray in consecutive slots, and those share corner
         // pairs.  Each lane takes kRun consecutive records (one 64-byte
@@ -703,15 +786,14 @@ __global__ __launch_bounds__(kAccThreads) __attribute__((amdgpu_waves_per_eu(4))
         constexpr int kGroups = 2;  // runs per lane in flight (4 and 6 measured slower)
         const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
         constexpr int kWaveSpan = 64 * kRun;
-        for (uint32_t b0 = ch.y + (uint32_t)wv * kWaveSpan; b0 < ch.z;
-             b0 += (uint32_t)kGroups * kAccThreads * kRun) {
+        for (uint32_t b0 = r0 + (uint32_t)wv * kWaveSpan; b0 < r1; b0 += (uint32_t)kGroups * kAccThreads * kRun) {
             float4 r[kGroups][kRun];
 #pragma unroll
             for (int gi = 0; gi < kGroups; gi++)
 #pragma unroll
                 for (int k = 0; k < kRun; k++) {
                     const uint32_t i = b0 + (uint32_t)gi * kAccThreads * kRun + (uint32_t)(lane * kRun + k);
-                    r[gi][k] = i < ch.z ? rec[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+                    r[gi][k] = i < r1 ? rec[i] : make_float4(0.f, 0.f, 0.f, 0.f);
                 }
 #pragma unroll
             for (int gi = 0; gi < kGroups; gi++) {
@@ -724,15 +806,15 @@ __global__ __launch_bounds__(kAccThreads) __attribute__((amdgpu_waves_per_eu(4))
                     const int at[4] = {2 * s0, 2 * s0 + 1, 2 * s1, 2 * s1 + 1};
 #pragma unroll
                     for (int j = 0; j < 4; j++) {
-                        if (q[j]) lds_add(acc, at[j], q[j]);
-                        if (qf[j]) lds_add(acc, kFine + at[j], qf[j]);
-                        if (sm & (1u << j)) set_bit(sus, at[j]);
+                        if (q[j]) lds_add(S.acc, at[j], q[j]);
+                        if (qf[j]) lds_add(S.acc, kFine + at[j], qf[j]);
+                        if (sm & (1u << j)) set_bit(S.sus, at[j]);
                     }
                 };
 #pragma unroll
                 for (int k = 0; k < kRun; k++) {
                     const uint32_t i = b0 + (uint32_t)gi * kAccThreads * kRun + (uint32_t)(lane * kRun + k);
-                    if (i >= ch.z) break;
+                    if (i >= r1) break;
                     const uint32_t key = __float_as_uint(r[gi][k].x);
                     if (key != cur) {
                         flush();
@@ -752,167 +834,126 @@ __global__ __launch_bounds__(kAccThreads) __attribute__((amdgpu_waves_per_eu(4))
                         } else if (fin || isfinite(rp.c[j])) {
                             q[j] += fixed_of(rp.c[j], e);
                         } else if constexpr (ADAM) {
-                            set_bit(nf, rp.at[j]);
+                            set_bit(S.nf, rp.at[j]);
                         } else {
                             atomic_add_f32(gl + rp.at[j], rp.c[j]);
-                            s_flag = 1;
+                            S.flag = 1;
                         }
                     }
                 }
                 flush();
             }
         }
-    } else
-    for (uint32_t i0 = ch.y + threadIdx.x; i0 < ch.z; i0 += kBatch * kAccThreads) {
-        float4 r[kBatch];
+    } else {
+        for (uint32_t i0 = r0 + threadIdx.x; i0 < r1; i0 += kBatch * kAccThreads) {
+            float4 r[kBatch];
 #pragma unroll
-        for (int k = 0; k < kBatch; k++) {
-            const uint32_t i = i0 + k * kAccThreads;
-            r[k] = i < ch.z ? rec[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-#pragma unroll
-        for (int k = 0; k < kBatch; k++) {
-            if (i0 + k * kAccThreads >= ch.z) break;
-            const RecProducts rp = rec_products(r[k]);
-            if (rec_finite(r[k])) {
-#pragma unroll
-                for (int j = 0; j < 4; j++) lds_add(acc, rp.at[j], fixed_of(rp.c[j], e));
-            } else if constexpr (ADAM) {
-#pragma unroll
-                for (int j = 0; j < 4; j++) add_or_mark(acc, nf, rp.at[j], rp.c[j], e);
-            } else {
-#pragma unroll
-                for (int j = 0; j < 4; j++) add_checked(acc, gl, rp.at[j], rp.c[j], e, &s_flag);
+            for (int k = 0; k < kBatch; k++) {
+                const uint32_t i = i0 + k * kAccThreads;
+                r[k] = i < r1 ? rec[i] : make_float4(0.f, 0.f, 0.f, 0.f);
             }
-            mark_small(rp.c, rp.at);
+#pragma unroll
+            for (int k = 0; k < kBatch; k++) {
+                if (i0 + k * kAccThreads >= r1) break;
+                const RecProducts rp = rec_products(r[k]);
+                if (rec_finite(r[k])) {
+#pragma unroll
+                    for (int j = 0; j < 4; j++) lds_add(S.acc, rp.at[j], fixed_of(rp.c[j], e));
+                } else if constexpr (ADAM) {
+#pragma unroll
+                    for (int j = 0; j < 4; j++) add_or_mark(S.acc, S.nf, rp.at[j], rp.c[j], e);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; j++) add_checked(S.acc, gl, rp.at[j], rp.c[j], e, &S.flag);
+                }
+                mark_small(rp.c, rp.at);
+            }
         }
     }
     __syncthreads();
-    if (kb > 1) {
-        // A bin of several chunks: every chunk stores its sums (and non-finite
-        // bits) as a partial slice; the last one to finish adds them all up
-        // (exact integer sums) and finishes the bin as its sole owner.
-        unsigned long long* mine = part + (size_t)(pbase + pj) * (2 * kSlice);
-        for (int i = threadIdx.x; i < nw; i += kAccThreads) mine[i] = acc[i];
-        uint32_t* msus = part_sus + (size_t)(pbase + pj) * kNfWords;
-        for (int i = threadIdx.x; i < kNfWords; i += kAccThreads) {
-            msus[i] = sus[i];
-            if constexpr (ADAM) part_nf[(size_t)(pbase + pj) * kNfWords + i] = nf[i];
-        }
-        // done[bin]: chunks finished; done[kMaxBins + bin]: non-finite atomics seen
-        if (!ADAM && threadIdx.x == 0 && s_flag)
-            __hip_atomic_fetch_or(done + kMaxBins + bin, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __threadfence();
-        __syncthreads();
-        if (threadIdx.x == 0)
-            s_last = __hip_atomic_fetch_add(done + bin, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == kb - 1;
-        __syncthreads();
-        if (!s_last) return;
-        __threadfence();  // acquire: the other chunks' partial slices are visible
-        // the other chunks' sums onto this one's (still in LDS): each thread
-        // adds the words it owns, kMergeBatch loads in flight
-        constexpr int kMergeBatch = 2 * kSlice / kAccThreads;
-        for (uint32_t c = 0; c < kb; c++) {
-            if (c == pj) continue;
-            const unsigned long long* other = part + (size_t)(pbase + c) * (2 * kSlice);
-            unsigned long long t[kMergeBatch];
-#pragma unroll
-            for (int k = 0; k < kMergeBatch; k++) {
-                const int i = threadIdx.x + k * kAccThreads;
-                t[k] = i < nw ? other[i] : 0ull;
-            }
-#pragma unroll
-            for (int k = 0; k < kMergeBatch; k++) {
-                const int i = threadIdx.x + k * kAccThreads;
-                if (i < nw) acc[i] += t[k];
-            }
-            const uint32_t* osus = part_sus + (size_t)(pbase + c) * kNfWords;
-            for (int i = threadIdx.x; i < kNfWords; i += kAccThreads) {
-                sus[i] |= osus[i];
-                if constexpr (ADAM) nf[i] |= part_nf[(size_t)(pbase + c) * kNfWords + i];
-            }
-        }
-        if (threadIdx.x == 0) {
-            if (!ADAM && __hip_atomic_load(done + kMaxBins + bin, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
-                s_flag = 1;
-            done[bin] = 0u;
-            done[kMaxBins + bin] = 0u;
-        }
-        __syncthreads();
-    }
-    // The sole owner of the slice's sums.  Refinement (see the file comment)
-    // over the records of the whole bin, [r0, r1).
-    const uint32_t r0 = ch.y - pj * kChunk, r1 = r0 + tot;
+}
+
+// The sole owner of a bin's sums (every record [r0, r1) of the bin summed
+// into S): the refinement passes (see the file comment) over the records,
+// then the table update (ADAM) or the gradient store.
+template <bool ADAM>
+__device__ __forceinline__ void finish_slice(SliceLds<ADAM>& S, const SliceCtx& c, const float4* __restrict__ rec,
+                                             uint32_t r0, uint32_t r1, float* gl, int grads_zero,
+                                             const TableAdamArgs& ta)
+{
+    const int slots = c.slots, e = c.e, E = c.E, sfine = c.sfine;
+    const uint32_t thr = c.thr;
+    const bool dense = c.dense;
     bool refine = false;  // hashed slice: some gradients summed again (pass 1)
     bool tiny = false;    // gradients below 2^24 units of their finer scale
     if (dense) {
         // the two scales together, in units of the finer one
-        for (int i = threadIdx.x; i < 2 * slots; i += kAccThreads) {
-            if (!get_bit(sus, i)) continue;
-            const double c = ldexp((double)(long long)acc[i], sfine) + (double)(long long)acc[kFine + i];
-            if (fabs(c) < 0x1p24) {
-                set_bit(tny, i);
+        for_each_bit(S.sus, 2 * slots, [&](int i) {
+            const double v = ldexp((double)(long long)S.acc[i], sfine) + (double)(long long)S.acc[kFine + i];
+            if (fabs(v) < 0x1p24) {
+                set_bit(S.tny, i);
                 tiny = true;
             }
-        }
+        });
     } else {
         // keep the marks of gradients whose sums stayed below 2^24 quanta
+        // (each mark word owned by one thread)
         bool few = false;
-        for (int i = threadIdx.x; i < 2 * slots; i += kAccThreads) {
-            if (!get_bit_shared(sus, i)) continue;
-            const long long q = (long long)acc[i];
-            if (q > -kFewBits && q < kFewBits) few = true;
-            else clear_bit(sus, i);
+        for (int wi = threadIdx.x; wi < (2 * slots + 31) >> 5; wi += kAccThreads) {
+            uint32_t m = S.sus[wi], keep = m;
+            while (m) {
+                const int b = __ffs(m) - 1;
+                m &= m - 1;
+                const long long q = (long long)S.acc[wi * 32 + b];
+                if (q > -kFewBits && q < kFewBits) few = true;
+                else keep &= ~(1u << b);
+            }
+            S.sus[wi] = keep;
         }
         refine = __syncthreads_or(few);
     }
     if (refine) {
         // pass 1: the marked gradients' small products at scale e + sfine; a
         // product of 2^24 quanta or more marks its gradient for pass 2
-        for (int i = threadIdx.x; i < 2 * slots; i += kAccThreads)
-            if (get_bit(sus, i)) {
-                acc[i] = 0ull;
-                ex_off[i] = (uint8_t)sfine;
-            }
+        for_each_bit(S.sus, 2 * slots, [&](int i) {
+            S.acc[i] = 0ull;
+            S.ex_off[i] = (uint8_t)sfine;
+        });
         __syncthreads();
         bool big = false;
         for_each_record(rec, r0, r1, [&](const RecProducts& rp) {
 #pragma unroll
             for (int j = 0; j < 4; j++)
-                if (finite_bits(rp.c[j]) && rp.c[j] != 0.f && get_bit(sus, rp.at[j])) {
+                if (finite_bits(rp.c[j]) && rp.c[j] != 0.f && get_bit(S.sus, rp.at[j])) {
                     if (small_product(rp.c[j], thr)) {
-                        lds_add(acc, rp.at[j], fixed_of(rp.c[j], e + sfine));
+                        lds_add(S.acc, rp.at[j], fixed_of(rp.c[j], e + sfine));
                     } else {
-                        set_bit(aux, rp.at[j]);
+                        set_bit(S.aux, rp.at[j]);
                         big = true;
                     }
                 }
         });
         if (__syncthreads_or(big)) {
             // pass 2 (products cancelling): those gradients at scale e again
-            for (int i = threadIdx.x; i < 2 * slots; i += kAccThreads)
-                if (get_bit(aux, i)) {
-                    acc[i] = 0ull;
-                    clear_bit(sus, i);
-                }
+            for (int wi = threadIdx.x; wi < (2 * slots + 31) >> 5; wi += kAccThreads) S.sus[wi] &= ~S.aux[wi];
+            for_each_bit(S.aux, 2 * slots, [&](int i) { S.acc[i] = 0ull; });
             __syncthreads();
             for_each_record(rec, r0, r1, [&](const RecProducts& rp) {
 #pragma unroll
                 for (int j = 0; j < 4; j++)
-                    if (finite_bits(rp.c[j]) && get_bit(aux, rp.at[j])) lds_add(acc, rp.at[j], fixed_of(rp.c[j], e));
+                    if (finite_bits(rp.c[j]) && get_bit(S.aux, rp.at[j])) lds_add(S.acc, rp.at[j], fixed_of(rp.c[j], e));
             });
             __syncthreads();
         }
         // gradients whose finer sums stay below 2^24 units (products of a few
         // quanta at most)
-        for (int i = threadIdx.x; i < 2 * slots; i += kAccThreads) {
-            if (!get_bit(sus, i)) continue;
-            const long long q = (long long)acc[i];
+        for_each_bit(S.sus, 2 * slots, [&](int i) {
+            const long long q = (long long)S.acc[i];
             if (q > -kFewBits && q < kFewBits) {
-                set_bit(tny, i);
+                set_bit(S.tny, i);
                 tiny = true;
             }
-        }
+        });
     }
     const bool any_tiny = __syncthreads_or(tiny);
     if (any_tiny) {
@@ -921,33 +962,31 @@ __global__ __launch_bounds__(kAccThreads) __attribute__((amdgpu_waves_per_eu(4))
         // exponent it sets: |product| < 2^(Es + 1) gives min(49, 60 - lg) - Es,
         // Es <= E, an offset over e of E - Es in [0, 164]; the sum lands in
         // acc[i] (a dense slice's finer sum cleared)
-        for (int i = threadIdx.x; i < 2 * slots; i += kAccThreads)
-            if (get_bit(tny, i)) {
-                acc[i] = 0ull;
-                if (dense) acc[kFine + i] = 0ull;
-            }
+        for_each_bit(S.tny, 2 * slots, [&](int i) {
+            S.acc[i] = 0ull;
+            if (dense) S.acc[kFine + i] = 0ull;
+        });
         __syncthreads();
         for_each_record(rec, r0, r1, [&](const RecProducts& rp) {
 #pragma unroll
             for (int j = 0; j < 4; j++)
-                if (finite_bits(rp.c[j]) && rp.c[j] != 0.f && get_bit(tny, rp.at[j]))
-                    __hip_atomic_fetch_max(acc + rp.at[j], (unsigned long long)(__float_as_uint(rp.c[j]) & 0x7fffffffu),
+                if (finite_bits(rp.c[j]) && rp.c[j] != 0.f && get_bit(S.tny, rp.at[j]))
+                    __hip_atomic_fetch_max(S.acc + rp.at[j], (unsigned long long)(__float_as_uint(rp.c[j]) & 0x7fffffffu),
                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         });
         __syncthreads();
-        for (int i = threadIdx.x; i < 2 * slots; i += kAccThreads) {
-            if (!get_bit(tny, i)) continue;
-            const uint32_t mb = (uint32_t)acc[i];
+        for_each_bit(S.tny, 2 * slots, [&](int i) {
+            const uint32_t mb = (uint32_t)S.acc[i];
             const int Es = mb >= 0x800000u ? (int)(mb >> 23) - 127 : (mb ? 31 - __clz(mb) - 149 : E);
-            ex_off[i] = (uint8_t)min(255, max(0, E - Es));
-            acc[i] = 0ull;
-        }
+            S.ex_off[i] = (uint8_t)min(255, max(0, E - Es));
+            S.acc[i] = 0ull;
+        });
         __syncthreads();
         for_each_record(rec, r0, r1, [&](const RecProducts& rp) {
 #pragma unroll
             for (int j = 0; j < 4; j++)
-                if (finite_bits(rp.c[j]) && rp.c[j] != 0.f && get_bit(tny, rp.at[j]))
-                    lds_add(acc, rp.at[j], fixed_of(rp.c[j], e + ex_off[rp.at[j]]));
+                if (finite_bits(rp.c[j]) && rp.c[j] != 0.f && get_bit(S.tny, rp.at[j]))
+                    lds_add(S.acc, rp.at[j], fixed_of(rp.c[j], e + S.ex_off[rp.at[j]]));
         });
         __syncthreads();
     }
@@ -955,13 +994,13 @@ __global__ __launch_bounds__(kAccThreads) __attribute__((amdgpu_waves_per_eu(4))
     // a dense slice's two scales combined in fp64 first) and whether its sum
     // is nonzero
     auto grad_of = [&](int i, float& g) -> bool {
-        const long long q = (long long)acc[i];
-        if ((refine || any_tiny) && (get_bit(tny, i) || (refine && get_bit(sus, i)))) {
-            g = ldexpf((float)q, -(e + (int)ex_off[i]));
+        const long long q = (long long)S.acc[i];
+        if ((refine || any_tiny) && (get_bit(S.tny, i) || (refine && get_bit(S.sus, i)))) {
+            g = ldexpf((float)q, -(e + (int)S.ex_off[i]));
             return q != 0;
         }
         if (dense) {
-            const long long f = (long long)acc[kFine + i];
+            const long long f = (long long)S.acc[kFine + i];
             if (f == 0) g = ldexpf((float)q, -e);
             else if (q == 0) g = ldexpf((float)f, -(e + sfine));
             else g = (float)(ldexp((double)q, -e) + ldexp((double)f, -(e + sfine)));
@@ -972,13 +1011,14 @@ __global__ __launch_bounds__(kAccThreads) __attribute__((amdgpu_waves_per_eu(4))
     };
     if constexpr (ADAM) {
         // update every entry the sums reached
-        for (int s0 = threadIdx.x; s0 < slots; s0 += kAdamBatch * kAccThreads) table_adam_batch(ta, ebase, s0, slots, grad_of, nf);
+        for (int s0 = threadIdx.x; s0 < slots; s0 += kAdamBatch * kAccThreads)
+            table_adam_batch(ta, c.ebase, s0, slots, grad_of, S.nf);
         return;
     }
     {
         // non-finite products went to the entries by fp32 atomics: then the
         // sums follow by atomics too
-        const bool atomic = s_flag != 0;
+        const bool atomic = S.flag != 0;
         float2* g2 = reinterpret_cast<float2*>(gl);
         if (atomic || grads_zero) {
             for (int s = threadIdx.x; s < slots; s += kAccThreads) {
@@ -993,6 +1033,7 @@ __global__ __launch_bounds__(kAccThreads) __attribute__((amdgpu_waves_per_eu(4))
             }
         } else {
             // read-modify-write, kBatch entries per thread in flight
+            constexpr int kBatch = 8;
             for (int s0 = threadIdx.x; s0 < slots; s0 += kBatch * kAccThreads) {
                 float2 o[kBatch];
 #pragma unroll
@@ -1013,6 +1054,135 @@ __global__ __launch_bounds__(kAccThreads) __attribute__((amdgpu_waves_per_eu(4))
     }
 }
 
+// Parameters shared by the two accumulate launches.
+struct AccArgs {
+    const float4* rec;
+    const uint4* chunks;
+    const uint4* merges;
+    const uint32_t* nchunks;  // [3]: first phase's chunks, bins to merge, all chunks
+    const uint32_t* totals;
+    const uint32_t* lvlmax;
+    float* grads;             // stored path
+    unsigned long long* part;
+    uint32_t* part_nf;
+    uint32_t* part_sus;
+    uint32_t* part_flag;
+    int grads_zero;
+};
+
+// One chunk: its sums in LDS (int64 fixed point, ds_add_u64).  A bin of one
+// chunk is finished here (refinement, then the table update or the gradient
+// store); a chunk of a bin of several stores its sums and marks as its
+// partial slice for the bin's merge.
+template <bool ADAM>
+__device__ __forceinline__ void do_chunk(SliceLds<ADAM>& S, const ScatterArgs& a, const AccArgs& g, uint32_t ci,
+                                         const TableAdamArgs& ta)
+{
+    const uint4 ch = g.chunks[ci];
+    const SliceCtx c = slice_ctx(a, (int)ch.x, g.totals, g.lvlmax);
+    float* gl = ADAM ? nullptr : g.grads + c.ebase * 2;
+    const int nu = c.used();
+    for (int k = threadIdx.x; k < nu; k += kAccThreads) S.acc[c.word(k)] = 0ull;
+    for (int i = threadIdx.x; i < kNfWords; i += kAccThreads) {
+        S.sus[i] = S.aux[i] = S.tny[i] = 0u;
+        if constexpr (ADAM) S.nf[i] = 0u;
+    }
+    if (threadIdx.x == 0) S.flag = 0;
+    __syncthreads();
+    sum_records(S, c, g.rec, ch.y, ch.z, gl);
+    if (ch.w != kSoleOwner) {
+        unsigned long long* mine = g.part + (size_t)ch.w * (2 * kSlice);
+        for (int k = threadIdx.x; k < nu; k += kAccThreads) mine[k] = S.acc[c.word(k)];
+        for (int i = threadIdx.x; i < kNfWords; i += kAccThreads) {
+            g.part_sus[(size_t)ch.w * kNfWords + i] = S.sus[i];
+            if constexpr (ADAM) g.part_nf[(size_t)ch.w * kNfWords + i] = S.nf[i];
+        }
+        if (!ADAM && threadIdx.x == 0) g.part_flag[ch.w] = (uint32_t)S.flag;
+        return;
+    }
+    finish_slice(S, c, g.rec, ch.y, ch.z, gl, g.grads_zero, ta);
+}
+
+// One bin of several chunks (its partial slices are complete): the exact sum
+// of the partial slices, then the sole owner's finish over all the bin's
+// records.  Each thread adds the words it owns, two slices' loads in flight.
+template <bool ADAM>
+__device__ __forceinline__ void do_merge(SliceLds<ADAM>& S, const ScatterArgs& a, const AccArgs& g, uint32_t mi,
+                                         const TableAdamArgs& ta)
+{
+    const uint4 mg = g.merges[mi];  // bin, first record, first partial slice, chunks
+    const SliceCtx c = slice_ctx(a, (int)mg.x, g.totals, g.lvlmax);
+    float* gl = ADAM ? nullptr : g.grads + c.ebase * 2;
+    const uint32_t p0 = mg.z, kb = mg.w;
+    const int nu = c.used();
+    constexpr int kWords = 2 * kSlice / kAccThreads;  // words per thread
+    unsigned long long sum[kWords];
+#pragma unroll
+    for (int k = 0; k < kWords; k++) sum[k] = 0ull;
+    for (uint32_t j = 0; j < kb; j += 2) {
+        const unsigned long long* o0 = g.part + (size_t)(p0 + j) * (2 * kSlice);
+        const unsigned long long* o1 = g.part + (size_t)(p0 + min(j + 1, kb - 1)) * (2 * kSlice);
+        const bool two = j + 1 < kb;
+        unsigned long long t0[kWords], t1[kWords];
+#pragma unroll
+        for (int k = 0; k < kWords; k++) {
+            const int w = threadIdx.x + k * kAccThreads;
+            t0[k] = w < nu ? o0[w] : 0ull;
+            t1[k] = (two && w < nu) ? o1[w] : 0ull;
+        }
+#pragma unroll
+        for (int k = 0; k < kWords; k++) sum[k] += t0[k] + t1[k];
+    }
+#pragma unroll
+    for (int k = 0; k < kWords; k++) {
+        const int w = threadIdx.x + k * kAccThreads;
+        if (w < nu) S.acc[c.word(w)] = sum[k];
+    }
+    for (int i = threadIdx.x; i < kNfWords; i += kAccThreads) {
+        uint32_t su = 0u, n = 0u;
+        for (uint32_t j = 0; j < kb; j++) {
+            su |= g.part_sus[(size_t)(p0 + j) * kNfWords + i];
+            if constexpr (ADAM) n |= g.part_nf[(size_t)(p0 + j) * kNfWords + i];
+        }
+        S.sus[i] = su;
+        S.aux[i] = S.tny[i] = 0u;
+        if constexpr (ADAM) S.nf[i] = n;
+    }
+    if (threadIdx.x == 0) {
+        uint32_t f = 0u;
+        if (!ADAM)
+            for (uint32_t j = 0; j < kb; j++) f |= g.part_flag[p0 + j];
+        S.flag = (int)f;
+    }
+    __syncthreads();
+    finish_slice(S, c, g.rec, mg.y, mg.y + c.tot, gl, g.grads_zero, ta);
+}
+
+// The accumulate pass in two launches.  Phase 1: chunks [0, nchunks[0]) --
+// every chunk of the bins of several chunks (first: the heaviest work), then
+// bins of one chunk.  Phase 2 (after phase 1: the kernel boundary orders the
+// partial slices, no device-scope fence or counter is needed): the merges of
+// the bins of several chunks, beside the last bins of one chunk (chunks
+// [nchunks[0], nchunks[2])), so that the merges run on a busy GPU.  Two
+// blocks per CU (the LDS holds two slices): at most 128 VGPRs.
+template <bool ADAM, bool PHASE2>
+__global__ __launch_bounds__(kAccThreads) __attribute__((amdgpu_waves_per_eu(4))) void scatter_accumulate_kernel(
+    const ScatterArgs a, const AccArgs g, const TableAdamArgs ta)
+{
+    __shared__ SliceLds<ADAM> S;
+    if constexpr (!PHASE2) {
+        if (blockIdx.x < g.nchunks[0]) do_chunk(S, a, g, blockIdx.x, ta);
+    } else {
+        const uint32_t nm = g.nchunks[1];
+        if (blockIdx.x < nm) {
+            do_merge(S, a, g, blockIdx.x, ta);
+        } else {
+            const uint32_t ci = g.nchunks[0] + (blockIdx.x - nm);
+            if (ci < g.nchunks[2]) do_chunk(S, a, g, ci, ta);
+        }
+    }
+}
+
 }  // namespace
 
 struct ScatterPlan {
@@ -1028,11 +1198,12 @@ struct ScatterPlan {
     uint32_t* lvlmax = nullptr;
     uint32_t* lvlmax_final = nullptr;
     uint4* chunks = nullptr;
-    uint32_t* nchunks = nullptr;
+    uint4* merges = nullptr;             // bins of several chunks
+    uint32_t* nchunks = nullptr;         // [3]: first phase's chunks, bins to merge, chunks
     unsigned long long* part = nullptr;  // partial slices of the chunks of multi-chunk bins
-    uint32_t* done = nullptr;            // [2 kMaxBins]: chunks finished, non-finite atomics seen
     uint32_t* part_nf = nullptr;         // non-finite bits of the partial slices (fused table update)
     uint32_t* part_sus = nullptr;        // small-product marks of the partial slices
+    uint32_t* part_flag = nullptr;       // per partial slice: non-finite products went by atomics (stored path)
 };
 
 namespace {
@@ -1092,46 +1263,49 @@ size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
 
 namespace {
 
-// Byte offsets of a plan's buffers.  The per-bin counters come first:
-// kernels leave them zero after every call, so a region that starts zero
-// stays zero whatever the configuration.
+// Byte offsets of a plan's buffers (every call rewrites what it reads: no
+// buffer needs to start zero).
 struct PlanLayout {
-    size_t o_don, o_prt, o_pnf, o_psu, o_rec, o_cnt, o_tot, o_lmx, o_lmf, o_chk, o_nch, zero_end, bytes;
+    size_t o_prt, o_pnf, o_psu, o_pfl, o_rec, o_cnt, o_tot, o_lmx, o_lmf, o_chk, o_mrg, o_nch, bytes;
 };
 
-// Partial slices: every chunk of a multi-chunk bin has one; a bin of t > kChunk
-// records has ceil(t / kChunk) < t / kChunk + 1 chunks and there are fewer
-// than recs / kChunk such bins, so 2 recs / kChunk + 1 slices suffice.
-// with_nf: room for the fused table update's non-finite bits of every
-// partial slice (plans of the training step; the allocation-free plan has
-// none).
-bool plan_shape(const GridMeta& m, int maxN, ScatterPlan& p, PlanLayout& lay, int max_multi_cap = 0,
-                bool with_nf = false)
+// Partial slices: every chunk of a split bin has one; a bin of t > split
+// records has ceil(t / C) < t / C + 1 chunks (C = chunk) and there are fewer
+// than recs / split <= recs / C such bins, so 2 recs / C + 1 slices suffice.  with_nf: room
+// for the fused table update's non-finite bits of every partial slice (plans
+// of the training step; the allocation-free plan has none).
+bool plan_shape(const GridMeta& m, int maxN, ScatterPlan& p, PlanLayout& lay, uint32_t chunk, uint32_t split,
+                int max_multi_cap = 0, bool with_nf = false)
 {
     ScatterArgs a;
     if (maxN < 1 || !layout(m, a)) return false;
     const unsigned long long recs = 4ull * (unsigned long long)m.numLevels * (unsigned long long)maxN;
-    if (recs >= (1ull << 30)) return false;  // chunk and partial indices stay below 2^16
+    // record indices fit 32 bits, chunks of split bins (< recs / chunk + bins)
+    // the chunk table's 18-bit counters
+    if (recs >= (1ull << 30) || chunk < 8192u || split < chunk) return false;
     a.rounds = (maxN + kRound - 1) / kRound;
+    a.chunk = chunk;
+    a.split = split;
     p.maxN = maxN;
     p.meta = m;
     p.args = a;
-    p.max_chunks = (int)(recs / kChunk) + a.bins + 1;
-    p.max_multi = (int)(2 * (recs / kChunk) + 1);
+    p.max_chunks = (int)(recs / chunk) + a.bins + 1;
+    p.max_multi = (int)(2 * (recs / chunk) + 1);
     const int multi = std::max(p.max_multi, max_multi_cap);
+    const size_t max_merges = (size_t)std::min<unsigned long long>(recs / chunk + 1, (unsigned long long)a.bins);
     size_t off = 0;
-    lay.o_don = off; off = align_up(off + (size_t)2 * kMaxBins * 4);
-    lay.zero_end = off;
     lay.o_prt = off; off = align_up(off + (size_t)multi * 2 * kSlice * 8);
     lay.o_pnf = off; off = align_up(off + (with_nf ? (size_t)multi * kNfWords * 4 : 0));
     lay.o_psu = off; off = align_up(off + (size_t)multi * kNfWords * 4);
+    lay.o_pfl = off; off = align_up(off + (size_t)multi * 4);
     lay.o_rec = off; off = align_up(off + recs * sizeof(float4));
     lay.o_cnt = off; off = align_up(off + (size_t)a.rounds * a.bins * 4);
     lay.o_tot = off; off = align_up(off + (size_t)a.bins * 4);
     lay.o_lmx = off; off = align_up(off + (size_t)a.rounds * a.L * 4);
     lay.o_lmf = off; off = align_up(off + (size_t)a.L * 4);
     lay.o_chk = off; off = align_up(off + (size_t)p.max_chunks * sizeof(uint4));
-    lay.o_nch = off; off = align_up(off + 4);
+    lay.o_mrg = off; off = align_up(off + max_merges * sizeof(uint4));
+    lay.o_nch = off; off = align_up(off + 3 * 4);
     lay.bytes = off;
     return true;
 }
@@ -1145,11 +1319,12 @@ void plan_bind(ScatterPlan& p, char* base, const PlanLayout& lay)
     p.lvlmax = reinterpret_cast<uint32_t*>(base + lay.o_lmx);
     p.lvlmax_final = reinterpret_cast<uint32_t*>(base + lay.o_lmf);
     p.chunks = reinterpret_cast<uint4*>(base + lay.o_chk);
+    p.merges = reinterpret_cast<uint4*>(base + lay.o_mrg);
     p.nchunks = reinterpret_cast<uint32_t*>(base + lay.o_nch);
     p.part = reinterpret_cast<unsigned long long*>(base + lay.o_prt);
-    p.done = reinterpret_cast<uint32_t*>(base + lay.o_don);
     p.part_nf = lay.o_pnf < lay.o_psu ? reinterpret_cast<uint32_t*>(base + lay.o_pnf) : nullptr;
     p.part_sus = reinterpret_cast<uint32_t*>(base + lay.o_psu);
+    p.part_flag = reinterpret_cast<uint32_t*>(base + lay.o_pfl);
 }
 
 }  // namespace
@@ -1158,7 +1333,7 @@ ScatterPlan* scatter_plan_create(const GridMeta& m, int maxN)
 {
     auto* p = new ScatterPlan();
     PlanLayout lay;
-    if (!plan_shape(m, maxN, *p, lay, 0, /*with_nf=*/true)) {
+    if (!plan_shape(m, maxN, *p, lay, kChunk, kSplit, 0, /*with_nf=*/true)) {
         delete p;
         return nullptr;
     }
@@ -1169,14 +1344,6 @@ ScatterPlan* scatter_plan_create(const GridMeta& m, int maxN)
         GRAFT_HIP_CHECK(e);
     }
     plan_bind(*p, static_cast<char*>(mem), lay);
-    // the per-bin counters start (and are left) zero
-    e = hipMemset(mem, 0, lay.zero_end);
-    if (e == hipSuccess) e = hipDeviceSynchronize();
-    if (e != hipSuccess) {
-        (void)hipFree(mem);
-        delete p;
-        GRAFT_HIP_CHECK(e);
-    }
     return p;
 }
 
@@ -1211,7 +1378,7 @@ void scatter_launch(ScatterPlan* p, const GridMeta& m, const __half* denc, const
     a.rounds = (N + kRound - 1) / kRound;
     const auto* dh = reinterpret_cast<const _Float16*>(denc);
     const size_t lds_count = (size_t)(a.bins + a.L) * 4;
-    const size_t lds_dist = (size_t)(3 * a.bins) * 4;
+    const size_t lds_dist = (size_t)(((a.bins + 1) & ~1) + 2 * a.bins) * 4;
     hipLaunchKernelGGL(scatter_count_kernel, dim3(a.rounds), dim3(kBinThreads), lds_count, stream, a, pos, dh,
                        p->counts, p->lvlmax);
     GRAFT_LAUNCH_CHECK();
@@ -1221,19 +1388,28 @@ void scatter_launch(ScatterPlan* p, const GridMeta& m, const __half* denc, const
     GRAFT_LAUNCH_CHECK();
     const uint32_t cap = (uint32_t)(4ull * (unsigned long long)a.L * (unsigned long long)p->maxN);
     hipLaunchKernelGGL(scatter_distribute_kernel, dim3(a.rounds), dim3(kBinThreads), lds_dist, stream, a, pos, dh,
-                       p->counts, p->totals, p->rec, cap, p->chunks, p->nchunks);
+                       p->counts, p->totals, p->rec, cap, p->chunks, p->merges, p->nchunks);
     GRAFT_LAUNCH_CHECK();
     if (wait_before) GRAFT_HIP_CHECK(hipStreamWaitEvent(stream, wait_before, 0));
     const unsigned long long recs = 4ull * (unsigned long long)a.L * (unsigned long long)N;
-    const int grid = (int)std::min<unsigned long long>(recs / kChunk + a.bins + 1, (unsigned long long)p->max_chunks);
-    if (ta)
-        hipLaunchKernelGGL(scatter_accumulate_kernel<true>, dim3(grid), dim3(kAccThreads), 0, stream, a, p->rec,
-                           p->chunks, p->nchunks, p->totals, p->lvlmax_final, nullptr, p->part, p->done, 0,
-                           p->part_nf, p->part_sus, *ta);
-    else
-        hipLaunchKernelGGL(scatter_accumulate_kernel<false>, dim3(grid), dim3(kAccThreads), 0, stream, a, p->rec,
-                           p->chunks, p->nchunks, p->totals, p->lvlmax_final, grads, p->part, p->done,
-                           grads_zero ? 1 : 0, nullptr, p->part_sus, TableAdamArgs{});
+    const int grid = (int)std::min<unsigned long long>(recs / a.chunk + a.bins + 1, (unsigned long long)p->max_chunks);
+    const int mgrid = (int)std::min<unsigned long long>(recs / a.chunk + 1, (unsigned long long)a.bins);
+    AccArgs g{p->rec, p->chunks, p->merges, p->nchunks, p->totals, p->lvlmax_final, grads, p->part, p->part_nf,
+              p->part_sus, p->part_flag, grads_zero ? 1 : 0};
+    const int grid2 = mgrid + (int)std::min<unsigned long long>(kLateChunks, (unsigned long long)a.bins);
+    if (ta) {
+        hipLaunchKernelGGL((scatter_accumulate_kernel<true, false>), dim3(grid), dim3(kAccThreads), 0, stream, a, g,
+                           *ta);
+        GRAFT_LAUNCH_CHECK();
+        hipLaunchKernelGGL((scatter_accumulate_kernel<true, true>), dim3(grid2), dim3(kAccThreads), 0, stream, a, g,
+                           *ta);
+    } else {
+        hipLaunchKernelGGL((scatter_accumulate_kernel<false, false>), dim3(grid), dim3(kAccThreads), 0, stream, a, g,
+                           TableAdamArgs{});
+        GRAFT_LAUNCH_CHECK();
+        hipLaunchKernelGGL((scatter_accumulate_kernel<false, true>), dim3(grid2), dim3(kAccThreads), 0, stream, a, g,
+                           TableAdamArgs{});
+    }
     GRAFT_LAUNCH_CHECK();
 }
 
@@ -1294,9 +1470,9 @@ void hash_scatter(const GridMeta& m, const __half* denc, const float* pos, int p
 // ---------------------------------------------------------------------------
 // Allocation-free variant.  The scratch is one file-scope device array per
 // GPU (kNoAllocBytes; each GPU the library runs on keeps it until the process
-// ends).  Its per-bin counters (offset 0) start zero and every call leaves
-// them zero; the rest is rewritten by every call.  Batches above one sub-batch run as consecutive
-// sub-batches on the caller's stream.  All calls on one GPU share the array:
+// ends).  Every call rewrites what it reads of it (nothing needs to start
+// zero).  Batches above one sub-batch run as consecutive sub-batches on the
+// caller's stream.  All calls on one GPU share the array:
 // calls that overlap on one GPU (two streams, or two threads) race.
 // ---------------------------------------------------------------------------
 
@@ -1305,7 +1481,7 @@ namespace {
 constexpr size_t kNoAllocBytes = (size_t)48 << 20;
 constexpr unsigned long long kNoAllocRecords = 1ull << 21;  // corner-pair records per sub-batch
 constexpr size_t kNoAllocCountWords = (size_t)1 << 20;       // rounds x bins per sub-batch
-constexpr int kNoAllocMulti = (int)(2 * (kNoAllocRecords / kChunk)) + 1;  // partial slices per sub-batch
+constexpr int kNoAllocMulti = (int)(2 * (kNoAllocRecords / kChunkNoAlloc)) + 1;  // partial slices per sub-batch
 constexpr int kMaxDevices = 64;
 
 static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
@@ -1313,15 +1489,9 @@ static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
 char* g_noalloc_base[kMaxDevices];
 std::mutex g_noalloc_mu;
 
-__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* p, size_t n)
-{
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
-        p[i] = 0u;
-}
-
-// The array's device address on the current GPU (looked up, and its counter
-// region cleared on the caller's stream, on the first call on each GPU).
-char* noalloc_base(hipStream_t stream, size_t zero_bytes)
+// The array's device address on the current GPU (looked up on the first call
+// on each GPU).
+char* noalloc_base()
 {
     int dev = 0;
     GRAFT_HIP_CHECK(hipGetDevice(&dev));
@@ -1331,9 +1501,6 @@ char* noalloc_base(hipStream_t stream, size_t zero_bytes)
         void* ptr = nullptr;
         GRAFT_HIP_CHECK(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
         if (!ptr) throw std::runtime_error("hash scatter (no-alloc): no device address for the scratch array");
-        hipLaunchKernelGGL(zero_words_kernel, dim3(256), dim3(256), 0, stream, static_cast<uint32_t*>(ptr),
-                           zero_bytes / 4);
-        GRAFT_LAUNCH_CHECK();
         g_noalloc_base[dev] = static_cast<char*>(ptr);
     }
     return g_noalloc_base[dev];
@@ -1358,9 +1525,10 @@ void hash_scatter_noalloc(const GridMeta& m, const __half* denc, const float* po
     if (sub < kRound) throw std::runtime_error("hash scatter (no-alloc): grid beyond the fixed scratch");
     ScatterPlan plan;
     PlanLayout lay;
-    if (!plan_shape(m, sub, plan, lay, kNoAllocMulti) || plan.max_multi > kNoAllocMulti || lay.bytes > kNoAllocBytes)
+    if (!plan_shape(m, sub, plan, lay, kChunkNoAlloc, kChunkNoAlloc, kNoAllocMulti) || plan.max_multi > kNoAllocMulti ||
+        lay.bytes > kNoAllocBytes)
         throw std::runtime_error("hash scatter (no-alloc): grid beyond the fixed scratch");
-    plan_bind(plan, noalloc_base(stream, lay.zero_end), lay);
+    plan_bind(plan, noalloc_base(), lay);
     const int D = 2 * m.numLevels;
     for (int off = 0; off < N; off += sub) {
         const int n = std::min(sub, N - off);

@@ -41,9 +41,17 @@ def est(tfs):
     return pkg().estimate_num_cascades(np.stack(tfs))
 
 
+def as_4x4(c2w34):
+    """[n, 3, 4] camera-to-world matrices as [n, 16] row-major 4x4."""
+    n = c2w34.shape[0]
+    m = np.tile(np.eye(4), (n, 1, 1))
+    m[:, :3, :] = c2w34
+    return m.astype(np.float32).reshape(n, 16)
+
+
 def test_orbit_is_bounded():
-    tf = scenes.cameras(100, 1.5, seed=2024)
-    assert est(list(np.asarray(tf, np.float32).reshape(-1, 16))) == 1
+    # the bench's 100 orbit cameras (radius 1.5, looking at the origin)
+    assert est(list(as_4x4(scenes.cameras(100, 1.5, seed=2024)))) == 1
     rng = np.random.default_rng(0)
     centre = np.array([0.3, -0.2, 0.1])
     poses = []

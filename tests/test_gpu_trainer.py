@@ -74,7 +74,9 @@ def test_trainer_takes_the_loaders_cascade_estimate(dev, kind, want):
     P = pkg()
     n, W, H = 12, 16, 16
     if kind == "orbit":
-        tf = np.asarray(scenes.cameras(n, 1.5, seed=3), np.float32).reshape(n, 16)
+        tf = np.tile(np.eye(4, dtype=np.float32), (n, 1, 1))
+        tf[:, :3, :] = scenes.cameras(n, 1.5, seed=3)
+        tf = tf.reshape(n, 16)
     else:
         tf = np.tile(np.eye(4, dtype=np.float32).reshape(16), (n, 1))
         tf[:, 3] = np.linspace(-1.0, 1.0, n)   # a row of parallel cameras looking down -z
