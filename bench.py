@@ -698,6 +698,15 @@ def components(P, torch, stream, sp):
         "hash_encode_frac_of_gather_ceiling_2p20": round(req20 / (t_enc20 * 1e-3) / gather[1], 4),
         "hash_encode_frac_of_copy_2p20": round(enc_gbs20 / copy_gbs["1gib"], 4),
         "hash_encode_gbs_2p20": round(enc_gbs20, 1)})
+    # the same fraction from L2 requests counted by rocprofv3 (TCP_TCC_READ_REQ_sum on these launches, committed
+    # summary) instead of the line model: counted requests per sample x samples / this run's time / this run's
+    # per-XCD random-line rate
+    l2 = profile_json(L2_FILE)
+    if l2:
+        for tag, n, t in (("2p18", BATCH, t_enc), ("2p20", big, t_enc20)):
+            rq = l2["encode"][tag]["l2_requests_per_sample"]
+            out[f"hash_encode_l2_requests_per_sample_counted_{tag}"] = rq
+            out[f"hash_encode_frac_of_gather_ceiling_counted_{tag}"] = round(rq * n / (t * 1e-3) / gather[1], 4)
     del d_pos20, d_enc20, sink
 
     # both heads forward + backward at 2^18 (density 32-64-16 on N(0,1) inputs, SH of
