@@ -17,6 +17,7 @@
 #include "nerf_math.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace graft {
 
@@ -269,33 +270,61 @@ __global__ __launch_bounds__(256) void color_grad_kernel(const ColorGradArgs a, 
 // The arithmetic per sample is the reference's; only the association of the
 // products and sums differs (scans instead of left-to-right folds), so
 // results agree with the serial kernels above to fp32 rounding.
-__device__ __forceinline__ float wave_sum(float v)
+// Wave-wide sums and scans on DPP moves (row shifts and rotations within the
+// 16-lane rows, then the four row totals through v_readlane): no LDS
+// permutes.  bound_ctrl off: a lane whose source lies outside its row keeps
+// `old` (the identity).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float old, float v)
 {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;  // identical in every lane: each pairwise add is commutative
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old),
+                                                                 __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+constexpr int kRowShr1 = 0x111, kRowShr2 = 0x112, kRowShr4 = 0x114, kRowShr8 = 0x118;
+constexpr int kRowRor1 = 0x121, kRowRor2 = 0x122, kRowRor4 = 0x124, kRowRor8 = 0x128;
+constexpr int kWaveShr1 = 0x138;
+
+__device__ __forceinline__ float lane_value(float v, int lane)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
 }
 
+// the sum over the wave, identical in every lane: each row's sum by rotations
+// (every lane of a row adds the same pairs, commutatively), then the rows'
+__device__ __forceinline__ float wave_sum(float v)
+{
+    v += dpp<kRowRor8>(0.0f, v);
+    v += dpp<kRowRor4>(0.0f, v);
+    v += dpp<kRowRor2>(0.0f, v);
+    v += dpp<kRowRor1>(0.0f, v);
+    return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+}
+
+// exclusive prefix sum / product over the lanes
 __device__ __forceinline__ float wave_excl_sum(float v, int lane)
 {
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const float u = __shfl_up(v, o, 64);
-        if (lane >= o) v += u;
-    }
-    const float e = __shfl_up(v, 1, 64);
-    return lane == 0 ? 0.0f : e;
+    v += dpp<kRowShr1>(0.0f, v);
+    v += dpp<kRowShr2>(0.0f, v);
+    v += dpp<kRowShr4>(0.0f, v);
+    v += dpp<kRowShr8>(0.0f, v);
+    const float r0 = lane_value(v, 15), r1 = lane_value(v, 31), r2 = lane_value(v, 47);
+    const int row = lane >> 4;
+    const float below = row == 0 ? 0.0f : row == 1 ? r0 : row == 2 ? r0 + r1 : (r0 + r1) + r2;
+    if (row != 0) v = below + v;
+    return dpp<kWaveShr1>(0.0f, v);
 }
 
 __device__ __forceinline__ float wave_excl_prod(float v, int lane)
 {
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const float u = __shfl_up(v, o, 64);
-        if (lane >= o) v *= u;
-    }
-    const float e = __shfl_up(v, 1, 64);
-    return lane == 0 ? 1.0f : e;
+    v *= dpp<kRowShr1>(1.0f, v);
+    v *= dpp<kRowShr2>(1.0f, v);
+    v *= dpp<kRowShr4>(1.0f, v);
+    v *= dpp<kRowShr8>(1.0f, v);
+    const float r0 = lane_value(v, 15), r1 = lane_value(v, 31), r2 = lane_value(v, 47);
+    const int row = lane >> 4;
+    const float below = row == 0 ? 1.0f : row == 1 ? r0 : row == 2 ? r0 * r1 : (r0 * r1) * r2;
+    if (row != 0) v = below * v;
+    return dpp<kWaveShr1>(1.0f, v);
 }
 
 // Per-sample terms of the compositing pass (compositing.cu:131-160).
@@ -341,6 +370,204 @@ __device__ __forceinline__ GradSample grad_sample(const ColorGradArgs& g, uint32
     return s;
 }
 
+// One ray of the fused render gradient.  NC > 0: every lane holds at most NC
+// samples (cnt <= 64 NC), kept in registers from pass A to B and from C to D
+// (the loads and exponentials of B and D are not repeated), and pass C takes
+// pass A's colours and pass B's dL/dw from registers (the caller checks that
+// they are the same arrays); NC == 0: any count, each pass reloads its
+// samples.
+template <int NC>
+__device__ __forceinline__ void render_grad_ray(const CompositeArgs& a, const ColorGradArgs& gr, uint32_t r,
+                                                int lane, uint32_t start, float bs)
+{
+    constexpr int M = NC > 0 ? NC : 1;
+    const float c23 = 2.0f / 3;
+    const uint32_t off = a.offsets[r], cnt = a.counts[r];
+    const float d_prior = a.depth_prior ? a.depth_prior[r] : -1.0f;
+    const float s_prior = a.sigma_prior ? a.sigma_prior[r] : -1.0f;
+    const float dwl = (d_prior >= 0) ? a.lambda_depth : 0.0f;
+    const float t_near = (cnt > 0) ? fmaxf(a.t[off], 1e-4f) : 1.0f;
+    const float t_far = (cnt > 0) ? a.t[off + cnt - 1] : 1.0f;
+    const float g_far = 1.0f - t_near / fmaxf(t_far, t_near + 1e-4f);
+    const float inv_g = (g_far > 1e-6f) ? (1.0f / g_far) : 0.0f;
+    const uint32_t run = (cnt + 63) / 64;
+    const uint32_t k0 = min((uint32_t)lane * run, cnt), k1 = min(k0 + run, cnt);
+    // f(sample index, cache slot) over the lane's run; the slot is a
+    // compile-time constant, so the caches stay in registers
+    static_assert(NC <= 2, "at most two cached samples per lane");
+    auto each = [&](auto&& f) {
+        if constexpr (NC > 0) {
+            if (k0 < k1) f(k0, std::integral_constant<int, 0>{});
+            if constexpr (NC > 1)
+                if (k0 + 1 < k1) f(k0 + 1, std::integral_constant<int, 1>{});
+        } else {
+            for (uint32_t i = k0; i < k1; i++) f(i, std::integral_constant<int, 0>{});
+        }
+    };
+    CompSample cs[M];
+    GradSample gs[M];
+    float cg_w[M], co_r[M], co_g[M], co_b[M];  // pass A's colours and pass B's dL/dw
+    float d_w[M], d_r[M], d_g[M], d_b[M];      // pass C's, for pass D
+
+    // ---- A: transmittance and weighted sums of the compositing ----
+    float tl = 1.0f, sr = 0.f, sg = 0.f, sb = 0.f, sd = 0.f, sw = 0.f, swm = 0.f, se = 0.f;
+    each([&](uint32_t i, int q) {
+        const uint32_t idx = off + i;
+        const CompSample c = comp_sample(a, idx, i, cnt, t_near, inv_g, d_prior, s_prior);
+        const float* cc = a.rgb + (size_t)a.rgb_stride * idx;
+        const float w = c.alpha * tl;
+        const float c0 = cc[0], c1 = cc[1], c2 = cc[2];
+        sr += w * c0;
+        sg += w * c1;
+        sb += w * c2;
+        sd += w * c.t;
+        sw += w;
+        swm += w * c.m;
+        se += c.e;
+        tl *= (1.0f - c.alpha);
+        if constexpr (NC > 0) {
+            cs[q] = c;
+            co_r[q] = c0;
+            co_g[q] = c1;
+            co_b[q] = c2;
+        }
+    });
+    const float tj = wave_excl_prod(tl, lane);
+    const float t_end = __shfl(tj * tl, 63, 64);
+    const float lw = tj * sw, lwm = tj * swm;
+    float rc = wave_sum(tj * sr), gc = wave_sum(tj * sg), bc = wave_sum(tj * sb);
+    const float depth = wave_sum(tj * sd);
+    const float dw_g = wave_sum(lw), dwm_g = wave_sum(lwm);
+    const float dls = 1.0f / fmaxf(wave_sum(se), 1e-8f);
+    float dw_s = wave_excl_sum(lw, lane), dwm_s = wave_excl_sum(lwm, lane);
+
+    // ---- B: distortion (+ depth prior) gradient per weight ----
+    float tr = tj, wgl = 0.0f;
+    each([&](uint32_t i, int q) {
+        const uint32_t idx = off + i;
+        CompSample c;
+        if constexpr (NC > 0) c = cs[q];
+        else c = comp_sample(a, idx, i, cnt, t_near, inv_g, d_prior, s_prior);
+        const float w = c.alpha * tr;
+        tr *= (1.0f - c.alpha);
+        const float dloss = -(c.e * dls) * (1.0f / fmaxf(w, 1e-6f));
+        const float bil = c.m * (2 * dw_s - dw_g) + (dwm_g - 2 * dwm_s);
+        const float g = a.lambda_dist * (2 * (bil) + c23 * w * c.ds) + dwl * dloss;
+        a.dw[idx] = g;
+        if constexpr (NC > 0) cg_w[q] = g;
+        wgl += w * g;
+        dw_s += w;
+        dwm_s += w * c.m;
+    });
+    const float wgs = wave_sum(wgl);
+    rc += t_end * a.bg.x;
+    gc += t_end * a.bg.y;
+    bc += t_end * a.bg.z;
+    const float pr = 2.0f * (rc - a.rgb_true[3 * r]);
+    const float pg = 2.0f * (gc - a.rgb_true[3 * r + 1]);
+    const float pb = 2.0f * (bc - a.rgb_true[3 * r + 2]);
+    if (lane == 0) {
+        a.weight_sum[r] = wgs;
+        a.final_rgb[3 * r] = rc;
+        a.final_rgb[3 * r + 1] = gc;
+        a.final_rgb[3 * r + 2] = bc;
+        a.final_depth[r] = depth;
+        a.phi[3 * r] = pr;
+        a.phi[3 * r + 1] = pg;
+        a.phi[3 * r + 2] = pb;
+    }
+
+    // ---- C: the colour gradient's transmittance and weighted sums ----
+    // (the colour outputs and dL/dw of pass A and B when they are the same
+    // arrays, else loaded)
+    float tl2 = 1.0f, qr = 0.f, qg = 0.f, qb = 0.f, qw = 0.f;
+    each([&](uint32_t j, int q) {
+        const uint32_t gi = off + j;
+        const size_t i = (size_t)gi - start;
+        const GradSample s = grad_sample(gr, gi, i, j, cnt);
+        float c0, c1, c2, gw;
+        if constexpr (NC > 0) {
+            c0 = co_r[q];
+            c1 = co_g[q];
+            c2 = co_b[q];
+            gw = cg_w[q];
+        } else {
+            const float* co = gr.color_out + (size_t)gr.color_stride * i;
+            c0 = co[0];
+            c1 = co[1];
+            c2 = co[2];
+            gw = gr.dw[i];
+        }
+        const float w = tl2 * s.alpha;
+        qr += w * c0;
+        qg += w * c1;
+        qb += w * c2;
+        qw += w * gw;
+        tl2 *= (1.0f - s.alpha);
+        if constexpr (NC > 0) {
+            gs[q] = s;
+            d_r[q] = c0;
+            d_g[q] = c1;
+            d_b[q] = c2;
+            d_w[q] = gw;
+        }
+    });
+    const float tj2 = wave_excl_prod(tl2, lane);
+    float cr2 = wave_excl_sum(tj2 * qr, lane), cg2 = wave_excl_sum(tj2 * qg, lane);
+    float cb2 = wave_excl_sum(tj2 * qb, lane), wg = wave_excl_sum(tj2 * qw, lane);
+
+    // ---- D: colour gradient and d sigma per sample ----
+    float T2 = tj2;
+    each([&](uint32_t j, int q) {
+        const uint32_t gi = off + j;
+        const size_t i = (size_t)gi - start;
+        GradSample s;
+        float c_r, c_g, c_b, gw;
+        if constexpr (NC > 0) {
+            s = gs[q];
+            c_r = d_r[q];
+            c_g = d_g[q];
+            c_b = d_b[q];
+            gw = d_w[q];
+        } else {
+            s = grad_sample(gr, gi, i, j, cnt);
+            const float* co = gr.color_out + (size_t)gr.color_stride * i;
+            c_r = co[0];
+            c_g = co[1];
+            c_b = co[2];
+            gw = gr.dw[i];
+        }
+        const float w = T2 * s.alpha;
+        cr2 += w * c_r;
+        cg2 += w * c_g;
+        cb2 += w * c_b;
+        wg += w * gw;
+        float g_r = pr * w * c_r * (1.0f - c_r) * gr.loss_scale * bs;
+        float g_g = pg * w * c_g * (1.0f - c_g) * gr.loss_scale * bs;
+        float g_b = pb * w * c_b * (1.0f - c_b) * gr.loss_scale * bs;
+        g_r = clamp_half_range(g_r);
+        g_g = clamp_half_range(g_g);
+        g_b = clamp_half_range(g_b);
+        if (g_r != g_r || g_g != g_g || g_b != g_b) g_r = g_g = g_b = 0.0f;
+        _Float16* cgo = reinterpret_cast<_Float16*>(gr.color_grad) + (size_t)gr.grad_stride * i;
+        cgo[0] = to_h(g_r);
+        cgo[1] = to_h(g_g);
+        cgo[2] = to_h(g_b);
+        for (int k = 3; k < gr.grad_stride; k++) cgo[k] = (_Float16)0.0f;
+        const float dr = T2 * c_r * (1.0f - s.alpha) - (rc - cr2);
+        const float dg = T2 * c_g * (1.0f - s.alpha) - (gc - cg2);
+        const float db = T2 * c_b * (1.0f - s.alpha) - (bc - cb2);
+        const float suffix = wgs - wg;
+        float dsi = s.delta * (dr * pr + dg * pg + db * pb);
+        dsi += s.delta * (gw * T2 * (1.0f - s.alpha) - suffix);
+        float dsv = dsi * s.sigma * gr.loss_scale * bs;
+        dsv = clamp_half_range(dsv);
+        if (dsv != dsv) dsv = 0.0f;
+        gr.dsigma[i] = dsv;
+        T2 = T2 * (1.0f - s.alpha);
+    });
+}
+
 __global__ __launch_bounds__(256) void render_grad_kernel(const CompositeArgs a, const ColorGradArgs gr,
                                                           const uint32_t* __restrict__ d_rays, uint32_t rays_max)
 {
@@ -349,133 +576,15 @@ __global__ __launch_bounds__(256) void render_grad_kernel(const CompositeArgs a,
     const uint32_t nwaves = gridDim.x * 4;
     const uint32_t start = gr.offsets[0];
     const float bs = 1.0f / (float)gr.total_rays;
-    const float c23 = 2.0f / 3;
+    // pass B's dL/dw and pass A's colours are pass C's when the arrays, their
+    // numbering (a batch starting at sample 0) and the sample times are the
+    // same (the training step's case)
+    const bool same = start == 0u && gr.initial_offset == 0u && a.dw == gr.dw && a.rgb == gr.color_out &&
+                      a.rgb_stride == gr.color_stride && a.t == gr.t && a.offsets == gr.offsets &&
+                      a.counts == gr.counts;
     for (uint32_t r = blockIdx.x * 4 + (threadIdx.x >> 6); r < R; r += nwaves) {  // wave-uniform
-        const uint32_t off = a.offsets[r], cnt = a.counts[r];
-        const float d_prior = a.depth_prior ? a.depth_prior[r] : -1.0f;
-        const float s_prior = a.sigma_prior ? a.sigma_prior[r] : -1.0f;
-        const float dwl = (d_prior >= 0) ? a.lambda_depth : 0.0f;
-        const float t_near = (cnt > 0) ? fmaxf(a.t[off], 1e-4f) : 1.0f;
-        const float t_far = (cnt > 0) ? a.t[off + cnt - 1] : 1.0f;
-        const float g_far = 1.0f - t_near / fmaxf(t_far, t_near + 1e-4f);
-        const float inv_g = (g_far > 1e-6f) ? (1.0f / g_far) : 0.0f;
-        const uint32_t run = (cnt + 63) / 64;
-        const uint32_t k0 = min((uint32_t)lane * run, cnt), k1 = min(k0 + run, cnt);
-
-        // ---- A: transmittance and weighted sums of the compositing ----
-        float tl = 1.0f, sr = 0.f, sg = 0.f, sb = 0.f, sd = 0.f, sw = 0.f, swm = 0.f, se = 0.f;
-        for (uint32_t i = k0; i < k1; i++) {
-            const uint32_t idx = off + i;
-            const CompSample c = comp_sample(a, idx, i, cnt, t_near, inv_g, d_prior, s_prior);
-            const float* cc = a.rgb + (size_t)a.rgb_stride * idx;
-            const float w = c.alpha * tl;
-            sr += w * cc[0];
-            sg += w * cc[1];
-            sb += w * cc[2];
-            sd += w * c.t;
-            sw += w;
-            swm += w * c.m;
-            se += c.e;
-            tl *= (1.0f - c.alpha);
-        }
-        const float tj = wave_excl_prod(tl, lane);
-        const float t_end = __shfl(tj * tl, 63, 64);
-        const float lw = tj * sw, lwm = tj * swm;
-        float rc = wave_sum(tj * sr), gc = wave_sum(tj * sg), bc = wave_sum(tj * sb);
-        const float depth = wave_sum(tj * sd);
-        const float dw_g = wave_sum(lw), dwm_g = wave_sum(lwm);
-        const float dls = 1.0f / fmaxf(wave_sum(se), 1e-8f);
-        float dw_s = wave_excl_sum(lw, lane), dwm_s = wave_excl_sum(lwm, lane);
-
-        // ---- B: distortion (+ depth prior) gradient per weight ----
-        float tr = tj, wgl = 0.0f;
-        for (uint32_t i = k0; i < k1; i++) {
-            const uint32_t idx = off + i;
-            const CompSample c = comp_sample(a, idx, i, cnt, t_near, inv_g, d_prior, s_prior);
-            const float w = c.alpha * tr;
-            tr *= (1.0f - c.alpha);
-            const float dloss = -(c.e * dls) * (1.0f / fmaxf(w, 1e-6f));
-            const float bil = c.m * (2 * dw_s - dw_g) + (dwm_g - 2 * dwm_s);
-            const float g = a.lambda_dist * (2 * (bil) + c23 * w * c.ds) + dwl * dloss;
-            a.dw[idx] = g;
-            wgl += w * g;
-            dw_s += w;
-            dwm_s += w * c.m;
-        }
-        const float wgs = wave_sum(wgl);
-        rc += t_end * a.bg.x;
-        gc += t_end * a.bg.y;
-        bc += t_end * a.bg.z;
-        const float pr = 2.0f * (rc - a.rgb_true[3 * r]);
-        const float pg = 2.0f * (gc - a.rgb_true[3 * r + 1]);
-        const float pb = 2.0f * (bc - a.rgb_true[3 * r + 2]);
-        if (lane == 0) {
-            a.weight_sum[r] = wgs;
-            a.final_rgb[3 * r] = rc;
-            a.final_rgb[3 * r + 1] = gc;
-            a.final_rgb[3 * r + 2] = bc;
-            a.final_depth[r] = depth;
-            a.phi[3 * r] = pr;
-            a.phi[3 * r + 1] = pg;
-            a.phi[3 * r + 2] = pb;
-        }
-
-        // ---- C: the colour gradient's transmittance and weighted sums ----
-        float tl2 = 1.0f, qr = 0.f, qg = 0.f, qb = 0.f, qw = 0.f;
-        for (uint32_t j = k0; j < k1; j++) {
-            const uint32_t gi = off + j;
-            const size_t i = (size_t)gi - start;
-            const GradSample s = grad_sample(gr, gi, i, j, cnt);
-            const float* co = gr.color_out + (size_t)gr.color_stride * i;
-            const float w = tl2 * s.alpha;
-            qr += w * co[0];
-            qg += w * co[1];
-            qb += w * co[2];
-            qw += w * gr.dw[i];
-            tl2 *= (1.0f - s.alpha);
-        }
-        const float tj2 = wave_excl_prod(tl2, lane);
-        float cr2 = wave_excl_sum(tj2 * qr, lane), cg2 = wave_excl_sum(tj2 * qg, lane);
-        float cb2 = wave_excl_sum(tj2 * qb, lane), wg = wave_excl_sum(tj2 * qw, lane);
-
-        // ---- D: colour gradient and d sigma per sample ----
-        float T2 = tj2;
-        for (uint32_t j = k0; j < k1; j++) {
-            const uint32_t gi = off + j;
-            const size_t i = (size_t)gi - start;
-            const GradSample s = grad_sample(gr, gi, i, j, cnt);
-            const float* co = gr.color_out + (size_t)gr.color_stride * i;
-            const float c_r = co[0], c_g = co[1], c_b = co[2];
-            const float gw = gr.dw[i];
-            const float w = T2 * s.alpha;
-            cr2 += w * c_r;
-            cg2 += w * c_g;
-            cb2 += w * c_b;
-            wg += w * gw;
-            float g_r = pr * w * c_r * (1.0f - c_r) * gr.loss_scale * bs;
-            float g_g = pg * w * c_g * (1.0f - c_g) * gr.loss_scale * bs;
-            float g_b = pb * w * c_b * (1.0f - c_b) * gr.loss_scale * bs;
-            g_r = clamp_half_range(g_r);
-            g_g = clamp_half_range(g_g);
-            g_b = clamp_half_range(g_b);
-            if (g_r != g_r || g_g != g_g || g_b != g_b) g_r = g_g = g_b = 0.0f;
-            _Float16* cgo = reinterpret_cast<_Float16*>(gr.color_grad) + (size_t)gr.grad_stride * i;
-            cgo[0] = to_h(g_r);
-            cgo[1] = to_h(g_g);
-            cgo[2] = to_h(g_b);
-            for (int q = 3; q < gr.grad_stride; q++) cgo[q] = (_Float16)0.0f;
-            const float dr = T2 * c_r * (1.0f - s.alpha) - (rc - cr2);
-            const float dg = T2 * c_g * (1.0f - s.alpha) - (gc - cg2);
-            const float db = T2 * c_b * (1.0f - s.alpha) - (bc - cb2);
-            const float suffix = wgs - wg;
-            float dsi = s.delta * (dr * pr + dg * pg + db * pb);
-            dsi += s.delta * (gw * T2 * (1.0f - s.alpha) - suffix);
-            float dsv = dsi * s.sigma * gr.loss_scale * bs;
-            dsv = clamp_half_range(dsv);
-            if (dsv != dsv) dsv = 0.0f;
-            gr.dsigma[i] = dsv;
-            T2 = T2 * (1.0f - s.alpha);
-        }
+        if (same && a.counts[r] <= 128u) render_grad_ray<2>(a, gr, r, lane, start, bs);
+        else render_grad_ray<0>(a, gr, r, lane, start, bs);
     }
 }
 
