@@ -840,17 +840,37 @@ __device__ __forceinline__ void put_b(float* s, int bofs, int mo, float v, int r
 // Blocks [0, color_blocks) accumulate the colour head's gradients over every
 // tile, the others the density head's: each block partial is one head's row
 // of the workspace.
-// The first live tile of t, t + stride, t + 2 stride, ... (ntiles if none):
-// 64 candidates per step, one per lane; wave-uniform.
-__device__ __forceinline__ int next_live(const uint32_t* __restrict__ live, int t, int stride, int ntiles, int lane)
-{
-    for (; t < ntiles; t += 64 * stride) {
-        const int c = t + lane * stride;
-        const uint64_t m = __ballot(c < ntiles && live[c] != 0u);
-        if (m) return t + (__ffsll((unsigned long long)m) - 1) * stride;
+// A wave's live tiles among t0, t0 + stride, t0 + 2 stride, ... in order
+// (wave-uniform): the flags of 64 candidates are loaded at once, one per lane,
+// and kept as a mask, so that finding the next tile waits for no load (a wave
+// of the step visits at most 64 candidates).
+struct LiveTiles {
+    const uint32_t* live;
+    int base, stride, ntiles, lane;
+    uint64_t mask;
+    __device__ LiveTiles(const uint32_t* __restrict__ l, int t0, int st, int nt, int ln)
+        : live(l), base(t0), stride(st), ntiles(nt), lane(ln)
+    {
+        load();
     }
-    return ntiles;
-}
+    __device__ void load()
+    {
+        const int c = base + lane * stride;
+        mask = __ballot(c < ntiles && live[c] != 0u);
+    }
+    // the next live tile, ntiles once there is none
+    __device__ int next()
+    {
+        while (mask == 0ull) {
+            base += 64 * stride;
+            if (base >= ntiles) return ntiles;
+            load();
+        }
+        const int i = __ffsll((unsigned long long)mask) - 1;
+        mask &= mask - 1ull;
+        return base + i * stride;
+    }
+};
 
 // LIVE: p.tile_live holds the dX kernel's flags and only live tiles are visited
 template <bool LIVE>
@@ -893,11 +913,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void h
             // nothing), in order
             // invalid samples: zero dL/dy; the next live tile's inputs are in
             // flight while this one computes
-            int tile = next_live(p.tile_live, rb * waves + wave, stride, ntiles, lane);
+            LiveTiles lt(p.tile_live, rb * waves + wave, stride, ntiles, lane);
+            int tile = lt.next();
             BwdIn in = load_bwd(p, tile * 16 + r, tile < ntiles && tile * 16 + r < N, g);
             while (tile < ntiles) {
                 reload_fence();
-                const int nt = next_live(p.tile_live, tile + stride, stride, ntiles, lane);
+                const int nt = lt.next();
                 const BwdIn nxt = load_bwd(p, nt * 16 + r, nt < ntiles && nt * 16 + r < N, g);
                 Acts a;
                 recompute_tile(w, sbias, in.enc, in.cin, g, a);
@@ -966,13 +987,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void h
                 d1 = valid ? ld_h4(p.dloss + (size_t)n * DOUT + 4 * g) : h4zero();
             };
             if constexpr (LIVE) {
-                int t = next_live(p.tile_live, tile, stride, ntiles, lane);
+                LiveTiles lt(p.tile_live, tile, stride, ntiles, lane);
+                int t = lt.next();
                 h8 enc;
                 h4 d1;
                 load(t, enc, d1);
                 while (t < ntiles) {
                     reload_fence();
-                    const int nt = next_live(p.tile_live, t + stride, stride, ntiles, lane);
+                    const int nt = lt.next();
                     h8 enc_n;
                     h4 d1_n;
                     load(nt, enc_n, d1_n);
