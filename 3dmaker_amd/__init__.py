@@ -100,7 +100,7 @@ class StepBuffers(C.Structure):
         "num_steps", "ray_offsets", "positions", "ray_indices", "t_sorted", "density_out", "color_input",
         "color_output", "sigma", "render_rgb", "phi", "dw", "weight_sum", "dsigma", "color_dx", "density_grad",
         "result")] + [("trainSteps", C.c_int), ("windowStart", C.c_uint32), ("encodings", C.c_void_p),
-                      ("encodingPlane", C.c_uint32), ("activationsSaved", C.c_int)]
+                      ("encodingPlane", C.c_uint32), ("activationsSaved", C.c_int), ("density_stride", C.c_int)]
 
 
 class RefreshBuffers(C.Structure):

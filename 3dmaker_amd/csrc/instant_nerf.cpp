@@ -617,6 +617,8 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
             // the 16x16x32 heads store no activations: the backward recomputes them
             fa.dacts = b.heads_packed ? nullptr : db.activations;
             fa.density_out = b.density_out;
+            // the heads store the density logit 0 alone (all the step reads of it)
+            fa.density_stride = b.heads_packed ? 1 : 16;
             fa.dirs = cd;
             fa.ray_idx = S.ray_idx;
             fa.density_bias = o.densityBias;
@@ -669,6 +671,7 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
             ga.offsets = S.offsets;
             ga.t = S.t_sorted;
             ga.density_out = b.density_out;
+            ga.density_stride = b.heads_packed ? 1 : 16;
             ga.color_out = cb.padded_outputs;
             ga.color_stride = cstride;
             ga.phi = b.phi;
@@ -1138,6 +1141,7 @@ InstantNerf::StepBuffers InstantNerf::stepBuffers() const
     s.ray_indices = S.ray_idx;
     s.t_sorted = S.t_sorted;
     s.density_out = b.density_out;
+    s.densityStride = b.heads_packed ? 1 : 16;
     s.color_input = b.color_in;
     s.color_output = m_colorMLP->buffers().padded_outputs;
     s.sigma = b.sigma;

@@ -70,7 +70,8 @@ struct NerfFwdArgs {
     const __half* const* dW = nullptr;
     const float* const* dB = nullptr;
     __half* const* dacts = nullptr;  // device array: encodings, hidden activations
-    float* density_out = nullptr;    // [N x 16]
+    float* density_out = nullptr;    // [N x density_stride]
+    int density_stride = 16;         // 1 (the 16x16x32 heads only): the density logit 0 alone, [N]
     const float3* dirs = nullptr;    // per ray
     const uint32_t* ray_idx = nullptr;
     float density_bias = 0.0f;

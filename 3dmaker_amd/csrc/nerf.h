@@ -143,7 +143,8 @@ struct ColorGradArgs {
     const uint32_t* counts;
     const uint32_t* offsets;
     const float* t;
-    const float* density_out;
+    const float* density_out;   // [N x density_stride]: the density logit 0 first
+    int density_stride = 16;    // 16 in the reference layout; 1: the logit alone
     const float* color_out;     // [N x color_stride]
     int color_stride;           // 3 in the reference layout
     const float* phi;

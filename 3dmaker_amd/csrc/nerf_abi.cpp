@@ -763,6 +763,7 @@ int inerf_step_buffers(Inerf* h, InerfStepBuffers* out)
         out->encodings = b.encodings;
         out->encodingPlane = b.encodingPlane;
         out->activationsSaved = b.activationsSaved;
+        out->density_stride = b.densityStride;
     });
 }
 int inerf_save(Inerf* h, const char* path)

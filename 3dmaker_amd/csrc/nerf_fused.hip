@@ -256,11 +256,13 @@ void nerf_forward(const NerfFwdArgs& a, int N, hipStream_t stream, const uint32_
         h.out_act = a.out_act;
         h.sigma = a.sigma;
         h.density_out = a.density_out;
+        h.density_stride = a.density_stride;
         h.color_out = a.color_out;
         h.color_in = a.color_in;
         nerf_heads_forward(h, N, stream, d_n);
         return;
     }
+    if (a.density_stride != 16) throw std::runtime_error("NeRF forward: a compact density output needs the MFMA heads");
     NerfFwdParams p{};
     p.pos = a.pos;
     p.pos_stride = a.pos_stride;

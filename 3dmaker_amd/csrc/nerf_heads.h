@@ -28,7 +28,8 @@ struct NerfHeadsFwd {
     float density_bias = 0.0f;
     int out_act = 1;               // colour output: 0 none, 1 sigmoid
     float* sigma = nullptr;        // [N]
-    float* density_out = nullptr;  // nullable [N x 16] (logits + bias, before sanitising)
+    float* density_out = nullptr;  // nullable [N x density_stride] (logits + bias, before sanitising)
+    int density_stride = 16;       // 16: the density head's whole output; 1: its logit 0 alone
     float* color_out = nullptr;    // [N x 8]
     __half* color_in = nullptr;    // [N x 32]: sanitised logits | SH (the backward's input; nullable
                                    // for an inference caller)

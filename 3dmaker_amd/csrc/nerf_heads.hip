@@ -470,7 +470,8 @@ struct FwdParams {
     int N;
     float density_bias;
     float* sigma;     // [N]
-    float* dout;      // nullable [N x 16]
+    float* dout;      // nullable [N x 16], or [N] (logit 0 alone) when dout_full is false
+    bool dout_full;
     float* cout;      // [N x COUT]
     _Float16* cin;    // nullable [N x 32]
 };
@@ -494,7 +495,10 @@ __global__ __launch_bounds__(256) void heads_fwd_kernel(const FwdParams p)
         Acts a;
         forward_tile(w, sbias, in, g, a);
         if (!valid) continue;
-        if (p.dout) *reinterpret_cast<f4*>(p.dout + (size_t)n * DOUT + 4 * g) = a.y;
+        if (p.dout) {
+            if (p.dout_full) *reinterpret_cast<f4*>(p.dout + (size_t)n * DOUT + 4 * g) = a.y;
+            else if (g == 0) p.dout[n] = a.y[0];
+        }
         if (g == 0) p.sigma[n] = nerf_expf(fminf(sanitize_logit(a.y[0]) - p.density_bias, 8.0f));
         if (p.cin) {
             st_h4(p.cin + (size_t)n * 32 + 4 * g, lo4(a.cin));
@@ -1151,7 +1155,10 @@ void nerf_heads_forward(const NerfHeadsFwd& a, int N, hipStream_t s, const uint3
     p.N = N;
     p.density_bias = a.density_bias;
     p.sigma = a.sigma;
+    if (a.density_stride != 16 && a.density_stride != 1)
+        throw std::runtime_error("NeRF heads: the density output stride must be 16 or 1");
     p.dout = a.density_out;
+    p.dout_full = a.density_stride == 16;
     p.cout = a.color_out;
     p.cin = reinterpret_cast<_Float16*>(a.color_in);
     const int ntiles = (N + 15) / 16;

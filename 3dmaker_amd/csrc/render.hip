@@ -208,7 +208,7 @@ __global__ __launch_bounds__(256) void color_grad_kernel(const ColorGradArgs a, 
         const size_t i = gi - start;
         const float tc = a.t[gi];
         const float delta = (j == cnt - 1) ? 1e-3f : fmaxf(a.t[gi + 1] - tc, 0.0f);
-        const float sigma = nerf_expf(fminf(a.density_out[16 * i] - a.bias, 8.0f));
+        const float sigma = nerf_expf(fminf(a.density_out[(size_t)a.density_stride * i] - a.bias, 8.0f));
         const float alpha = 1.0f - nerf_expf(-sigma * delta);
         const float w = T * alpha;
         const float* co = a.color_out + (size_t)a.color_stride * i;
@@ -365,7 +365,7 @@ __device__ __forceinline__ GradSample grad_sample(const ColorGradArgs& g, uint32
     GradSample s;
     const float tc = g.t[gi];
     s.delta = (j == cnt - 1) ? 1e-3f : fmaxf(g.t[gi + 1] - tc, 0.0f);
-    s.sigma = nerf_expf(fminf(g.density_out[16 * i] - g.bias, 8.0f));
+    s.sigma = nerf_expf(fminf(g.density_out[(size_t)g.density_stride * i] - g.bias, 8.0f));
     s.alpha = 1.0f - nerf_expf(-s.sigma * s.delta);
     return s;
 }
@@ -763,6 +763,7 @@ void color_grad(const ColorGradArgs& a, const uint32_t* d_rays, uint32_t rays_ma
 {
     if (rays_max == 0) return;
     if (a.total_rays == 0) throw std::runtime_error("color grad: totalRaysBatch must be > 0");
+    if (a.density_stride < 1) throw std::runtime_error("color grad: density output stride must be >= 1");
     hipLaunchKernelGGL(color_grad_kernel, dim3(blocks_for(rays_max)), dim3(256), 0, s, a, d_rays, rays_max);
     GRAFT_LAUNCH_CHECK();
 }
@@ -772,6 +773,7 @@ void render_grad(const CompositeArgs& a, const ColorGradArgs& g, const uint32_t*
 {
     if (rays_max == 0) return;
     if (g.total_rays == 0) throw std::runtime_error("color grad: totalRaysBatch must be > 0");
+    if (g.density_stride < 1) throw std::runtime_error("color grad: density output stride must be >= 1");
     if (!a.rgb_true || !a.phi) throw std::runtime_error("render_grad: needs ground truth and phi");
     const int blocks = (int)std::min<uint32_t>((rays_max + 3) / 4, (uint32_t)num_cus() * 8);
     hipLaunchKernelGGL(render_grad_kernel, dim3(blocks), dim3(256), 0, s, a, g, d_rays, rays_max);

@@ -166,7 +166,7 @@ public:
         float4* positions;        // [batchSize]
         uint32_t* ray_indices;    // [batchSize]
         float* t_sorted;          // [batchSize]
-        float* density_out;       // [batchSize x 16]
+        float* density_out;       // [batchSize x densityStride]: density logit 0 first
         half* color_input;        // [batchSize x 32]
         float* color_output;      // [batchSize x 8] (padded head output)
         float* sigma;             // [batchSize]
@@ -185,6 +185,8 @@ public:
         int activationsSaved;     // 0: the heads' hidden activations are recomputed, not kept in
                                   // the TinyMLP activation buffers; color_dx then holds only the
                                   // logit features (the SH features are 0)
+        int densityStride;        // 16 (the density head's whole output) or 1 (the 16x16x32 heads:
+                                  // the logit alone; the others are in color_input, sanitised)
     };
     StepBuffers stepBuffers() const;
 

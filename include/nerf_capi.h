@@ -43,7 +43,7 @@ typedef struct InerfStepBuffers {
     float* positions;       /* float4 [batch] */
     uint32_t* ray_indices;
     float* t_sorted;
-    float* density_out;     /* [batch x 16] */
+    float* density_out;     /* [batch x density_stride]: density logit 0 first */
     GRAFT_HALF* color_input;
     float* color_output;    /* [batch x 8] */
     float* sigma;
@@ -60,6 +60,7 @@ typedef struct InerfStepBuffers {
     GRAFT_HALF* encodings;  /* [numLevels][encodingPlane] feature pairs of the last step */
     uint32_t encodingPlane;
     int activationsSaved;   /* 0: hidden activations recomputed, not stored; color_dx holds the logit features only */
+    int density_stride;     /* 16, or 1 (the logit alone) */
 } InerfStepBuffers;
 
 /* InstantNerf::refreshBuffers (introspection, no reference counterpart). */
