@@ -35,7 +35,9 @@ Prints ONE JSON line.
 from __future__ import annotations
 
 import argparse
+import contextlib
 import ctypes as C
+import gc
 import importlib
 import json
 import math
@@ -209,6 +211,21 @@ def options(P, cascades=1):
     o.bgColor[:] = [1.0, 1.0, 1.0]
     o.minDensityThreshold, o.decayValue, o.densityBias = 0.01, 0.95, 0.0
     return o
+
+
+@contextlib.contextmanager
+def timed_region():
+    """Timed steps with no cyclic-garbage collection inside them.  A full collection walks every object the
+    process tracks (torch's among them: about 0.05-0.07 s) and stalls the host, and with it the GPU, which
+    runs at most a step ahead of the host: one inside a 20-step window would be most of its time.  The
+    collector runs before the window instead, and the setup's objects are frozen out of later collections
+    (gc.freeze in main)."""
+    gc.collect()
+    gc.disable()
+    try:
+        yield
+    finally:
+        gc.enable()
 
 
 def cosine_lr(step):
@@ -517,10 +534,11 @@ def five_cascades(P, torch, feed, hfeed, sp):
     tr = Trainer(nerf, feed, sp)
     tr.run(PRETRAIN_STEPS)
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    hits = tr.run(256)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    with timed_region():
+        t0 = time.perf_counter()
+        hits = tr.run(256)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
     tr.run(ANNEAL - tr.step)
     torch.cuda.synchronize()
     out = {"ms_per_step": round(wall * 1e3 / len(hits), 4), "samples_per_s": round(float(np.sum(hits)) / wall, 1),
@@ -839,14 +857,17 @@ def main():
 
     nerf = P.Nerf(options(P, args.cascades))
     tr = Trainer(nerf, feed, sp)
+    gc.collect()
+    gc.freeze()
     # the benchmark is quoted past the early occupancy phase (every cell sampled for steps < 256,
     # InstantNerf.cu:488-494), then --warmup untimed steps
     tr.run(PRETRAIN_STEPS)
     tr.run(args.warmup)
     torch.cuda.synchronize()
     if args.profile_steps:
-        hits = tr.run(args.profile_steps)
-        torch.cuda.synchronize()
+        with timed_region():
+            hits = tr.run(args.profile_steps)
+            torch.cuda.synchronize()
         # Copy calibration for HBM counters: an elementwise kernel reading and
         # writing exactly COPY_BYTES each (torch's neg), three launches.
         src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=dev)
@@ -860,10 +881,11 @@ def main():
 
     torch.cuda.synchronize()
     timed_from, calls0 = tr.step, tr.calls
-    t0 = time.perf_counter()
-    hits = tr.run(args.steps)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    with timed_region():
+        t0 = time.perf_counter()
+        hits = tr.run(args.steps)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
     calls_timed = tr.calls - calls0
     steps = len(hits)
     samples = int(np.sum(hits, dtype=np.int64))
@@ -879,8 +901,9 @@ def main():
     prof_from = tr.step
     nerf.set_profiling(True)
     nerf.reset_stats()
-    prof_hits = tr.run(PROFILE_STEPS)
-    torch.cuda.synchronize()
+    with timed_region():
+        prof_hits = tr.run(PROFILE_STEPS)
+        torch.cuda.synchronize()
     nerf.set_profiling(False)
     st = nerf.stats()
     n_prof = float(np.mean(prof_hits))
@@ -888,10 +911,11 @@ def main():
     # per training step: mean per call x calls / steps (march and occupancy run less than once a step)
     stage_ms_per_step = {k: round(v[0] * v[1] / len(prof_hits), 4) for k, v in st.items()}
     steady_from = tr.step
-    t1 = time.perf_counter()
-    steady_hits = tr.run(STEADY_STEPS)
-    torch.cuda.synchronize()
-    steady_wall = time.perf_counter() - t1
+    with timed_region():
+        t1 = time.perf_counter()
+        steady_hits = tr.run(STEADY_STEPS)
+        torch.cuda.synchronize()
+        steady_wall = time.perf_counter() - t1
     steady = {"window": [steady_from, steady_from + len(steady_hits)],
               "refreshes": sum(1 for k in range(steady_from, steady_from + len(steady_hits)) if k % 16 == 0),
               "ms_per_step": round(steady_wall * 1e3 / len(steady_hits), 4),
