@@ -176,6 +176,28 @@ def test_march_small_grid_bit_exact(dev, R, batch_frac, K):
     check_march(got, want)
 
 
+@pytest.mark.parametrize("res,Cc,L,p,raw,R", [(32, 3, 4, 0.95, False, 2000), (32, 2, 6, 0.9, False, 2000),
+                                              (32, 2, 4, 0.85, True, 2000), (64, 2, 7, 0.92, True, 1000),
+                                              (256, 1, 9, 0.97, False, 300), (30, 2, 3, 0.9, True, 1500)])
+def test_march_runs_and_mip_levels_bit_exact(dev, res, Cc, L, p, raw, R):
+    """Long runs of occupied voxels (the march takes several voxels per memory wait along
+    them) at every kernel width (mip levels <= 4, <= 8, > 8), and grids whose mip levels are
+    independent random bits (a run may end at any level, an unoccupied voxel under an
+    occupied coarse cell or the reverse)."""
+    print(f"[march runs] res={res} C={Cc} L={L} p={p} raw={raw}", flush=True)
+    rng = np.random.default_rng(L * 100 + Cc)
+    if raw:
+        cells = sum((res >> l) ** 3 for l in range(L))
+        bits = (rng.random(Cc * cells) < p).astype(np.uint8)
+        bits = np.packbits(np.concatenate([bits, np.zeros((-len(bits)) % 8, np.uint8)]), bitorder="little")
+    else:
+        bits = scenes.pack_grid([rng.random((res,) * 3) < p for _ in range(Cc)], L)
+    o, d = random_rays(R, L)
+    got, want = run_march(dev, o, d, bits, res, Cc, L, 2, 1 << 30)
+    check_march(got, want)
+    assert got["total"] > 20 * R
+
+
 def test_march_edge_cases(dev):
     res, Cc, L = 16, 2, 3
     rng = np.random.default_rng(7)
