@@ -332,12 +332,14 @@ struct CompSample {
     float t, delta, m, ds, alpha, e;
 };
 
-__device__ __forceinline__ CompSample comp_sample(const CompositeArgs& a, uint32_t idx, uint32_t i, uint32_t cnt,
-                                                  float t_near, float inv_g, float d_prior, float s_prior)
+// From its loaded inputs: the sample's t, the next sample's t (read only when
+// i < cnt - 1) and sigma.
+__device__ __forceinline__ CompSample comp_terms(float t, float t_next_in, float sigma, uint32_t i, uint32_t cnt,
+                                                 float t_near, float inv_g, float d_prior, float s_prior)
 {
     CompSample c;
-    c.t = a.t[idx];
-    float t_next = (i < cnt - 1) ? a.t[idx + 1] : (c.t + 1e-3f);
+    c.t = t;
+    float t_next = (i < cnt - 1) ? t_next_in : (c.t + 1e-3f);
     c.delta = t_next - c.t;
     if (c.delta < 0.0f) {
         c.delta = 0.0f;
@@ -348,10 +350,18 @@ __device__ __forceinline__ CompSample comp_sample(const CompositeArgs& a, uint32
     c.m = 0.5f * (s + s_next);
     c.ds = s_next - s;
     if (c.ds < 0.0f) c.ds = 0.0f;
-    c.alpha = 1.0f - nerf_expf(-a.sigma[idx] * c.delta);
+    c.alpha = 1.0f - nerf_expf(-sigma * c.delta);
     const float tx = (c.t - d_prior) / s_prior;
     c.e = nerf_expf(-0.5f * tx * tx) * c.delta;
     return c;
+}
+
+__device__ __forceinline__ CompSample comp_sample(const CompositeArgs& a, uint32_t idx, uint32_t i, uint32_t cnt,
+                                                  float t_near, float inv_g, float d_prior, float s_prior)
+{
+    const float t = a.t[idx];
+    const float t_next = (i < cnt - 1) ? a.t[idx + 1] : 0.0f;
+    return comp_terms(t, t_next, a.sigma[idx], i, cnt, t_near, inv_g, d_prior, s_prior);
 }
 
 // Per-sample terms of the colour-gradient pass (otherKernels.cu:349-356).
@@ -359,23 +369,35 @@ struct GradSample {
     float delta, sigma, alpha;
 };
 
+// From its loaded inputs: the sample's t, the next one's (read only when
+// j < cnt - 1) and the density output.
+__device__ __forceinline__ GradSample grad_terms(float tc, float t_next, float density, float bias, uint32_t j,
+                                                 uint32_t cnt)
+{
+    GradSample s;
+    s.delta = (j == cnt - 1) ? 1e-3f : fmaxf(t_next - tc, 0.0f);
+    s.sigma = nerf_expf(fminf(density - bias, 8.0f));
+    s.alpha = 1.0f - nerf_expf(-s.sigma * s.delta);
+    return s;
+}
+
 __device__ __forceinline__ GradSample grad_sample(const ColorGradArgs& g, uint32_t gi, size_t i, uint32_t j,
                                                   uint32_t cnt)
 {
-    GradSample s;
     const float tc = g.t[gi];
-    s.delta = (j == cnt - 1) ? 1e-3f : fmaxf(g.t[gi + 1] - tc, 0.0f);
-    s.sigma = nerf_expf(fminf(g.density_out[(size_t)g.density_stride * i] - g.bias, 8.0f));
-    s.alpha = 1.0f - nerf_expf(-s.sigma * s.delta);
-    return s;
+    const float t_next = (j == cnt - 1) ? 0.0f : g.t[gi + 1];
+    return grad_terms(tc, t_next, g.density_out[(size_t)g.density_stride * i], g.bias, j, cnt);
 }
 
 // One ray of the fused render gradient.  NC > 0: every lane holds at most NC
 // samples (cnt <= 64 NC), kept in registers from pass A to B and from C to D
 // (the loads and exponentials of B and D are not repeated), and pass C takes
 // pass A's colours and pass B's dL/dw from registers (the caller checks that
-// they are the same arrays); NC == 0: any count, each pass reloads its
-// samples.
+// they are the same arrays), and every load of the ray (its samples' t, next
+// t, sigma, colour and density output, the ray's first and last t and target
+// colour) is issued at once before pass A; NC == 0: any count, each pass
+// reloads its samples.  A ray without samples writes what the passes would
+// (their sums are +0 and the transmittance 1) and nothing else.
 template <int NC>
 __device__ __forceinline__ void render_grad_ray(const CompositeArgs& a, const ColorGradArgs& gr, uint32_t r,
                                                 int lane, uint32_t start, float bs)
@@ -383,6 +405,44 @@ __device__ __forceinline__ void render_grad_ray(const CompositeArgs& a, const Co
     constexpr int M = NC > 0 ? NC : 1;
     const float c23 = 2.0f / 3;
     const uint32_t off = a.offsets[r], cnt = a.counts[r];
+    const float true_r = a.rgb_true[3 * r], true_g = a.rgb_true[3 * r + 1], true_b = a.rgb_true[3 * r + 2];
+    if (cnt == 0) {  // wave-uniform
+        if (lane == 0) {
+            const float t_end = 1.0f, zero = 0.0f;
+            float rc = zero, gc = zero, bc = zero;
+            rc += t_end * a.bg.x;
+            gc += t_end * a.bg.y;
+            bc += t_end * a.bg.z;
+            a.weight_sum[r] = zero;
+            a.final_rgb[3 * r] = rc;
+            a.final_rgb[3 * r + 1] = gc;
+            a.final_rgb[3 * r + 2] = bc;
+            a.final_depth[r] = zero;
+            a.phi[3 * r] = 2.0f * (rc - true_r);
+            a.phi[3 * r + 1] = 2.0f * (gc - true_g);
+            a.phi[3 * r + 2] = 2.0f * (bc - true_b);
+        }
+        return;
+    }
+    const uint32_t run = (cnt + 63) / 64;
+    const uint32_t k0 = min((uint32_t)lane * run, cnt), k1 = min(k0 + run, cnt);
+    // NC > 0: the lane's samples' inputs (a lane without a sample in a slot
+    // reads the ray's last sample and ignores it)
+    float in_t[M], in_tn[M], in_sig[M], in_c0[M], in_c1[M], in_c2[M], in_den[M];
+    if constexpr (NC > 0) {
+#pragma unroll
+        for (int q = 0; q < NC; q++) {
+            const uint32_t i = min(k0 + (uint32_t)q, cnt - 1), idx = off + i;
+            in_t[q] = a.t[idx];
+            in_tn[q] = a.t[i < cnt - 1 ? idx + 1 : idx];
+            in_sig[q] = a.sigma[idx];
+            const float* cc = a.rgb + (size_t)a.rgb_stride * idx;
+            in_c0[q] = cc[0];
+            in_c1[q] = cc[1];
+            in_c2[q] = cc[2];
+            in_den[q] = gr.density_out[(size_t)gr.density_stride * idx];
+        }
+    }
     const float d_prior = a.depth_prior ? a.depth_prior[r] : -1.0f;
     const float s_prior = a.sigma_prior ? a.sigma_prior[r] : -1.0f;
     const float dwl = (d_prior >= 0) ? a.lambda_depth : 0.0f;
@@ -390,8 +450,6 @@ __device__ __forceinline__ void render_grad_ray(const CompositeArgs& a, const Co
     const float t_far = (cnt > 0) ? a.t[off + cnt - 1] : 1.0f;
     const float g_far = 1.0f - t_near / fmaxf(t_far, t_near + 1e-4f);
     const float inv_g = (g_far > 1e-6f) ? (1.0f / g_far) : 0.0f;
-    const uint32_t run = (cnt + 63) / 64;
-    const uint32_t k0 = min((uint32_t)lane * run, cnt), k1 = min(k0 + run, cnt);
     // f(sample index, cache slot) over the lane's run; the slot is a
     // compile-time constant, so the caches stay in registers
     static_assert(NC <= 2, "at most two cached samples per lane");
@@ -413,10 +471,21 @@ __device__ __forceinline__ void render_grad_ray(const CompositeArgs& a, const Co
     float tl = 1.0f, sr = 0.f, sg = 0.f, sb = 0.f, sd = 0.f, sw = 0.f, swm = 0.f, se = 0.f;
     each([&](uint32_t i, int q) {
         const uint32_t idx = off + i;
-        const CompSample c = comp_sample(a, idx, i, cnt, t_near, inv_g, d_prior, s_prior);
-        const float* cc = a.rgb + (size_t)a.rgb_stride * idx;
+        CompSample c;
+        float c0, c1, c2;
+        if constexpr (NC > 0) {
+            c = comp_terms(in_t[q], in_tn[q], in_sig[q], i, cnt, t_near, inv_g, d_prior, s_prior);
+            c0 = in_c0[q];
+            c1 = in_c1[q];
+            c2 = in_c2[q];
+        } else {
+            c = comp_sample(a, idx, i, cnt, t_near, inv_g, d_prior, s_prior);
+            const float* cc = a.rgb + (size_t)a.rgb_stride * idx;
+            c0 = cc[0];
+            c1 = cc[1];
+            c2 = cc[2];
+        }
         const float w = c.alpha * tl;
-        const float c0 = cc[0], c1 = cc[1], c2 = cc[2];
         sr += w * c0;
         sg += w * c1;
         sb += w * c2;
@@ -463,9 +532,9 @@ __device__ __forceinline__ void render_grad_ray(const CompositeArgs& a, const Co
     rc += t_end * a.bg.x;
     gc += t_end * a.bg.y;
     bc += t_end * a.bg.z;
-    const float pr = 2.0f * (rc - a.rgb_true[3 * r]);
-    const float pg = 2.0f * (gc - a.rgb_true[3 * r + 1]);
-    const float pb = 2.0f * (bc - a.rgb_true[3 * r + 2]);
+    const float pr = 2.0f * (rc - true_r);
+    const float pg = 2.0f * (gc - true_g);
+    const float pb = 2.0f * (bc - true_b);
     if (lane == 0) {
         a.weight_sum[r] = wgs;
         a.final_rgb[3 * r] = rc;
@@ -484,7 +553,9 @@ __device__ __forceinline__ void render_grad_ray(const CompositeArgs& a, const Co
     each([&](uint32_t j, int q) {
         const uint32_t gi = off + j;
         const size_t i = (size_t)gi - start;
-        const GradSample s = grad_sample(gr, gi, i, j, cnt);
+        GradSample s;
+        if constexpr (NC > 0) s = grad_terms(in_t[q], in_tn[q], in_den[q], gr.bias, j, cnt);
+        else s = grad_sample(gr, gi, i, j, cnt);
         float c0, c1, c2, gw;
         if constexpr (NC > 0) {
             c0 = co_r[q];
