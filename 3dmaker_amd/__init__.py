@@ -213,6 +213,7 @@ SIGNATURES = {
     "inerf_set_next_rays": (_i, [_vp, _vp, _vp, _u32]),
     "inerf_set_bg_color": (_i, [_vp, _f, _f, _f]),
     "inerf_set_step_limit": (_i, [_vp, _i]),
+    "inerf_set_keep_color_dx": (_i, [_vp, _i]),
     "inerf_last_rays_trained": (_u32, [_vp]),
     "inerf_set_profiling": (_i, [_vp, _i]),
     "inerf_print_stats": (_i, [_vp]),
@@ -536,6 +537,11 @@ class Nerf:
 
     def last_rays_trained(self):
         return int(self._L.inerf_last_rays_trained(self.h))
+
+    def set_keep_color_dx(self, on):
+        """Keep each step's colour dL/d(input) in step_buffers().color_dx (introspection; the step
+        with recomputed activations does not store it otherwise)."""
+        self._c(self._L.inerf_set_keep_color_dx(self.h, int(on)))
 
     def set_bg_color(self, r, g, b):
         self._c(self._L.inerf_set_bg_color(self.h, float(r), float(g), float(b)))

@@ -711,7 +711,7 @@ void InstantNerf::trainWithRaysHit(const float3* d_rays_o, const float3* d_rays_
         hb.dsigma = b.dsigma;
         hb.denc = db.dx_out;
         hb.density_dy = db.dloss;
-        hb.color_dx = b.color_dx;
+        hb.color_dx = m_keepColorDx ? b.color_dx : nullptr;  // read by nothing in the step
         hb.tile_live = b.tile_live;
         const bool heads = b.heads_packed != nullptr;
         const bool fused_dx = !heads && graft::nerf_backward_dx(bx, 0, stream);  // shape check only (N = 0)

@@ -649,6 +649,10 @@ int inerf_set_step_limit(Inerf* h, int max_steps)
     return NERF_CALL("inerf_set_step_limit", h->nerf.setStepLimit(max_steps));
 }
 uint32_t inerf_last_rays_trained(Inerf* h) { return h ? h->nerf.lastRaysTrained() : 0u; }
+int inerf_set_keep_color_dx(Inerf* h, int on)
+{
+    return NERF_CALL("inerf_set_keep_color_dx", h->nerf.setKeepColorDx(on != 0));
+}
 int inerf_set_bg_color(Inerf* h, float r, float g, float b)
 {
     return NERF_CALL("inerf_set_bg_color", h->nerf.setBgColor(make_float3(r, g, b)));

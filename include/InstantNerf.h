@@ -121,6 +121,12 @@ public:
     // the rest.
     void setStepLimit(int maxSteps) { m_stepLimit = maxSteps > 0 ? maxSteps : 0; }
     uint32_t lastRaysTrained() const { return m_lastRaysTrained; }
+    // Addition (introspection): keep the colour head's dL/d(input) of each
+    // step in stepBuffers().color_dx.  The step with recomputed activations
+    // (activationsSaved 0) reads none of it and stores it only when this is
+    // on (off by default); the other path always stores it (its density
+    // gradient glue reads it).
+    void setKeepColorDx(bool keep) { m_keepColorDx = keep; }
 
     // InstantNerf.cu:359-583.  d_rays_depth / d_rays_sigma may be null (depth
     // supervision off), d_rgb_true must be set, hitCounts (host, nullable)
@@ -175,7 +181,7 @@ public:
         float* dw;                // [batchSize]
         float* weight_sum;        // [rayChunkSize]
         float* dsigma;            // [batchSize]
-        half* color_dx;           // [batchSize x 32]
+        half* color_dx;           // [batchSize x 32]; with activationsSaved 0 only after setKeepColorDx(true)
         half* density_grad;       // [batchSize x 16]
         uint32_t* result;         // [2]: active rays, compacted samples of the last step
         int trainSteps;
@@ -224,6 +230,7 @@ private:
     uint32_t m_windowStart = 0;
     int m_stepLimit = 0;
     uint32_t m_lastRaysTrained = 0;
+    bool m_keepColorDx = false;
 
     uint8_t* d_occupancyGrid = nullptr;
     size_t m_occupancyBytes = 0;

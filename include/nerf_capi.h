@@ -59,7 +59,8 @@ typedef struct InerfStepBuffers {
     uint32_t windowStart;   /* first ray of the last step within the last call's rays */
     GRAFT_HALF* encodings;  /* [numLevels][encodingPlane] feature pairs of the last step */
     uint32_t encodingPlane;
-    int activationsSaved;   /* 0: hidden activations recomputed, not stored; color_dx holds the logit features only */
+    int activationsSaved;   /* 0: hidden activations recomputed, not stored; color_dx holds the logit features only,
+                               and only after inerf_set_keep_color_dx(h, 1) */
     int density_stride;     /* 16, or 1 (the logit alone) */
 } InerfStepBuffers;
 
@@ -91,6 +92,11 @@ int inerf_set_bg_color(Inerf* h, float r, float g, float b);
  * most max_steps optimizer steps per inerf_train call (0: no limit). */
 int inerf_set_step_limit(Inerf* h, int max_steps);
 uint32_t inerf_last_rays_trained(Inerf* h);
+/* InstantNerf::setKeepColorDx (no reference counterpart; introspection for
+ * tests): on != 0 keeps each step's colour dL/d(input) in the step buffers'
+ * color_dx, which the step with recomputed activations otherwise does not
+ * store. */
+int inerf_set_keep_color_dx(Inerf* h, int on);
 int inerf_set_profiling(Inerf* h, int on);
 int inerf_print_stats(Inerf* h);
 /* Per-stage profiling means as "stage:mean_ms:calls;..." into buf (NUL-terminated,

@@ -82,6 +82,7 @@ def test_c5_full_scale_steps_match_oracle(views, cascades):
     imgs, tf, focal = views
     opts = c5_options(P, cascades)
     nerf = P.Nerf(opts)
+    nerf.set_keep_color_dx(True)  # check_step compares the colour dX
     feed = Feed(P, imgs, tf, focal)
     rng = np.random.default_rng(100 + cascades)
     seed = int(rng.integers(0, 1 << 32))

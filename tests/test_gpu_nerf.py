@@ -443,6 +443,7 @@ def test_instant_nerf_step_matches_oracle_chain(dev):
     P = pkg()
     opts = small_options(P, batch=1 << 16)
     nerf = P.Nerf(opts)
+    nerf.set_keep_color_dx(True)  # the colour dX is checked below
     res, Cc, L = 32, 2, 4
     rng = np.random.default_rng(13)
     c = (np.arange(res) + 0.5) / res * 3 - 1.5
